@@ -1,0 +1,80 @@
+/* SolveDelta chunked recurrence on MI355X (gfx950): C-ABI of libsolvedelta_hip.so.
+ *
+ * The library replaces the reference's native operator for this path:
+ *   - sd_fwd      <- causallsso/ops/operator.py:13-55 (solvedelta_native forward) and
+ *                    causallsso/ops/residual_frame/operator.py:154-304 (its composition:
+ *                    L2 norms, predictor C solve, sources, exterior S memory);
+ *   - sd_bwd      <- the autograd backward of that composition
+ *                    (residual_frame/operator.py:74-138, predictor.py:130-282);
+ *   - sd_decode   <- residual_frame/recurrent.py:188-327 (T = 1 recurrent inference).
+ *
+ * Conventions (identical to the reference's public operands):
+ *   u,h,q [B,T,H,r], keys/erase_raw [B,T,H,1,r], values/write_raw [B,T,H,1,V]: bf16,
+ *   arbitrary outer strides (in elements), unit innermost stride;
+ *   associative_log_decay [B,T,H,r] fp32 (unit inner stride); geometry_write (gamma)
+ *   fp32 addressed as gamma[b*sb + t*st + h*sh] (strides 0 broadcast [H] / [1,H]);
+ *   initial / final states: C [B,H,r,r] (prediction = C u) and S [B,H,r,V], fp32,
+ *   contiguous.  Erase/write gates are raw logits; the sigmoid is applied inside.
+ *   Widths: 1 <= r, V <= 128.  Any T >= 1 (tails are neutrally padded inside).
+ *
+ * All entry points enqueue work on `stream` and never allocate or synchronise:
+ * scratch comes from the caller's workspace, whose size the *_workspace_bytes
+ * queries return.  Return value: 0 on success, SD_ERR_* otherwise.
+ */
+#ifndef SOLVEDELTA_H
+#define SOLVEDELTA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SD_OK 0
+#define SD_ERR_SHAPE 1    /* unsupported sizes (maps to ValueError)          */
+#define SD_ERR_ARG 2      /* null pointer / bad stride (maps to ValueError)  */
+#define SD_ERR_WORKSPACE 3 /* workspace too small (maps to ValueError)        */
+#define SD_ERR_LAUNCH 4   /* HIP launch failure (maps to RuntimeError)       */
+
+typedef struct {
+  const void *data;   /* element (b,t,h,c) at data[b*sb + t*st + h*sh + c] */
+  int64_t sb, st, sh; /* strides in elements */
+} sd_view;
+
+typedef struct {
+  int B, T, H, r, V;
+  sd_view u, h, q, k, v, erase_raw, write_raw; /* bf16 */
+  sd_view log_decay;                           /* fp32 */
+  sd_view gamma;                               /* fp32, no channel axis */
+  const float *C0, *S0;                        /* nullable initial state */
+} sd_inputs;
+
+/* Forward. out: bf16 [B,T,H,V] contiguous. C_T / S_T nullable.
+ * The workspace also holds what sd_bwd needs; keep it alive until then. */
+size_t sd_fwd_workspace_bytes(int B, int T, int H, int r, int V);
+int sd_fwd(const sd_inputs *in, void *out, float *C_T, float *S_T, void *workspace,
+           size_t workspace_bytes, void *stream);
+
+/* Backward of sd_fwd with the same inputs and the forward's workspace.
+ * dout: bf16 [B,T,H,V] contiguous (nullable = zero); dC_T, dS_T fp32 (nullable).
+ * Gradient outputs, all contiguous: du,dh,dq,dk,dv,derase,dwrite bf16 in the
+ * shapes of the inputs; dlog_decay fp32 [B,T,H,r]; dgamma fp32 [B,T,H];
+ * dC0, dS0 fp32 (nullable). */
+size_t sd_bwd_workspace_bytes(int B, int T, int H, int r, int V);
+int sd_bwd(const sd_inputs *in, const void *fwd_workspace, const void *dout, const float *dC_T,
+           const float *dS_T, void *du, void *dh, void *dq, void *dk, void *dv, void *derase,
+           void *dwrite, float *dlog_decay, float *dgamma, float *dC0, float *dS0,
+           void *workspace, size_t workspace_bytes, void *stream);
+
+/* One-token recurrent step (T must be 1). out: bf16 [B,1,H,V] contiguous.
+ * C_T / S_T receive the advanced state; they may alias C0 / S0 (in place). */
+int sd_decode(const sd_inputs *in, void *out, float *C_T, float *S_T, void *stream);
+
+/* Library version string. */
+const char *sd_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,7 @@
+"""SolveDelta chunked recurrence on MI355X (gfx950): hand-written HIP kernels
+behind the reference's ``solvedelta_native`` operator API."""
+from .operator import solvedelta_native
+from .state import RELATIVE_FRAME_RADIUS, SolveDeltaState, solvedelta_zero_state
+
+__all__ = ["solvedelta_native", "SolveDeltaState", "solvedelta_zero_state",
+           "RELATIVE_FRAME_RADIUS"]

@@ -1,0 +1,69 @@
+"""ctypes binding of libsolvedelta_hip.so (declared in include/solvedelta.h).
+
+The product path needs the built HIP library: loading fails loudly when it is
+missing; there is no CPU or PyTorch fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsolvedelta_hip.so")
+
+SD_OK, SD_ERR_SHAPE, SD_ERR_ARG, SD_ERR_WORKSPACE, SD_ERR_LAUNCH = 0, 1, 2, 3, 4
+
+
+class SdView(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("sb", ctypes.c_int64), ("st", ctypes.c_int64),
+                ("sh", ctypes.c_int64)]
+
+
+class SdInputs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int), ("T", ctypes.c_int), ("H", ctypes.c_int),
+                ("r", ctypes.c_int), ("V", ctypes.c_int),
+                ("u", SdView), ("h", SdView), ("q", SdView), ("k", SdView), ("v", SdView),
+                ("erase_raw", SdView), ("write_raw", SdView), ("log_decay", SdView),
+                ("gamma", SdView), ("C0", ctypes.c_void_p), ("S0", ctypes.c_void_p)]
+
+
+EXPORTS = {
+    "sd_version": (ctypes.c_char_p, []),
+    "sd_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 5),
+    "sd_fwd": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
+                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "sd_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 5),
+    "sd_bwd": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
+                              ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_void_p] * 12
+               + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "sd_decode": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_void_p]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Loads the HIP library once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: build the HIP extension first "
+            "(python -m solvedelta_amd.build)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in EXPORTS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == SD_OK:
+        return
+    if rc in (SD_ERR_SHAPE, SD_ERR_ARG, SD_ERR_WORKSPACE):
+        raise ValueError(f"{what}: rejected by the HIP library (code {rc})")
+    raise RuntimeError(f"{what}: HIP launch failed (code {rc})")

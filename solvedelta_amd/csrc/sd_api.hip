@@ -1,0 +1,104 @@
+// Host side of the C-ABI: validation, workspace layout and kernel launches.
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include "../../include/solvedelta.h"
+#include "sd_internal.h"
+
+
+using namespace sd;
+
+namespace {
+
+constexpr int kBT = 64, kKD = 128;
+
+struct Carver {
+  char* base; size_t off = 0;
+  template <class T> T* take(size_t count) {
+    off = (off + 255) & ~size_t(255);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
+  const size_t n = (size_t)B * H, NT = (T + kBT - 1) / kBT, Tp = NT * kBT;
+  const size_t panel = n * Tp * kKD, states = n * NT * kKD * kKD;
+  Carver c{(char*)base};
+  FwdWs w;
+  w.Xc = c.take<float>(states);
+  w.Xs = c.take<float>(states);
+  w.delta = c.take<float>(panel);
+  w.d = c.take<float>(panel);
+  w.wS = c.take<float>(panel);
+  w.Wc = c.take<float>(panel);
+  w.Uc = c.take<float>(panel);
+  w.Kc = c.take<float>(panel);
+  w.Gam = c.take<float>(n * NT * kKD);
+  w.Ws = c.take<float>(panel);
+  w.Us = c.take<float>(panel);
+  w.Ks = c.take<float>(panel);
+  w.Qs = c.take<float>(panel);
+  w.Ps = c.take<float>(n * NT * kBT * kBT);
+  if (total) *total = c.off + 256;
+  return w;
+}
+
+bool view_ok(const sd_view& v) { return v.data != nullptr; }
+
+int check_inputs(const sd_inputs* in) {
+  if (!in) return SD_ERR_ARG;
+  if (in->B < 1 || in->T < 1 || in->H < 1 || in->r < 1 || in->V < 1) return SD_ERR_SHAPE;
+  if (in->r > kKD || in->V > kKD) return SD_ERR_SHAPE;
+  if (!view_ok(in->u) || !view_ok(in->h) || !view_ok(in->q) || !view_ok(in->k) ||
+      !view_ok(in->v) || !view_ok(in->erase_raw) || !view_ok(in->write_raw) ||
+      !view_ok(in->log_decay) || !view_ok(in->gamma))
+    return SD_ERR_ARG;
+  return SD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sd_version(void) { return "solvedelta_amd 0.1 (gfx950)"; }
+
+size_t sd_fwd_workspace_bytes(int B, int T, int H, int r, int V) {
+  (void)r; (void)V;
+  size_t total = 0;
+  carve_fwd(nullptr, B, T, H, &total);
+  return total;
+}
+
+int sd_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* workspace,
+           size_t workspace_bytes, void* stream) {
+  int rc = check_inputs(in);
+  if (rc) return rc;
+  if (!out || !workspace) return SD_ERR_ARG;
+  size_t need = 0;
+  FwdWs w = carve_fwd(workspace, in->B, in->T, in->H, &need);
+  if (workspace_bytes < need) return SD_ERR_WORKSPACE;
+  return launch_fwd(in, out, C_T, S_T, w, (hipStream_t)stream);
+}
+
+int sd_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, void* stream) {
+  int rc = check_inputs(in);
+  if (rc) return rc;
+  if (in->T != 1) return SD_ERR_SHAPE;
+  if (!out) return SD_ERR_ARG;
+  return launch_decode(in, out, C_T, S_T, (hipStream_t)stream);
+}
+
+size_t sd_bwd_workspace_bytes(int B, int T, int H, int r, int V) {
+  (void)B; (void)T; (void)H; (void)r; (void)V;
+  return 256;
+}
+
+int sd_bwd(const sd_inputs* in, const void* fwd_workspace, const void* dout, const float* dC_T,
+           const float* dS_T, void* du, void* dh, void* dq, void* dk, void* dv, void* derase,
+           void* dwrite, float* dlog_decay, float* dgamma, float* dC0, float* dS0,
+           void* workspace, size_t workspace_bytes, void* stream) {
+  return SD_ERR_LAUNCH;  // backward kernels not built yet
+}
+
+}  // extern "C"

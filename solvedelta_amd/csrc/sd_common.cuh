@@ -1,0 +1,276 @@
+// Shared device code for the SolveDelta chunk kernels (gfx950 / CDNA4).
+//
+// Every chunk kernel works on one (batch, head) sequence and one chunk of
+// BT = 64 tokens, split into 4 blocks of BS = 16 tokens.  Widths are padded to
+// KD = 128 (key / geometry width r) and VD = 128 (value width V); padding
+// coordinates are zero and stay zero through the recurrence.
+//
+// Decay handling (no reciprocal decays are ever formed):
+//   G_i   = in-chunk inclusive prefix of log-decay g (fp32),
+//   R_J   = G at the row before block J (0 for block 0),
+//   exp(Gx_i - G_j) = exp(Gx_i - R_J) * exp(R_J - G_j)   for j in block J, i >= J0.
+// The first factor is <= 1.  The second lies in [1, exp(drop_J)] where drop_J is
+// the decay accumulated inside block J; coordinates with drop_J > TAU ("wild")
+// are removed from the factored product and added back exactly.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+namespace sd {
+
+constexpr int BT = 64;     // chunk length
+constexpr int BS = 16;     // block length inside a chunk
+constexpr int NB = BT / BS;
+constexpr int KD = 128;    // padded key width
+constexpr int VD = 128;    // padded value width
+constexpr float TAU = 30.f;
+constexpr float RHO = 0.625f;
+constexpr int NTHREADS = 256;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+__device__ __forceinline__ float bf2f(__bf16 x) { return (float)x; }
+__device__ __forceinline__ __bf16 f2bf(float x) { return (__bf16)x; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ f4 zero4() { f4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
+
+// Split an fp32 value into a bf16 high part and a bf16 residual.
+__device__ __forceinline__ void split_bf(float x, __bf16& hi, __bf16& lo) {
+  hi = f2bf(x);
+  lo = f2bf(x - bf2f(hi));
+}
+
+// D(16x16) += A(16xK) * B(Kx16), K a multiple of 32, operands produced by
+// lambdas fa(m, k) and fb(k, n) as fp32 values.  Both operands are split into
+// bf16 hi + lo parts and multiplied as hi*hi + hi*lo + lo*hi (three MFMAs), which
+// keeps ~16 mantissa bits per product (the dropped lo*lo term is ~2^-16 relative).
+// Output layout: lane holds D[(lane>>4)*4 + e][lane & 15], e = 0..3.
+template <class FA, class FB>
+__device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
+  const int l = lane_id();
+  const int m = l & 15, kq = (l >> 4) * 8;
+  for (int k0 = 0; k0 < K; k0 += 32) {
+    bf16x8 ah, al, bh, bl;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 h, lo;
+      split_bf(fa(m, k0 + kq + e), h, lo);
+      ah[e] = h; al[e] = lo;
+      split_bf(fb(k0 + kq + e, m), h, lo);
+      bh[e] = h; bl[e] = lo;
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// D(16x16) += A(16x16) * B(16x16) with the K=16 bf16 MFMA, same 3-term split.
+template <class FA, class FB>
+__device__ __forceinline__ f4 mma_k16(FA fa, FB fb, f4 acc) {
+  const int l = lane_id();
+  const int m = l & 15, kq = (l >> 4) * 4;
+  bf16x4 ah, al, bh, bl;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    __bf16 h, lo;
+    split_bf(fa(m, kq + e), h, lo);
+    ah[e] = h; al[e] = lo;
+    split_bf(fb(kq + e, m), h, lo);
+    bh[e] = h; bl[e] = lo;
+  }
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ int out_row(int e) { return (lane_id() >> 4) * 4 + e; }
+__device__ __forceinline__ int out_col() { return lane_id() & 15; }
+
+// ---------------------------------------------------------------------------
+// Chunk-local shared state
+// ---------------------------------------------------------------------------
+constexpr int GS = KD + 4;  // fp32 panel row stride (floats)
+constexpr int LS = BT + 1;  // 64x64 fp32 matrix row stride
+
+struct ChunkDecay {
+  float G[BT][GS];          // inclusive prefix
+  float R[NB][KD];          // block references
+  unsigned char wild[NB][KD];
+  int nwild[NB];
+  short wlist[NB][KD];
+};
+
+// Loads g (fp32, [B,T,H,r] strided, token stride st, row pointer base at
+// token t0) and builds G, R and the wild lists.  Tokens >= T load 0 (neutral).
+__device__ inline void build_decay(ChunkDecay& cd, const float* g, long long st, int t0, int T,
+                                   int r) {
+  const int tid = threadIdx.x;
+  if (tid < KD) {
+    const int c = tid;
+    float acc = 0.f;
+    for (int i = 0; i < BT; ++i) {
+      const int t = t0 + i;
+      float x = (t < T && c < r) ? g[(long long)t * st + c] : 0.f;
+      acc += x;
+      cd.G[i][c] = acc;
+    }
+    cd.R[0][c] = 0.f;
+    for (int J = 1; J < NB; ++J) cd.R[J][c] = cd.G[J * BS - 1][c];
+    for (int J = 0; J < NB; ++J) {
+      float drop = cd.R[J][c] - cd.G[J * BS + BS - 1][c];
+      cd.wild[J][c] = drop > TAU ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  if (tid < NB) {
+    int n = 0;
+    for (int c = 0; c < KD; ++c)
+      if (cd.wild[tid][c]) cd.wlist[tid][n++] = (short)c;
+    cd.nwild[tid] = n;
+  }
+  __syncthreads();
+}
+
+// Gx for the erase side: inclusive (G_i) or exclusive (G_{i-1} = G_i - g_i).
+// The exclusive prefix is G[i-1] (0 for i = 0).
+__device__ __forceinline__ float gx_excl(const ChunkDecay& cd, int i, int c) {
+  return i > 0 ? cd.G[i - 1][c] : 0.f;
+}
+
+// Decayed Gram M_ij = sum_c X_ic Y_jc exp(Gx_ic - G_jc), j<i (strict) or j<=i,
+// written to M (64 x LS, fp32); entries above the diagonal set to 0.
+// X(i,c), Y(j,c) are lambdas returning fp32; EXCL selects Gx.
+template <bool EXCL, class FX, class FY>
+__device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, float* M,
+                             int ldm = LS) {
+  const int w = wave_id();
+  // 10 lower block pairs (I >= J), distributed over 4 waves.
+  for (int p = w; p < 10; p += 4) {
+    int I = 0, J = p;
+    while (J > I) { J -= I + 1; ++I; }  // p -> (I, J) with J <= I
+    const int I0 = I * BS, J0 = J * BS;
+    const float* RJ = cd.R[J];
+    auto fa = [&](int m, int c) {
+      const int i = I0 + m;
+      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+      return X(i, c) * __expf(gx - RJ[c]);
+    };
+    auto fb = [&](int c, int n) {
+      const int j = J0 + n;
+      return cd.wild[J][c] ? 0.f : Y(j, c) * __expf(RJ[c] - cd.G[j][c]);
+    };
+    f4 acc = mma_k32(fa, fb, KD, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I0 + out_row(e), j = J0 + out_col();
+      const bool keep = strict ? (j < i) : (j <= i);
+      M[i * ldm + j] = keep ? acc[e] : 0.f;
+    }
+  }
+  // Zero the strictly-upper block pairs.
+  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) M[i * ldm + j] = 0.f;
+  }
+  __syncthreads();
+  // Exact fix-up for wild coordinates.
+  for (int J = 0; J < NB; ++J) {
+    const int nw = cd.nwild[J];
+    if (nw == 0) continue;
+    const int J0 = J * BS;
+    const int npairs = (BT - J0) * BS;
+    for (int idx = threadIdx.x; idx < npairs; idx += NTHREADS) {
+      const int i = J0 + idx / BS, j = J0 + idx % BS;
+      const bool keep = strict ? (j < i) : (j <= i);
+      if (!keep) continue;
+      float s = 0.f;
+      for (int q = 0; q < nw; ++q) {
+        const int c = cd.wlist[J][q];
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        s += X(i, c) * Y(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      }
+      M[i * ldm + j] += s;
+    }
+  }
+  __syncthreads();
+}
+
+// (I + L)^{-1} for strictly-lower L (64x64, stride LS), in place -> A.
+// Diagonal 16x16 blocks by forward substitution (one lane per column), then
+// off-diagonal blocks A_IJ = -A_II * sum_{K=J}^{I-1} L_IK A_KJ by distance.
+// tmp: 64 x LS scratch.
+__device__ void unit_lower_inverse(float* L, float* tmp) {
+  const int tid = threadIdx.x;
+  // Phase 0: diagonal blocks.  Thread (B, j): block B = tid/16 (tid < 64), column j.
+  float col[BS];
+  if (tid < NB * BS) {
+    const int B = tid / BS, j = tid % BS, B0 = B * BS;
+#pragma unroll
+    for (int i = 0; i < BS; ++i) {
+      float s = (i == j) ? 1.f : 0.f;
+      for (int m = j; m < i; ++m) s -= L[(B0 + i) * LS + B0 + m] * col[m];
+      col[i] = (i >= j) ? s : 0.f;
+    }
+  }
+  __syncthreads();
+  if (tid < NB * BS) {
+    const int B = tid / BS, j = tid % BS, B0 = B * BS;
+    for (int i = 0; i < BS; ++i) tmp[(B0 + i) * LS + B0 + j] = col[i];
+  }
+  __syncthreads();
+  // tmp holds the diagonal inverses; L still holds the strict lower part.
+  for (int dist = 1; dist < NB; ++dist) {
+    // T_IJ = sum_{K=J}^{I-1} L_IK A_KJ  (A_KJ already in tmp for K-J < dist)
+    float tv[4];
+    int nt = 0;
+    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += NTHREADS) {
+      const int J = idx / (BS * BS), rem = idx % (BS * BS);
+      const int I = J + dist, i = rem / BS, j = rem % BS;
+      float s = 0.f;
+      for (int K = J; K < I; ++K)
+        for (int m = 0; m < BS; ++m)
+          s += L[(I * BS + i) * LS + K * BS + m] * tmp[(K * BS + m) * LS + J * BS + j];
+      tv[nt++] = s;
+    }
+    __syncthreads();
+    nt = 0;
+    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += NTHREADS) {
+      const int J = idx / (BS * BS), rem = idx % (BS * BS);
+      const int I = J + dist, i = rem / BS, j = rem % BS;
+      // stash T in the (still unused) upper block (J, I) of L
+      L[(J * BS + i) * LS + I * BS + j] = tv[nt++];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += NTHREADS) {
+      const int J = idx / (BS * BS), rem = idx % (BS * BS);
+      const int I = J + dist, i = rem / BS, j = rem % BS;
+      float s = 0.f;
+      for (int m = 0; m < BS; ++m)
+        s -= tmp[(I * BS + i) * LS + I * BS + m] * L[(J * BS + m) * LS + I * BS + j];
+      tmp[(I * BS + i) * LS + J * BS + j] = s;
+    }
+    __syncthreads();
+  }
+  // Copy back: A lower (incl. diagonal), zero upper.
+  for (int idx = tid; idx < BT * BT; idx += NTHREADS) {
+    const int i = idx / BT, j = idx % BT;
+    L[i * LS + j] = (j / BS <= i / BS) ? tmp[i * LS + j] : 0.f;
+  }
+  __syncthreads();
+}
+
+}  // namespace sd

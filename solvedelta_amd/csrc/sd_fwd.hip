@@ -1,0 +1,437 @@
+// Forward chunk kernels of the SolveDelta recurrence (gfx950).
+//
+// Pipeline for one call (n = b*H + h sequences, NT chunks of 64 tokens):
+//   k_prep_c   (chunk-parallel) predictor C: norms, decayed Gram L_C, (I+L_C)^-1,
+//              WY panels W_C, U_C, decayed keys, chunk decay;
+//   k_state<false> (sequential per sequence x 16-column tile) C state pass:
+//              delta = U - W X0, X <- Gamma X + K^T delta (X = C^T);
+//   k_prep_s   (chunk-parallel) primal d = k + C^T k, dual sources e, chi, z,
+//              then the S memory's Gram, inverse, WY panels and output pair P;
+//   k_state<true>  S state pass with the chunk output o = Q X0 + P w fused in.
+// The algebra is the generic pre-decay-read delta op: see the SolveDelta
+// chunk derivation restated in tests/chunk_model.py.
+#include "sd_common.cuh"
+#include "sd_internal.h"
+
+namespace sd {
+
+// ---------------------------------------------------------------------------
+// helpers for strided bf16 inputs
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ const __bf16* vrow(const sd_view& v, int b, int t, int h) {
+  return (const __bf16*)v.data + (long long)b * v.sb + (long long)t * v.st + (long long)h * v.sh;
+}
+__device__ __forceinline__ float gamma_at(const sd_view& g, int b, int t, int h) {
+  return ((const float*)g.data)[(long long)b * g.sb + (long long)t * g.st + (long long)h * g.sh];
+}
+
+// Normalise one 128-wide row held as (x0 = coord lane, x1 = coord lane+64).
+__device__ __forceinline__ void l2norm2(float& x0, float& x1, float* rs_out) {
+  float ss = wave_sum(x0 * x0 + x1 * x1);
+  float rs = rsqrtf(ss + 1e-24f);
+  x0 *= rs;
+  x1 *= rs;
+  if (rs_out) *rs_out = rs;
+}
+
+__device__ __forceinline__ void load_row2(const sd_view& v, int b, int t, int h, int T, int w,
+                                          float& x0, float& x1) {
+  const int l = lane_id();
+  x0 = 0.f;
+  x1 = 0.f;
+  if (t < T) {
+    const __bf16* p = vrow(v, b, t, h);
+    if (l < w) x0 = bf2f(p[l]);
+    if (l + 64 < w) x1 = bf2f(p[l + 64]);
+  }
+}
+
+constexpr int PS = KD + 8;  // bf16 panel row stride
+
+// ---------------------------------------------------------------------------
+// k_prep_c
+// ---------------------------------------------------------------------------
+struct PrepCSmem {
+  ChunkDecay cd;
+  float M[BT * LS];
+  float tmp[BT * LS];
+  float Uh[BT][GS];   // normalised u
+  __bf16 Hh[BT][PS];  // h (raw bf16, exact)
+  float gam[BT];
+};
+
+__global__ __launch_bounds__(NTHREADS) void k_prep_c(FwdParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  PrepCSmem& s = *reinterpret_cast<PrepCSmem*>(smem_raw);
+  const int ch = blockIdx.x, n = blockIdx.y;
+  const int b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  const int T = p.T, r = p.r;
+  const sd_inputs& in = p.in;
+  const float* g = (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
+                   (long long)hh * in.log_decay.sh;
+  build_decay(s.cd, g, in.log_decay.st, t0, T, r);
+  const int w = wave_id(), l = lane_id();
+  for (int i = w; i < BT; i += 4) {
+    const int t = t0 + i;
+    float x0, x1;
+    load_row2(in.u, b, t, hh, T, r, x0, x1);
+    l2norm2(x0, x1, nullptr);
+    s.Uh[i][l] = x0;
+    s.Uh[i][l + 64] = x1;
+    load_row2(in.h, b, t, hh, T, r, x0, x1);
+    s.Hh[i][l] = f2bf(x0);
+    s.Hh[i][l + 64] = f2bf(x1);
+    if (l == 0) s.gam[i] = t < T ? gamma_at(in.gamma, b, t, hh) : 0.f;
+  }
+  __syncthreads();
+  const ChunkDecay& cd = s.cd;
+  // L_ij = gamma_i sum_c u_ic u_jc exp(G_{i-1,c} - G_jc), j < i
+  decayed_gram<true>(
+      cd, [&](int i, int c) { return s.gam[i] * s.Uh[i][c]; },
+      [&](int j, int c) { return s.Uh[j][c]; }, true, s.M);
+  unit_lower_inverse(s.M, s.tmp);
+  // W = A diag(gamma) (u e^{Gexcl}),  U = A diag(gamma) h
+  const long long rowbase = (long long)n * p.Tp + t0;
+  for (int cb = 2 * w; cb < 2 * w + 2; ++cb) {
+    for (int I = 0; I < NB; ++I) {
+      const int K = I < 2 ? 32 : 64;
+      auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k] * s.gam[k]; };
+      f4 aw = mma_k32(fa,
+                      [&](int k, int nn) {
+                        const int c = cb * 16 + nn;
+                        return s.Uh[k][c] * __expf(gx_excl(cd, k, c));
+                      },
+                      K, zero4());
+      f4 au = mma_k32(fa, [&](int k, int nn) { return bf2f(s.Hh[k][cb * 16 + nn]); }, K, zero4());
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const long long row = rowbase + I * BS + out_row(e);
+        const int c = cb * 16 + out_col();
+        p.Wc[row * KD + c] = -aw[e];
+        p.Uc[row * KD + c] = au[e];
+      }
+    }
+  }
+  // decayed keys (transposed per chunk) and chunk decay
+  const long long cbase = ((long long)n * p.NT + ch);
+  for (int idx = threadIdx.x; idx < KD * BT; idx += NTHREADS) {
+    const int c = idx / BT, i = idx % BT;
+    p.Kc[cbase * KD * BT + idx] = s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
+  }
+  if (threadIdx.x < KD) p.Gam[cbase * KD + threadIdx.x] = __expf(cd.G[BT - 1][threadIdx.x]);
+}
+
+// ---------------------------------------------------------------------------
+// k_state: sequential chunk pass over one 16-column tile of the state.
+//   X <- state [KD x 16] in MFMA accumulators (wave w owns rows 32w..32w+31)
+//   per chunk: Xs[ch] = X;  w = U + Wneg X;  (COL_OUT) o = Q X + P w;
+//              X = Gamma X + Kt w
+// ---------------------------------------------------------------------------
+struct StateSmem {
+  float Xt[16][KD + 4];  // X0 tile, transposed [col][row]
+  float wt[16][BT + 4];  // w tile, transposed [col][token]
+};
+
+template <bool COL_OUT>
+__global__ __launch_bounds__(NTHREADS) void k_state(StateParams p) {
+  __shared__ StateSmem s;
+  const int tile = blockIdx.x, n = blockIdx.y;
+  const int w = wave_id();
+  const int col = tile * 16 + out_col();  // this lane's state column
+  f4 X[2];
+  // initial state
+  for (int q = 0; q < 2; ++q)
+    for (int e = 0; e < 4; ++e) {
+      const int row = (2 * w + q) * 16 + out_row(e);
+      float x = 0.f;
+      if (p.init && row < p.rows && col < p.cols)
+        x = p.init_transposed ? p.init[(long long)n * p.rows * p.cols + (long long)col * p.rows + row]
+                              : p.init[(long long)n * p.rows * p.cols + (long long)row * p.cols + col];
+      X[q][e] = x;
+    }
+  for (int ch = 0; ch < p.NT; ++ch) {
+    const long long cidx = (long long)n * p.NT + ch;
+    const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
+    // save X0 and stage it transposed ([col][row]) for the MFMA B operand
+    for (int q = 0; q < 2; ++q)
+      for (int e = 0; e < 4; ++e) {
+        const int row = (2 * w + q) * 16 + out_row(e);
+        const float x = X[q][e];
+        if (p.Xs) p.Xs[cidx * KD * KD + (long long)row * KD + col] = x;
+        s.Xt[out_col()][row] = x;
+      }
+    __syncthreads();
+    // w = U + Wneg X  (token block w)
+    f4 acc;
+    for (int e = 0; e < 4; ++e)
+      acc[e] = p.U[(rowbase + w * 16 + out_row(e)) * KD + col];
+    {
+      const float* Wb = p.Wneg + (rowbase + w * 16) * KD;
+      acc = mma_k32([&](int m, int k) { return Wb[(long long)m * KD + k]; },
+                    [&](int k, int nn) { return s.Xt[nn][k]; }, KD, acc);
+    }
+    for (int e = 0; e < 4; ++e) {
+      const int tk = w * 16 + out_row(e);
+      p.wout[(rowbase + tk) * KD + col] = acc[e];
+      s.wt[out_col()][tk] = acc[e];
+    }
+    __syncthreads();
+    if (COL_OUT) {
+      // o = Q X0 + P w  (token block w), written as bf16 to out[b,t,h,v]
+      const float* Qb = p.Q + (rowbase + w * 16) * KD;
+      f4 o = mma_k32([&](int m, int k) { return Qb[(long long)m * KD + k]; },
+                     [&](int k, int nn) { return s.Xt[nn][k]; }, KD, zero4());
+      const float* Pb = p.P + cidx * BT * BT + (long long)(w * 16) * BT;
+      o = mma_k32([&](int m, int k) { return Pb[m * BT + k]; },
+                  [&](int k, int nn) { return s.wt[nn][k]; }, (w < 2 ? 32 : 64), o);
+      const int b = n / p.H, hh = n % p.H;
+      for (int e = 0; e < 4; ++e) {
+        const int t = ch * BT + w * 16 + out_row(e);
+        if (t < p.T && col < p.cols)
+          p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + col] = f2bf(o[e]);
+      }
+    }
+    // X = Gamma X + Kt w
+    const float* gam = p.Gam + cidx * KD;
+    const float* Kt = p.Kt + cidx * KD * BT;
+    for (int q = 0; q < 2; ++q) {
+      const int rb = 2 * w + q;
+      for (int e = 0; e < 4; ++e) X[q][e] *= gam[rb * 16 + out_row(e)];
+      X[q] = mma_k32([&](int m, int k) { return Kt[(long long)(rb * 16 + m) * BT + k]; },
+                     [&](int k, int nn) { return s.wt[nn][k]; }, BT, X[q]);
+    }
+    __syncthreads();
+  }
+  // final state
+  if (p.fin) {
+    for (int q = 0; q < 2; ++q)
+      for (int e = 0; e < 4; ++e) {
+        const int row = (2 * w + q) * 16 + out_row(e);
+        if (row < p.rows && col < p.cols) {
+          const long long base = (long long)n * p.rows * p.cols;
+          if (p.fin_transposed)
+            p.fin[base + (long long)col * p.rows + row] = X[q][e];
+          else
+            p.fin[base + (long long)row * p.cols + col] = X[q][e];
+        }
+      }
+  }
+}
+
+template __global__ void k_state<false>(StateParams);
+template __global__ void k_state<true>(StateParams);
+
+// ---------------------------------------------------------------------------
+// k_prep_s: primal d, dual sources, S-memory WY panels
+// LDS plan: Pa holds u then e, Pb holds k then chi, Pc holds d then serves as
+// the inverse's scratch once d has been consumed.
+// ---------------------------------------------------------------------------
+struct PrepSSmem {
+  ChunkDecay cd;
+  float M[BT * LS];
+  float Pa[BT][GS];
+  float Pb[BT][GS];
+  float Pc[BT][GS];
+};
+
+__global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  PrepSSmem& s = *reinterpret_cast<PrepSSmem*>(smem_raw);
+  const int ch = blockIdx.x, n = blockIdx.y;
+  const int b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  const int T = p.T, r = p.r, V = p.V;
+  const sd_inputs& in = p.in;
+  const float* g = (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
+                   (long long)hh * in.log_decay.sh;
+  build_decay(s.cd, g, in.log_decay.st, t0, T, r);
+  const ChunkDecay& cd = s.cd;
+  const int w = wave_id(), l = lane_id();
+  for (int i = w; i < BT; i += 4) {
+    const int t = t0 + i;
+    float x0, x1;
+    load_row2(in.u, b, t, hh, T, r, x0, x1);
+    l2norm2(x0, x1, nullptr);
+    s.Pa[i][l] = x0;
+    s.Pa[i][l + 64] = x1;
+    load_row2(in.k, b, t, hh, T, r, x0, x1);
+    l2norm2(x0, x1, nullptr);
+    s.Pb[i][l] = x0;
+    s.Pb[i][l + 64] = x1;
+  }
+  __syncthreads();
+  const long long rowbase = (long long)n * p.Tp + t0;
+  const long long cidx = (long long)n * p.NT + ch;
+  const float* delta = p.delta + rowbase * KD;
+  // M_ij = k_i . delta_j  (j <= i)
+  for (int pp = w; pp < 10; pp += 4) {
+    int I = 0, J = pp;
+    while (J > I) { J -= I + 1; ++I; }
+    f4 acc = mma_k32([&](int m, int c) { return s.Pb[I * BS + m][c]; },
+                     [&](int c, int nn) { return delta[(long long)(J * BS + nn) * KD + c]; }, KD,
+                     zero4());
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + out_row(e), j = J * BS + out_col();
+      s.M[i * LS + j] = j <= i ? acc[e] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) s.M[i * LS + j] = 0.f;
+  }
+  __syncthreads();
+  // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}
+  const float* X0 = p.Xc + cidx * KD * KD;
+  for (int q = 0; q < 2; ++q) {
+    const int cb = 2 * w + q;
+    for (int I = 0; I < NB; ++I) {
+      f4 a1 = mma_k32([&](int m, int bb) { return s.Pb[I * BS + m][bb]; },
+                      [&](int bb, int nn) { return X0[(long long)(cb * 16 + nn) * KD + bb]; }, KD,
+                      zero4());
+      f4 tot;
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + out_row(e), c = cb * 16 + out_col();
+        tot[e] = s.Pb[i][c] + __expf(cd.G[i][c]) * a1[e];
+      }
+      for (int J = 0; J <= I; ++J) {
+        f4 a2 = mma_k16([&](int m, int k) { return s.M[(I * BS + m) * LS + J * BS + k]; },
+                        [&](int k, int nn) {
+                          const int c = cb * 16 + nn, j = J * BS + k;
+                          return cd.wild[J][c] ? 0.f : s.Pa[j][c] * __expf(cd.R[J][c] - cd.G[j][c]);
+                        },
+                        zero4());
+        for (int e = 0; e < 4; ++e) {
+          const int i = I * BS + out_row(e), c = cb * 16 + out_col();
+          float add = __expf(cd.G[i][c] - cd.R[J][c]) * a2[e];
+          if (cd.wild[J][c]) {
+            add = 0.f;
+            for (int j = J * BS; j < J * BS + BS && j <= i; ++j)
+              add += s.M[i * LS + j] * s.Pa[j][c] * __expf(fminf(cd.G[i][c] - cd.G[j][c], 0.f));
+          }
+          tot[e] += add;
+        }
+      }
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + out_row(e), c = cb * 16 + out_col();
+        p.d[(rowbase + i) * KD + c] = tot[e];
+        s.Pc[i][c] = tot[e];
+      }
+    }
+  }
+  __syncthreads();
+  // sources (one wave per token row; e overwrites u, chi overwrites k)
+  for (int i = w; i < BT; i += 4) {
+    const int t = t0 + i;
+    const float u0 = s.Pa[i][l], u1 = s.Pa[i][l + 64];
+    const float k0 = s.Pb[i][l], k1 = s.Pb[i][l + 64];
+    const float d0 = delta[(long long)i * KD + l], d1 = delta[(long long)i * KD + l + 64];
+    float q0, q1, e0, e1;
+    load_row2(in.q, b, t, hh, T, r, q0, q1);
+    l2norm2(q0, q1, nullptr);
+    load_row2(in.erase_raw, b, t, hh, T, r, e0, e1);
+    const float usq = wave_sum(u0 * u0 + u1 * u1);
+    const float dsq = wave_sum(d0 * d0 + d1 * d1);
+    const float sc = RHO / sqrtf(RHO * RHO + usq * dsq);
+    const float p0 = sc * d0, p1 = sc * d1;
+    const float den = 1.f + wave_sum(p0 * u0 + p1 * u1);
+    const float b0 = k0 / (1.f + __expf(-e0)), b1 = k1 / (1.f + __expf(-e1));
+    const float ub = wave_sum(u0 * b0 + u1 * b1) / den;
+    const float uq = wave_sum(u0 * q0 + u1 * q1) / den;
+    const bool in0 = l < r, in1 = l + 64 < r;
+    s.Pa[i][l] = in0 ? b0 - p0 * ub : 0.f;
+    s.Pa[i][l + 64] = in1 ? b1 - p1 * ub : 0.f;
+    s.Pb[i][l] = in0 ? q0 - p0 * uq : 0.f;
+    s.Pb[i][l + 64] = in1 ? q1 - p1 * uq : 0.f;
+  }
+  __syncthreads();
+  // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i
+  decayed_gram<false>(
+      cd, [&](int i, int c) { return s.Pb[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
+      false, s.M);
+  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS)
+    p.Ps[cidx * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
+  for (int idx = threadIdx.x; idx < KD * BT; idx += NTHREADS) {
+    const int c = idx / BT, i = idx % BT;
+    p.Ks[cidx * KD * BT + idx] = s.Pc[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
+  }
+  for (int idx = threadIdx.x; idx < BT * KD; idx += NTHREADS) {
+    const int i = idx / KD, c = idx % KD;
+    p.Qs[(rowbase + i) * KD + c] = s.Pb[i][c] * __expf(cd.G[i][c]);
+  }
+  __syncthreads();
+  // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
+  decayed_gram<false>(
+      cd, [&](int i, int c) { return s.Pa[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
+      true, s.M);
+  unit_lower_inverse(s.M, &s.Pc[0][0]);
+  // W = A (e e^G), U = A z with z = sigmoid(write_raw) v read from the inputs
+  for (int cb = 2 * w; cb < 2 * w + 2; ++cb) {
+    for (int I = 0; I < NB; ++I) {
+      const int K = I < 2 ? 32 : 64;
+      auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k]; };
+      f4 aw = mma_k32(fa,
+                      [&](int k, int nn) {
+                        const int c = cb * 16 + nn;
+                        return s.Pa[k][c] * __expf(cd.G[k][c]);
+                      },
+                      K, zero4());
+      f4 au = mma_k32(fa,
+                      [&](int k, int nn) {
+                        const int c = cb * 16 + nn, t = t0 + k;
+                        if (t >= T || c >= V) return 0.f;
+                        const float vv = bf2f(vrow(in.v, b, t, hh)[c]);
+                        const float ww = bf2f(vrow(in.write_raw, b, t, hh)[c]);
+                        return vv / (1.f + __expf(-ww));
+                      },
+                      K, zero4());
+      for (int e = 0; e < 4; ++e) {
+        const long long row = rowbase + I * BS + out_row(e);
+        const int c = cb * 16 + out_col();
+        p.Ws[row * KD + c] = -aw[e];
+        p.Us[row * KD + c] = au[e];
+      }
+    }
+  }
+}
+
+size_t prep_c_smem() { return sizeof(PrepCSmem); }
+size_t prep_s_smem() { return sizeof(PrepSSmem); }
+
+int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const FwdWs& w,
+               hipStream_t st) {
+  
+  const int n = in->B * in->H, NT = (in->T + BT - 1) / BT, Tp = NT * BT;
+
+  FwdParams fp{};
+  fp.in = *in;
+  fp.H = in->H; fp.T = in->T; fp.r = in->r; fp.V = in->V; fp.NT = NT; fp.Tp = Tp;
+  fp.Xc = w.Xc; fp.delta = w.delta; fp.d = w.d;
+  fp.Wc = w.Wc; fp.Uc = w.Uc; fp.Kc = w.Kc; fp.Gam = w.Gam;
+  fp.Ws = w.Ws; fp.Us = w.Us; fp.Ks = w.Ks; fp.Qs = w.Qs; fp.Ps = w.Ps;
+
+  (void)hipFuncSetAttribute((const void*)k_prep_c, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)prep_c_smem());
+  (void)hipFuncSetAttribute((const void*)k_prep_s, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)prep_s_smem());
+  hipLaunchKernelGGL(k_prep_c, dim3(NT, n), dim3(256), prep_c_smem(), st, fp);
+
+  StateParams sc{};
+  sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
+  sc.Wneg = w.Wc; sc.U = w.Uc; sc.Kt = w.Kc; sc.Gam = w.Gam;
+  sc.Xs = w.Xc; sc.wout = w.delta;
+  sc.init = in->C0; sc.init_transposed = 1;
+  sc.fin = C_T; sc.fin_transposed = 1;
+  hipLaunchKernelGGL(k_state<false>, dim3(KD / 16, n), dim3(256), 0, st, sc);
+
+  hipLaunchKernelGGL(k_prep_s, dim3(NT, n), dim3(256), prep_s_smem(), st, fp);
+
+  StateParams ss{};
+  ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
+  ss.Wneg = w.Ws; ss.U = w.Us; ss.Kt = w.Ks; ss.Gam = w.Gam; ss.Q = w.Qs; ss.P = w.Ps;
+  ss.Xs = w.Xs; ss.wout = w.wS; ss.out = (__bf16*)out;
+  ss.init = in->S0; ss.init_transposed = 0;
+  ss.fin = S_T; ss.fin_transposed = 0;
+  hipLaunchKernelGGL(k_state<true>, dim3(KD / 16, n), dim3(256), 0, st, ss);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+}  // namespace sd

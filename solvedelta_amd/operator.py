@@ -1,0 +1,206 @@
+"""Public SolveDelta operator on MI355X: the drop-in for the reference's
+``solvedelta_native`` (causallsso/ops/operator.py:13-55 and
+causallsso/ops/residual_frame/operator.py:154-304).
+
+Same positional order, keyword arguments, return type, dtype/shape/stride
+checks and exception types as the reference; the arithmetic runs in the HIP
+library (include/solvedelta.h) on the current stream with no host sync.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .state import SolveDeltaState
+
+
+def _view(t: torch.Tensor) -> _lib.SdView:
+    return _lib.SdView(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def _gamma_view(g: torch.Tensor, B: int, T: int, H: int) -> _lib.SdView:
+    if g.shape == (H,):
+        return _lib.SdView(g.data_ptr(), 0, 0, g.stride(0))
+    if g.shape == (1, H):
+        return _lib.SdView(g.data_ptr(), 0, 0, g.stride(1))
+    return _lib.SdView(g.data_ptr(), g.stride(0), g.stride(1), g.stride(2))
+
+
+def _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0):
+    B, T, H, r = u.shape
+    V = values.shape[-1]
+    return _lib.SdInputs(
+        B, T, H, r, V, _view(u), _view(h), _view(q), _view(keys), _view(values),
+        _view(erase_raw), _view(write_raw), _view(log_decay), _gamma_view(gamma, B, T, H),
+        None if C0 is None else C0.data_ptr(), None if S0 is None else S0.data_ptr())
+
+
+def _stream(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+class _SolveDeltaFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,
+                want_state: bool):
+        lib = _lib.load()
+        B, T, H, r = u.shape
+        V = values.shape[-1]
+        dev = u.device
+        ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0)
+        out = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
+        C_T = torch.empty(B, H, r, r, dtype=torch.float32, device=dev) if want_state else None
+        S_T = torch.empty(B, H, r, V, dtype=torch.float32, device=dev) if want_state else None
+        nbytes = lib.sd_fwd_workspace_bytes(B, T, H, r, V)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        rc = lib.sd_fwd(ctypes.byref(ins), out.data_ptr(), _ptr(C_T), _ptr(S_T), ws.data_ptr(),
+                        nbytes, _stream(dev))
+        _lib.check(rc, "sd_fwd")
+        ctx.set_materialize_grads(False)
+        ctx.has_C0, ctx.has_S0 = C0 is not None, S0 is not None
+        empty = u.new_empty(0)
+        ctx.save_for_backward(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma,
+                              C0 if C0 is not None else empty, S0 if S0 is not None else empty, ws)
+        if want_state:
+            return out, C_T, S_T
+        return out, None, None
+
+    @staticmethod
+    def backward(ctx, dout, dC, dS):
+        lib = _lib.load()
+        (u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,
+         ws) = ctx.saved_tensors
+        C0 = C0 if ctx.has_C0 else None
+        S0 = S0 if ctx.has_S0 else None
+        B, T, H, r = u.shape
+        V = values.shape[-1]
+        dev = u.device
+        ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0)
+        dout = None if dout is None else dout.to(torch.bfloat16).contiguous()
+        dC = None if dC is None else dC.float().contiguous()
+        dS = None if dS is None else dS.float().contiguous()
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        du, dh, dq = (torch.empty(B, T, H, r, **bf) for _ in range(3))
+        dk, der = (torch.empty(B, T, H, 1, r, **bf) for _ in range(2))
+        dv, dwr = (torch.empty(B, T, H, 1, V, **bf) for _ in range(2))
+        dg = torch.empty(B, T, H, r, dtype=torch.float32, device=dev)
+        dgam = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+        dC0 = torch.empty(B, H, r, r, dtype=torch.float32, device=dev) if C0 is not None else None
+        dS0 = torch.empty(B, H, r, V, dtype=torch.float32, device=dev) if S0 is not None else None
+        nbytes = lib.sd_bwd_workspace_bytes(B, T, H, r, V)
+        bws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        rc = lib.sd_bwd(ctypes.byref(ins), ws.data_ptr(), _ptr(dout), _ptr(dC), _ptr(dS),
+                        du.data_ptr(), dh.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                        der.data_ptr(), dwr.data_ptr(), dg.data_ptr(), dgam.data_ptr(), _ptr(dC0),
+                        _ptr(dS0), bws.data_ptr(), nbytes, _stream(dev))
+        _lib.check(rc, "sd_bwd")
+        if gamma.shape != (B, T, H):
+            dgam = dgam.sum(dim=(0, 1)).reshape(gamma.shape)
+        return (du.to(u.dtype), dh.to(h.dtype), dq.to(q.dtype), dk.to(keys.dtype),
+                dv.to(values.dtype), dg.to(log_decay.dtype), der.to(erase_raw.dtype),
+                dwr.to(write_raw.dtype), dgam.to(gamma.dtype), dC0, dS0, None)
+
+
+def _decode(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, initial_state,
+            return_final_state):
+    """T = 1 recurrent step (reference: residual_frame/recurrent.py:188-327)."""
+    lib = _lib.load()
+    B, T, H, r = u.shape
+    V = values.shape[-1]
+    dev = u.device
+    C0 = S0 = None
+    if initial_state is not None:
+        C0, S0 = (s.contiguous() for s in initial_state)
+    ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0)
+    out = torch.empty(B, 1, H, V, dtype=torch.bfloat16, device=dev)
+    C_T = torch.empty(B, H, r, r, dtype=torch.float32, device=dev) if return_final_state else None
+    S_T = torch.empty(B, H, r, V, dtype=torch.float32, device=dev) if return_final_state else None
+    rc = lib.sd_decode(ctypes.byref(ins), out.data_ptr(), _ptr(C_T), _ptr(S_T), _stream(dev))
+    _lib.check(rc, "sd_decode")
+    if not return_final_state:
+        return out, None
+    return out, SolveDeltaState(C_T, S_T)
+
+
+def solvedelta_native(
+    u: torch.Tensor,
+    h: torch.Tensor,
+    q: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    associative_log_decay: torch.Tensor,
+    erase_raw: torch.Tensor,
+    write_raw: torch.Tensor,
+    geometry_write: torch.Tensor,
+    *,
+    initial_state: Optional[SolveDeltaState] = None,
+    return_final_state: bool = False,
+) -> tuple[torch.Tensor, Optional[SolveDeltaState]]:
+    """Dense K=1 SolveDelta from raw fused-projection views.
+
+    Checks follow ops/operator.py:28-40 then residual_frame/operator.py:169-196
+    and :251-261 in that order; raw erase/write logits are activated inside.
+    """
+    if u.device.type != "cuda" or u.dtype != torch.bfloat16:
+        raise TypeError("solvedelta_native requires BF16 CUDA activations")
+    if keys.ndim != 5 or keys.shape[-2] != 1:
+        raise ValueError("the current production path requires num_edits=1")
+    if erase_raw.shape != keys.shape or erase_raw.dtype != torch.bfloat16:
+        raise ValueError("erase_raw must be BF16 with the same shape as keys")
+    if write_raw.shape != values.shape or write_raw.dtype != torch.bfloat16:
+        raise ValueError("write_raw must be BF16 with the same shape as values")
+    if any(x.stride(-1) != 1 for x in (u, h, q, keys, values, erase_raw, write_raw)):
+        raise ValueError("native vector operands require unit innermost stride")
+    if u.ndim != 4:
+        raise ValueError("u must have shape [B,T,H,r]")
+    B, T, H, r = u.shape
+    if h.shape != u.shape or q.shape != u.shape:
+        raise ValueError("h and q must match u")
+    if keys.shape != (B, T, H, 1, r):
+        raise ValueError("Residual-Frame SolveDelta requires keys [B,T,H,1,r]")
+    if values.ndim != 5 or values.shape[:4] != (B, T, H, 1):
+        raise ValueError("values must have shape [B,T,H,1,d_v]")
+    V = values.shape[-1]
+    if associative_log_decay.shape != (B, T, H, r):
+        raise ValueError("associative_log_decay must have shape [B,T,H,r]")
+    if geometry_write.shape not in ((H,), (1, H), (B, T, H)):
+        raise ValueError("geometry_write must have shape [H], [1,H], or [B,T,H]")
+    if any(x.dtype != u.dtype for x in (h, q, keys, values, erase_raw, write_raw)):
+        raise TypeError("all public vector operands must be BF16")
+    if associative_log_decay.dtype != torch.float32:
+        raise TypeError("associative_log_decay must be FP32")
+    if geometry_write.dtype != torch.float32:
+        raise TypeError("geometry_write must be FP32")
+    if r > 128 or V > 128:
+        raise ValueError("the MI355X path supports key and value widths up to 128")
+    if associative_log_decay.stride(-1) != 1:
+        associative_log_decay = associative_log_decay.contiguous()
+    if initial_state is not None:
+        expected = ((B, H, r, r), (B, H, r, V))
+        if any(s.shape != e for s, e in zip(initial_state, expected)):
+            raise ValueError("initial_state shapes do not match the input geometry")
+        if any(s.dtype != torch.float32 for s in initial_state):
+            raise TypeError("all continuation states must be FP32")
+
+    if T == 1 and not torch.is_grad_enabled():
+        return _decode(u, h, q, keys, values, associative_log_decay, erase_raw, write_raw,
+                       geometry_write, initial_state, return_final_state)
+
+    C0 = S0 = None
+    if initial_state is not None:
+        C0, S0 = (s.contiguous() for s in initial_state)
+    out, C_T, S_T = _SolveDeltaFn.apply(u, h, q, keys, values, associative_log_decay, erase_raw,
+                                        write_raw, geometry_write, C0, S0, return_final_state)
+    if not return_final_state:
+        return out, None
+    return out, SolveDeltaState(C_T, S_T)
+
+
+__all__ = ["solvedelta_native"]

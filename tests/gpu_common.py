@@ -1,0 +1,69 @@
+"""Shared helpers for the GPU parity tests: seeded inputs in the reference's
+conventions and error metrics against the FP64 oracle."""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from oracle.sd_oracle import OracleState, solvedelta_oracle_raw
+
+
+def make_inputs(B, T, H, r, V, *, seed=0, device="cuda", decay="softplus", gamma=0.9,
+                gamma_shape="BTH", requires_grad=False, gate_scale=1.0):
+    """Config-1 style inputs: u,h,q,k,v ~ N(0,1) bf16 (q,k per-head L2-normalised),
+    raw erase/write ~ N(0,1), log-decay = -softplus(N(0,1)), gamma constant."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    n = lambda *s: torch.randn(*s, generator=g)
+    u, h = n(B, T, H, r), n(B, T, H, r)
+    q = F.normalize(n(B, T, H, r), dim=-1)
+    k = F.normalize(n(B, T, H, 1, r), dim=-1)
+    v = n(B, T, H, 1, V)
+    er, wr = gate_scale * n(B, T, H, 1, r), gate_scale * n(B, T, H, 1, V)
+    if decay == "softplus":
+        gd = -F.softplus(n(B, T, H, r))
+    elif decay == "small":
+        gd = -0.02 * torch.rand(B, T, H, r, generator=g)
+    elif decay == "extreme":
+        gd = torch.full((B, T, H, r), -100.0)
+    else:
+        gd = torch.zeros(B, T, H, r)
+    if gamma_shape == "BTH":
+        gm = torch.full((B, T, H), float(gamma))
+    elif gamma_shape == "H":
+        gm = torch.full((H,), float(gamma))
+    else:
+        gm = torch.full((1, H), float(gamma))
+    bf = lambda x: x.to(torch.bfloat16).to(device)
+    args = [bf(u), bf(h), bf(q), bf(k), bf(v), gd.float().to(device), bf(er), bf(wr),
+            gm.float().to(device)]
+    if requires_grad:
+        args = [a.requires_grad_() for a in args]
+    return args
+
+
+def make_state(B, H, r, V, *, seed=1, scale=0.02, device="cuda", requires_grad=False):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    C = (scale * torch.randn(B, H, r, r, generator=g)).to(device)
+    S = (scale * torch.randn(B, H, r, V, generator=g)).to(device)
+    if requires_grad:
+        C.requires_grad_()
+        S.requires_grad_()
+    return C, S
+
+
+def oracle_of(args, state=None, **kw):
+    """FP64 oracle on the exact (bf16-quantised) inputs, on the CPU."""
+    d = [a.detach().double().cpu() for a in args]
+    st = None if state is None else OracleState(*(s.detach().double().cpu() for s in state))
+    return solvedelta_oracle_raw(*d, initial_state=st, **kw)
+
+
+def rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def max_rel(a, b):
+    """max |a-b| / max |b| (max-norm relative error)."""
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
