@@ -1,0 +1,161 @@
+"""Benchmark: SolveDelta layer forward + full VJP on one MI355X.
+
+Workload (timed at configs[1]'s shape): B=4, T=2048,
+H=8, r=V=128, bf16 operands, FP32 state, chunk 64 inside the HIP kernels.
+Synthetic seeded inputs: u,h,v ~ N(0,1); q,k per-head L2-normalised N(0,1);
+raw erase/write ~ N(0,1) (gates sigmoid(N(0,1))); log-decay = -softplus(N(0,1));
+gamma = 0.9 (the mixer's default sigmoid(log 9)); random FP32 initial (C,S) at
+0.02 N(0,1); upstream dO ~ N(0,1).  One step = solvedelta_native forward plus
+torch.autograd.grad for all 9 inputs and both initial states.
+
+Prints ONE JSON line (rank 0).  Besides the throughput it reports:
+  roofline      the step's dominant kernel, timed with HIP events on its launch
+                stream inside a second pass over the same K steps, against the
+                bf16 dense MFMA peak (its algorithmic flops per launch are the
+                chunk GEMMs it evaluates, counted once at 2*M*N*K);
+  cpu_baseline  the FP64 token-loop oracle (oracle/sd_oracle.py) forward+VJP on
+                the host cores, on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+B, T, H, R, V, CH = 4, 2048, 8, 128, 128, 64
+PEAK_MFMA_BF16 = 2.5e15
+PEAK_HBM = 8.0e12
+
+# Algorithmic flops per (sequence, 64-token chunk) of each chunk kernel at
+# r = V = 128: dense GEMM products 2*M*N*K, lower-triangular ones at half.
+_G = 2 * 64 * 128 * 128      # (64 x 128) @ (128 x 128)
+_T = 64 * 64 * 128           # triangular (64 x 64 x 128) product, halved
+FLOPS_PER_CHUNK = {
+    "k_prep_c": 3 * _T,                          # L, W, U
+    "state_c_fwd": 2 * _G,                       # w = U - W X, X += K^T w
+    "k_prep_s": 6 * _T + _G,                     # k.delta, apply, P, L, W, U; K X0^T
+    "state_s_fwd": 3 * _G + _T,                  # w, Q X0, X update; P w
+    "k_bprep_s": 2 * 64 ** 3 // 2 + 2 * _T * 2 // 2 + _T,  # N = P A, dU, Wk
+    "state_s_bwd": 3 * _G,                       # dw, injection, lambda update
+    "k_grad_s": 3 * _G + 6 * _T,                 # dw X0, dO X0, w lam; M1, M2, 2 apply, 2 apply_t
+    "k_bprep_c": _T + 64 ** 3 + 2 * 2 * 64 * 64 * 128 // 2 + _T,
+    "state_c_bwd": 3 * _G,
+    "k_grad_c": 3 * _G + 7 * _T,
+}
+
+
+def make_inputs(device, seed=0, b=B, t=T):
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(seed)
+    n = lambda *s: torch.randn(*s, generator=g)
+    bf = lambda x: x.to(torch.bfloat16).to(device).requires_grad_()
+    u, h = bf(n(b, t, H, R)), bf(n(b, t, H, R))
+    q = bf(F.normalize(n(b, t, H, R), dim=-1))
+    k = bf(F.normalize(n(b, t, H, 1, R), dim=-1))
+    v = bf(n(b, t, H, 1, V))
+    gd = (-F.softplus(n(b, t, H, R))).to(device).requires_grad_()
+    er, wr = bf(n(b, t, H, 1, R)), bf(n(b, t, H, 1, V))
+    gm = torch.full((b, t, H), 0.9, device=device).requires_grad_()
+    C0 = (0.02 * n(b, H, R, R)).to(device).requires_grad_()
+    S0 = (0.02 * n(b, H, R, V)).to(device).requires_grad_()
+    dO = n(b, t, H, V).to(torch.bfloat16).to(device)
+    return [u, h, q, k, v, gd, er, wr, gm], (C0, S0), dO
+
+
+def cpu_baseline(budget_s=15.0):
+    """FP64 oracle forward + autograd VJP on the host, bounded sample: all 32
+    (b,h) sequences, T tokens with T grown until one pass costs ~budget_s/2."""
+    from oracle.sd_oracle import OracleState, solvedelta_oracle_raw
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+
+    def run(tt):
+        ins, st, dO = make_inputs("cpu", seed=1, t=tt)
+        ins = [x.detach().double().requires_grad_() for x in ins]
+        st = [x.detach().double().requires_grad_() for x in st]
+        t0 = time.perf_counter()
+        o, _ = solvedelta_oracle_raw(*ins, initial_state=OracleState(*st))
+        torch.autograd.grad(o, ins + st, dO.double())
+        return time.perf_counter() - t0
+
+    tt, dt = 8, run(8)
+    while dt < budget_s / 2 and tt < 512:
+        tt *= 2
+        dt = run(tt)
+    return {"value": B * tt / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"FP64 torch token-loop oracle F+VJP, B={B} H={H} r=V={R}, T={tt} "
+                      f"({dt:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the per-(batch, head) recurrence shards with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    from solvedelta_amd import _lib, solvedelta_native
+    dev = torch.device("cuda:0")
+    ins, st, dO = make_inputs(dev)
+    leaves = ins + list(st)
+
+    def step():
+        out, _ = solvedelta_native(*ins, initial_state=st, return_final_state=False)
+        return torch.autograd.grad(out, leaves, dO)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / a.steps
+
+    # second pass: per-kernel HIP-event timing on the launch stream
+    _lib.profile_enable(True)
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    prof = _lib.profile_read()
+    _lib.profile_enable(False)
+    nchunks = B * H * (T // CH)
+    dom = max(prof, key=lambda k: prof[k][0])
+    tot_ms, cnt = prof[dom]
+    avg_s = tot_ms / cnt / 1e3
+    flops = FLOPS_PER_CHUNK.get(dom, 0) * nchunks
+    achieved = flops / avg_s / 1e12
+    roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3),
+            "peak": PEAK_MFMA_BF16 / 1e12, "unit": "TFLOP/s",
+            "frac": round(achieved * 1e12 / PEAK_MFMA_BF16, 5), "traffic": None,
+            "avg_us": round(avg_s * 1e6, 2),
+            "kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in sorted(prof.items())}}
+    res = {
+        "metric": "SolveDelta layer fwd+bwd tokens/s @B4 T2048 H8 d128; % MFMA/HBM roofline",
+        "value": round(B * T / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "SolveDelta core operator forward + full VJP (configs[2] timed "
+                               "at configs[1] shape)", "global_batch": B, "seq_len": T,
+                   "heads": H, "dk": R, "dv": V, "chunk": CH, "parallelism": "single-gpu"},
+        "roofline": roof,
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -71,6 +71,13 @@ int sd_bwd(const sd_inputs *in, const void *fwd_workspace, const void *dout, con
  * C_T / S_T receive the advanced state; they may alias C0 / S0 (in place). */
 int sd_decode(const sd_inputs *in, void *out, float *C_T, float *S_T, void *stream);
 
+/* Opt-in per-kernel timing with HIP events on the launch stream (no
+ * counterpart in the reference; used by bench.py).  sd_profile_enable(1)
+ * clears the totals and starts recording; sd_profile_read writes lines
+ * "kernel total_ms launches" into buf and returns the bytes needed. */
+int sd_profile_enable(int on);
+size_t sd_profile_read(char *buf, size_t len);
+
 /* Library version string. */
 const char *sd_version(void);
 

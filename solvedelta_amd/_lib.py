@@ -34,8 +34,10 @@ EXPORTS = {
                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "sd_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 5),
     "sd_bwd": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
-                              ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_void_p] * 12
+                              ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_void_p] * 11
                + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "sd_profile_enable": (ctypes.c_int, [ctypes.c_int]),
+    "sd_profile_read": (ctypes.c_size_t, [ctypes.c_char_p, ctypes.c_size_t]),
     "sd_decode": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
                                  ctypes.c_void_p, ctypes.c_void_p]),
 }
@@ -67,3 +69,20 @@ def check(rc: int, what: str) -> None:
     if rc in (SD_ERR_SHAPE, SD_ERR_ARG, SD_ERR_WORKSPACE):
         raise ValueError(f"{what}: rejected by the HIP library (code {rc})")
     raise RuntimeError(f"{what}: HIP launch failed (code {rc})")
+
+
+def profile_enable(on: bool) -> None:
+    load().sd_profile_enable(1 if on else 0)
+
+
+def profile_read() -> dict:
+    """Per-kernel (total_ms, launches) recorded since profile_enable(True)."""
+    lib = load()
+    n = lib.sd_profile_read(None, 0)
+    buf = ctypes.create_string_buffer(n + 16)
+    lib.sd_profile_read(buf, len(buf))
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, ms, cnt = line.split()
+        out[name] = (float(ms), int(cnt))
+    return out

@@ -23,11 +23,15 @@ struct Carver {
 
 FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
   const size_t n = (size_t)B * H, NT = (T + kBT - 1) / kBT, Tp = NT * kBT;
-  const size_t panel = n * Tp * kKD, states = n * NT * kKD * kKD;
+  const size_t panel = n * Tp * kKD, states = n * (NT + 1) * kKD * kKD, amat = n * NT * kBT * kBT;
   Carver c{(char*)base};
   FwdWs w;
   w.Xc = c.take<float>(states);
   w.Xs = c.take<float>(states);
+  w.Ac = c.take<float>(amat);
+  w.As = c.take<float>(amat);
+  w.e = c.take<float>(panel);
+  w.chi = c.take<float>(panel);
   w.delta = c.take<float>(panel);
   w.d = c.take<float>(panel);
   w.wS = c.take<float>(panel);
@@ -40,6 +44,21 @@ FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
   w.Ks = c.take<float>(panel);
   w.Qs = c.take<float>(panel);
   w.Ps = c.take<float>(n * NT * kBT * kBT);
+  if (total) *total = c.off + 256;
+  return w;
+}
+
+BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
+  const size_t n = (size_t)B * H, NT = (T + kBT - 1) / kBT, Tp = NT * kBT;
+  const size_t panel = n * Tp * kKD, states = n * (NT + 1) * kKD * kKD;
+  Carver c{(char*)base};
+  BwdWs w;
+  w.Lc = c.take<float>(states);
+  w.Ls = c.take<float>(states);
+  float** panels[] = {&w.dU, &w.Wk, &w.At1, &w.B1, &w.Ant, &w.dwS, &w.dwC, &w.de, &w.dchi,
+                      &w.dd, &w.dgS, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
+                      &w.dgC};
+  for (float** pp : panels) *pp = c.take<float>(panel);
   if (total) *total = c.off + 256;
   return w;
 }
@@ -90,15 +109,27 @@ int sd_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, void* stre
 }
 
 size_t sd_bwd_workspace_bytes(int B, int T, int H, int r, int V) {
-  (void)B; (void)T; (void)H; (void)r; (void)V;
-  return 256;
+  (void)r; (void)V;
+  size_t total = 0;
+  carve_bwd(nullptr, B, T, H, &total);
+  return total;
 }
 
 int sd_bwd(const sd_inputs* in, const void* fwd_workspace, const void* dout, const float* dC_T,
            const float* dS_T, void* du, void* dh, void* dq, void* dk, void* dv, void* derase,
            void* dwrite, float* dlog_decay, float* dgamma, float* dC0, float* dS0,
            void* workspace, size_t workspace_bytes, void* stream) {
-  return SD_ERR_LAUNCH;  // backward kernels not built yet
+  int rc = check_inputs(in);
+  if (rc) return rc;
+  if (!fwd_workspace || !workspace || !du || !dh || !dq || !dk || !dv || !derase || !dwrite ||
+      !dlog_decay || !dgamma)
+    return SD_ERR_ARG;
+  size_t need = 0;
+  BwdWs bw = carve_bwd(workspace, in->B, in->T, in->H, &need);
+  if (workspace_bytes < need) return SD_ERR_WORKSPACE;
+  FwdWs fw = carve_fwd((void*)fwd_workspace, in->B, in->T, in->H, nullptr);
+  return launch_bwd(in, fw, bw, dout, dC_T, dS_T, du, dh, dq, dk, dv, derase, dwrite, dlog_decay,
+                    dgamma, dC0, dS0, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,552 @@
+// Backward (VJP) chunk kernels of the SolveDelta recurrence (gfx950).
+//
+// Mirror of the forward, in reverse order, recomputing nothing per token that
+// the forward workspace keeps (chunk states, (I+L)^-1, WY/key panels, delta,
+// d, e, chi, w).  For each op (S memory first, then C predictor):
+//   k_bprep_*   chunk-parallel: dU = (P A)^T rhs (+ A^T ext), Wk = A^T K^,
+//               and the reverse-pass injection panels;
+//   k_state<false> with rev = 1: lambda <- Gamma lambda + A1 B1 - x~^T dw,
+//               dw = dU + Wk lambda, storing the chunk-end cotangents;
+//   k_grad_*    chunk-parallel closed-form gradients of (k, x, v, q) and the
+//               in-chunk reverse cumulative sum that closes the decay gradient.
+// Between the ops k_src_bwd transposes the dual sources (phi, den, e, chi, z)
+// and the q/erase/write/value gates; k_final closes u, k, h, gamma, log-decay.
+// The closed forms are the ones checked against FP64 autograd in
+// tests/chunk_model.py (Op.backward, sources_bwd, backward_seq).
+#include "sd_common.cuh"
+#include "sd_internal.h"
+
+namespace sd {
+
+struct BwdParams {
+  sd_inputs in;
+  int H, T, r, V, NT, Tp;
+  FwdWs f;
+  BwdWs g;
+  const __bf16* dout;  // nullable
+  __bf16 *du, *dh, *dq, *dk, *dv, *der, *dwr;
+  float *dg, *dgam;
+};
+
+__device__ __forceinline__ const __bf16* brow(const sd_view& v, int b, int t, int h) {
+  return (const __bf16*)v.data + (long long)b * v.sb + (long long)t * v.st + (long long)h * v.sh;
+}
+
+__device__ __forceinline__ float dout_at(const BwdParams& p, int b, int t, int h, int c) {
+  if (!p.dout || t >= p.T || c >= p.V) return 0.f;
+  return bf2f(p.dout[(((long long)b * p.T + t) * p.H + h) * p.V + c]);
+}
+
+__device__ __forceinline__ void ldrow2(const sd_view& v, int b, int t, int h, int T, int w,
+                                       float& x0, float& x1) {
+  const int l = lane_id();
+  x0 = 0.f;
+  x1 = 0.f;
+  if (t < T) {
+    const __bf16* q = brow(v, b, t, h);
+    if (l < w) x0 = bf2f(q[l]);
+    if (l + 64 < w) x1 = bf2f(q[l + 64]);
+  }
+}
+
+__device__ __forceinline__ float norm2(float& x0, float& x1) {
+  const float rs = rsqrtf(wave_sum(x0 * x0 + x1 * x1) + 1e-24f);
+  x0 *= rs;
+  x1 *= rs;
+  return rs;
+}
+
+__device__ __forceinline__ const float* gptr(const sd_inputs& in, int b, int h) {
+  return (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
+         (long long)h * in.log_decay.sh;
+}
+
+// 64x64 N = P A (both 64 x LS in LDS) -> N (64 x LS)
+__device__ void mat64_mul(const float* P, const float* A, float* N) {
+  const int I = wave_id();
+  for (int J = 0; J < NB; ++J) {
+    f4 acc = mma_k32([&](int m, int k) { return P[(I * BS + m) * LS + k]; },
+                     [&](int k, int nn) { return A[k * LS + J * BS + nn]; }, BT, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) N[(I * BS + out_row(e)) * LS + J * BS + out_col()] = acc[e];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// S memory
+// ---------------------------------------------------------------------------
+struct BprepSSmem {
+  ChunkDecay cd;
+  float A[BT * LS];
+  float P[BT * LS];
+  float N[BT * LS];
+};
+
+__global__ __launch_bounds__(NTHREADS) void k_bprep_s(BwdParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  BprepSSmem& s = *reinterpret_cast<BprepSSmem*>(smem_raw);
+  const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
+  const ChunkDecay& cd = s.cd;
+  const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
+  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS) {
+    s.A[(idx / BT) * LS + idx % BT] = p.f.As[cidx * BT * BT + idx];
+    s.P[(idx / BT) * LS + idx % BT] = p.f.Ps[cidx * BT * BT + idx];
+  }
+  __syncthreads();
+  mat64_mul(s.P, s.A, s.N);
+  __syncthreads();
+  const int w = wave_id();
+  const float* Kt = p.f.Ks + cidx * KD * BT;
+  for (int cb = 2 * w; cb < 2 * w + 2; ++cb)
+    for (int Jb = 0; Jb < NB; ++Jb) {
+      // dU_j = sum_l N_lj dO_l ;  Wk_j = sum_i A_ij K^_i
+      f4 du = mma_k32([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; },
+                      [&](int k, int nn) { return dout_at(p, b, t0 + k, hh, cb * 16 + nn); }, BT,
+                      zero4());
+      f4 wk = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
+                      [&](int k, int nn) { return Kt[(long long)(cb * 16 + nn) * BT + k]; }, BT,
+                      zero4());
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const long long row = rowbase + Jb * BS + out_row(e);
+        const int c = cb * 16 + out_col();
+        p.g.dU[row * KD + c] = du[e];
+        p.g.Wk[row * KD + c] = wk[e];
+      }
+    }
+  for (int idx = threadIdx.x; idx < BT * KD; idx += NTHREADS) {
+    const int i = idx / KD, c = idx % KD;
+    const long long o = (rowbase + i) * KD + c;
+    p.g.Ant[o] = -p.f.e[o] * __expf(cd.G[i][c]);
+    p.g.B1[o] = dout_at(p, b, t0 + i, hh, c);
+  }
+}
+
+struct GradSmem {
+  ChunkDecay cd;
+  float M1[BT * LS];
+  float M2[BT * LS];
+  float M3[BT * LS];
+  float dG[BT][GS];
+};
+
+__global__ __launch_bounds__(NTHREADS) void k_grad_s(BwdParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  GradSmem& s = *reinterpret_cast<GradSmem*>(smem_raw);
+  const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
+  const ChunkDecay& cd = s.cd;
+  const long long rowbase = (long long)n * p.Tp + t0;
+  const long long sidx = (long long)n * (p.NT + 1) + ch;
+  const float* dw = p.g.dwS + rowbase * KD;
+  const float* wv = p.f.wS + rowbase * KD;
+  const float* dd_ = p.f.d + rowbase * KD;
+  const float* ee = p.f.e + rowbase * KD;
+  const float* chi = p.f.chi + rowbase * KD;
+  const float* dO = p.g.B1 + rowbase * KD;  // fp32 copy of the output cotangent
+  const float* X0 = p.f.Xs + sidx * KD * KD;
+  const float* XC = X0 + KD * KD;
+  const float* lam = p.g.Ls + sidx * KD * KD;
+  // M1_ij = dw_i . w_j (j < i);  M2_li = dO_l . w_i (l >= i)
+  plain_pair([&](int i, int c) { return dw[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
+             true, s.M1);
+  plain_pair([&](int i, int c) { return dO[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
+             false, s.M2);
+  __syncthreads();
+  const int w = wave_id();
+  auto D = [&](int j, int c) { return dd_[j * KD + c]; };
+  auto E = [&](int j, int c) { return ee[j * KD + c]; };
+  auto Q = [&](int j, int c) { return chi[j * KD + c]; };
+  for (int cb = 2 * w; cb < 2 * w + 2; ++cb)
+    for (int I = 0; I < NB; ++I) {
+      f4 a = mma_k32([&](int m, int v) { return dw[(I * BS + m) * KD + v]; },
+                     [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
+      f4 ap = decayed_apply_tile<false>(cd, s.M1, D, I, cb);
+      f4 bq = mma_k32([&](int m, int v) { return dO[(I * BS + m) * KD + v]; },
+                      [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
+      f4 bp = decayed_apply_tile<false>(cd, s.M2, D, I, cb);
+      f4 kl = mma_k32([&](int m, int v) { return wv[(I * BS + m) * KD + v]; },
+                      [&](int v, int nn) { return lam[(cb * 16 + nn) * KD + v]; }, KD, zero4());
+      f4 k2 = decayed_apply_t_tile<false>(cd, s.M2, Q, I, cb);
+      f4 k3 = decayed_apply_t_tile<false>(cd, s.M1, E, I, cb);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + out_row(e), c = cb * 16 + out_col();
+        const float eg = __expf(cd.G[i][c]);
+        const float de = -(eg * a[e] + ap[e]);
+        const float dchi = eg * bq[e] + bp[e];
+        const float ddv = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[e] + k2[e] - k3[e];
+        const long long o = (rowbase + i) * KD + c;
+        p.g.de[o] = de;
+        p.g.dchi[o] = dchi;
+        p.g.dd[o] = ddv;
+        s.dG[i][c] = chi[i * KD + c] * dchi - dd_[i * KD + c] * ddv + ee[i * KD + c] * de;
+      }
+    }
+  __syncthreads();
+  if (threadIdx.x < KD) {
+    const int c = threadIdx.x;
+    float acc = 0.f;
+    for (int v = 0; v < KD; ++v) acc += XC[c * KD + v] * lam[c * KD + v];
+    for (int i = BT - 1; i >= 0; --i) {
+      acc += s.dG[i][c];
+      p.g.dgS[(rowbase + i) * KD + c] = acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sources transpose: one wave per token.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
+  const int n = blockIdx.y, b = n / p.H, hh = n % p.H;
+  const int t = blockIdx.x * 4 + wave_id();
+  if (t >= p.T) return;
+  const int l = lane_id(), r = p.r, V = p.V;
+  const long long row = ((long long)n * p.Tp + t) * KD;
+  float u0, u1, k0, k1, q0, q1, e0, e1, w0, w1, v0, v1;
+  ldrow2(p.in.u, b, t, hh, p.T, r, u0, u1);
+  norm2(u0, u1);
+  ldrow2(p.in.k, b, t, hh, p.T, r, k0, k1);
+  norm2(k0, k1);
+  ldrow2(p.in.q, b, t, hh, p.T, r, q0, q1);
+  const float rq = norm2(q0, q1);
+  ldrow2(p.in.erase_raw, b, t, hh, p.T, r, e0, e1);
+  ldrow2(p.in.write_raw, b, t, hh, p.T, V, w0, w1);
+  ldrow2(p.in.v, b, t, hh, p.T, V, v0, v1);
+  const float d0 = p.f.delta[row + l], d1 = p.f.delta[row + l + 64];
+  const float de0 = p.g.de[row + l], de1 = p.g.de[row + l + 64];
+  const float dc0 = p.g.dchi[row + l], dc1 = p.g.dchi[row + l + 64];
+  const float dz0 = p.g.dwS[row + l], dz1 = p.g.dwS[row + l + 64];
+  const float usq = wave_sum(u0 * u0 + u1 * u1);
+  const float dsq = wave_sum(d0 * d0 + d1 * d1);
+  const float N = sqrtf(RHO * RHO + usq * dsq);
+  const float sc = RHO / N;
+  const float p0 = sc * d0, p1 = sc * d1;
+  const float den = 1.f + wave_sum(p0 * u0 + p1 * u1);
+  const float se0 = 1.f / (1.f + __expf(-e0)), se1 = 1.f / (1.f + __expf(-e1));
+  const float sw0 = 1.f / (1.f + __expf(-w0)), sw1 = 1.f / (1.f + __expf(-w1));
+  const float b0 = se0 * k0, b1 = se1 * k1;
+  const float sb = wave_sum(u0 * b0 + u1 * b1) / den;
+  const float sq = wave_sum(u0 * q0 + u1 * q1) / den;
+  // z = sigmoid(wr) v
+  const float dv0 = sw0 * dz0, dv1 = sw1 * dz1;
+  const float dwr0 = dz0 * v0 * sw0 * (1.f - sw0), dwr1 = dz1 * v1 * sw1 * (1.f - sw1);
+  // e = b - phi sb ; chi = q - phi sq
+  const float dsb = -wave_sum(p0 * de0 + p1 * de1);
+  const float dsq_ = -wave_sum(p0 * dc0 + p1 * dc1);
+  const float dub = dsb / den, duq = dsq_ / den;
+  const float dden = -(dsb * sb + dsq_ * sq) / den;
+  float dph0 = -sb * de0 - sq * dc0 + dden * u0, dph1 = -sb * de1 - sq * dc1 + dden * u1;
+  float duh0 = dub * b0 + duq * q0 + dden * p0, duh1 = dub * b1 + duq * q1 + dden * p1;
+  const float db0 = de0 + dub * u0, db1 = de1 + dub * u1;
+  const float dqh0 = dc0 + duq * u0, dqh1 = dc1 + duq * u1;
+  const float dkh0 = db0 * se0, dkh1 = db1 * se1;
+  const float der0 = db0 * k0 * se0 * (1.f - se0), der1 = db1 * k1 * se1 * (1.f - se1);
+  // phi = rho delta / N,  N^2 = rho^2 + usq dsq
+  const float ds = wave_sum(dph0 * d0 + dph1 * d1);
+  float ddl0 = sc * dph0, ddl1 = sc * dph1;
+  const float dN = -RHO * ds / (N * N);
+  const float dN2 = dN / (2.f * N);
+  duh0 += 2.f * dN2 * dsq * u0;
+  duh1 += 2.f * dN2 * dsq * u1;
+  ddl0 += 2.f * dN2 * usq * d0;
+  ddl1 += 2.f * dN2 * usq * d1;
+  // q L2 norm transpose
+  const float qd = wave_sum(dqh0 * q0 + dqh1 * q1);
+  const float dq0 = (dqh0 - qd * q0) * rq, dq1 = (dqh1 - qd * q1) * rq;
+  const long long tok = ((long long)b * p.T + t) * p.H + hh;
+  if (l < r) {
+    p.dq[tok * r + l] = f2bf(dq0);
+    p.der[tok * r + l] = f2bf(der0);
+  }
+  if (l + 64 < r) {
+    p.dq[tok * r + l + 64] = f2bf(dq1);
+    p.der[tok * r + l + 64] = f2bf(der1);
+  }
+  if (l < V) {
+    p.dv[tok * V + l] = f2bf(dv0);
+    p.dwr[tok * V + l] = f2bf(dwr0);
+  }
+  if (l + 64 < V) {
+    p.dv[tok * V + l + 64] = f2bf(dv1);
+    p.dwr[tok * V + l + 64] = f2bf(dwr1);
+  }
+  const float dd0 = p.g.dd[row + l], dd1 = p.g.dd[row + l + 64];
+  p.g.ddelta[row + l] = l < r ? ddl0 : 0.f;
+  p.g.ddelta[row + l + 64] = l + 64 < r ? ddl1 : 0.f;
+  p.g.du_src[row + l] = duh0;
+  p.g.du_src[row + l + 64] = duh1;
+  p.g.dk_src[row + l] = dkh0 + dd0;
+  p.g.dk_src[row + l + 64] = dkh1 + dd1;
+}
+
+// ---------------------------------------------------------------------------
+// C predictor
+// ---------------------------------------------------------------------------
+struct BprepCSmem {
+  ChunkDecay cd;
+  float A[BT * LS];
+  float P[BT * LS];
+  float N[BT * LS];
+  float Uh[BT][GS];
+  float Kh[BT][GS];
+  float gam[BT];
+};
+
+__global__ __launch_bounds__(NTHREADS) void k_bprep_c(BwdParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  BprepCSmem& s = *reinterpret_cast<BprepCSmem*>(smem_raw);
+  const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
+  const ChunkDecay& cd = s.cd;
+  const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
+  const int w = wave_id(), l = lane_id();
+  for (int i = w; i < BT; i += 4) {
+    const int t = t0 + i;
+    float x0, x1;
+    ldrow2(p.in.u, b, t, hh, p.T, p.r, x0, x1);
+    norm2(x0, x1);
+    s.Uh[i][l] = x0;
+    s.Uh[i][l + 64] = x1;
+    ldrow2(p.in.k, b, t, hh, p.T, p.r, x0, x1);
+    norm2(x0, x1);
+    s.Kh[i][l] = x0;
+    s.Kh[i][l + 64] = x1;
+    if (l == 0)
+      s.gam[i] = t < p.T ? ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                                          (long long)t * p.in.gamma.st +
+                                                          (long long)hh * p.in.gamma.sh]
+                         : 0.f;
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS)
+    s.A[(idx / BT) * LS + idx % BT] = p.f.Ac[cidx * BT * BT + idx];
+  __syncthreads();
+  const float* ddp = p.g.dd + rowbase * KD;
+  // P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic}, i <= l
+  decayed_gram<false>(
+      cd, [&](int i, int c) { return ddp[i * KD + c]; }, [&](int j, int c) { return s.Uh[j][c]; },
+      false, s.P);
+  mat64_mul(s.P, s.A, s.N);
+  __syncthreads();
+  const float* ddl = p.g.ddelta + rowbase * KD;
+  const float* Kt = p.f.Kc + cidx * KD * BT;
+  for (int cb = 2 * w; cb < 2 * w + 2; ++cb)
+    for (int Jb = 0; Jb < NB; ++Jb) {
+      // dU_j = sum_i A_ij ddelta_i + sum_l N_lj k_l ;  Wk_j = sum_i A_ij K^_i
+      f4 du = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
+                      [&](int k, int nn) { return ddl[k * KD + cb * 16 + nn]; }, BT, zero4());
+      du = mma_k32([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; },
+                   [&](int k, int nn) { return s.Kh[k][cb * 16 + nn]; }, BT, du);
+      f4 wk = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
+                      [&](int k, int nn) { return Kt[(long long)(cb * 16 + nn) * BT + k]; }, BT,
+                      zero4());
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const long long row = rowbase + Jb * BS + out_row(e);
+        const int c = cb * 16 + out_col();
+        p.g.dU[row * KD + c] = du[e];
+        p.g.Wk[row * KD + c] = wk[e];
+      }
+    }
+  for (int idx = threadIdx.x; idx < BT * KD; idx += NTHREADS) {
+    const int i = idx / KD, c = idx % KD;
+    const long long o = (rowbase + i) * KD + c;
+    p.g.At1[o] = ddp[i * KD + c] * __expf(cd.G[i][c]);
+    p.g.B1[o] = s.Kh[i][c];
+    p.g.Ant[o] = -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c));
+  }
+}
+
+struct GradCSmem {
+  ChunkDecay cd;
+  float M1[BT * LS];
+  float M2[BT * LS];
+  float M3[BT * LS];
+  float dG[BT][GS];
+  float Uh[BT][GS];
+  float gam[BT];
+};
+
+__global__ __launch_bounds__(NTHREADS) void k_grad_c(BwdParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  GradCSmem& s = *reinterpret_cast<GradCSmem*>(smem_raw);
+  const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
+  const ChunkDecay& cd = s.cd;
+  const long long rowbase = (long long)n * p.Tp + t0;
+  const long long sidx = (long long)n * (p.NT + 1) + ch;
+  const int w = wave_id(), l = lane_id();
+  for (int i = w; i < BT; i += 4) {
+    const int t = t0 + i;
+    float x0, x1;
+    ldrow2(p.in.u, b, t, hh, p.T, p.r, x0, x1);
+    norm2(x0, x1);
+    s.Uh[i][l] = x0;
+    s.Uh[i][l + 64] = x1;
+    if (l == 0)
+      s.gam[i] = t < p.T ? ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                                          (long long)t * p.in.gamma.st +
+                                                          (long long)hh * p.in.gamma.sh]
+                         : 0.f;
+  }
+  __syncthreads();
+  const float* dw = p.g.dwC + rowbase * KD;
+  const float* wv = p.f.delta + rowbase * KD;
+  const float* ddp = p.g.dd + rowbase * KD;   // cotangent of the C-op output
+  const float* kh = p.g.B1 + rowbase * KD;    // normalised keys
+  const float* dprim = p.f.d + rowbase * KD;  // d = k + output
+  const float* X0 = p.f.Xc + sidx * KD * KD;
+  const float* XC = X0 + KD * KD;
+  const float* lam = p.g.Lc + sidx * KD * KD;
+  plain_pair([&](int i, int c) { return dw[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
+             true, s.M1);
+  plain_pair([&](int i, int c) { return kh[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
+             false, s.M2);
+  __syncthreads();
+  decayed_gram<false>(
+      cd, [&](int i, int c) { return ddp[i * KD + c]; }, [&](int j, int c) { return s.Uh[j][c]; },
+      false, s.M3);
+  auto U = [&](int j, int c) { return s.Uh[j][c]; };
+  auto Xg = [&](int j, int c) { return s.gam[j] * s.Uh[j][c]; };
+  auto DO = [&](int j, int c) { return ddp[j * KD + c]; };
+  for (int cb = 2 * w; cb < 2 * w + 2; ++cb)
+    for (int I = 0; I < NB; ++I) {
+      f4 a = mma_k32([&](int m, int v) { return dw[(I * BS + m) * KD + v]; },
+                     [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
+      f4 ap = decayed_apply_tile<true>(cd, s.M1, U, I, cb);
+      f4 kl = mma_k32([&](int m, int v) { return wv[(I * BS + m) * KD + v]; },
+                      [&](int v, int nn) { return lam[(cb * 16 + nn) * KD + v]; }, KD, zero4());
+      f4 k2 = decayed_apply_t_tile<false>(cd, s.M2, DO, I, cb);
+      f4 k3 = decayed_apply_t_tile<true>(cd, s.M1, Xg, I, cb);
+      f4 dq = mma_k32([&](int m, int aa) {
+                        const int i = I * BS + m;
+                        return ddp[i * KD + aa] * __expf(cd.G[i][aa]);
+                      },
+                      [&](int aa, int nn) { return X0[aa * KD + cb * 16 + nn]; }, KD, zero4());
+      dq = mma_k32([&](int m, int j) { return s.M3[(I * BS + m) * LS + j]; },
+                   [&](int j, int nn) { return wv[j * KD + cb * 16 + nn]; }, (I < 2 ? 32 : 64), dq);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + out_row(e), c = cb * 16 + out_col();
+        const float dx = -(__expf(gx_excl(cd, i, c)) * a[e] + ap[e]);
+        const float dk = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[e] + k2[e] - k3[e];
+        const long long o = (rowbase + i) * KD + c;
+        p.g.dxC[o] = dx;
+        p.g.dkC[o] = dk;
+        p.g.dqC[o] = dq[e];
+        const float outv = dprim[i * KD + c] - kh[i * KD + c];
+        s.dG[i][c] = outv * ddp[i * KD + c] - s.Uh[i][c] * dk;
+      }
+    }
+  __syncthreads();
+  if (threadIdx.x < KD) {
+    const int c = threadIdx.x;
+    float acc = 0.f;
+    for (int v = 0; v < KD; ++v) acc += XC[c * KD + v] * lam[c * KD + v];
+    for (int i = BT - 1; i >= 0; --i) {
+      acc += s.dG[i][c];
+      if (i + 1 < BT) acc += s.gam[i + 1] * s.Uh[i + 1][c] * p.g.dxC[(rowbase + i + 1) * KD + c];
+      p.g.dgC[(rowbase + i) * KD + c] = acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Final closure: u, k, h, gamma, log-decay.  One wave per token.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTHREADS) void k_final(BwdParams p) {
+  const int n = blockIdx.y, b = n / p.H, hh = n % p.H;
+  const int t = blockIdx.x * 4 + wave_id();
+  if (t >= p.T) return;
+  const int l = lane_id(), r = p.r;
+  const long long row = ((long long)n * p.Tp + t) * KD;
+  float u0, u1, k0, k1, h0, h1;
+  ldrow2(p.in.u, b, t, hh, p.T, r, u0, u1);
+  const float ru = norm2(u0, u1);
+  ldrow2(p.in.k, b, t, hh, p.T, r, k0, k1);
+  const float rk = norm2(k0, k1);
+  ldrow2(p.in.h, b, t, hh, p.T, r, h0, h1);
+  const float gm = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                                   (long long)t * p.in.gamma.st +
+                                                   (long long)hh * p.in.gamma.sh];
+  const float dx0 = p.g.dxC[row + l], dx1 = p.g.dxC[row + l + 64];
+  const float dv0 = p.g.dwC[row + l], dv1 = p.g.dwC[row + l + 64];
+  const float du0 = p.g.du_src[row + l] + p.g.dkC[row + l] + gm * dx0;
+  const float du1 = p.g.du_src[row + l + 64] + p.g.dkC[row + l + 64] + gm * dx1;
+  const float dk0 = p.g.dk_src[row + l] + p.g.dqC[row + l];
+  const float dk1 = p.g.dk_src[row + l + 64] + p.g.dqC[row + l + 64];
+  const float dgam = wave_sum(u0 * dx0 + u1 * dx1 + h0 * dv0 + h1 * dv1);
+  const float ud = wave_sum(du0 * u0 + du1 * u1);
+  const float kd = wave_sum(dk0 * k0 + dk1 * k1);
+  const long long tok = ((long long)b * p.T + t) * p.H + hh;
+  if (l < r) {
+    p.du[tok * r + l] = f2bf((du0 - ud * u0) * ru);
+    p.dk[tok * r + l] = f2bf((dk0 - kd * k0) * rk);
+    p.dh[tok * r + l] = f2bf(gm * dv0);
+    p.dg[tok * r + l] = p.g.dgS[row + l] + p.g.dgC[row + l];
+  }
+  if (l + 64 < r) {
+    p.du[tok * r + l + 64] = f2bf((du1 - ud * u1) * ru);
+    p.dk[tok * r + l + 64] = f2bf((dk1 - kd * k1) * rk);
+    p.dh[tok * r + l + 64] = f2bf(gm * dv1);
+    p.dg[tok * r + l + 64] = p.g.dgS[row + l + 64] + p.g.dgC[row + l + 64];
+  }
+  if (l == 0) p.dgam[tok] = dgam;
+}
+
+// ---------------------------------------------------------------------------
+int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void* dout,
+               const float* dC_T, const float* dS_T, void* du, void* dh, void* dq, void* dk,
+               void* dv, void* derase, void* dwrite, float* dlog_decay, float* dgamma,
+               float* dC0, float* dS0, hipStream_t st) {
+  const int n = in->B * in->H, NT = (in->T + BT - 1) / BT, Tp = NT * BT;
+  BwdParams p{};
+  p.in = *in;
+  p.H = in->H; p.T = in->T; p.r = in->r; p.V = in->V; p.NT = NT; p.Tp = Tp;
+  p.f = fw;
+  p.g = bw;
+  p.dout = (const __bf16*)dout;
+  p.du = (__bf16*)du; p.dh = (__bf16*)dh; p.dq = (__bf16*)dq; p.dk = (__bf16*)dk;
+  p.dv = (__bf16*)dv; p.der = (__bf16*)derase; p.dwr = (__bf16*)dwrite;
+  p.dg = dlog_decay; p.dgam = dgamma;
+  (void)hipFuncSetAttribute((const void*)k_bprep_s, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(BprepSSmem));
+  (void)hipFuncSetAttribute((const void*)k_grad_s, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(GradSmem));
+  (void)hipFuncSetAttribute((const void*)k_bprep_c, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(BprepCSmem));
+  (void)hipFuncSetAttribute((const void*)k_grad_c, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(GradCSmem));
+  const dim3 chunks(NT, n), rows((Tp + 3) / 4, n), blk(NTHREADS);
+  // S memory
+  SD_LAUNCH("k_bprep_s", k_bprep_s, chunks, blk, sizeof(BprepSSmem), st, p);
+  StateParams ss{};
+  ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
+  ss.rev = 1; ss.kt_token_major = 1;
+  ss.Wneg = bw.Wk; ss.U = bw.dU; ss.Kt = bw.Ant; ss.Gam = fw.Gam;
+  ss.At1 = fw.Qs; ss.B1 = bw.B1;
+  ss.Xs = bw.Ls; ss.wout = bw.dwS;
+  ss.init = dS_T; ss.init_transposed = 0;
+  ss.fin = dS0; ss.fin_transposed = 0;
+  launch_state("state_s_bwd", ss, false, n, st);
+  SD_LAUNCH("k_grad_s", k_grad_s, chunks, blk, sizeof(GradSmem), st, p);
+  SD_LAUNCH("k_src_bwd", k_src_bwd, rows, blk, 0, st, p);
+  // C predictor
+  SD_LAUNCH("k_bprep_c", k_bprep_c, chunks, blk, sizeof(BprepCSmem), st, p);
+  StateParams sc{};
+  sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
+  sc.rev = 1; sc.kt_token_major = 1;
+  sc.Wneg = bw.Wk; sc.U = bw.dU; sc.Kt = bw.Ant; sc.Gam = fw.Gam;
+  sc.At1 = bw.At1; sc.B1 = bw.B1;
+  sc.Xs = bw.Lc; sc.wout = bw.dwC;
+  sc.init = dC_T; sc.init_transposed = 1;
+  sc.fin = dC0; sc.fin_transposed = 1;
+  launch_state("state_c_bwd", sc, false, n, st);
+  SD_LAUNCH("k_grad_c", k_grad_c, chunks, blk, sizeof(GradCSmem), st, p);
+  SD_LAUNCH("k_final", k_final, rows, blk, 0, st, p);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+}  // namespace sd

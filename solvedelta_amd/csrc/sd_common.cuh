@@ -274,3 +274,93 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
 }
 
 }  // namespace sd
+
+namespace sd {
+
+// Tile (rows of block I, columns cb*16..cb*16+15) of
+//   R_ic = sum_{j<=i} M_ij Y_jc exp(Gx_ic - G_jc),
+// M lower-triangular (64 x LS, zero where the pair is excluded).
+template <bool EXCL, class FY>
+__device__ f4 decayed_apply_tile(const ChunkDecay& cd, const float* M, FY Y, int I, int cb) {
+  f4 tot = zero4();
+  for (int J = 0; J <= I; ++J) {
+    f4 a2 = mma_k16([&](int m, int k) { return M[(I * BS + m) * LS + J * BS + k]; },
+                    [&](int k, int nn) {
+                      const int c = cb * 16 + nn, j = J * BS + k;
+                      return cd.wild[J][c] ? 0.f : Y(j, c) * __expf(cd.R[J][c] - cd.G[j][c]);
+                    },
+                    zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + out_row(e), c = cb * 16 + out_col();
+      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+      float add;
+      if (cd.wild[J][c]) {
+        add = 0.f;
+        for (int j = J * BS; j < J * BS + BS; ++j)
+          add += M[i * LS + j] * Y(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      } else {
+        add = __expf(gx - cd.R[J][c]) * a2[e];
+      }
+      tot[e] += add;
+    }
+  }
+  return tot;
+}
+
+// Tile (rows of block Jb, columns cb*16..) of
+//   R_jc = sum_{i>=j} M_ij X_ic exp(Gx_ic - G_jc),  M lower-triangular.
+template <bool EXCL, class FX>
+__device__ f4 decayed_apply_t_tile(const ChunkDecay& cd, const float* M, FX X, int Jb, int cb) {
+  f4 acc = zero4();
+  for (int I = Jb; I < NB; ++I) {
+    acc = mma_k16([&](int m, int k) { return M[(I * BS + k) * LS + Jb * BS + m]; },
+                  [&](int k, int nn) {
+                    const int c = cb * 16 + nn, i = I * BS + k;
+                    const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+                    return X(i, c) * __expf(gx - cd.R[Jb][c]);
+                  },
+                  acc);
+  }
+  f4 res;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int j = Jb * BS + out_row(e), c = cb * 16 + out_col();
+    if (cd.wild[Jb][c]) {
+      float s = 0.f;
+      for (int i = j; i < BT; ++i) {
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        s += M[i * LS + j] * X(i, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      }
+      res[e] = s;
+    } else {
+      res[e] = __expf(cd.R[Jb][c] - cd.G[j][c]) * acc[e];
+    }
+  }
+  return res;
+}
+
+// Plain (undecayed) pair M_ij = sum_c X_ic Y_jc over c < KD for the 10 lower
+// block pairs, masked strictly (j < i) or inclusively (j <= i); upper blocks 0.
+template <class FX, class FY>
+__device__ void plain_pair(FX X, FY Y, bool strict, float* M) {
+  const int w = wave_id();
+  for (int p = w; p < 10; p += 4) {
+    int I = 0, J = p;
+    while (J > I) { J -= I + 1; ++I; }
+    f4 acc = mma_k32([&](int m, int c) { return X(I * BS + m, c); },
+                     [&](int c, int nn) { return Y(J * BS + nn, c); }, KD, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + out_row(e), j = J * BS + out_col();
+      const bool keep = strict ? (j < i) : (j <= i);
+      M[i * LS + j] = keep ? acc[e] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) M[i * LS + j] = 0.f;
+  }
+}
+
+}  // namespace sd

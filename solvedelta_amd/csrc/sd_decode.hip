@@ -147,7 +147,7 @@ __global__ __launch_bounds__(NTHREADS) void k_decode(sd_inputs in, __bf16* out, 
 int launch_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, hipStream_t st) {
   (void)hipFuncSetAttribute((const void*)k_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)sizeof(DecodeSmem));
-  hipLaunchKernelGGL(k_decode, dim3(in->B * in->H), dim3(NTHREADS), sizeof(DecodeSmem), st, *in,
+  SD_LAUNCH("k_decode", k_decode, dim3(in->B * in->H), dim3(NTHREADS), sizeof(DecodeSmem), st, *in,
                      (__bf16*)out, C_T, S_T);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }

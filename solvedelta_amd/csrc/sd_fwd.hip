@@ -90,6 +90,8 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_c(FwdParams p) {
       cd, [&](int i, int c) { return s.gam[i] * s.Uh[i][c]; },
       [&](int j, int c) { return s.Uh[j][c]; }, true, s.M);
   unit_lower_inverse(s.M, s.tmp);
+  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS)
+    p.Ac[((long long)n * p.NT + ch) * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
   // W = A diag(gamma) (u e^{Gexcl}),  U = A diag(gamma) h
   const long long rowbase = (long long)n * p.Tp + t0;
   for (int cb = 2 * w; cb < 2 * w + 2; ++cb) {
@@ -134,6 +136,7 @@ struct StateSmem {
 
 template <bool COL_OUT>
 __global__ __launch_bounds__(NTHREADS) void k_state(StateParams p) {
+  const int NS = p.NT + 1;  // state slots per sequence
   __shared__ StateSmem s;
   const int tile = blockIdx.x, n = blockIdx.y;
   const int w = wave_id();
@@ -149,15 +152,17 @@ __global__ __launch_bounds__(NTHREADS) void k_state(StateParams p) {
                               : p.init[(long long)n * p.rows * p.cols + (long long)row * p.cols + col];
       X[q][e] = x;
     }
-  for (int ch = 0; ch < p.NT; ++ch) {
+  for (int it = 0; it < p.NT; ++it) {
+    const int ch = p.rev ? p.NT - 1 - it : it;
     const long long cidx = (long long)n * p.NT + ch;
+    const long long sidx = (long long)n * NS + ch;
     const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
     // save X0 and stage it transposed ([col][row]) for the MFMA B operand
     for (int q = 0; q < 2; ++q)
       for (int e = 0; e < 4; ++e) {
         const int row = (2 * w + q) * 16 + out_row(e);
         const float x = X[q][e];
-        if (p.Xs) p.Xs[cidx * KD * KD + (long long)row * KD + col] = x;
+        if (p.Xs) p.Xs[sidx * KD * KD + (long long)row * KD + col] = x;
         s.Xt[out_col()][row] = x;
       }
     __syncthreads();
@@ -191,18 +196,37 @@ __global__ __launch_bounds__(NTHREADS) void k_state(StateParams p) {
           p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + col] = f2bf(o[e]);
       }
     }
-    // X = Gamma X + Kt w
+    // X = Gamma X + Kt w (+ At1 B1)
     const float* gam = p.Gam + cidx * KD;
-    const float* Kt = p.Kt + cidx * KD * BT;
     for (int q = 0; q < 2; ++q) {
       const int rb = 2 * w + q;
       for (int e = 0; e < 4; ++e) X[q][e] *= gam[rb * 16 + out_row(e)];
-      X[q] = mma_k32([&](int m, int k) { return Kt[(long long)(rb * 16 + m) * BT + k]; },
-                     [&](int k, int nn) { return s.wt[nn][k]; }, BT, X[q]);
+      if (p.kt_token_major) {
+        const float* Kt = p.Kt + rowbase * KD;
+        X[q] = mma_k32([&](int m, int k) { return Kt[(long long)k * KD + rb * 16 + m]; },
+                       [&](int k, int nn) { return s.wt[nn][k]; }, BT, X[q]);
+      } else {
+        const float* Kt = p.Kt + cidx * KD * BT;
+        X[q] = mma_k32([&](int m, int k) { return Kt[(long long)(rb * 16 + m) * BT + k]; },
+                       [&](int k, int nn) { return s.wt[nn][k]; }, BT, X[q]);
+      }
+      if (p.At1) {
+        const float* A1 = p.At1 + rowbase * KD;
+        const float* B1 = p.B1 + rowbase * KD;
+        X[q] = mma_k32([&](int m, int k) { return A1[(long long)k * KD + rb * 16 + m]; },
+                       [&](int k, int nn) { return B1[(long long)k * KD + tile * 16 + nn]; }, BT,
+                       X[q]);
+      }
     }
     __syncthreads();
   }
-  // final state
+  // final state (also kept as slot NT for the backward)
+  if (p.Xs && !p.rev)
+    for (int q = 0; q < 2; ++q)
+      for (int e = 0; e < 4; ++e) {
+        const int row = (2 * w + q) * 16 + out_row(e);
+        p.Xs[((long long)n * NS + p.NT) * KD * KD + (long long)row * KD + col] = X[q][e];
+      }
   if (p.fin) {
     for (int q = 0; q < 2; ++q)
       for (int e = 0; e < 4; ++e) {
@@ -220,6 +244,14 @@ __global__ __launch_bounds__(NTHREADS) void k_state(StateParams p) {
 
 template __global__ void k_state<false>(StateParams);
 template __global__ void k_state<true>(StateParams);
+
+void launch_state(const char* name, const StateParams& sp, bool col_out, int nseq,
+                  hipStream_t st) {
+  if (col_out)
+    SD_LAUNCH(name, k_state<true>, dim3(KD / 16, nseq), dim3(NTHREADS), 0, st, sp);
+  else
+    SD_LAUNCH(name, k_state<false>, dim3(KD / 16, nseq), dim3(NTHREADS), 0, st, sp);
+}
 
 // ---------------------------------------------------------------------------
 // k_prep_s: primal d, dual sources, S-memory WY panels
@@ -280,7 +312,7 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
   }
   __syncthreads();
   // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}
-  const float* X0 = p.Xc + cidx * KD * KD;
+  const float* X0 = p.Xc + ((long long)n * (p.NT + 1) + ch) * KD * KD;
   for (int q = 0; q < 2; ++q) {
     const int cb = 2 * w + q;
     for (int I = 0; I < NB; ++I) {
@@ -341,6 +373,10 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
     s.Pa[i][l + 64] = in1 ? b1 - p1 * ub : 0.f;
     s.Pb[i][l] = in0 ? q0 - p0 * uq : 0.f;
     s.Pb[i][l + 64] = in1 ? q1 - p1 * uq : 0.f;
+    p.e[(rowbase + i) * KD + l] = s.Pa[i][l];
+    p.e[(rowbase + i) * KD + l + 64] = s.Pa[i][l + 64];
+    p.chi[(rowbase + i) * KD + l] = s.Pb[i][l];
+    p.chi[(rowbase + i) * KD + l + 64] = s.Pb[i][l + 64];
   }
   __syncthreads();
   // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i
@@ -363,6 +399,8 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
       cd, [&](int i, int c) { return s.Pa[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
       true, s.M);
   unit_lower_inverse(s.M, &s.Pc[0][0]);
+  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS)
+    p.As[cidx * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
   // W = A (e e^G), U = A z with z = sigmoid(write_raw) v read from the inputs
   for (int cb = 2 * w; cb < 2 * w + 2; ++cb) {
     for (int I = 0; I < NB; ++I) {
@@ -405,6 +443,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   fp.in = *in;
   fp.H = in->H; fp.T = in->T; fp.r = in->r; fp.V = in->V; fp.NT = NT; fp.Tp = Tp;
   fp.Xc = w.Xc; fp.delta = w.delta; fp.d = w.d;
+  fp.Ac = w.Ac; fp.As = w.As; fp.e = w.e; fp.chi = w.chi;
   fp.Wc = w.Wc; fp.Uc = w.Uc; fp.Kc = w.Kc; fp.Gam = w.Gam;
   fp.Ws = w.Ws; fp.Us = w.Us; fp.Ks = w.Ks; fp.Qs = w.Qs; fp.Ps = w.Ps;
 
@@ -412,7 +451,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
                             (int)prep_c_smem());
   (void)hipFuncSetAttribute((const void*)k_prep_s, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)prep_s_smem());
-  hipLaunchKernelGGL(k_prep_c, dim3(NT, n), dim3(256), prep_c_smem(), st, fp);
+  SD_LAUNCH("k_prep_c", k_prep_c, dim3(NT, n), dim3(256), prep_c_smem(), st, fp);
 
   StateParams sc{};
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
@@ -420,9 +459,9 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   sc.Xs = w.Xc; sc.wout = w.delta;
   sc.init = in->C0; sc.init_transposed = 1;
   sc.fin = C_T; sc.fin_transposed = 1;
-  hipLaunchKernelGGL(k_state<false>, dim3(KD / 16, n), dim3(256), 0, st, sc);
+  launch_state("state_c_fwd", sc, false, n, st);
 
-  hipLaunchKernelGGL(k_prep_s, dim3(NT, n), dim3(256), prep_s_smem(), st, fp);
+  SD_LAUNCH("k_prep_s", k_prep_s, dim3(NT, n), dim3(256), prep_s_smem(), st, fp);
 
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
@@ -430,7 +469,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   ss.Xs = w.Xs; ss.wout = w.wS; ss.out = (__bf16*)out;
   ss.init = in->S0; ss.init_transposed = 0;
   ss.fin = S_T; ss.fin_transposed = 0;
-  hipLaunchKernelGGL(k_state<true>, dim3(KD / 16, n), dim3(256), 0, st, ss);
+  launch_state("state_s_fwd", ss, true, n, st);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 

@@ -12,8 +12,12 @@ namespace sd {
 // [n][NT][...] (per-chunk), n = B*H, Tp = NT*64.
 struct FwdWs {
   // kept for the backward
-  float* Xc;     // C-op chunk-entering states X = C^T     [n][NT][128][128]
-  float* Xs;     // S-op chunk-entering states              [n][NT][128][128]
+  float* Xc;     // C-op chunk-entering states X = C^T     [n][NT+1][128][128] (slot NT = final)
+  float* Xs;     // S-op chunk-entering states              [n][NT+1][128][128]
+  float* Ac;     // C-op (I+L)^-1 per chunk                 [n][NT][64][64]
+  float* As;     // S-op (I+L)^-1 per chunk                 [n][NT][64][64]
+  float* e;      // dual erase source e                     [n][Tp][128]
+  float* chi;    // dual query chi                          [n][Tp][128]
   float* delta;  // predictor write delta (C-op w)          [n][Tp][128]
   float* d;      // primal address d = k + C^T k            [n][Tp][128]
   float* wS;     // S-op w = z - S~^T e                     [n][Tp][128]
@@ -25,25 +29,54 @@ struct FwdWs {
 struct FwdParams {
   sd_inputs in;
   int H, T, r, V, NT, Tp;
-  float *Xc, *delta, *d;
+  float *Xc, *delta, *d, *Ac, *As, *e, *chi;
   float* Wc; float* Uc; float* Kc; float* Gam;
   float* Ws; float* Us; float* Ks; float* Qs; float* Ps;
 };
 
+// Sequential chunk pass, forward (state X) or reverse (cotangent lambda):
+//   slot[ch] = X;  w = U + Wneg X;  X = Gamma X + Kt w (+ At1 B1)
+// Kt is chunk-transposed [128][64] (kt_token_major = 0) or a token-major panel.
 struct StateParams {
-  int H, T, NT, Tp, rows, cols;
+  int H, T, NT, Tp, rows, cols, rev, kt_token_major;
   const float* Wneg; const float* U; const float* Kt; const float* Gam;
+  const float* At1; const float* B1;  // optional injection (token-major panels)
   const float* Q; const float* P;  // output operands (COL_OUT)
   float* Xs; float* wout; __bf16* out;
   const float* init; int init_transposed;
   float* fin; int fin_transposed;
 };
 
+void prof_begin(const char* name, hipStream_t st);
+void prof_end(hipStream_t st);
+#define SD_LAUNCH(name, kern, grid, block, smem, st, ...)                 \
+  do {                                                                   \
+    ::sd::prof_begin(name, st);                                          \
+    hipLaunchKernelGGL(kern, grid, block, smem, st, __VA_ARGS__);        \
+    ::sd::prof_end(st);                                                  \
+  } while (0)
+
+void launch_state(const char* name, const StateParams& sp, bool col_out, int nseq,
+                  hipStream_t st);
 size_t prep_c_smem();
 size_t prep_s_smem();
 
 int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const FwdWs& w,
                hipStream_t st);
+struct BwdWs {
+  float* Lc;   // C-op chunk-end cotangents                [n][NT+1][128][128]
+  float* Ls;   // S-op chunk-end cotangents
+  float* dU; float* Wk; float* At1; float* B1; float* Ant;  // reverse-pass panels (reused)
+  float* dwS; float* dwC;          // dw of each op           [n][Tp][128]
+  float* de; float* dchi; float* dd; float* dgS;
+  float* ddelta; float* du_src; float* dk_src;
+  float* dkC; float* dxC; float* dqC; float* dgC;
+};
+
+int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void* dout,
+               const float* dC_T, const float* dS_T, void* du, void* dh, void* dq, void* dk,
+               void* dv, void* derase, void* dwrite, float* dlog_decay, float* dgamma,
+               float* dC0, float* dS0, hipStream_t st);
 int launch_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, hipStream_t st);
 
 }  // namespace sd

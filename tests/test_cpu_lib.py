@@ -1,0 +1,80 @@
+"""CPU-side checks of the native boundary: the C-ABI library loads and exports
+every symbol include/solvedelta.h declares, the host-side validation raises the
+reference's exception types, and the C token loop agrees with the FP64 oracle."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "solvedelta.h")).read()
+    return sorted(set(re.findall(r"\b(sd_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from solvedelta_amd import _lib
+    lib = _lib.load()
+    names = _declared()
+    assert "sd_fwd" in names and "sd_bwd" in names and "sd_decode" in names
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.EXPORTS, name
+    assert lib.sd_version().startswith(b"solvedelta_amd")
+
+
+def test_workspace_queries_and_argument_rejection():
+    from solvedelta_amd import _lib
+    lib = _lib.load()
+    small = lib.sd_fwd_workspace_bytes(1, 64, 1, 16, 16)
+    big = lib.sd_fwd_workspace_bytes(4, 2048, 8, 128, 128)
+    assert 0 < small < big
+    assert lib.sd_bwd_workspace_bytes(4, 2048, 8, 128, 128) > 0
+    ins = _lib.SdInputs()
+    ins.B, ins.T, ins.H, ins.r, ins.V = 1, 4, 1, 200, 16  # r > 128
+    assert lib.sd_fwd(ctypes.byref(ins), None, None, None, None, 0, None) == _lib.SD_ERR_SHAPE
+    ins.r = 16  # null operand pointers
+    assert lib.sd_fwd(ctypes.byref(ins), None, None, None, None, 0, None) == _lib.SD_ERR_ARG
+
+
+def test_operator_rejects_like_the_reference():
+    from solvedelta_amd import solvedelta_native
+    x = torch.zeros(1, 4, 1, 8, dtype=torch.bfloat16)
+    k = torch.zeros(1, 4, 1, 1, 8, dtype=torch.bfloat16)
+    g = torch.zeros(1, 4, 1, 8)
+    gm = torch.zeros(1)
+    with pytest.raises(TypeError):  # CPU tensors: ops/operator.py:28-29
+        solvedelta_native(x, x, x, k, k, g, k, k, gm)
+
+
+def test_c_token_loop_matches_oracle():
+    from oracle.sd_oracle import OracleState, solvedelta_oracle_raw
+    so = os.path.join(ROOT, "oracle", "libsd_token_loop.so")
+    if not os.path.exists(so):
+        import subprocess
+        subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True)
+    lib = ctypes.CDLL(so)
+    B, T, H, r, V = 2, 9, 2, 8, 6
+    g = torch.Generator().manual_seed(3)
+    n = lambda *s: torch.randn(*s, generator=g)
+    u, h, q, k = n(B, T, H, r), n(B, T, H, r), n(B, T, H, r), n(B, T, H, r)
+    v, er, wr = n(B, T, H, V), n(B, T, H, r), n(B, T, H, V)
+    gd = -torch.nn.functional.softplus(n(B, T, H, r))
+    gm = torch.full((B, T, H), 0.8)
+    C0, S0 = 0.1 * n(B, H, r, r), 0.1 * n(B, H, r, V)
+    o_ref, st = solvedelta_oracle_raw(*(x.double() for x in (u, h, q, k[:, :, :, None], v[:, :, :, None], gd,
+                                      er[:, :, :, None], wr[:, :, :, None], gm)),
+                                      initial_state=OracleState(C0.double(), S0.double()))
+    arrs = [np.ascontiguousarray(x.numpy(), dtype=np.float32) for x in (u, h, q, k, v, gd, er, wr, gm)]
+    C, S = C0.numpy().astype(np.float32).copy(), S0.numpy().astype(np.float32).copy()
+    out = np.zeros((B, T, H, V), np.float32)
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    assert lib.sd_cpu_forward_f64(B, T, H, r, V, *(ptr(a) for a in arrs), ptr(C), ptr(S), ptr(out)) == 0
+    np.testing.assert_allclose(out, o_ref.numpy(), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(C, st.predictor.numpy(), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(S, st.S.numpy(), rtol=1e-5, atol=1e-5)
