@@ -45,11 +45,13 @@ EXPORTS = {
 _lib = None
 
 
-def load(path: str = LIB_PATH) -> ctypes.CDLL:
-    """Loads the HIP library once; raises if it has not been built."""
+def load(path: str = None) -> ctypes.CDLL:
+    """Loads the HIP library once; raises if it has not been built.
+    SD_LIBRARY overrides the path (used for instrumented builds)."""
     global _lib
     if _lib is not None:
         return _lib
+    path = path or os.environ.get("SD_LIBRARY", LIB_PATH)
     if not os.path.exists(path):
         raise RuntimeError(
             f"{path} is missing: build the HIP extension first "

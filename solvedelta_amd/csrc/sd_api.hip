@@ -55,7 +55,7 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   BwdWs w;
   w.Lc = c.take<float>(states);
   w.Ls = c.take<float>(states);
-  float** panels[] = {&w.dU, &w.Wk, &w.At1, &w.B1, &w.Ant, &w.dwS, &w.dwC, &w.de, &w.dchi,
+  float** panels[] = {&w.dU, &w.Wk, &w.At1, &w.B1, &w.B1t, &w.Ant, &w.dwS, &w.dwC, &w.de, &w.dchi,
                       &w.dd, &w.dgS, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
                       &w.dgC};
   for (float** pp : panels) *pp = c.take<float>(panel);

@@ -63,8 +63,8 @@ __device__ __forceinline__ const float* gptr(const sd_inputs& in, int b, int h) 
 
 // 64x64 N = P A (both 64 x LS in LDS) -> N (64 x LS)
 __device__ void mat64_mul(const float* P, const float* A, float* N) {
-  const int I = wave_id();
-  for (int J = 0; J < NB; ++J) {
+  for (int tt = wave_id(); tt < NB * NB; tt += CW) {
+    const int I = tt / NB, J = tt % NB;
     f4 acc = mma_k32([&](int m, int k) { return P[(I * BS + m) * LS + k]; },
                      [&](int k, int nn) { return A[k * LS + J * BS + nn]; }, BT, zero4());
 #pragma unroll
@@ -82,14 +82,14 @@ struct BprepSSmem {
   float N[BT * LS];
 };
 
-__global__ __launch_bounds__(NTHREADS) void k_bprep_s(BwdParams p) {
+__global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   BprepSSmem& s = *reinterpret_cast<BprepSSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
-  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
     s.A[(idx / BT) * LS + idx % BT] = p.f.As[cidx * BT * BT + idx];
     s.P[(idx / BT) * LS + idx % BT] = p.f.Ps[cidx * BT * BT + idx];
   }
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(NTHREADS) void k_bprep_s(BwdParams p) {
   __syncthreads();
   const int w = wave_id();
   const float* Kt = p.f.Ks + cidx * KD * BT;
-  for (int cb = 2 * w; cb < 2 * w + 2; ++cb)
+  for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_l N_lj dO_l ;  Wk_j = sum_i A_ij K^_i
       f4 du = mma_k32([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; },
@@ -115,11 +115,16 @@ __global__ __launch_bounds__(NTHREADS) void k_bprep_s(BwdParams p) {
         p.g.Wk[row * KD + c] = wk[e];
       }
     }
-  for (int idx = threadIdx.x; idx < BT * KD; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
     const int i = idx / KD, c = idx % KD;
-    const long long o = (rowbase + i) * KD + c;
-    p.g.Ant[o] = -p.f.e[o] * __expf(cd.G[i][c]);
-    p.g.B1[o] = dout_at(p, b, t0 + i, hh, c);
+    p.g.B1[(rowbase + i) * KD + c] = dout_at(p, b, t0 + i, hh, c);
+  }
+  for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {  // chunk-transposed panels
+    const int c = idx / BT, i = idx % BT;
+    const long long o = (rowbase + i) * KD + c, ot = cidx * KD * BT + idx;
+    p.g.Ant[ot] = -p.f.e[o] * __expf(cd.G[i][c]);
+    p.g.At1[ot] = p.f.Qs[o];
+    p.g.B1t[ot] = dout_at(p, b, t0 + i, hh, c);
   }
 }
 
@@ -131,11 +136,13 @@ struct GradSmem {
   float dG[BT][GS];
 };
 
-__global__ __launch_bounds__(NTHREADS) void k_grad_s(BwdParams p) {
+__global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GradSmem& s = *reinterpret_cast<GradSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  SD_MARK(0, 0);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
+  SD_MARK(0, 1);
   const ChunkDecay& cd = s.cd;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
@@ -154,22 +161,30 @@ __global__ __launch_bounds__(NTHREADS) void k_grad_s(BwdParams p) {
   plain_pair([&](int i, int c) { return dO[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
              false, s.M2);
   __syncthreads();
+  SD_MARK(0, 2);
   const int w = wave_id();
   auto D = [&](int j, int c) { return dd_[j * KD + c]; };
   auto E = [&](int j, int c) { return ee[j * KD + c]; };
   auto Q = [&](int j, int c) { return chi[j * KD + c]; };
-  for (int cb = 2 * w; cb < 2 * w + 2; ++cb)
+  for (int cb = w; cb < w + 1; ++cb)
     for (int I = 0; I < NB; ++I) {
+      const bool mk = cb == 0 && I == 0;
+      if (mk) SD_MARK(0, 3);
       f4 a = mma_k32([&](int m, int v) { return dw[(I * BS + m) * KD + v]; },
                      [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
+      if (mk) SD_MARK(0, 4);
       f4 ap = decayed_apply_tile<false>(cd, s.M1, D, I, cb);
+      if (mk) SD_MARK(0, 5);
       f4 bq = mma_k32([&](int m, int v) { return dO[(I * BS + m) * KD + v]; },
                       [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
       f4 bp = decayed_apply_tile<false>(cd, s.M2, D, I, cb);
       f4 kl = mma_k32([&](int m, int v) { return wv[(I * BS + m) * KD + v]; },
                       [&](int v, int nn) { return lam[(cb * 16 + nn) * KD + v]; }, KD, zero4());
+      if (mk) SD_MARK(0, 6);
       f4 k2 = decayed_apply_t_tile<false>(cd, s.M2, Q, I, cb);
+      if (mk) SD_MARK(0, 7);
       f4 k3 = decayed_apply_t_tile<false>(cd, s.M1, E, I, cb);
+      if (mk) SD_MARK(0, 8);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + out_row(e), c = cb * 16 + out_col();
@@ -184,7 +199,9 @@ __global__ __launch_bounds__(NTHREADS) void k_grad_s(BwdParams p) {
         s.dG[i][c] = chi[i * KD + c] * dchi - dd_[i * KD + c] * ddv + ee[i * KD + c] * de;
       }
     }
+  SD_MARK(0, 9);
   __syncthreads();
+  SD_MARK(0, 10);
   if (threadIdx.x < KD) {
     const int c = threadIdx.x;
     float acc = 0.f;
@@ -194,6 +211,7 @@ __global__ __launch_bounds__(NTHREADS) void k_grad_s(BwdParams p) {
       p.g.dgS[(rowbase + i) * KD + c] = acc;
     }
   }
+  SD_MARK(0, 11);
 }
 
 // ---------------------------------------------------------------------------
@@ -295,7 +313,7 @@ struct BprepCSmem {
   float gam[BT];
 };
 
-__global__ __launch_bounds__(NTHREADS) void k_bprep_c(BwdParams p) {
+__global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   BprepCSmem& s = *reinterpret_cast<BprepCSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
@@ -303,7 +321,8 @@ __global__ __launch_bounds__(NTHREADS) void k_bprep_c(BwdParams p) {
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
   const int w = wave_id(), l = lane_id();
-  for (int i = w; i < BT; i += 4) {
+#pragma unroll
+  for (int i = w; i < BT; i += CW) {
     const int t = t0 + i;
     float x0, x1;
     ldrow2(p.in.u, b, t, hh, p.T, p.r, x0, x1);
@@ -320,7 +339,7 @@ __global__ __launch_bounds__(NTHREADS) void k_bprep_c(BwdParams p) {
                                                           (long long)hh * p.in.gamma.sh]
                          : 0.f;
   }
-  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS)
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     s.A[(idx / BT) * LS + idx % BT] = p.f.Ac[cidx * BT * BT + idx];
   __syncthreads();
   const float* ddp = p.g.dd + rowbase * KD;
@@ -332,7 +351,7 @@ __global__ __launch_bounds__(NTHREADS) void k_bprep_c(BwdParams p) {
   __syncthreads();
   const float* ddl = p.g.ddelta + rowbase * KD;
   const float* Kt = p.f.Kc + cidx * KD * BT;
-  for (int cb = 2 * w; cb < 2 * w + 2; ++cb)
+  for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_i A_ij ddelta_i + sum_l N_lj k_l ;  Wk_j = sum_i A_ij K^_i
       f4 du = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
@@ -350,12 +369,16 @@ __global__ __launch_bounds__(NTHREADS) void k_bprep_c(BwdParams p) {
         p.g.Wk[row * KD + c] = wk[e];
       }
     }
-  for (int idx = threadIdx.x; idx < BT * KD; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
     const int i = idx / KD, c = idx % KD;
-    const long long o = (rowbase + i) * KD + c;
-    p.g.At1[o] = ddp[i * KD + c] * __expf(cd.G[i][c]);
-    p.g.B1[o] = s.Kh[i][c];
-    p.g.Ant[o] = -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c));
+    p.g.B1[(rowbase + i) * KD + c] = s.Kh[i][c];
+  }
+  for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {  // chunk-transposed panels
+    const int c = idx / BT, i = idx % BT;
+    const long long ot = cidx * KD * BT + idx;
+    p.g.At1[ot] = ddp[i * KD + c] * __expf(cd.G[i][c]);
+    p.g.B1t[ot] = s.Kh[i][c];
+    p.g.Ant[ot] = -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c));
   }
 }
 
@@ -369,7 +392,7 @@ struct GradCSmem {
   float gam[BT];
 };
 
-__global__ __launch_bounds__(NTHREADS) void k_grad_c(BwdParams p) {
+__global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GradCSmem& s = *reinterpret_cast<GradCSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
@@ -378,7 +401,8 @@ __global__ __launch_bounds__(NTHREADS) void k_grad_c(BwdParams p) {
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
   const int w = wave_id(), l = lane_id();
-  for (int i = w; i < BT; i += 4) {
+#pragma unroll
+  for (int i = w; i < BT; i += CW) {
     const int t = t0 + i;
     float x0, x1;
     ldrow2(p.in.u, b, t, hh, p.T, p.r, x0, x1);
@@ -411,7 +435,7 @@ __global__ __launch_bounds__(NTHREADS) void k_grad_c(BwdParams p) {
   auto U = [&](int j, int c) { return s.Uh[j][c]; };
   auto Xg = [&](int j, int c) { return s.gam[j] * s.Uh[j][c]; };
   auto DO = [&](int j, int c) { return ddp[j * KD + c]; };
-  for (int cb = 2 * w; cb < 2 * w + 2; ++cb)
+  for (int cb = w; cb < w + 1; ++cb)
     for (int I = 0; I < NB; ++I) {
       f4 a = mma_k32([&](int m, int v) { return dw[(I * BS + m) * KD + v]; },
                      [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
@@ -519,32 +543,32 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
                             (int)sizeof(BprepCSmem));
   (void)hipFuncSetAttribute((const void*)k_grad_c, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)sizeof(GradCSmem));
-  const dim3 chunks(NT, n), rows((Tp + 3) / 4, n), blk(NTHREADS);
+  const dim3 chunks(NT, n), rows((Tp + 3) / 4, n), blk(NTHREADS), cblk(CT);
   // S memory
-  SD_LAUNCH("k_bprep_s", k_bprep_s, chunks, blk, sizeof(BprepSSmem), st, p);
+  SD_LAUNCH("k_bprep_s", k_bprep_s, chunks, cblk, sizeof(BprepSSmem), st, p);
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
-  ss.rev = 1; ss.kt_token_major = 1;
+  ss.rev = 1;
   ss.Wneg = bw.Wk; ss.U = bw.dU; ss.Kt = bw.Ant; ss.Gam = fw.Gam;
-  ss.At1 = fw.Qs; ss.B1 = bw.B1;
+  ss.At1 = bw.At1; ss.B1 = bw.B1t;
   ss.Xs = bw.Ls; ss.wout = bw.dwS;
   ss.init = dS_T; ss.init_transposed = 0;
   ss.fin = dS0; ss.fin_transposed = 0;
   launch_state("state_s_bwd", ss, false, n, st);
-  SD_LAUNCH("k_grad_s", k_grad_s, chunks, blk, sizeof(GradSmem), st, p);
+  SD_LAUNCH("k_grad_s", k_grad_s, chunks, cblk, sizeof(GradSmem), st, p);
   SD_LAUNCH("k_src_bwd", k_src_bwd, rows, blk, 0, st, p);
   // C predictor
-  SD_LAUNCH("k_bprep_c", k_bprep_c, chunks, blk, sizeof(BprepCSmem), st, p);
+  SD_LAUNCH("k_bprep_c", k_bprep_c, chunks, cblk, sizeof(BprepCSmem), st, p);
   StateParams sc{};
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
-  sc.rev = 1; sc.kt_token_major = 1;
+  sc.rev = 1;
   sc.Wneg = bw.Wk; sc.U = bw.dU; sc.Kt = bw.Ant; sc.Gam = fw.Gam;
-  sc.At1 = bw.At1; sc.B1 = bw.B1;
+  sc.At1 = bw.At1; sc.B1 = bw.B1t;
   sc.Xs = bw.Lc; sc.wout = bw.dwC;
   sc.init = dC_T; sc.init_transposed = 1;
   sc.fin = dC0; sc.fin_transposed = 1;
   launch_state("state_c_bwd", sc, false, n, st);
-  SD_LAUNCH("k_grad_c", k_grad_c, chunks, blk, sizeof(GradCSmem), st, p);
+  SD_LAUNCH("k_grad_c", k_grad_c, chunks, cblk, sizeof(GradCSmem), st, p);
   SD_LAUNCH("k_final", k_final, rows, blk, 0, st, p);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }

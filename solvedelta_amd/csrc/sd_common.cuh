@@ -17,6 +17,19 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
+// Compile-time section timer for kernel tuning (off unless SD_SECTION_TIMING is
+// defined): workgroup (0,0) thread 0 records s_memrealtime at marks 0..31.
+#ifdef SD_SECTION_TIMING
+static __device__ unsigned long long sd_section_ticks[8][32];
+#define SD_MARK(slot, idx)                                                              \
+  do {                                                                                  \
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)                         \
+      sd_section_ticks[slot][idx] = __builtin_amdgcn_s_memrealtime();                   \
+  } while (0)
+#else
+#define SD_MARK(slot, idx) do { } while (0)
+#endif
+
 namespace sd {
 
 constexpr int BT = 64;     // chunk length
@@ -26,7 +39,9 @@ constexpr int KD = 128;    // padded key width
 constexpr int VD = 128;    // padded value width
 constexpr float TAU = 30.f;
 constexpr float RHO = 0.625f;
-constexpr int NTHREADS = 256;
+constexpr int NTHREADS = 256;  // sequential / per-token kernels
+constexpr int CT = 512;        // chunk-parallel kernels: 8 waves, one 16-column block each
+constexpr int CW = CT / 64;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -61,19 +76,37 @@ template <class FA, class FB>
 __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
   const int l = lane_id();
   const int m = l & 15, kq = (l >> 4) * 8;
-  for (int k0 = 0; k0 < K; k0 += 32) {
-    bf16x8 ah, al, bh, bl;
+  // Gather every operand first (K <= 128) so all loads are in flight together,
+  // then split and multiply.
+  float av[4][8], bv[4][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      __bf16 h, lo;
-      split_bf(fa(m, k0 + kq + e), h, lo);
-      ah[e] = h; al[e] = lo;
-      split_bf(fb(k0 + kq + e, m), h, lo);
-      bh[e] = h; bl[e] = lo;
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks * 32 < K) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        av[ks][e] = fa(m, ks * 32 + kq + e);
+        bv[ks][e] = fb(ks * 32 + kq + e, m);
+      }
     }
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks * 32 < K) {
+      bf16x8 ah, al, bh, bl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        __bf16 h, lo;
+        split_bf(av[ks][e], h, lo);
+        ah[e] = h; al[e] = lo;
+        split_bf(bv[ks][e], h, lo);
+        bh[e] = h; bl[e] = lo;
+      }
+#ifndef SD_EXPERIMENT_ONE_TERM
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+#endif
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+    }
   }
   return acc;
 }
@@ -121,11 +154,16 @@ __device__ inline void build_decay(ChunkDecay& cd, const float* g, long long st,
   const int tid = threadIdx.x;
   if (tid < KD) {
     const int c = tid;
-    float acc = 0.f;
-    for (int i = 0; i < BT; ++i) {
+    float x[BT];
+#pragma unroll
+    for (int i = 0; i < BT; ++i) {  // all loads in flight before the scan
       const int t = t0 + i;
-      float x = (t < T && c < r) ? g[(long long)t * st + c] : 0.f;
-      acc += x;
+      x[i] = (t < T && c < r) ? g[(long long)t * st + c] : 0.f;
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < BT; ++i) {
+      acc += x[i];
       cd.G[i][c] = acc;
     }
     cd.R[0][c] = 0.f;
@@ -136,11 +174,17 @@ __device__ inline void build_decay(ChunkDecay& cd, const float* g, long long st,
     }
   }
   __syncthreads();
-  if (tid < NB) {
-    int n = 0;
-    for (int c = 0; c < KD; ++c)
-      if (cd.wild[tid][c]) cd.wlist[tid][n++] = (short)c;
-    cd.nwild[tid] = n;
+  {  // wild lists: wave J scans block J's coordinates with ballots
+    const int w = tid >> 6, l = tid & 63;
+    if (w < NB) {
+      const bool f0 = cd.wild[w][l] != 0, f1 = cd.wild[w][l + 64] != 0;
+      const unsigned long long m0 = __ballot(f0), m1 = __ballot(f1);
+      const unsigned long long below = (l == 0) ? 0ull : (~0ull >> (64 - l));
+      const int n0 = __popcll(m0);
+      if (f0) cd.wlist[w][__popcll(m0 & below)] = (short)l;
+      if (f1) cd.wlist[w][n0 + __popcll(m1 & below)] = (short)(l + 64);
+      if (l == 0) cd.nwild[w] = n0 + __popcll(m1);
+    }
   }
   __syncthreads();
 }
@@ -159,7 +203,7 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
                              int ldm = LS) {
   const int w = wave_id();
   // 10 lower block pairs (I >= J), distributed over 4 waves.
-  for (int p = w; p < 10; p += 4) {
+  for (int p = w; p < 10; p += CW) {
     int I = 0, J = p;
     while (J > I) { J -= I + 1; ++I; }  // p -> (I, J) with J <= I
     const int I0 = I * BS, J0 = J * BS;
@@ -182,7 +226,7 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
     }
   }
   // Zero the strictly-upper block pairs.
-  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
     const int i = idx / BT, j = idx % BT;
     if ((j / BS) > (i / BS)) M[i * ldm + j] = 0.f;
   }
@@ -193,7 +237,7 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
     if (nw == 0) continue;
     const int J0 = J * BS;
     const int npairs = (BT - J0) * BS;
-    for (int idx = threadIdx.x; idx < npairs; idx += NTHREADS) {
+    for (int idx = threadIdx.x; idx < npairs; idx += CT) {
       const int i = J0 + idx / BS, j = J0 + idx % BS;
       const bool keep = strict ? (j < i) : (j <= i);
       if (!keep) continue;
@@ -237,7 +281,7 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
     // T_IJ = sum_{K=J}^{I-1} L_IK A_KJ  (A_KJ already in tmp for K-J < dist)
     float tv[4];
     int nt = 0;
-    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += NTHREADS) {
+    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += CT) {
       const int J = idx / (BS * BS), rem = idx % (BS * BS);
       const int I = J + dist, i = rem / BS, j = rem % BS;
       float s = 0.f;
@@ -248,14 +292,14 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
     }
     __syncthreads();
     nt = 0;
-    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += NTHREADS) {
+    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += CT) {
       const int J = idx / (BS * BS), rem = idx % (BS * BS);
       const int I = J + dist, i = rem / BS, j = rem % BS;
       // stash T in the (still unused) upper block (J, I) of L
       L[(J * BS + i) * LS + I * BS + j] = tv[nt++];
     }
     __syncthreads();
-    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += NTHREADS) {
+    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += CT) {
       const int J = idx / (BS * BS), rem = idx % (BS * BS);
       const int I = J + dist, i = rem / BS, j = rem % BS;
       float s = 0.f;
@@ -266,7 +310,7 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
     __syncthreads();
   }
   // Copy back: A lower (incl. diagonal), zero upper.
-  for (int idx = tid; idx < BT * BT; idx += NTHREADS) {
+  for (int idx = tid; idx < BT * BT; idx += CT) {
     const int i = idx / BT, j = idx % BT;
     L[i * LS + j] = (j / BS <= i / BS) ? tmp[i * LS + j] : 0.f;
   }
@@ -345,7 +389,7 @@ __device__ f4 decayed_apply_t_tile(const ChunkDecay& cd, const float* M, FX X, i
 template <class FX, class FY>
 __device__ void plain_pair(FX X, FY Y, bool strict, float* M) {
   const int w = wave_id();
-  for (int p = w; p < 10; p += 4) {
+  for (int p = w; p < 10; p += CW) {
     int I = 0, J = p;
     while (J > I) { J -= I + 1; ++I; }
     f4 acc = mma_k32([&](int m, int c) { return X(I * BS + m, c); },
@@ -357,7 +401,7 @@ __device__ void plain_pair(FX X, FY Y, bool strict, float* M) {
       M[i * LS + j] = keep ? acc[e] : 0.f;
     }
   }
-  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
     const int i = idx / BT, j = idx % BT;
     if ((j / BS) > (i / BS)) M[i * LS + j] = 0.f;
   }

@@ -60,7 +60,7 @@ struct PrepCSmem {
   float gam[BT];
 };
 
-__global__ __launch_bounds__(NTHREADS) void k_prep_c(FwdParams p) {
+__global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepCSmem& s = *reinterpret_cast<PrepCSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y;
@@ -71,7 +71,8 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_c(FwdParams p) {
                    (long long)hh * in.log_decay.sh;
   build_decay(s.cd, g, in.log_decay.st, t0, T, r);
   const int w = wave_id(), l = lane_id();
-  for (int i = w; i < BT; i += 4) {
+#pragma unroll
+  for (int i = w; i < BT; i += CW) {
     const int t = t0 + i;
     float x0, x1;
     load_row2(in.u, b, t, hh, T, r, x0, x1);
@@ -90,11 +91,11 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_c(FwdParams p) {
       cd, [&](int i, int c) { return s.gam[i] * s.Uh[i][c]; },
       [&](int j, int c) { return s.Uh[j][c]; }, true, s.M);
   unit_lower_inverse(s.M, s.tmp);
-  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS)
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.Ac[((long long)n * p.NT + ch) * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
   // W = A diag(gamma) (u e^{Gexcl}),  U = A diag(gamma) h
   const long long rowbase = (long long)n * p.Tp + t0;
-  for (int cb = 2 * w; cb < 2 * w + 2; ++cb) {
+  for (int cb = w; cb < w + 1; ++cb) {
     for (int I = 0; I < NB; ++I) {
       const int K = I < 2 ? 32 : 64;
       auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k] * s.gam[k]; };
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_c(FwdParams p) {
   }
   // decayed keys (transposed per chunk) and chunk decay
   const long long cbase = ((long long)n * p.NT + ch);
-  for (int idx = threadIdx.x; idx < KD * BT; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {
     const int c = idx / BT, i = idx % BT;
     p.Kc[cbase * KD * BT + idx] = s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
   }
@@ -126,111 +127,217 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_c(FwdParams p) {
 // ---------------------------------------------------------------------------
 // k_state: sequential chunk pass over one 16-column tile of the state.
 //   X <- state [KD x 16] in MFMA accumulators (wave w owns rows 32w..32w+31)
-//   per chunk: Xs[ch] = X;  w = U + Wneg X;  (COL_OUT) o = Q X + P w;
-//              X = Gamma X + Kt w
+//   per chunk: slot[ch] = X;  w = U + Wneg X;  (COL_OUT) o = Q X + P w;
+//              X = Gamma X + Kt w (+ At1 B1)
+// Operand layouts (all fp32, K contiguous so each lane's 8-element fragment is
+// two 16-byte loads): Wneg, Q, U token-major [Tp][128]; Kt, At1 chunk-transposed
+// [128][64]; B1 chunk-transposed [128 cols][64 tokens]; P [64][64].
+// The next chunk's fragments are loaded into registers while the current chunk
+// computes, so the global latency leaves the sequential critical path.
 // ---------------------------------------------------------------------------
 struct StateSmem {
   float Xt[16][KD + 4];  // X0 tile, transposed [col][row]
   float wt[16][BT + 4];  // w tile, transposed [col][token]
 };
 
-template <bool COL_OUT>
+template <bool COL_OUT, bool INJ>
+struct StateFrags {
+  float4 W[4][2];
+  float4 K[2][2][2];
+  float4 Q[COL_OUT ? 4 : 1][2];
+  float4 P[COL_OUT ? 2 : 1][2];
+  float4 A1[INJ ? 2 : 1][2][2];
+  float4 B1[INJ ? 2 : 1][2];
+  float U[4];
+  float4 gam[2];
+};
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+template <bool COL_OUT, bool INJ>
+__device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
+                                                 StateFrags<COL_OUT, INJ>& f) {
+  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+  const long long cidx = (long long)n * p.NT + ch;
+  const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
+  const int col = tile * 16 + m;
+  const float* Wb = p.Wneg + (rowbase + w * 16 + m) * KD + kq;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    f.W[ks][0] = ld4(Wb + ks * 32);
+    f.W[ks][1] = ld4(Wb + ks * 32 + 4);
+  }
+  const float* Kb = p.Kt + cidx * KD * BT;
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const float* a = Kb + (long long)((2 * w + q) * 16 + m) * BT + ks * 32 + kq;
+      f.K[q][ks][0] = ld4(a);
+      f.K[q][ks][1] = ld4(a + 4);
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) f.U[e] = p.U[(rowbase + w * 16 + (l >> 4) * 4 + e) * KD + col];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) f.gam[q] = ld4(p.Gam + cidx * KD + (2 * w + q) * 16 + (l >> 4) * 4);
+  if constexpr (COL_OUT) {
+    const float* Qb = p.Q + (rowbase + w * 16 + m) * KD + kq;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      f.Q[ks][0] = ld4(Qb + ks * 32);
+      f.Q[ks][1] = ld4(Qb + ks * 32 + 4);
+    }
+    const float* Pb = p.P + cidx * BT * BT + (long long)(w * 16 + m) * BT + kq;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      f.P[ks][0] = ld4(Pb + ks * 32);
+      f.P[ks][1] = ld4(Pb + ks * 32 + 4);
+    }
+  }
+  if constexpr (INJ) {
+    const float* Ab = p.At1 + cidx * KD * BT;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float* a = Ab + (long long)((2 * w + q) * 16 + m) * BT + ks * 32 + kq;
+        f.A1[q][ks][0] = ld4(a);
+        f.A1[q][ks][1] = ld4(a + 4);
+      }
+    const float* Bb = p.B1 + cidx * KD * BT + (long long)col * BT + kq;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      f.B1[ks][0] = ld4(Bb + ks * 32);
+      f.B1[ks][1] = ld4(Bb + ks * 32 + 4);
+    }
+  }
+}
+
+// 3-term split-bf16 MFMA on register fragments (8 fp32 values each).
+__device__ __forceinline__ f4 mma3(const float4& a0, const float4& a1, const float4& b0,
+                                   const float4& b1, f4 acc) {
+  const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+  bf16x8 ah, al, bh, bl;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    __bf16 h, lo;
+    split_bf(av[e], h, lo);
+    ah[e] = h; al[e] = lo;
+    split_bf(bv[e], h, lo);
+    bh[e] = h; bl[e] = lo;
+  }
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+
+template <bool COL_OUT, bool INJ>
 __global__ __launch_bounds__(NTHREADS) void k_state(StateParams p) {
+  __shared__ __align__(16) StateSmem s;
   const int NS = p.NT + 1;  // state slots per sequence
-  __shared__ StateSmem s;
-  const int tile = blockIdx.x, n = blockIdx.y;
-  const int w = wave_id();
-  const int col = tile * 16 + out_col();  // this lane's state column
+  // Workgroups are dispatched round-robin over the 8 XCDs by linear id; when the
+  // sequence count allows, map ids so that the 8 column tiles of a sequence run
+  // on one XCD and share its L2 copy of the chunk panels.
+  int tile, n;
+  {
+    const int L = blockIdx.x, nseq = gridDim.x / 8;
+    if (nseq % 8 == 0) {
+      const int x = L % 8, j = L / 8;
+      tile = j % 8;
+      n = (j / 8) * 8 + x;
+    } else {
+      tile = L % 8;
+      n = L / 8;
+    }
+  }
+  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
+  const int col = tile * 16 + m;  // this lane's state column
   f4 X[2];
-  // initial state
   for (int q = 0; q < 2; ++q)
     for (int e = 0; e < 4; ++e) {
-      const int row = (2 * w + q) * 16 + out_row(e);
+      const int row = (2 * w + q) * 16 + r4 + e;
       float x = 0.f;
       if (p.init && row < p.rows && col < p.cols)
         x = p.init_transposed ? p.init[(long long)n * p.rows * p.cols + (long long)col * p.rows + row]
                               : p.init[(long long)n * p.rows * p.cols + (long long)row * p.cols + col];
       X[q][e] = x;
     }
+  StateFrags<COL_OUT, INJ> cur, nxt;
+  load_state_frags(p, n, p.rev ? p.NT - 1 : 0, tile, cur);
   for (int it = 0; it < p.NT; ++it) {
     const int ch = p.rev ? p.NT - 1 - it : it;
-    const long long cidx = (long long)n * p.NT + ch;
     const long long sidx = (long long)n * NS + ch;
     const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
-    // save X0 and stage it transposed ([col][row]) for the MFMA B operand
-    for (int q = 0; q < 2; ++q)
-      for (int e = 0; e < 4; ++e) {
-        const int row = (2 * w + q) * 16 + out_row(e);
-        const float x = X[q][e];
-        if (p.Xs) p.Xs[sidx * KD * KD + (long long)row * KD + col] = x;
-        s.Xt[out_col()][row] = x;
-      }
+    if (it + 1 < p.NT) load_state_frags(p, n, p.rev ? ch - 1 : ch + 1, tile, nxt);
+    // save X0 and stage it transposed ([col][row]) for the B operand
+    for (int q = 0; q < 2; ++q) {
+      const int row0 = (2 * w + q) * 16 + r4;
+      if (p.Xs)
+        for (int e = 0; e < 4; ++e) p.Xs[sidx * KD * KD + (long long)(row0 + e) * KD + col] = X[q][e];
+      *reinterpret_cast<float4*>(&s.Xt[m][row0]) = make_float4(X[q][0], X[q][1], X[q][2], X[q][3]);
+    }
     __syncthreads();
     // w = U + Wneg X  (token block w)
-    f4 acc;
-    for (int e = 0; e < 4; ++e)
-      acc[e] = p.U[(rowbase + w * 16 + out_row(e)) * KD + col];
-    {
-      const float* Wb = p.Wneg + (rowbase + w * 16) * KD;
-      acc = mma_k32([&](int m, int k) { return Wb[(long long)m * KD + k]; },
-                    [&](int k, int nn) { return s.Xt[nn][k]; }, KD, acc);
+    f4 acc = {cur.U[0], cur.U[1], cur.U[2], cur.U[3]};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const float* xb = &s.Xt[m][ks * 32 + kq];
+      acc = mma3(cur.W[ks][0], cur.W[ks][1], ld4(xb), ld4(xb + 4), acc);
     }
     for (int e = 0; e < 4; ++e) {
-      const int tk = w * 16 + out_row(e);
+      const int tk = w * 16 + r4 + e;
       p.wout[(rowbase + tk) * KD + col] = acc[e];
-      s.wt[out_col()][tk] = acc[e];
     }
+    *reinterpret_cast<float4*>(&s.wt[m][w * 16 + r4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     __syncthreads();
-    if (COL_OUT) {
+    if constexpr (COL_OUT) {
       // o = Q X0 + P w  (token block w), written as bf16 to out[b,t,h,v]
-      const float* Qb = p.Q + (rowbase + w * 16) * KD;
-      f4 o = mma_k32([&](int m, int k) { return Qb[(long long)m * KD + k]; },
-                     [&](int k, int nn) { return s.Xt[nn][k]; }, KD, zero4());
-      const float* Pb = p.P + cidx * BT * BT + (long long)(w * 16) * BT;
-      o = mma_k32([&](int m, int k) { return Pb[m * BT + k]; },
-                  [&](int k, int nn) { return s.wt[nn][k]; }, (w < 2 ? 32 : 64), o);
+      f4 o = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const float* xb = &s.Xt[m][ks * 32 + kq];
+        o = mma3(cur.Q[ks][0], cur.Q[ks][1], ld4(xb), ld4(xb + 4), o);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks == 1 && w < 2) break;
+        const float* wb = &s.wt[m][ks * 32 + kq];
+        o = mma3(cur.P[ks][0], cur.P[ks][1], ld4(wb), ld4(wb + 4), o);
+      }
       const int b = n / p.H, hh = n % p.H;
       for (int e = 0; e < 4; ++e) {
-        const int t = ch * BT + w * 16 + out_row(e);
+        const int t = ch * BT + w * 16 + r4 + e;
         if (t < p.T && col < p.cols)
           p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + col] = f2bf(o[e]);
       }
     }
     // X = Gamma X + Kt w (+ At1 B1)
-    const float* gam = p.Gam + cidx * KD;
+#pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int rb = 2 * w + q;
-      for (int e = 0; e < 4; ++e) X[q][e] *= gam[rb * 16 + out_row(e)];
-      if (p.kt_token_major) {
-        const float* Kt = p.Kt + rowbase * KD;
-        X[q] = mma_k32([&](int m, int k) { return Kt[(long long)k * KD + rb * 16 + m]; },
-                       [&](int k, int nn) { return s.wt[nn][k]; }, BT, X[q]);
-      } else {
-        const float* Kt = p.Kt + cidx * KD * BT;
-        X[q] = mma_k32([&](int m, int k) { return Kt[(long long)(rb * 16 + m) * BT + k]; },
-                       [&](int k, int nn) { return s.wt[nn][k]; }, BT, X[q]);
-      }
-      if (p.At1) {
-        const float* A1 = p.At1 + rowbase * KD;
-        const float* B1 = p.B1 + rowbase * KD;
-        X[q] = mma_k32([&](int m, int k) { return A1[(long long)k * KD + rb * 16 + m]; },
-                       [&](int k, int nn) { return B1[(long long)k * KD + tile * 16 + nn]; }, BT,
-                       X[q]);
+      const float gv[4] = {cur.gam[q].x, cur.gam[q].y, cur.gam[q].z, cur.gam[q].w};
+      for (int e = 0; e < 4; ++e) X[q][e] *= gv[e];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float* wb = &s.wt[m][ks * 32 + kq];
+        X[q] = mma3(cur.K[q][ks][0], cur.K[q][ks][1], ld4(wb), ld4(wb + 4), X[q]);
+        if constexpr (INJ) X[q] = mma3(cur.A1[q][ks][0], cur.A1[q][ks][1], cur.B1[ks][0], cur.B1[ks][1], X[q]);
       }
     }
     __syncthreads();
+    cur = nxt;
   }
   // final state (also kept as slot NT for the backward)
   if (p.Xs && !p.rev)
     for (int q = 0; q < 2; ++q)
       for (int e = 0; e < 4; ++e) {
-        const int row = (2 * w + q) * 16 + out_row(e);
+        const int row = (2 * w + q) * 16 + r4 + e;
         p.Xs[((long long)n * NS + p.NT) * KD * KD + (long long)row * KD + col] = X[q][e];
       }
   if (p.fin) {
     for (int q = 0; q < 2; ++q)
       for (int e = 0; e < 4; ++e) {
-        const int row = (2 * w + q) * 16 + out_row(e);
+        const int row = (2 * w + q) * 16 + r4 + e;
         if (row < p.rows && col < p.cols) {
           const long long base = (long long)n * p.rows * p.cols;
           if (p.fin_transposed)
@@ -242,15 +349,15 @@ __global__ __launch_bounds__(NTHREADS) void k_state(StateParams p) {
   }
 }
 
-template __global__ void k_state<false>(StateParams);
-template __global__ void k_state<true>(StateParams);
-
 void launch_state(const char* name, const StateParams& sp, bool col_out, int nseq,
                   hipStream_t st) {
+  const dim3 grid((KD / 16) * nseq), blk(NTHREADS);
   if (col_out)
-    SD_LAUNCH(name, k_state<true>, dim3(KD / 16, nseq), dim3(NTHREADS), 0, st, sp);
+    SD_LAUNCH(name, (k_state<true, false>), grid, blk, 0, st, sp);
+  else if (sp.At1)
+    SD_LAUNCH(name, (k_state<false, true>), grid, blk, 0, st, sp);
   else
-    SD_LAUNCH(name, k_state<false>, dim3(KD / 16, nseq), dim3(NTHREADS), 0, st, sp);
+    SD_LAUNCH(name, (k_state<false, false>), grid, blk, 0, st, sp);
 }
 
 // ---------------------------------------------------------------------------
@@ -266,7 +373,7 @@ struct PrepSSmem {
   float Pc[BT][GS];
 };
 
-__global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
+__global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepSSmem& s = *reinterpret_cast<PrepSSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y;
@@ -278,7 +385,8 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
   build_decay(s.cd, g, in.log_decay.st, t0, T, r);
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id();
-  for (int i = w; i < BT; i += 4) {
+#pragma unroll
+  for (int i = w; i < BT; i += CW) {
     const int t = t0 + i;
     float x0, x1;
     load_row2(in.u, b, t, hh, T, r, x0, x1);
@@ -295,7 +403,7 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
   const long long cidx = (long long)n * p.NT + ch;
   const float* delta = p.delta + rowbase * KD;
   // M_ij = k_i . delta_j  (j <= i)
-  for (int pp = w; pp < 10; pp += 4) {
+  for (int pp = w; pp < 10; pp += CW) {
     int I = 0, J = pp;
     while (J > I) { J -= I + 1; ++I; }
     f4 acc = mma_k32([&](int m, int c) { return s.Pb[I * BS + m][c]; },
@@ -306,15 +414,15 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
       s.M[i * LS + j] = j <= i ? acc[e] : 0.f;
     }
   }
-  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
     const int i = idx / BT, j = idx % BT;
     if ((j / BS) > (i / BS)) s.M[i * LS + j] = 0.f;
   }
   __syncthreads();
   // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}
   const float* X0 = p.Xc + ((long long)n * (p.NT + 1) + ch) * KD * KD;
-  for (int q = 0; q < 2; ++q) {
-    const int cb = 2 * w + q;
+  for (int q = 0; q < 1; ++q) {
+    const int cb = w + q;
     for (int I = 0; I < NB; ++I) {
       f4 a1 = mma_k32([&](int m, int bb) { return s.Pb[I * BS + m][bb]; },
                       [&](int bb, int nn) { return X0[(long long)(cb * 16 + nn) * KD + bb]; }, KD,
@@ -351,7 +459,8 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
   }
   __syncthreads();
   // sources (one wave per token row; e overwrites u, chi overwrites k)
-  for (int i = w; i < BT; i += 4) {
+#pragma unroll
+  for (int i = w; i < BT; i += CW) {
     const int t = t0 + i;
     const float u0 = s.Pa[i][l], u1 = s.Pa[i][l + 64];
     const float k0 = s.Pb[i][l], k1 = s.Pb[i][l + 64];
@@ -383,13 +492,13 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
   decayed_gram<false>(
       cd, [&](int i, int c) { return s.Pb[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
       false, s.M);
-  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS)
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.Ps[cidx * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
-  for (int idx = threadIdx.x; idx < KD * BT; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {
     const int c = idx / BT, i = idx % BT;
     p.Ks[cidx * KD * BT + idx] = s.Pc[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
   }
-  for (int idx = threadIdx.x; idx < BT * KD; idx += NTHREADS) {
+  for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
     const int i = idx / KD, c = idx % KD;
     p.Qs[(rowbase + i) * KD + c] = s.Pb[i][c] * __expf(cd.G[i][c]);
   }
@@ -399,10 +508,10 @@ __global__ __launch_bounds__(NTHREADS) void k_prep_s(FwdParams p) {
       cd, [&](int i, int c) { return s.Pa[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
       true, s.M);
   unit_lower_inverse(s.M, &s.Pc[0][0]);
-  for (int idx = threadIdx.x; idx < BT * BT; idx += NTHREADS)
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.As[cidx * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
   // W = A (e e^G), U = A z with z = sigmoid(write_raw) v read from the inputs
-  for (int cb = 2 * w; cb < 2 * w + 2; ++cb) {
+  for (int cb = w; cb < w + 1; ++cb) {
     for (int I = 0; I < NB; ++I) {
       const int K = I < 2 ? 32 : 64;
       auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k]; };
@@ -451,7 +560,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
                             (int)prep_c_smem());
   (void)hipFuncSetAttribute((const void*)k_prep_s, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)prep_s_smem());
-  SD_LAUNCH("k_prep_c", k_prep_c, dim3(NT, n), dim3(256), prep_c_smem(), st, fp);
+  SD_LAUNCH("k_prep_c", k_prep_c, dim3(NT, n), dim3(CT), prep_c_smem(), st, fp);
 
   StateParams sc{};
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
@@ -461,7 +570,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   sc.fin = C_T; sc.fin_transposed = 1;
   launch_state("state_c_fwd", sc, false, n, st);
 
-  SD_LAUNCH("k_prep_s", k_prep_s, dim3(NT, n), dim3(256), prep_s_smem(), st, fp);
+  SD_LAUNCH("k_prep_s", k_prep_s, dim3(NT, n), dim3(CT), prep_s_smem(), st, fp);
 
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;

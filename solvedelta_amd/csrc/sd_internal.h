@@ -36,9 +36,9 @@ struct FwdParams {
 
 // Sequential chunk pass, forward (state X) or reverse (cotangent lambda):
 //   slot[ch] = X;  w = U + Wneg X;  X = Gamma X + Kt w (+ At1 B1)
-// Kt is chunk-transposed [128][64] (kt_token_major = 0) or a token-major panel.
+// Kt, At1 are chunk-transposed [128][64]; B1 is chunk-transposed [128 cols][64 tokens].
 struct StateParams {
-  int H, T, NT, Tp, rows, cols, rev, kt_token_major;
+  int H, T, NT, Tp, rows, cols, rev;
   const float* Wneg; const float* U; const float* Kt; const float* Gam;
   const float* At1; const float* B1;  // optional injection (token-major panels)
   const float* Q; const float* P;  // output operands (COL_OUT)
@@ -66,7 +66,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
 struct BwdWs {
   float* Lc;   // C-op chunk-end cotangents                [n][NT+1][128][128]
   float* Ls;   // S-op chunk-end cotangents
-  float* dU; float* Wk; float* At1; float* B1; float* Ant;  // reverse-pass panels (reused)
+  float* dU; float* Wk; float* At1; float* B1; float* B1t; float* Ant;  // reverse-pass panels (reused)
   float* dwS; float* dwC;          // dw of each op           [n][Tp][128]
   float* de; float* dchi; float* dd; float* dgS;
   float* ddelta; float* du_src; float* dk_src;

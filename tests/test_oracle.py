@@ -20,7 +20,14 @@ from oracle.sd_oracle import (
     zero_state,
 )
 
-torch.set_default_dtype(torch.float64)
+
+
+@pytest.fixture(autouse=True)
+def _fp64_default():
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def small_inputs(T=6, r=8, V=5, seed=7):
