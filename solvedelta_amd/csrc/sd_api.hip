@@ -57,7 +57,7 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.Ls = c.take<float>(states);
   float** panels[] = {&w.dU, &w.Wk, &w.At1, &w.B1, &w.B1t, &w.Ant, &w.dwS, &w.dwC, &w.de, &w.dchi,
                       &w.dd, &w.dgS, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
-                      &w.dgC};
+                      &w.dgC, &w.uh, &w.xdx};
   for (float** pp : panels) *pp = c.take<float>(panel);
   if (total) *total = c.off + 256;
   return w;

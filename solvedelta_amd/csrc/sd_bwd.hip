@@ -132,9 +132,36 @@ struct GradSmem {
   ChunkDecay cd;
   float M1[BT * LS];
   float M2[BT * LS];
-  float M3[BT * LS];
-  float dG[BT][GS];
 };
+
+// Rowsum of X_C (.) lambda for row c, then the in-chunk reverse cumulative sum of
+// the decay cotangent held (un-summed) in dg; thread c < 128 owns column c.
+__device__ void close_decay_gradient(const float* XC, const float* lam, float* dg, const float* shift) {
+  if (threadIdx.x < KD) {
+    const int c = threadIdx.x;
+    float acc = 0.f;
+    const float* xr = XC + c * KD;
+    const float* lr = lam + c * KD;
+#pragma unroll 8
+    for (int v = 0; v < KD; v += 4) {
+      const float4 x = ld4g(xr + v), y = ld4g(lr + v);
+      acc += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+    }
+    for (int i0 = BT - 16; i0 >= 0; i0 -= 16) {  // 16 loads in flight per step
+      float col[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int i = i0 + q;
+        col[q] = dg[i * KD + c] + (shift && i + 1 < BT ? shift[(i + 1) * KD + c] : 0.f);
+      }
+#pragma unroll
+      for (int q = 15; q >= 0; --q) {
+        acc += col[q];
+        dg[(i0 + q) * KD + c] = acc;
+      }
+    }
+  }
+}
 
 __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -160,57 +187,65 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
              true, s.M1);
   plain_pair([&](int i, int c) { return dO[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
              false, s.M2);
-  __syncthreads();
-  SD_MARK(0, 2);
-  const int w = wave_id();
-  auto D = [&](int j, int c) { return dd_[j * KD + c]; };
-  auto E = [&](int j, int c) { return ee[j * KD + c]; };
-  auto Q = [&](int j, int c) { return chi[j * KD + c]; };
-  for (int cb = w; cb < w + 1; ++cb)
-    for (int I = 0; I < NB; ++I) {
-      const bool mk = cb == 0 && I == 0;
-      if (mk) SD_MARK(0, 3);
-      f4 a = mma_k32([&](int m, int v) { return dw[(I * BS + m) * KD + v]; },
-                     [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
-      if (mk) SD_MARK(0, 4);
-      f4 ap = decayed_apply_tile<false>(cd, s.M1, D, I, cb);
-      if (mk) SD_MARK(0, 5);
-      f4 bq = mma_k32([&](int m, int v) { return dO[(I * BS + m) * KD + v]; },
-                      [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
-      f4 bp = decayed_apply_tile<false>(cd, s.M2, D, I, cb);
-      f4 kl = mma_k32([&](int m, int v) { return wv[(I * BS + m) * KD + v]; },
-                      [&](int v, int nn) { return lam[(cb * 16 + nn) * KD + v]; }, KD, zero4());
-      if (mk) SD_MARK(0, 6);
-      f4 k2 = decayed_apply_t_tile<false>(cd, s.M2, Q, I, cb);
-      if (mk) SD_MARK(0, 7);
-      f4 k3 = decayed_apply_t_tile<false>(cd, s.M1, E, I, cb);
-      if (mk) SD_MARK(0, 8);
+  const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+  // row-block x column-block products over V (K = 128), all operand blocks in flight at once
+  f4 a[NB], bq[NB], kl[NB];
+  {
+    Blk B, A[2];
+    load_blk(B, X0 + cb * 16 * KD, KD);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = I * BS + out_row(e), c = cb * 16 + out_col();
-        const float eg = __expf(cd.G[i][c]);
-        const float de = -(eg * a[e] + ap[e]);
-        const float dchi = eg * bq[e] + bp[e];
-        const float ddv = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[e] + k2[e] - k3[e];
-        const long long o = (rowbase + i) * KD + c;
-        p.g.de[o] = de;
-        p.g.dchi[o] = dchi;
-        p.g.dd[o] = ddv;
-        s.dG[i][c] = chi[i * KD + c] * dchi - dd_[i * KD + c] * ddv + ee[i * KD + c] * de;
-      }
+    for (int I0 = 0; I0 < NB; I0 += 2) {
+      load_blk(A[0], dw + I0 * BS * KD, KD);
+      load_blk(A[1], dw + (I0 + 1) * BS * KD, KD);
+      a[I0] = mma_blk(A[0], B, zero4());
+      a[I0 + 1] = mma_blk(A[1], B, zero4());
+      load_blk(A[0], dO + I0 * BS * KD, KD);
+      load_blk(A[1], dO + (I0 + 1) * BS * KD, KD);
+      bq[I0] = mma_blk(A[0], B, zero4());
+      bq[I0 + 1] = mma_blk(A[1], B, zero4());
     }
-  SD_MARK(0, 9);
-  __syncthreads();
-  SD_MARK(0, 10);
-  if (threadIdx.x < KD) {
-    const int c = threadIdx.x;
-    float acc = 0.f;
-    for (int v = 0; v < KD; ++v) acc += XC[c * KD + v] * lam[c * KD + v];
-    for (int i = BT - 1; i >= 0; --i) {
-      acc += s.dG[i][c];
-      p.g.dgS[(rowbase + i) * KD + c] = acc;
+    load_blk(B, lam + cb * 16 * KD, KD);
+#pragma unroll
+    for (int I0 = 0; I0 < NB; I0 += 2) {
+      load_blk(A[0], wv + I0 * BS * KD, KD);
+      load_blk(A[1], wv + (I0 + 1) * BS * KD, KD);
+      kl[I0] = mma_blk(A[0], B, zero4());
+      kl[I0 + 1] = mma_blk(A[1], B, zero4());
     }
   }
+  float Sd[NB][4], Se[NB][4], Sq[NB][4];
+  load_slab(Sd, dd_, cb);
+  load_slab(Se, ee, cb);
+  load_slab(Sq, chi, cb);
+  __syncthreads();  // M1, M2 complete
+  SD_MARK(0, 2);
+  auto D = [&](int j, int cc) { return dd_[j * KD + cc]; };
+  auto E = [&](int j, int cc) { return ee[j * KD + cc]; };
+  auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
+  float* dg = p.g.dgS + rowbase * KD;
+#pragma unroll 1
+  for (int I = 0; I < NB; ++I) {
+    const f4 ap = apply_slab<false>(cd, s.M1, Sd, I, cb, D);
+    const f4 bp = apply_slab<false>(cd, s.M2, Sd, I, cb, D);
+    const f4 k2 = apply_t_slab<false>(cd, s.M2, Sq, I, cb, Q);
+    const f4 k3 = apply_t_slab<false>(cd, s.M1, Se, I, cb, E);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + r4 + e;
+      const float eg = __expf(cd.G[i][c]);
+      const float de = -(eg * a[I][e] + ap[e]);
+      const float dchi = eg * bq[I][e] + bp[e];
+      const float ddv = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[I][e] + k2[e] - k3[e];
+      const long long o = (rowbase + i) * KD + c;
+      p.g.de[o] = de;
+      p.g.dchi[o] = dchi;
+      p.g.dd[o] = ddv;
+      dg[i * KD + c] = Sq[I][e] * dchi - Sd[I][e] * ddv + Se[I][e] * de;
+    }
+  }
+  SD_MARK(0, 9);
+  __syncthreads();
+  close_decay_gradient(XC, lam, dg, nullptr);
   SD_MARK(0, 11);
 }
 
@@ -372,6 +407,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
     const int i = idx / KD, c = idx % KD;
     p.g.B1[(rowbase + i) * KD + c] = s.Kh[i][c];
+    p.g.uh[(rowbase + i) * KD + c] = s.Uh[i][c];
   }
   for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {  // chunk-transposed panels
     const int c = idx / BT, i = idx % BT;
@@ -386,9 +422,6 @@ struct GradCSmem {
   ChunkDecay cd;
   float M1[BT * LS];
   float M2[BT * LS];
-  float M3[BT * LS];
-  float dG[BT][GS];
-  float Uh[BT][GS];
   float gam[BT];
 };
 
@@ -400,81 +433,105 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   const ChunkDecay& cd = s.cd;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
-  const int w = wave_id(), l = lane_id();
-#pragma unroll
-  for (int i = w; i < BT; i += CW) {
-    const int t = t0 + i;
-    float x0, x1;
-    ldrow2(p.in.u, b, t, hh, p.T, p.r, x0, x1);
-    norm2(x0, x1);
-    s.Uh[i][l] = x0;
-    s.Uh[i][l + 64] = x1;
-    if (l == 0)
-      s.gam[i] = t < p.T ? ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
-                                                          (long long)t * p.in.gamma.st +
-                                                          (long long)hh * p.in.gamma.sh]
-                         : 0.f;
+  const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+  if (threadIdx.x < BT) {
+    const int t = t0 + threadIdx.x;
+    s.gam[threadIdx.x] = t < p.T ? ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                                                   (long long)t * p.in.gamma.st +
+                                                                   (long long)hh * p.in.gamma.sh]
+                                 : 0.f;
   }
-  __syncthreads();
   const float* dw = p.g.dwC + rowbase * KD;
   const float* wv = p.f.delta + rowbase * KD;
   const float* ddp = p.g.dd + rowbase * KD;   // cotangent of the C-op output
   const float* kh = p.g.B1 + rowbase * KD;    // normalised keys
+  const float* uh = p.g.uh + rowbase * KD;    // normalised u
   const float* dprim = p.f.d + rowbase * KD;  // d = k + output
   const float* X0 = p.f.Xc + sidx * KD * KD;
   const float* XC = X0 + KD * KD;
   const float* lam = p.g.Lc + sidx * KD * KD;
-  plain_pair([&](int i, int c) { return dw[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
+  plain_pair([&](int i, int cc) { return dw[i * KD + cc]; }, [&](int j, int cc) { return wv[j * KD + cc]; },
              true, s.M1);
-  plain_pair([&](int i, int c) { return kh[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
+  plain_pair([&](int i, int cc) { return kh[i * KD + cc]; }, [&](int j, int cc) { return wv[j * KD + cc]; },
              false, s.M2);
-  __syncthreads();
-  decayed_gram<false>(
-      cd, [&](int i, int c) { return ddp[i * KD + c]; }, [&](int j, int c) { return s.Uh[j][c]; },
-      false, s.M3);
-  auto U = [&](int j, int c) { return s.Uh[j][c]; };
-  auto Xg = [&](int j, int c) { return s.gam[j] * s.Uh[j][c]; };
-  auto DO = [&](int j, int c) { return ddp[j * KD + c]; };
-  for (int cb = w; cb < w + 1; ++cb)
-    for (int I = 0; I < NB; ++I) {
-      f4 a = mma_k32([&](int m, int v) { return dw[(I * BS + m) * KD + v]; },
-                     [&](int v, int nn) { return X0[(cb * 16 + nn) * KD + v]; }, KD, zero4());
-      f4 ap = decayed_apply_tile<true>(cd, s.M1, U, I, cb);
-      f4 kl = mma_k32([&](int m, int v) { return wv[(I * BS + m) * KD + v]; },
-                      [&](int v, int nn) { return lam[(cb * 16 + nn) * KD + v]; }, KD, zero4());
-      f4 k2 = decayed_apply_t_tile<false>(cd, s.M2, DO, I, cb);
-      f4 k3 = decayed_apply_t_tile<true>(cd, s.M1, Xg, I, cb);
-      f4 dq = mma_k32([&](int m, int aa) {
-                        const int i = I * BS + m;
-                        return ddp[i * KD + aa] * __expf(cd.G[i][aa]);
-                      },
-                      [&](int aa, int nn) { return X0[aa * KD + cb * 16 + nn]; }, KD, zero4());
-      dq = mma_k32([&](int m, int j) { return s.M3[(I * BS + m) * LS + j]; },
-                   [&](int j, int nn) { return wv[j * KD + cb * 16 + nn]; }, (I < 2 ? 32 : 64), dq);
+  f4 a[NB], kl[NB];
+  {
+    Blk B, A[2];
+    load_blk(B, X0 + cb * 16 * KD, KD);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = I * BS + out_row(e), c = cb * 16 + out_col();
-        const float dx = -(__expf(gx_excl(cd, i, c)) * a[e] + ap[e]);
-        const float dk = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[e] + k2[e] - k3[e];
-        const long long o = (rowbase + i) * KD + c;
-        p.g.dxC[o] = dx;
-        p.g.dkC[o] = dk;
-        p.g.dqC[o] = dq[e];
-        const float outv = dprim[i * KD + c] - kh[i * KD + c];
-        s.dG[i][c] = outv * ddp[i * KD + c] - s.Uh[i][c] * dk;
-      }
+    for (int I0 = 0; I0 < NB; I0 += 2) {
+      load_blk(A[0], dw + I0 * BS * KD, KD);
+      load_blk(A[1], dw + (I0 + 1) * BS * KD, KD);
+      a[I0] = mma_blk(A[0], B, zero4());
+      a[I0 + 1] = mma_blk(A[1], B, zero4());
     }
-  __syncthreads();
-  if (threadIdx.x < KD) {
-    const int c = threadIdx.x;
-    float acc = 0.f;
-    for (int v = 0; v < KD; ++v) acc += XC[c * KD + v] * lam[c * KD + v];
-    for (int i = BT - 1; i >= 0; --i) {
-      acc += s.dG[i][c];
-      if (i + 1 < BT) acc += s.gam[i + 1] * s.Uh[i + 1][c] * p.g.dxC[(rowbase + i + 1) * KD + c];
-      p.g.dgC[(rowbase + i) * KD + c] = acc;
+    load_blk(B, lam + cb * 16 * KD, KD);
+#pragma unroll
+    for (int I0 = 0; I0 < NB; I0 += 2) {
+      load_blk(A[0], wv + I0 * BS * KD, KD);
+      load_blk(A[1], wv + (I0 + 1) * BS * KD, KD);
+      kl[I0] = mma_blk(A[0], B, zero4());
+      kl[I0 + 1] = mma_blk(A[1], B, zero4());
     }
   }
+  float Su[NB][4], Sdd[NB][4], So[NB][4];
+  load_slab(Su, uh, cb);
+  load_slab(Sdd, ddp, cb);
+  load_slab(So, dprim, cb);
+  {
+    float Sk[NB][4];
+    load_slab(Sk, kh, cb);
+#pragma unroll
+    for (int J = 0; J < NB; ++J)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) So[J][e] -= Sk[J][e];  // C-op output o = d - k
+  }
+  __syncthreads();  // M1, M2, gam complete
+  auto U = [&](int j, int cc) { return uh[j * KD + cc]; };
+  auto Xg = [&](int j, int cc) { return s.gam[j] * uh[j * KD + cc]; };
+  auto DO = [&](int j, int cc) { return ddp[j * KD + cc]; };
+  float Sx[NB][4];
+#pragma unroll
+  for (int J = 0; J < NB; ++J)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Sx[J][e] = s.gam[J * BS + r4 + e] * Su[J][e];
+  float* dg = p.g.dgC + rowbase * KD;
+#pragma unroll 1
+  for (int I = 0; I < NB; ++I) {
+    const f4 ap = apply_slab<true>(cd, s.M1, Su, I, cb, U);
+    const f4 k2 = apply_t_slab<false>(cd, s.M2, Sdd, I, cb, DO);
+    const f4 k3 = apply_t_slab<true>(cd, s.M1, Sx, I, cb, Xg);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + r4 + e;
+      const float dx = -(__expf(gx_excl(cd, i, c)) * a[I][e] + ap[e]);
+      const float dk = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[I][e] + k2[e] - k3[e];
+      const long long o = (rowbase + i) * KD + c;
+      p.g.dxC[o] = dx;
+      p.g.dkC[o] = dk;
+      dg[i * KD + c] = So[I][e] * Sdd[I][e] - Su[I][e] * dk;
+      p.g.xdx[o] = Sx[I][e] * dx;
+    }
+  }
+  __syncthreads();  // M1 free: P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) into M1
+  decayed_gram<false>(
+      cd, [&](int i, int cc) { return ddp[i * KD + cc]; }, [&](int j, int cc) { return uh[j * KD + cc]; },
+      false, s.M1);
+  // dq = (dd e^G) X0 + P' w
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    f4 dq = mma_k32([&](int m, int aa) {
+                      const int i = I * BS + m;
+                      return ddp[i * KD + aa] * __expf(cd.G[i][aa]);
+                    },
+                    [&](int aa, int nn) { return X0[aa * KD + cb * 16 + nn]; }, KD, zero4());
+    dq = mma_k32([&](int m, int j) { return s.M1[(I * BS + m) * LS + j]; },
+                 [&](int j, int nn) { return wv[j * KD + cb * 16 + nn]; }, (I < 2 ? 32 : 64), dq);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p.g.dqC[(rowbase + I * BS + r4 + e) * KD + c] = dq[e];
+  }
+  __syncthreads();
+  close_decay_gradient(XC, lam, dg, p.g.xdx + rowbase * KD);
 }
 
 // ---------------------------------------------------------------------------

@@ -408,3 +408,153 @@ __device__ void plain_pair(FX X, FY Y, bool strict, float* M) {
 }
 
 }  // namespace sd
+
+namespace sd {
+
+// ---------------------------------------------------------------------------
+// Register-fragment helpers for the chunk-parallel kernels.
+// A "block" is 16 rows x 128 K-contiguous fp32 values; its MFMA A- and B-fragment
+// addressing is identical (lane m = lane&15 owns row m, 8 consecutive K).
+// A "slab" is one 16-column block of a token panel, held in the MFMA output /
+// K=16 B-operand layout: slab[J][e] = P[J*16 + (lane>>4)*4 + e][cb*16 + (lane&15)].
+// ---------------------------------------------------------------------------
+struct Blk { float4 v[4][2]; };
+
+__device__ __forceinline__ float4 ld4g(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+__device__ __forceinline__ void load_blk(Blk& b, const float* rows, int ld) {
+  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+  const float* a = rows + (long long)m * ld + kq;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    b.v[ks][0] = ld4g(a + ks * 32);
+    b.v[ks][1] = ld4g(a + ks * 32 + 4);
+  }
+}
+
+__device__ __forceinline__ f4 mma3v(const float* av, const float* bv, f4 acc) {
+  bf16x8 ah, al, bh, bl;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    __bf16 h, lo;
+    split_bf(av[e], h, lo);
+    ah[e] = h; al[e] = lo;
+    split_bf(bv[e], h, lo);
+    bh[e] = h; bl[e] = lo;
+  }
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ f4 mma_blk(const Blk& A, const Blk& B, f4 acc) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const float av[8] = {A.v[ks][0].x, A.v[ks][0].y, A.v[ks][0].z, A.v[ks][0].w,
+                         A.v[ks][1].x, A.v[ks][1].y, A.v[ks][1].z, A.v[ks][1].w};
+    const float bv[8] = {B.v[ks][0].x, B.v[ks][0].y, B.v[ks][0].z, B.v[ks][0].w,
+                         B.v[ks][1].x, B.v[ks][1].y, B.v[ks][1].z, B.v[ks][1].w};
+    acc = mma3v(av, bv, acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ void load_slab(float (&s)[NB][4], const float* panel, int cb) {
+  const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+#pragma unroll
+  for (int J = 0; J < NB; ++J)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[J][e] = panel[(J * BS + r4 + e) * KD + c];
+}
+
+__device__ __forceinline__ f4 mma16s(const float* av, const float* bv, f4 acc) {
+  bf16x4 ah, al, bh, bl;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    __bf16 h, lo;
+    split_bf(av[e], h, lo);
+    ah[e] = h; al[e] = lo;
+    split_bf(bv[e], h, lo);
+    bh[e] = h; bl[e] = lo;
+  }
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
+}
+
+// R_ic = sum_{j<=i} M_ij Y_jc exp(Gx_ic - G_jc) for row block I and this lane's
+// column, with Y given as a slab; Yw(j, c) is read only for wild coordinates.
+template <bool EXCL, class FW>
+__device__ f4 apply_slab(const ChunkDecay& cd, const float* M, const float (&Y)[NB][4], int I, int cb,
+                         FW Yw) {
+  const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
+  f4 tot = zero4();
+#pragma unroll
+  for (int J = 0; J < NB; ++J) {
+    if (J > I) break;
+    const bool wild = cd.wild[J][c];
+    float av[4], bv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      av[e] = M[(I * BS + m) * LS + J * BS + r4 + e];
+      bv[e] = wild ? 0.f : Y[J][e] * __expf(cd.R[J][c] - cd.G[J * BS + r4 + e][c]);
+    }
+    // lanes hold B columns n = lane&15 = this lane's c: B[k][n] = Yhat[J*16 + k][c]
+    const f4 a2 = mma16s(av, bv, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + r4 + e;
+      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+      float add;
+      if (wild) {
+        add = 0.f;
+        for (int j = J * BS; j < J * BS + BS; ++j)
+          add += M[i * LS + j] * Yw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      } else {
+        add = __expf(gx - cd.R[J][c]) * a2[e];
+      }
+      tot[e] += add;
+    }
+  }
+  return tot;
+}
+
+// R_jc = sum_{i>=j} M_ij X_ic exp(Gx_ic - G_jc) for row block Jb, X as a slab.
+template <bool EXCL, class FW>
+__device__ f4 apply_t_slab(const ChunkDecay& cd, const float* M, const float (&X)[NB][4], int Jb,
+                           int cb, FW Xw) {
+  const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
+  f4 acc = zero4();
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    if (I < Jb) continue;
+    float av[4], bv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + r4 + e;
+      av[e] = M[i * LS + Jb * BS + m];
+      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+      bv[e] = X[I][e] * __expf(gx - cd.R[Jb][c]);
+    }
+    acc = mma16s(av, bv, acc);
+  }
+  f4 res;
+  const bool wild = cd.wild[Jb][c];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int j = Jb * BS + r4 + e;
+    if (wild) {
+      float s = 0.f;
+      for (int i = j; i < BT; ++i) {
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        s += M[i * LS + j] * Xw(i, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      }
+      res[e] = s;
+    } else {
+      res[e] = __expf(cd.R[Jb][c] - cd.G[j][c]) * acc[e];
+    }
+  }
+  return res;
+}
+
+}  // namespace sd
