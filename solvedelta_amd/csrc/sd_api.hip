@@ -19,6 +19,12 @@ struct Carver {
     off += count * sizeof(T);
     return p;
   }
+  SP take_sp(size_t count) {
+    SP s;
+    s.hi = take<__bf16>(count);
+    s.lo = take<__bf16>(count);
+    return s;
+  }
 };
 
 FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
@@ -35,15 +41,15 @@ FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
   w.delta = c.take<float>(panel);
   w.d = c.take<float>(panel);
   w.wS = c.take<float>(panel);
-  w.Wc = c.take<float>(panel);
+  w.Wc = c.take_sp(panel);
   w.Uc = c.take<float>(panel);
-  w.Kc = c.take<float>(panel);
+  w.Kc = c.take_sp(panel);
   w.Gam = c.take<float>(n * NT * kKD);
-  w.Ws = c.take<float>(panel);
+  w.Ws = c.take_sp(panel);
   w.Us = c.take<float>(panel);
-  w.Ks = c.take<float>(panel);
-  w.Qs = c.take<float>(panel);
-  w.Ps = c.take<float>(n * NT * kBT * kBT);
+  w.Ks = c.take_sp(panel);
+  w.Qs = c.take_sp(panel);
+  w.Ps = c.take_sp(n * NT * kBT * kBT);
   if (total) *total = c.off + 256;
   return w;
 }
@@ -55,7 +61,11 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   BwdWs w;
   w.Lc = c.take<float>(states);
   w.Ls = c.take<float>(states);
-  float** panels[] = {&w.dU, &w.Wk, &w.At1, &w.B1, &w.B1t, &w.Ant, &w.dwS, &w.dwC, &w.de, &w.dchi,
+  w.Wk = c.take_sp(panel);
+  w.At1 = c.take_sp(panel);
+  w.B1t = c.take_sp(panel);
+  w.Ant = c.take_sp(panel);
+  float** panels[] = {&w.dU, &w.B1, &w.dwS, &w.dwC, &w.de, &w.dchi,
                       &w.dd, &w.dgS, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
                       &w.dgC, &w.uh, &w.xdx};
   for (float** pp : panels) *pp = c.take<float>(panel);

@@ -91,13 +91,13 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
     s.A[(idx / BT) * LS + idx % BT] = p.f.As[cidx * BT * BT + idx];
-    s.P[(idx / BT) * LS + idx % BT] = p.f.Ps[cidx * BT * BT + idx];
+    s.P[(idx / BT) * LS + idx % BT] = sp_load(p.f.Ps, cidx * BT * BT + idx);
   }
   __syncthreads();
   mat64_mul(s.P, s.A, s.N);
   __syncthreads();
   const int w = wave_id();
-  const float* Kt = p.f.Ks + cidx * KD * BT;
+  const long long kbase = cidx * KD * BT;
   for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_l N_lj dO_l ;  Wk_j = sum_i A_ij K^_i
@@ -105,14 +105,14 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
                       [&](int k, int nn) { return dout_at(p, b, t0 + k, hh, cb * 16 + nn); }, BT,
                       zero4());
       f4 wk = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
-                      [&](int k, int nn) { return Kt[(long long)(cb * 16 + nn) * BT + k]; }, BT,
-                      zero4());
+                      [&](int k, int nn) { return sp_load(p.f.Ks, kbase + (cb * 16 + nn) * BT + k); },
+                      BT, zero4());
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + Jb * BS + out_row(e);
         const int c = cb * 16 + out_col();
         p.g.dU[row * KD + c] = du[e];
-        p.g.Wk[row * KD + c] = wk[e];
+        sp_store(p.g.Wk, row * KD + c, wk[e]);
       }
     }
   for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
@@ -122,9 +122,9 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {  // chunk-transposed panels
     const int c = idx / BT, i = idx % BT;
     const long long o = (rowbase + i) * KD + c, ot = cidx * KD * BT + idx;
-    p.g.Ant[ot] = -p.f.e[o] * __expf(cd.G[i][c]);
-    p.g.At1[ot] = p.f.Qs[o];
-    p.g.B1t[ot] = dout_at(p, b, t0 + i, hh, c);
+    sp_store(p.g.Ant, ot, -p.f.e[o] * __expf(cd.G[i][c]));
+    sp_store(p.g.At1, ot, sp_load(p.f.Qs, o));
+    sp_store(p.g.B1t, ot, dout_at(p, b, t0 + i, hh, c));
   }
 }
 
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   mat64_mul(s.P, s.A, s.N);
   __syncthreads();
   const float* ddl = p.g.ddelta + rowbase * KD;
-  const float* Kt = p.f.Kc + cidx * KD * BT;
+  const long long kbase = cidx * KD * BT;
   for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_i A_ij ddelta_i + sum_l N_lj k_l ;  Wk_j = sum_i A_ij K^_i
@@ -394,14 +394,14 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       du = mma_k32([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; },
                    [&](int k, int nn) { return s.Kh[k][cb * 16 + nn]; }, BT, du);
       f4 wk = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
-                      [&](int k, int nn) { return Kt[(long long)(cb * 16 + nn) * BT + k]; }, BT,
-                      zero4());
+                      [&](int k, int nn) { return sp_load(p.f.Kc, kbase + (cb * 16 + nn) * BT + k); },
+                      BT, zero4());
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + Jb * BS + out_row(e);
         const int c = cb * 16 + out_col();
         p.g.dU[row * KD + c] = du[e];
-        p.g.Wk[row * KD + c] = wk[e];
+        sp_store(p.g.Wk, row * KD + c, wk[e]);
       }
     }
   for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
@@ -412,9 +412,9 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {  // chunk-transposed panels
     const int c = idx / BT, i = idx % BT;
     const long long ot = cidx * KD * BT + idx;
-    p.g.At1[ot] = ddp[i * KD + c] * __expf(cd.G[i][c]);
-    p.g.B1t[ot] = s.Kh[i][c];
-    p.g.Ant[ot] = -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c));
+    sp_store(p.g.At1, ot, ddp[i * KD + c] * __expf(cd.G[i][c]));
+    sp_store(p.g.B1t, ot, s.Kh[i][c]);
+    sp_store(p.g.Ant, ot, -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c)));
   }
 }
 

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
-        p.Wc[row * KD + c] = -aw[e];
+        sp_store(p.Wc, row * KD + c, -aw[e]);
         p.Uc[row * KD + c] = au[e];
       }
     }
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   const long long cbase = ((long long)n * p.NT + ch);
   for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {
     const int c = idx / BT, i = idx % BT;
-    p.Kc[cbase * KD * BT + idx] = s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
+    sp_store(p.Kc, cbase * KD * BT + idx, s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]));
   }
   if (threadIdx.x < KD) p.Gam[cbase * KD + threadIdx.x] = __expf(cd.G[BT - 1][threadIdx.x]);
 }
@@ -135,226 +135,262 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
 // The next chunk's fragments are loaded into registers while the current chunk
 // computes, so the global latency leaves the sequential critical path.
 // ---------------------------------------------------------------------------
+// State workgroup geometry: 4 waves own a 128 x 16 state tile; wave w holds
+// state rows 32w..32w+31 (SRB = 2 row blocks) in MFMA accumulators and computes
+// the w / o tile of token block w; 8 workgroups cover the 128 state columns of
+// a sequence.  (One wave per SIMD: the per-chunk MFMA chain is the critical
+// path, so spreading the tile over more waves per CU only serialises them.)
+constexpr int SCOLS = 16;
+constexpr int SWAVES = 4;
+constexpr int SRB = KD / 16 / SWAVES;
+constexpr int STHREADS = SWAVES * 64;
+constexpr int STILES = KD / SCOLS;
+
 struct StateSmem {
-  float Xt[16][KD + 4];  // X0 tile, transposed [col][row]
-  float wt[16][BT + 4];  // w tile, transposed [col][token]
+  __bf16 Xh[SCOLS][KD + 8];  // X0 tile, transposed [col][row], split hi / lo
+  __bf16 Xl[SCOLS][KD + 8];
+  __bf16 wh[SCOLS][BT + 8];  // w tile, transposed [col][token], split hi / lo
+  __bf16 wl[SCOLS][BT + 8];
 };
+
+struct Frag { bf16x8 h, l; };
 
 template <bool COL_OUT, bool INJ>
 struct StateFrags {
-  float4 W[4][2];
-  float4 K[2][2][2];
-  float4 Q[COL_OUT ? 4 : 1][2];
-  float4 P[COL_OUT ? 2 : 1][2];
-  float4 A1[INJ ? 2 : 1][2][2];
-  float4 B1[INJ ? 2 : 1][2];
+  Frag W[4];
+  Frag K[SRB][2];
+  Frag Q[COL_OUT ? 4 : 1];
+  Frag P[COL_OUT ? 2 : 1];
+  Frag A1[INJ ? SRB : 1][2];
+  Frag B1[INJ ? 2 : 1];
   float U[4];
-  float4 gam[2];
+  float4 gam[SRB];
 };
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ bf16x8 ldb8(const __bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ Frag ldfrag(const SP& sp, long long off) {
+  Frag f;
+  f.h = ldb8(sp.hi + off);
+  f.l = ldb8(sp.lo + off);
+  return f;
+}
 
 template <bool COL_OUT, bool INJ>
 __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
                                                  StateFrags<COL_OUT, INJ>& f) {
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+  const int tb = w;  // this wave's token block
   const long long cidx = (long long)n * p.NT + ch;
   const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
-  const int col = tile * 16 + m;
-  const float* Wb = p.Wneg + (rowbase + w * 16 + m) * KD + kq;
+  const long long wb = (rowbase + tb * 16 + m) * KD + kq;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    f.W[ks][0] = ld4(Wb + ks * 32);
-    f.W[ks][1] = ld4(Wb + ks * 32 + 4);
-  }
-  const float* Kb = p.Kt + cidx * KD * BT;
+  for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldfrag(p.Wneg, wb + ks * 32);
 #pragma unroll
-  for (int q = 0; q < 2; ++q)
+  for (int q = 0; q < SRB; ++q)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const float* a = Kb + (long long)((2 * w + q) * 16 + m) * BT + ks * 32 + kq;
-      f.K[q][ks][0] = ld4(a);
-      f.K[q][ks][1] = ld4(a + 4);
-    }
+    for (int ks = 0; ks < 2; ++ks)
+      f.K[q][ks] = ldfrag(p.Kt, cidx * KD * BT + (long long)((SRB * w + q) * 16 + m) * BT + ks * 32 + kq);
+  const int col = tile * SCOLS + m;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) f.U[e] = p.U[(rowbase + w * 16 + (l >> 4) * 4 + e) * KD + col];
+  for (int e = 0; e < 4; ++e) f.U[e] = p.U[(rowbase + tb * 16 + (l >> 4) * 4 + e) * KD + col];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) f.gam[q] = ld4(p.Gam + cidx * KD + (2 * w + q) * 16 + (l >> 4) * 4);
+  for (int q = 0; q < SRB; ++q) f.gam[q] = ld4(p.Gam + cidx * KD + (SRB * w + q) * 16 + (l >> 4) * 4);
   if constexpr (COL_OUT) {
-    const float* Qb = p.Q + (rowbase + w * 16 + m) * KD + kq;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      f.Q[ks][0] = ld4(Qb + ks * 32);
-      f.Q[ks][1] = ld4(Qb + ks * 32 + 4);
-    }
-    const float* Pb = p.P + cidx * BT * BT + (long long)(w * 16 + m) * BT + kq;
+    for (int ks = 0; ks < 4; ++ks) f.Q[ks] = ldfrag(p.Q, wb + ks * 32);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      f.P[ks][0] = ld4(Pb + ks * 32);
-      f.P[ks][1] = ld4(Pb + ks * 32 + 4);
-    }
+    for (int ks = 0; ks < 2; ++ks)
+      f.P[ks] = ldfrag(p.P, cidx * BT * BT + (long long)(tb * 16 + m) * BT + ks * 32 + kq);
   }
   if constexpr (INJ) {
-    const float* Ab = p.At1 + cidx * KD * BT;
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int q = 0; q < SRB; ++q)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const float* a = Ab + (long long)((2 * w + q) * 16 + m) * BT + ks * 32 + kq;
-        f.A1[q][ks][0] = ld4(a);
-        f.A1[q][ks][1] = ld4(a + 4);
-      }
-    const float* Bb = p.B1 + cidx * KD * BT + (long long)col * BT + kq;
+      for (int ks = 0; ks < 2; ++ks)
+        f.A1[q][ks] =
+            ldfrag(p.At1, cidx * KD * BT + (long long)((SRB * w + q) * 16 + m) * BT + ks * 32 + kq);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      f.B1[ks][0] = ld4(Bb + ks * 32);
-      f.B1[ks][1] = ld4(Bb + ks * 32 + 4);
-    }
+    for (int ks = 0; ks < 2; ++ks)
+      f.B1[ks] = ldfrag(p.B1, cidx * KD * BT + (long long)col * BT + ks * 32 + kq);
   }
 }
 
-// 3-term split-bf16 MFMA on register fragments (8 fp32 values each).
-__device__ __forceinline__ f4 mma3(const float4& a0, const float4& a1, const float4& b0,
-                                   const float4& b1, f4 acc) {
-  const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-  const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-  bf16x8 ah, al, bh, bl;
+// hi*hi + hi*lo + lo*hi on pre-split fragments.
+__device__ __forceinline__ f4 mma3f(const Frag& a, const Frag& b, f4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ void stage_split4(__bf16* hi, __bf16* lo, f4 v) {
+  bf16x4 h, l;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    __bf16 h, lo;
-    split_bf(av[e], h, lo);
-    ah[e] = h; al[e] = lo;
-    split_bf(bv[e], h, lo);
-    bh[e] = h; bl[e] = lo;
+  for (int e = 0; e < 4; ++e) {
+    __bf16 a, b;
+    split_bf(v[e], a, b);
+    h[e] = a;
+    l[e] = b;
   }
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+  *reinterpret_cast<bf16x4*>(hi) = h;
+  *reinterpret_cast<bf16x4*>(lo) = l;
+}
+
+// One chunk of the sequential pass with its operand fragments already in registers.
+template <bool COL_OUT, bool INJ>
+__device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, int n, int ch, int tile,
+                                           const StateFrags<COL_OUT, INJ>& cur, f4 (&X)[SRB]) {
+  const int NS = p.NT + 1;
+  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
+  const int tb = w;
+  const long long sidx = (long long)n * NS + ch;
+  const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
+  // save X0 and stage it split and transposed ([col][row]) for the B operand
+  const int col = tile * SCOLS + m;
+#pragma unroll
+  for (int q = 0; q < SRB; ++q) {
+    const int row0 = (SRB * w + q) * 16 + r4;
+    if (p.Xs)
+      for (int e = 0; e < 4; ++e) p.Xs[sidx * KD * KD + (long long)(row0 + e) * KD + col] = X[q][e];
+    stage_split4(&s.Xh[m][row0], &s.Xl[m][row0], X[q]);
+  }
+  __syncthreads();
+  // w = U + Wneg X  (token block tb, column half)
+  const int lc = m;  // local column of this lane in the w / o tile
+  f4 acc = {cur.U[0], cur.U[1], cur.U[2], cur.U[3]};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    Frag xb;
+    xb.h = ldb8(&s.Xh[lc][ks * 32 + kq]);
+    xb.l = ldb8(&s.Xl[lc][ks * 32 + kq]);
+    acc = mma3f(cur.W[ks], xb, acc);
+  }
+  const int gcol = tile * SCOLS + lc;
+  for (int e = 0; e < 4; ++e) p.wout[(rowbase + tb * 16 + r4 + e) * KD + gcol] = acc[e];
+  stage_split4(&s.wh[lc][tb * 16 + r4], &s.wl[lc][tb * 16 + r4], acc);
+  __syncthreads();
+  // X = Gamma X + Kt w (+ At1 B1): the recurrence's critical path
+  Frag wf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    wf[ks].h = ldb8(&s.wh[m][ks * 32 + kq]);
+    wf[ks].l = ldb8(&s.wl[m][ks * 32 + kq]);
+  }
+#pragma unroll
+  for (int q = 0; q < SRB; ++q) {
+    const float gv[4] = {cur.gam[q].x, cur.gam[q].y, cur.gam[q].z, cur.gam[q].w};
+    for (int e = 0; e < 4; ++e) X[q][e] *= gv[e];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      X[q] = mma3f(cur.K[q][ks], wf[ks], X[q]);
+      if constexpr (INJ) X[q] = mma3f(cur.A1[q][ks], cur.B1[ks], X[q]);
+    }
+  }
+  if constexpr (COL_OUT) {
+    // o = Q X0 + P w  (token block tb, column half), written as bf16 to out[b,t,h,v]
+    f4 o = zero4();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      Frag xb;
+      xb.h = ldb8(&s.Xh[lc][ks * 32 + kq]);
+      xb.l = ldb8(&s.Xl[lc][ks * 32 + kq]);
+      o = mma3f(cur.Q[ks], xb, o);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (ks == 1 && tb < 2) break;
+      o = mma3f(cur.P[ks], wf[ks], o);
+    }
+    const int b = n / p.H, hh = n % p.H;
+    for (int e = 0; e < 4; ++e) {
+      const int t = ch * BT + tb * 16 + r4 + e;
+      if (t < p.T && gcol < p.cols)
+        p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + gcol] = f2bf(o[e]);
+    }
+  }
+  __syncthreads();
 }
 
 template <bool COL_OUT, bool INJ>
-__global__ __launch_bounds__(NTHREADS) void k_state(StateParams p) {
+__global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   __shared__ __align__(16) StateSmem s;
   const int NS = p.NT + 1;  // state slots per sequence
   // Workgroups are dispatched round-robin over the 8 XCDs by linear id; when the
-  // sequence count allows, map ids so that the 8 column tiles of a sequence run
+  // sequence count allows, map ids so that the column tiles of a sequence run
   // on one XCD and share its L2 copy of the chunk panels.
   int tile, n;
   {
-    const int L = blockIdx.x, nseq = gridDim.x / 8;
+    const int L = blockIdx.x, nseq = gridDim.x / STILES;
     if (nseq % 8 == 0) {
       const int x = L % 8, j = L / 8;
-      tile = j % 8;
-      n = (j / 8) * 8 + x;
+      tile = j % STILES;
+      n = (j / STILES) * 8 + x;
     } else {
-      tile = L % 8;
-      n = L / 8;
+      tile = L % STILES;
+      n = L / STILES;
     }
   }
-  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
-  const int col = tile * 16 + m;  // this lane's state column
-  f4 X[2];
-  for (int q = 0; q < 2; ++q)
+  const int w = wave_id(), l = lane_id(), m = l & 15, r4 = (l >> 4) * 4;
+  f4 X[SRB];
+  for (int q = 0; q < SRB; ++q)
     for (int e = 0; e < 4; ++e) {
-      const int row = (2 * w + q) * 16 + r4 + e;
+      const int row = (SRB * w + q) * 16 + r4 + e, col = tile * SCOLS + m;
       float x = 0.f;
       if (p.init && row < p.rows && col < p.cols)
         x = p.init_transposed ? p.init[(long long)n * p.rows * p.cols + (long long)col * p.rows + row]
                               : p.init[(long long)n * p.rows * p.cols + (long long)row * p.cols + col];
       X[q][e] = x;
     }
-  StateFrags<COL_OUT, INJ> cur, nxt;
-  load_state_frags(p, n, p.rev ? p.NT - 1 : 0, tile, cur);
-  for (int it = 0; it < p.NT; ++it) {
-    const int ch = p.rev ? p.NT - 1 - it : it;
-    const long long sidx = (long long)n * NS + ch;
-    const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
-    if (it + 1 < p.NT) load_state_frags(p, n, p.rev ? ch - 1 : ch + 1, tile, nxt);
-    // save X0 and stage it transposed ([col][row]) for the B operand
-    for (int q = 0; q < 2; ++q) {
-      const int row0 = (2 * w + q) * 16 + r4;
-      if (p.Xs)
-        for (int e = 0; e < 4; ++e) p.Xs[sidx * KD * KD + (long long)(row0 + e) * KD + col] = X[q][e];
-      *reinterpret_cast<float4*>(&s.Xt[m][row0]) = make_float4(X[q][0], X[q][1], X[q][2], X[q][3]);
+  // Operand fragments are prefetched ahead into rotating register buffers (no
+  // copies, so a buffer's loads are only waited on when it becomes current).
+  const int NT = p.NT;
+  auto chunk_of = [&](int it) { return p.rev ? NT - 1 - it : it; };
+  if constexpr (SWAVES == 4) {  // one wave per SIMD: room for two chunks ahead
+    StateFrags<COL_OUT, INJ> f0, f1, f2;
+    load_state_frags(p, n, chunk_of(0), tile, f0);
+    if (NT > 1) load_state_frags(p, n, chunk_of(1), tile, f1);
+    for (int it = 0; it < NT; it += 3) {
+      if (it + 2 < NT) load_state_frags(p, n, chunk_of(it + 2), tile, f2);
+      state_step(p, s, n, chunk_of(it), tile, f0, X);
+      if (it + 1 >= NT) break;
+      if (it + 3 < NT) load_state_frags(p, n, chunk_of(it + 3), tile, f0);
+      state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
+      if (it + 2 >= NT) break;
+      if (it + 4 < NT) load_state_frags(p, n, chunk_of(it + 4), tile, f1);
+      state_step(p, s, n, chunk_of(it + 2), tile, f2, X);
     }
-    __syncthreads();
-    // w = U + Wneg X  (token block w)
-    f4 acc = {cur.U[0], cur.U[1], cur.U[2], cur.U[3]};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const float* xb = &s.Xt[m][ks * 32 + kq];
-      acc = mma3(cur.W[ks][0], cur.W[ks][1], ld4(xb), ld4(xb + 4), acc);
+  } else {
+    StateFrags<COL_OUT, INJ> f0, f1;  // one chunk ahead (register budget)
+    load_state_frags(p, n, chunk_of(0), tile, f0);
+    for (int it = 0; it < NT; it += 2) {
+      if (it + 1 < NT) load_state_frags(p, n, chunk_of(it + 1), tile, f1);
+      state_step(p, s, n, chunk_of(it), tile, f0, X);
+      if (it + 1 >= NT) break;
+      if (it + 2 < NT) load_state_frags(p, n, chunk_of(it + 2), tile, f0);
+      state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
     }
-    for (int e = 0; e < 4; ++e) {
-      const int tk = w * 16 + r4 + e;
-      p.wout[(rowbase + tk) * KD + col] = acc[e];
-    }
-    *reinterpret_cast<float4*>(&s.wt[m][w * 16 + r4]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    __syncthreads();
-    if constexpr (COL_OUT) {
-      // o = Q X0 + P w  (token block w), written as bf16 to out[b,t,h,v]
-      f4 o = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const float* xb = &s.Xt[m][ks * 32 + kq];
-        o = mma3(cur.Q[ks][0], cur.Q[ks][1], ld4(xb), ld4(xb + 4), o);
-      }
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks == 1 && w < 2) break;
-        const float* wb = &s.wt[m][ks * 32 + kq];
-        o = mma3(cur.P[ks][0], cur.P[ks][1], ld4(wb), ld4(wb + 4), o);
-      }
-      const int b = n / p.H, hh = n % p.H;
-      for (int e = 0; e < 4; ++e) {
-        const int t = ch * BT + w * 16 + r4 + e;
-        if (t < p.T && col < p.cols)
-          p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + col] = f2bf(o[e]);
-      }
-    }
-    // X = Gamma X + Kt w (+ At1 B1)
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const float gv[4] = {cur.gam[q].x, cur.gam[q].y, cur.gam[q].z, cur.gam[q].w};
-      for (int e = 0; e < 4; ++e) X[q][e] *= gv[e];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const float* wb = &s.wt[m][ks * 32 + kq];
-        X[q] = mma3(cur.K[q][ks][0], cur.K[q][ks][1], ld4(wb), ld4(wb + 4), X[q]);
-        if constexpr (INJ) X[q] = mma3(cur.A1[q][ks][0], cur.A1[q][ks][1], cur.B1[ks][0], cur.B1[ks][1], X[q]);
-      }
-    }
-    __syncthreads();
-    cur = nxt;
   }
   // final state (also kept as slot NT for the backward)
-  if (p.Xs && !p.rev)
-    for (int q = 0; q < 2; ++q)
-      for (int e = 0; e < 4; ++e) {
-        const int row = (2 * w + q) * 16 + r4 + e;
-        p.Xs[((long long)n * NS + p.NT) * KD * KD + (long long)row * KD + col] = X[q][e];
+  for (int q = 0; q < SRB; ++q)
+    for (int e = 0; e < 4; ++e) {
+      const int row = (SRB * w + q) * 16 + r4 + e, col = tile * SCOLS + m;
+      if (p.Xs && !p.rev) p.Xs[((long long)n * NS + p.NT) * KD * KD + (long long)row * KD + col] = X[q][e];
+      if (p.fin && row < p.rows && col < p.cols) {
+        const long long base = (long long)n * p.rows * p.cols;
+        if (p.fin_transposed)
+          p.fin[base + (long long)col * p.rows + row] = X[q][e];
+        else
+          p.fin[base + (long long)row * p.cols + col] = X[q][e];
       }
-  if (p.fin) {
-    for (int q = 0; q < 2; ++q)
-      for (int e = 0; e < 4; ++e) {
-        const int row = (2 * w + q) * 16 + r4 + e;
-        if (row < p.rows && col < p.cols) {
-          const long long base = (long long)n * p.rows * p.cols;
-          if (p.fin_transposed)
-            p.fin[base + (long long)col * p.rows + row] = X[q][e];
-          else
-            p.fin[base + (long long)row * p.cols + col] = X[q][e];
-        }
-      }
-  }
+    }
 }
 
 void launch_state(const char* name, const StateParams& sp, bool col_out, int nseq,
                   hipStream_t st) {
-  const dim3 grid((KD / 16) * nseq), blk(NTHREADS);
+  const dim3 grid(STILES * nseq), blk(STHREADS);
   if (col_out)
     SD_LAUNCH(name, (k_state<true, false>), grid, blk, 0, st, sp);
-  else if (sp.At1)
+  else if (sp.At1.hi)
     SD_LAUNCH(name, (k_state<false, true>), grid, blk, 0, st, sp);
   else
     SD_LAUNCH(name, (k_state<false, false>), grid, blk, 0, st, sp);
@@ -493,14 +529,14 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       cd, [&](int i, int c) { return s.Pb[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
       false, s.M);
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
-    p.Ps[cidx * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
+    sp_store(p.Ps, cidx * BT * BT + idx, s.M[(idx / BT) * LS + idx % BT]);
   for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {
     const int c = idx / BT, i = idx % BT;
-    p.Ks[cidx * KD * BT + idx] = s.Pc[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
+    sp_store(p.Ks, cidx * KD * BT + idx, s.Pc[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]));
   }
   for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
     const int i = idx / KD, c = idx % KD;
-    p.Qs[(rowbase + i) * KD + c] = s.Pb[i][c] * __expf(cd.G[i][c]);
+    sp_store(p.Qs, (rowbase + i) * KD + c, s.Pb[i][c] * __expf(cd.G[i][c]));
   }
   __syncthreads();
   // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
@@ -533,7 +569,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
-        p.Ws[row * KD + c] = -aw[e];
+        sp_store(p.Ws, row * KD + c, -aw[e]);
         p.Us[row * KD + c] = au[e];
       }
     }

@@ -8,6 +8,25 @@
 
 namespace sd {
 
+// A "split panel": an fp32 panel stored as bf16 high part + bf16 residual
+// (same bytes as fp32, ~16 mantissa bits).  MFMA consumers load both halves as
+// ready-made bf16 fragments instead of converting fp32 operands on every use.
+struct SP {
+  __bf16* hi;
+  __bf16* lo;
+};
+
+#ifdef __HIPCC__
+__device__ __forceinline__ void sp_store(const SP& sp, long long i, float x) {
+  const __bf16 h = (__bf16)x;
+  sp.hi[i] = h;
+  sp.lo[i] = (__bf16)(x - (float)h);
+}
+__device__ __forceinline__ float sp_load(const SP& sp, long long i) {
+  return (float)sp.hi[i] + (float)sp.lo[i];
+}
+#endif
+
 // Forward workspace: every buffer is [n][Tp][128] (token panels) or
 // [n][NT][...] (per-chunk), n = B*H, Tp = NT*64.
 struct FwdWs {
@@ -22,16 +41,16 @@ struct FwdWs {
   float* d;      // primal address d = k + C^T k            [n][Tp][128]
   float* wS;     // S-op w = z - S~^T e                     [n][Tp][128]
   // transient panels
-  float* Wc; float* Uc; float* Kc; float* Gam;
-  float* Ws; float* Us; float* Ks; float* Qs; float* Ps;
+  SP Wc; float* Uc; SP Kc; float* Gam;
+  SP Ws; float* Us; SP Ks; SP Qs; SP Ps;
 };
 
 struct FwdParams {
   sd_inputs in;
   int H, T, r, V, NT, Tp;
   float *Xc, *delta, *d, *Ac, *As, *e, *chi;
-  float* Wc; float* Uc; float* Kc; float* Gam;
-  float* Ws; float* Us; float* Ks; float* Qs; float* Ps;
+  SP Wc; float* Uc; SP Kc; float* Gam;
+  SP Ws; float* Us; SP Ks; SP Qs; SP Ps;
 };
 
 // Sequential chunk pass, forward (state X) or reverse (cotangent lambda):
@@ -39,9 +58,9 @@ struct FwdParams {
 // Kt, At1 are chunk-transposed [128][64]; B1 is chunk-transposed [128 cols][64 tokens].
 struct StateParams {
   int H, T, NT, Tp, rows, cols, rev;
-  const float* Wneg; const float* U; const float* Kt; const float* Gam;
-  const float* At1; const float* B1;  // optional injection (token-major panels)
-  const float* Q; const float* P;  // output operands (COL_OUT)
+  SP Wneg; const float* U; SP Kt; const float* Gam;
+  SP At1; SP B1;  // optional injection
+  SP Q; SP P;     // output operands (COL_OUT)
   float* Xs; float* wout; __bf16* out;
   const float* init; int init_transposed;
   float* fin; int fin_transposed;
@@ -66,7 +85,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
 struct BwdWs {
   float* Lc;   // C-op chunk-end cotangents                [n][NT+1][128][128]
   float* Ls;   // S-op chunk-end cotangents
-  float* dU; float* Wk; float* At1; float* B1; float* B1t; float* Ant;  // reverse-pass panels (reused)
+  float* dU; SP Wk; SP At1; float* B1; SP B1t; SP Ant;  // reverse-pass panels (reused)
   float* dwS; float* dwC;          // dw of each op           [n][Tp][128]
   float* de; float* dchi; float* dd; float* dgS;
   float* ddelta; float* du_src; float* dk_src;
