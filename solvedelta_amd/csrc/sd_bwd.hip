@@ -33,20 +33,22 @@ __device__ __forceinline__ const __bf16* brow(const sd_view& v, int b, int t, in
 }
 
 __device__ __forceinline__ float dout_at(const BwdParams& p, int b, int t, int h, int c) {
-  if (!p.dout || t >= p.T || c >= p.V) return 0.f;
-  return bf2f(p.dout[(((long long)b * p.T + t) * p.H + h) * p.V + c]);
+  if (!p.dout) return 0.f;
+  const bool ok = t < p.T && c < p.V;
+  const float x = bf2f(p.dout[(((long long)b * p.T + (t < p.T ? t : p.T - 1)) * p.H + h) * p.V +
+                              (c < p.V ? c : p.V - 1)]);
+  return ok ? x : 0.f;
 }
 
+// Branch-free row load (see load_row2 in the forward kernels).
 __device__ __forceinline__ void ldrow2(const sd_view& v, int b, int t, int h, int T, int w,
                                        float& x0, float& x1) {
   const int l = lane_id();
-  x0 = 0.f;
-  x1 = 0.f;
-  if (t < T) {
-    const __bf16* q = brow(v, b, t, h);
-    if (l < w) x0 = bf2f(q[l]);
-    if (l + 64 < w) x1 = bf2f(q[l + 64]);
-  }
+  const bool tv = t < T;
+  const __bf16* q = brow(v, b, tv ? t : T - 1, h);
+  const float a0 = bf2f(q[l < w ? l : w - 1]), a1 = bf2f(q[l + 64 < w ? l + 64 : w - 1]);
+  x0 = (tv && l < w) ? a0 : 0.f;
+  x1 = (tv && l + 64 < w) ? a1 : 0.f;
 }
 
 __device__ __forceinline__ float norm2(float& x0, float& x1) {

@@ -264,9 +264,10 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
   if (tid < NB * BS) {
     const int B = tid / BS, j = tid % BS, B0 = B * BS;
 #pragma unroll
-    for (int i = 0; i < BS; ++i) {
+    for (int i = 0; i < BS; ++i) {  // compile-time indices keep col[] in registers
       float s = (i == j) ? 1.f : 0.f;
-      for (int m = j; m < i; ++m) s -= L[(B0 + i) * LS + B0 + m] * col[m];
+#pragma unroll
+      for (int m = 0; m < i; ++m) s -= L[(B0 + i) * LS + B0 + m] * col[m];
       col[i] = (i >= j) ? s : 0.f;
     }
   }

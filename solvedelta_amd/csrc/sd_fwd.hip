@@ -34,16 +34,17 @@ __device__ __forceinline__ void l2norm2(float& x0, float& x1, float* rs_out) {
   if (rs_out) *rs_out = rs;
 }
 
+// Branch-free row load (lane holds coords lane and lane+64): out-of-range tokens
+// and coordinates read a valid element and are selected to 0, so unrolled loops
+// can issue every load before the first use.
 __device__ __forceinline__ void load_row2(const sd_view& v, int b, int t, int h, int T, int w,
                                           float& x0, float& x1) {
   const int l = lane_id();
-  x0 = 0.f;
-  x1 = 0.f;
-  if (t < T) {
-    const __bf16* p = vrow(v, b, t, h);
-    if (l < w) x0 = bf2f(p[l]);
-    if (l + 64 < w) x1 = bf2f(p[l + 64]);
-  }
+  const bool tv = t < T;
+  const __bf16* p = vrow(v, b, tv ? t : T - 1, h);
+  const float a0 = bf2f(p[l < w ? l : w - 1]), a1 = bf2f(p[l + 64 < w ? l + 64 : w - 1]);
+  x0 = (tv && l < w) ? a0 : 0.f;
+  x1 = (tv && l + 64 < w) ? a1 : 0.f;
 }
 
 constexpr int PS = KD + 8;  // bf16 panel row stride
@@ -418,7 +419,9 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   const sd_inputs& in = p.in;
   const float* g = (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
                    (long long)hh * in.log_decay.sh;
+  SD_MARK(2, 0);
   build_decay(s.cd, g, in.log_decay.st, t0, T, r);
+  SD_MARK(2, 1);
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id();
 #pragma unroll
@@ -435,6 +438,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     s.Pb[i][l + 64] = x1;
   }
   __syncthreads();
+  SD_MARK(2, 2);
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long cidx = (long long)n * p.NT + ch;
   const float* delta = p.delta + rowbase * KD;
@@ -455,6 +459,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     if ((j / BS) > (i / BS)) s.M[i * LS + j] = 0.f;
   }
   __syncthreads();
+  SD_MARK(2, 3);
   // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}
   const float* X0 = p.Xc + ((long long)n * (p.NT + 1) + ch) * KD * KD;
   for (int q = 0; q < 1; ++q) {
@@ -494,6 +499,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     }
   }
   __syncthreads();
+  SD_MARK(2, 4);
   // sources (one wave per token row; e overwrites u, chi overwrites k)
 #pragma unroll
   for (int i = w; i < BT; i += CW) {
@@ -524,6 +530,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     p.chi[(rowbase + i) * KD + l + 64] = s.Pb[i][l + 64];
   }
   __syncthreads();
+  SD_MARK(2, 5);
   // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i
   decayed_gram<false>(
       cd, [&](int i, int c) { return s.Pb[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
@@ -539,33 +546,39 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     sp_store(p.Qs, (rowbase + i) * KD + c, s.Pb[i][c] * __expf(cd.G[i][c]));
   }
   __syncthreads();
+  SD_MARK(2, 6);
   // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
   decayed_gram<false>(
       cd, [&](int i, int c) { return s.Pa[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
       true, s.M);
+  SD_MARK(2, 7);
   unit_lower_inverse(s.M, &s.Pc[0][0]);
+  SD_MARK(2, 8);
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.As[cidx * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
-  // W = A (e e^G), U = A z with z = sigmoid(write_raw) v read from the inputs
-  for (int cb = w; cb < w + 1; ++cb) {
+  // WY operands staged once: Pa <- e e^G, Pb <- z = sigmoid(write_raw) v
+  for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
+    const int i = idx / KD, c = idx % KD;
+    s.Pa[i][c] *= __expf(cd.G[i][c]);
+  }
+#pragma unroll
+  for (int i = w; i < BT; i += CW) {
+    float v0, v1, w0, w1;
+    load_row2(in.v, b, t0 + i, hh, T, V, v0, v1);
+    load_row2(in.write_raw, b, t0 + i, hh, T, V, w0, w1);
+    s.Pb[i][l] = v0 / (1.f + __expf(-w0));
+    s.Pb[i][l + 64] = v1 / (1.f + __expf(-w1));
+  }
+  __syncthreads();
+  // W = A (e e^G), U = A z
+  {
+    const int cb = w;
+#pragma unroll
     for (int I = 0; I < NB; ++I) {
       const int K = I < 2 ? 32 : 64;
       auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k]; };
-      f4 aw = mma_k32(fa,
-                      [&](int k, int nn) {
-                        const int c = cb * 16 + nn;
-                        return s.Pa[k][c] * __expf(cd.G[k][c]);
-                      },
-                      K, zero4());
-      f4 au = mma_k32(fa,
-                      [&](int k, int nn) {
-                        const int c = cb * 16 + nn, t = t0 + k;
-                        if (t >= T || c >= V) return 0.f;
-                        const float vv = bf2f(vrow(in.v, b, t, hh)[c]);
-                        const float ww = bf2f(vrow(in.write_raw, b, t, hh)[c]);
-                        return vv / (1.f + __expf(-ww));
-                      },
-                      K, zero4());
+      f4 aw = mma_k32(fa, [&](int k, int nn) { return s.Pa[k][cb * 16 + nn]; }, K, zero4());
+      f4 au = mma_k32(fa, [&](int k, int nn) { return s.Pb[k][cb * 16 + nn]; }, K, zero4());
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
@@ -574,6 +587,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       }
     }
   }
+  SD_MARK(2, 9);
 }
 
 size_t prep_c_smem() { return sizeof(PrepCSmem); }
