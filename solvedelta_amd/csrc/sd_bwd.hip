@@ -134,44 +134,77 @@ struct GradSmem {
   ChunkDecay cd;
   float M1[BT * LS];
   float M2[BT * LS];
+  float red[4][KD];
 };
 
-// Rowsum of X_C (.) lambda for row c, then the in-chunk reverse cumulative sum of
-// the decay cotangent held (un-summed) in dg; thread c < 128 owns column c.
-__device__ void close_decay_gradient(const float* XC, const float* lam, float* dg, const float* shift) {
-  if (threadIdx.x < KD) {
-    const int c = threadIdx.x;
-    float acc = 0.f;
-    const float* xr = XC + c * KD;
-    const float* lr = lam + c * KD;
-#pragma unroll 8
-    for (int v = 0; v < KD; v += 4) {
-      const float4 x = ld4g(xr + v), y = ld4g(lr + v);
-      acc += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
-    }
-    for (int i0 = BT - 16; i0 >= 0; i0 -= 16) {  // 16 loads in flight per step
-      float col[16];
+// Decay-gradient closure for one chunk (all 512 threads): rowsum(X_C (.) lambda)
+// per coordinate plus the in-chunk reverse cumulative sum of the un-summed decay
+// cotangent in dg (+ the one-row shift of `shift`), written back to dg.
+// Thread (part, c): c = tid & 127 owns a coordinate, part = tid >> 7 a quarter
+// of the rows / value columns; every load is issued before the first sum.
+__device__ void close_decay_gradient(const float* XC, const float* lam, float* dg, const float* shift,
+                                     float (*red)[KD]) {
+  const int c = threadIdx.x & (KD - 1), part = threadIdx.x >> 7;
+  float4 xv[8], lv[8];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int i = i0 + q;
-        col[q] = dg[i * KD + c] + (shift && i + 1 < BT ? shift[(i + 1) * KD + c] : 0.f);
-      }
-#pragma unroll
-      for (int q = 15; q >= 0; --q) {
-        acc += col[q];
-        dg[(i0 + q) * KD + c] = acc;
-      }
-    }
+  for (int q = 0; q < 8; ++q) {
+    xv[q] = ld4g(XC + c * KD + part * 32 + q * 4);
+    lv[q] = ld4g(lam + c * KD + part * 32 + q * 4);
   }
+  float col[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int i = part * 16 + q;
+    col[q] = dg[i * KD + c] + ((shift && i + 1 < BT) ? shift[(i + 1) * KD + c] : 0.f);
+  }
+  float rs = 0.f;
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    rs += xv[q].x * lv[q].x + xv[q].y * lv[q].y + xv[q].z * lv[q].z + xv[q].w * lv[q].w;
+  float blk = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) blk += col[q];
+  red[part][c] = rs;
+  __syncthreads();
+  const float rowsum = red[0][c] + red[1][c] + red[2][c] + red[3][c];
+  __syncthreads();
+  red[part][c] = blk;
+  __syncthreads();
+  float acc = rowsum;  // carry from the later row quarters
+  for (int pp = part + 1; pp < 4; ++pp) acc += red[pp][c];
+#pragma unroll
+  for (int q = 15; q >= 0; --q) {
+    acc += col[q];
+    dg[(part * 16 + q) * KD + c] = acc;
+  }
+}
+
+// out[I] = rows_I(src) x B^T for the four 16-row blocks of a chunk panel (K = 128),
+// with the next row block's load in flight while the current one multiplies.
+__device__ __forceinline__ void rows_times_blk(const float* src, const BlkS& B, f4 (&out)[NB]) {
+  Blk cur, nxt;
+  load_blk(nxt, src, KD);
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    cur = nxt;
+    if (I + 1 < NB) load_blk(nxt, src + (I + 1) * BS * KD, KD);
+    BlkS a;
+    split_blk(cur, a);
+    out[I] = mma_blks(a, B, zero4());
+  }
+}
+
+__device__ __forceinline__ void load_split_blk(const float* rows, BlkS& o) {
+  Blk raw;
+  load_blk(raw, rows, KD);
+  split_blk(raw, o);
 }
 
 __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GradSmem& s = *reinterpret_cast<GradSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
-  SD_MARK(0, 0);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
-  SD_MARK(0, 1);
   const ChunkDecay& cd = s.cd;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
@@ -185,70 +218,67 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const float* XC = X0 + KD * KD;
   const float* lam = p.g.Ls + sidx * KD * KD;
   // M1_ij = dw_i . w_j (j < i);  M2_li = dO_l . w_i (l >= i)
-  plain_pair([&](int i, int c) { return dw[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
-             true, s.M1);
-  plain_pair([&](int i, int c) { return dO[i * KD + c]; }, [&](int j, int c) { return wv[j * KD + c]; },
-             false, s.M2);
+  plain_pairs2(dw, dO, wv, s.M1, s.M2);
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
-  // row-block x column-block products over V (K = 128), all operand blocks in flight at once
-  f4 a[NB], bq[NB], kl[NB];
-  {
-    Blk B, A[2];
-    load_blk(B, X0 + cb * 16 * KD, KD);
-#pragma unroll
-    for (int I0 = 0; I0 < NB; I0 += 2) {
-      load_blk(A[0], dw + I0 * BS * KD, KD);
-      load_blk(A[1], dw + (I0 + 1) * BS * KD, KD);
-      a[I0] = mma_blk(A[0], B, zero4());
-      a[I0 + 1] = mma_blk(A[1], B, zero4());
-      load_blk(A[0], dO + I0 * BS * KD, KD);
-      load_blk(A[1], dO + (I0 + 1) * BS * KD, KD);
-      bq[I0] = mma_blk(A[0], B, zero4());
-      bq[I0 + 1] = mma_blk(A[1], B, zero4());
-    }
-    load_blk(B, lam + cb * 16 * KD, KD);
-#pragma unroll
-    for (int I0 = 0; I0 < NB; I0 += 2) {
-      load_blk(A[0], wv + I0 * BS * KD, KD);
-      load_blk(A[1], wv + (I0 + 1) * BS * KD, KD);
-      kl[I0] = mma_blk(A[0], B, zero4());
-      kl[I0 + 1] = mma_blk(A[1], B, zero4());
-    }
-  }
-  float Sd[NB][4], Se[NB][4], Sq[NB][4];
-  load_slab(Sd, dd_, cb);
-  load_slab(Se, ee, cb);
-  load_slab(Sq, chi, cb);
-  __syncthreads();  // M1, M2 complete
-  SD_MARK(0, 2);
   auto D = [&](int j, int cc) { return dd_[j * KD + cc]; };
   auto E = [&](int j, int cc) { return ee[j * KD + cc]; };
   auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
   float* dg = p.g.dgS + rowbase * KD;
-#pragma unroll 1
-  for (int I = 0; I < NB; ++I) {
-    const f4 ap = apply_slab<false>(cd, s.M1, Sd, I, cb, D);
-    const f4 bp = apply_slab<false>(cd, s.M2, Sd, I, cb, D);
-    const f4 k2 = apply_t_slab<false>(cd, s.M2, Sq, I, cb, Q);
-    const f4 k3 = apply_t_slab<false>(cd, s.M1, Se, I, cb, E);
+  Tab1 t1;
+  // Pass A: de = -(e^G (dw X0^T) + apply(M1, d)),  dchi = e^G (dO X0^T) + apply(M2, d)
+  {
+    f4 a[NB], bq[NB];
+    {
+      BlkS B;
+      load_split_blk(X0 + cb * 16 * KD, B);
+      rows_times_blk(dw, B, a);
+      rows_times_blk(dO, B, bq);
+    }
+    float Sd[NB][4];
+    load_slab(Sd, dd_, cb);
+    make_tab1(cd, cb, t1);
+    __syncthreads();  // M1, M2 complete
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = I * BS + r4 + e;
-      const float eg = __expf(cd.G[i][c]);
-      const float de = -(eg * a[I][e] + ap[e]);
-      const float dchi = eg * bq[I][e] + bp[e];
-      const float ddv = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[I][e] + k2[e] - k3[e];
-      const long long o = (rowbase + i) * KD + c;
-      p.g.de[o] = de;
-      p.g.dchi[o] = dchi;
-      p.g.dd[o] = ddv;
-      dg[i * KD + c] = Sq[I][e] * dchi - Sd[I][e] * ddv + Se[I][e] * de;
+    for (int I = 0; I < NB; ++I) {
+      f4 ap, bp;
+      apply2_tab<false>(cd, s.M1, s.M2, Sd, I, cb, t1, D, ap, bp);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + r4 + e;
+        const float eg = __expf(cd.G[i][c]);
+        const long long o = (rowbase + i) * KD + c;
+        p.g.de[o] = -(eg * a[I][e] + ap[e]);
+        p.g.dchi[o] = eg * bq[I][e] + bp[e];
+      }
     }
   }
-  SD_MARK(0, 9);
+  // Pass B: dd = e^{G_C - G} (w lam^T) + apply_t(M2, chi) - apply_t(M1, e); decay terms
+  {
+    f4 kl[NB];
+    {
+      BlkS B;
+      load_split_blk(lam + cb * 16 * KD, B);
+      rows_times_blk(wv, B, kl);
+    }
+    float Se[NB][4], Sq[NB][4];
+    load_slab(Se, ee, cb);
+    load_slab(Sq, chi, cb);
+#pragma unroll
+    for (int I = 0; I < NB; ++I) {
+      f4 k2, k3;
+      apply_t2_tab<false>(cd, s.M2, Sq, s.M1, Se, I, cb, t1, Q, E, k2, k3);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + r4 + e;
+        const long long o = (rowbase + i) * KD + c;
+        const float ddv = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[I][e] + k2[e] - k3[e];
+        p.g.dd[o] = ddv;
+        dg[i * KD + c] = Sq[I][e] * p.g.dchi[o] - dd_[i * KD + c] * ddv + Se[I][e] * p.g.de[o];
+      }
+    }
+  }
   __syncthreads();
-  close_decay_gradient(XC, lam, dg, nullptr);
-  SD_MARK(0, 11);
+  close_decay_gradient(XC, lam, dg, nullptr, s.red);
 }
 
 // ---------------------------------------------------------------------------
@@ -425,6 +455,7 @@ struct GradCSmem {
   float M1[BT * LS];
   float M2[BT * LS];
   float gam[BT];
+  float red[4][KD];
 };
 
 __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
@@ -452,29 +483,15 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   const float* X0 = p.f.Xc + sidx * KD * KD;
   const float* XC = X0 + KD * KD;
   const float* lam = p.g.Lc + sidx * KD * KD;
-  plain_pair([&](int i, int cc) { return dw[i * KD + cc]; }, [&](int j, int cc) { return wv[j * KD + cc]; },
-             true, s.M1);
-  plain_pair([&](int i, int cc) { return kh[i * KD + cc]; }, [&](int j, int cc) { return wv[j * KD + cc]; },
-             false, s.M2);
+  // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
+  plain_pairs2(dw, kh, wv, s.M1, s.M2);
   f4 a[NB], kl[NB];
   {
-    Blk B, A[2];
-    load_blk(B, X0 + cb * 16 * KD, KD);
-#pragma unroll
-    for (int I0 = 0; I0 < NB; I0 += 2) {
-      load_blk(A[0], dw + I0 * BS * KD, KD);
-      load_blk(A[1], dw + (I0 + 1) * BS * KD, KD);
-      a[I0] = mma_blk(A[0], B, zero4());
-      a[I0 + 1] = mma_blk(A[1], B, zero4());
-    }
-    load_blk(B, lam + cb * 16 * KD, KD);
-#pragma unroll
-    for (int I0 = 0; I0 < NB; I0 += 2) {
-      load_blk(A[0], wv + I0 * BS * KD, KD);
-      load_blk(A[1], wv + (I0 + 1) * BS * KD, KD);
-      kl[I0] = mma_blk(A[0], B, zero4());
-      kl[I0 + 1] = mma_blk(A[1], B, zero4());
-    }
+    BlkS B;
+    load_split_blk(X0 + cb * 16 * KD, B);
+    rows_times_blk(dw, B, a);
+    load_split_blk(lam + cb * 16 * KD, B);
+    rows_times_blk(wv, B, kl);
   }
   float Su[NB][4], Sdd[NB][4], So[NB][4];
   load_slab(Su, uh, cb);
@@ -488,6 +505,11 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) So[J][e] -= Sk[J][e];  // C-op output o = d - k
   }
+  Tab1 t1;
+  Tab2 tx, ti;
+  make_tab1(cd, cb, t1);
+  make_tab2<true>(cd, cb, tx);
+  make_tab2<false>(cd, cb, ti);
   __syncthreads();  // M1, M2, gam complete
   auto U = [&](int j, int cc) { return uh[j * KD + cc]; };
   auto Xg = [&](int j, int cc) { return s.gam[j] * uh[j * KD + cc]; };
@@ -498,11 +520,11 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) Sx[J][e] = s.gam[J * BS + r4 + e] * Su[J][e];
   float* dg = p.g.dgC + rowbase * KD;
-#pragma unroll 1
+#pragma unroll
   for (int I = 0; I < NB; ++I) {
-    const f4 ap = apply_slab<true>(cd, s.M1, Su, I, cb, U);
-    const f4 k2 = apply_t_slab<false>(cd, s.M2, Sdd, I, cb, DO);
-    const f4 k3 = apply_t_slab<true>(cd, s.M1, Sx, I, cb, Xg);
+    const f4 ap = apply_tab<true>(cd, s.M1, Su, I, cb, t1, tx, U);
+    const f4 k2 = apply_t_tab<false>(cd, s.M2, Sdd, I, cb, t1, ti, DO);
+    const f4 k3 = apply_t_tab<true>(cd, s.M1, Sx, I, cb, t1, tx, Xg);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = I * BS + r4 + e;
@@ -533,7 +555,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     for (int e = 0; e < 4; ++e) p.g.dqC[(rowbase + I * BS + r4 + e) * KD + c] = dq[e];
   }
   __syncthreads();
-  close_decay_gradient(XC, lam, dg, p.g.xdx + rowbase * KD);
+  close_decay_gradient(XC, lam, dg, p.g.xdx + rowbase * KD, s.red);
 }
 
 // ---------------------------------------------------------------------------

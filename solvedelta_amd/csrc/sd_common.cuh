@@ -137,7 +137,7 @@ __device__ __forceinline__ int out_col() { return lane_id() & 15; }
 // Chunk-local shared state
 // ---------------------------------------------------------------------------
 constexpr int GS = KD + 4;  // fp32 panel row stride (floats)
-constexpr int LS = BT + 1;  // 64x64 fp32 matrix row stride
+constexpr int LS = BT + 4;  // 64x64 fp32 matrix row stride (16-byte aligned rows)
 
 struct ChunkDecay {
   float G[BT][GS];          // inclusive prefix
@@ -556,6 +556,270 @@ __device__ f4 apply_t_slab(const ChunkDecay& cd, const float* M, const float (&X
     }
   }
   return res;
+}
+
+}  // namespace sd
+
+namespace sd {
+
+// Pre-split (bf16 hi + lo) MFMA operand fragment and the 3-term product.
+struct Frag { bf16x8 h, l; };
+
+__device__ __forceinline__ f4 mma3f(const Frag& a, const Frag& b, f4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, acc, 0, 0, 0);
+}
+
+struct BlkS { Frag f[4]; };
+
+__device__ __forceinline__ void split_blk(const Blk& b, BlkS& o) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const float v[8] = {b.v[ks][0].x, b.v[ks][0].y, b.v[ks][0].z, b.v[ks][0].w,
+                        b.v[ks][1].x, b.v[ks][1].y, b.v[ks][1].z, b.v[ks][1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 h, l;
+      split_bf(v[e], h, l);
+      o.f[ks].h[e] = h;
+      o.f[ks].l[e] = l;
+    }
+  }
+}
+
+__device__ __forceinline__ f4 mma_blks(const BlkS& A, const BlkS& B, f4 acc) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) acc = mma3f(A.f[ks], B.f[ks], acc);
+  return acc;
+}
+
+// Both plain pair matrices sharing the right factor:
+//   M1_ij = X1_i . Y_j (j < i),  M2_ij = X2_i . Y_j (j <= i),  over KD = 128.
+// Each wave loads the three row blocks of its block pair once.
+template <class P1, class P2, class PY>
+__device__ void plain_pairs2(P1 x1, P2 x2, PY y, float* M1, float* M2) {
+  const int w = wave_id();
+  for (int pp = w; pp < 10; pp += CW) {
+    int I = 0, J = pp;
+    while (J > I) { J -= I + 1; ++I; }
+    Blk a1, a2, bb;
+    load_blk(a1, x1 + I * BS * KD, KD);
+    load_blk(a2, x2 + I * BS * KD, KD);
+    load_blk(bb, y + J * BS * KD, KD);
+    BlkS s1, s2, sb;
+    split_blk(a1, s1);
+    split_blk(a2, s2);
+    split_blk(bb, sb);
+    const f4 r1 = mma_blks(s1, sb, zero4());
+    const f4 r2 = mma_blks(s2, sb, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + out_row(e), j = J * BS + out_col();
+      M1[i * LS + j] = j < i ? r1[e] : 0.f;
+      M2[i * LS + j] = j <= i ? r2[e] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) {
+      M1[i * LS + j] = 0.f;
+      M2[i * LS + j] = 0.f;
+    }
+  }
+}
+
+// Per-lane decay factors for the slab applies of one 16-column block:
+//   E1[J][e]     = exp(R_J - G_j), j = J*16 + (lane>>4)*4 + e  (0 for wild coords)
+//   E2[pi(I,J)][e] = exp(Gx_i - R_J), i = I*16 + (lane>>4)*4 + e, J <= I
+__device__ __forceinline__ int pidx(int I, int J) { return I * (I + 1) / 2 + J; }
+
+struct Tab1 { float E1[NB][4]; };
+struct Tab2 { float E2[10][4]; };
+
+__device__ __forceinline__ void make_tab1(const ChunkDecay& cd, int cb, Tab1& t) {
+  const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+#pragma unroll
+  for (int J = 0; J < NB; ++J) {
+    const bool wild = cd.wild[J][c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t.E1[J][e] = wild ? 0.f : __expf(cd.R[J][c] - cd.G[J * BS + r4 + e][c]);
+  }
+}
+
+template <bool EXCL>
+__device__ __forceinline__ void make_tab2(const ChunkDecay& cd, int cb, Tab2& t) {
+  const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+#pragma unroll
+  for (int I = 0; I < NB; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + r4 + e;
+      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+#pragma unroll
+      for (int J = 0; J <= I; ++J) t.E2[pidx(I, J)][e] = __expf(gx - cd.R[J][c]);
+    }
+}
+
+// Slab applies with precomputed factors (see apply_slab / apply_t_slab).
+template <bool EXCL, class FW>
+__device__ f4 apply_tab(const ChunkDecay& cd, const float* M, const float (&Y)[NB][4], int I, int cb,
+                        const Tab1& t1, const Tab2& t2, FW Yw) {
+  const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
+  f4 tot = zero4();
+#pragma unroll
+  for (int J = 0; J < NB; ++J) {
+    if (J > I) break;
+    const float4 mv = *reinterpret_cast<const float4*>(&M[(I * BS + m) * LS + J * BS + r4]);
+    const float av[4] = {mv.x, mv.y, mv.z, mv.w};
+    float bv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bv[e] = Y[J][e] * t1.E1[J][e];
+    const f4 a2 = mma16s(av, bv, zero4());
+    if (cd.wild[J][c]) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + r4 + e;
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        float add = 0.f;
+        for (int j = J * BS; j < J * BS + BS; ++j)
+          add += M[i * LS + j] * Yw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+        tot[e] += add;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tot[e] += t2.E2[pidx(I, J)][e] * a2[e];
+    }
+  }
+  return tot;
+}
+
+template <bool EXCL, class FW>
+__device__ f4 apply_t_tab(const ChunkDecay& cd, const float* M, const float (&X)[NB][4], int Jb,
+                          int cb, const Tab1& t1, const Tab2& t2, FW Xw) {
+  const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
+  f4 acc = zero4();
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    if (I < Jb) continue;
+    float av[4], bv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      av[e] = M[(I * BS + r4 + e) * LS + Jb * BS + m];
+      bv[e] = X[I][e] * t2.E2[pidx(I, Jb)][e];
+    }
+    acc = mma16s(av, bv, acc);
+  }
+  f4 res;
+  if (cd.wild[Jb][c]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = Jb * BS + r4 + e;
+      float s = 0.f;
+      for (int i = j; i < BT; ++i) {
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        s += M[i * LS + j] * Xw(i, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      }
+      res[e] = s;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) res[e] = t1.E1[Jb][e] * acc[e];
+  }
+  return res;
+}
+
+
+// Two applies sharing Y (and so every decay factor): R1 with M1, R2 with M2.
+template <bool EXCL, class FW>
+__device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M2,
+                           const float (&Y)[NB][4], int I, int cb, const Tab1& t1, FW Yw, f4& r1,
+                           f4& r2) {
+  const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
+  r1 = zero4();
+  r2 = zero4();
+#pragma unroll
+  for (int J = 0; J < NB; ++J) {
+    if (J > I) break;
+    const float4 m1 = *reinterpret_cast<const float4*>(&M1[(I * BS + m) * LS + J * BS + r4]);
+    const float4 m2 = *reinterpret_cast<const float4*>(&M2[(I * BS + m) * LS + J * BS + r4]);
+    const float a1[4] = {m1.x, m1.y, m1.z, m1.w}, a2v[4] = {m2.x, m2.y, m2.z, m2.w};
+    float bv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bv[e] = Y[J][e] * t1.E1[J][e];
+    const f4 p1 = mma16s(a1, bv, zero4());
+    const f4 p2 = mma16s(a2v, bv, zero4());
+    if (cd.wild[J][c]) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + r4 + e;
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        float s1 = 0.f, s2 = 0.f;
+        for (int j = J * BS; j < J * BS + BS; ++j) {
+          const float f = Yw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+          s1 += M1[i * LS + j] * f;
+          s2 += M2[i * LS + j] * f;
+        }
+        r1[e] += s1;
+        r2[e] += s2;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = I * BS + r4 + e;
+        const float f = __expf((EXCL ? gx_excl(cd, i, c) : cd.G[i][c]) - cd.R[J][c]);
+        r1[e] += f * p1[e];
+        r2[e] += f * p2[e];
+      }
+    }
+  }
+}
+
+// Two transposed applies sharing the decay factors: R1 = M1 with X1, R2 = M2 with X2.
+template <bool EXCL, class FW1, class FW2>
+__device__ void apply_t2_tab(const ChunkDecay& cd, const float* M1, const float (&X1)[NB][4],
+                             const float* M2, const float (&X2)[NB][4], int Jb, int cb,
+                             const Tab1& t1, FW1 X1w, FW2 X2w, f4& r1, f4& r2) {
+  const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
+  f4 acc1 = zero4(), acc2 = zero4();
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    if (I < Jb) continue;
+    float av1[4], av2[4], bv1[4], bv2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = (I * BS + r4 + e) * LS + Jb * BS + m;
+      av1[e] = M1[row];
+      av2[e] = M2[row];
+      const int i = I * BS + r4 + e;
+      const float f = __expf((EXCL ? gx_excl(cd, i, c) : cd.G[i][c]) - cd.R[Jb][c]);
+      bv1[e] = X1[I][e] * f;
+      bv2[e] = X2[I][e] * f;
+    }
+    acc1 = mma16s(av1, bv1, acc1);
+    acc2 = mma16s(av2, bv2, acc2);
+  }
+  if (cd.wild[Jb][c]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = Jb * BS + r4 + e;
+      float s1 = 0.f, s2 = 0.f;
+      for (int i = j; i < BT; ++i) {
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        const float f = __expf(fminf(gx - cd.G[j][c], 0.f));
+        s1 += M1[i * LS + j] * X1w(i, c) * f;
+        s2 += M2[i * LS + j] * X2w(i, c) * f;
+      }
+      r1[e] = s1;
+      r2[e] = s2;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r1[e] = t1.E1[Jb][e] * acc1[e];
+      r2[e] = t1.E1[Jb][e] * acc2[e];
+    }
+  }
 }
 
 }  // namespace sd

@@ -154,8 +154,6 @@ struct StateSmem {
   __bf16 wl[SCOLS][BT + 8];
 };
 
-struct Frag { bf16x8 h, l; };
-
 template <bool COL_OUT, bool INJ>
 struct StateFrags {
   Frag W[4];
@@ -217,12 +215,6 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
   }
 }
 
-// hi*hi + hi*lo + lo*hi on pre-split fragments.
-__device__ __forceinline__ f4 mma3f(const Frag& a, const Frag& b, f4 acc) {
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, acc, 0, 0, 0);
-}
 
 __device__ __forceinline__ void stage_split4(__bf16* hi, __bf16* lo, f4 v) {
   bf16x4 h, l;
