@@ -78,3 +78,23 @@ def test_c_token_loop_matches_oracle():
     np.testing.assert_allclose(out, o_ref.numpy(), rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(C, st.predictor.numpy(), rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(S, st.S.numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_packed_segment_plan_on_cpu():
+    """Plan semantics of packing.py:43-150: compaction, reset splits, first
+    segment inherits the initial state unless it starts with a reset."""
+    from solvedelta_amd.segments import build_packed_segments
+    valid = torch.tensor([[1, 1, 0, 1, 1, 1], [0, 0, 0, 0, 0, 0], [1, 1, 1, 1, 0, 1]], dtype=torch.bool)
+    reset = torch.zeros_like(valid)
+    reset[0, 4] = True
+    reset[2, 0] = True
+    reset[1, 2] = True  # on an invalid token: ignored
+    plan = build_packed_segments(valid, reset)
+    assert plan.num_tokens == 10 and plan.num_segments == 3
+    assert plan.segment_batch.tolist() == [0, 0, 2]
+    assert plan.segment_lengths.tolist() == [3, 2, 5]
+    assert plan.use_initial.tolist() == [True, False, False]
+    assert plan.last_segment.tolist() == [1, -1, 2]
+    assert plan.max_seqlen == 5
+    with pytest.raises(ValueError):
+        build_packed_segments(valid.int(), reset)
