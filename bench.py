@@ -94,6 +94,54 @@ def cpu_baseline(budget_s=15.0):
                       f"({dt:.1f} s)"}
 
 
+def decode_bench(dev, steps=256, streams=64):
+    """Config 3: 64 independent streams x H=8, r=V=128, FP32 states C,S ~ 0.01 N(0,1)
+    advanced in place by `steps` T=1 calls of the C-ABI (inputs drawn as config 1)."""
+    import ctypes
+    from solvedelta_amd import _lib
+    lib = _lib.load()
+    ins, _, _ = make_inputs(dev, seed=3, b=streams, t=steps)
+    ins = [x.detach() for x in ins]
+    g = torch.Generator().manual_seed(4)
+    C = (0.01 * torch.randn(streams, H, R, R, generator=g)).to(dev)
+    S = (0.01 * torch.randn(streams, H, R, V, generator=g)).to(dev)
+    out = torch.empty(streams, 1, H, V, dtype=torch.bfloat16, device=dev)
+    from solvedelta_amd.operator import _inputs
+    calls = []
+    for t in range(steps):
+        step = [x[:, t:t + 1] for x in ins]
+        calls.append(_inputs(*step, C, S))
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def run():
+        for c in calls:
+            rc = lib.sd_decode(ctypes.byref(c), out.data_ptr(), C.data_ptr(), S.data_ptr(), stream)
+            if rc:
+                raise RuntimeError(f"sd_decode failed ({rc})")
+
+    run()
+    torch.cuda.synchronize()
+    _lib.profile_enable(True)
+    t0 = time.perf_counter()
+    run()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    prof = _lib.profile_read()
+    _lib.profile_enable(False)
+    ms, cnt = prof["k_decode"]
+    per_step = ms / cnt / 1e3
+    state_bytes = 2 * streams * H * (R * R + R * V) * 4      # read + write C and S
+    in_bytes = streams * H * (7 * R * 2 + R * 4 + 4 + V * 2)  # bf16 vectors, fp32 decay, gamma, out
+    gbs = (state_bytes + in_bytes) / per_step / 1e9
+    return {"workload": f"decode {streams} streams x H={H} r=V={R}, {steps} T=1 steps, state in place",
+            "value": round(streams * steps / dt, 1), "unit": "tokens/s",
+            "kernel_us": round(per_step * 1e6, 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM / 1e9,
+                         "unit": "GB/s", "frac": round(gbs * 1e9 / PEAK_HBM, 4),
+                         "bytes_per_launch": state_bytes + in_bytes,
+                         "note": "64 MiB state fits the 256 MB MALL; see DESIGN.md"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -152,6 +200,7 @@ def main():
                    "heads": H, "dk": R, "dv": V, "chunk": CH, "parallelism": "single-gpu"},
         "roofline": roof,
     }
+    res["decode"] = decode_bench(dev)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

@@ -136,12 +136,14 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
 // The next chunk's fragments are loaded into registers while the current chunk
 // computes, so the global latency leaves the sequential critical path.
 // ---------------------------------------------------------------------------
-// State workgroup geometry: 4 waves own a 128 x 16 state tile; wave w holds
-// state rows 32w..32w+31 (SRB = 2 row blocks) in MFMA accumulators and computes
-// the w / o tile of token block w; 8 workgroups cover the 128 state columns of
-// a sequence.  (One wave per SIMD: the per-chunk MFMA chain is the critical
-// path, so spreading the tile over more waves per CU only serialises them.)
+// State workgroup geometry: 4 waves (one per SIMD) own a 128 x SCOLS state tile
+// split into HALVES 16-column halves; wave w holds state rows 32w..32w+31 (SRB = 2
+// row blocks) of every half in MFMA accumulators and computes the w / o tiles of
+// token block w.  KD / SCOLS workgroups cover a sequence's state columns; every
+// one of them reads the chunk's full W and K panels, so wider tiles mean less
+// panel traffic per chunk step.
 constexpr int SCOLS = 16;
+constexpr int HALVES = SCOLS / 16;
 constexpr int SWAVES = 4;
 constexpr int SRB = KD / 16 / SWAVES;
 constexpr int STHREADS = SWAVES * 64;
@@ -161,8 +163,8 @@ struct StateFrags {
   Frag Q[COL_OUT ? 4 : 1];
   Frag P[COL_OUT ? 2 : 1];
   Frag A1[INJ ? SRB : 1][2];
-  Frag B1[INJ ? 2 : 1];
-  float U[4];
+  Frag B1[INJ ? HALVES : 1][2];
+  float U[HALVES][4];
   float4 gam[SRB];
 };
 
@@ -190,9 +192,11 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
       f.K[q][ks] = ldfrag(p.Kt, cidx * KD * BT + (long long)((SRB * w + q) * 16 + m) * BT + ks * 32 + kq);
-  const int col = tile * SCOLS + m;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) f.U[e] = p.U[(rowbase + tb * 16 + (l >> 4) * 4 + e) * KD + col];
+  for (int h = 0; h < HALVES; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      f.U[h][e] = p.U[(rowbase + tb * 16 + (l >> 4) * 4 + e) * KD + tile * SCOLS + h * 16 + m];
 #pragma unroll
   for (int q = 0; q < SRB; ++q) f.gam[q] = ld4(p.Gam + cidx * KD + (SRB * w + q) * 16 + (l >> 4) * 4);
   if constexpr (COL_OUT) {
@@ -210,11 +214,13 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
         f.A1[q][ks] =
             ldfrag(p.At1, cidx * KD * BT + (long long)((SRB * w + q) * 16 + m) * BT + ks * 32 + kq);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      f.B1[ks] = ldfrag(p.B1, cidx * KD * BT + (long long)col * BT + ks * 32 + kq);
+    for (int h = 0; h < HALVES; ++h)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        f.B1[h][ks] = ldfrag(p.B1, cidx * KD * BT + (long long)(tile * SCOLS + h * 16 + m) * BT +
+                                       ks * 32 + kq);
   }
 }
-
 
 __device__ __forceinline__ void stage_split4(__bf16* hi, __bf16* lo, f4 v) {
   bf16x4 h, l;
@@ -232,73 +238,87 @@ __device__ __forceinline__ void stage_split4(__bf16* hi, __bf16* lo, f4 v) {
 // One chunk of the sequential pass with its operand fragments already in registers.
 template <bool COL_OUT, bool INJ>
 __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, int n, int ch, int tile,
-                                           const StateFrags<COL_OUT, INJ>& cur, f4 (&X)[SRB]) {
+                                           const StateFrags<COL_OUT, INJ>& cur,
+                                           f4 (&X)[SRB][HALVES]) {
   const int NS = p.NT + 1;
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
   const int tb = w;
   const long long sidx = (long long)n * NS + ch;
   const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
   // save X0 and stage it split and transposed ([col][row]) for the B operand
-  const int col = tile * SCOLS + m;
 #pragma unroll
-  for (int q = 0; q < SRB; ++q) {
-    const int row0 = (SRB * w + q) * 16 + r4;
-    if (p.Xs)
-      for (int e = 0; e < 4; ++e) p.Xs[sidx * KD * KD + (long long)(row0 + e) * KD + col] = X[q][e];
-    stage_split4(&s.Xh[m][row0], &s.Xl[m][row0], X[q]);
-  }
+  for (int q = 0; q < SRB; ++q)
+#pragma unroll
+    for (int h = 0; h < HALVES; ++h) {
+      const int row0 = (SRB * w + q) * 16 + r4, col = tile * SCOLS + h * 16 + m;
+      if (p.Xs)
+        for (int e = 0; e < 4; ++e) p.Xs[sidx * KD * KD + (long long)(row0 + e) * KD + col] = X[q][h][e];
+      stage_split4(&s.Xh[h * 16 + m][row0], &s.Xl[h * 16 + m][row0], X[q][h]);
+    }
   __syncthreads();
-  // w = U + Wneg X  (token block tb, column half)
-  const int lc = m;  // local column of this lane in the w / o tile
-  f4 acc = {cur.U[0], cur.U[1], cur.U[2], cur.U[3]};
+  // w = U + Wneg X0 (token block tb, each half).  The work that does not depend
+  // on this chunk's w -- Gamma X (+ At1 B1) and the output's Q X0 -- is issued
+  // alongside so the independent MFMA chains overlap.
+  f4 acc[HALVES], o[HALVES];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    Frag xb;
-    xb.h = ldb8(&s.Xh[lc][ks * 32 + kq]);
-    xb.l = ldb8(&s.Xl[lc][ks * 32 + kq]);
-    acc = mma3f(cur.W[ks], xb, acc);
+  for (int h = 0; h < HALVES; ++h) {
+    acc[h] = {cur.U[h][0], cur.U[h][1], cur.U[h][2], cur.U[h][3]};
+    o[h] = zero4();
   }
-  const int gcol = tile * SCOLS + lc;
-  for (int e = 0; e < 4; ++e) p.wout[(rowbase + tb * 16 + r4 + e) * KD + gcol] = acc[e];
-  stage_split4(&s.wh[lc][tb * 16 + r4], &s.wl[lc][tb * 16 + r4], acc);
-  __syncthreads();
-  // X = Gamma X + Kt w (+ At1 B1): the recurrence's critical path
-  Frag wf[2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    wf[ks].h = ldb8(&s.wh[m][ks * 32 + kq]);
-    wf[ks].l = ldb8(&s.wl[m][ks * 32 + kq]);
-  }
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int h = 0; h < HALVES; ++h) {
+      Frag xb;
+      xb.h = ldb8(&s.Xh[h * 16 + m][ks * 32 + kq]);
+      xb.l = ldb8(&s.Xl[h * 16 + m][ks * 32 + kq]);
+      acc[h] = mma3f(cur.W[ks], xb, acc[h]);
+      if constexpr (COL_OUT) o[h] = mma3f(cur.Q[ks], xb, o[h]);
+    }
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
     const float gv[4] = {cur.gam[q].x, cur.gam[q].y, cur.gam[q].z, cur.gam[q].w};
-    for (int e = 0; e < 4; ++e) X[q][e] *= gv[e];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      X[q] = mma3f(cur.K[q][ks], wf[ks], X[q]);
-      if constexpr (INJ) X[q] = mma3f(cur.A1[q][ks], cur.B1[ks], X[q]);
+    for (int h = 0; h < HALVES; ++h) {
+      for (int e = 0; e < 4; ++e) X[q][h][e] *= gv[e];
+      if constexpr (INJ) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) X[q][h] = mma3f(cur.A1[q][ks], cur.B1[h][ks], X[q][h]);
+      }
     }
   }
-  if constexpr (COL_OUT) {
-    // o = Q X0 + P w  (token block tb, column half), written as bf16 to out[b,t,h,v]
-    f4 o = zero4();
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      Frag xb;
-      xb.h = ldb8(&s.Xh[lc][ks * 32 + kq]);
-      xb.l = ldb8(&s.Xl[lc][ks * 32 + kq]);
-      o = mma3f(cur.Q[ks], xb, o);
-    }
+  for (int h = 0; h < HALVES; ++h) {
+    const int gcol = tile * SCOLS + h * 16 + m;
+    for (int e = 0; e < 4; ++e) p.wout[(rowbase + tb * 16 + r4 + e) * KD + gcol] = acc[h][e];
+    stage_split4(&s.wh[h * 16 + m][tb * 16 + r4], &s.wl[h * 16 + m][tb * 16 + r4], acc[h]);
+  }
+  __syncthreads();
+  // X += Kt w: the recurrence's critical path (and o += P w)
+#pragma unroll
+  for (int h = 0; h < HALVES; ++h) {
+    Frag wf[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      if (ks == 1 && tb < 2) break;
-      o = mma3f(cur.P[ks], wf[ks], o);
+      wf[ks].h = ldb8(&s.wh[h * 16 + m][ks * 32 + kq]);
+      wf[ks].l = ldb8(&s.wl[h * 16 + m][ks * 32 + kq]);
     }
-    const int b = n / p.H, hh = n % p.H;
-    for (int e = 0; e < 4; ++e) {
-      const int t = ch * BT + tb * 16 + r4 + e;
-      if (t < p.T && gcol < p.cols)
-        p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + gcol] = f2bf(o[e]);
+#pragma unroll
+    for (int q = 0; q < SRB; ++q)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) X[q][h] = mma3f(cur.K[q][ks], wf[ks], X[q][h]);
+    if constexpr (COL_OUT) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks == 1 && tb < 2) break;
+        o[h] = mma3f(cur.P[ks], wf[ks], o[h]);
+      }
+      const int b = n / p.H, hh = n % p.H, gcol = tile * SCOLS + h * 16 + m;
+      for (int e = 0; e < 4; ++e) {
+        const int t = ch * BT + tb * 16 + r4 + e;
+        if (t < p.T && gcol < p.cols)
+          p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + gcol] = f2bf(o[h][e]);
+      }
     }
   }
   __syncthreads();
@@ -324,58 +344,54 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
     }
   }
   const int w = wave_id(), l = lane_id(), m = l & 15, r4 = (l >> 4) * 4;
-  f4 X[SRB];
+  f4 X[SRB][HALVES];
   for (int q = 0; q < SRB; ++q)
-    for (int e = 0; e < 4; ++e) {
-      const int row = (SRB * w + q) * 16 + r4 + e, col = tile * SCOLS + m;
-      float x = 0.f;
-      if (p.init && row < p.rows && col < p.cols)
-        x = p.init_transposed ? p.init[(long long)n * p.rows * p.cols + (long long)col * p.rows + row]
-                              : p.init[(long long)n * p.rows * p.cols + (long long)row * p.cols + col];
-      X[q][e] = x;
-    }
-  // Operand fragments are prefetched ahead into rotating register buffers (no
-  // copies, so a buffer's loads are only waited on when it becomes current).
+    for (int h = 0; h < HALVES; ++h)
+      for (int e = 0; e < 4; ++e) {
+        const int row = (SRB * w + q) * 16 + r4 + e, col = tile * SCOLS + h * 16 + m;
+        float x = 0.f;
+        if (p.init && row < p.rows && col < p.cols)
+          x = p.init_transposed ? p.init[(long long)n * p.rows * p.cols + (long long)col * p.rows + row]
+                                : p.init[(long long)n * p.rows * p.cols + (long long)row * p.cols + col];
+        X[q][h][e] = x;
+      }
   const int NT = p.NT;
   auto chunk_of = [&](int it) { return p.rev ? NT - 1 - it : it; };
-  if constexpr (SWAVES == 4) {  // one wave per SIMD: room for two chunks ahead
-    StateFrags<COL_OUT, INJ> f0, f1, f2;
-    load_state_frags(p, n, chunk_of(0), tile, f0);
-    if (NT > 1) load_state_frags(p, n, chunk_of(1), tile, f1);
-    for (int it = 0; it < NT; it += 3) {
-      if (it + 2 < NT) load_state_frags(p, n, chunk_of(it + 2), tile, f2);
-      state_step(p, s, n, chunk_of(it), tile, f0, X);
-      if (it + 1 >= NT) break;
-      if (it + 3 < NT) load_state_frags(p, n, chunk_of(it + 3), tile, f0);
-      state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
-      if (it + 2 >= NT) break;
-      if (it + 4 < NT) load_state_frags(p, n, chunk_of(it + 4), tile, f1);
-      state_step(p, s, n, chunk_of(it + 2), tile, f2, X);
-    }
-  } else {
-    StateFrags<COL_OUT, INJ> f0, f1;  // one chunk ahead (register budget)
-    load_state_frags(p, n, chunk_of(0), tile, f0);
-    for (int it = 0; it < NT; it += 2) {
-      if (it + 1 < NT) load_state_frags(p, n, chunk_of(it + 1), tile, f1);
-      state_step(p, s, n, chunk_of(it), tile, f0, X);
-      if (it + 1 >= NT) break;
-      if (it + 2 < NT) load_state_frags(p, n, chunk_of(it + 2), tile, f0);
-      state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
-    }
+  // Loaded latency of these panel fetches is ~2.5 us (longer than one chunk
+  // step), so fragments are prefetched two chunks ahead in three rotating
+  // register buffers.  The loop body is straight-line (no breaks; clamped,
+  // unconditional prefetches) so the compiler's wait counts only cover the
+  // buffer being consumed; the last one or two chunks run after the loop.
+  auto clampc = [&](int it2) { return chunk_of(it2 < NT ? it2 : NT - 1); };
+  StateFrags<COL_OUT, INJ> f0, f1, f2;
+  load_state_frags(p, n, clampc(0), tile, f0);
+  load_state_frags(p, n, clampc(1), tile, f1);
+  int it = 0;
+  for (; it + 2 < NT; it += 3) {
+    load_state_frags(p, n, clampc(it + 2), tile, f2);
+    state_step(p, s, n, chunk_of(it), tile, f0, X);
+    load_state_frags(p, n, clampc(it + 3), tile, f0);
+    state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
+    load_state_frags(p, n, clampc(it + 4), tile, f1);
+    state_step(p, s, n, chunk_of(it + 2), tile, f2, X);
   }
+  if (it < NT) state_step(p, s, n, chunk_of(it), tile, f0, X);
+  if (it + 1 < NT) state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
   // final state (also kept as slot NT for the backward)
   for (int q = 0; q < SRB; ++q)
-    for (int e = 0; e < 4; ++e) {
-      const int row = (SRB * w + q) * 16 + r4 + e, col = tile * SCOLS + m;
-      if (p.Xs && !p.rev) p.Xs[((long long)n * NS + p.NT) * KD * KD + (long long)row * KD + col] = X[q][e];
-      if (p.fin && row < p.rows && col < p.cols) {
-        const long long base = (long long)n * p.rows * p.cols;
-        if (p.fin_transposed)
-          p.fin[base + (long long)col * p.rows + row] = X[q][e];
-        else
-          p.fin[base + (long long)row * p.cols + col] = X[q][e];
+    for (int h = 0; h < HALVES; ++h)
+      for (int e = 0; e < 4; ++e) {
+        const int row = (SRB * w + q) * 16 + r4 + e, col = tile * SCOLS + h * 16 + m;
+        if (p.Xs && !p.rev)
+          p.Xs[((long long)n * NS + p.NT) * KD * KD + (long long)row * KD + col] = X[q][h][e];
+        if (p.fin && row < p.rows && col < p.cols) {
+          const long long base = (long long)n * p.rows * p.cols;
+          if (p.fin_transposed)
+            p.fin[base + (long long)col * p.rows + row] = X[q][h][e];
+          else
+            p.fin[base + (long long)row * p.cols + col] = X[q][h][e];
+        }
       }
-    }
 }
 
 void launch_state(const char* name, const StateParams& sp, bool col_out, int nseq,
@@ -608,6 +624,9 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
   sc.Wneg = w.Wc; sc.U = w.Uc; sc.Kt = w.Kc; sc.Gam = w.Gam;
   sc.Xs = w.Xc; sc.wout = w.delta;
+#ifdef SD_EXPERIMENT_NO_XS
+  sc.Xs = nullptr;
+#endif
   sc.init = in->C0; sc.init_transposed = 1;
   sc.fin = C_T; sc.fin_transposed = 1;
   launch_state("state_c_fwd", sc, false, n, st);
@@ -618,6 +637,9 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
   ss.Wneg = w.Ws; ss.U = w.Us; ss.Kt = w.Ks; ss.Gam = w.Gam; ss.Q = w.Qs; ss.P = w.Ps;
   ss.Xs = w.Xs; ss.wout = w.wS; ss.out = (__bf16*)out;
+#ifdef SD_EXPERIMENT_NO_XS
+  ss.Xs = nullptr;
+#endif
   ss.init = in->S0; ss.init_transposed = 0;
   ss.fin = S_T; ss.fin_transposed = 0;
   launch_state("state_s_fwd", ss, true, n, st);
