@@ -130,13 +130,6 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   }
 }
 
-struct GradSmem {
-  ChunkDecay cd;
-  float M1[BT * LS];
-  float M2[BT * LS];
-  float red[4][KD];
-};
-
 // Decay-gradient closure for one chunk (all 512 threads): rowsum(X_C (.) lambda)
 // per coordinate plus the in-chunk reverse cumulative sum of the un-summed decay
 // cotangent in dg (+ the one-row shift of `shift`), written back to dg.
@@ -179,33 +172,19 @@ __device__ void close_decay_gradient(const float* XC, const float* lam, float* d
   }
 }
 
-// out[I] = rows_I(src) x B^T for the four 16-row blocks of a chunk panel (K = 128),
-// with the next row block's load in flight while the current one multiplies.
-__device__ __forceinline__ void rows_times_blk(const float* src, const BlkS& B, f4 (&out)[NB]) {
-  Blk cur, nxt;
-  load_blk(nxt, src, KD);
-#pragma unroll
-  for (int I = 0; I < NB; ++I) {
-    cur = nxt;
-    if (I + 1 < NB) load_blk(nxt, src + (I + 1) * BS * KD, KD);
-    BlkS a;
-    split_blk(cur, a);
-    out[I] = mma_blks(a, B, zero4());
-  }
-}
-
-__device__ __forceinline__ void load_split_blk(const float* rows, BlkS& o) {
-  Blk raw;
-  load_blk(raw, rows, KD);
-  split_blk(raw, o);
-}
+struct GradSmem {
+  ChunkDecay cd;
+  float M1[BT * LS];
+  float M2[BT * LS];
+  float red[4][KD];
+  LPanel PA;  // dw, then dO
+  LPanel PW;  // w
+};
 
 __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GradSmem& s = *reinterpret_cast<GradSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
-  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
-  const ChunkDecay& cd = s.cd;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
   const float* dw = p.g.dwS + rowbase * KD;
@@ -217,26 +196,50 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const float* X0 = p.f.Xs + sidx * KD * KD;
   const float* XC = X0 + KD * KD;
   const float* lam = p.g.Ls + sidx * KD * KD;
-  // M1_ij = dw_i . w_j (j < i);  M2_li = dO_l . w_i (l >= i)
-  plain_pairs2(dw, dO, wv, s.M1, s.M2);
+  stage_panel(s.PA, dw);
+  stage_panel(s.PW, wv);
+  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
+  const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+  // M1_ij = dw_i . w_j (j < i)
+  lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
+  // a = dw X0^T, kl = w lam^T for this wave's column block (K = 128)
+  f4 a[NB], bq[NB], kl[NB];
+  BlkS BX;
+  load_split_blk_g(X0 + cb * 16 * KD, BX);
+  {
+    BlkS BL;
+    load_split_blk_g(lam + cb * 16 * KD, BL);
+#pragma unroll
+    for (int I = 0; I < NB; ++I) {
+      BlkS A;
+      lblk(s.PA, I * BS, A);
+      a[I] = mma_blks(A, BX, zero4());
+      lblk(s.PW, I * BS, A);
+      kl[I] = mma_blks(A, BL, zero4());
+    }
+  }
+  __syncthreads();  // PA free
+  stage_panel(s.PA, dO);
+  __syncthreads();
+  // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T
+  lds_pair(&s.PA, nullptr, s.PW, s.M2, false);
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    BlkS A;
+    lblk(s.PA, I * BS, A);
+    bq[I] = mma_blks(A, BX, zero4());
+  }
   auto D = [&](int j, int cc) { return dd_[j * KD + cc]; };
   auto E = [&](int j, int cc) { return ee[j * KD + cc]; };
   auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
   float* dg = p.g.dgS + rowbase * KD;
   Tab1 t1;
+  make_tab1(cd, cb, t1);
   // Pass A: de = -(e^G (dw X0^T) + apply(M1, d)),  dchi = e^G (dO X0^T) + apply(M2, d)
   {
-    f4 a[NB], bq[NB];
-    {
-      BlkS B;
-      load_split_blk(X0 + cb * 16 * KD, B);
-      rows_times_blk(dw, B, a);
-      rows_times_blk(dO, B, bq);
-    }
     float Sd[NB][4];
     load_slab(Sd, dd_, cb);
-    make_tab1(cd, cb, t1);
     __syncthreads();  // M1, M2 complete
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
@@ -254,12 +257,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   }
   // Pass B: dd = e^{G_C - G} (w lam^T) + apply_t(M2, chi) - apply_t(M1, e); decay terms
   {
-    f4 kl[NB];
-    {
-      BlkS B;
-      load_split_blk(lam + cb * 16 * KD, B);
-      rows_times_blk(wv, B, kl);
-    }
     float Se[NB][4], Sq[NB][4];
     load_slab(Se, ee, cb);
     load_slab(Sq, chi, cb);
@@ -456,24 +453,17 @@ struct GradCSmem {
   float M2[BT * LS];
   float gam[BT];
   float red[4][KD];
+  LPanel PA;  // dw, then dd e^G
+  LPanel PW;  // delta
 };
 
 __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GradCSmem& s = *reinterpret_cast<GradCSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
-  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
-  const ChunkDecay& cd = s.cd;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
-  if (threadIdx.x < BT) {
-    const int t = t0 + threadIdx.x;
-    s.gam[threadIdx.x] = t < p.T ? ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
-                                                                   (long long)t * p.in.gamma.st +
-                                                                   (long long)hh * p.in.gamma.sh]
-                                 : 0.f;
-  }
   const float* dw = p.g.dwC + rowbase * KD;
   const float* wv = p.f.delta + rowbase * KD;
   const float* ddp = p.g.dd + rowbase * KD;   // cotangent of the C-op output
@@ -483,15 +473,33 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   const float* X0 = p.f.Xc + sidx * KD * KD;
   const float* XC = X0 + KD * KD;
   const float* lam = p.g.Lc + sidx * KD * KD;
+  if (threadIdx.x < BT) {
+    const int t = t0 + threadIdx.x;
+    s.gam[threadIdx.x] = t < p.T ? ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                                                   (long long)t * p.in.gamma.st +
+                                                                   (long long)hh * p.in.gamma.sh]
+                                 : 0.f;
+  }
+  stage_panel(s.PA, dw);
+  stage_panel(s.PW, wv);
+  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
+  const ChunkDecay& cd = s.cd;
   // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
-  plain_pairs2(dw, kh, wv, s.M1, s.M2);
+  lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
+  lds_pair(nullptr, kh, s.PW, s.M2, false);
   f4 a[NB], kl[NB];
   {
-    BlkS B;
-    load_split_blk(X0 + cb * 16 * KD, B);
-    rows_times_blk(dw, B, a);
-    load_split_blk(lam + cb * 16 * KD, B);
-    rows_times_blk(wv, B, kl);
+    BlkS BX, BL;
+    load_split_blk_g(X0 + cb * 16 * KD, BX);
+    load_split_blk_g(lam + cb * 16 * KD, BL);
+#pragma unroll
+    for (int I = 0; I < NB; ++I) {
+      BlkS A;
+      lblk(s.PA, I * BS, A);
+      a[I] = mma_blks(A, BX, zero4());
+      lblk(s.PW, I * BS, A);
+      kl[I] = mma_blks(A, BL, zero4());
+    }
   }
   float Su[NB][4], Sdd[NB][4], So[NB][4];
   load_slab(Su, uh, cb);
@@ -510,7 +518,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   make_tab1(cd, cb, t1);
   make_tab2<true>(cd, cb, tx);
   make_tab2<false>(cd, cb, ti);
-  __syncthreads();  // M1, M2, gam complete
+  __syncthreads();  // M1, M2 complete; PA free
+  // PA <- dd e^G for the dq product (staged now, consumed after the applies)
+  stage_panel(s.PA, ddp, [&](int i, int cc) { return __expf(cd.G[i][cc]); });
   auto U = [&](int j, int cc) { return uh[j * KD + cc]; };
   auto Xg = [&](int j, int cc) { return s.gam[j] * uh[j * KD + cc]; };
   auto DO = [&](int j, int cc) { return ddp[j * KD + cc]; };
@@ -541,18 +551,35 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   decayed_gram<false>(
       cd, [&](int i, int cc) { return ddp[i * KD + cc]; }, [&](int j, int cc) { return uh[j * KD + cc]; },
       false, s.M1);
-  // dq = (dd e^G) X0 + P' w
+  // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
+  {
+    BlkS BX;
+    {
+      const int kq = (l >> 4) * 8;
+      Blk raw;
 #pragma unroll
-  for (int I = 0; I < NB; ++I) {
-    f4 dq = mma_k32([&](int m, int aa) {
-                      const int i = I * BS + m;
-                      return ddp[i * KD + aa] * __expf(cd.G[i][aa]);
-                    },
-                    [&](int aa, int nn) { return X0[aa * KD + cb * 16 + nn]; }, KD, zero4());
-    dq = mma_k32([&](int m, int j) { return s.M1[(I * BS + m) * LS + j]; },
-                 [&](int j, int nn) { return wv[j * KD + cb * 16 + nn]; }, (I < 2 ? 32 : 64), dq);
+      for (int ks = 0; ks < 4; ++ks) {
+        float v[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) p.g.dqC[(rowbase + I * BS + r4 + e) * KD + c] = dq[e];
+        for (int e = 0; e < 8; ++e) v[e] = X0[(ks * 32 + kq + e) * KD + c];
+        raw.v[ks][0] = make_float4(v[0], v[1], v[2], v[3]);
+        raw.v[ks][1] = make_float4(v[4], v[5], v[6], v[7]);
+      }
+      split_blk(raw, BX);
+    }
+#pragma unroll
+    for (int I = 0; I < NB; ++I) {
+      BlkS A;
+      lblk(s.PA, I * BS, A);
+      f4 dq = mma_blks(A, BX, zero4());
+      dq = mma_k32([&](int m, int j) { return s.M1[(I * BS + m) * LS + j]; },
+                   [&](int j, int nn) {
+                     return (float)s.PW.h[j][cb * 16 + nn] + (float)s.PW.l[j][cb * 16 + nn];
+                   },
+                   (I < 2 ? 32 : 64), dq);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p.g.dqC[(rowbase + I * BS + r4 + e) * KD + c] = dq[e];
+    }
   }
   __syncthreads();
   close_decay_gradient(XC, lam, dg, p.g.xdx + rowbase * KD, s.red);

@@ -822,4 +822,89 @@ __device__ void apply_t2_tab(const ChunkDecay& cd, const float* M1, const float 
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Pre-split LDS panels: a 64 x 128 fp32 chunk panel held as bf16 hi + bf16 lo,
+// row-major with K contiguous, so every wave reads MFMA-ready fragments with
+// 16-byte LDS loads instead of re-splitting fp32 operands on each use.
+// ---------------------------------------------------------------------------
+constexpr int LPS = KD + 8;  // row stride (bf16 elements), keeps 16-byte alignment
+
+struct LPanel {
+  __bf16 h[BT][LPS];
+  __bf16 l[BT][LPS];
+};
+
+// All CT threads: src is a [64][128] fp32 panel (row stride KD) in global memory;
+// optional scale(i, c) multiplies each element before the split.
+template <class FS>
+__device__ __forceinline__ void stage_panel(LPanel& P, const float* src, FS scale) {
+  constexpr int PER = BT * KD / 4 / CT;  // float4 per thread
+  float4 v[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) v[q] = ld4g(src + (threadIdx.x + q * CT) * 4);
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
+    const float x[4] = {v[q].x * scale(i, c), v[q].y * scale(i, c + 1), v[q].z * scale(i, c + 2),
+                        v[q].w * scale(i, c + 3)};
+    bf16x4 hh, ll;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      __bf16 a, b;
+      split_bf(x[e], a, b);
+      hh[e] = a;
+      ll[e] = b;
+    }
+    *reinterpret_cast<bf16x4*>(&P.h[i][c]) = hh;
+    *reinterpret_cast<bf16x4*>(&P.l[i][c]) = ll;
+  }
+}
+
+__device__ __forceinline__ void stage_panel(LPanel& P, const float* src) {
+  stage_panel(P, src, [](int, int) { return 1.f; });
+}
+
+// Fragments of the 16-row block starting at row0 (A or B operand layout).
+__device__ __forceinline__ void lblk(const LPanel& P, int row0, BlkS& o) {
+  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    o.f[ks].h = *reinterpret_cast<const bf16x8*>(&P.h[row0 + m][ks * 32 + kq]);
+    o.f[ks].l = *reinterpret_cast<const bf16x8*>(&P.l[row0 + m][ks * 32 + kq]);
+  }
+}
+
+__device__ __forceinline__ void load_split_blk_g(const float* rows, BlkS& o) {
+  Blk raw;
+  load_blk(raw, rows, KD);
+  split_blk(raw, o);
+}
+
+// Pair matrix M = A Y^T over K = 128 (strict: j < i, else j <= i), Y from an LDS
+// panel and A from an LDS panel (Ag == nullptr) or a global fp32 panel.
+__device__ void lds_pair(const LPanel* A, const float* Ag, const LPanel& Y, float* M, bool strict) {
+  const int w = wave_id();
+  for (int pp = w; pp < 10; pp += CW) {
+    int I = 0, J = pp;
+    while (J > I) { J -= I + 1; ++I; }
+    BlkS a, y;
+    if (Ag)
+      load_split_blk_g(Ag + I * BS * KD, a);
+    else
+      lblk(*A, I * BS, a);
+    lblk(Y, J * BS, y);
+    const f4 r = mma_blks(a, y, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + out_row(e), j = J * BS + out_col();
+      M[i * LS + j] = (strict ? j < i : j <= i) ? r[e] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) M[i * LS + j] = 0.f;
+  }
+}
+
 }  // namespace sd
