@@ -253,6 +253,21 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
   __syncthreads();
 }
 
+__device__ __forceinline__ f4 mma16s(const float* av, const float* bv, f4 acc) {
+  bf16x4 ah, al, bh, bl;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    __bf16 h, lo;
+    split_bf(av[e], h, lo);
+    ah[e] = h; al[e] = lo;
+    split_bf(bv[e], h, lo);
+    bh[e] = h; bl[e] = lo;
+  }
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
+}
+
 // (I + L)^{-1} for strictly-lower L (64x64, stride LS), in place -> A.
 // Diagonal 16x16 blocks by forward substitution (one lane per column), then
 // off-diagonal blocks A_IJ = -A_II * sum_{K=J}^{I-1} L_IK A_KJ by distance.
@@ -278,35 +293,34 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
   }
   __syncthreads();
   // tmp holds the diagonal inverses; L still holds the strict lower part.
+  // Off-diagonal blocks by distance, one wave per block, on the K=16 MFMA:
+  //   T = sum_{K=J}^{I-1} L_IK A_KJ,   A_IJ = -A_II T.
+  // The MFMA output layout (lane: rows (lane>>4)*4+e, column lane&15) is the
+  // K=16 B-operand layout, so T feeds the second product from registers.
   for (int dist = 1; dist < NB; ++dist) {
-    // T_IJ = sum_{K=J}^{I-1} L_IK A_KJ  (A_KJ already in tmp for K-J < dist)
-    float tv[4];
-    int nt = 0;
-    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += CT) {
-      const int J = idx / (BS * BS), rem = idx % (BS * BS);
-      const int I = J + dist, i = rem / BS, j = rem % BS;
-      float s = 0.f;
-      for (int K = J; K < I; ++K)
-        for (int m = 0; m < BS; ++m)
-          s += L[(I * BS + i) * LS + K * BS + m] * tmp[(K * BS + m) * LS + J * BS + j];
-      tv[nt++] = s;
-    }
-    __syncthreads();
-    nt = 0;
-    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += CT) {
-      const int J = idx / (BS * BS), rem = idx % (BS * BS);
-      const int I = J + dist, i = rem / BS, j = rem % BS;
-      // stash T in the (still unused) upper block (J, I) of L
-      L[(J * BS + i) * LS + I * BS + j] = tv[nt++];
-    }
-    __syncthreads();
-    for (int idx = tid; idx < (NB - dist) * BS * BS; idx += CT) {
-      const int J = idx / (BS * BS), rem = idx % (BS * BS);
-      const int I = J + dist, i = rem / BS, j = rem % BS;
-      float s = 0.f;
-      for (int m = 0; m < BS; ++m)
-        s -= tmp[(I * BS + i) * LS + I * BS + m] * L[(J * BS + m) * LS + I * BS + j];
-      tmp[(I * BS + i) * LS + J * BS + j] = s;
+    const int wv = tid >> 6;
+    if (wv < NB - dist) {
+      const int J = wv, I = J + dist;
+      const int l = tid & 63, m = l & 15, r4 = (l >> 4) * 4;
+      f4 t = zero4();
+      for (int K = J; K < I; ++K) {
+        float av[4], bv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          av[e] = L[(I * BS + m) * LS + K * BS + r4 + e];
+          bv[e] = tmp[(K * BS + r4 + e) * LS + J * BS + m];
+        }
+        t = mma16s(av, bv, t);
+      }
+      float av[4], bv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        av[e] = tmp[(I * BS + m) * LS + I * BS + r4 + e];
+        bv[e] = t[e];
+      }
+      const f4 a = mma16s(av, bv, zero4());
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tmp[(I * BS + r4 + e) * LS + J * BS + m] = -a[e];
     }
     __syncthreads();
   }
@@ -468,20 +482,6 @@ __device__ __forceinline__ void load_slab(float (&s)[NB][4], const float* panel,
     for (int e = 0; e < 4; ++e) s[J][e] = panel[(J * BS + r4 + e) * KD + c];
 }
 
-__device__ __forceinline__ f4 mma16s(const float* av, const float* bv, f4 acc) {
-  bf16x4 ah, al, bh, bl;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    __bf16 h, lo;
-    split_bf(av[e], h, lo);
-    ah[e] = h; al[e] = lo;
-    split_bf(bv[e], h, lo);
-    bh[e] = h; bl[e] = lo;
-  }
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
-}
 
 // R_ic = sum_{j<=i} M_ij Y_jc exp(Gx_ic - G_jc) for row block I and this lane's
 // column, with Y given as a slab; Yw(j, c) is read only for wild coordinates.

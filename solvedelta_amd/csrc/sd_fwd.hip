@@ -468,41 +468,41 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   }
   __syncthreads();
   SD_MARK(2, 3);
-  // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}
+  // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}  (this wave's column block)
   const float* X0 = p.Xc + ((long long)n * (p.NT + 1) + ch) * KD * KD;
-  for (int q = 0; q < 1; ++q) {
-    const int cb = w + q;
+  {
+    const int cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+    BlkS BX;
+    load_split_blk_g(X0 + cb * 16 * KD, BX);
+    float Su[NB][4];
+#pragma unroll
+    for (int J = 0; J < NB; ++J)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Su[J][e] = s.Pa[J * BS + r4 + e][c];
+    Tab1 t1;
+    Tab2 t2;
+    make_tab1(cd, cb, t1);
+    make_tab2<false>(cd, cb, t2);
+    auto Uw = [&](int j, int cc) { return s.Pa[j][cc]; };
+#pragma unroll
     for (int I = 0; I < NB; ++I) {
-      f4 a1 = mma_k32([&](int m, int bb) { return s.Pb[I * BS + m][bb]; },
-                      [&](int bb, int nn) { return X0[(long long)(cb * 16 + nn) * KD + bb]; }, KD,
-                      zero4());
-      f4 tot;
-      for (int e = 0; e < 4; ++e) {
-        const int i = I * BS + out_row(e), c = cb * 16 + out_col();
-        tot[e] = s.Pb[i][c] + __expf(cd.G[i][c]) * a1[e];
+      Blk raw;
+      const int m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        raw.v[ks][0] = *reinterpret_cast<const float4*>(&s.Pb[I * BS + m][ks * 32 + kq]);
+        raw.v[ks][1] = *reinterpret_cast<const float4*>(&s.Pb[I * BS + m][ks * 32 + kq + 4]);
       }
-      for (int J = 0; J <= I; ++J) {
-        f4 a2 = mma_k16([&](int m, int k) { return s.M[(I * BS + m) * LS + J * BS + k]; },
-                        [&](int k, int nn) {
-                          const int c = cb * 16 + nn, j = J * BS + k;
-                          return cd.wild[J][c] ? 0.f : s.Pa[j][c] * __expf(cd.R[J][c] - cd.G[j][c]);
-                        },
-                        zero4());
-        for (int e = 0; e < 4; ++e) {
-          const int i = I * BS + out_row(e), c = cb * 16 + out_col();
-          float add = __expf(cd.G[i][c] - cd.R[J][c]) * a2[e];
-          if (cd.wild[J][c]) {
-            add = 0.f;
-            for (int j = J * BS; j < J * BS + BS && j <= i; ++j)
-              add += s.M[i * LS + j] * s.Pa[j][c] * __expf(fminf(cd.G[i][c] - cd.G[j][c], 0.f));
-          }
-          tot[e] += add;
-        }
-      }
+      BlkS A;
+      split_blk(raw, A);
+      const f4 a1 = mma_blks(A, BX, zero4());
+      const f4 ap = apply_tab<false>(cd, s.M, Su, I, cb, t1, t2, Uw);
+#pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int i = I * BS + out_row(e), c = cb * 16 + out_col();
-        p.d[(rowbase + i) * KD + c] = tot[e];
-        s.Pc[i][c] = tot[e];
+        const int i = I * BS + r4 + e;
+        const float dv = s.Pb[i][c] + __expf(cd.G[i][c]) * a1[e] + ap[e];
+        p.d[(rowbase + i) * KD + c] = dv;
+        s.Pc[i][c] = dv;
       }
     }
   }
