@@ -10,9 +10,11 @@ torch.autograd.grad for all 9 inputs and both initial states.
 
 Prints ONE JSON line (rank 0).  Besides the throughput it reports:
   roofline      the step's dominant kernel, timed with HIP events on its launch
-                stream inside a second pass over the same K steps, against the
-                bf16 dense MFMA peak (its algorithmic flops per launch are the
-                chunk GEMMs it evaluates, counted once at 2*M*N*K);
+                stream inside a second pass over the same K steps, against HBM
+                (its algorithmic bytes per launch: each tensor region of its
+                interface once; its flops per byte sit far below the MFMA ridge,
+                and the MFMA rate is reported beside it), with the HBM traffic
+                the counters measured for it and the whole step's floor;
   cpu_baseline  the FP64 token-loop oracle (oracle/sd_oracle.py) forward+VJP on
                 the host cores, on a bounded sample of the same workload.
 """
@@ -51,6 +53,46 @@ FLOPS_PER_CHUNK = {
 }
 
 
+# Algorithmic bytes per (sequence, 64-token chunk) of each kernel: every global
+# tensor region the kernel's interface reads or writes, counted once.  Units:
+# a bf16 input/output panel [64 x 128] 16 KiB; an FP32 panel, or an FP32 panel
+# stored as bf16 hi + lo halves, 32 KiB; an FP32 chunk-boundary state
+# [128 x 128] 64 KiB; a 64 x 64 FP32 block 16 KiB.  Reads + writes:
+_IN, _P, _S, _A = 16384, 32768, 65536, 16384
+BYTES_PER_CHUNK = {
+    "k_prep_c": (2 * _IN + _P) + (_A + 3 * _P),             # u,h,decay -> A,W,U,K
+    "state_c_fwd": 3 * _P + (_S + _P),                      # W,U,K -> state slot, delta
+    "k_prep_s": (6 * _IN + 2 * _P + _S) + (2 * _A + 7 * _P),  # inputs,decay,delta,C0 -> A,P,U,K,Q,W,chi,d,e
+    "state_s_fwd": (4 * _P + _A) + (_S + _P + _IN),         # W,U,K,Q,P -> state slot, w, out
+    "k_bprep_s": (2 * _A + 5 * _P) + 5 * _P,                # A,P,e,k,decay,K,Q -> dU,Wk,At1,B1t,Ant
+    "state_s_bwd": 5 * _P + (_S + _P),                      # Wk,dU,Ant,At1,B1t -> lambda slot, dw
+    "state_c_bwd": 5 * _P + (_S + _P),
+    "k_grad_s": (7 * _P + 3 * _S) + 4 * _P,                 # dw,chi,d,e,w,k,decay,X0,XC,lambda -> dchi,dd,de,dg
+    "k_src_bwd": (6 * _IN + 5 * _P) + (3 * _P + 4 * _IN),   # inputs,delta,d*,dw -> du,dk,ddelta,dq,dv,der,dwr
+    "k_bprep_c": (_A + 2 * _IN + 4 * _P) + 7 * _P,          # A,u,k,decay,K,dd,ddelta -> k,dU,u,Ant,At1,B1t,Wk
+    "k_grad_c": (7 * _P + 3 * _S) + 5 * _P,                 # dw,delta,dd,k,u,d,decay,X0,XC,lambda -> dx,dk,dg,xdx,dq
+    "k_final": (3 * _IN + 8 * _P) + (3 * _IN + _P),         # u,h,k, 8 partial grads -> du,dh,dk,dlog_decay
+}
+
+# HBM bytes per dispatch of each kernel at this workload, from rocprofv3 counter
+# runs (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads for a
+# plain 1 GiB device copy: x2.0 and x1.0); the runs and the table are in
+# profiles/fwd_bwd_B4_T2048_H8_d128_hbm_traffic.txt.  Static figures: a kernel
+# change needs a new counter run.
+TRAFFIC_MB = {
+    "k_prep_c": 186.0, "state_c_fwd": 206.2, "k_prep_s": 533.9, "state_s_fwd": 273.4,
+    "k_bprep_s": 392.3, "state_s_bwd": 271.3, "state_c_bwd": 271.3, "k_grad_s": 1058.9,
+    "k_src_bwd": 436.3, "k_bprep_c": 458.4, "k_grad_c": 1062.9, "k_final": 403.6,
+}
+
+
+_NTH = B * T * H
+STEP_FLOOR_BYTES = (_NTH * 2564 + B * H * 4 * R * R * 4          # forward
+                    + _NTH * (7 * 2 * R + 4 * R + 4 + 2 * V)     # backward: inputs, dO
+                    + _NTH * (7 * 2 * R + 4 * R + 4)             # backward: cotangents
+                    + B * H * 4 * R * R * 4)                     # dC_T, dS_T, dC0, dS0
+
+
 def make_inputs(device, seed=0, b=B, t=T):
     import torch.nn.functional as F
     g = torch.Generator().manual_seed(seed)
@@ -69,9 +111,10 @@ def make_inputs(device, seed=0, b=B, t=T):
     return [u, h, q, k, v, gd, er, wr, gm], (C0, S0), dO
 
 
-def cpu_baseline(budget_s=15.0):
+def cpu_baseline(budget_s=24.0):
     """FP64 oracle forward + autograd VJP on the host, bounded sample: all 32
-    (b,h) sequences, T tokens with T grown until one pass costs ~budget_s/2."""
+    (b,h) sequences, T tokens with T doubled (up to the full T) while the next
+    pass is predicted to stay under budget_s."""
     from oracle.sd_oracle import OracleState, solvedelta_oracle_raw
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
@@ -85,8 +128,8 @@ def cpu_baseline(budget_s=15.0):
         torch.autograd.grad(o, ins + st, dO.double())
         return time.perf_counter() - t0
 
-    tt, dt = 8, run(8)
-    while dt < budget_s / 2 and tt < 512:
+    tt, dt = 64, run(64)
+    while dt * 2.2 < budget_s and tt < T:
         tt *= 2
         dt = run(tt)
     return {"value": B * tt / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
@@ -139,7 +182,19 @@ def decode_bench(dev, steps=256, streams=64):
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM / 1e9,
                          "unit": "GB/s", "frac": round(gbs * 1e9 / PEAK_HBM, 4),
                          "bytes_per_launch": state_bytes + in_bytes,
-                         "note": "64 MiB state fits the 256 MB MALL; see DESIGN.md"}}
+                         "note": "the 64 MiB of state fits the 256 MB last-level cache"}}
+
+
+def copy_calibration(dev, nbytes=1 << 30):
+    """A plain device copy of `nbytes` (read nbytes, write nbytes), launched a few
+    times: the FETCH_SIZE / WRITE_SIZE counters of these launches give the
+    factor that turns the counters of the operator's kernels into bytes."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 3}), flush=True)
 
 
 def main():
@@ -148,14 +203,20 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the per-(batch, head) recurrence shards with no exchange; see DESIGN.md)",
+              "(the per-(batch, head) recurrence shards over GPUs with no exchange)",
               file=sys.stderr)
         sys.exit(2)
-    from solvedelta_amd import _lib, solvedelta_native
     dev = torch.device("cuda:0")
+    if a.copy_calibration:
+        copy_calibration(dev)
+        return
+    from solvedelta_amd import _lib, solvedelta_native
     ins, st, dO = make_inputs(dev)
     leaves = ins + list(st)
 
@@ -184,12 +245,24 @@ def main():
     tot_ms, cnt = prof[dom]
     avg_s = tot_ms / cnt / 1e3
     flops = FLOPS_PER_CHUNK.get(dom, 0) * nchunks
-    achieved = flops / avg_s / 1e12
-    roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3),
-            "peak": PEAK_MFMA_BF16 / 1e12, "unit": "TFLOP/s",
-            "frac": round(achieved * 1e12 / PEAK_MFMA_BF16, 5), "traffic": None,
+    nbytes = BYTES_PER_CHUNK[dom] * nchunks
+    # Arithmetic intensity flops/bytes of every kernel here is far below the
+    # MFMA/HBM ridge (2.5e15 / 8e12 = 312 flop/B), so HBM is the bounding roof.
+    gbs = nbytes / avg_s / 1e9
+    roof = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1),
+            "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(gbs * 1e9 / PEAK_HBM, 4),
+            "algorithmic_bytes": nbytes, "intensity_flop_per_byte": round(flops / nbytes, 1),
+            "mfma_tflops": round(flops / avg_s / 1e12, 3),
+            "traffic": TRAFFIC_MB[dom] * 1e6 if dom in TRAFFIC_MB else None,
+            "traffic_unit": "bytes per launch",
             "avg_us": round(avg_s * 1e6, 2),
-            "kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in sorted(prof.items())}}
+            "kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in sorted(prof.items())},
+            # whole step against its own floor: each operator input, output and
+            # boundary state touched once (forward 2,564 B per token-head plus
+            # 256 KiB of C0/S0/C_T/S_T per sequence; backward re-reads the inputs
+            # and dO and writes the 11 cotangents)
+            "step_floor_us": round(STEP_FLOOR_BYTES / PEAK_HBM * 1e6, 1),
+            "step_frac": round(STEP_FLOOR_BYTES / PEAK_HBM / dt, 4)}
     res = {
         "metric": "SolveDelta layer fwd+bwd tokens/s @B4 T2048 H8 d128; % MFMA/HBM roofline",
         "value": round(B * T / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
@@ -200,7 +273,8 @@ def main():
                    "heads": H, "dk": R, "dv": V, "chunk": CH, "parallelism": "single-gpu"},
         "roofline": roof,
     }
-    res["decode"] = decode_bench(dev)
+    if not a.no_decode:
+        res["decode"] = decode_bench(dev)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
