@@ -2,153 +2,245 @@
 // (reference: causallsso/ops/residual_frame/recurrent.py:33-185 and FLA's
 // fused recurrent DPLR step it delegates to).
 //
-// One 256-thread workgroup per (batch, head).  C is staged through LDS so the
-// row reductions (C u) and column reductions (C'^T k) both read it once from
-// HBM; S is streamed column-wise (two threads per value column, 64 rows each).
-// State traffic per (b,h): read C and S once, write C' and S' once.
+// One 256-thread workgroup per (batch, head).  Every thread owns a 16-row x
+// 4-column patch of C and of S (columns 4*(tid & 31), rows 16*(tid >> 5)), and
+// issues all 32 of its 16-byte state loads before any arithmetic, so the whole
+// 128 KiB of state per (b,h) is in flight at once and the HBM latency is paid
+// once.  Row reductions of C (C u) go through an LDS copy of C; column
+// reductions (C'^T k, S'^T e, S^T chi) reduce the patches across the eight row
+// groups (lane xor 32, then the four waves through LDS).  The new states are
+// written back from registers with 16-byte stores.
+// State traffic per (b,h): read C and S once, write C' and S' once.  In place
+// (C_T == C0, S_T == S0) is allowed: a workgroup reads its state before it
+// writes it and touches no other workgroup's.
 #include "sd_common.cuh"
 #include "sd_internal.h"
 
 namespace sd {
 
+constexpr int DCS = KD + 4;  // LDS row stride of C (16-byte aligned rows)
+
 struct DecodeSmem {
-  float C[KD][KD + 1];
-  float u[KD], k[KD], q[KD], g[KD], hh[KD], er[KD];
-  float delta[KD], d[KD], e[KD], chi[KD], z[VD], pred[VD];
-  float red[8];
+  float C[KD][DCS];
+  float u[KD], k[KD], q[KD], eg[KD], hh[KD];
+  float delta[KD], d[KD], e[KD], chi[KD], z[VD];
+  float4 part[4][32];
+  float red[4][4];
 };
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wave_sum(v);
+// Sum of up to four per-thread values over the workgroup (one barrier pair).
+template <int N>
+__device__ __forceinline__ void block_sums(float (&v)[N], float (&red)[4][4]) {
+#pragma unroll
+  for (int m = 0; m < N; ++m) v[m] = wave_sum(v[m]);
   __syncthreads();
-  if (lane_id() == 0) red[wave_id()] = v;
+  if (lane_id() == 0)
+#pragma unroll
+    for (int m = 0; m < N; ++m) red[wave_id()][m] = v[m];
   __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
+#pragma unroll
+  for (int m = 0; m < N; ++m) v[m] = red[0][m] + red[1][m] + red[2][m] + red[3][m];
+}
+
+// Column sums of the per-thread float4 partials over the 8 row groups: the
+// result for columns 4*(tid & 31) .. +3 is returned to every thread.
+__device__ __forceinline__ float4 col_sums(float4 v, float4 (&part)[4][32]) {
+  v.x += __shfl_xor(v.x, 32, 64);
+  v.y += __shfl_xor(v.y, 32, 64);
+  v.z += __shfl_xor(v.z, 32, 64);
+  v.w += __shfl_xor(v.w, 32, 64);
+  __syncthreads();
+  if (lane_id() < 32) part[wave_id()][lane_id()] = v;
+  __syncthreads();
+  const int cg = threadIdx.x & 31;
+  float4 r = part[0][cg];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    const float4 t = part[w][cg];
+    r.x += t.x; r.y += t.y; r.z += t.z; r.w += t.w;
+  }
+  return r;
+}
+
+__device__ __forceinline__ float4 ld4(const float* base, int row, int col, int ld, int nrow,
+                                      int ncol, bool vec) {
+  if (!base || row >= nrow) return make_float4(0.f, 0.f, 0.f, 0.f);
+  const float* p = base + (long long)row * ld + col;
+  if (vec && col + 3 < ncol) return *reinterpret_cast<const float4*>(p);
+  float t[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) t[m] = col + m < ncol ? p[m] : 0.f;
+  return make_float4(t[0], t[1], t[2], t[3]);
+}
+
+__device__ __forceinline__ void st4(float* base, int row, int col, int ld, int nrow, int ncol,
+                                    bool vec, float4 v) {
+  if (row >= nrow) return;
+  float* p = base + (long long)row * ld + col;
+  if (vec && col + 3 < ncol) {
+    *reinterpret_cast<float4*>(p) = v;
+    return;
+  }
+  const float t[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    if (col + m < ncol) p[m] = t[m];
+}
+
+__device__ __forceinline__ float f4get(const float4& v, int m) {
+  return m == 0 ? v.x : m == 1 ? v.y : m == 2 ? v.z : v.w;
 }
 
 __global__ __launch_bounds__(NTHREADS) void k_decode(sd_inputs in, __bf16* out, float* C_T,
-                                                     float* S_T) {
+                                                     float* S_T, int vec) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   DecodeSmem& s = *reinterpret_cast<DecodeSmem*>(smem_raw);
   const int n = blockIdx.x, b = n / in.H, hd = n % in.H;
   const int r = in.r, V = in.V, tid = threadIdx.x;
+  const int cg = tid & 31, c0 = cg * 4, rg = tid >> 5, i0 = rg * 16;
+  // ---- issue every state load first
+  const float* C0 = in.C0 ? in.C0 + (long long)n * r * r : nullptr;
+  const float* S0 = in.S0 ? in.S0 + (long long)n * r * V : nullptr;
+  float4 cv[16], sv[16];
+#pragma unroll
+  for (int a = 0; a < 16; ++a) cv[a] = ld4(C0, i0 + a, c0, r, r, r, vec);
+#pragma unroll
+  for (int a = 0; a < 16; ++a) sv[a] = ld4(S0, i0 + a, c0, V, r, V, vec);
   auto ld = [&](const sd_view& v, int c, int w) -> float {
     if (c >= w) return 0.f;
     return bf2f(((const __bf16*)v.data)[(long long)b * v.sb + (long long)hd * v.sh + c]);
   };
-  float uu = 0.f, kk = 0.f, qq = 0.f;
+  float uu = 0.f, kk = 0.f, qq = 0.f, er = 0.f;
   if (tid < KD) {
     const int c = tid;
     uu = ld(in.u, c, r); kk = ld(in.k, c, r); qq = ld(in.q, c, r);
+    er = ld(in.erase_raw, c, r);
     s.hh[c] = ld(in.h, c, r);
-    s.er[c] = ld(in.erase_raw, c, r);
-    s.g[c] = c < r ? ((const float*)in.log_decay.data)[(long long)b * in.log_decay.sb +
-                                                       (long long)hd * in.log_decay.sh + c]
-                   : 0.f;
+    s.eg[c] = c < r ? __expf(((const float*)in.log_decay.data)[(long long)b * in.log_decay.sb +
+                                                               (long long)hd * in.log_decay.sh + c])
+                    : 0.f;
     s.z[c] = ld(in.v, c, V) / (1.f + __expf(-ld(in.write_raw, c, V)));
-  }
-  const float su = block_sum(uu * uu, s.red);
-  const float sk = block_sum(kk * kk, s.red);
-  const float sq = block_sum(qq * qq, s.red);
-  if (tid < KD) {
-    s.u[tid] = uu * rsqrtf(su + 1e-24f);
-    s.k[tid] = kk * rsqrtf(sk + 1e-24f);
-    s.q[tid] = qq * rsqrtf(sq + 1e-24f);
   }
   const float gam = ((const float*)in.gamma.data)[(long long)b * in.gamma.sb +
                                                   (long long)hd * in.gamma.sh];
-  // stage C (zero when no initial state)
-  const float* C0 = in.C0 ? in.C0 + (long long)n * r * r : nullptr;
-  for (int idx = tid; idx < KD * KD; idx += NTHREADS) {
-    const int i = idx / KD, j = idx % KD;
-    s.C[i][j] = (C0 && i < r && j < r) ? C0[(long long)i * r + j] : 0.f;
+  {
+    float sq3[3] = {uu * uu, kk * kk, qq * qq};
+    block_sums(sq3, s.red);
+    uu *= rsqrtf(sq3[0] + 1e-24f);
+    kk *= rsqrtf(sq3[1] + 1e-24f);
+    qq *= rsqrtf(sq3[2] + 1e-24f);
   }
+  if (tid < KD) {
+    s.u[tid] = uu;
+    s.k[tid] = kk;
+  }
+#pragma unroll
+  for (int a = 0; a < 16; ++a) *reinterpret_cast<float4*>(&s.C[i0 + a][c0]) = cv[a];
   __syncthreads();
   // delta_i = gamma (h_i - sum_j C_ij u_j): two threads per row
   {
     const int i = tid >> 1, half = tid & 1;
     float acc = 0.f;
-    for (int j = half * 64; j < half * 64 + 64; ++j) acc += s.C[i][j] * s.u[j];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const int j = half * 64 + m * 4;
+      const float4 c = *reinterpret_cast<const float4*>(&s.C[i][j]);
+      acc += c.x * s.u[j] + c.y * s.u[j + 1] + c.z * s.u[j + 2] + c.w * s.u[j + 3];
+    }
     acc += __shfl_xor(acc, 1, 64);
     if (half == 0) s.delta[i] = gam * (s.hh[i] - acc);
   }
   __syncthreads();
-  // C' = C diag(e^g) + delta u^T
-  for (int idx = tid; idx < KD * KD; idx += NTHREADS) {
-    const int i = idx / KD, j = idx % KD;
-    s.C[i][j] = s.C[i][j] * __expf(s.g[j]) + s.delta[i] * s.u[j];
-  }
-  __syncthreads();
-  if (C_T) {
-    float* Cn = C_T + (long long)n * r * r;
-    for (int idx = tid; idx < r * r; idx += NTHREADS) Cn[idx] = s.C[idx / r][idx % r];
-  }
-  // d_j = k_j + sum_i C'_ij k_i: two threads per column
+  // C' = C diag(e^g) + delta u^T in registers; d_j = k_j + sum_i C'_ij k_i
   {
-    const int j = tid >> 1, half = tid & 1;
-    float acc = 0.f;
-    for (int i = half * 64; i < half * 64 + 64; ++i) acc += s.C[i][j] * s.k[i];
-    acc += __shfl_xor(acc, 1, 64);
-    if (half == 0) s.d[j] = s.k[j] + acc;
+    float egc[4], uc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      egc[m] = s.eg[c0 + m];
+      uc[m] = s.u[c0 + m];
+    }
+    float4 dp = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      const float dl = s.delta[i0 + a], ki = s.k[i0 + a];
+      float4& c = cv[a];
+      c.x = c.x * egc[0] + dl * uc[0];
+      c.y = c.y * egc[1] + dl * uc[1];
+      c.z = c.z * egc[2] + dl * uc[2];
+      c.w = c.w * egc[3] + dl * uc[3];
+      dp.x += c.x * ki; dp.y += c.y * ki; dp.z += c.z * ki; dp.w += c.w * ki;
+    }
+    if (C_T) {
+      float* Cn = C_T + (long long)n * r * r;
+#pragma unroll
+      for (int a = 0; a < 16; ++a) st4(Cn, i0 + a, c0, r, r, r, vec, cv[a]);
+    }
+    dp = col_sums(dp, s.part);
+    if (rg == 0) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) s.d[c0 + m] = s.k[c0 + m] + f4get(dp, m);
+    }
   }
-  // sources
+  // sources: phi = rho delta / sqrt(rho^2 + |u|^2 |delta|^2), den = 1 + phi.u
   const float dl = tid < KD ? s.delta[tid] : 0.f;
-  const float uv = tid < KD ? s.u[tid] : 0.f;
-  const float usq = block_sum(uv * uv, s.red);
-  const float dsq = block_sum(dl * dl, s.red);
-  const float sc = RHO / sqrtf(RHO * RHO + usq * dsq);
-  const float phi = sc * dl;
-  const float den = 1.f + block_sum(phi * uv, s.red);
-  const float bb = tid < KD ? s.k[tid] / (1.f + __expf(-s.er[tid])) : 0.f;
-  const float qv = tid < KD ? s.q[tid] : 0.f;
-  const float ub = block_sum(uv * bb, s.red) / den;
-  const float uq = block_sum(uv * qv, s.red) / den;
+  float nrm[2] = {uu * uu, dl * dl};
+  block_sums(nrm, s.red);
+  const float phi = RHO / sqrtf(RHO * RHO + nrm[0] * nrm[1]) * dl;
+  float pd[1] = {phi * uu};
+  block_sums(pd, s.red);
+  const float den = 1.f + pd[0];
+  const float bb = tid < KD ? kk / (1.f + __expf(-er)) : 0.f;
+  float pr2[2] = {uu * bb, uu * qq};
+  block_sums(pr2, s.red);
   if (tid < KD) {
-    s.e[tid] = bb - phi * ub;
-    s.chi[tid] = qv - phi * uq;
+    s.e[tid] = bb - phi * (pr2[0] / den);
+    s.chi[tid] = qq - phi * (pr2[1] / den);
   }
   __syncthreads();
-  // S: two threads per value column v, rows split in halves
+  // S' = D S + d (z - (D S)^T e)^T ;  o = S'^T chi
   {
-    const int v = tid >> 1, half = tid & 1;
-    const float* S0 = in.S0 ? in.S0 + (long long)n * r * V : nullptr;
-    float sv[64];
-    float pr = 0.f;
+    float4 pr = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int a = 0; a < 64; ++a) {
-      const int i = half * 64 + a;
-      float x = (S0 && i < r && v < V) ? S0[(long long)i * V + v] : 0.f;
-      x *= __expf(s.g[i]);
-      sv[a] = x;
-      pr += x * s.e[i];
+    for (int a = 0; a < 16; ++a) {
+      const float g = s.eg[i0 + a], ei = s.e[i0 + a];
+      float4& x = sv[a];
+      x.x *= g; x.y *= g; x.z *= g; x.w *= g;
+      pr.x += x.x * ei; pr.y += x.y * ei; pr.z += x.z * ei; pr.w += x.w * ei;
     }
-    pr += __shfl_xor(pr, 1, 64);
-    const float upd = s.z[v] - pr;
-    float o = 0.f;
+    pr = col_sums(pr, s.part);
+    float upd[4];
 #pragma unroll
-    for (int a = 0; a < 64; ++a) {
-      const int i = half * 64 + a;
-      sv[a] += s.d[i] * upd;
-      o += sv[a] * s.chi[i];
+    for (int m = 0; m < 4; ++m) upd[m] = s.z[c0 + m] - f4get(pr, m);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      const float di = s.d[i0 + a], ci = s.chi[i0 + a];
+      float4& x = sv[a];
+      x.x += di * upd[0]; x.y += di * upd[1]; x.z += di * upd[2]; x.w += di * upd[3];
+      o.x += x.x * ci; o.y += x.y * ci; o.z += x.z * ci; o.w += x.w * ci;
     }
-    o += __shfl_xor(o, 1, 64);
-    if (S_T && v < V) {
+    if (S_T) {
       float* Sn = S_T + (long long)n * r * V;
 #pragma unroll
-      for (int a = 0; a < 64; ++a) {
-        const int i = half * 64 + a;
-        if (i < r) Sn[(long long)i * V + v] = sv[a];
-      }
+      for (int a = 0; a < 16; ++a) st4(Sn, i0 + a, c0, V, r, V, vec, sv[a]);
     }
-    if (half == 0 && v < V) out[(long long)n * V + v] = f2bf(o);
+    o = col_sums(o, s.part);
+    if (rg == 0) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        if (c0 + m < V) out[(long long)n * V + c0 + m] = f2bf(f4get(o, m));
+    }
   }
 }
 
 int launch_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, hipStream_t st) {
   (void)hipFuncSetAttribute((const void*)k_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)sizeof(DecodeSmem));
+  auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const int vec = (in->r % 4 == 0) && (in->V % 4 == 0) && al(in->C0) && al(in->S0) && al(C_T) &&
+                  al(S_T);
   SD_LAUNCH("k_decode", k_decode, dim3(in->B * in->H), dim3(NTHREADS), sizeof(DecodeSmem), st, *in,
-                     (__bf16*)out, C_T, S_T);
+            (__bf16*)out, C_T, S_T, vec);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 
