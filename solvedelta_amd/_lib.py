@@ -40,6 +40,23 @@ EXPORTS = {
     "sd_profile_read": (ctypes.c_size_t, [ctypes.c_char_p, ctypes.c_size_t]),
     "sd_decode": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
                                  ctypes.c_void_p, ctypes.c_void_p]),
+    # mixer frontend / readout (include/solvedelta_mixer.h)
+    "sd_conv4_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 3),
+    "sd_conv4_silu_fwd": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_int64] + [ctypes.c_void_p] * 5),
+    "sd_conv4_silu_bwd": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_int64] + [ctypes.c_void_p] * 8
+                          + [ctypes.c_size_t, ctypes.c_void_p]),
+    "sd_kda_gate_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 3),
+    "sd_kda_gate_fwd": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64]
+                        + [ctypes.c_void_p] * 4),
+    "sd_kda_gate_bwd": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64]
+                        + [ctypes.c_void_p] * 7 + [ctypes.c_size_t, ctypes.c_void_p]),
+    "sd_rmsnorm_gated_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 2),
+    "sd_rmsnorm_gated_fwd": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_float]
+                             + [ctypes.c_void_p] * 6),
+    "sd_rmsnorm_gated_bwd": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_float]
+                             + [ctypes.c_void_p] * 9 + [ctypes.c_size_t, ctypes.c_void_p]),
 }
 
 _lib = None

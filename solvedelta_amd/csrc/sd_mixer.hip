@@ -1,0 +1,404 @@
+// Mixer frontend and readout of the SolveDelta layer on MI355X:
+//   * causal depthwise conv4 + SiLU with initial / final state
+//     (reference: causallsso/model.py:119-136, CPU semantics :146-164);
+//   * the KDA decay gate  log_decay = -exp(log_rate[h]) * softplus(raw + bias[h, c])
+//     (reference: causallsso/model.py:375-390);
+//   * the sigmoid-gated RMSNorm feeding the output projection
+//     (reference: causallsso/ops/norm_gate.py:20-43 definition, :46-150 owner).
+// Forward and backward of each; parameter-gradient reductions are two-stage
+// (per-workgroup partials in the caller's workspace, then one reduction kernel),
+// so results are deterministic.  All arithmetic is FP32; bf16 in / out.
+#include <hip/hip_runtime.h>
+
+#include "sd_common.cuh"
+#include "sd_internal.h"
+#include "../../include/solvedelta_mixer.h"
+
+namespace sd {
+
+__device__ __forceinline__ float silu(float a) { return a / (1.f + __expf(-a)); }
+__device__ __forceinline__ float sigm(float a) { return 1.f / (1.f + __expf(-a)); }
+// torch.nn.functional.softplus with its default threshold 20
+__device__ __forceinline__ float softplus20(float x) {
+  return x > 20.f ? x : log1pf(__expf(x));
+}
+
+// ---------------------------------------------------------------------------
+// conv4 + SiLU.  One thread per (channel, batch row, 64-token chunk); the three
+// previous inputs slide through registers.  xs[-3..-1] is the initial state
+// (zeros when absent); y_t = silu(sum_k w_k xs[t-3+k]).
+// ---------------------------------------------------------------------------
+constexpr int CONV_TC = 64;
+
+struct ConvArgs {
+  int B, T, D;
+  const __bf16* x;
+  long long sb, st;
+  const float* w;       // [D][4]
+  const __bf16* init;   // [B][D][3] or null
+};
+
+__device__ __forceinline__ float conv_x(const ConvArgs& a, int b, int t, int d) {
+  if (t >= 0) return bf2f(a.x[(long long)b * a.sb + (long long)t * a.st + d]);
+  if (!a.init) return 0.f;
+  return bf2f(a.init[((long long)b * a.D + d) * 3 + (t + 3)]);
+}
+
+__global__ __launch_bounds__(NTHREADS) void k_conv_fwd(ConvArgs a, __bf16* y, __bf16* fin) {
+  const int d = blockIdx.x * NTHREADS + threadIdx.x, b = blockIdx.z;
+  if (d >= a.D) return;
+  const int t0 = blockIdx.y * CONV_TC, t1 = min(a.T, t0 + CONV_TC);
+  const float w0 = a.w[d * 4], w1 = a.w[d * 4 + 1], w2 = a.w[d * 4 + 2], w3 = a.w[d * 4 + 3];
+  float xm3 = conv_x(a, b, t0 - 3, d), xm2 = conv_x(a, b, t0 - 2, d), xm1 = conv_x(a, b, t0 - 1, d);
+  for (int t = t0; t < t1; ++t) {
+    const float x = conv_x(a, b, t, d);
+    const float acc = w0 * xm3 + w1 * xm2 + w2 * xm1 + w3 * x;
+    y[((long long)b * a.T + t) * a.D + d] = f2bf(silu(acc));
+    xm3 = xm2; xm2 = xm1; xm1 = x;
+  }
+  if (fin && t1 == a.T) {  // the chunk that holds the last token writes the state
+    __bf16* f = fin + ((long long)b * a.D + d) * 3;
+    f[0] = f2bf(conv_x(a, b, a.T - 3, d));
+    f[1] = f2bf(conv_x(a, b, a.T - 2, d));
+    f[2] = f2bf(conv_x(a, b, a.T - 1, d));
+  }
+}
+
+// Backward.  da_t = dy_t silu'(a_t);  dx_s = sum_k w_k da_{s+3-k} (+ dfinal);
+// dw_k = sum_t da_t xs[t-3+k];  dinit_j = sum_{k<=j} w_k da_{j-k} (+ dfinal).
+// Thread (d, b, chunk) walks t = t0 .. t1+2 keeping x and da windows of 4.
+__global__ __launch_bounds__(NTHREADS) void k_conv_bwd(ConvArgs a, const __bf16* dy,
+                                                       const __bf16* dfin, __bf16* dx,
+                                                       float* dinit, float* dw_part) {
+  const int d = blockIdx.x * NTHREADS + threadIdx.x, b = blockIdx.z;
+  if (d >= a.D) return;
+  const int T = a.T, t0 = blockIdx.y * CONV_TC, t1 = min(T, t0 + CONV_TC);
+  const float w0 = a.w[d * 4], w1 = a.w[d * 4 + 1], w2 = a.w[d * 4 + 2], w3 = a.w[d * 4 + 3];
+  // dfinal_m is the cotangent of xs[T-3+m]
+  float df[3] = {0.f, 0.f, 0.f};
+  if (dfin)
+    for (int m = 0; m < 3; ++m) df[m] = bf2f(dfin[((long long)b * a.D + d) * 3 + m]);
+  float xm3 = conv_x(a, b, t0 - 3, d), xm2 = conv_x(a, b, t0 - 2, d), xm1 = conv_x(a, b, t0 - 1, d);
+  float da3 = 0.f, da2 = 0.f, da1 = 0.f;  // da_{t-3}, da_{t-2}, da_{t-1}
+  float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f;
+  const int tend = min(T, t1 + 3);
+  for (int t = t0; t < t1 + 3; ++t) {
+    float da = 0.f, x = 0.f;
+    if (t < tend) {
+      x = conv_x(a, b, t, d);
+      const float acc = w0 * xm3 + w1 * xm2 + w2 * xm1 + w3 * x;
+      const float sg = sigm(acc);
+      da = bf2f(dy[((long long)b * T + t) * a.D + d]) * sg * (1.f + acc * (1.f - sg));
+      if (t < t1) {
+        g0 += da * xm3; g1 += da * xm2; g2 += da * xm1; g3 += da * x;
+      }
+    }
+    const int s = t - 3;  // dx_s needs da_{s..s+3} = (da3, da2, da1, da)
+    if (s >= t0) {
+      float v = w3 * da3 + w2 * da2 + w1 * da1 + w0 * da;
+      if (s >= T - 3) v += df[s - (T - 3)];
+      dx[((long long)b * T + s) * a.D + d] = f2bf(v);
+    }
+    da3 = da2; da2 = da1; da1 = da;
+    xm3 = xm2; xm2 = xm1; xm1 = x;
+    if (t == t0 + 2 && t0 == 0 && dinit) {
+      // da_0 .. da_2 are now in (da3, da2, da1) (zeros beyond T)
+      const float e0 = da3, e1 = da2, e2 = da1;
+      float* di = dinit + ((long long)b * a.D + d) * 3;
+      // xs[-3+j] feeds a_t for t = j - k >= 0 with weight w_k (k <= j)
+      float v0 = w0 * e0;
+      float v1 = w1 * e0 + w0 * e1;
+      float v2 = w2 * e0 + w1 * e1 + w0 * e2;
+      // final-state cotangents that land on the initial state (T < 3)
+      for (int m = 0; m < 3; ++m) {
+        const int j = T + m;  // xs index T-3+m  ->  init slot j when j < 3
+        if (j < 3) (j == 0 ? v0 : j == 1 ? v1 : v2) += df[m];
+      }
+      di[0] = v0; di[1] = v1; di[2] = v2;
+    }
+  }
+  float* p = dw_part + (((long long)b * gridDim.y + blockIdx.y) * a.D + d) * 4;
+  p[0] = g0; p[1] = g1; p[2] = g2; p[3] = g3;
+}
+
+// dw[d][k] = sum over partial slots
+__global__ __launch_bounds__(NTHREADS) void k_sum_parts(const float* part, int nparts, int width,
+                                                        float* out) {
+  const int i = blockIdx.x * NTHREADS + threadIdx.x;
+  if (i >= width) return;
+  float s = 0.f;
+  for (int p = 0; p < nparts; ++p) s += part[(long long)p * width + i];
+  out[i] = s;
+}
+
+// ---------------------------------------------------------------------------
+// KDA decay gate.  raw [N][H*r] bf16 (row stride), bias [H*r], log_rate [H].
+// ---------------------------------------------------------------------------
+constexpr int GATE_TR = 64;  // rows per backward workgroup
+
+__global__ __launch_bounds__(NTHREADS) void k_gate_fwd(int N, int H, int r, const __bf16* raw,
+                                                       long long rs, const float* log_rate,
+                                                       const float* bias, float* out) {
+  const int HR = H * r;
+  const long long i = (long long)blockIdx.x * NTHREADS + threadIdx.x;
+  if (i >= (long long)N * HR) return;
+  const int c = (int)(i % HR);
+  const long long n = i / HR;
+  const float x = bf2f(raw[n * rs + c]) + bias[c];
+  out[i] = -__expf(log_rate[c / r]) * softplus20(x);
+}
+
+// draw = dout * (-exp(lr)) * sigmoid(raw + bias) (softplus' is 1 above the
+// threshold); partials: dbias_c = sum draw, dlr_c = sum dout * out.
+__global__ __launch_bounds__(NTHREADS) void k_gate_bwd(int N, int H, int r, const __bf16* raw,
+                                                       long long rs, const float* log_rate,
+                                                       const float* bias, const float* dout,
+                                                       __bf16* draw, float* part) {
+  const int HR = H * r;
+  const int c = blockIdx.x * NTHREADS + threadIdx.x;
+  if (c >= HR) return;
+  const int n0 = blockIdx.y * GATE_TR, n1 = min(N, n0 + GATE_TR);
+  const float rate = __expf(log_rate[c / r]), bc = bias[c];
+  float db = 0.f, dl = 0.f;
+  for (int n = n0; n < n1; ++n) {
+    const float x = bf2f(raw[(long long)n * rs + c]) + bc;
+    const float g = dout[(long long)n * HR + c];
+    const float sp = softplus20(x);
+    const float dx = -rate * g * (x > 20.f ? 1.f : sigm(x));
+    draw[(long long)n * HR + c] = f2bf(dx);
+    db += dx;
+    dl += -rate * sp * g;
+  }
+  part[(long long)blockIdx.y * 2 * HR + c] = db;
+  part[(long long)blockIdx.y * 2 * HR + HR + c] = dl;
+}
+
+// One workgroup per head: dbias[c] for the head's columns, dlog_rate[h].
+__global__ __launch_bounds__(NTHREADS) void k_gate_reduce(int H, int r, int nparts,
+                                                          const float* part, float* dbias,
+                                                          float* dlog_rate) {
+  __shared__ float red[NTHREADS / 64];
+  const int h = blockIdx.x, HR = H * r;
+  float acc = 0.f;
+  for (int cc = threadIdx.x; cc < r; cc += NTHREADS) {
+    const int c = h * r + cc;
+    float db = 0.f, dl = 0.f;
+    for (int p = 0; p < nparts; ++p) {
+      db += part[(long long)p * 2 * HR + c];
+      dl += part[(long long)p * 2 * HR + HR + c];
+    }
+    dbias[c] = db;
+    acc += dl;
+  }
+  acc = wave_sum(acc);
+  if (lane_id() == 0) red[wave_id()] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int w = 0; w < NTHREADS / 64; ++w) s += red[w];
+    dlog_rate[h] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sigmoid-gated RMSNorm: y = x rstd w sigmoid(g), rstd = 1/sqrt(mean(x^2) + eps).
+// One wave per row of width D <= 256 (4 elements per lane).
+// ---------------------------------------------------------------------------
+constexpr int RMS_ROWS = 4;     // rows (waves) per workgroup
+constexpr int RMS_PART = 64;    // rows per dweight partial
+
+__device__ __forceinline__ void rms_row(const __bf16* x, const __bf16* g, const float* w, int D,
+                                        float (&xv)[4], float (&gv)[4], float (&wv)[4]) {
+  const int l = lane_id();
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int c = l + 64 * m;
+    const bool ok = c < D;
+    xv[m] = ok ? bf2f(x[c]) : 0.f;
+    gv[m] = ok ? bf2f(g[c]) : 0.f;
+    wv[m] = ok ? w[c] : 0.f;
+  }
+}
+
+__global__ __launch_bounds__(RMS_ROWS * 64) void k_rms_fwd(int N, int D, float eps,
+                                                           const __bf16* x, const __bf16* g,
+                                                           const float* w, __bf16* y,
+                                                           float* rstd_out) {
+  const int n = blockIdx.x * RMS_ROWS + wave_id();
+  if (n >= N) return;
+  float xv[4], gv[4], wv[4];
+  rms_row(x + (long long)n * D, g + (long long)n * D, w, D, xv, gv, wv);
+  const float ss = wave_sum(xv[0] * xv[0] + xv[1] * xv[1] + xv[2] * xv[2] + xv[3] * xv[3]);
+  const float rs = rsqrtf(ss / D + eps);
+  const int l = lane_id();
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int c = l + 64 * m;
+    if (c < D) y[(long long)n * D + c] = f2bf(xv[m] * rs * wv[m] * sigm(gv[m]));
+  }
+  if (rstd_out && l == 0) rstd_out[n] = rs;
+}
+
+// dx = rstd (gy - xhat mean(gy xhat)), gy = dy w s;  dg = dy xhat w s (1 - s);
+// dw_c = sum dy xhat s;  y (recomputed for the projection's weight gradient).
+__global__ __launch_bounds__(RMS_ROWS * 64) void k_rms_bwd(int N, int D, float eps,
+                                                           const __bf16* x, const __bf16* g,
+                                                           const float* w, const __bf16* dy,
+                                                           __bf16* dx, __bf16* dg, __bf16* y,
+                                                           float* part) {
+  __shared__ float pw[RMS_ROWS][256];
+  const int l = lane_id(), wv_ = wave_id();
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  // a workgroup covers RMS_PART rows: each wave walks RMS_PART / RMS_ROWS of them
+  const int base = blockIdx.x * RMS_PART;
+  for (int rr = wv_; rr < RMS_PART; rr += RMS_ROWS) {
+    const int n = base + rr;
+    if (n >= N) break;
+    float xv[4], gv[4], wv[4], dv[4];
+    rms_row(x + (long long)n * D, g + (long long)n * D, w, D, xv, gv, wv);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int c = l + 64 * m;
+      dv[m] = c < D ? bf2f(dy[(long long)n * D + c]) : 0.f;
+    }
+    const float ss = wave_sum(xv[0] * xv[0] + xv[1] * xv[1] + xv[2] * xv[2] + xv[3] * xv[3]);
+    const float rs = rsqrtf(ss / D + eps);
+    float gy[4], xh[4], sg[4], dot = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      sg[m] = sigm(gv[m]);
+      xh[m] = xv[m] * rs;
+      gy[m] = dv[m] * wv[m] * sg[m];
+      dot += gy[m] * xh[m];
+    }
+    dot = wave_sum(dot) / D;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int c = l + 64 * m;
+      if (c < D) {
+        const long long o = (long long)n * D + c;
+        dx[o] = f2bf(rs * (gy[m] - xh[m] * dot));
+        dg[o] = f2bf(dv[m] * xh[m] * wv[m] * sg[m] * (1.f - sg[m]));
+        if (y) y[o] = f2bf(xh[m] * wv[m] * sg[m]);
+        acc[m] += dv[m] * xh[m] * sg[m];
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) pw[wv_][l + 64 * m] = acc[m];
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += RMS_ROWS * 64) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < RMS_ROWS; ++k) s += pw[k][c];
+    part[(long long)blockIdx.x * D + c] = s;
+  }
+}
+
+static inline int cdiv(long long a, int b) { return (int)((a + b - 1) / b); }
+
+}  // namespace sd
+
+using namespace sd;
+
+extern "C" {
+
+size_t sd_conv4_workspace_bytes(int B, int T, int D) {
+  if (B <= 0 || T <= 0 || D <= 0) return 0;
+  return (size_t)B * cdiv(T, CONV_TC) * D * 4 * sizeof(float);
+}
+
+int sd_conv4_silu_fwd(int B, int T, int D, const void* x, int64_t x_sb, int64_t x_st,
+                      const float* w, const void* init, void* y, void* final_state, void* stream) {
+  if (B <= 0 || T <= 0 || D <= 0) return SD_ERR_SHAPE;
+  if (!x || !w || !y) return SD_ERR_ARG;
+  ConvArgs a{B, T, D, (const __bf16*)x, x_sb, x_st, w, (const __bf16*)init};
+  dim3 grid(cdiv(D, NTHREADS), cdiv(T, CONV_TC), B);
+  SD_LAUNCH("k_conv_fwd", k_conv_fwd, grid, dim3(NTHREADS), 0, (hipStream_t)stream, a,
+            (__bf16*)y, (__bf16*)final_state);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+int sd_conv4_silu_bwd(int B, int T, int D, const void* x, int64_t x_sb, int64_t x_st,
+                      const float* w, const void* init, const void* dy, const void* dfinal,
+                      void* dx, float* dw, float* dinit, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  if (B <= 0 || T <= 0 || D <= 0) return SD_ERR_SHAPE;
+  if (!x || !w || !dy || !dx || !dw || !workspace) return SD_ERR_ARG;
+  if (workspace_bytes < sd_conv4_workspace_bytes(B, T, D)) return SD_ERR_WORKSPACE;
+  ConvArgs a{B, T, D, (const __bf16*)x, x_sb, x_st, w, (const __bf16*)init};
+  const int nch = cdiv(T, CONV_TC);
+  hipStream_t st = (hipStream_t)stream;
+  SD_LAUNCH("k_conv_bwd", k_conv_bwd, dim3(cdiv(D, NTHREADS), nch, B), dim3(NTHREADS), 0, st, a,
+            (const __bf16*)dy, (const __bf16*)dfinal, (__bf16*)dx, dinit, (float*)workspace);
+  SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(4LL * D, NTHREADS)), dim3(NTHREADS), 0, st,
+            (const float*)workspace, B * nch, 4 * D, dw);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+size_t sd_kda_gate_workspace_bytes(int N, int H, int r) {
+  if (N <= 0 || H <= 0 || r <= 0) return 0;
+  return (size_t)cdiv(N, GATE_TR) * 2 * H * r * sizeof(float);
+}
+
+int sd_kda_gate_fwd(int N, int H, int r, const void* raw, int64_t raw_row_stride,
+                    const float* log_rate, const float* bias, float* out, void* stream) {
+  if (N <= 0 || H <= 0 || r <= 0) return SD_ERR_SHAPE;
+  if (!raw || !log_rate || !bias || !out) return SD_ERR_ARG;
+  SD_LAUNCH("k_gate_fwd", k_gate_fwd, dim3(cdiv((long long)N * H * r, NTHREADS)), dim3(NTHREADS),
+            0, (hipStream_t)stream, N, H, r, (const __bf16*)raw, raw_row_stride, log_rate, bias,
+            out);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+int sd_kda_gate_bwd(int N, int H, int r, const void* raw, int64_t raw_row_stride,
+                    const float* log_rate, const float* bias, const float* dout, void* draw,
+                    float* dlog_rate, float* dbias, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  if (N <= 0 || H <= 0 || r <= 0) return SD_ERR_SHAPE;
+  if (!raw || !log_rate || !bias || !dout || !draw || !dlog_rate || !dbias || !workspace)
+    return SD_ERR_ARG;
+  if (workspace_bytes < sd_kda_gate_workspace_bytes(N, H, r)) return SD_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  const int np = cdiv(N, GATE_TR);
+  SD_LAUNCH("k_gate_bwd", k_gate_bwd, dim3(cdiv(H * r, NTHREADS), np), dim3(NTHREADS), 0, st, N,
+            H, r, (const __bf16*)raw, raw_row_stride, log_rate, bias, dout, (__bf16*)draw,
+            (float*)workspace);
+  SD_LAUNCH("k_gate_reduce", k_gate_reduce, dim3(H), dim3(NTHREADS), 0, st, H, r, np,
+            (const float*)workspace, dbias, dlog_rate);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+size_t sd_rmsnorm_gated_workspace_bytes(int N, int D) {
+  if (N <= 0 || D <= 0) return 0;
+  return (size_t)cdiv(N, RMS_PART) * D * sizeof(float);
+}
+
+int sd_rmsnorm_gated_fwd(int N, int D, float eps, const void* x, const void* gate,
+                         const float* weight, void* y, float* rstd, void* stream) {
+  if (N <= 0 || D <= 0 || D > 256) return SD_ERR_SHAPE;
+  if (!x || !gate || !weight || !y) return SD_ERR_ARG;
+  SD_LAUNCH("k_rms_fwd", k_rms_fwd, dim3(cdiv(N, RMS_ROWS)), dim3(RMS_ROWS * 64), 0,
+            (hipStream_t)stream, N, D, eps, (const __bf16*)x, (const __bf16*)gate, weight,
+            (__bf16*)y, rstd);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+int sd_rmsnorm_gated_bwd(int N, int D, float eps, const void* x, const void* gate,
+                         const float* weight, const void* dy, void* dx, void* dgate,
+                         float* dweight, void* y, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  if (N <= 0 || D <= 0 || D > 256) return SD_ERR_SHAPE;
+  if (!x || !gate || !weight || !dy || !dx || !dgate || !dweight || !workspace) return SD_ERR_ARG;
+  if (workspace_bytes < sd_rmsnorm_gated_workspace_bytes(N, D)) return SD_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  const int np = cdiv(N, RMS_PART);
+  SD_LAUNCH("k_rms_bwd", k_rms_bwd, dim3(np), dim3(RMS_ROWS * 64), 0, st, N, D, eps,
+            (const __bf16*)x, (const __bf16*)gate, weight, (const __bf16*)dy, (__bf16*)dx,
+            (__bf16*)dgate, (__bf16*)y, (float*)workspace);
+  SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(D, NTHREADS)), dim3(NTHREADS), 0, st,
+            (const float*)workspace, np, D, dweight);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+}  // extern "C"

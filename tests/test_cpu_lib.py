@@ -1,5 +1,5 @@
 """CPU-side checks of the native boundary: the C-ABI library loads and exports
-every symbol include/solvedelta.h declares, the host-side validation raises the
+every symbol include/*.h declares, the host-side validation raises the
 reference's exception types, and the C token loop agrees with the FP64 oracle."""
 import ctypes
 import os
@@ -13,7 +13,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _declared():
-    text = open(os.path.join(ROOT, "include", "solvedelta.h")).read()
+    inc = os.path.join(ROOT, "include")
+    text = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc))
+                   if f.endswith(".h"))
     return sorted(set(re.findall(r"\b(sd_[a-z_]+)\s*\(", text)))
 
 
