@@ -185,6 +185,47 @@ def decode_bench(dev, steps=256, streams=64):
                          "note": "the 64 MiB of state fits the 256 MB last-level cache"}}
 
 
+def lm_bench(dev, steps=5, warmup=2):
+    """Config 4: SolveDelta causal LM forward + backward, hidden 1024, 24 layers,
+    H=8, r=V=128, vocab 32000, conv4, FP32 master weights under bf16 autocast,
+    B=2, T=1024 uniform-random token ids with labels = inputs; eager steps and
+    the HIP-graph captured step (optimizer outside, as in the reference)."""
+    from solvedelta_amd.graph import SolveDeltaGraphedTrainingStep
+    from solvedelta_amd.lm import SolveDeltaForCausalLM, SolveDeltaLMConfig
+    torch.manual_seed(0)
+    cfg = SolveDeltaLMConfig(hidden_size=1024, num_heads=8, head_k_dim=128, head_v_dim=128,
+                             num_hidden_layers=24, vocab_size=32000)
+    model = SolveDeltaForCausalLM(cfg).to(dev).train()
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 32000, (2, 1024), generator=g).to(dev)
+
+    def eager():
+        with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+            loss, _, _ = model(ids, labels=ids)
+        loss.backward()
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    t_eager = timed(eager)
+    step = SolveDeltaGraphedTrainingStep(model, ids, ids)
+    t_graph = timed(lambda: step(ids, ids).backward())
+    ntok = 2 * 1024
+    return {"workload": "causal LM F+B, hidden 1024 x 24 layers, H=8 r=V=128, vocab 32000, "
+                        "B=2 T=1024, FP32 master weights + bf16 autocast",
+            "params": sum(p.numel() for p in model.parameters()),
+            "eager_ms_per_step": round(t_eager * 1e3, 3),
+            "graph_ms_per_step": round(t_graph * 1e3, 3),
+            "value": round(ntok / t_graph, 1), "unit": "tokens/s"}
+
+
 def copy_calibration(dev, nbytes=1 << 30):
     """A plain device copy of `nbytes` (read nbytes, write nbytes), launched a few
     times: the FETCH_SIZE / WRITE_SIZE counters of these launches give the
@@ -204,6 +245,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-lm", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -275,6 +317,8 @@ def main():
     }
     if not a.no_decode:
         res["decode"] = decode_bench(dev)
+    if not a.no_lm:
+        res["causal_lm"] = lm_bench(dev)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

@@ -643,14 +643,10 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   p.du = (__bf16*)du; p.dh = (__bf16*)dh; p.dq = (__bf16*)dq; p.dk = (__bf16*)dk;
   p.dv = (__bf16*)dv; p.der = (__bf16*)derase; p.dwr = (__bf16*)dwrite;
   p.dg = dlog_decay; p.dgam = dgamma;
-  (void)hipFuncSetAttribute((const void*)k_bprep_s, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(BprepSSmem));
-  (void)hipFuncSetAttribute((const void*)k_grad_s, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(GradSmem));
-  (void)hipFuncSetAttribute((const void*)k_bprep_c, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(BprepCSmem));
-  (void)hipFuncSetAttribute((const void*)k_grad_c, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(GradCSmem));
+  SD_SMEM_ONCE(k_bprep_s, (int)sizeof(BprepSSmem));
+  SD_SMEM_ONCE(k_grad_s, (int)sizeof(GradSmem));
+  SD_SMEM_ONCE(k_bprep_c, (int)sizeof(BprepCSmem));
+  SD_SMEM_ONCE(k_grad_c, (int)sizeof(GradCSmem));
   const dim3 chunks(NT, n), rows((Tp + 3) / 4, n), blk(NTHREADS), cblk(CT);
   // S memory
   SD_LAUNCH("k_bprep_s", k_bprep_s, chunks, cblk, sizeof(BprepSSmem), st, p);

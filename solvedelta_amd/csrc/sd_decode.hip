@@ -234,8 +234,7 @@ __global__ __launch_bounds__(NTHREADS) void k_decode(sd_inputs in, __bf16* out, 
 }
 
 int launch_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, hipStream_t st) {
-  (void)hipFuncSetAttribute((const void*)k_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(DecodeSmem));
+  SD_SMEM_ONCE(k_decode, (int)sizeof(DecodeSmem));
   auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   const int vec = (in->r % 4 == 0) && (in->V % 4 == 0) && al(in->C0) && al(in->S0) && al(C_T) &&
                   al(S_T);

@@ -614,10 +614,8 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   fp.Wc = w.Wc; fp.Uc = w.Uc; fp.Kc = w.Kc; fp.Gam = w.Gam;
   fp.Ws = w.Ws; fp.Us = w.Us; fp.Ks = w.Ks; fp.Qs = w.Qs; fp.Ps = w.Ps;
 
-  (void)hipFuncSetAttribute((const void*)k_prep_c, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)prep_c_smem());
-  (void)hipFuncSetAttribute((const void*)k_prep_s, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)prep_s_smem());
+  SD_SMEM_ONCE(k_prep_c, (int)prep_c_smem());
+  SD_SMEM_ONCE(k_prep_s, (int)prep_s_smem());
   SD_LAUNCH("k_prep_c", k_prep_c, dim3(NT, n), dim3(CT), prep_c_smem(), st, fp);
 
   StateParams sc{};

@@ -68,6 +68,26 @@ struct StateParams {
 
 void prof_begin(const char* name, hipStream_t st);
 void prof_end(hipStream_t st);
+// Raises a kernel's dynamic-LDS limit once per device.  The attribute call is
+// not a stream operation; doing it only on the first (eager) launch keeps it
+// out of graph captures of later calls.
+inline void set_smem_once(const void* fn, int bytes, unsigned char* done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    return;
+  }
+  if (!done[dev]) {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    done[dev] = 1;
+  }
+}
+#define SD_SMEM_ONCE(kern, bytes)                                  \
+  do {                                                             \
+    static unsigned char sd_smem_done_[64] = {};                   \
+    ::sd::set_smem_once((const void*)(kern), (int)(bytes), sd_smem_done_); \
+  } while (0)
+
 #define SD_LAUNCH(name, kern, grid, block, smem, st, ...)                 \
   do {                                                                   \
     ::sd::prof_begin(name, st);                                          \

@@ -24,39 +24,44 @@ __device__ __forceinline__ float softplus20(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// conv4 + SiLU.  One thread per (channel, batch row, 64-token chunk); the three
-// previous inputs slide through registers.  xs[-3..-1] is the initial state
-// (zeros when absent); y_t = silu(sum_k w_k xs[t-3+k]).
+// conv4 + SiLU.  One thread per (channel, batch row, CONV_TC-token chunk): the
+// chunk's inputs (plus the 3-token halo) are loaded into registers up front so
+// the loads overlap, then the window slides through registers.  xs[-3..-1] is
+// the initial state (zeros when absent); y_t = silu(sum_k w_k xs[t-3+k]).
 // ---------------------------------------------------------------------------
-constexpr int CONV_TC = 64;
+constexpr int CONV_TC = 32;
 
 struct ConvArgs {
   int B, T, D;
-  const __bf16* x;
+  const __bf16* __restrict__ x;
   long long sb, st;
-  const float* w;       // [D][4]
-  const __bf16* init;   // [B][D][3] or null
+  const float* __restrict__ w;       // [D][4]
+  const __bf16* __restrict__ init;   // [B][D][3] or null
 };
 
 __device__ __forceinline__ float conv_x(const ConvArgs& a, int b, int t, int d) {
+  if (t >= a.T) return 0.f;
   if (t >= 0) return bf2f(a.x[(long long)b * a.sb + (long long)t * a.st + d]);
   if (!a.init) return 0.f;
   return bf2f(a.init[((long long)b * a.D + d) * 3 + (t + 3)]);
 }
 
-__global__ __launch_bounds__(NTHREADS) void k_conv_fwd(ConvArgs a, __bf16* y, __bf16* fin) {
+__global__ __launch_bounds__(NTHREADS) void k_conv_fwd(ConvArgs a, __bf16* __restrict__ y,
+                                                       __bf16* __restrict__ fin) {
   const int d = blockIdx.x * NTHREADS + threadIdx.x, b = blockIdx.z;
   if (d >= a.D) return;
-  const int t0 = blockIdx.y * CONV_TC, t1 = min(a.T, t0 + CONV_TC);
+  const int t0 = blockIdx.y * CONV_TC;
   const float w0 = a.w[d * 4], w1 = a.w[d * 4 + 1], w2 = a.w[d * 4 + 2], w3 = a.w[d * 4 + 3];
-  float xm3 = conv_x(a, b, t0 - 3, d), xm2 = conv_x(a, b, t0 - 2, d), xm1 = conv_x(a, b, t0 - 1, d);
-  for (int t = t0; t < t1; ++t) {
-    const float x = conv_x(a, b, t, d);
-    const float acc = w0 * xm3 + w1 * xm2 + w2 * xm1 + w3 * x;
-    y[((long long)b * a.T + t) * a.D + d] = f2bf(silu(acc));
-    xm3 = xm2; xm2 = xm1; xm1 = x;
+  float xv[CONV_TC + 3];
+#pragma unroll
+  for (int j = 0; j < CONV_TC + 3; ++j) xv[j] = conv_x(a, b, t0 - 3 + j, d);
+#pragma unroll
+  for (int j = 0; j < CONV_TC; ++j) {
+    const int t = t0 + j;
+    const float acc = w0 * xv[j] + w1 * xv[j + 1] + w2 * xv[j + 2] + w3 * xv[j + 3];
+    if (t < a.T) y[((long long)b * a.T + t) * a.D + d] = f2bf(silu(acc));
   }
-  if (fin && t1 == a.T) {  // the chunk that holds the last token writes the state
+  if (fin && t0 + CONV_TC >= a.T) {  // the chunk that holds the last token writes the state
     __bf16* f = fin + ((long long)b * a.D + d) * 3;
     f[0] = f2bf(conv_x(a, b, a.T - 3, d));
     f[1] = f2bf(conv_x(a, b, a.T - 2, d));
@@ -66,75 +71,95 @@ __global__ __launch_bounds__(NTHREADS) void k_conv_fwd(ConvArgs a, __bf16* y, __
 
 // Backward.  da_t = dy_t silu'(a_t);  dx_s = sum_k w_k da_{s+3-k} (+ dfinal);
 // dw_k = sum_t da_t xs[t-3+k];  dinit_j = sum_{k<=j} w_k da_{j-k} (+ dfinal).
-// Thread (d, b, chunk) walks t = t0 .. t1+2 keeping x and da windows of 4.
-__global__ __launch_bounds__(NTHREADS) void k_conv_bwd(ConvArgs a, const __bf16* dy,
-                                                       const __bf16* dfin, __bf16* dx,
-                                                       float* dinit, float* dw_part) {
+// Thread (d, b, chunk) recomputes a_t for t in [t0, t0 + CONV_TC + 3) from
+// register-resident inputs (zero beyond T), so every dx of its chunk is local.
+__global__ __launch_bounds__(NTHREADS) void k_conv_bwd(ConvArgs a, const __bf16* __restrict__ dy,
+                                                       const __bf16* __restrict__ dfin,
+                                                       __bf16* __restrict__ dx,
+                                                       float* __restrict__ dinit,
+                                                       float* __restrict__ dw_part) {
   const int d = blockIdx.x * NTHREADS + threadIdx.x, b = blockIdx.z;
   if (d >= a.D) return;
-  const int T = a.T, t0 = blockIdx.y * CONV_TC, t1 = min(T, t0 + CONV_TC);
+  const int T = a.T, t0 = blockIdx.y * CONV_TC;
   const float w0 = a.w[d * 4], w1 = a.w[d * 4 + 1], w2 = a.w[d * 4 + 2], w3 = a.w[d * 4 + 3];
-  // dfinal_m is the cotangent of xs[T-3+m]
-  float df[3] = {0.f, 0.f, 0.f};
+  constexpr int NX = CONV_TC + 6, NA = CONV_TC + 3;
+  float xv[NX];   // xs[t0-3 .. t0+CONV_TC+2]
+  float gv[NA];   // dy[t0 .. t0+CONV_TC+2]
+#pragma unroll
+  for (int j = 0; j < NX; ++j) xv[j] = conv_x(a, b, t0 - 3 + j, d);
+#pragma unroll
+  for (int j = 0; j < NA; ++j) {
+    const int t = t0 + j;
+    gv[j] = t < T ? bf2f(dy[((long long)b * T + t) * a.D + d]) : 0.f;
+  }
+  float df[3] = {0.f, 0.f, 0.f};  // dfinal_m is the cotangent of xs[T-3+m]
   if (dfin)
+#pragma unroll
     for (int m = 0; m < 3; ++m) df[m] = bf2f(dfin[((long long)b * a.D + d) * 3 + m]);
-  float xm3 = conv_x(a, b, t0 - 3, d), xm2 = conv_x(a, b, t0 - 2, d), xm1 = conv_x(a, b, t0 - 1, d);
-  float da3 = 0.f, da2 = 0.f, da1 = 0.f;  // da_{t-3}, da_{t-2}, da_{t-1}
+  float da[NA];
   float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f;
-  const int tend = min(T, t1 + 3);
-  for (int t = t0; t < t1 + 3; ++t) {
-    float da = 0.f, x = 0.f;
-    if (t < tend) {
-      x = conv_x(a, b, t, d);
-      const float acc = w0 * xm3 + w1 * xm2 + w2 * xm1 + w3 * x;
-      const float sg = sigm(acc);
-      da = bf2f(dy[((long long)b * T + t) * a.D + d]) * sg * (1.f + acc * (1.f - sg));
-      if (t < t1) {
-        g0 += da * xm3; g1 += da * xm2; g2 += da * xm1; g3 += da * x;
-      }
+#pragma unroll
+  for (int j = 0; j < NA; ++j) {
+    const float acc = w0 * xv[j] + w1 * xv[j + 1] + w2 * xv[j + 2] + w3 * xv[j + 3];
+    const float sg = sigm(acc);
+    da[j] = gv[j] * sg * (1.f + acc * (1.f - sg));   // gv = 0 beyond T
+    if (j < CONV_TC) {
+      g0 += da[j] * xv[j]; g1 += da[j] * xv[j + 1]; g2 += da[j] * xv[j + 2];
+      g3 += da[j] * xv[j + 3];
     }
-    const int s = t - 3;  // dx_s needs da_{s..s+3} = (da3, da2, da1, da)
-    if (s >= t0) {
-      float v = w3 * da3 + w2 * da2 + w1 * da1 + w0 * da;
+  }
+#pragma unroll
+  for (int j = 0; j < CONV_TC; ++j) {
+    const int s = t0 + j;
+    if (s < T) {
+      float v = w3 * da[j] + w2 * da[j + 1] + w1 * da[j + 2] + w0 * da[j + 3];
       if (s >= T - 3) v += df[s - (T - 3)];
       dx[((long long)b * T + s) * a.D + d] = f2bf(v);
     }
-    da3 = da2; da2 = da1; da1 = da;
-    xm3 = xm2; xm2 = xm1; xm1 = x;
-    if (t == t0 + 2 && t0 == 0 && dinit) {
-      // da_0 .. da_2 are now in (da3, da2, da1) (zeros beyond T)
-      const float e0 = da3, e1 = da2, e2 = da1;
-      float* di = dinit + ((long long)b * a.D + d) * 3;
-      // xs[-3+j] feeds a_t for t = j - k >= 0 with weight w_k (k <= j)
-      float v0 = w0 * e0;
-      float v1 = w1 * e0 + w0 * e1;
-      float v2 = w2 * e0 + w1 * e1 + w0 * e2;
-      // final-state cotangents that land on the initial state (T < 3)
-      for (int m = 0; m < 3; ++m) {
-        const int j = T + m;  // xs index T-3+m  ->  init slot j when j < 3
-        if (j < 3) (j == 0 ? v0 : j == 1 ? v1 : v2) += df[m];
-      }
-      di[0] = v0; di[1] = v1; di[2] = v2;
+  }
+  if (t0 == 0 && dinit) {
+    // xs[-3+j] feeds a_t for t = j - k >= 0 with weight w_k (k <= j)
+    float v0 = w0 * da[0];
+    float v1 = w1 * da[0] + w0 * da[1];
+    float v2 = w2 * da[0] + w1 * da[1] + w0 * da[2];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {  // final-state cotangents that land on the initial state (T < 3)
+      const int j = T + m;
+      if (j < 3) (j == 0 ? v0 : j == 1 ? v1 : v2) += df[m];
     }
+    float* di = dinit + ((long long)b * a.D + d) * 3;
+    di[0] = v0; di[1] = v1; di[2] = v2;
   }
   float* p = dw_part + (((long long)b * gridDim.y + blockIdx.y) * a.D + d) * 4;
   p[0] = g0; p[1] = g1; p[2] = g2; p[3] = g3;
 }
 
-// dw[d][k] = sum over partial slots
-__global__ __launch_bounds__(NTHREADS) void k_sum_parts(const float* part, int nparts, int width,
-                                                        float* out) {
-  const int i = blockIdx.x * NTHREADS + threadIdx.x;
-  if (i >= width) return;
+// out[i] = sum_p part[p][i]: 32 columns x 8 partial rows per workgroup, the
+// eight row sums combined through LDS.
+__global__ __launch_bounds__(NTHREADS) void k_sum_parts(const float* __restrict__ part, int nparts,
+                                                        int width, float* __restrict__ out) {
+  __shared__ float red[8][33];
+  const int cx = threadIdx.x & 31, ry = threadIdx.x >> 5;
+  const int i = blockIdx.x * 32 + cx;
   float s = 0.f;
-  for (int p = 0; p < nparts; ++p) s += part[(long long)p * width + i];
-  out[i] = s;
+  if (i < width) {
+#pragma unroll 4
+    for (int p = ry; p < nparts; p += 8) s += part[(long long)p * width + i];
+  }
+  red[ry][cx] = s;
+  __syncthreads();
+  if (ry == 0 && i < width) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) t += red[k][cx];
+    out[i] = t;
+  }
 }
 
 // ---------------------------------------------------------------------------
 // KDA decay gate.  raw [N][H*r] bf16 (row stride), bias [H*r], log_rate [H].
 // ---------------------------------------------------------------------------
-constexpr int GATE_TR = 64;  // rows per backward workgroup
+constexpr int GATE_TR = 16;  // rows per backward workgroup
 
 __global__ __launch_bounds__(NTHREADS) void k_gate_fwd(int N, int H, int r, const __bf16* raw,
                                                        long long rs, const float* log_rate,
@@ -160,6 +185,7 @@ __global__ __launch_bounds__(NTHREADS) void k_gate_bwd(int N, int H, int r, cons
   const int n0 = blockIdx.y * GATE_TR, n1 = min(N, n0 + GATE_TR);
   const float rate = __expf(log_rate[c / r]), bc = bias[c];
   float db = 0.f, dl = 0.f;
+#pragma unroll 4
   for (int n = n0; n < n1; ++n) {
     const float x = bf2f(raw[(long long)n * rs + c]) + bc;
     const float g = dout[(long long)n * HR + c];
@@ -331,7 +357,7 @@ int sd_conv4_silu_bwd(int B, int T, int D, const void* x, int64_t x_sb, int64_t 
   hipStream_t st = (hipStream_t)stream;
   SD_LAUNCH("k_conv_bwd", k_conv_bwd, dim3(cdiv(D, NTHREADS), nch, B), dim3(NTHREADS), 0, st, a,
             (const __bf16*)dy, (const __bf16*)dfinal, (__bf16*)dx, dinit, (float*)workspace);
-  SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(4LL * D, NTHREADS)), dim3(NTHREADS), 0, st,
+  SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(4LL * D, 32)), dim3(NTHREADS), 0, st,
             (const float*)workspace, B * nch, 4 * D, dw);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
@@ -396,7 +422,7 @@ int sd_rmsnorm_gated_bwd(int N, int D, float eps, const void* x, const void* gat
   SD_LAUNCH("k_rms_bwd", k_rms_bwd, dim3(np), dim3(RMS_ROWS * 64), 0, st, N, D, eps,
             (const __bf16*)x, (const __bf16*)gate, weight, (const __bf16*)dy, (__bf16*)dx,
             (__bf16*)dgate, (__bf16*)y, (float*)workspace);
-  SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(D, NTHREADS)), dim3(NTHREADS), 0, st,
+  SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(D, 32)), dim3(NTHREADS), 0, st,
             (const float*)workspace, np, D, dweight);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }

@@ -342,6 +342,37 @@ class RMSNormGated(nn.Module):
 
 
 # --------------------------------------------------------------------------
+# projection split
+# --------------------------------------------------------------------------
+class _SplitColumns(torch.autograd.Function):
+    """Column pieces of the packed projection as views; the backward writes the
+    pieces' gradients into one buffer and zeroes only the unused columns (a
+    strided fill), instead of slice/split backward's zeros + concatenation."""
+
+    @staticmethod
+    def forward(ctx, x, sizes):
+        ctx.sizes, ctx.shape, ctx.dtype = sizes, x.shape, x.dtype
+        ctx.set_materialize_grads(False)
+        return tuple(x[..., : sum(sizes)].split(sizes, dim=-1))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        dev = next(t for t in grads if t is not None).device
+        g = torch.empty(ctx.shape, dtype=ctx.dtype, device=dev)
+        off = 0
+        for n, gi in zip(ctx.sizes, grads):
+            dst = g[..., off:off + n]
+            if gi is None:
+                dst.fill_(0.0)
+            else:
+                dst.copy_(gi)
+            off += n
+        if off < ctx.shape[-1]:
+            g[..., off:].fill_(0.0)
+        return g, None
+
+
+# --------------------------------------------------------------------------
 # the mixer
 # --------------------------------------------------------------------------
 class SolveDelta(nn.Module):
@@ -416,12 +447,10 @@ class SolveDelta(nn.Module):
             plan = build_packed_segments(valid_mask, reset_mask)
         conv_state = initial_state.conv if initial_state is not None else None
         sizes = self.projection_sizes
-        used = proj[..., : self.projection_width]
         final_conv = None
         if self.config.use_short_conv:
             qkv_w = sum(sizes[:3])
-            qkv_proj = used[..., :qkv_w]
-            rest = used[..., qkv_w:].split(sizes[3:], dim=-1)
+            qkv_proj, *rest = _SplitColumns.apply(proj, (qkv_w,) + tuple(sizes[3:]))
             if conv_state is not None and (conv_state.shape != (B, qkv_w, 3)):
                 raise ValueError("conv initial state must have shape [B,D,3]")
             if plan is None:
@@ -432,7 +461,7 @@ class SolveDelta(nn.Module):
                                                   return_final_state)
             q_raw, k_raw, v_raw = qkv.split(sizes[:3], dim=-1)
         else:
-            parts = used.split(sizes, dim=-1)
+            parts = _SplitColumns.apply(proj, tuple(sizes))
             q_raw, k_raw, v_raw = (F.silu(t) for t in parts[:3])
             rest = parts[3:]
         u_raw, h_raw, erase_raw, write_raw, geometry_raw, decay_hidden, gate_hidden = rest

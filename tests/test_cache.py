@@ -47,3 +47,27 @@ def test_segment_reset_mask():
         segment_reset_mask(h, torch.tensor([0.0, 10.0]))
     with pytest.raises(ValueError):
         segment_reset_mask(h, torch.tensor([0]))
+
+
+def test_graphed_step_validates_like_the_reference():
+    from solvedelta_amd.graph import SolveDeltaGraphedTrainingStep
+    from solvedelta_amd.lm import SolveDeltaForCausalLM, SolveDeltaLMConfig
+    cfg = SolveDeltaLMConfig(hidden_size=32, num_heads=2, head_k_dim=16, head_v_dim=16,
+                             num_hidden_layers=1, hidden_ratio=2, vocab_size=11)
+    model = SolveDeltaForCausalLM(cfg)
+    ids = torch.zeros(1, 4, dtype=torch.long)
+    with pytest.raises(TypeError):
+        SolveDeltaGraphedTrainingStep(torch.nn.Linear(2, 2), ids, ids)
+    with pytest.raises(ValueError):
+        SolveDeltaGraphedTrainingStep(model.eval(), ids, ids)
+    with pytest.raises(ValueError):                     # host tensors
+        SolveDeltaGraphedTrainingStep(model.train(), ids, ids)
+    with pytest.raises(TypeError):
+        SolveDeltaGraphedTrainingStep(model.train(), ids, ids, num_warmup_iters=True)
+    # reference parameter names line up (modeling_solvedelta.py module tree)
+    names = {n for n, _ in model.named_parameters()}
+    for n in ("model.embeddings.weight", "model.layers.0.mixer_norm.weight",
+              "model.layers.0.mixer.mixer.in_proj.weight", "model.layers.0.mlp.gate_up_proj.weight",
+              "model.layers.0.mlp.down_proj.weight", "model.norm.weight", "lm_head.weight",
+              "model.layers.0.mixer.mixer.associative_decay_bias"):
+        assert n in names, n
