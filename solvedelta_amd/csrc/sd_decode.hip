@@ -3,10 +3,12 @@
 // fused recurrent DPLR step it delegates to).
 //
 // One 256-thread workgroup per (batch, head).  Every thread owns a 16-row x
-// 4-column patch of C and of S (columns 4*(tid & 31), rows 16*(tid >> 5)), and
-// issues all 32 of its 16-byte state loads before any arithmetic, so the whole
-// 128 KiB of state per (b,h) is in flight at once and the HBM latency is paid
-// once.  Row reductions of C (C u) go through an LDS copy of C; column
+// 4-column patch of C and of S (columns 4*(tid & 31), rows 16*(tid >> 5)).  It
+// issues the token's vector loads, then all 32 of its 16-byte state loads (C
+// first) before any arithmetic, so the whole 128 KiB of state per (b,h) is in
+// flight at once and the norms and the C phase overlap the S loads.  The
+// r = V = 128 instantiation has no per-element guards: guarded loads compile
+// to branches that each wait for the previous load.  Row reductions of C (C u) go through an LDS copy of C; column
 // reductions (C'^T k, S'^T e, S^T chi) reduce the patches across the eight row
 // groups (lane xor 32, then the four waves through LDS).  The new states are
 // written back from registers with 16-byte stores.
@@ -62,25 +64,29 @@ __device__ __forceinline__ float4 col_sums(float4 v, float4 (&part)[4][32]) {
   return r;
 }
 
+// FULL: r = V = 128, 16-byte aligned states: unguarded 16-byte accesses (no
+// per-element branches, so all loads stay in flight together).
+template <bool FULL>
 __device__ __forceinline__ float4 ld4(const float* base, int row, int col, int ld, int nrow,
-                                      int ncol, bool vec) {
+                                      int ncol) {
+  if constexpr (FULL) return *reinterpret_cast<const float4*>(base + (long long)row * ld + col);
   if (!base || row >= nrow) return make_float4(0.f, 0.f, 0.f, 0.f);
   const float* p = base + (long long)row * ld + col;
-  if (vec && col + 3 < ncol) return *reinterpret_cast<const float4*>(p);
   float t[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) t[m] = col + m < ncol ? p[m] : 0.f;
   return make_float4(t[0], t[1], t[2], t[3]);
 }
 
+template <bool FULL>
 __device__ __forceinline__ void st4(float* base, int row, int col, int ld, int nrow, int ncol,
-                                    bool vec, float4 v) {
-  if (row >= nrow) return;
-  float* p = base + (long long)row * ld + col;
-  if (vec && col + 3 < ncol) {
-    *reinterpret_cast<float4*>(p) = v;
+                                    float4 v) {
+  if constexpr (FULL) {
+    *reinterpret_cast<float4*>(base + (long long)row * ld + col) = v;
     return;
   }
+  if (row >= nrow) return;
+  float* p = base + (long long)row * ld + col;
   const float t[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
   for (int m = 0; m < 4; ++m)
@@ -91,38 +97,52 @@ __device__ __forceinline__ float f4get(const float4& v, int m) {
   return m == 0 ? v.x : m == 1 ? v.y : m == 2 ? v.z : v.w;
 }
 
+template <bool FULL>
 __global__ __launch_bounds__(NTHREADS) void k_decode(sd_inputs in, __bf16* out, float* C_T,
-                                                     float* S_T, int vec) {
+                                                     float* S_T) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   DecodeSmem& s = *reinterpret_cast<DecodeSmem*>(smem_raw);
   const int n = blockIdx.x, b = n / in.H, hd = n % in.H;
   const int r = in.r, V = in.V, tid = threadIdx.x;
   const int cg = tid & 31, c0 = cg * 4, rg = tid >> 5, i0 = rg * 16;
-  // ---- issue every state load first
+  auto ld = [&](const sd_view& v, int c, int w) -> float {
+    if (!FULL && c >= w) return 0.f;
+    return bf2f(((const __bf16*)v.data)[(long long)b * v.sb + (long long)hd * v.sh + c]);
+  };
+  // ---- the token's vectors, then every state load (C before S), all issued
+  // before any of them is consumed; the norms and the C phase proceed while
+  // the S loads are still in flight
+  // every thread loads channel tid & 127 (branch-free, so the loads stay in
+  // flight); threads >= 128 drop their copies after the barrier below
+  float uu, kk, qq, er, hv, gl = 0.f, vv, wr;
+  {
+    const int c = tid & (KD - 1);
+    uu = ld(in.u, c, r); kk = ld(in.k, c, r); qq = ld(in.q, c, r);
+    er = ld(in.erase_raw, c, r);
+    hv = ld(in.h, c, r);
+    if (FULL || c < r)
+      gl = ((const float*)in.log_decay.data)[(long long)b * in.log_decay.sb +
+                                             (long long)hd * in.log_decay.sh + c];
+    vv = ld(in.v, c, V);
+    wr = ld(in.write_raw, c, V);
+  }
+  const float gam = ((const float*)in.gamma.data)[(long long)b * in.gamma.sb +
+                                                  (long long)hd * in.gamma.sh];
   const float* C0 = in.C0 ? in.C0 + (long long)n * r * r : nullptr;
   const float* S0 = in.S0 ? in.S0 + (long long)n * r * V : nullptr;
   float4 cv[16], sv[16];
 #pragma unroll
-  for (int a = 0; a < 16; ++a) cv[a] = ld4(C0, i0 + a, c0, r, r, r, vec);
+  for (int a = 0; a < 16; ++a) cv[a] = ld4<FULL>(C0, i0 + a, c0, r, r, r);
 #pragma unroll
-  for (int a = 0; a < 16; ++a) sv[a] = ld4(S0, i0 + a, c0, V, r, V, vec);
-  auto ld = [&](const sd_view& v, int c, int w) -> float {
-    if (c >= w) return 0.f;
-    return bf2f(((const __bf16*)v.data)[(long long)b * v.sb + (long long)hd * v.sh + c]);
-  };
-  float uu = 0.f, kk = 0.f, qq = 0.f, er = 0.f;
+  for (int a = 0; a < 16; ++a) sv[a] = ld4<FULL>(S0, i0 + a, c0, V, r, V);
+  __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use
+  if (tid >= KD) uu = kk = qq = er = 0.f;
   if (tid < KD) {
     const int c = tid;
-    uu = ld(in.u, c, r); kk = ld(in.k, c, r); qq = ld(in.q, c, r);
-    er = ld(in.erase_raw, c, r);
-    s.hh[c] = ld(in.h, c, r);
-    s.eg[c] = c < r ? __expf(((const float*)in.log_decay.data)[(long long)b * in.log_decay.sb +
-                                                               (long long)hd * in.log_decay.sh + c])
-                    : 0.f;
-    s.z[c] = ld(in.v, c, V) / (1.f + __expf(-ld(in.write_raw, c, V)));
+    s.hh[c] = hv;
+    s.eg[c] = (FULL || c < r) ? __expf(gl) : 0.f;
+    s.z[c] = vv / (1.f + __expf(-wr));
   }
-  const float gam = ((const float*)in.gamma.data)[(long long)b * in.gamma.sb +
-                                                  (long long)hd * in.gamma.sh];
   {
     float sq3[3] = {uu * uu, kk * kk, qq * qq};
     block_sums(sq3, s.red);
@@ -173,7 +193,7 @@ __global__ __launch_bounds__(NTHREADS) void k_decode(sd_inputs in, __bf16* out, 
     if (C_T) {
       float* Cn = C_T + (long long)n * r * r;
 #pragma unroll
-      for (int a = 0; a < 16; ++a) st4(Cn, i0 + a, c0, r, r, r, vec, cv[a]);
+      for (int a = 0; a < 16; ++a) st4<FULL>(Cn, i0 + a, c0, r, r, r, cv[a]);
     }
     dp = col_sums(dp, s.part);
     if (rg == 0) {
@@ -222,24 +242,29 @@ __global__ __launch_bounds__(NTHREADS) void k_decode(sd_inputs in, __bf16* out, 
     if (S_T) {
       float* Sn = S_T + (long long)n * r * V;
 #pragma unroll
-      for (int a = 0; a < 16; ++a) st4(Sn, i0 + a, c0, V, r, V, vec, sv[a]);
+      for (int a = 0; a < 16; ++a) st4<FULL>(Sn, i0 + a, c0, V, r, V, sv[a]);
     }
     o = col_sums(o, s.part);
     if (rg == 0) {
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        if (c0 + m < V) out[(long long)n * V + c0 + m] = f2bf(f4get(o, m));
+        if (FULL || c0 + m < V) out[(long long)n * V + c0 + m] = f2bf(f4get(o, m));
     }
   }
 }
 
 int launch_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, hipStream_t st) {
-  SD_SMEM_ONCE(k_decode, (int)sizeof(DecodeSmem));
+  SD_SMEM_ONCE(k_decode<true>, (int)sizeof(DecodeSmem));
+  SD_SMEM_ONCE(k_decode<false>, (int)sizeof(DecodeSmem));
   auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
-  const int vec = (in->r % 4 == 0) && (in->V % 4 == 0) && al(in->C0) && al(in->S0) && al(C_T) &&
-                  al(S_T);
-  SD_LAUNCH("k_decode", k_decode, dim3(in->B * in->H), dim3(NTHREADS), sizeof(DecodeSmem), st, *in,
-            (__bf16*)out, C_T, S_T, vec);
+  const bool full = in->r == KD && in->V == VD && in->C0 && in->S0 && C_T && S_T && al(in->C0) &&
+                    al(in->S0) && al(C_T) && al(S_T);
+  if (full)
+    SD_LAUNCH("k_decode", k_decode<true>, dim3(in->B * in->H), dim3(NTHREADS), sizeof(DecodeSmem),
+              st, *in, (__bf16*)out, C_T, S_T);
+  else
+    SD_LAUNCH("k_decode", k_decode<false>, dim3(in->B * in->H), dim3(NTHREADS), sizeof(DecodeSmem),
+              st, *in, (__bf16*)out, C_T, S_T);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 
