@@ -37,7 +37,7 @@ __device__ __forceinline__ float dout_at(const BwdParams& p, int b, int t, int h
   const bool ok = t < p.T && c < p.V;
   const float x = bf2f(p.dout[(((long long)b * p.T + (t < p.T ? t : p.T - 1)) * p.H + h) * p.V +
                               (c < p.V ? c : p.V - 1)]);
-  return ok ? x : 0.f;
+  return keep_if(ok, x);
 }
 
 // Branch-free row load (see load_row2 in the forward kernels).
@@ -47,8 +47,8 @@ __device__ __forceinline__ void ldrow2(const sd_view& v, int b, int t, int h, in
   const bool tv = t < T;
   const __bf16* q = brow(v, b, tv ? t : T - 1, h);
   const float a0 = bf2f(q[l < w ? l : w - 1]), a1 = bf2f(q[l + 64 < w ? l + 64 : w - 1]);
-  x0 = (tv && l < w) ? a0 : 0.f;
-  x1 = (tv && l + 64 < w) ? a1 : 0.f;
+  x0 = keep_if(tv && l < w, a0);
+  x1 = keep_if(tv && l + 64 < w, a1);
 }
 
 __device__ __forceinline__ float norm2(float& x0, float& x1) {
@@ -385,6 +385,13 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
   const int w = wave_id(), l = lane_id();
+  if (threadIdx.x < BT) {  // clamped token, then select (a guarded load would branch and wait)
+    const int t = t0 + threadIdx.x;
+    const float gv = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                                    (long long)(t < p.T ? t : p.T - 1) * p.in.gamma.st +
+                                                    (long long)hh * p.in.gamma.sh];
+    s.gam[threadIdx.x] = keep_if(t < p.T, gv);
+  }
 #pragma unroll
   for (int i = w; i < BT; i += CW) {
     const int t = t0 + i;
@@ -397,11 +404,6 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     norm2(x0, x1);
     s.Kh[i][l] = x0;
     s.Kh[i][l + 64] = x1;
-    if (l == 0)
-      s.gam[i] = t < p.T ? ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
-                                                          (long long)t * p.in.gamma.st +
-                                                          (long long)hh * p.in.gamma.sh]
-                         : 0.f;
   }
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     s.A[(idx / BT) * LS + idx % BT] = p.f.Ac[cidx * BT * BT + idx];
@@ -475,10 +477,12 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   const float* lam = p.g.Lc + sidx * KD * KD;
   if (threadIdx.x < BT) {
     const int t = t0 + threadIdx.x;
-    s.gam[threadIdx.x] = t < p.T ? ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
-                                                                   (long long)t * p.in.gamma.st +
-                                                                   (long long)hh * p.in.gamma.sh]
-                                 : 0.f;
+    {  // clamped token, then select (a guarded load would branch and wait)
+      const float gv = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                                      (long long)(t < p.T ? t : p.T - 1) * p.in.gamma.st +
+                                                      (long long)hh * p.in.gamma.sh];
+      s.gam[threadIdx.x] = keep_if(t < p.T, gv);
+    }
   }
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);

@@ -48,6 +48,13 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// v where ok, else 0, for a value loaded from a clamped (always valid) address.
+// A multiply rather than a select: with a wave-uniform condition the compiler
+// turns `ok ? v : 0` back into a branch around the load that then waits for it,
+// which serialises every load of an unrolled gather.  (v is finite data, so
+// v * 0 == 0.)
+__device__ __forceinline__ float keep_if(bool ok, float v) { return v * (ok ? 1.f : 0.f); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
 __device__ __forceinline__ float bf2f(__bf16 x) { return (float)x; }
@@ -132,6 +139,40 @@ __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
   return acc;
 }
 
+// mma_k32 with the operand gathers split into a raw-load pass and a transform
+// pass: la(m, k) / lb(k, n) fetch the raw values (for global operands, every
+// load is issued before the first use), xa(m, k, x) / xb(k, n, x) turn them into
+// the operand values.  A lambda that loads and computes per element makes each
+// load wait for the previous one's use.
+template <class LA, class XA, class LB, class XB>
+__device__ __forceinline__ f4 mma_k32_lx(LA la, XA xa, LB lb, XB xb, int K, f4 acc) {
+  const int l = lane_id();
+  const int m = l & 15, kq = (l >> 4) * 8;
+  float av[4][8], bv[4][8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks * 32 < K) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        av[ks][e] = la(m, ks * 32 + kq + e);
+        bv[ks][e] = lb(ks * 32 + kq + e, m);
+      }
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks * 32 < K) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        av[ks][e] = xa(m, ks * 32 + kq + e, av[ks][e]);
+        bv[ks][e] = xb(ks * 32 + kq + e, m, bv[ks][e]);
+      }
+    }
+  }
+  return mma_k32([&](int mm, int k) { return av[k >> 5][k & 7]; },
+                 [&](int k, int nn) { return bv[k >> 5][k & 7]; }, K, acc);
+}
+
 // D(16x16) += A(16x16) * B(16x16) with the K=16 bf16 MFMA, same 3-term split.
 template <class FA, class FB>
 __device__ __forceinline__ f4 mma_k16(FA fa, FB fb, f4 acc) {
@@ -170,7 +211,7 @@ struct ChunkDecay {
 
 // Loads g (fp32, [B,T,H,r] strided, token stride st, row pointer base at
 // token t0) and builds G, R and the wild lists.  Tokens >= T load 0 (neutral).
-__device__ inline void build_decay(ChunkDecay& cd, const float* g, long long st, int t0, int T,
+__device__ __forceinline__ void build_decay(ChunkDecay& cd, const float* g, long long st, int t0, int T,
                                    int r) {
   const int tid = threadIdx.x;
   if (tid < KD) {
@@ -179,7 +220,9 @@ __device__ inline void build_decay(ChunkDecay& cd, const float* g, long long st,
 #pragma unroll
     for (int i = 0; i < BT; ++i) {  // all loads in flight before the scan
       const int t = t0 + i;
-      x[i] = (t < T && c < r) ? g[(long long)t * st + c] : 0.f;
+      // clamped address + select (a guarded load would branch and wait)
+      const float v = g[(long long)(t < T ? t : T - 1) * st + (c < r ? c : r - 1)];
+      x[i] = keep_if(t < T && c < r, v);
     }
     float acc = 0.f;
 #pragma unroll
@@ -229,16 +272,18 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
     while (J > I) { J -= I + 1; ++I; }  // p -> (I, J) with J <= I
     const int I0 = I * BS, J0 = J * BS;
     const float* RJ = cd.R[J];
-    auto fa = [&](int m, int c) {
-      const int i = I0 + m;
-      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
-      return X(i, c) * __expf(gx - RJ[c]);
-    };
-    auto fb = [&](int c, int n) {
-      const int j = J0 + n;
-      return cd.wild[J][c] ? 0.f : Y(j, c) * __expf(RJ[c] - cd.G[j][c]);
-    };
-    f4 acc = mma_k32(fa, fb, KD, zero4());
+    f4 acc = mma_k32_lx(
+        [&](int m, int c) { return X(I0 + m, c); },
+        [&](int m, int c, float x) {
+          const int i = I0 + m;
+          const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+          return x * __expf(gx - RJ[c]);
+        },
+        [&](int c, int n) { return Y(J0 + n, c); },
+        [&](int c, int n, float y) {
+          return cd.wild[J][c] ? 0.f : y * __expf(RJ[c] - cd.G[J0 + n][c]);
+        },
+        KD, zero4());
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = I0 + out_row(e), j = J0 + out_col();

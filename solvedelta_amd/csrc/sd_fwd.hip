@@ -43,8 +43,8 @@ __device__ __forceinline__ void load_row2(const sd_view& v, int b, int t, int h,
   const bool tv = t < T;
   const __bf16* p = vrow(v, b, tv ? t : T - 1, h);
   const float a0 = bf2f(p[l < w ? l : w - 1]), a1 = bf2f(p[l + 64 < w ? l + 64 : w - 1]);
-  x0 = (tv && l < w) ? a0 : 0.f;
-  x1 = (tv && l + 64 < w) ? a1 : 0.f;
+  x0 = keep_if(tv && l < w, a0);
+  x1 = keep_if(tv && l + 64 < w, a1);
 }
 
 constexpr int PS = KD + 8;  // bf16 panel row stride
@@ -72,6 +72,11 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
                    (long long)hh * in.log_decay.sh;
   build_decay(s.cd, g, in.log_decay.st, t0, T, r);
   const int w = wave_id(), l = lane_id();
+  if (threadIdx.x < BT) {  // branch-free: clamped token, then select
+    const int t = t0 + threadIdx.x;
+    const float gv = gamma_at(in.gamma, b, t < T ? t : T - 1, hh);
+    s.gam[threadIdx.x] = keep_if(t < T, gv);
+  }
 #pragma unroll
   for (int i = w; i < BT; i += CW) {
     const int t = t0 + i;
@@ -83,7 +88,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     load_row2(in.h, b, t, hh, T, r, x0, x1);
     s.Hh[i][l] = f2bf(x0);
     s.Hh[i][l + 64] = f2bf(x1);
-    if (l == 0) s.gam[i] = t < T ? gamma_at(in.gamma, b, t, hh) : 0.f;
+
   }
   __syncthreads();
   const ChunkDecay& cd = s.cd;
