@@ -32,13 +32,23 @@ __device__ __forceinline__ const __bf16* brow(const sd_view& v, int b, int t, in
   return (const __bf16*)v.data + (long long)b * v.sb + (long long)t * v.st + (long long)h * v.sh;
 }
 
-__device__ __forceinline__ float dout_at(const BwdParams& p, int b, int t, int h, int c) {
-  if (!p.dout) return 0.f;
-  const bool ok = t < p.T && c < p.V;
-  const float x = bf2f(p.dout[(((long long)b * p.T + (t < p.T ? t : p.T - 1)) * p.H + h) * p.V +
-                              (c < p.V ? c : p.V - 1)]);
-  return keep_if(ok, x);
+
+// dout_at split into a raw load (clamped address) and its use.
+struct DoutRaw {
+  __bf16 x;
+  bool ok;
+};
+// A missing cotangent reads this zero element instead (pointer select, no branch).
+__device__ const __bf16 sd_zero_bf16[1] = {};
+__device__ __forceinline__ DoutRaw dout_raw(const BwdParams& p, int b, int t, int h, int c) {
+  const bool has = p.dout != nullptr;
+  const bool ok = has && t < p.T && c < p.V;
+  const __bf16* base = has ? (const __bf16*)p.dout : sd_zero_bf16;
+  const long long i = (((long long)b * p.T + (t < p.T ? t : p.T - 1)) * p.H + h) * p.V +
+                      (c < p.V ? c : p.V - 1);
+  return {base[has ? i : 0], ok};
 }
+__device__ __forceinline__ float dout_val(DoutRaw r) { return keep_if(r.ok, bf2f(r.x)); }
 
 // Branch-free row load (see load_row2 in the forward kernels).
 __device__ __forceinline__ void ldrow2(const sd_view& v, int b, int t, int h, int T, int w,
@@ -91,9 +101,21 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
-  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
-    s.A[(idx / BT) * LS + idx % BT] = p.f.As[cidx * BT * BT + idx];
-    s.P[(idx / BT) * LS + idx % BT] = sp_load(p.f.Ps, cidx * BT * BT + idx);
+  {
+    constexpr int PA = BT * BT / CT;
+    float av[PA];
+    SPRaw pv[PA];
+#pragma unroll
+    for (int q = 0; q < PA; ++q) {
+      av[q] = p.f.As[cidx * BT * BT + threadIdx.x + q * CT];
+      pv[q] = sp_raw(p.f.Ps, cidx * BT * BT + threadIdx.x + q * CT);
+    }
+#pragma unroll
+    for (int q = 0; q < PA; ++q) {
+      const int idx = threadIdx.x + q * CT;
+      s.A[(idx / BT) * LS + idx % BT] = av[q];
+      s.P[(idx / BT) * LS + idx % BT] = sp_val(pv[q]);
+    }
   }
   __syncthreads();
   mat64_mul(s.P, s.A, s.N);
@@ -103,12 +125,12 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_l N_lj dO_l ;  Wk_j = sum_i A_ij K^_i
-      f4 du = mma_k32([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; },
-                      [&](int k, int nn) { return dout_at(p, b, t0 + k, hh, cb * 16 + nn); }, BT,
-                      zero4());
-      f4 wk = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
-                      [&](int k, int nn) { return sp_load(p.f.Ks, kbase + (cb * 16 + nn) * BT + k); },
-                      BT, zero4());
+      f4 du = mma_k32_lx([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; }, XId(),
+                         [&](int k, int nn) { return dout_raw(p, b, t0 + k, hh, cb * 16 + nn); },
+                         [](int, int, DoutRaw r) { return dout_val(r); }, BT, zero4());
+      f4 wk = mma_k32_lx([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; }, XId(),
+                         [&](int k, int nn) { return sp_raw(p.f.Ks, kbase + (cb * 16 + nn) * BT + k); },
+                         [](int, int, SPRaw r) { return sp_val(r); }, BT, zero4());
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + Jb * BS + out_row(e);
@@ -117,16 +139,42 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
         sp_store(p.g.Wk, row * KD + c, wk[e]);
       }
     }
-  for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
-    const int i = idx / KD, c = idx % KD;
-    p.g.B1[(rowbase + i) * KD + c] = dout_at(p, b, t0 + i, hh, c);
+  // elementwise panels: every load of the thread's 16 elements is issued before
+  // the first store (a store between loads would keep later loads behind it)
+  constexpr int PER = BT * KD / CT;
+  {
+    DoutRaw d[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = threadIdx.x + q * CT, i = idx / KD, c = idx % KD;
+      d[q] = dout_raw(p, b, t0 + i, hh, c);
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = threadIdx.x + q * CT, i = idx / KD, c = idx % KD;
+      p.g.B1[(rowbase + i) * KD + c] = dout_val(d[q]);
+    }
   }
-  for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {  // chunk-transposed panels
-    const int c = idx / BT, i = idx % BT;
-    const long long o = (rowbase + i) * KD + c, ot = cidx * KD * BT + idx;
-    sp_store(p.g.Ant, ot, -p.f.e[o] * __expf(cd.G[i][c]));
-    sp_store(p.g.At1, ot, sp_load(p.f.Qs, o));
-    sp_store(p.g.B1t, ot, dout_at(p, b, t0 + i, hh, c));
+  {  // chunk-transposed panels
+    float ev[PER];
+    SPRaw qv[PER];
+    DoutRaw d[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = threadIdx.x + q * CT, c = idx / BT, i = idx % BT;
+      const long long o = (rowbase + i) * KD + c;
+      ev[q] = p.f.e[o];
+      qv[q] = sp_raw(p.f.Qs, o);
+      d[q] = dout_raw(p, b, t0 + i, hh, c);
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = threadIdx.x + q * CT, c = idx / BT, i = idx % BT;
+      const long long ot = cidx * KD * BT + idx;
+      sp_store(p.g.Ant, ot, -ev[q] * __expf(cd.G[i][c]));
+      sp_store(p.g.At1, ot, sp_val(qv[q]));
+      sp_store(p.g.B1t, ot, dout_val(d[q]));
+    }
   }
 }
 
@@ -424,9 +472,9 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
                       [&](int k, int nn) { return ddl[k * KD + cb * 16 + nn]; }, BT, zero4());
       du = mma_k32([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; },
                    [&](int k, int nn) { return s.Kh[k][cb * 16 + nn]; }, BT, du);
-      f4 wk = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
-                      [&](int k, int nn) { return sp_load(p.f.Kc, kbase + (cb * 16 + nn) * BT + k); },
-                      BT, zero4());
+      f4 wk = mma_k32_lx([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; }, XId(),
+                         [&](int k, int nn) { return sp_raw(p.f.Kc, kbase + (cb * 16 + nn) * BT + k); },
+                         [](int, int, SPRaw r) { return sp_val(r); }, BT, zero4());
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + Jb * BS + out_row(e);

@@ -148,30 +148,39 @@ template <class LA, class XA, class LB, class XB>
 __device__ __forceinline__ f4 mma_k32_lx(LA la, XA xa, LB lb, XB xb, int K, f4 acc) {
   const int l = lane_id();
   const int m = l & 15, kq = (l >> 4) * 8;
+  using RA = decltype(la(0, 0));
+  using RB = decltype(lb(0, 0));
+  RA ar[4][8];
+  RB br[4][8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks * 32 < K) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ar[ks][e] = la(m, ks * 32 + kq + e);
+        br[ks][e] = lb(ks * 32 + kq + e, m);
+      }
+    }
+  }
   float av[4][8], bv[4][8];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     if (ks * 32 < K) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        av[ks][e] = la(m, ks * 32 + kq + e);
-        bv[ks][e] = lb(ks * 32 + kq + e, m);
-      }
-    }
-  }
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    if (ks * 32 < K) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        av[ks][e] = xa(m, ks * 32 + kq + e, av[ks][e]);
-        bv[ks][e] = xb(ks * 32 + kq + e, m, bv[ks][e]);
+        av[ks][e] = xa(m, ks * 32 + kq + e, ar[ks][e]);
+        bv[ks][e] = xb(ks * 32 + kq + e, m, br[ks][e]);
       }
     }
   }
   return mma_k32([&](int mm, int k) { return av[k >> 5][k & 7]; },
                  [&](int k, int nn) { return bv[k >> 5][k & 7]; }, K, acc);
 }
+
+// Identity transform for an operand gathered as plain fp32.
+struct XId {
+  __device__ float operator()(int, int, float x) const { return x; }
+};
 
 // D(16x16) += A(16x16) * B(16x16) with the K=16 bf16 MFMA, same 3-term split.
 template <class FA, class FB>

@@ -25,6 +25,12 @@ __device__ __forceinline__ void sp_store(const SP& sp, long long i, float x) {
 __device__ __forceinline__ float sp_load(const SP& sp, long long i) {
   return (float)sp.hi[i] + (float)sp.lo[i];
 }
+// Raw halves of a split value (load now, combine later with sp_val).
+struct SPRaw {
+  __bf16 h, l;
+};
+__device__ __forceinline__ SPRaw sp_raw(const SP& sp, long long i) { return {sp.hi[i], sp.lo[i]}; }
+__device__ __forceinline__ float sp_val(SPRaw r) { return (float)r.h + (float)r.l; }
 #endif
 
 // Forward workspace: every buffer is [n][Tp][128] (token panels) or
