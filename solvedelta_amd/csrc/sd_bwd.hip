@@ -284,10 +284,15 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   float* dg = p.g.dgS + rowbase * KD;
   Tab1 t1;
   make_tab1(cd, cb, t1);
-  // Pass A: de = -(e^G (dw X0^T) + apply(M1, d)),  dchi = e^G (dO X0^T) + apply(M2, d)
+  // This wave's d, e, chi slabs, loaded once for both passes (no global loads
+  // between the passes' stores, which would wait for them).
+  float Sd[NB][4], Se[NB][4], Sq[NB][4], pdg[NB][4];
+  load_slab(Sd, dd_, cb);
+  load_slab(Se, ee, cb);
+  load_slab(Sq, chi, cb);
+  // Pass A: de = -(e^G (dw X0^T) + apply(M1, d)),  dchi = e^G (dO X0^T) + apply(M2, d);
+  // the decay terms chi.dchi + e.de of dg
   {
-    float Sd[NB][4];
-    load_slab(Sd, dd_, cb);
     __syncthreads();  // M1, M2 complete
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
@@ -298,16 +303,15 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
         const int i = I * BS + r4 + e;
         const float eg = __expf(cd.G[i][c]);
         const long long o = (rowbase + i) * KD + c;
-        p.g.de[o] = -(eg * a[I][e] + ap[e]);
-        p.g.dchi[o] = eg * bq[I][e] + bp[e];
+        const float dev = -(eg * a[I][e] + ap[e]), dcv = eg * bq[I][e] + bp[e];
+        p.g.de[o] = dev;
+        p.g.dchi[o] = dcv;
+        pdg[I][e] = Sq[I][e] * dcv + Se[I][e] * dev;
       }
     }
   }
-  // Pass B: dd = e^{G_C - G} (w lam^T) + apply_t(M2, chi) - apply_t(M1, e); decay terms
+  // Pass B: dd = e^{G_C - G} (w lam^T) + apply_t(M2, chi) - apply_t(M1, e); dg -= d.dd
   {
-    float Se[NB][4], Sq[NB][4];
-    load_slab(Se, ee, cb);
-    load_slab(Sq, chi, cb);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       f4 k2, k3;
@@ -318,7 +322,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
         const long long o = (rowbase + i) * KD + c;
         const float ddv = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[I][e] + k2[e] - k3[e];
         p.g.dd[o] = ddv;
-        dg[i * KD + c] = Sq[I][e] * p.g.dchi[o] - dd_[i * KD + c] * ddv + Se[I][e] * p.g.de[o];
+        dg[i * KD + c] = pdg[I][e] - Sd[I][e] * ddv;
       }
     }
   }
