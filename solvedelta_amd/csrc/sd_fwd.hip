@@ -513,17 +513,29 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   }
   __syncthreads();
   SD_MARK(2, 4);
-  // sources (one wave per token row; e overwrites u, chi overwrites k)
+  // sources (one wave per token row; e overwrites u, chi overwrites k).  The
+  // wave's rows of delta, q and erase are all loaded before the first row is
+  // processed: the rows' global stores would otherwise hold each next row's
+  // loads behind them.
+  constexpr int RPW = BT / CW;  // rows per wave
+  float dq_[RPW][2], qq_[RPW][2], er_[RPW][2];
 #pragma unroll
-  for (int i = w; i < BT; i += CW) {
-    const int t = t0 + i;
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int i = w + rr * CW, t = t0 + i;
+    dq_[rr][0] = delta[(long long)i * KD + l];
+    dq_[rr][1] = delta[(long long)i * KD + l + 64];
+    load_row2(in.q, b, t, hh, T, r, qq_[rr][0], qq_[rr][1]);
+    load_row2(in.erase_raw, b, t, hh, T, r, er_[rr][0], er_[rr][1]);
+  }
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int i = w + rr * CW;
     const float u0 = s.Pa[i][l], u1 = s.Pa[i][l + 64];
     const float k0 = s.Pb[i][l], k1 = s.Pb[i][l + 64];
-    const float d0 = delta[(long long)i * KD + l], d1 = delta[(long long)i * KD + l + 64];
-    float q0, q1, e0, e1;
-    load_row2(in.q, b, t, hh, T, r, q0, q1);
+    const float d0 = dq_[rr][0], d1 = dq_[rr][1];
+    float q0 = qq_[rr][0], q1 = qq_[rr][1];
+    const float e0 = er_[rr][0], e1 = er_[rr][1];
     l2norm2(q0, q1, nullptr);
-    load_row2(in.erase_raw, b, t, hh, T, r, e0, e1);
     const float usq = wave_sum(u0 * u0 + u1 * u1);
     const float dsq = wave_sum(d0 * d0 + d1 * d1);
     const float sc = RHO / sqrtf(RHO * RHO + usq * dsq);
