@@ -108,7 +108,8 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
 #pragma unroll
     for (int q = 0; q < PA; ++q) {
       av[q] = p.f.As[cidx * BT * BT + threadIdx.x + q * CT];
-      pv[q] = sp_raw(p.f.Ps, cidx * BT * BT + threadIdx.x + q * CT);
+      const int idx = threadIdx.x + q * CT;
+      pv[q] = sp_raw(p.f.Ps, cidx * BT * BT + frag_off(idx / BT, idx % BT, BT));
     }
 #pragma unroll
     for (int q = 0; q < PA; ++q) {
@@ -129,14 +130,14 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
                          [&](int k, int nn) { return dout_raw(p, b, t0 + k, hh, cb * 16 + nn); },
                          [](int, int, DoutRaw r) { return dout_val(r); }, BT, zero4());
       f4 wk = mma_k32_lx([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; }, XId(),
-                         [&](int k, int nn) { return sp_raw(p.f.Ks, kbase + (cb * 16 + nn) * BT + k); },
+                         [&](int k, int nn) { return sp_raw(p.f.Ks, kbase + frag_off(cb * 16 + nn, k, BT)); },
                          [](int, int, SPRaw r) { return sp_val(r); }, BT, zero4());
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + Jb * BS + out_row(e);
         const int c = cb * 16 + out_col();
         p.g.dU[row * KD + c] = du[e];
-        sp_store(p.g.Wk, row * KD + c, wk[e]);
+        sp_store(p.g.Wk, rowbase * KD + frag_off(Jb * BS + out_row(e), c, KD), wk[e]);
       }
     }
   // elementwise panels: every load of the thread's 16 elements is issued before
@@ -155,25 +156,48 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       p.g.B1[(rowbase + i) * KD + c] = dout_val(d[q]);
     }
   }
-  {  // chunk-transposed panels
-    float ev[PER];
-    SPRaw qv[PER];
-    DoutRaw d[PER];
+  {  // chunk-transposed panels, fragment order: a thread's two pieces are
+     // (state row c, tokens i0 .. i0+7); all their loads are issued first
+    constexpr int NPC = KD * BT / 8 / CT;
+    float ev[NPC][8];
+    SPRaw qv[NPC][8];
+    DoutRaw d[NPC][8];
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int idx = threadIdx.x + q * CT, c = idx / BT, i = idx % BT;
-      const long long o = (rowbase + i) * KD + c;
-      ev[q] = p.f.e[o];
-      qv[q] = sp_raw(p.f.Qs, o);
-      d[q] = dout_raw(p, b, t0 + i, hh, c);
+    for (int q = 0; q < NPC; ++q) {
+      const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
+      const int c = (block / (BT / 32)) * 16 + (lane & 15);
+      const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = i0 + e;
+        ev[q][e] = p.f.e[(rowbase + i) * KD + c];
+        qv[q][e] = sp_raw(p.f.Qs, rowbase * KD + frag_off(i, c, KD));
+        d[q][e] = dout_raw(p, b, t0 + i, hh, c);
+      }
     }
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int idx = threadIdx.x + q * CT, c = idx / BT, i = idx % BT;
-      const long long ot = cidx * KD * BT + idx;
-      sp_store(p.g.Ant, ot, -ev[q] * __expf(cd.G[i][c]));
-      sp_store(p.g.At1, ot, sp_val(qv[q]));
-      sp_store(p.g.B1t, ot, dout_val(d[q]));
+    for (int q = 0; q < NPC; ++q) {
+      const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
+      const int c = (block / (BT / 32)) * 16 + (lane & 15);
+      const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
+      bf16x8 ah, al, qh, ql, dh, dl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        __bf16 x, y;
+        split_bf(-ev[q][e] * __expf(cd.G[i0 + e][c]), x, y);
+        ah[e] = x; al[e] = y;
+        split_bf(sp_val(qv[q][e]), x, y);
+        qh[e] = x; ql[e] = y;
+        split_bf(dout_val(d[q][e]), x, y);
+        dh[e] = x; dl[e] = y;
+      }
+      const long long ot = cidx * KD * BT + (long long)pc * 8;
+      *reinterpret_cast<bf16x8*>(p.g.Ant.hi + ot) = ah;
+      *reinterpret_cast<bf16x8*>(p.g.Ant.lo + ot) = al;
+      *reinterpret_cast<bf16x8*>(p.g.At1.hi + ot) = qh;
+      *reinterpret_cast<bf16x8*>(p.g.At1.lo + ot) = ql;
+      *reinterpret_cast<bf16x8*>(p.g.B1t.hi + ot) = dh;
+      *reinterpret_cast<bf16x8*>(p.g.B1t.lo + ot) = dl;
     }
   }
 }
@@ -477,14 +501,14 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       du = mma_k32([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; },
                    [&](int k, int nn) { return s.Kh[k][cb * 16 + nn]; }, BT, du);
       f4 wk = mma_k32_lx([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; }, XId(),
-                         [&](int k, int nn) { return sp_raw(p.f.Kc, kbase + (cb * 16 + nn) * BT + k); },
+                         [&](int k, int nn) { return sp_raw(p.f.Kc, kbase + frag_off(cb * 16 + nn, k, BT)); },
                          [](int, int, SPRaw r) { return sp_val(r); }, BT, zero4());
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + Jb * BS + out_row(e);
         const int c = cb * 16 + out_col();
         p.g.dU[row * KD + c] = du[e];
-        sp_store(p.g.Wk, row * KD + c, wk[e]);
+        sp_store(p.g.Wk, rowbase * KD + frag_off(Jb * BS + out_row(e), c, KD), wk[e]);
       }
     }
   for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
@@ -492,13 +516,14 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     p.g.B1[(rowbase + i) * KD + c] = s.Kh[i][c];
     p.g.uh[(rowbase + i) * KD + c] = s.Uh[i][c];
   }
-  for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {  // chunk-transposed panels
-    const int c = idx / BT, i = idx % BT;
-    const long long ot = cidx * KD * BT + idx;
-    sp_store(p.g.At1, ot, ddp[i * KD + c] * __expf(cd.G[i][c]));
-    sp_store(p.g.B1t, ot, s.Kh[i][c]);
-    sp_store(p.g.Ant, ot, -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c)));
-  }
+  // chunk-transposed panels, fragment order
+  store_frag_panel<KD, BT>(p.g.At1.hi, p.g.At1.lo, cidx * KD * BT,
+                           [&](int c, int i) { return ddp[i * KD + c] * __expf(cd.G[i][c]); });
+  store_frag_panel<KD, BT>(p.g.B1t.hi, p.g.B1t.lo, cidx * KD * BT,
+                           [&](int c, int i) { return s.Kh[i][c]; });
+  store_frag_panel<KD, BT>(p.g.Ant.hi, p.g.Ant.lo, cidx * KD * BT, [&](int c, int i) {
+    return -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c));
+  });
 }
 
 struct GradCSmem {

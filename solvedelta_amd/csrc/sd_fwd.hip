@@ -116,17 +116,16 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
-        sp_store(p.Wc, row * KD + c, -aw[e]);
+        sp_store(p.Wc, rowbase * KD + frag_off(I * BS + out_row(e), c, KD), -aw[e]);
         p.Uc[row * KD + c] = au[e];
       }
     }
   }
   // decayed keys (transposed per chunk) and chunk decay
   const long long cbase = ((long long)n * p.NT + ch);
-  for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {
-    const int c = idx / BT, i = idx % BT;
-    sp_store(p.Kc, cbase * KD * BT + idx, s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]));
-  }
+  store_frag_panel<KD, BT>(p.Kc.hi, p.Kc.lo, cbase * KD * BT, [&](int c, int i) {
+    return s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
+  });
   if (threadIdx.x < KD) p.Gam[cbase * KD + threadIdx.x] = __expf(cd.G[BT - 1][threadIdx.x]);
 }
 
@@ -189,14 +188,14 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
   const int tb = w;  // this wave's token block
   const long long cidx = (long long)n * p.NT + ch;
   const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
-  const long long wb = (rowbase + tb * 16 + m) * KD + kq;
+  const long long wb = rowbase * KD;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldfrag(p.Wneg, wb + ks * 32);
+  for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldfrag(p.Wneg, wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
 #pragma unroll
   for (int q = 0; q < SRB; ++q)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      f.K[q][ks] = ldfrag(p.Kt, cidx * KD * BT + (long long)((SRB * w + q) * 16 + m) * BT + ks * 32 + kq);
+      f.K[q][ks] = ldfrag(p.Kt, cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
 #pragma unroll
   for (int h = 0; h < HALVES; ++h)
 #pragma unroll
@@ -206,10 +205,10 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
   for (int q = 0; q < SRB; ++q) f.gam[q] = ld4(p.Gam + cidx * KD + (SRB * w + q) * 16 + (l >> 4) * 4);
   if constexpr (COL_OUT) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) f.Q[ks] = ldfrag(p.Q, wb + ks * 32);
+    for (int ks = 0; ks < 4; ++ks) f.Q[ks] = ldfrag(p.Q, wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      f.P[ks] = ldfrag(p.P, cidx * BT * BT + (long long)(tb * 16 + m) * BT + ks * 32 + kq);
+      f.P[ks] = ldfrag(p.P, cidx * BT * BT + frag_off(tb * 16 + m, ks * 32 + kq, BT));
   }
   if constexpr (INJ) {
 #pragma unroll
@@ -217,13 +216,12 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         f.A1[q][ks] =
-            ldfrag(p.At1, cidx * KD * BT + (long long)((SRB * w + q) * 16 + m) * BT + ks * 32 + kq);
+            ldfrag(p.At1, cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
 #pragma unroll
     for (int h = 0; h < HALVES; ++h)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        f.B1[h][ks] = ldfrag(p.B1, cidx * KD * BT + (long long)(tile * SCOLS + h * 16 + m) * BT +
-                                       ks * 32 + kq);
+        f.B1[h][ks] = ldfrag(p.B1, cidx * KD * BT + frag_off(tile * SCOLS + h * 16 + m, ks * 32 + kq, BT));
   }
 }
 
@@ -375,10 +373,15 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   for (; it + 2 < NT; it += 3) {
     load_state_frags(p, n, clampc(it + 2), tile, f2);
     state_step(p, s, n, chunk_of(it), tile, f0, X);
+    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 0);
     load_state_frags(p, n, clampc(it + 3), tile, f0);
+    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 1);
     state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
+    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 2);
     load_state_frags(p, n, clampc(it + 4), tile, f1);
+    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 3);
     state_step(p, s, n, chunk_of(it + 2), tile, f2, X);
+    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 4);
   }
   if (it < NT) state_step(p, s, n, chunk_of(it), tile, f0, X);
   if (it + 1 < NT) state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
@@ -560,16 +563,13 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   decayed_gram<false>(
       cd, [&](int i, int c) { return s.Pb[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
       false, s.M);
-  for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
-    sp_store(p.Ps, cidx * BT * BT + idx, s.M[(idx / BT) * LS + idx % BT]);
-  for (int idx = threadIdx.x; idx < KD * BT; idx += CT) {
-    const int c = idx / BT, i = idx % BT;
-    sp_store(p.Ks, cidx * KD * BT + idx, s.Pc[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]));
-  }
-  for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
-    const int i = idx / KD, c = idx % KD;
-    sp_store(p.Qs, (rowbase + i) * KD + c, s.Pb[i][c] * __expf(cd.G[i][c]));
-  }
+  store_frag_panel<BT, BT>(p.Ps.hi, p.Ps.lo, cidx * BT * BT,
+                           [&](int i, int j) { return s.M[i * LS + j]; });
+  store_frag_panel<KD, BT>(p.Ks.hi, p.Ks.lo, cidx * KD * BT, [&](int c, int i) {
+    return s.Pc[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
+  });
+  store_frag_panel<BT, KD>(p.Qs.hi, p.Qs.lo, rowbase * KD,
+                           [&](int i, int c) { return s.Pb[i][c] * __expf(cd.G[i][c]); });
   __syncthreads();
   SD_MARK(2, 6);
   // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
@@ -607,7 +607,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
-        sp_store(p.Ws, row * KD + c, -aw[e]);
+        sp_store(p.Ws, rowbase * KD + frag_off(I * BS + out_row(e), c, KD), -aw[e]);
         p.Us[row * KD + c] = au[e];
       }
     }

@@ -25,6 +25,16 @@ __device__ __forceinline__ void sp_store(const SP& sp, long long i, float x) {
 __device__ __forceinline__ float sp_load(const SP& sp, long long i) {
   return (float)sp.hi[i] + (float)sp.lo[i];
 }
+// Fragment order of a per-chunk split panel of R rows x C columns (C = 64 or
+// 128): each 16-row x 32-column MFMA operand block is 512 consecutive
+// elements, lane-major (lane = 16 * ((col % 32) / 8) + row % 16, 8 elements
+// per lane), so the sequential state pass reads a fragment as one contiguous
+// 1 KiB 16-byte-per-lane load instead of 16 half-used cache lines.
+__device__ __forceinline__ long long frag_off(int row, int col, int C) {
+  return ((long long)(row >> 4) * (C >> 5) + (col >> 5)) * 512 +
+         ((((col & 31) >> 3) << 4) + (row & 15)) * 8 + (col & 7);
+}
+
 // Raw halves of a split value (load now, combine later with sp_val).
 struct SPRaw {
   __bf16 h, l;
