@@ -90,9 +90,10 @@ __device__ void mat64_mul(const float* P, const float* A, float* N) {
 struct BprepSSmem {
   ChunkDecay cd;
   float A[BT * LS];
-  float P[BT * LS];
+  float P[BT * LS];  // P and N are contiguous: reused as a 64 x 128 staging panel
   float N[BT * LS];
 };
+static_assert(2 * BT * LS >= BT * KD, "P + N hold a 64 x 128 panel");
 
 __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -123,6 +124,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   __syncthreads();
   const int w = wave_id();
   const long long kbase = cidx * KD * BT;
+  f4 wks[NB];
   for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_l N_lj dO_l ;  Wk_j = sum_i A_ij K^_i
@@ -137,9 +139,21 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
         const long long row = rowbase + Jb * BS + out_row(e);
         const int c = cb * 16 + out_col();
         p.g.dU[row * KD + c] = du[e];
-        sp_store(p.g.Wk, rowbase * KD + frag_off(Jb * BS + out_row(e), c, KD), wk[e]);
       }
+      wks[Jb] = wk;
     }
+  // Wk staged in the free P / N rows, then stored in fragment order
+  __syncthreads();
+  {
+    float* Wst = s.P;  // 64 x 128 fits in P and N
+#pragma unroll
+    for (int Jb = 0; Jb < NB; ++Jb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Wst[(Jb * BS + out_row(e)) * KD + w * 16 + out_col()] = wks[Jb][e];
+    __syncthreads();
+    store_frag_panel<BT, KD>(p.g.Wk.hi, p.g.Wk.lo, rowbase * KD,
+                             [&](int i, int c) { return Wst[i * KD + c]; });
+  }
   // elementwise panels: every load of the thread's 16 elements is issued before
   // the first store (a store between loads would keep later loads behind it)
   constexpr int PER = BT * KD / CT;
@@ -493,6 +507,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   __syncthreads();
   const float* ddl = p.g.ddelta + rowbase * KD;
   const long long kbase = cidx * KD * BT;
+  f4 wks[NB];
   for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_i A_ij ddelta_i + sum_l N_lj k_l ;  Wk_j = sum_i A_ij K^_i
@@ -508,9 +523,20 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
         const long long row = rowbase + Jb * BS + out_row(e);
         const int c = cb * 16 + out_col();
         p.g.dU[row * KD + c] = du[e];
-        sp_store(p.g.Wk, rowbase * KD + frag_off(Jb * BS + out_row(e), c, KD), wk[e]);
       }
+      wks[Jb] = wk;
     }
+  __syncthreads();
+  {
+    float* Wst = s.P;  // 64 x 128 fits in P and N
+#pragma unroll
+    for (int Jb = 0; Jb < NB; ++Jb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Wst[(Jb * BS + out_row(e)) * KD + w * 16 + out_col()] = wks[Jb][e];
+    __syncthreads();
+    store_frag_panel<BT, KD>(p.g.Wk.hi, p.g.Wk.lo, rowbase * KD,
+                             [&](int i, int c) { return Wst[i * KD + c]; });
+  }
   for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
     const int i = idx / KD, c = idx % KD;
     p.g.B1[(rowbase + i) * KD + c] = s.Kh[i][c];

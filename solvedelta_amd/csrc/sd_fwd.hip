@@ -607,11 +607,13 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
-        sp_store(p.Ws, rowbase * KD + frag_off(I * BS + out_row(e), c, KD), -aw[e]);
+        s.Pc[I * BS + out_row(e)][c] = -aw[e];  // staged for the fragment-order store
         p.Us[row * KD + c] = au[e];
       }
     }
   }
+  __syncthreads();
+  store_frag_panel<BT, KD>(p.Ws.hi, p.Ws.lo, rowbase * KD, [&](int i, int c) { return s.Pc[i][c]; });
   SD_MARK(2, 9);
 }
 
