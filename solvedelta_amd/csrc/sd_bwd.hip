@@ -482,18 +482,25 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
                                                     (long long)hh * p.in.gamma.sh];
     s.gam[threadIdx.x] = keep_if(t < p.T, gv);
   }
+{
+    constexpr int RPW = BT / CW;  // every row's loads before the first reduction
+    float ux[RPW][2], kx[RPW][2];
 #pragma unroll
-  for (int i = w; i < BT; i += CW) {
-    const int t = t0 + i;
-    float x0, x1;
-    ldrow2(p.in.u, b, t, hh, p.T, p.r, x0, x1);
-    norm2(x0, x1);
-    s.Uh[i][l] = x0;
-    s.Uh[i][l + 64] = x1;
-    ldrow2(p.in.k, b, t, hh, p.T, p.r, x0, x1);
-    norm2(x0, x1);
-    s.Kh[i][l] = x0;
-    s.Kh[i][l + 64] = x1;
+    for (int rr = 0; rr < RPW; ++rr) {
+      const int t = t0 + w + rr * CW;
+      ldrow2(p.in.u, b, t, hh, p.T, p.r, ux[rr][0], ux[rr][1]);
+      ldrow2(p.in.k, b, t, hh, p.T, p.r, kx[rr][0], kx[rr][1]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      const int i = w + rr * CW;
+      norm2(ux[rr][0], ux[rr][1]);
+      norm2(kx[rr][0], kx[rr][1]);
+      s.Uh[i][l] = ux[rr][0];
+      s.Uh[i][l + 64] = ux[rr][1];
+      s.Kh[i][l] = kx[rr][0];
+      s.Kh[i][l + 64] = kx[rr][1];
+    }
   }
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     s.A[(idx / BT) * LS + idx % BT] = p.f.Ac[cidx * BT * BT + idx];

@@ -77,18 +77,26 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     const float gv = gamma_at(in.gamma, b, t < T ? t : T - 1, hh);
     s.gam[threadIdx.x] = keep_if(t < T, gv);
   }
+{
+    // every row's loads first: a row's reduction would otherwise hold the next
+    // row's loads behind it
+    constexpr int RPW = BT / CW;
+    float ux[RPW][2], hx[RPW][2];
 #pragma unroll
-  for (int i = w; i < BT; i += CW) {
-    const int t = t0 + i;
-    float x0, x1;
-    load_row2(in.u, b, t, hh, T, r, x0, x1);
-    l2norm2(x0, x1, nullptr);
-    s.Uh[i][l] = x0;
-    s.Uh[i][l + 64] = x1;
-    load_row2(in.h, b, t, hh, T, r, x0, x1);
-    s.Hh[i][l] = f2bf(x0);
-    s.Hh[i][l + 64] = f2bf(x1);
-
+    for (int rr = 0; rr < RPW; ++rr) {
+      const int t = t0 + w + rr * CW;
+      load_row2(in.u, b, t, hh, T, r, ux[rr][0], ux[rr][1]);
+      load_row2(in.h, b, t, hh, T, r, hx[rr][0], hx[rr][1]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      const int i = w + rr * CW;
+      l2norm2(ux[rr][0], ux[rr][1], nullptr);
+      s.Uh[i][l] = ux[rr][0];
+      s.Uh[i][l + 64] = ux[rr][1];
+      s.Hh[i][l] = f2bf(hx[rr][0]);
+      s.Hh[i][l + 64] = f2bf(hx[rr][1]);
+    }
   }
   __syncthreads();
   const ChunkDecay& cd = s.cd;
@@ -440,18 +448,25 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   SD_MARK(2, 1);
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id();
+{
+    constexpr int RPW = BT / CW;  // every row's loads first (see k_prep_c)
+    float ux[RPW][2], kx[RPW][2];
 #pragma unroll
-  for (int i = w; i < BT; i += CW) {
-    const int t = t0 + i;
-    float x0, x1;
-    load_row2(in.u, b, t, hh, T, r, x0, x1);
-    l2norm2(x0, x1, nullptr);
-    s.Pa[i][l] = x0;
-    s.Pa[i][l + 64] = x1;
-    load_row2(in.k, b, t, hh, T, r, x0, x1);
-    l2norm2(x0, x1, nullptr);
-    s.Pb[i][l] = x0;
-    s.Pb[i][l + 64] = x1;
+    for (int rr = 0; rr < RPW; ++rr) {
+      const int t = t0 + w + rr * CW;
+      load_row2(in.u, b, t, hh, T, r, ux[rr][0], ux[rr][1]);
+      load_row2(in.k, b, t, hh, T, r, kx[rr][0], kx[rr][1]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      const int i = w + rr * CW;
+      l2norm2(ux[rr][0], ux[rr][1], nullptr);
+      l2norm2(kx[rr][0], kx[rr][1], nullptr);
+      s.Pa[i][l] = ux[rr][0];
+      s.Pa[i][l + 64] = ux[rr][1];
+      s.Pb[i][l] = kx[rr][0];
+      s.Pb[i][l + 64] = kx[rr][1];
+    }
   }
   __syncthreads();
   SD_MARK(2, 2);
@@ -586,13 +601,20 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     const int i = idx / KD, c = idx % KD;
     s.Pa[i][c] *= __expf(cd.G[i][c]);
   }
+{
+    constexpr int RPW = BT / CW;
+    float vx[RPW][2], wx[RPW][2];
 #pragma unroll
-  for (int i = w; i < BT; i += CW) {
-    float v0, v1, w0, w1;
-    load_row2(in.v, b, t0 + i, hh, T, V, v0, v1);
-    load_row2(in.write_raw, b, t0 + i, hh, T, V, w0, w1);
-    s.Pb[i][l] = v0 / (1.f + __expf(-w0));
-    s.Pb[i][l + 64] = v1 / (1.f + __expf(-w1));
+    for (int rr = 0; rr < RPW; ++rr) {
+      load_row2(in.v, b, t0 + w + rr * CW, hh, T, V, vx[rr][0], vx[rr][1]);
+      load_row2(in.write_raw, b, t0 + w + rr * CW, hh, T, V, wx[rr][0], wx[rr][1]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      const int i = w + rr * CW;
+      s.Pb[i][l] = vx[rr][0] / (1.f + __expf(-wx[rr][0]));
+      s.Pb[i][l + 64] = vx[rr][1] / (1.f + __expf(-wx[rr][1]));
+    }
   }
   __syncthreads();
   // W = A (e e^G), U = A z
