@@ -282,11 +282,13 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const float* X0 = p.f.Xs + sidx * KD * KD;
   const float* XC = X0 + KD * KD;
   const float* lam = p.g.Ls + sidx * KD * KD;
+  SD_MARK(7, 0);
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+  SD_MARK(7, 1);
   // M1_ij = dw_i . w_j (j < i)
   lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
   // a = dw X0^T, kl = w lam^T for this wave's column block (K = 128)
@@ -305,6 +307,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
       kl[I] = mma_blks(A, BL, zero4());
     }
   }
+  SD_MARK(7, 2);
   __syncthreads();  // PA free
   stage_panel(s.PA, dO);
   __syncthreads();
@@ -316,6 +319,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
     lblk(s.PA, I * BS, A);
     bq[I] = mma_blks(A, BX, zero4());
   }
+  SD_MARK(7, 3);
   auto D = [&](int j, int cc) { return dd_[j * KD + cc]; };
   auto E = [&](int j, int cc) { return ee[j * KD + cc]; };
   auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
@@ -328,6 +332,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   load_slab(Sd, dd_, cb);
   load_slab(Se, ee, cb);
   load_slab(Sq, chi, cb);
+  SD_MARK(7, 4);
   // Pass A: de = -(e^G (dw X0^T) + apply(M1, d)),  dchi = e^G (dO X0^T) + apply(M2, d);
   // the decay terms chi.dchi + e.de of dg
   {
@@ -348,6 +353,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
       }
     }
   }
+  SD_MARK(7, 5);
   // Pass B: dd = e^{G_C - G} (w lam^T) + apply_t(M2, chi) - apply_t(M1, e); dg -= d.dd
   {
 #pragma unroll
@@ -364,8 +370,10 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
       }
     }
   }
+  SD_MARK(7, 6);
   __syncthreads();
   close_decay_gradient(XC, lam, dg, nullptr, s.red);
+  SD_MARK(7, 7);
 }
 
 // ---------------------------------------------------------------------------
@@ -594,13 +602,16 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       s.gam[threadIdx.x] = keep_if(t < p.T, gv);
     }
   }
+  SD_MARK(3, 0);
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
+  SD_MARK(3, 1);
   const ChunkDecay& cd = s.cd;
   // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
   lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
   lds_pair(nullptr, kh, s.PW, s.M2, false);
+  SD_MARK(3, 2);
   f4 a[NB], kl[NB];
   {
     BlkS BX, BL;
@@ -615,6 +626,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       kl[I] = mma_blks(A, BL, zero4());
     }
   }
+  SD_MARK(3, 3);
   float Su[NB][4], Sdd[NB][4], So[NB][4];
   load_slab(Su, uh, cb);
   load_slab(Sdd, ddp, cb);
@@ -633,6 +645,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   make_tab2<true>(cd, cb, tx);
   make_tab2<false>(cd, cb, ti);
   __syncthreads();  // M1, M2 complete; PA free
+  SD_MARK(3, 4);
   // PA <- dd e^G for the dq product (staged now, consumed after the applies)
   stage_panel(s.PA, ddp, [&](int i, int cc) { return __expf(cd.G[i][cc]); });
   auto U = [&](int j, int cc) { return uh[j * KD + cc]; };
@@ -643,6 +656,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   for (int J = 0; J < NB; ++J)
 #pragma unroll
     for (int e = 0; e < 4; ++e) Sx[J][e] = s.gam[J * BS + r4 + e] * Su[J][e];
+  SD_MARK(3, 5);
   float* dg = p.g.dgC + rowbase * KD;
 #pragma unroll
   for (int I = 0; I < NB; ++I) {
@@ -661,10 +675,12 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       p.g.xdx[o] = Sx[I][e] * dx;
     }
   }
+  SD_MARK(3, 6);
   __syncthreads();  // M1 free: P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) into M1
   decayed_gram<false>(
       cd, [&](int i, int cc) { return ddp[i * KD + cc]; }, [&](int j, int cc) { return uh[j * KD + cc]; },
       false, s.M1);
+  SD_MARK(3, 7);
   // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
   {
     BlkS BX;
@@ -696,7 +712,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     }
   }
   __syncthreads();
+  SD_MARK(3, 8);
   close_decay_gradient(XC, lam, dg, p.g.xdx + rowbase * KD, s.red);
+  SD_MARK(3, 9);
 }
 
 // ---------------------------------------------------------------------------
