@@ -43,7 +43,8 @@ FLOPS_PER_CHUNK = {
     "k_prep_c": 3 * _T,                          # L, W, U
     "state_c_fwd": 2 * _G,                       # w = U - W X, X += K^T w
     "k_prep_s": 6 * _T + _G,                     # k.delta, apply, P, L, W, U; K X0^T
-    "state_s_fwd": 3 * _G + _T,                  # w, Q X0, X update; P w
+    "state_s_fwd": 2 * _G,                       # w = U - W X, X += K^T w
+    "k_out_s": _G + _T,                          # o = Q X0 + P w
     "k_bprep_s": 2 * 64 ** 3 // 2 + 2 * _T * 2 // 2 + _T,  # N = P A, dU, Wk
     "state_s_bwd": 3 * _G,                       # dw, injection, lambda update
     "k_grad_s": 3 * _G + 6 * _T,                 # dw X0, dO X0, w lam; M1, M2, 2 apply, 2 apply_t
@@ -63,7 +64,8 @@ BYTES_PER_CHUNK = {
     "k_prep_c": (2 * _IN + _P) + (_A + 3 * _P),             # u,h,decay -> A,W,U,K
     "state_c_fwd": 3 * _P + (_S + _P),                      # W,U,K -> state slot, delta
     "k_prep_s": (6 * _IN + 2 * _P + _S) + (2 * _A + 7 * _P),  # inputs,decay,delta,C0 -> A,P,U,K,Q,W,chi,d,e
-    "state_s_fwd": (4 * _P + _A) + (_S + _P + _IN),         # W,U,K,Q,P -> state slot, w, out
+    "state_s_fwd": 3 * _P + (_S + _P),                      # W,U,K -> state slot, w
+    "k_out_s": (_S + 2 * _P + _A) + _IN,                    # X0,w,Q,P -> out
     "k_bprep_s": (2 * _A + 5 * _P) + 5 * _P,                # A,P,e,k,decay,K,Q -> dU,Wk,At1,B1t,Ant
     "state_s_bwd": 5 * _P + (_S + _P),                      # Wk,dU,Ant,At1,B1t -> lambda slot, dw
     "state_c_bwd": 5 * _P + (_S + _P),

@@ -642,6 +642,79 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
 size_t prep_c_smem() { return sizeof(PrepCSmem); }
 size_t prep_s_smem() { return sizeof(PrepSSmem); }
 
+// ---------------------------------------------------------------------------
+// k_out_s: the S memory's readout o = Q~ X0 + P w for every chunk in parallel,
+// from the chunk-entering states the sequential pass saved (so the pass itself
+// carries no output work).  One wave per 16-column block of the output.
+// ---------------------------------------------------------------------------
+struct OutParams {
+  int H, T, NT, Tp, V;
+  const float* Xs;  // [n][NT+1][128][128] chunk-entering S
+  const float* w;   // [n][Tp][128] S-op w
+  SP Q, P;          // fragment-ordered Q~ [64][128] and P [64][64] per chunk
+  __bf16* out;      // [B,T,H,V]
+};
+
+__global__ __launch_bounds__(CT) void k_out_s(OutParams p) {
+  const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H;
+  const int cb = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
+  const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + ch * BT;
+  const float* X0 = p.Xs + ((long long)n * (p.NT + 1) + ch) * KD * KD;
+  const float* wv = p.w + rowbase * KD;
+  // B operands (column block cb): X0 over K = 128 state rows, w over the 64 tokens
+  float xr[4][8], wr[2][8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xr[ks][e] = X0[(ks * 32 + kq + e) * KD + cb * 16 + m];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wr[ks][e] = wv[(ks * 32 + kq + e) * KD + cb * 16 + m];
+  Frag bx[4], bw[2];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 h, lo;
+      split_bf(xr[ks][e], h, lo);
+      bx[ks].h[e] = h;
+      bx[ks].l[e] = lo;
+    }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 h, lo;
+      split_bf(wr[ks][e], h, lo);
+      bw[ks].h[e] = h;
+      bw[ks].l[e] = lo;
+    }
+  const int col = cb * 16 + m;
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    Frag q[4], pf[2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) q[ks] = ldfrag(p.Q, rowbase * KD + frag_off(I * BS + m, ks * 32 + kq, KD));
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) pf[ks] = ldfrag(p.P, cidx * BT * BT + frag_off(I * BS + m, ks * 32 + kq, BT));
+    f4 acc = zero4();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mma3f(q[ks], bx[ks], acc);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (ks == 1 && I < 2) break;  // P is lower triangular: tokens 32.. only reach rows 32..
+      acc = mma3f(pf[ks], bw[ks], acc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = ch * BT + I * BS + r4 + e;
+      if (t < p.T && col < p.V)
+        p.out[(((long long)b * p.T + t) * p.H + hh) * p.V + col] = f2bf(acc[e]);
+    }
+  }
+}
+
 int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const FwdWs& w,
                hipStream_t st) {
   
@@ -663,9 +736,6 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
   sc.Wneg = w.Wc; sc.U = w.Uc; sc.Kt = w.Kc; sc.Gam = w.Gam;
   sc.Xs = w.Xc; sc.wout = w.delta;
-#ifdef SD_EXPERIMENT_NO_XS
-  sc.Xs = nullptr;
-#endif
   sc.init = in->C0; sc.init_transposed = 1;
   sc.fin = C_T; sc.fin_transposed = 1;
   launch_state("state_c_fwd", sc, false, n, st);
@@ -674,14 +744,16 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
 
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
-  ss.Wneg = w.Ws; ss.U = w.Us; ss.Kt = w.Ks; ss.Gam = w.Gam; ss.Q = w.Qs; ss.P = w.Ps;
-  ss.Xs = w.Xs; ss.wout = w.wS; ss.out = (__bf16*)out;
-#ifdef SD_EXPERIMENT_NO_XS
-  ss.Xs = nullptr;
-#endif
+  ss.Wneg = w.Ws; ss.U = w.Us; ss.Kt = w.Ks; ss.Gam = w.Gam;
+  ss.Xs = w.Xs; ss.wout = w.wS;
   ss.init = in->S0; ss.init_transposed = 0;
   ss.fin = S_T; ss.fin_transposed = 0;
-  launch_state("state_s_fwd", ss, true, n, st);
+  launch_state("state_s_fwd", ss, false, n, st);
+
+  OutParams op{};
+  op.H = in->H; op.T = in->T; op.NT = NT; op.Tp = Tp; op.V = in->V;
+  op.Xs = w.Xs; op.w = w.wS; op.Q = w.Qs; op.P = w.Ps; op.out = (__bf16*)out;
+  SD_LAUNCH("k_out_s", k_out_s, dim3(NT, n), dim3(CT), 0, st, op);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 
