@@ -790,7 +790,7 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   ss.Xs = bw.Ls; ss.wout = bw.dwS;
   ss.init = dS_T; ss.init_transposed = 0;
   ss.fin = dS0; ss.fin_transposed = 0;
-  launch_state("state_s_bwd", ss, false, n, st);
+  launch_state("state_s_bwd", ss, n, st);
   SD_LAUNCH("k_grad_s", k_grad_s, chunks, cblk, sizeof(GradSmem), st, p);
   SD_LAUNCH("k_src_bwd", k_src_bwd, rows, blk, 0, st, p);
   // C predictor
@@ -803,7 +803,7 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   sc.Xs = bw.Lc; sc.wout = bw.dwC;
   sc.init = dC_T; sc.init_transposed = 1;
   sc.fin = dC0; sc.fin_transposed = 1;
-  launch_state("state_c_bwd", sc, false, n, st);
+  launch_state("state_c_bwd", sc, n, st);
   SD_LAUNCH("k_grad_c", k_grad_c, chunks, cblk, sizeof(GradCSmem), st, p);
   SD_LAUNCH("k_final", k_final, rows, blk, 0, st, p);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;

@@ -140,7 +140,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
 // ---------------------------------------------------------------------------
 // k_state: sequential chunk pass over one 16-column tile of the state.
 //   X <- state [KD x 16] in MFMA accumulators (wave w owns rows 32w..32w+31)
-//   per chunk: slot[ch] = X;  w = U + Wneg X;  (COL_OUT) o = Q X + P w;
+//   per chunk: slot[ch] = X;  w = U + Wneg X;
 //              X = Gamma X + Kt w (+ At1 B1)
 // Operand layouts (all fp32, K contiguous so each lane's 8-element fragment is
 // two 16-byte loads): Wneg, Q, U token-major [Tp][128]; Kt, At1 chunk-transposed
@@ -168,12 +168,10 @@ struct StateSmem {
   __bf16 wl[SCOLS][BT + 8];
 };
 
-template <bool COL_OUT, bool INJ>
+template <bool INJ>
 struct StateFrags {
   Frag W[4];
   Frag K[SRB][2];
-  Frag Q[COL_OUT ? 4 : 1];
-  Frag P[COL_OUT ? 2 : 1];
   Frag A1[INJ ? SRB : 1][2];
   Frag B1[INJ ? HALVES : 1][2];
   float U[HALVES][4];
@@ -189,9 +187,9 @@ __device__ __forceinline__ Frag ldfrag(const SP& sp, long long off) {
   return f;
 }
 
-template <bool COL_OUT, bool INJ>
+template <bool INJ>
 __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
-                                                 StateFrags<COL_OUT, INJ>& f) {
+                                                 StateFrags<INJ>& f) {
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
   const int tb = w;  // this wave's token block
   const long long cidx = (long long)n * p.NT + ch;
@@ -211,13 +209,6 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
       f.U[h][e] = p.U[(rowbase + tb * 16 + (l >> 4) * 4 + e) * KD + tile * SCOLS + h * 16 + m];
 #pragma unroll
   for (int q = 0; q < SRB; ++q) f.gam[q] = ld4(p.Gam + cidx * KD + (SRB * w + q) * 16 + (l >> 4) * 4);
-  if constexpr (COL_OUT) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) f.Q[ks] = ldfrag(p.Q, wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      f.P[ks] = ldfrag(p.P, cidx * BT * BT + frag_off(tb * 16 + m, ks * 32 + kq, BT));
-  }
   if constexpr (INJ) {
 #pragma unroll
     for (int q = 0; q < SRB; ++q)
@@ -247,9 +238,9 @@ __device__ __forceinline__ void stage_split4(__bf16* hi, __bf16* lo, f4 v) {
 }
 
 // One chunk of the sequential pass with its operand fragments already in registers.
-template <bool COL_OUT, bool INJ>
+template <bool INJ>
 __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, int n, int ch, int tile,
-                                           const StateFrags<COL_OUT, INJ>& cur,
+                                           const StateFrags<INJ>& cur,
                                            f4 (&X)[SRB][HALVES]) {
   const int NS = p.NT + 1;
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
@@ -268,14 +259,11 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
     }
   __syncthreads();
   // w = U + Wneg X0 (token block tb, each half).  The work that does not depend
-  // on this chunk's w -- Gamma X (+ At1 B1) and the output's Q X0 -- is issued
-  // alongside so the independent MFMA chains overlap.
-  f4 acc[HALVES], o[HALVES];
+  // on this chunk's w -- Gamma X (+ At1 B1) -- is issued alongside so the
+  // independent MFMA chains overlap.
+  f4 acc[HALVES];
 #pragma unroll
-  for (int h = 0; h < HALVES; ++h) {
-    acc[h] = {cur.U[h][0], cur.U[h][1], cur.U[h][2], cur.U[h][3]};
-    o[h] = zero4();
-  }
+  for (int h = 0; h < HALVES; ++h) acc[h] = {cur.U[h][0], cur.U[h][1], cur.U[h][2], cur.U[h][3]};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -284,7 +272,6 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
       xb.h = ldb8(&s.Xh[h * 16 + m][ks * 32 + kq]);
       xb.l = ldb8(&s.Xl[h * 16 + m][ks * 32 + kq]);
       acc[h] = mma3f(cur.W[ks], xb, acc[h]);
-      if constexpr (COL_OUT) o[h] = mma3f(cur.Q[ks], xb, o[h]);
     }
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
@@ -305,7 +292,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
     stage_split4(&s.wh[h * 16 + m][tb * 16 + r4], &s.wl[h * 16 + m][tb * 16 + r4], acc[h]);
   }
   __syncthreads();
-  // X += Kt w: the recurrence's critical path (and o += P w)
+  // X += Kt w: the recurrence's critical path
 #pragma unroll
   for (int h = 0; h < HALVES; ++h) {
     Frag wf[2];
@@ -318,24 +305,11 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
     for (int q = 0; q < SRB; ++q)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) X[q][h] = mma3f(cur.K[q][ks], wf[ks], X[q][h]);
-    if constexpr (COL_OUT) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks == 1 && tb < 2) break;
-        o[h] = mma3f(cur.P[ks], wf[ks], o[h]);
-      }
-      const int b = n / p.H, hh = n % p.H, gcol = tile * SCOLS + h * 16 + m;
-      for (int e = 0; e < 4; ++e) {
-        const int t = ch * BT + tb * 16 + r4 + e;
-        if (t < p.T && gcol < p.cols)
-          p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + gcol] = f2bf(o[h][e]);
-      }
-    }
   }
   __syncthreads();
 }
 
-template <bool COL_OUT, bool INJ>
+template <bool INJ>
 __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   __shared__ __align__(16) StateSmem s;
   const int NS = p.NT + 1;  // state slots per sequence
@@ -374,22 +348,22 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   // unconditional prefetches) so the compiler's wait counts only cover the
   // buffer being consumed; the last one or two chunks run after the loop.
   auto clampc = [&](int it2) { return chunk_of(it2 < NT ? it2 : NT - 1); };
-  StateFrags<COL_OUT, INJ> f0, f1, f2;
+  StateFrags<INJ> f0, f1, f2;
   load_state_frags(p, n, clampc(0), tile, f0);
   load_state_frags(p, n, clampc(1), tile, f1);
   int it = 0;
   for (; it + 2 < NT; it += 3) {
     load_state_frags(p, n, clampc(it + 2), tile, f2);
     state_step(p, s, n, chunk_of(it), tile, f0, X);
-    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 0);
+    if (!INJ && it == 15) SD_MARK(6, 0);
     load_state_frags(p, n, clampc(it + 3), tile, f0);
-    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 1);
+    if (!INJ && it == 15) SD_MARK(6, 1);
     state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
-    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 2);
+    if (!INJ && it == 15) SD_MARK(6, 2);
     load_state_frags(p, n, clampc(it + 4), tile, f1);
-    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 3);
+    if (!INJ && it == 15) SD_MARK(6, 3);
     state_step(p, s, n, chunk_of(it + 2), tile, f2, X);
-    if (!COL_OUT && !INJ && it == 15) SD_MARK(6, 4);
+    if (!INJ && it == 15) SD_MARK(6, 4);
   }
   if (it < NT) state_step(p, s, n, chunk_of(it), tile, f0, X);
   if (it + 1 < NT) state_step(p, s, n, chunk_of(it + 1), tile, f1, X);
@@ -410,15 +384,12 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
       }
 }
 
-void launch_state(const char* name, const StateParams& sp, bool col_out, int nseq,
-                  hipStream_t st) {
+void launch_state(const char* name, const StateParams& sp, int nseq, hipStream_t st) {
   const dim3 grid(STILES * nseq), blk(STHREADS);
-  if (col_out)
-    SD_LAUNCH(name, (k_state<true, false>), grid, blk, 0, st, sp);
-  else if (sp.At1.hi)
-    SD_LAUNCH(name, (k_state<false, true>), grid, blk, 0, st, sp);
+  if (sp.At1.hi)
+    SD_LAUNCH(name, k_state<true>, grid, blk, 0, st, sp);
   else
-    SD_LAUNCH(name, (k_state<false, false>), grid, blk, 0, st, sp);
+    SD_LAUNCH(name, k_state<false>, grid, blk, 0, st, sp);
 }
 
 // ---------------------------------------------------------------------------
@@ -738,7 +709,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   sc.Xs = w.Xc; sc.wout = w.delta;
   sc.init = in->C0; sc.init_transposed = 1;
   sc.fin = C_T; sc.fin_transposed = 1;
-  launch_state("state_c_fwd", sc, false, n, st);
+  launch_state("state_c_fwd", sc, n, st);
 
   SD_LAUNCH("k_prep_s", k_prep_s, dim3(NT, n), dim3(CT), prep_s_smem(), st, fp);
 
@@ -748,7 +719,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   ss.Xs = w.Xs; ss.wout = w.wS;
   ss.init = in->S0; ss.init_transposed = 0;
   ss.fin = S_T; ss.fin_transposed = 0;
-  launch_state("state_s_fwd", ss, false, n, st);
+  launch_state("state_s_fwd", ss, n, st);
 
   OutParams op{};
   op.H = in->H; op.T = in->T; op.NT = NT; op.Tp = Tp; op.V = in->V;

@@ -76,8 +76,7 @@ struct StateParams {
   int H, T, NT, Tp, rows, cols, rev;
   SP Wneg; const float* U; SP Kt; const float* Gam;
   SP At1; SP B1;  // optional injection
-  SP Q; SP P;     // output operands (COL_OUT)
-  float* Xs; float* wout; __bf16* out;
+  float* Xs; float* wout;
   const float* init; int init_transposed;
   float* fin; int fin_transposed;
 };
@@ -111,8 +110,7 @@ inline void set_smem_once(const void* fn, int bytes, unsigned char* done) {
     ::sd::prof_end(st);                                                  \
   } while (0)
 
-void launch_state(const char* name, const StateParams& sp, bool col_out, int nseq,
-                  hipStream_t st);
+void launch_state(const char* name, const StateParams& sp, int nseq, hipStream_t st);
 size_t prep_c_smem();
 size_t prep_s_smem();
 
