@@ -139,6 +139,22 @@ def cpu_baseline(budget_s=24.0):
                       f"({dt:.1f} s)"}
 
 
+def forward_bench(ins, st, steps, warmup):
+    """Config 1: the same layer forward only (no autograd), same inputs."""
+    from solvedelta_amd import solvedelta_native
+    with torch.no_grad():
+        for _ in range(warmup):
+            solvedelta_native(*ins, initial_state=st, return_final_state=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            solvedelta_native(*ins, initial_state=st, return_final_state=True)
+        torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"workload": "layer forward, B=4 T=2048 H=8 r=V=128, final states returned",
+            "value": round(B * T / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4)}
+
+
 def decode_bench(dev, steps=256, streams=64):
     """Config 3: 64 independent streams x H=8, r=V=128, FP32 states C,S ~ 0.01 N(0,1)
     advanced in place by `steps` T=1 calls of the C-ABI (inputs drawn as config 1)."""
@@ -317,6 +333,7 @@ def main():
                    "heads": H, "dk": R, "dv": V, "chunk": CH, "parallelism": "single-gpu"},
         "roofline": roof,
     }
+    res["forward"] = forward_bench(ins, st, a.steps, a.warmup)
     if not a.no_decode:
         res["decode"] = decode_bench(dev)
     if not a.no_lm:
