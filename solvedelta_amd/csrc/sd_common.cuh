@@ -210,25 +210,6 @@ __device__ __forceinline__ void store_frag_panel(__bf16* hi, __bf16* lo, long lo
   }
 }
 
-// D(16x16) += A(16x16) * B(16x16) with the K=16 bf16 MFMA, same 3-term split.
-template <class FA, class FB>
-__device__ __forceinline__ f4 mma_k16(FA fa, FB fb, f4 acc) {
-  const int l = lane_id();
-  const int m = l & 15, kq = (l >> 4) * 4;
-  bf16x4 ah, al, bh, bl;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    __bf16 h, lo;
-    split_bf(fa(m, kq + e), h, lo);
-    ah[e] = h; al[e] = lo;
-    split_bf(fb(kq + e, m), h, lo);
-    bh[e] = h; bl[e] = lo;
-  }
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
-}
-
 __device__ __forceinline__ int out_row(int e) { return (lane_id() >> 4) * 4 + e; }
 __device__ __forceinline__ int out_col() { return lane_id() & 15; }
 
@@ -439,92 +420,6 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
 
 namespace sd {
 
-// Tile (rows of block I, columns cb*16..cb*16+15) of
-//   R_ic = sum_{j<=i} M_ij Y_jc exp(Gx_ic - G_jc),
-// M lower-triangular (64 x LS, zero where the pair is excluded).
-template <bool EXCL, class FY>
-__device__ f4 decayed_apply_tile(const ChunkDecay& cd, const float* M, FY Y, int I, int cb) {
-  f4 tot = zero4();
-  for (int J = 0; J <= I; ++J) {
-    f4 a2 = mma_k16([&](int m, int k) { return M[(I * BS + m) * LS + J * BS + k]; },
-                    [&](int k, int nn) {
-                      const int c = cb * 16 + nn, j = J * BS + k;
-                      return cd.wild[J][c] ? 0.f : Y(j, c) * __expf(cd.R[J][c] - cd.G[j][c]);
-                    },
-                    zero4());
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = I * BS + out_row(e), c = cb * 16 + out_col();
-      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
-      float add;
-      if (cd.wild[J][c]) {
-        add = 0.f;
-        for (int j = J * BS; j < J * BS + BS; ++j)
-          add += M[i * LS + j] * Y(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
-      } else {
-        add = __expf(gx - cd.R[J][c]) * a2[e];
-      }
-      tot[e] += add;
-    }
-  }
-  return tot;
-}
-
-// Tile (rows of block Jb, columns cb*16..) of
-//   R_jc = sum_{i>=j} M_ij X_ic exp(Gx_ic - G_jc),  M lower-triangular.
-template <bool EXCL, class FX>
-__device__ f4 decayed_apply_t_tile(const ChunkDecay& cd, const float* M, FX X, int Jb, int cb) {
-  f4 acc = zero4();
-  for (int I = Jb; I < NB; ++I) {
-    acc = mma_k16([&](int m, int k) { return M[(I * BS + k) * LS + Jb * BS + m]; },
-                  [&](int k, int nn) {
-                    const int c = cb * 16 + nn, i = I * BS + k;
-                    const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
-                    return X(i, c) * __expf(gx - cd.R[Jb][c]);
-                  },
-                  acc);
-  }
-  f4 res;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int j = Jb * BS + out_row(e), c = cb * 16 + out_col();
-    if (cd.wild[Jb][c]) {
-      float s = 0.f;
-      for (int i = j; i < BT; ++i) {
-        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
-        s += M[i * LS + j] * X(i, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
-      }
-      res[e] = s;
-    } else {
-      res[e] = __expf(cd.R[Jb][c] - cd.G[j][c]) * acc[e];
-    }
-  }
-  return res;
-}
-
-// Plain (undecayed) pair M_ij = sum_c X_ic Y_jc over c < KD for the 10 lower
-// block pairs, masked strictly (j < i) or inclusively (j <= i); upper blocks 0.
-template <class FX, class FY>
-__device__ void plain_pair(FX X, FY Y, bool strict, float* M) {
-  const int w = wave_id();
-  for (int p = w; p < 10; p += CW) {
-    int I = 0, J = p;
-    while (J > I) { J -= I + 1; ++I; }
-    f4 acc = mma_k32([&](int m, int c) { return X(I * BS + m, c); },
-                     [&](int c, int nn) { return Y(J * BS + nn, c); }, KD, zero4());
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = I * BS + out_row(e), j = J * BS + out_col();
-      const bool keep = strict ? (j < i) : (j <= i);
-      M[i * LS + j] = keep ? acc[e] : 0.f;
-    }
-  }
-  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
-    const int i = idx / BT, j = idx % BT;
-    if ((j / BS) > (i / BS)) M[i * LS + j] = 0.f;
-  }
-}
-
 }  // namespace sd
 
 namespace sd {
@@ -550,33 +445,6 @@ __device__ __forceinline__ void load_blk(Blk& b, const float* rows, int ld) {
   }
 }
 
-__device__ __forceinline__ f4 mma3v(const float* av, const float* bv, f4 acc) {
-  bf16x8 ah, al, bh, bl;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    __bf16 h, lo;
-    split_bf(av[e], h, lo);
-    ah[e] = h; al[e] = lo;
-    split_bf(bv[e], h, lo);
-    bh[e] = h; bl[e] = lo;
-  }
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
-}
-
-__device__ __forceinline__ f4 mma_blk(const Blk& A, const Blk& B, f4 acc) {
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const float av[8] = {A.v[ks][0].x, A.v[ks][0].y, A.v[ks][0].z, A.v[ks][0].w,
-                         A.v[ks][1].x, A.v[ks][1].y, A.v[ks][1].z, A.v[ks][1].w};
-    const float bv[8] = {B.v[ks][0].x, B.v[ks][0].y, B.v[ks][0].z, B.v[ks][0].w,
-                         B.v[ks][1].x, B.v[ks][1].y, B.v[ks][1].z, B.v[ks][1].w};
-    acc = mma3v(av, bv, acc);
-  }
-  return acc;
-}
-
 __device__ __forceinline__ void load_slab(float (&s)[NB][4], const float* panel, int cb) {
   const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
 #pragma unroll
@@ -585,81 +453,6 @@ __device__ __forceinline__ void load_slab(float (&s)[NB][4], const float* panel,
     for (int e = 0; e < 4; ++e) s[J][e] = panel[(J * BS + r4 + e) * KD + c];
 }
 
-
-// R_ic = sum_{j<=i} M_ij Y_jc exp(Gx_ic - G_jc) for row block I and this lane's
-// column, with Y given as a slab; Yw(j, c) is read only for wild coordinates.
-template <bool EXCL, class FW>
-__device__ f4 apply_slab(const ChunkDecay& cd, const float* M, const float (&Y)[NB][4], int I, int cb,
-                         FW Yw) {
-  const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
-  f4 tot = zero4();
-#pragma unroll
-  for (int J = 0; J < NB; ++J) {
-    if (J > I) break;
-    const bool wild = cd.wild[J][c];
-    float av[4], bv[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      av[e] = M[(I * BS + m) * LS + J * BS + r4 + e];
-      bv[e] = wild ? 0.f : Y[J][e] * __expf(cd.R[J][c] - cd.G[J * BS + r4 + e][c]);
-    }
-    // lanes hold B columns n = lane&15 = this lane's c: B[k][n] = Yhat[J*16 + k][c]
-    const f4 a2 = mma16s(av, bv, zero4());
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = I * BS + r4 + e;
-      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
-      float add;
-      if (wild) {
-        add = 0.f;
-        for (int j = J * BS; j < J * BS + BS; ++j)
-          add += M[i * LS + j] * Yw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
-      } else {
-        add = __expf(gx - cd.R[J][c]) * a2[e];
-      }
-      tot[e] += add;
-    }
-  }
-  return tot;
-}
-
-// R_jc = sum_{i>=j} M_ij X_ic exp(Gx_ic - G_jc) for row block Jb, X as a slab.
-template <bool EXCL, class FW>
-__device__ f4 apply_t_slab(const ChunkDecay& cd, const float* M, const float (&X)[NB][4], int Jb,
-                           int cb, FW Xw) {
-  const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
-  f4 acc = zero4();
-#pragma unroll
-  for (int I = 0; I < NB; ++I) {
-    if (I < Jb) continue;
-    float av[4], bv[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = I * BS + r4 + e;
-      av[e] = M[i * LS + Jb * BS + m];
-      const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
-      bv[e] = X[I][e] * __expf(gx - cd.R[Jb][c]);
-    }
-    acc = mma16s(av, bv, acc);
-  }
-  f4 res;
-  const bool wild = cd.wild[Jb][c];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int j = Jb * BS + r4 + e;
-    if (wild) {
-      float s = 0.f;
-      for (int i = j; i < BT; ++i) {
-        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
-        s += M[i * LS + j] * Xw(i, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
-      }
-      res[e] = s;
-    } else {
-      res[e] = __expf(cd.R[Jb][c] - cd.G[j][c]) * acc[e];
-    }
-  }
-  return res;
-}
 
 }  // namespace sd
 
@@ -695,41 +488,6 @@ __device__ __forceinline__ f4 mma_blks(const BlkS& A, const BlkS& B, f4 acc) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) acc = mma3f(A.f[ks], B.f[ks], acc);
   return acc;
-}
-
-// Both plain pair matrices sharing the right factor:
-//   M1_ij = X1_i . Y_j (j < i),  M2_ij = X2_i . Y_j (j <= i),  over KD = 128.
-// Each wave loads the three row blocks of its block pair once.
-template <class P1, class P2, class PY>
-__device__ void plain_pairs2(P1 x1, P2 x2, PY y, float* M1, float* M2) {
-  const int w = wave_id();
-  for (int pp = w; pp < 10; pp += CW) {
-    int I = 0, J = pp;
-    while (J > I) { J -= I + 1; ++I; }
-    Blk a1, a2, bb;
-    load_blk(a1, x1 + I * BS * KD, KD);
-    load_blk(a2, x2 + I * BS * KD, KD);
-    load_blk(bb, y + J * BS * KD, KD);
-    BlkS s1, s2, sb;
-    split_blk(a1, s1);
-    split_blk(a2, s2);
-    split_blk(bb, sb);
-    const f4 r1 = mma_blks(s1, sb, zero4());
-    const f4 r2 = mma_blks(s2, sb, zero4());
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = I * BS + out_row(e), j = J * BS + out_col();
-      M1[i * LS + j] = j < i ? r1[e] : 0.f;
-      M2[i * LS + j] = j <= i ? r2[e] : 0.f;
-    }
-  }
-  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
-    const int i = idx / BT, j = idx % BT;
-    if ((j / BS) > (i / BS)) {
-      M1[i * LS + j] = 0.f;
-      M2[i * LS + j] = 0.f;
-    }
-  }
 }
 
 // Per-lane decay factors for the slab applies of one 16-column block:
