@@ -291,10 +291,22 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   SD_MARK(7, 1);
   // M1_ij = dw_i . w_j (j < i)
   lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
-  // a = dw X0^T, kl = w lam^T for this wave's column block (K = 128)
+  // a = dw X0^T for this wave's column block (K = 128)
   f4 a[NB], bq[NB], kl[NB];
   BlkS BX;
   load_split_blk_g(X0 + cb * 16 * KD, BX);
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+    BlkS A;
+    lblk(s.PA, I * BS, A);
+    a[I] = mma_blks(A, BX, zero4());
+  }
+  SD_MARK(7, 2);
+  __syncthreads();  // PA free
+  stage_panel(s.PA, dO);
+  __syncthreads();
+  // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T;  kl = w lam^T
+  lds_pair(&s.PA, nullptr, s.PW, s.M2, false);
   {
     BlkS BL;
     load_split_blk_g(lam + cb * 16 * KD, BL);
@@ -302,23 +314,20 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
     for (int I = 0; I < NB; ++I) {
       BlkS A;
       lblk(s.PA, I * BS, A);
-      a[I] = mma_blks(A, BX, zero4());
+      bq[I] = mma_blks(A, BX, zero4());
       lblk(s.PW, I * BS, A);
       kl[I] = mma_blks(A, BL, zero4());
     }
   }
-  SD_MARK(7, 2);
-  __syncthreads();  // PA free
-  stage_panel(s.PA, dO);
-  __syncthreads();
-  // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T
-  lds_pair(&s.PA, nullptr, s.PW, s.M2, false);
+  // kl is consumed only by pass B: park it in the dead PA panel (lane-private
+  // slots) so it holds no registers through pass A.
+  float* const kl_park = reinterpret_cast<float*>(&s.PA);
+  static_assert(sizeof(LPanel) >= NB * 4 * CT * sizeof(float), "kl park slot");
+  __syncthreads();  // every wave is done reading PA
 #pragma unroll
-  for (int I = 0; I < NB; ++I) {
-    BlkS A;
-    lblk(s.PA, I * BS, A);
-    bq[I] = mma_blks(A, BX, zero4());
-  }
+  for (int I = 0; I < NB; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kl_park[(I * 4 + e) * CT + threadIdx.x] = kl[I][e];
   SD_MARK(7, 3);
   auto D = [&](int j, int cc) { return dd_[j * KD + cc]; };
   auto E = [&](int j, int cc) { return ee[j * KD + cc]; };
@@ -335,6 +344,11 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   SD_MARK(7, 4);
   // Pass A: de = -(e^G (dw X0^T) + apply(M1, d)),  dchi = e^G (dO X0^T) + apply(M2, d);
   // the decay terms chi.dchi + e.de of dg
+  // Chunk-uniform output bases with 32-bit lane offsets: 64-bit per-row
+  // addresses would not fit in registers beside the slabs.
+  float* const de_b = p.g.de + rowbase * KD;
+  float* const dchi_b = p.g.dchi + rowbase * KD;
+  float* const dd_b = p.g.dd + rowbase * KD;
   {
     __syncthreads();  // M1, M2 complete
 #pragma unroll
@@ -345,17 +359,30 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
         const float eg = __expf(cd.G[i][c]);
-        const long long o = (rowbase + i) * KD + c;
         const float dev = -(eg * a[I][e] + ap[e]), dcv = eg * bq[I][e] + bp[e];
-        p.g.de[o] = dev;
-        p.g.dchi[o] = dcv;
+        a[I][e] = dev;  // results take the registers of the products they consume
+        bq[I][e] = dcv;
         pdg[I][e] = Sq[I][e] * dcv + Se[I][e] * dev;
       }
     }
+    // Stores after the pass: a store issued before a register reload would make
+    // the reload wait for it (loads and stores share one counter).
+#pragma unroll
+    for (int I = 0; I < NB; ++I)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned o = (unsigned)((I * BS + r4 + e) * KD + c);
+        de_b[o] = a[I][e];
+        dchi_b[o] = bq[I][e];
+      }
   }
   SD_MARK(7, 5);
   // Pass B: dd = e^{G_C - G} (w lam^T) + apply_t(M2, chi) - apply_t(M1, e); dg -= d.dd
   {
+#pragma unroll
+    for (int I = 0; I < NB; ++I)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kl[I][e] = kl_park[(I * 4 + e) * CT + threadIdx.x];
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       f4 k2, k3;
@@ -363,12 +390,19 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
-        const long long o = (rowbase + i) * KD + c;
         const float ddv = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[I][e] + k2[e] - k3[e];
-        p.g.dd[o] = ddv;
-        dg[i * KD + c] = pdg[I][e] - Sd[I][e] * ddv;
+        kl[I][e] = ddv;
+        pdg[I][e] -= Sd[I][e] * ddv;
       }
     }
+#pragma unroll
+    for (int I = 0; I < NB; ++I)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned o = (unsigned)((I * BS + r4 + e) * KD + c);
+        dd_b[o] = kl[I][e];
+        dg[o] = pdg[I][e];
+      }
   }
   SD_MARK(7, 6);
   __syncthreads();
@@ -658,6 +692,10 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     for (int e = 0; e < 4; ++e) Sx[J][e] = s.gam[J * BS + r4 + e] * Su[J][e];
   SD_MARK(3, 5);
   float* dg = p.g.dgC + rowbase * KD;
+  // chunk-uniform output bases, 32-bit lane offsets (keeps addresses out of VGPR pairs)
+  float* const dx_b = p.g.dxC + rowbase * KD;
+  float* const dk_b = p.g.dkC + rowbase * KD;
+  float* const xdx_b = p.g.xdx + rowbase * KD;
 #pragma unroll
   for (int I = 0; I < NB; ++I) {
     const f4 ap = apply_tab<true>(cd, s.M1, Su, I, cb, t1, tx, U);
@@ -668,11 +706,11 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       const int i = I * BS + r4 + e;
       const float dx = -(__expf(gx_excl(cd, i, c)) * a[I][e] + ap[e]);
       const float dk = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[I][e] + k2[e] - k3[e];
-      const long long o = (rowbase + i) * KD + c;
-      p.g.dxC[o] = dx;
-      p.g.dkC[o] = dk;
-      dg[i * KD + c] = So[I][e] * Sdd[I][e] - Su[I][e] * dk;
-      p.g.xdx[o] = Sx[I][e] * dx;
+      const unsigned o = (unsigned)(i * KD + c);
+      dx_b[o] = dx;
+      dk_b[o] = dk;
+      dg[o] = So[I][e] * Sdd[I][e] - Su[I][e] * dk;
+      xdx_b[o] = Sx[I][e] * dx;
     }
   }
   SD_MARK(3, 6);
@@ -683,6 +721,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   SD_MARK(3, 7);
   // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
   {
+    float* const dq_b = p.g.dqC + rowbase * KD;
     BlkS BX;
     {
       const int kq = (l >> 4) * 8;
@@ -708,7 +747,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
                    },
                    (I < 2 ? 32 : 64), dq);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) p.g.dqC[(rowbase + I * BS + r4 + e) * KD + c] = dq[e];
+      for (int e = 0; e < 4; ++e) dq_b[(unsigned)((I * BS + r4 + e) * KD + c)] = dq[e];
     }
   }
   __syncthreads();

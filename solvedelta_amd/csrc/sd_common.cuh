@@ -87,6 +87,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// Sum over each 16-lane DPP row, returned to all 16 lanes of that row (no
+// readlane, so four token rows reduce at once in one wave).
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_add(v, 0);
+  v = dpp_add(v, 1);
+  v = dpp_add(v, 2);
+  return dpp_add(v, 3);
+}
+
 __device__ __forceinline__ f4 zero4() { f4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // Split an fp32 value into a bf16 high part and a bf16 residual.
@@ -543,6 +552,7 @@ __device__ f4 apply_tab(const ChunkDecay& cd, const float* M, const float (&Y)[N
         const int i = I * BS + r4 + e;
         const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
         float add = 0.f;
+        #pragma unroll 1  // rare wild path: keep it small and low-pressure
         for (int j = J * BS; j < J * BS + BS; ++j)
           add += M[i * LS + j] * Yw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
         tot[e] += add;
@@ -577,6 +587,7 @@ __device__ f4 apply_t_tab(const ChunkDecay& cd, const float* M, const float (&X)
     for (int e = 0; e < 4; ++e) {
       const int j = Jb * BS + r4 + e;
       float s = 0.f;
+      #pragma unroll 1  // rare wild path: keep it small and low-pressure
       for (int i = j; i < BT; ++i) {
         const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
         s += M[i * LS + j] * Xw(i, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
@@ -616,6 +627,7 @@ __device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M
         const int i = I * BS + r4 + e;
         const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
         float s1 = 0.f, s2 = 0.f;
+        #pragma unroll 1  // rare wild path: keep it small and low-pressure
         for (int j = J * BS; j < J * BS + BS; ++j) {
           const float f = Yw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
           s1 += M1[i * LS + j] * f;
@@ -665,6 +677,7 @@ __device__ void apply_t2_tab(const ChunkDecay& cd, const float* M1, const float 
     for (int e = 0; e < 4; ++e) {
       const int j = Jb * BS + r4 + e;
       float s1 = 0.f, s2 = 0.f;
+      #pragma unroll 1  // rare wild path: keep it small and low-pressure
       for (int i = j; i < BT; ++i) {
         const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
         const float f = __expf(fminf(gx - cd.G[j][c], 0.f));

@@ -25,15 +25,6 @@ __device__ __forceinline__ float gamma_at(const sd_view& g, int b, int t, int h)
   return ((const float*)g.data)[(long long)b * g.sb + (long long)t * g.st + (long long)h * g.sh];
 }
 
-// Normalise one 128-wide row held as (x0 = coord lane, x1 = coord lane+64).
-__device__ __forceinline__ void l2norm2(float& x0, float& x1, float* rs_out) {
-  float ss = wave_sum(x0 * x0 + x1 * x1);
-  float rs = rsqrtf(ss + 1e-24f);
-  x0 *= rs;
-  x1 *= rs;
-  if (rs_out) *rs_out = rs;
-}
-
 // Branch-free row load (lane holds coords lane and lane+64): out-of-range tokens
 // and coordinates read a valid element and are selected to 0, so unrolled loops
 // can issue every load before the first use.
@@ -45,6 +36,35 @@ __device__ __forceinline__ void load_row2(const sd_view& v, int b, int t, int h,
   const float a0 = bf2f(p[l < w ? l : w - 1]), a1 = bf2f(p[l + 64 < w ? l + 64 : w - 1]);
   x0 = keep_if(tv && l < w, a0);
   x1 = keep_if(tv && l + 64 < w, a1);
+}
+
+// 16-lane row layout for per-token row work: a wave covers four token rows at
+// once, lane (l & 15) of DPP row (l >> 4) holding columns (l & 15) + 16 q, so a
+// row's reductions are four in-row DPP adds.  A chunk's 64 rows take two such
+// groups per wave: row16(w, g) = 8 w + 4 g + (l >> 4).
+constexpr int RQ = KD / 16;
+__device__ __forceinline__ int row16(int w, int g) { return w * 8 + g * 4 + (lane_id() >> 4); }
+
+// Branch-free 16-lane row load (see load_row2), columns (l & 15) + 16 q.
+__device__ __forceinline__ void load_row16(const sd_view& v, int b, int t, int h, int T, int w,
+                                           float (&x)[RQ]) {
+  const int cl = lane_id() & 15;
+  const bool tv = t < T;
+  const __bf16* p = vrow(v, b, tv ? t : T - 1, h);
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    const int c = cl + 16 * q;
+    x[q] = keep_if(tv && c < w, bf2f(p[c < w ? c : w - 1]));
+  }
+}
+
+__device__ __forceinline__ void l2norm16(float (&x)[RQ]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) ss += x[q] * x[q];
+  const float rs = rsqrtf(row16_sum(ss) + 1e-24f);
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) x[q] *= rs;
 }
 
 constexpr int PS = KD + 8;  // bf16 panel row stride
@@ -80,22 +100,23 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
 {
     // every row's loads first: a row's reduction would otherwise hold the next
     // row's loads behind it
-    constexpr int RPW = BT / CW;
-    float ux[RPW][2], hx[RPW][2];
+    const int cl = l & 15;
+    float ux[2][RQ], hx[2][RQ];
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const int t = t0 + w + rr * CW;
-      load_row2(in.u, b, t, hh, T, r, ux[rr][0], ux[rr][1]);
-      load_row2(in.h, b, t, hh, T, r, hx[rr][0], hx[rr][1]);
+    for (int g = 0; g < 2; ++g) {
+      const int t = t0 + row16(w, g);
+      load_row16(in.u, b, t, hh, T, r, ux[g]);
+      load_row16(in.h, b, t, hh, T, r, hx[g]);
     }
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const int i = w + rr * CW;
-      l2norm2(ux[rr][0], ux[rr][1], nullptr);
-      s.Uh[i][l] = ux[rr][0];
-      s.Uh[i][l + 64] = ux[rr][1];
-      s.Hh[i][l] = f2bf(hx[rr][0]);
-      s.Hh[i][l + 64] = f2bf(hx[rr][1]);
+    for (int g = 0; g < 2; ++g) {
+      const int i = row16(w, g);
+      l2norm16(ux[g]);
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        s.Uh[i][cl + 16 * q] = ux[g][q];
+        s.Hh[i][cl + 16 * q] = f2bf(hx[g][q]);
+      }
     }
   }
   __syncthreads();
@@ -420,23 +441,24 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id();
 {
-    constexpr int RPW = BT / CW;  // every row's loads first (see k_prep_c)
-    float ux[RPW][2], kx[RPW][2];
+    const int cl = l & 15;  // every row's loads first (see k_prep_c)
+    float ux[2][RQ], kx[2][RQ];
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const int t = t0 + w + rr * CW;
-      load_row2(in.u, b, t, hh, T, r, ux[rr][0], ux[rr][1]);
-      load_row2(in.k, b, t, hh, T, r, kx[rr][0], kx[rr][1]);
+    for (int g = 0; g < 2; ++g) {
+      const int t = t0 + row16(w, g);
+      load_row16(in.u, b, t, hh, T, r, ux[g]);
+      load_row16(in.k, b, t, hh, T, r, kx[g]);
     }
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const int i = w + rr * CW;
-      l2norm2(ux[rr][0], ux[rr][1], nullptr);
-      l2norm2(kx[rr][0], kx[rr][1], nullptr);
-      s.Pa[i][l] = ux[rr][0];
-      s.Pa[i][l + 64] = ux[rr][1];
-      s.Pb[i][l] = kx[rr][0];
-      s.Pb[i][l + 64] = kx[rr][1];
+    for (int g = 0; g < 2; ++g) {
+      const int i = row16(w, g);
+      l2norm16(ux[g]);
+      l2norm16(kx[g]);
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        s.Pa[i][cl + 16 * q] = ux[g][q];
+        s.Pb[i][cl + 16 * q] = kx[g][q];
+      }
     }
   }
   __syncthreads();
@@ -502,47 +524,68 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   }
   __syncthreads();
   SD_MARK(2, 4);
-  // sources (one wave per token row; e overwrites u, chi overwrites k).  The
-  // wave's rows of delta, q and erase are all loaded before the first row is
-  // processed: the rows' global stores would otherwise hold each next row's
-  // loads behind them.
-  constexpr int RPW = BT / CW;  // rows per wave
-  float dq_[RPW][2], qq_[RPW][2], er_[RPW][2];
+  // sources (16-lane row layout; e overwrites u, chi overwrites k).  Both row
+  // groups' delta, q and erase are loaded before the first row is processed:
+  // the rows' global stores would otherwise hold the next rows' loads behind them.
+  {
+    const int cl = l & 15;
+    float dq_[2][RQ], qq_[2][RQ], er_[2][RQ];
 #pragma unroll
-  for (int rr = 0; rr < RPW; ++rr) {
-    const int i = w + rr * CW, t = t0 + i;
-    dq_[rr][0] = delta[(long long)i * KD + l];
-    dq_[rr][1] = delta[(long long)i * KD + l + 64];
-    load_row2(in.q, b, t, hh, T, r, qq_[rr][0], qq_[rr][1]);
-    load_row2(in.erase_raw, b, t, hh, T, r, er_[rr][0], er_[rr][1]);
-  }
+    for (int g = 0; g < 2; ++g) {
+      const int i = row16(w, g), t = t0 + i;
 #pragma unroll
-  for (int rr = 0; rr < RPW; ++rr) {
-    const int i = w + rr * CW;
-    const float u0 = s.Pa[i][l], u1 = s.Pa[i][l + 64];
-    const float k0 = s.Pb[i][l], k1 = s.Pb[i][l + 64];
-    const float d0 = dq_[rr][0], d1 = dq_[rr][1];
-    float q0 = qq_[rr][0], q1 = qq_[rr][1];
-    const float e0 = er_[rr][0], e1 = er_[rr][1];
-    l2norm2(q0, q1, nullptr);
-    const float usq = wave_sum(u0 * u0 + u1 * u1);
-    const float dsq = wave_sum(d0 * d0 + d1 * d1);
-    const float sc = RHO / sqrtf(RHO * RHO + usq * dsq);
-    const float p0 = sc * d0, p1 = sc * d1;
-    const float den = 1.f + wave_sum(p0 * u0 + p1 * u1);
-    const float b0 = k0 / (1.f + __expf(-e0)), b1 = k1 / (1.f + __expf(-e1));
-    const float ub = wave_sum(u0 * b0 + u1 * b1) / den;
-    const float uq = wave_sum(u0 * q0 + u1 * q1) / den;
-    const bool in0 = l < r, in1 = l + 64 < r;
-    s.Pa[i][l] = in0 ? b0 - p0 * ub : 0.f;
-    s.Pa[i][l + 64] = in1 ? b1 - p1 * ub : 0.f;
-    s.Pb[i][l] = in0 ? q0 - p0 * uq : 0.f;
-    s.Pb[i][l + 64] = in1 ? q1 - p1 * uq : 0.f;
-    p.e[(rowbase + i) * KD + l] = s.Pa[i][l];
-    p.e[(rowbase + i) * KD + l + 64] = s.Pa[i][l + 64];
-    p.chi[(rowbase + i) * KD + l] = s.Pb[i][l];
-    p.chi[(rowbase + i) * KD + l + 64] = s.Pb[i][l + 64];
+      for (int q = 0; q < RQ; ++q) dq_[g][q] = delta[i * KD + cl + 16 * q];
+      load_row16(in.q, b, t, hh, T, r, qq_[g]);
+      load_row16(in.erase_raw, b, t, hh, T, r, er_[g]);
+    }
+    SD_MARK(2, 10);
+    float* const e_b = p.e + rowbase * KD;
+    float* const chi_b = p.chi + rowbase * KD;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int i = row16(w, g);
+      float u[RQ], k[RQ];
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        u[q] = s.Pa[i][cl + 16 * q];
+        k[q] = s.Pb[i][cl + 16 * q];
+      }
+      l2norm16(qq_[g]);
+      float usq = 0.f, dsq = 0.f;
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        usq += u[q] * u[q];
+        dsq += dq_[g][q] * dq_[g][q];
+      }
+      usq = row16_sum(usq);
+      dsq = row16_sum(dsq);
+      const float sc = RHO / sqrtf(RHO * RHO + usq * dsq);
+      float pv[RQ], bv[RQ], pu = 0.f, ubs = 0.f, uqs = 0.f;
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        pv[q] = sc * dq_[g][q];
+        bv[q] = k[q] / (1.f + __expf(-er_[g][q]));
+        pu += pv[q] * u[q];
+        ubs += u[q] * bv[q];
+        uqs += u[q] * qq_[g][q];
+      }
+      const float den = 1.f + row16_sum(pu);
+      const float ub = row16_sum(ubs) / den;
+      const float uq = row16_sum(uqs) / den;
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        const int c = cl + 16 * q;
+        const bool in = c < r;
+        const float ev = in ? bv[q] - pv[q] * ub : 0.f;
+        const float xv = in ? qq_[g][q] - pv[q] * uq : 0.f;
+        s.Pa[i][c] = ev;
+        s.Pb[i][c] = xv;
+        e_b[i * KD + c] = ev;
+        chi_b[i * KD + c] = xv;
+      }
+    }
   }
+  SD_MARK(2, 12);
   __syncthreads();
   SD_MARK(2, 5);
   // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i
