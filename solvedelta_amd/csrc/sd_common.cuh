@@ -280,6 +280,14 @@ __device__ __forceinline__ void build_decay(ChunkDecay& cd, const float* g, long
   __syncthreads();
 }
 
+// exp(x) on a non-wild coordinate, 0 on a wild one, without a branch (a
+// per-element branch around the exp serialises the gathers it sits among).  A
+// wild coordinate's argument can exceed the fp32 exp range, so it is clamped
+// before the mask; a non-wild argument is at most TAU and is left unchanged.
+__device__ __forceinline__ float exp_unless_wild(bool wild, float x) {
+  return keep_if(!wild, __expf(fminf(x, 2.f * TAU)));
+}
+
 // Gx for the erase side: inclusive (G_i) or exclusive (G_{i-1} = G_i - g_i).
 // The exclusive prefix is G[i-1] (0 for i = 0).
 __device__ __forceinline__ float gx_excl(const ChunkDecay& cd, int i, int c) {
@@ -289,7 +297,7 @@ __device__ __forceinline__ float gx_excl(const ChunkDecay& cd, int i, int c) {
 // Decayed Gram M_ij = sum_c X_ic Y_jc exp(Gx_ic - G_jc), j<i (strict) or j<=i,
 // written to M (64 x LS, fp32); entries above the diagonal set to 0.
 // X(i,c), Y(j,c) are lambdas returning fp32; EXCL selects Gx.
-template <bool EXCL, class FX, class FY>
+template <bool EXCL, int MS = -1, class FX, class FY>
 __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, float* M,
                              int ldm = LS) {
   const int w = wave_id();
@@ -308,7 +316,7 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
         },
         [&](int c, int n) { return Y(J0 + n, c); },
         [&](int c, int n, float y) {
-          return cd.wild[J][c] ? 0.f : y * __expf(RJ[c] - cd.G[J0 + n][c]);
+          return y * exp_unless_wild(cd.wild[J][c] != 0, RJ[c] - cd.G[J0 + n][c]);
         },
         KD, zero4());
 #pragma unroll
@@ -318,12 +326,14 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
       M[i * ldm + j] = keep ? acc[e] : 0.f;
     }
   }
+  if constexpr (MS >= 0) SD_MARK(MS, 13);
   // Zero the strictly-upper block pairs.
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
     const int i = idx / BT, j = idx % BT;
     if ((j / BS) > (i / BS)) M[i * ldm + j] = 0.f;
   }
   __syncthreads();
+  if constexpr (MS >= 0) SD_MARK(MS, 14);
   // Exact fix-up for wild coordinates.
   for (int J = 0; J < NB; ++J) {
     const int nw = cd.nwild[J];
@@ -513,7 +523,7 @@ __device__ __forceinline__ void make_tab1(const ChunkDecay& cd, int cb, Tab1& t)
   for (int J = 0; J < NB; ++J) {
     const bool wild = cd.wild[J][c];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) t.E1[J][e] = wild ? 0.f : __expf(cd.R[J][c] - cd.G[J * BS + r4 + e][c]);
+    for (int e = 0; e < 4; ++e) t.E1[J][e] = exp_unless_wild(wild, cd.R[J][c] - cd.G[J * BS + r4 + e][c]);
   }
 }
 

@@ -602,7 +602,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   __syncthreads();
   SD_MARK(2, 6);
   // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
-  decayed_gram<false>(
+  decayed_gram<false, 2>(
       cd, [&](int i, int c) { return s.Pa[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
       true, s.M);
   SD_MARK(2, 7);
