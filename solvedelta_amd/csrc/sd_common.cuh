@@ -291,7 +291,7 @@ __device__ __forceinline__ float exp_unless_wild(bool wild, float x) {
 // Gx for the erase side: inclusive (G_i) or exclusive (G_{i-1} = G_i - g_i).
 // The exclusive prefix is G[i-1] (0 for i = 0).
 __device__ __forceinline__ float gx_excl(const ChunkDecay& cd, int i, int c) {
-  return i > 0 ? cd.G[i - 1][c] : 0.f;
+  return keep_if(i > 0, cd.G[i > 0 ? i - 1 : 0][c]);  // clamped read + mask: no branch
 }
 
 // Decayed Gram M_ij = sum_c X_ic Y_jc exp(Gx_ic - G_jc), j<i (strict) or j<=i,
