@@ -73,6 +73,17 @@ __device__ __forceinline__ const float* gptr(const sd_inputs& in, int b, int h) 
          (long long)h * in.log_decay.sh;
 }
 
+// A wave's 64 x 16 output column block (MFMA layout, block Jb in v[Jb]) stored
+// after the loop that made it: a store between the loop's gathers would hold
+// every later gather behind it.
+__device__ __forceinline__ void store_du_slab(float* base, const f4 (&v)[NB]) {
+  const int c = wave_id() * 16 + out_col();
+#pragma unroll
+  for (int Jb = 0; Jb < NB; ++Jb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) base[(unsigned)((Jb * BS + out_row(e)) * KD + c)] = v[Jb][e];
+}
+
 // 64x64 N = P A (both 64 x LS in LDS) -> N (64 x LS)
 __device__ void mat64_mul(const float* P, const float* A, float* N) {
   for (int tt = wave_id(); tt < NB * NB; tt += CW) {
@@ -124,7 +135,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   __syncthreads();
   const int w = wave_id();
   const long long kbase = cidx * KD * BT;
-  f4 wks[NB];
+  f4 wks[NB], dus[NB];
   for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_l N_lj dO_l ;  Wk_j = sum_i A_ij K^_i
@@ -134,14 +145,10 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       f4 wk = mma_k32_lx([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; }, XId(),
                          [&](int k, int nn) { return sp_raw(p.f.Ks, kbase + frag_off(cb * 16 + nn, k, BT)); },
                          [](int, int, SPRaw r) { return sp_val(r); }, BT, zero4());
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const long long row = rowbase + Jb * BS + out_row(e);
-        const int c = cb * 16 + out_col();
-        p.g.dU[row * KD + c] = du[e];
-      }
+      dus[Jb] = du;
       wks[Jb] = wk;
     }
+  store_du_slab(p.g.dU + rowbase * KD, dus);
   // Wk staged in the free P / N rows, then stored in fragment order
   __syncthreads();
   {
@@ -525,23 +532,24 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     s.gam[threadIdx.x] = keep_if(t < p.T, gv);
   }
 {
-    constexpr int RPW = BT / CW;  // every row's loads before the first reduction
-    float ux[RPW][2], kx[RPW][2];
+    const int cl = l & 15;  // 16-lane rows: every row's loads before the first reduction
+    float ux[2][RQ], kx[2][RQ];
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const int t = t0 + w + rr * CW;
-      ldrow2(p.in.u, b, t, hh, p.T, p.r, ux[rr][0], ux[rr][1]);
-      ldrow2(p.in.k, b, t, hh, p.T, p.r, kx[rr][0], kx[rr][1]);
+    for (int g = 0; g < 2; ++g) {
+      const int t = t0 + row16(w, g);
+      ld_row16(brow(p.in.u, b, t < p.T ? t : p.T - 1, hh), t < p.T, p.r, ux[g]);
+      ld_row16(brow(p.in.k, b, t < p.T ? t : p.T - 1, hh), t < p.T, p.r, kx[g]);
     }
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const int i = w + rr * CW;
-      norm2(ux[rr][0], ux[rr][1]);
-      norm2(kx[rr][0], kx[rr][1]);
-      s.Uh[i][l] = ux[rr][0];
-      s.Uh[i][l + 64] = ux[rr][1];
-      s.Kh[i][l] = kx[rr][0];
-      s.Kh[i][l + 64] = kx[rr][1];
+    for (int g = 0; g < 2; ++g) {
+      const int i = row16(w, g);
+      l2norm16(ux[g]);
+      l2norm16(kx[g]);
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        s.Uh[i][cl + 16 * q] = ux[g][q];
+        s.Kh[i][cl + 16 * q] = kx[g][q];
+      }
     }
   }
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
@@ -556,7 +564,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   __syncthreads();
   const float* ddl = p.g.ddelta + rowbase * KD;
   const long long kbase = cidx * KD * BT;
-  f4 wks[NB];
+  f4 wks[NB], dus[NB];
   for (int cb = w; cb < w + 1; ++cb)
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_i A_ij ddelta_i + sum_l N_lj k_l ;  Wk_j = sum_i A_ij K^_i
@@ -567,14 +575,10 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       f4 wk = mma_k32_lx([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; }, XId(),
                          [&](int k, int nn) { return sp_raw(p.f.Kc, kbase + frag_off(cb * 16 + nn, k, BT)); },
                          [](int, int, SPRaw r) { return sp_val(r); }, BT, zero4());
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const long long row = rowbase + Jb * BS + out_row(e);
-        const int c = cb * 16 + out_col();
-        p.g.dU[row * KD + c] = du[e];
-      }
+      dus[Jb] = du;
       wks[Jb] = wk;
     }
+  store_du_slab(p.g.dU + rowbase * KD, dus);
   __syncthreads();
   {
     float* Wst = s.P;  // 64 x 128 fits in P and N

@@ -96,6 +96,34 @@ __device__ __forceinline__ float row16_sum(float v) {
   return dpp_add(v, 3);
 }
 
+// 16-lane row layout for per-token row work: a wave covers four token rows at
+// once, lane (l & 15) of DPP row (l >> 4) holding columns (l & 15) + 16 q, so a
+// row's reductions are four in-row DPP adds.  A chunk's 64 rows take two such
+// groups per wave: row16(w, g) = 8 w + 4 g + (l >> 4).
+constexpr int RQ = KD / 16;
+__device__ __forceinline__ int row16(int w, int g) { return w * 8 + g * 4 + (lane_id() >> 4); }
+
+// One bf16 row (row pointer p of a clamped token; tv false selects zeros) in the
+// 16-lane layout; columns >= w read a valid element and are selected to 0, so
+// unrolled loops can issue every load before the first use.
+__device__ __forceinline__ void ld_row16(const __bf16* p, bool tv, int w, float (&x)[RQ]) {
+  const int cl = lane_id() & 15;
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    const int c = cl + 16 * q;
+    x[q] = keep_if(tv && c < w, bf2f(p[c < w ? c : w - 1]));
+  }
+}
+
+__device__ __forceinline__ void l2norm16(float (&x)[RQ]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) ss += x[q] * x[q];
+  const float rs = rsqrtf(row16_sum(ss) + 1e-24f);
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) x[q] *= rs;
+}
+
 __device__ __forceinline__ f4 zero4() { f4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // Split an fp32 value into a bf16 high part and a bf16 residual.

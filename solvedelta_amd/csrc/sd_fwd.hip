@@ -38,33 +38,10 @@ __device__ __forceinline__ void load_row2(const sd_view& v, int b, int t, int h,
   x1 = keep_if(tv && l + 64 < w, a1);
 }
 
-// 16-lane row layout for per-token row work: a wave covers four token rows at
-// once, lane (l & 15) of DPP row (l >> 4) holding columns (l & 15) + 16 q, so a
-// row's reductions are four in-row DPP adds.  A chunk's 64 rows take two such
-// groups per wave: row16(w, g) = 8 w + 4 g + (l >> 4).
-constexpr int RQ = KD / 16;
-__device__ __forceinline__ int row16(int w, int g) { return w * 8 + g * 4 + (lane_id() >> 4); }
-
 // Branch-free 16-lane row load (see load_row2), columns (l & 15) + 16 q.
 __device__ __forceinline__ void load_row16(const sd_view& v, int b, int t, int h, int T, int w,
                                            float (&x)[RQ]) {
-  const int cl = lane_id() & 15;
-  const bool tv = t < T;
-  const __bf16* p = vrow(v, b, tv ? t : T - 1, h);
-#pragma unroll
-  for (int q = 0; q < RQ; ++q) {
-    const int c = cl + 16 * q;
-    x[q] = keep_if(tv && c < w, bf2f(p[c < w ? c : w - 1]));
-  }
-}
-
-__device__ __forceinline__ void l2norm16(float (&x)[RQ]) {
-  float ss = 0.f;
-#pragma unroll
-  for (int q = 0; q < RQ; ++q) ss += x[q] * x[q];
-  const float rs = rsqrtf(row16_sum(ss) + 1e-24f);
-#pragma unroll
-  for (int q = 0; q < RQ; ++q) x[q] *= rs;
+  ld_row16(vrow(v, b, t < T ? t : T - 1, h), t < T, w, x);
 }
 
 constexpr int PS = KD + 8;  // bf16 panel row stride
