@@ -384,19 +384,14 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
   __syncthreads();
 }
 
+// D(16x16) += A(16x16) B(16x16) with lane (g = l >> 4, m = l & 15) holding
+// av[e] = A[m][4g + e] and bv[e] = B[4g + e][m]: four fp32 16x16x4 MFMAs, one per
+// e, each summing over g.  Exact fp32 products and no operand conversions, which
+// keeps these short products off the (busier) vector ALU.
 __device__ __forceinline__ f4 mma16s(const float* av, const float* bv, f4 acc) {
-  bf16x4 ah, al, bh, bl;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    __bf16 h, lo;
-    split_bf(av[e], h, lo);
-    ah[e] = h; al[e] = lo;
-    split_bf(bv[e], h, lo);
-    bh[e] = h; bl[e] = lo;
-  }
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
+  for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[e], acc, 0, 0, 0);
+  return acc;
 }
 
 // (I + L)^{-1} for strictly-lower L (64x64, stride LS), in place -> A.
@@ -542,14 +537,19 @@ __device__ __forceinline__ f4 mma_blks(const BlkS& A, const BlkS& B, f4 acc) {
 //   E2[pi(I,J)][e] = exp(Gx_i - R_J), i = I*16 + (lane>>4)*4 + e, J <= I
 __device__ __forceinline__ int pidx(int I, int J) { return I * (I + 1) / 2 + J; }
 
-struct Tab1 { float E1[NB][4]; };
+struct Tab1 {
+  float E1[NB][4];
+  unsigned wm;  // bit J: this lane's coordinate is wild in block J (read once, not per use)
+};
 struct Tab2 { float E2[10][4]; };
 
 __device__ __forceinline__ void make_tab1(const ChunkDecay& cd, int cb, Tab1& t) {
   const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+  t.wm = 0;
 #pragma unroll
   for (int J = 0; J < NB; ++J) {
     const bool wild = cd.wild[J][c];
+    t.wm |= (wild ? 1u : 0u) << J;
 #pragma unroll
     for (int e = 0; e < 4; ++e) t.E1[J][e] = exp_unless_wild(wild, cd.R[J][c] - cd.G[J * BS + r4 + e][c]);
   }
@@ -584,7 +584,7 @@ __device__ f4 apply_tab(const ChunkDecay& cd, const float* M, const float (&Y)[N
 #pragma unroll
     for (int e = 0; e < 4; ++e) bv[e] = Y[J][e] * t1.E1[J][e];
     const f4 a2 = mma16s(av, bv, zero4());
-    if (cd.wild[J][c]) {
+    if ((t1.wm >> J) & 1u) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
@@ -620,7 +620,7 @@ __device__ f4 apply_t_tab(const ChunkDecay& cd, const float* M, const float (&X)
     acc = mma16s(av, bv, acc);
   }
   f4 res;
-  if (cd.wild[Jb][c]) {
+  if ((t1.wm >> Jb) & 1u) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int j = Jb * BS + r4 + e;
@@ -659,7 +659,7 @@ __device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M
     for (int e = 0; e < 4; ++e) bv[e] = Y[J][e] * t1.E1[J][e];
     const f4 p1 = mma16s(a1, bv, zero4());
     const f4 p2 = mma16s(a2v, bv, zero4());
-    if (cd.wild[J][c]) {
+    if ((t1.wm >> J) & 1u) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
@@ -710,7 +710,7 @@ __device__ void apply_t2_tab(const ChunkDecay& cd, const float* M1, const float 
     acc1 = mma16s(av1, bv1, acc1);
     acc2 = mma16s(av2, bv2, acc2);
   }
-  if (cd.wild[Jb][c]) {
+  if ((t1.wm >> Jb) & 1u) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int j = Jb * BS + r4 + e;
