@@ -166,10 +166,8 @@ __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
         split_bf(bv[ks][e], h, lo);
         bh[e] = h; bl[e] = lo;
       }
-#ifndef SD_EXPERIMENT_ONE_TERM
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
-#endif
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
     }
   }

@@ -162,11 +162,21 @@ constexpr int STILES = KD / SCOLS;
 // faster on the forward passes and push the reverse passes past 512 registers.
 constexpr int PF = 3;
 
+// fp32 staging row stride: 16-byte aligned rows, and the four 16-lane groups of
+// an MFMA output tile (rows 4 apart) land on distinct LDS banks.
+constexpr int XFS = SCOLS + 4;
+
 struct StateSmem {
   __bf16 Xh[SCOLS][KD + 8];  // X0 tile, transposed [col][row], split hi / lo
   __bf16 Xl[SCOLS][KD + 8];
   __bf16 wh[SCOLS][BT + 8];  // w tile, transposed [col][token], split hi / lo
   __bf16 wl[SCOLS][BT + 8];
+  // fp32 copies of the X0 slot and the w tile, row-major, written back to global
+  // memory as 16-byte pieces: a wave may hold at most 63 memory operations in
+  // flight, and the prefetch ring needs that budget more than scalar stores do.
+  float Xf[KD][XFS];
+  float wf[BT][XFS];
+  float Uf[BT][XFS];  // U tile, staged from one 16-byte load per thread
 };
 
 template <bool INJ>
@@ -175,7 +185,7 @@ struct StateFrags {
   Frag K[SRB][2];
   Frag A1[INJ ? SRB : 1][2];
   Frag B1[INJ ? HALVES : 1][2];
-  float U[HALVES][4];
+  float4 U4;  // U tile piece: token threadIdx / (SCOLS / 4), columns 4 (threadIdx % (SCOLS / 4))
   float4 gam[SRB];
 };
 
@@ -203,11 +213,11 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
       f.K[q][ks] = ldfrag(p.Kt, cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
-#pragma unroll
-  for (int h = 0; h < HALVES; ++h)
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      f.U[h][e] = p.U[(rowbase + tb * 16 + (l >> 4) * 4 + e) * KD + tile * SCOLS + h * 16 + m];
+  {
+    constexpr int C4 = SCOLS / 4;
+    static_assert(BT * C4 == STHREADS, "one U piece per thread");
+    f.U4 = ld4(p.U + (rowbase + threadIdx.x / C4) * KD + tile * SCOLS + (threadIdx.x % C4) * 4);
+  }
 #pragma unroll
   for (int q = 0; q < SRB; ++q) f.gam[q] = ld4(p.Gam + cidx * KD + (SRB * w + q) * 16 + (l >> 4) * 4);
   if constexpr (INJ) {
@@ -254,17 +264,29 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
 #pragma unroll
     for (int h = 0; h < HALVES; ++h) {
       const int row0 = (SRB * w + q) * 16 + r4, col = tile * SCOLS + h * 16 + m;
-      if (p.Xs)
-        for (int e = 0; e < 4; ++e) p.Xs[sidx * KD * KD + (long long)(row0 + e) * KD + col] = X[q][h][e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s.Xf[row0 + e][h * 16 + m] = X[q][h][e];
       stage_split4(&s.Xh[h * 16 + m][row0], &s.Xl[h * 16 + m][row0], X[q][h]);
     }
+  *reinterpret_cast<float4*>(&s.Uf[threadIdx.x / (SCOLS / 4)][(threadIdx.x % (SCOLS / 4)) * 4]) = cur.U4;
   __syncthreads();
+  if (p.Xs) {  // slot write-back: 128 rows x SCOLS columns as float4 pieces
+    constexpr int C4 = SCOLS / 4;
+#pragma unroll
+    for (int j = 0; j < KD * C4 / STHREADS; ++j) {
+      const int idx = threadIdx.x + j * STHREADS, row = idx / C4, c4 = idx % C4;
+      *reinterpret_cast<float4*>(p.Xs + sidx * KD * KD + (long long)row * KD + tile * SCOLS + c4 * 4) =
+          *reinterpret_cast<const float4*>(&s.Xf[row][c4 * 4]);
+    }
+  }
   // w = U + Wneg X0 (token block tb, each half).  The work that does not depend
   // on this chunk's w -- Gamma X (+ At1 B1) -- is issued alongside so the
   // independent MFMA chains overlap.
   f4 acc[HALVES];
 #pragma unroll
-  for (int h = 0; h < HALVES; ++h) acc[h] = {cur.U[h][0], cur.U[h][1], cur.U[h][2], cur.U[h][3]};
+  for (int h = 0; h < HALVES; ++h)
+    acc[h] = {s.Uf[tb * 16 + r4][h * 16 + m], s.Uf[tb * 16 + r4 + 1][h * 16 + m],
+              s.Uf[tb * 16 + r4 + 2][h * 16 + m], s.Uf[tb * 16 + r4 + 3][h * 16 + m]};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -288,11 +310,18 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
   }
 #pragma unroll
   for (int h = 0; h < HALVES; ++h) {
-    const int gcol = tile * SCOLS + h * 16 + m;
-    for (int e = 0; e < 4; ++e) p.wout[(rowbase + tb * 16 + r4 + e) * KD + gcol] = acc[h][e];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s.wf[tb * 16 + r4 + e][h * 16 + m] = acc[h][e];
     stage_split4(&s.wh[h * 16 + m][tb * 16 + r4], &s.wl[h * 16 + m][tb * 16 + r4], acc[h]);
   }
   __syncthreads();
+  {  // w write-back: 64 tokens x SCOLS columns as float4 pieces
+    constexpr int C4 = SCOLS / 4;
+    static_assert(BT * C4 == STHREADS, "one w piece per thread");
+    const int tok = threadIdx.x / C4, c4 = threadIdx.x % C4;
+    *reinterpret_cast<float4*>(p.wout + (rowbase + tok) * KD + tile * SCOLS + c4 * 4) =
+        *reinterpret_cast<const float4*>(&s.wf[tok][c4 * 4]);
+  }
   // X += Kt w: the recurrence's critical path
 #pragma unroll
   for (int h = 0; h < HALVES; ++h) {
