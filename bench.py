@@ -82,9 +82,10 @@ BYTES_PER_CHUNK = {
 # profiles/fwd_bwd_B4_T2048_H8_d128_hbm_traffic.txt.  Static figures: a kernel
 # change needs a new counter run.
 TRAFFIC_MB = {
-    "k_prep_c": 186.0, "state_c_fwd": 206.2, "k_prep_s": 535.9, "state_s_fwd": 273.5,
-    "k_bprep_s": 396.2, "state_s_bwd": 271.3, "state_c_bwd": 271.3, "k_grad_s": 962.7,
-    "k_src_bwd": 436.3, "k_bprep_c": 453.8, "k_grad_c": 1058.8, "k_final": 403.6,
+    "k_prep_c": 185.9, "state_c_fwd": 207.1, "k_prep_s": 524.0, "state_s_fwd": 207.1,
+    "k_out_s": 163.7, "k_bprep_s": 396.3, "state_s_bwd": 271.3, "state_c_bwd": 271.3,
+    "k_grad_s": 705.4, "k_src_bwd": 436.3, "k_bprep_c": 453.6, "k_grad_c": 939.4,
+    "k_final": 403.6,
 }
 
 
