@@ -223,37 +223,47 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   }
 }
 
+// Lambda-block load for the key product, fused with the decay closure's row
+// sums: wave cb loads rows cb*16 .. cb*16+15 of lambda (split for the MFMA) and
+// the same elements of X_C, and leaves rowsum_c(X_C (.) lambda) partials (one
+// per 32-column lane group) in rsum[g][c], so the closure need not read either
+// 64 KiB block again.
+__device__ __forceinline__ void load_lam_rowsum(const float* lam, const float* XC, int cb, BlkS& BL,
+                                                float (*rsum)[KD]) {
+  Blk rl, rx;
+  load_blk(rl, lam + cb * 16 * KD, KD);
+  load_blk(rx, XC + cb * 16 * KD, KD);
+  float acc = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      acc += rl.v[ks][h].x * rx.v[ks][h].x + rl.v[ks][h].y * rx.v[ks][h].y +
+             rl.v[ks][h].z * rx.v[ks][h].z + rl.v[ks][h].w * rx.v[ks][h].w;
+  const int l = lane_id();
+  rsum[l >> 4][cb * 16 + (l & 15)] = acc;
+  split_blk(rl, BL);
+}
+
 // Decay-gradient closure for one chunk (all 512 threads): rowsum(X_C (.) lambda)
-// per coordinate plus the in-chunk reverse cumulative sum of the un-summed decay
-// cotangent in dg (+ the one-row shift of `shift`), written back to dg.
-// Thread (part, c): c = tid & 127 owns a coordinate, part = tid >> 7 a quarter
-// of the rows / value columns; every load is issued before the first sum.
-__device__ void close_decay_gradient(const float* XC, const float* lam, float* dg, const float* shift,
+// per coordinate (from the partials load_lam_rowsum left in rsum) plus the
+// in-chunk reverse cumulative sum of the un-summed decay cotangent in dg (+ the
+// one-row shift of `shift`), written back to dg.  Thread (part, c): c = tid & 127
+// owns a coordinate, part = tid >> 7 a quarter of the rows; every load is issued
+// before the first sum.
+__device__ void close_decay_gradient(const float (*rsum)[KD], float* dg, const float* shift,
                                      float (*red)[KD]) {
   const int c = threadIdx.x & (KD - 1), part = threadIdx.x >> 7;
-  float4 xv[8], lv[8];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    xv[q] = ld4g(XC + c * KD + part * 32 + q * 4);
-    lv[q] = ld4g(lam + c * KD + part * 32 + q * 4);
-  }
   float col[16];
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int i = part * 16 + q;
     col[q] = dg[i * KD + c] + ((shift && i + 1 < BT) ? shift[(i + 1) * KD + c] : 0.f);
   }
-  float rs = 0.f;
-#pragma unroll
-  for (int q = 0; q < 8; ++q)
-    rs += xv[q].x * lv[q].x + xv[q].y * lv[q].y + xv[q].z * lv[q].z + xv[q].w * lv[q].w;
+  const float rowsum = rsum[0][c] + rsum[1][c] + rsum[2][c] + rsum[3][c];
   float blk = 0.f;
 #pragma unroll
   for (int q = 0; q < 16; ++q) blk += col[q];
-  red[part][c] = rs;
-  __syncthreads();
-  const float rowsum = red[0][c] + red[1][c] + red[2][c] + red[3][c];
-  __syncthreads();
   red[part][c] = blk;
   __syncthreads();
   float acc = rowsum;  // carry from the later row quarters
@@ -270,6 +280,7 @@ struct GradSmem {
   float M1[BT * LS];
   float M2[BT * LS];
   float red[4][KD];
+  float rsum[4][KD];  // rowsum(X_C (.) lambda) partials
   LPanel PA;  // dw, then dO
   LPanel PW;  // w
 };
@@ -316,7 +327,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   lds_pair(&s.PA, nullptr, s.PW, s.M2, false);
   {
     BlkS BL;
-    load_split_blk_g(lam + cb * 16 * KD, BL);
+    load_lam_rowsum(lam, XC, cb, BL, s.rsum);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       BlkS A;
@@ -413,7 +424,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   }
   SD_MARK(7, 6);
   __syncthreads();
-  close_decay_gradient(XC, lam, dg, nullptr, s.red);
+  close_decay_gradient(s.rsum, dg, nullptr, s.red);
   SD_MARK(7, 7);
 }
 
@@ -611,6 +622,7 @@ struct GradCSmem {
   float M2[BT * LS];
   float gam[BT];
   float red[4][KD];
+  float rsum[4][KD];  // rowsum(X_C (.) lambda) partials
   LPanel PA;  // dw, then dd e^G
   LPanel PW;  // delta
 };
@@ -654,7 +666,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   {
     BlkS BX, BL;
     load_split_blk_g(X0 + cb * 16 * KD, BX);
-    load_split_blk_g(lam + cb * 16 * KD, BL);
+    load_lam_rowsum(lam, XC, cb, BL, s.rsum);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       BlkS A;
@@ -756,7 +768,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   }
   __syncthreads();
   SD_MARK(3, 8);
-  close_decay_gradient(XC, lam, dg, p.g.xdx + rowbase * KD, s.red);
+  close_decay_gradient(s.rsum, dg, p.g.xdx + rowbase * KD, s.red);
   SD_MARK(3, 9);
 }
 
