@@ -245,33 +245,32 @@ __device__ __forceinline__ void load_lam_rowsum(const float* lam, const float* X
   split_blk(rl, BL);
 }
 
-// Decay-gradient closure for one chunk (all 512 threads): rowsum(X_C (.) lambda)
-// per coordinate (from the partials load_lam_rowsum left in rsum) plus the
-// in-chunk reverse cumulative sum of the un-summed decay cotangent in dg (+ the
-// one-row shift of `shift`), written back to dg.  Thread (part, c): c = tid & 127
-// owns a coordinate, part = tid >> 7 a quarter of the rows; every load is issued
-// before the first sum.
-__device__ void close_decay_gradient(const float (*rsum)[KD], float* dg, const float* shift,
-                                     float (*red)[KD]) {
-  const int c = threadIdx.x & (KD - 1), part = threadIdx.x >> 7;
-  float col[16];
+// Decay-gradient closure for this wave's 16 columns, in registers: v holds the
+// un-summed decay cotangent of column c = cb*16 + (l & 15) at rows
+// 16 I + 4 (l >> 4) + e; it becomes the reverse cumulative sum over the chunk's
+// rows plus rowsum_c(X_C (.) lambda) (from the partials load_lam_rowsum left in
+// rsum).  The four lane groups exchange their block sums with shuffles.
+__device__ __forceinline__ void close_decay_column(float (&v)[NB][4], const float (*rsum)[KD], int cb) {
+  const int l = lane_id(), g = l >> 4, c = cb * 16 + (l & 15);
+  float later[NB], tot[NB];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int i = part * 16 + q;
-    col[q] = dg[i * KD + c] + ((shift && i + 1 < BT) ? shift[(i + 1) * KD + c] : 0.f);
+  for (int I = 0; I < NB; ++I) {
+    const float t = v[I][0] + v[I][1] + v[I][2] + v[I][3];
+    const float s1 = __shfl(t, (l + 16) & 63), s2 = __shfl(t, (l + 32) & 63),
+                s3 = __shfl(t, (l + 48) & 63);
+    later[I] = keep_if(g < 3, s1) + keep_if(g < 2, s2) + keep_if(g < 1, s3);  // groups after g
+    tot[I] = (t + s1) + (s2 + s3);
   }
-  const float rowsum = rsum[0][c] + rsum[1][c] + rsum[2][c] + rsum[3][c];
-  float blk = 0.f;
+  float acc = rsum[0][c] + rsum[1][c] + rsum[2][c] + rsum[3][c];  // carry from later blocks
 #pragma unroll
-  for (int q = 0; q < 16; ++q) blk += col[q];
-  red[part][c] = blk;
-  __syncthreads();
-  float acc = rowsum;  // carry from the later row quarters
-  for (int pp = part + 1; pp < 4; ++pp) acc += red[pp][c];
+  for (int I = NB - 1; I >= 0; --I) {
+    float run = acc + later[I];
 #pragma unroll
-  for (int q = 15; q >= 0; --q) {
-    acc += col[q];
-    dg[(part * 16 + q) * KD + c] = acc;
+    for (int e = 3; e >= 0; --e) {
+      run += v[I][e];
+      v[I][e] = run;
+    }
+    acc += tot[I];
   }
 }
 
@@ -279,7 +278,6 @@ struct GradSmem {
   ChunkDecay cd;
   float M1[BT * LS];
   float M2[BT * LS];
-  float red[4][KD];
   float rsum[4][KD];  // rowsum(X_C (.) lambda) partials
   LPanel PA;  // dw, then dO
   LPanel PW;  // w
@@ -413,6 +411,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
         pdg[I][e] -= Sd[I][e] * ddv;
       }
     }
+    close_decay_column(pdg, s.rsum, cb);
 #pragma unroll
     for (int I = 0; I < NB; ++I)
 #pragma unroll
@@ -423,9 +422,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
       }
   }
   SD_MARK(7, 6);
-  __syncthreads();
-  close_decay_gradient(s.rsum, dg, nullptr, s.red);
-  SD_MARK(7, 7);
 }
 
 // ---------------------------------------------------------------------------
@@ -621,7 +617,6 @@ struct GradCSmem {
   float M1[BT * LS];
   float M2[BT * LS];
   float gam[BT];
-  float red[4][KD];
   float rsum[4][KD];  // rowsum(X_C (.) lambda) partials
   LPanel PA;  // dw, then dd e^G
   LPanel PW;  // delta
@@ -711,7 +706,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   // chunk-uniform output bases, 32-bit lane offsets (keeps addresses out of VGPR pairs)
   float* const dx_b = p.g.dxC + rowbase * KD;
   float* const dk_b = p.g.dkC + rowbase * KD;
-  float* const xdx_b = p.g.xdx + rowbase * KD;
+  // decay cotangent: dg_i = o_i dd_i - u_i dk_i plus the shifted gamma u (.) dx
+  // term, closed in registers below (v = dg + xdx, then dg = suffix(v) - xdx)
+  float vv[NB][4], xs[NB][4];
 #pragma unroll
   for (int I = 0; I < NB; ++I) {
     const f4 ap = apply_tab<true>(cd, s.M1, Su, I, cb, t1, tx, U);
@@ -725,10 +722,16 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       const unsigned o = (unsigned)(i * KD + c);
       dx_b[o] = dx;
       dk_b[o] = dk;
-      dg[o] = So[I][e] * Sdd[I][e] - Su[I][e] * dk;
-      xdx_b[o] = Sx[I][e] * dx;
+      xs[I][e] = Sx[I][e] * dx;
+      vv[I][e] = So[I][e] * Sdd[I][e] - Su[I][e] * dk + xs[I][e];
     }
   }
+  // dg_i = rowsum + sum_{i' >= i} dg_i' + sum_{i' > i} xdx_i'
+  close_decay_column(vv, s.rsum, cb);
+#pragma unroll
+  for (int I = 0; I < NB; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dg[(unsigned)((I * BS + r4 + e) * KD + c)] = vv[I][e] - xs[I][e];
   SD_MARK(3, 6);
   __syncthreads();  // M1 free: P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) into M1
   decayed_gram<false>(
@@ -766,10 +769,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       for (int e = 0; e < 4; ++e) dq_b[(unsigned)((I * BS + r4 + e) * KD + c)] = dq[e];
     }
   }
-  __syncthreads();
   SD_MARK(3, 8);
-  close_decay_gradient(s.rsum, dg, p.g.xdx + rowbase * KD, s.red);
-  SD_MARK(3, 9);
 }
 
 // ---------------------------------------------------------------------------

@@ -124,7 +124,7 @@ struct BwdWs {
   float* de; float* dchi; float* dd; float* dgS;
   float* ddelta; float* du_src; float* dk_src;
   float* dkC; float* dxC; float* dqC; float* dgC;
-  float* uh; float* xdx;  // normalised u, and gamma u (.) dx for the decay closure
+  float* uh;  // normalised u
 };
 
 int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void* dout,
