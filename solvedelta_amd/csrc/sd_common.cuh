@@ -18,16 +18,28 @@
 #include <stdint.h>
 
 // Compile-time section timer for kernel tuning (off unless SD_SECTION_TIMING is
-// defined): workgroup (0,0) thread 0 records s_memrealtime at marks 0..31.
+// defined): workgroup (0, SD_MARK_Y) thread 0 records s_memrealtime at marks 0..31.
 #ifdef SD_SECTION_TIMING
+#ifndef SD_MARK_Y
+#define SD_MARK_Y 0  // workgroup row whose chunk 0 is timed
+#endif
 static __device__ unsigned long long sd_section_ticks[8][32];
 #define SD_MARK(slot, idx)                                                              \
   do {                                                                                  \
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)                         \
+    if (blockIdx.x == 0 && blockIdx.y == SD_MARK_Y && threadIdx.x == 0)                 \
       sd_section_ticks[slot][idx] = __builtin_amdgcn_s_memrealtime();                   \
+  } while (0)
+// Per-workgroup start / end ticks of one kernel (tuning builds only).
+static __device__ unsigned long long sd_wg_ticks[2][4096];
+#define SD_WG_TRACE(end)                                                                \
+  do {                                                                                  \
+    if (threadIdx.x == 0)                                                               \
+      sd_wg_ticks[end][(blockIdx.y * gridDim.x + blockIdx.x) & 4095] =                  \
+          __builtin_amdgcn_s_memrealtime();                                             \
   } while (0)
 #else
 #define SD_MARK(slot, idx) do { } while (0)
+#define SD_WG_TRACE(end) do { } while (0)
 #endif
 
 namespace sd {

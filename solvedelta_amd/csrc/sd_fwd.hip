@@ -434,6 +434,7 @@ struct PrepSSmem {
 __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepSSmem& s = *reinterpret_cast<PrepSSmem*>(smem_raw);
+  SD_WG_TRACE(0);
   const int ch = blockIdx.x, n = blockIdx.y;
   const int b = n / p.H, hh = n % p.H, t0 = ch * BT;
   const int T = p.T, r = p.r, V = p.V;
@@ -656,6 +657,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   __syncthreads();
   store_frag_panel<BT, KD>(p.Ws.hi, p.Ws.lo, rowbase * KD, [&](int i, int c) { return s.Pc[i][c]; });
   SD_MARK(2, 9);
+  SD_WG_TRACE(1);
 }
 
 size_t prep_c_smem() { return sizeof(PrepCSmem); }
