@@ -50,7 +50,36 @@ __device__ __forceinline__ DoutRaw dout_raw(const BwdParams& p, int b, int t, in
 }
 __device__ __forceinline__ float dout_val(DoutRaw r) { return keep_if(r.ok, bf2f(r.x)); }
 
-// Branch-free row load (see load_row2 in the forward kernels).
+// Stages the chunk's output cotangent (bf16, read in place; padded tokens and
+// columns read 0) as a split LDS panel.  All CT threads; every load is issued
+// before the first split.
+__device__ __forceinline__ void stage_dout_panel(LPanel& P, const BwdParams& p, int b, int t0, int hh) {
+  constexpr int PER = BT * KD / 4 / CT;  // 4-column groups per thread
+  DoutRaw d[PER][4];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d[q][e] = dout_raw(p, b, t0 + i, hh, c + e);
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
+    bf16x4 hh4, ll4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      __bf16 a, b2;
+      split_bf(dout_val(d[q][e]), a, b2);
+      hh4[e] = a;
+      ll4[e] = b2;
+    }
+    *reinterpret_cast<bf16x4*>(&P.h[i][c]) = hh4;
+    *reinterpret_cast<bf16x4*>(&P.l[i][c]) = ll4;
+  }
+}
+
+// Branch-free row load: out-of-range tokens and coordinates read a valid element
+// and are selected to 0 (a guarded load would branch and wait).
 __device__ __forceinline__ void ldrow2(const sd_view& v, int b, int t, int h, int T, int w,
                                        float& x0, float& x1) {
   const int l = lane_id();
@@ -160,22 +189,6 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
     __syncthreads();
     store_frag_panel<BT, KD>(p.g.Wk.hi, p.g.Wk.lo, rowbase * KD,
                              [&](int i, int c) { return Wst[i * KD + c]; });
-  }
-  // elementwise panels: every load of the thread's 16 elements is issued before
-  // the first store (a store between loads would keep later loads behind it)
-  constexpr int PER = BT * KD / CT;
-  {
-    DoutRaw d[PER];
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int idx = threadIdx.x + q * CT, i = idx / KD, c = idx % KD;
-      d[q] = dout_raw(p, b, t0 + i, hh, c);
-    }
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int idx = threadIdx.x + q * CT, i = idx / KD, c = idx % KD;
-      p.g.B1[(rowbase + i) * KD + c] = dout_val(d[q]);
-    }
   }
   {  // chunk-transposed panels, fragment order: a thread's two pieces are
      // (state row c, tokens i0 .. i0+7); all their loads are issued first
@@ -294,7 +307,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const float* dd_ = p.f.d + rowbase * KD;
   const float* ee = p.f.e + rowbase * KD;
   const float* chi = p.f.chi + rowbase * KD;
-  const float* dO = p.g.B1 + rowbase * KD;  // fp32 copy of the output cotangent
   const float* X0 = p.f.Xs + sidx * KD * KD;
   const float* XC = X0 + KD * KD;
   const float* lam = p.g.Ls + sidx * KD * KD;
@@ -319,7 +331,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   }
   SD_MARK(7, 2);
   __syncthreads();  // PA free
-  stage_panel(s.PA, dO);
+  stage_dout_panel(s.PA, p, b, t0, hh);
   __syncthreads();
   // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T;  kl = w lam^T
   lds_pair(&s.PA, nullptr, s.PW, s.M2, false);
