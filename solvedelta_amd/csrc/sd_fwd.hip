@@ -533,9 +533,11 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   // sources (16-lane row layout; e overwrites u, chi overwrites k).  Both row
   // groups' delta, q and erase are loaded before the first row is processed:
   // the rows' global stores would otherwise hold the next rows' loads behind them.
+  constexpr int RPW = BT / CW;
+  float zz[RPW][2];
   {
     const int cl = l & 15;
-    float dq_[2][RQ], qq_[2][RQ], er_[2][RQ];
+    float dq_[2][RQ], qq_[2][RQ], er_[2][RQ], vx[RPW][2], wx[RPW][2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g), t = t0 + i;
@@ -543,6 +545,11 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       for (int q = 0; q < RQ; ++q) dq_[g][q] = delta[i * KD + cl + 16 * q];
       load_row16(in.q, b, t, hh, T, r, qq_[g]);
       load_row16(in.erase_raw, b, t, hh, T, r, er_[g]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      load_row2(in.v, b, t0 + w + rr * CW, hh, T, V, vx[rr][0], vx[rr][1]);
+      load_row2(in.write_raw, b, t0 + w + rr * CW, hh, T, V, wx[rr][0], wx[rr][1]);
     }
     SD_MARK(2, 10);
     float* const e_b = p.e + rowbase * KD;
@@ -590,6 +597,11 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
         chi_b[i * KD + c] = xv;
       }
     }
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      zz[rr][0] = vx[rr][0] / (1.f + __expf(-wx[rr][0]));
+      zz[rr][1] = vx[rr][1] / (1.f + __expf(-wx[rr][1]));
+    }
   }
   SD_MARK(2, 12);
   __syncthreads();
@@ -621,20 +633,10 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     const int i = idx / KD, c = idx % KD;
     s.Pa[i][c] *= __expf(cd.G[i][c]);
   }
-{
-    constexpr int RPW = BT / CW;
-    float vx[RPW][2], wx[RPW][2];
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      load_row2(in.v, b, t0 + w + rr * CW, hh, T, V, vx[rr][0], vx[rr][1]);
-      load_row2(in.write_raw, b, t0 + w + rr * CW, hh, T, V, wx[rr][0], wx[rr][1]);
-    }
-#pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const int i = w + rr * CW;
-      s.Pb[i][l] = vx[rr][0] / (1.f + __expf(-wx[rr][0]));
-      s.Pb[i][l + 64] = vx[rr][1] / (1.f + __expf(-wx[rr][1]));
-    }
+  for (int rr = 0; rr < RPW; ++rr) {
+    s.Pb[w + rr * CW][l] = zz[rr][0];
+    s.Pb[w + rr * CW][l + 64] = zz[rr][1];
   }
   __syncthreads();
   // W = A (e e^G), U = A z

@@ -35,6 +35,7 @@ def _check(out, st, eo, es, tag, frob=1e-2):
     (1, 256, 1, 128, 128, 5, "softplus", True),
     (1, 19, 2, 16, 16, 6, "small", True),
     (1, 1, 2, 16, 16, 7, "small", True),
+    (1, 70, 2, 20, 12, 8, "softplus", True),   # widths not a multiple of 8: element-wise row loads
 ])
 def test_forward_matches_oracle(B, T, H, r, V, seed, decay, with_state):
     args = make_inputs(B, T, H, r, V, seed=seed, decay=decay)
