@@ -428,7 +428,10 @@ struct PrepSSmem {
   float M[BT * LS];
   float Pa[BT][GS];
   float Pb[BT][GS];
-  float Pc[BT][GS];
+  union {
+    float Pc[BT][GS];
+    LPanel Kp;  // the keys split once (bf16 hi + lo) for the M Gram and X0 k, before d is formed
+  };
 };
 
 __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
@@ -472,13 +475,34 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long cidx = (long long)n * p.NT + ch;
   const float* delta = p.delta + rowbase * KD;
+  {  // keys split once into a shared panel (every wave would otherwise split all of them)
+    constexpr int PER = BT * KD / 4 / CT;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
+      const float4 v = *reinterpret_cast<const float4*>(&s.Pb[i][c]);
+      const float x[4] = {v.x, v.y, v.z, v.w};
+      bf16x4 hh4, ll4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        __bf16 a, b2;
+        split_bf(x[e], a, b2);
+        hh4[e] = a;
+        ll4[e] = b2;
+      }
+      *reinterpret_cast<bf16x4*>(&s.Kp.h[i][c]) = hh4;
+      *reinterpret_cast<bf16x4*>(&s.Kp.l[i][c]) = ll4;
+    }
+  }
+  __syncthreads();
   // M_ij = k_i . delta_j  (j <= i)
   for (int pp = w; pp < 10; pp += CW) {
     int I = 0, J = pp;
     while (J > I) { J -= I + 1; ++I; }
-    f4 acc = mma_k32([&](int m, int c) { return s.Pb[I * BS + m][c]; },
-                     [&](int c, int nn) { return delta[(long long)(J * BS + nn) * KD + c]; }, KD,
-                     zero4());
+    BlkS A, D;
+    load_split_blk_g(delta + J * BS * KD, D);
+    lblk(s.Kp, I * BS, A);
+    const f4 acc = mma_blks(A, D, zero4());
     for (int e = 0; e < 4; ++e) {
       const int i = I * BS + out_row(e), j = J * BS + out_col();
       s.M[i * LS + j] = j <= i ? acc[e] : 0.f;
@@ -506,23 +530,21 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     make_tab1(cd, cb, t1);
     make_tab2<false>(cd, cb, t2);
     auto Uw = [&](int j, int cc) { return s.Pa[j][cc]; };
+    f4 a1[NB];  // X0 k for this wave's column block, from the shared split keys
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
-      Blk raw;
-      const int m = l & 15, kq = (l >> 4) * 8;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        raw.v[ks][0] = *reinterpret_cast<const float4*>(&s.Pb[I * BS + m][ks * 32 + kq]);
-        raw.v[ks][1] = *reinterpret_cast<const float4*>(&s.Pb[I * BS + m][ks * 32 + kq + 4]);
-      }
       BlkS A;
-      split_blk(raw, A);
-      const f4 a1 = mma_blks(A, BX, zero4());
+      lblk(s.Kp, I * BS, A);
+      a1[I] = mma_blks(A, BX, zero4());
+    }
+    __syncthreads();  // the split keys are dead: d is formed in their place
+#pragma unroll
+    for (int I = 0; I < NB; ++I) {
       const f4 ap = apply_tab<false>(cd, s.M, Su, I, cb, t1, t2, Uw);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
-        const float dv = s.Pb[i][c] + __expf(cd.G[i][c]) * a1[e] + ap[e];
+        const float dv = s.Pb[i][c] + __expf(cd.G[i][c]) * a1[I][e] + ap[e];
         p.d[(rowbase + i) * KD + c] = dv;
         s.Pc[i][c] = dv;
       }
