@@ -127,12 +127,27 @@ __device__ void mat64_mul(const float* P, const float* A, float* N) {
 // ---------------------------------------------------------------------------
 // S memory
 // ---------------------------------------------------------------------------
+// A 64 x 64 operand split into bf16 hi / lo, row-major with K contiguous.
+constexpr int SPS = BT + 8;  // row stride (bf16 elements), keeps 16-byte alignment
+struct SPanel64 {
+  __bf16 h[BT][SPS];
+  __bf16 l[BT][SPS];
+};
+
 struct BprepSSmem {
   ChunkDecay cd;
   float A[BT * LS];
   float P[BT * LS];  // P and N are contiguous: reused as a 64 x 128 staging panel
   float N[BT * LS];
+  SPanel64 At, Nt;   // A^T and N^T split once: the MFMA A operands of Wk and dU
 };
+
+__device__ __forceinline__ Frag ldfrag_g(const SP& sp, long long off) {
+  Frag f;
+  f.h = *reinterpret_cast<const bf16x8*>(sp.hi + off);
+  f.l = *reinterpret_cast<const bf16x8*>(sp.lo + off);
+  return f;
+}
 static_assert(2 * BT * LS >= BT * KD, "P + N hold a 64 x 128 panel");
 
 __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
@@ -162,21 +177,59 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   __syncthreads();
   mat64_mul(s.P, s.A, s.N);
   __syncthreads();
-  const int w = wave_id();
+  {  // A^T, N^T split once (each wave would otherwise split all of them)
+    constexpr int PER = BT * BT / CT;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = threadIdx.x + q * CT, j = idx / BT, k = idx % BT;
+      __bf16 a, b2;
+      split_bf(s.A[k * LS + j], a, b2);
+      s.At.h[j][k] = a;
+      s.At.l[j][k] = b2;
+      split_bf(s.N[k * LS + j], a, b2);
+      s.Nt.h[j][k] = a;
+      s.Nt.l[j][k] = b2;
+    }
+  }
+  __syncthreads();
+  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
   const long long kbase = cidx * KD * BT;
   f4 wks[NB], dus[NB];
-  for (int cb = w; cb < w + 1; ++cb)
+  {
+    const int cb = w;
+    // B operands, shared by the four output blocks: dO (exact in bf16, so its
+    // split has no low part) gathered over the chunk's tokens, and the stored
+    // split key panel K^ read as ready-made fragments.
+    bf16x8 db[2];
+    Frag kf[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      DoutRaw r[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = dout_raw(p, b, t0 + ks * 32 + kq + e, hh, cb * 16 + m);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) db[ks][e] = (__bf16)dout_val(r[e]);
+      kf[ks] = ldfrag_g(p.f.Ks, kbase + frag_off(cb * 16 + m, ks * 32 + kq, BT));
+    }
+#pragma unroll
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_l N_lj dO_l ;  Wk_j = sum_i A_ij K^_i
-      f4 du = mma_k32_lx([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; }, XId(),
-                         [&](int k, int nn) { return dout_raw(p, b, t0 + k, hh, cb * 16 + nn); },
-                         [](int, int, DoutRaw r) { return dout_val(r); }, BT, zero4());
-      f4 wk = mma_k32_lx([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; }, XId(),
-                         [&](int k, int nn) { return sp_raw(p.f.Ks, kbase + frag_off(cb * 16 + nn, k, BT)); },
-                         [](int, int, SPRaw r) { return sp_val(r); }, BT, zero4());
+      f4 du = zero4(), wk = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 nh = *reinterpret_cast<const bf16x8*>(&s.Nt.h[Jb * BS + m][ks * 32 + kq]);
+        const bf16x8 nl = *reinterpret_cast<const bf16x8*>(&s.Nt.l[Jb * BS + m][ks * 32 + kq]);
+        du = __builtin_amdgcn_mfma_f32_16x16x32_bf16(nl, db[ks], du, 0, 0, 0);
+        du = __builtin_amdgcn_mfma_f32_16x16x32_bf16(nh, db[ks], du, 0, 0, 0);
+        Frag af;
+        af.h = *reinterpret_cast<const bf16x8*>(&s.At.h[Jb * BS + m][ks * 32 + kq]);
+        af.l = *reinterpret_cast<const bf16x8*>(&s.At.l[Jb * BS + m][ks * 32 + kq]);
+        wk = mma3f(af, kf[ks], wk);
+      }
       dus[Jb] = du;
       wks[Jb] = wk;
     }
+  }
   store_du_slab(p.g.dU + rowbase * KD, dus);
   // Wk staged in the free P / N rows, then stored in fragment order
   __syncthreads();
