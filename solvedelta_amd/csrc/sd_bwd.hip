@@ -134,6 +134,19 @@ struct SPanel64 {
   __bf16 l[BT][SPS];
 };
 
+// Eight fp32 values (one lane's K slice of an MFMA operand) split into bf16 hi / lo.
+__device__ __forceinline__ Frag split8(const float (&v)[8]) {
+  Frag f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    __bf16 a, b2;
+    split_bf(v[e], a, b2);
+    f.h[e] = a;
+    f.l[e] = b2;
+  }
+  return f;
+}
+
 struct BprepSSmem {
   ChunkDecay cd;
   float A[BT * LS];
@@ -637,19 +650,48 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   const float* ddl = p.g.ddelta + rowbase * KD;
   const long long kbase = cidx * KD * BT;
   f4 wks[NB], dus[NB];
-  for (int cb = w; cb < w + 1; ++cb)
+  {
+    const int cb = w, m = l & 15, kq = (l >> 4) * 8;
+    // B operands, shared by the four output blocks: ddelta (global) and the
+    // normalised keys (LDS) split once, the stored split key panel K^ read as
+    // ready-made fragments.
+    Frag bd[2], bk[2], kf[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float vd[8], vk[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vd[e] = ddl[(ks * 32 + kq + e) * KD + cb * 16 + m];
+        vk[e] = s.Kh[ks * 32 + kq + e][cb * 16 + m];
+      }
+      bd[ks] = split8(vd);
+      bk[ks] = split8(vk);
+      kf[ks] = ldfrag_g(p.f.Kc, kbase + frag_off(cb * 16 + m, ks * 32 + kq, BT));
+    }
+#pragma unroll
     for (int Jb = 0; Jb < NB; ++Jb) {
       // dU_j = sum_i A_ij ddelta_i + sum_l N_lj k_l ;  Wk_j = sum_i A_ij K^_i
-      f4 du = mma_k32([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; },
-                      [&](int k, int nn) { return ddl[k * KD + cb * 16 + nn]; }, BT, zero4());
-      du = mma_k32([&](int m, int k) { return s.N[k * LS + Jb * BS + m]; },
-                   [&](int k, int nn) { return s.Kh[k][cb * 16 + nn]; }, BT, du);
-      f4 wk = mma_k32_lx([&](int m, int k) { return s.A[k * LS + Jb * BS + m]; }, XId(),
-                         [&](int k, int nn) { return sp_raw(p.f.Kc, kbase + frag_off(cb * 16 + nn, k, BT)); },
-                         [](int, int, SPRaw r) { return sp_val(r); }, BT, zero4());
+      f4 du = zero4(), wk = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        float va[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) va[e] = s.A[(ks * 32 + kq + e) * LS + Jb * BS + m];
+        const Frag fa = split8(va);
+        du = mma3f(fa, bd[ks], du);
+        wk = mma3f(fa, kf[ks], wk);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        float vn[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vn[e] = s.N[(ks * 32 + kq + e) * LS + Jb * BS + m];
+        du = mma3f(split8(vn), bk[ks], du);
+      }
       dus[Jb] = du;
       wks[Jb] = wk;
     }
+  }
   store_du_slab(p.g.dU + rowbase * KD, dus);
   __syncthreads();
   {
