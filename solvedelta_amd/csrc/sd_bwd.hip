@@ -862,16 +862,33 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       }
       split_blk(raw, BX);
     }
+    // P' delta: the delta column block's stored hi / lo halves are the B operand
+    // as they are (gathered once for the four row blocks)
+    Frag pw[2];
+    {
+      const int m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pw[ks].h[e] = s.PW.h[ks * 32 + kq + e][cb * 16 + m];
+          pw[ks].l[e] = s.PW.l[ks * 32 + kq + e][cb * 16 + m];
+        }
+    }
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       BlkS A;
       lblk(s.PA, I * BS, A);
       f4 dq = mma_blks(A, BX, zero4());
-      dq = mma_k32([&](int m, int j) { return s.M1[(I * BS + m) * LS + j]; },
-                   [&](int j, int nn) {
-                     return (float)s.PW.h[j][cb * 16 + nn] + (float)s.PW.l[j][cb * 16 + nn];
-                   },
-                   (I < 2 ? 32 : 64), dq);
+      const int m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks == 1 && I < 2) break;  // P' is lower triangular: rows < 32 reach tokens < 32
+        float va[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) va[e] = s.M1[(I * BS + m) * LS + ks * 32 + kq + e];
+        dq = mma3f(split8(va), pw[ks], dq);
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) dq_b[(unsigned)((I * BS + r4 + e) * KD + c)] = dq[e];
     }
