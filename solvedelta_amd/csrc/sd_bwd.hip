@@ -286,10 +286,10 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
         __bf16 x, y;
         split_bf(-ev[q][e] * __expf(cd.G[i0 + e][c]), x, y);
         ah[e] = x; al[e] = y;
-        split_bf(sp_val(qv[q][e]), x, y);
-        qh[e] = x; ql[e] = y;
-        split_bf(dout_val(d[q][e]), x, y);
-        dh[e] = x; dl[e] = y;
+        qh[e] = qv[q][e].h;  // a transposed copy of an already split panel
+        ql[e] = qv[q][e].l;
+        dh[e] = (__bf16)dout_val(d[q][e]);  // exact in bf16: no low half
+        dl[e] = (__bf16)0.f;
       }
       const long long ot = cidx * KD * BT + (long long)pc * 8;
       *reinterpret_cast<bf16x8*>(p.g.Ant.hi + ot) = ah;
