@@ -829,4 +829,113 @@ __device__ void lds_pair(const LPanel* A, const float* Ag, const LPanel& Y, floa
   }
 }
 
+
+// Y side of a decayed Gram staged once for all block pairs:
+//   Yt[j][c] = Y(j, c) exp(R_J[c] - G[j][c])   (J = j / BS; 0 on a wild coordinate of J),
+// split into bf16 hi / lo.  Every block J is used by 4 - J pairs, and each pair would
+// otherwise recompute its transform.  All CT threads; every value is read before the
+// first barrier, so Yt may share storage with what Y reads.
+template <class FY>
+__device__ void stage_ytilde(LPanel& Yt, const ChunkDecay& cd, FY Y) {
+  constexpr int PER = BT * KD / 4 / CT;  // 4-column groups per thread
+  float v[PER][4];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 4, j = idx / KD, c = idx % KD, J = j / BS;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[q][e] = Y(j, c + e) *
+                exp_unless_wild(cd.wild[J][c + e] != 0, cd.R[J][c + e] - cd.G[j][c + e]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 4, j = idx / KD, c = idx % KD;
+    bf16x4 hh4, ll4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      __bf16 a, b2;
+      split_bf(v[q][e], a, b2);
+      hh4[e] = a;
+      ll4[e] = b2;
+    }
+    *reinterpret_cast<bf16x4*>(&Yt.h[j][c]) = hh4;
+    *reinterpret_cast<bf16x4*>(&Yt.l[j][c]) = ll4;
+  }
+  __syncthreads();
+}
+
+// decayed_gram with its Y side staged by stage_ytilde: per pair only the X side
+// (X(i, c) exp(Gx_ic - R_J[c])) is transformed and split; Yraw(j, c) gives the
+// untransformed Y for the exact wild-coordinate fix-up.
+template <bool EXCL, class FX, class FYR>
+__device__ void decayed_gram_yt(const ChunkDecay& cd, FX X, const LPanel& Yt, FYR Yraw, bool strict,
+                                float* M, int ldm = LS) {
+  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+  for (int p = w; p < 10; p += CW) {
+    int I = 0, J = p;
+    while (J > I) { J -= I + 1; ++I; }  // p -> (I, J) with J <= I
+    const int I0 = I * BS, J0 = J * BS, i = I0 + m;
+    const float* RJ = cd.R[J];
+    float xr[4][8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xr[ks][e] = X(i, ks * 32 + kq + e);
+    BlkS A, B;
+    lblk(Yt, J0, B);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = ks * 32 + kq + e;
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        v[e] = xr[ks][e] * __expf(gx - RJ[c]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        __bf16 h, lo;
+        split_bf(v[e], h, lo);
+        A.f[ks].h[e] = h;
+        A.f[ks].l[e] = lo;
+      }
+    }
+    const f4 acc = mma_blks(A, B, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ii = I0 + out_row(e), j = J0 + out_col();
+      const bool keep = strict ? (j < ii) : (j <= ii);
+      M[ii * ldm + j] = keep ? acc[e] : 0.f;
+    }
+  }
+  // Zero the strictly-upper block pairs.
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int ii = idx / BT, j = idx % BT;
+    if ((j / BS) > (ii / BS)) M[ii * ldm + j] = 0.f;
+  }
+  __syncthreads();
+  // Exact fix-up for wild coordinates.
+  for (int J = 0; J < NB; ++J) {
+    const int nw = cd.nwild[J];
+    if (nw == 0) continue;
+    const int J0 = J * BS;
+    const int npairs = (BT - J0) * BS;
+    for (int idx = threadIdx.x; idx < npairs; idx += CT) {
+      const int ii = J0 + idx / BS, j = J0 + idx % BS;
+      const bool keep = strict ? (j < ii) : (j <= ii);
+      if (!keep) continue;
+      float sacc = 0.f;
+#pragma unroll 1
+      for (int q = 0; q < nw; ++q) {
+        const int c = cd.wlist[J][q];
+        const float gx = EXCL ? gx_excl(cd, ii, c) : cd.G[ii][c];
+        sacc += X(ii, c) * Yraw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      }
+      M[ii * ldm + j] += sacc;
+    }
+  }
+  __syncthreads();
+}
+
 }  // namespace sd

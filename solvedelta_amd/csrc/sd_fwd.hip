@@ -430,7 +430,7 @@ struct PrepSSmem {
   float Pb[BT][GS];
   union {
     float Pc[BT][GS];
-    LPanel Kp;  // the keys split once (bf16 hi + lo) for the M Gram and X0 k, before d is formed
+    LPanel Kp;  // keys split once for the M Gram and X0 k (before d), then d's staged Gram form
   };
 };
 
@@ -628,23 +628,25 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   SD_MARK(2, 12);
   __syncthreads();
   SD_MARK(2, 5);
+  // panels that read d and chi as they are, then d's Gram form staged once for
+  // both decayed Grams below (in d's own storage; the wild fix-ups read the
+  // global copy of d)
+  stage_ytilde(s.Kp, cd, [&](int j, int c) { return s.Pc[j][c]; });
+  const float* const dg_ = p.d + rowbase * KD;
+  auto Draw = [&](int j, int c) { return dg_[j * KD + c]; };
   // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i
-  decayed_gram<false>(
-      cd, [&](int i, int c) { return s.Pb[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
-      false, s.M);
+  decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pb[i][c]; }, s.Kp, Draw, false, s.M);
   store_frag_panel<BT, BT>(p.Ps.hi, p.Ps.lo, cidx * BT * BT,
                            [&](int i, int j) { return s.M[i * LS + j]; });
   store_frag_panel<KD, BT>(p.Ks.hi, p.Ks.lo, cidx * KD * BT, [&](int c, int i) {
-    return s.Pc[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
+    return dg_[i * KD + c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
   });
   store_frag_panel<BT, KD>(p.Qs.hi, p.Qs.lo, rowbase * KD,
                            [&](int i, int c) { return s.Pb[i][c] * __expf(cd.G[i][c]); });
   __syncthreads();
   SD_MARK(2, 6);
   // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
-  decayed_gram<false, 2>(
-      cd, [&](int i, int c) { return s.Pa[i][c]; }, [&](int j, int c) { return s.Pc[j][c]; },
-      true, s.M);
+  decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pa[i][c]; }, s.Kp, Draw, true, s.M);
   SD_MARK(2, 7);
   unit_lower_inverse(s.M, &s.Pc[0][0]);
   SD_MARK(2, 8);
