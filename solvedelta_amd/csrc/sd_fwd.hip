@@ -56,6 +56,7 @@ struct PrepCSmem {
   float Uh[BT][GS];   // normalised u
   __bf16 Hh[BT][PS];  // h (raw bf16, exact)
   float gam[BT];
+  LPanel Yt;          // the L Gram's Y side (u), transformed and split once
 };
 
 __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
@@ -99,8 +100,9 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   __syncthreads();
   const ChunkDecay& cd = s.cd;
   // L_ij = gamma_i sum_c u_ic u_jc exp(G_{i-1,c} - G_jc), j < i
-  decayed_gram<true>(
-      cd, [&](int i, int c) { return s.gam[i] * s.Uh[i][c]; },
+  stage_ytilde(s.Yt, cd, [&](int j, int c) { return s.Uh[j][c]; });
+  decayed_gram_yt<true>(
+      cd, [&](int i, int c) { return s.gam[i] * s.Uh[i][c]; }, s.Yt,
       [&](int j, int c) { return s.Uh[j][c]; }, true, s.M);
   unit_lower_inverse(s.M, s.tmp);
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
