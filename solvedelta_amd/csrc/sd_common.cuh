@@ -224,11 +224,6 @@ __device__ __forceinline__ f4 mma_k32_lx(LA la, XA xa, LB lb, XB xb, int K, f4 a
                  [&](int k, int nn) { return bv[k >> 5][k & 7]; }, K, acc);
 }
 
-// Identity transform for an operand gathered as plain fp32.
-struct XId {
-  __device__ float operator()(int, int, float x) const { return x; }
-};
-
 // Writes a per-chunk R x C panel (C = 64 or 128) split into bf16 hi / lo halves
 // in fragment order (see frag_off): each piece is one lane's 16 bytes of one
 // 16 x 32 operand block -- a fixed row and 8 consecutive columns -- produced

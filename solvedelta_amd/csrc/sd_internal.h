@@ -22,9 +22,6 @@ __device__ __forceinline__ void sp_store(const SP& sp, long long i, float x) {
   sp.hi[i] = h;
   sp.lo[i] = (__bf16)(x - (float)h);
 }
-__device__ __forceinline__ float sp_load(const SP& sp, long long i) {
-  return (float)sp.hi[i] + (float)sp.lo[i];
-}
 // Fragment order of a per-chunk split panel of R rows x C columns (C = 64 or
 // 128): each 16-row x 32-column MFMA operand block is 512 consecutive
 // elements, lane-major (lane = 16 * ((col % 32) / 8) + row % 16, 8 elements
