@@ -156,6 +156,31 @@ def forward_bench(ins, st, steps, warmup):
             "value": round(B * T / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4)}
 
 
+def refshape_bench(dev, steps, warmup):
+    """Forward + full VJP at the shape the reference's own README quotes its core
+    F+B timing on (B=1 T=1024 H=8 r=V=128; 0.905 ms on an RTX 5070 Ti,
+    BASELINE.md): a like-for-like point beside the headline, not the metric."""
+    from solvedelta_amd import solvedelta_native
+    ins, st, dO = make_inputs(dev, seed=5, b=1, t=1024)
+    leaves = ins + list(st)
+
+    def step():
+        out, _ = solvedelta_native(*ins, initial_state=st, return_final_state=False)
+        return torch.autograd.grad(out, leaves, dO)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"workload": "operator forward + full VJP, B=1 T=1024 H=8 r=V=128",
+            "value": round(1024 / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4),
+            "reference_published_ms": 0.905, "reference_hardware": "RTX 5070 Ti"}
+
+
 def decode_bench(dev, steps=256, streams=64):
     """Config 3: 64 independent streams x H=8, r=V=128, FP32 states C,S ~ 0.01 N(0,1)
     advanced in place by `steps` T=1 calls of the C-ABI (inputs drawn as config 1)."""
@@ -335,6 +360,7 @@ def main():
         "roofline": roof,
     }
     res["forward"] = forward_bench(ins, st, a.steps, a.warmup)
+    res["reference_shape"] = refshape_bench(dev, a.steps, a.warmup)
     if not a.no_decode:
         res["decode"] = decode_bench(dev)
     if not a.no_lm:
