@@ -428,7 +428,9 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
   float* dg = p.g.dgS + rowbase * KD;
   Tab1 t1;
+  Tab3 t3;
   make_tab1(cd, cb, t1);
+  make_tab3(cd, cb, t3);
   // This wave's d, e, chi slabs, loaded once for both passes (no global loads
   // between the passes' stores, which would wait for them).
   float Sd[NB][4], Se[NB][4], Sq[NB][4], pdg[NB][4];
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       f4 ap, bp;
-      apply2_tab<false>(cd, s.M1, s.M2, Sd, I, cb, t1, D, ap, bp);
+      apply2_tab<false>(cd, s.M1, s.M2, Sd, I, cb, t1, t3, D, ap, bp);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
@@ -480,7 +482,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       f4 k2, k3;
-      apply_t2_tab<false>(cd, s.M2, Sq, s.M1, Se, I, cb, t1, Q, E, k2, k3);
+      apply_t2_tab<false>(cd, s.M2, Sq, s.M1, Se, I, cb, t1, t3, Q, E, k2, k3);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;

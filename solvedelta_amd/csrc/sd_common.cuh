@@ -574,6 +574,23 @@ __device__ __forceinline__ void make_tab2(const ChunkDecay& cd, int cb, Tab2& t)
     }
 }
 
+// Factored inclusive block factors: exp(G_i - R_J) = rowf[I][e] * colf[pidx(I, J)]
+// with rowf = exp(G_i - R_I) (i = I*BS + r4 + e) and colf = exp(R_I - R_J) for this
+// lane's coordinate; both exponents are <= 0.  22 exps per lane instead of one per
+// (row, block) pair.
+struct Tab3 { float rowf[NB][4]; float colf[10]; };
+
+__device__ __forceinline__ void make_tab3(const ChunkDecay& cd, int cb, Tab3& t) {
+  const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+#pragma unroll
+  for (int I = 0; I < NB; ++I) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t.rowf[I][e] = __expf(cd.G[I * BS + r4 + e][c] - cd.R[I][c]);
+#pragma unroll
+    for (int J = 0; J <= I; ++J) t.colf[pidx(I, J)] = J == I ? 1.f : __expf(cd.R[I][c] - cd.R[J][c]);
+  }
+}
+
 // Slab applies with precomputed factors (see apply_slab / apply_t_slab).
 template <bool EXCL, class FW>
 __device__ f4 apply_tab(const ChunkDecay& cd, const float* M, const float (&Y)[NB][4], int I, int cb,
@@ -648,8 +665,9 @@ __device__ f4 apply_t_tab(const ChunkDecay& cd, const float* M, const float (&X)
 // Two applies sharing Y (and so every decay factor): R1 with M1, R2 with M2.
 template <bool EXCL, class FW>
 __device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M2,
-                           const float (&Y)[NB][4], int I, int cb, const Tab1& t1, FW Yw, f4& r1,
-                           f4& r2) {
+                           const float (&Y)[NB][4], int I, int cb, const Tab1& t1, const Tab3& t3,
+                           FW Yw, f4& r1, f4& r2) {
+  static_assert(!EXCL, "the factored block factors are inclusive");
   const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
   r1 = zero4();
   r2 = zero4();
@@ -682,8 +700,7 @@ __device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int i = I * BS + r4 + e;
-        const float f = __expf((EXCL ? gx_excl(cd, i, c) : cd.G[i][c]) - cd.R[J][c]);
+        const float f = t3.rowf[I][e] * t3.colf[pidx(I, J)];
         r1[e] += f * p1[e];
         r2[e] += f * p2[e];
       }
@@ -695,7 +712,8 @@ __device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M
 template <bool EXCL, class FW1, class FW2>
 __device__ void apply_t2_tab(const ChunkDecay& cd, const float* M1, const float (&X1)[NB][4],
                              const float* M2, const float (&X2)[NB][4], int Jb, int cb,
-                             const Tab1& t1, FW1 X1w, FW2 X2w, f4& r1, f4& r2) {
+                             const Tab1& t1, const Tab3& t3, FW1 X1w, FW2 X2w, f4& r1, f4& r2) {
+  static_assert(!EXCL, "the factored block factors are inclusive");
   const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
   f4 acc1 = zero4(), acc2 = zero4();
 #pragma unroll
@@ -707,8 +725,7 @@ __device__ void apply_t2_tab(const ChunkDecay& cd, const float* M1, const float 
       const int row = (I * BS + r4 + e) * LS + Jb * BS + m;
       av1[e] = M1[row];
       av2[e] = M2[row];
-      const int i = I * BS + r4 + e;
-      const float f = __expf((EXCL ? gx_excl(cd, i, c) : cd.G[i][c]) - cd.R[Jb][c]);
+      const float f = t3.rowf[I][e] * t3.colf[pidx(I, Jb)];
       bv1[e] = X1[I][e] * f;
       bv2[e] = X2[I][e] * f;
     }
