@@ -428,9 +428,11 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
   float* dg = p.g.dgS + rowbase * KD;
   Tab1 t1;
-  Tab3 t3;
+  RowF rf;
+  ColF cf;
   make_tab1(cd, cb, t1);
-  make_tab3(cd, cb, t3);
+  make_rowf<false>(cd, cb, rf);
+  make_colf(cd, cb, cf);
   // This wave's d, e, chi slabs, loaded once for both passes (no global loads
   // between the passes' stores, which would wait for them).
   float Sd[NB][4], Se[NB][4], Sq[NB][4], pdg[NB][4];
@@ -450,7 +452,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       f4 ap, bp;
-      apply2_tab<false>(cd, s.M1, s.M2, Sd, I, cb, t1, t3, D, ap, bp);
+      apply2_tab<false>(cd, s.M1, s.M2, Sd, I, cb, t1, rf, cf, D, ap, bp);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
@@ -482,7 +484,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       f4 k2, k3;
-      apply_t2_tab<false>(cd, s.M2, Sq, s.M1, Se, I, cb, t1, t3, Q, E, k2, k3);
+      apply_t2_tab<false>(cd, s.M2, Sq, s.M1, Se, I, cb, t1, rf, cf, Q, E, k2, k3);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
@@ -794,10 +796,12 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       for (int e = 0; e < 4; ++e) So[J][e] -= Sk[J][e];  // C-op output o = d - k
   }
   Tab1 t1;
-  Tab2 tx, ti;
+  RowF rx, ri;  // exclusive / inclusive row factors
+  ColF cf;
   make_tab1(cd, cb, t1);
-  make_tab2<true>(cd, cb, tx);
-  make_tab2<false>(cd, cb, ti);
+  make_rowf<true>(cd, cb, rx);
+  make_rowf<false>(cd, cb, ri);
+  make_colf(cd, cb, cf);
   __syncthreads();  // M1, M2 complete; PA free
   SD_MARK(3, 4);
   // PA <- dd e^G for the dq product (staged now, consumed after the applies)
@@ -820,9 +824,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   float vv[NB][4], xs[NB][4];
 #pragma unroll
   for (int I = 0; I < NB; ++I) {
-    const f4 ap = apply_tab<true>(cd, s.M1, Su, I, cb, t1, tx, U);
-    const f4 k2 = apply_t_tab<false>(cd, s.M2, Sdd, I, cb, t1, ti, DO);
-    const f4 k3 = apply_t_tab<true>(cd, s.M1, Sx, I, cb, t1, tx, Xg);
+    const f4 ap = apply_tab<true>(cd, s.M1, Su, I, cb, t1, rx, cf, U);
+    const f4 k2 = apply_t_tab<false>(cd, s.M2, Sdd, I, cb, t1, ri, cf, DO);
+    const f4 k3 = apply_t_tab<true>(cd, s.M1, Sx, I, cb, t1, rx, cf, Xg);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = I * BS + r4 + e;

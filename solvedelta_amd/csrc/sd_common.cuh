@@ -538,15 +538,14 @@ __device__ __forceinline__ f4 mma_blks(const BlkS& A, const BlkS& B, f4 acc) {
 }
 
 // Per-lane decay factors for the slab applies of one 16-column block:
-//   E1[J][e]     = exp(R_J - G_j), j = J*16 + (lane>>4)*4 + e  (0 for wild coords)
-//   E2[pi(I,J)][e] = exp(Gx_i - R_J), i = I*16 + (lane>>4)*4 + e, J <= I
+//   E1[J][e] = exp(R_J - G_j), j = J*16 + (lane>>4)*4 + e  (0 for wild coords),
+// and exp(Gx_i - R_J) for the block pairs J <= I (RowF / ColF below).
 __device__ __forceinline__ int pidx(int I, int J) { return I * (I + 1) / 2 + J; }
 
 struct Tab1 {
   float E1[NB][4];
   unsigned wm;  // bit J: this lane's coordinate is wild in block J (read once, not per use)
 };
-struct Tab2 { float E2[10][4]; };
 
 __device__ __forceinline__ void make_tab1(const ChunkDecay& cd, int cb, Tab1& t) {
   const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
@@ -560,8 +559,15 @@ __device__ __forceinline__ void make_tab1(const ChunkDecay& cd, int cb, Tab1& t)
   }
 }
 
+// Block decay factors in factored form: exp(Gx_i - R_J) = RowF[I][e] * ColF[pidx(I, J)]
+// (i = I*BS + r4 + e, J <= I) with RowF = exp(Gx_i - R_I), Gx the inclusive or
+// exclusive prefix, and ColF = exp(R_I - R_J), for this lane's coordinate.  Every
+// exponent is <= 0 (the prefix only falls), so neither factor overflows.
+struct RowF { float f[NB][4]; };
+struct ColF { float f[10]; };
+
 template <bool EXCL>
-__device__ __forceinline__ void make_tab2(const ChunkDecay& cd, int cb, Tab2& t) {
+__device__ __forceinline__ void make_rowf(const ChunkDecay& cd, int cb, RowF& t) {
   const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
 #pragma unroll
   for (int I = 0; I < NB; ++I)
@@ -569,32 +575,24 @@ __device__ __forceinline__ void make_tab2(const ChunkDecay& cd, int cb, Tab2& t)
     for (int e = 0; e < 4; ++e) {
       const int i = I * BS + r4 + e;
       const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
-#pragma unroll
-      for (int J = 0; J <= I; ++J) t.E2[pidx(I, J)][e] = __expf(gx - cd.R[J][c]);
+      t.f[I][e] = __expf(gx - cd.R[I][c]);
     }
 }
 
-// Factored inclusive block factors: exp(G_i - R_J) = rowf[I][e] * colf[pidx(I, J)]
-// with rowf = exp(G_i - R_I) (i = I*BS + r4 + e) and colf = exp(R_I - R_J) for this
-// lane's coordinate; both exponents are <= 0.  22 exps per lane instead of one per
-// (row, block) pair.
-struct Tab3 { float rowf[NB][4]; float colf[10]; };
-
-__device__ __forceinline__ void make_tab3(const ChunkDecay& cd, int cb, Tab3& t) {
-  const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+__device__ __forceinline__ void make_colf(const ChunkDecay& cd, int cb, ColF& t) {
+  const int c = cb * 16 + (lane_id() & 15);
 #pragma unroll
-  for (int I = 0; I < NB; ++I) {
+  for (int I = 0; I < NB; ++I)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) t.rowf[I][e] = __expf(cd.G[I * BS + r4 + e][c] - cd.R[I][c]);
-#pragma unroll
-    for (int J = 0; J <= I; ++J) t.colf[pidx(I, J)] = J == I ? 1.f : __expf(cd.R[I][c] - cd.R[J][c]);
-  }
+    for (int J = 0; J <= I; ++J) t.f[pidx(I, J)] = J == I ? 1.f : __expf(cd.R[I][c] - cd.R[J][c]);
 }
 
-// Slab applies with precomputed factors (see apply_slab / apply_t_slab).
+// Slab applies with precomputed factors: R_I = sum_{J<=I} e^{Gx_i - R_J} (M_IJ (Y_J (.) E1_J))
+// for this wave's 16 columns, and the transposed form; wild coordinates take the
+// exact elementwise path.
 template <bool EXCL, class FW>
 __device__ f4 apply_tab(const ChunkDecay& cd, const float* M, const float (&Y)[NB][4], int I, int cb,
-                        const Tab1& t1, const Tab2& t2, FW Yw) {
+                        const Tab1& t1, const RowF& rf, const ColF& cf, FW Yw) {
   const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
   f4 tot = zero4();
 #pragma unroll
@@ -619,7 +617,7 @@ __device__ f4 apply_tab(const ChunkDecay& cd, const float* M, const float (&Y)[N
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) tot[e] += t2.E2[pidx(I, J)][e] * a2[e];
+      for (int e = 0; e < 4; ++e) tot[e] += rf.f[I][e] * cf.f[pidx(I, J)] * a2[e];
     }
   }
   return tot;
@@ -627,7 +625,7 @@ __device__ f4 apply_tab(const ChunkDecay& cd, const float* M, const float (&Y)[N
 
 template <bool EXCL, class FW>
 __device__ f4 apply_t_tab(const ChunkDecay& cd, const float* M, const float (&X)[NB][4], int Jb,
-                          int cb, const Tab1& t1, const Tab2& t2, FW Xw) {
+                          int cb, const Tab1& t1, const RowF& rf, const ColF& cf, FW Xw) {
   const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
   f4 acc = zero4();
 #pragma unroll
@@ -637,7 +635,7 @@ __device__ f4 apply_t_tab(const ChunkDecay& cd, const float* M, const float (&X)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       av[e] = M[(I * BS + r4 + e) * LS + Jb * BS + m];
-      bv[e] = X[I][e] * t2.E2[pidx(I, Jb)][e];
+      bv[e] = X[I][e] * (rf.f[I][e] * cf.f[pidx(I, Jb)]);
     }
     acc = mma16s(av, bv, acc);
   }
@@ -665,8 +663,8 @@ __device__ f4 apply_t_tab(const ChunkDecay& cd, const float* M, const float (&X)
 // Two applies sharing Y (and so every decay factor): R1 with M1, R2 with M2.
 template <bool EXCL, class FW>
 __device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M2,
-                           const float (&Y)[NB][4], int I, int cb, const Tab1& t1, const Tab3& t3,
-                           FW Yw, f4& r1, f4& r2) {
+                           const float (&Y)[NB][4], int I, int cb, const Tab1& t1, const RowF& rf,
+                           const ColF& cf, FW Yw, f4& r1, f4& r2) {
   static_assert(!EXCL, "the factored block factors are inclusive");
   const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
   r1 = zero4();
@@ -700,7 +698,7 @@ __device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float f = t3.rowf[I][e] * t3.colf[pidx(I, J)];
+        const float f = rf.f[I][e] * cf.f[pidx(I, J)];
         r1[e] += f * p1[e];
         r2[e] += f * p2[e];
       }
@@ -712,7 +710,8 @@ __device__ void apply2_tab(const ChunkDecay& cd, const float* M1, const float* M
 template <bool EXCL, class FW1, class FW2>
 __device__ void apply_t2_tab(const ChunkDecay& cd, const float* M1, const float (&X1)[NB][4],
                              const float* M2, const float (&X2)[NB][4], int Jb, int cb,
-                             const Tab1& t1, const Tab3& t3, FW1 X1w, FW2 X2w, f4& r1, f4& r2) {
+                             const Tab1& t1, const RowF& rf, const ColF& cf, FW1 X1w, FW2 X2w,
+                             f4& r1, f4& r2) {
   static_assert(!EXCL, "the factored block factors are inclusive");
   const int l = lane_id(), m = l & 15, r4 = (l >> 4) * 4, c = cb * 16 + m;
   f4 acc1 = zero4(), acc2 = zero4();
@@ -725,7 +724,7 @@ __device__ void apply_t2_tab(const ChunkDecay& cd, const float* M1, const float 
       const int row = (I * BS + r4 + e) * LS + Jb * BS + m;
       av1[e] = M1[row];
       av2[e] = M2[row];
-      const float f = t3.rowf[I][e] * t3.colf[pidx(I, Jb)];
+      const float f = rf.f[I][e] * cf.f[pidx(I, Jb)];
       bv1[e] = X1[I][e] * f;
       bv2[e] = X2[I][e] * f;
     }

@@ -528,9 +528,11 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) Su[J][e] = s.Pa[J * BS + r4 + e][c];
     Tab1 t1;
-    Tab2 t2;
+    RowF rf;
+    ColF cf;
     make_tab1(cd, cb, t1);
-    make_tab2<false>(cd, cb, t2);
+    make_rowf<false>(cd, cb, rf);
+    make_colf(cd, cb, cf);
     auto Uw = [&](int j, int cc) { return s.Pa[j][cc]; };
     f4 a1[NB];  // X0 k for this wave's column block, from the shared split keys
 #pragma unroll
@@ -542,7 +544,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     __syncthreads();  // the split keys are dead: d is formed in their place
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
-      const f4 ap = apply_tab<false>(cd, s.M, Su, I, cb, t1, t2, Uw);
+      const f4 ap = apply_tab<false>(cd, s.M, Su, I, cb, t1, rf, cf, Uw);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
