@@ -971,7 +971,7 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
   ss.rev = 1;
   ss.Wneg = bw.Wk; ss.U = bw.dU; ss.Kt = bw.Ant; ss.Gam = fw.Gam;
-  ss.At1 = bw.At1; ss.B1 = bw.B1t;
+  ss.At1 = bw.At1; ss.B1 = bw.B1t; ss.b1_exact = 1;  // B1t = dO, exact in bf16
   ss.Xs = bw.Ls; ss.wout = bw.dwS;
   ss.init = dS_T; ss.init_transposed = 0;
   ss.fin = dS0; ss.fin_transposed = 0;

@@ -200,7 +200,9 @@ __device__ __forceinline__ Frag ldfrag(const SP& sp, long long off) {
   return f;
 }
 
-template <bool INJ>
+// B1X: the injection's B operand is exact in bf16 (its stored low half is zero),
+// so only the high half is loaded and multiplied.
+template <bool INJ, bool B1X>
 __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
                                                  StateFrags<INJ>& f) {
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
@@ -233,7 +235,13 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
     for (int h = 0; h < HALVES; ++h)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        f.B1[h][ks] = ldfrag(p.B1, cidx * KD * BT + frag_off(tile * SCOLS + h * 16 + m, ks * 32 + kq, BT));
+      {
+        const long long o = cidx * KD * BT + frag_off(tile * SCOLS + h * 16 + m, ks * 32 + kq, BT);
+        if constexpr (B1X)
+          f.B1[h][ks].h = ldb8(p.B1.hi + o);
+        else
+          f.B1[h][ks] = ldfrag(p.B1, o);
+      }
   }
 }
 
@@ -251,7 +259,7 @@ __device__ __forceinline__ void stage_split4(__bf16* hi, __bf16* lo, f4 v) {
 }
 
 // One chunk of the sequential pass with its operand fragments already in registers.
-template <bool INJ>
+template <bool INJ, bool B1X>
 __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, int n, int ch, int tile,
                                            const StateFrags<INJ>& cur,
                                            f4 (&X)[SRB][HALVES]) {
@@ -306,7 +314,14 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
       for (int e = 0; e < 4; ++e) X[q][h][e] *= gv[e];
       if constexpr (INJ) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) X[q][h] = mma3f(cur.A1[q][ks], cur.B1[h][ks], X[q][h]);
+        for (int ks = 0; ks < 2; ++ks) {
+          if constexpr (B1X) {
+            X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks].l, cur.B1[h][ks].h, X[q][h], 0, 0, 0);
+            X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks].h, cur.B1[h][ks].h, X[q][h], 0, 0, 0);
+          } else {
+            X[q][h] = mma3f(cur.A1[q][ks], cur.B1[h][ks], X[q][h]);
+          }
+        }
       }
     }
   }
@@ -341,7 +356,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
   __syncthreads();
 }
 
-template <bool INJ>
+template <bool INJ, bool B1X>
 __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   __shared__ __align__(16) StateSmem s;
   const int NS = p.NT + 1;  // state slots per sequence
@@ -383,18 +398,18 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   auto clampc = [&](int it2) { return chunk_of(it2 < NT ? it2 : NT - 1); };
   StateFrags<INJ> f[PF];
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j) load_state_frags(p, n, clampc(j), tile, f[j]);
+  for (int j = 0; j < PF - 1; ++j) load_state_frags<INJ, B1X>(p, n, clampc(j), tile, f[j]);
   int it = 0;
   for (; it + PF - 1 < NT; it += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      load_state_frags(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
-      state_step(p, s, n, chunk_of(it + j), tile, f[j], X);
+      load_state_frags<INJ, B1X>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
+      state_step<INJ, B1X>(p, s, n, chunk_of(it + j), tile, f[j], X);
     }
   }
 #pragma unroll
   for (int j = 0; j < PF - 1; ++j)
-    if (it + j < NT) state_step(p, s, n, chunk_of(it + j), tile, f[j], X);
+    if (it + j < NT) state_step<INJ, B1X>(p, s, n, chunk_of(it + j), tile, f[j], X);
   // final state (also kept as slot NT for the backward)
   for (int q = 0; q < SRB; ++q)
     for (int h = 0; h < HALVES; ++h)
@@ -414,10 +429,12 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
 
 void launch_state(const char* name, const StateParams& sp, int nseq, hipStream_t st) {
   const dim3 grid(STILES * nseq), blk(STHREADS);
-  if (sp.At1.hi)
-    SD_LAUNCH(name, k_state<true>, grid, blk, 0, st, sp);
+  if (sp.At1.hi && sp.b1_exact)
+    SD_LAUNCH(name, (k_state<true, true>), grid, blk, 0, st, sp);
+  else if (sp.At1.hi)
+    SD_LAUNCH(name, (k_state<true, false>), grid, blk, 0, st, sp);
   else
-    SD_LAUNCH(name, k_state<false>, grid, blk, 0, st, sp);
+    SD_LAUNCH(name, (k_state<false, false>), grid, blk, 0, st, sp);
 }
 
 // ---------------------------------------------------------------------------

@@ -73,6 +73,7 @@ struct StateParams {
   int H, T, NT, Tp, rows, cols, rev;
   SP Wneg; const float* U; SP Kt; const float* Gam;
   SP At1; SP B1;  // optional injection
+  int b1_exact;     // B1 is exact in bf16: its low half is zero and not read
   float* Xs; float* wout;
   const float* init; int init_transposed;
   float* fin; int fin_transposed;
