@@ -280,7 +280,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
       const int c = (block / (BT / 32)) * 16 + (lane & 15);
       const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
-      bf16x8 ah, al, qh, ql, dh, dl;
+      bf16x8 ah, al, qh, ql, dh;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         __bf16 x, y;
@@ -288,8 +288,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
         ah[e] = x; al[e] = y;
         qh[e] = qv[q][e].h;  // a transposed copy of an already split panel
         ql[e] = qv[q][e].l;
-        dh[e] = (__bf16)dout_val(d[q][e]);  // exact in bf16: no low half
-        dl[e] = (__bf16)0.f;
+        dh[e] = (__bf16)dout_val(d[q][e]);  // exact in bf16: no low half is stored
       }
       const long long ot = cidx * KD * BT + (long long)pc * 8;
       *reinterpret_cast<bf16x8*>(p.g.Ant.hi + ot) = ah;
@@ -297,7 +296,6 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       *reinterpret_cast<bf16x8*>(p.g.At1.hi + ot) = qh;
       *reinterpret_cast<bf16x8*>(p.g.At1.lo + ot) = ql;
       *reinterpret_cast<bf16x8*>(p.g.B1t.hi + ot) = dh;
-      *reinterpret_cast<bf16x8*>(p.g.B1t.lo + ot) = dl;
     }
   }
 }
@@ -603,6 +601,7 @@ struct BprepCSmem {
   float Uh[BT][GS];
   float Kh[BT][GS];
   float gam[BT];
+  float krs[BT];  // 1 / |k_i|
 };
 
 __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
@@ -633,7 +632,8 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
       l2norm16(ux[g]);
-      l2norm16(kx[g]);
+      const float rk = l2norm16(kx[g]);
+      if ((l & 15) == 0) s.krs[i] = rk;
 #pragma unroll
       for (int q = 0; q < RQ; ++q) {
         s.Uh[i][cl + 16 * q] = ux[g][q];
@@ -714,10 +714,36 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     p.g.uh[(rowbase + i) * KD + c] = s.Uh[i][c];
   }
   // chunk-transposed panels, fragment order
-  store_frag_panel<KD, BT>(p.g.At1.hi, p.g.At1.lo, cidx * KD * BT,
-                           [&](int c, int i) { return ddp[i * KD + c] * __expf(cd.G[i][c]); });
-  store_frag_panel<KD, BT>(p.g.B1t.hi, p.g.B1t.lo, cidx * KD * BT,
-                           [&](int c, int i) { return s.Kh[i][c]; });
+  // The reverse pass's injection sum_i At1_ci Kh_i,col is formed as
+  // sum_i (At1_ci / |k_i|) k_i,col: its B operand is then the raw key input,
+  // exact in bf16, so only a high half is stored (and read).
+  store_frag_panel<KD, BT>(p.g.At1.hi, p.g.At1.lo, cidx * KD * BT, [&](int c, int i) {
+    return ddp[i * KD + c] * __expf(cd.G[i][c]) * s.krs[i];
+  });
+  {
+    constexpr int PIECES = KD * BT / 8, PER = PIECES / CT;
+    static_assert(PIECES % CT == 0, "whole pieces per thread");
+    __bf16 kr[PER][8];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
+      const int c = (block / (BT / 32)) * 16 + (lane & 15);
+      const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {  // clamped address + mask: no guarded load
+        const int t = t0 + i0 + e;
+        const float v = bf2f(brow(p.in.k, b, t < p.T ? t : p.T - 1, hh)[c < p.r ? c : p.r - 1]);
+        kr[q][e] = (__bf16)keep_if(t < p.T && c < p.r, v);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      bf16x8 h;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = kr[q][e];
+      *reinterpret_cast<bf16x8*>(p.g.B1t.hi + cidx * KD * BT + (long long)(threadIdx.x + q * CT) * 8) = h;
+    }
+  }
   store_frag_panel<KD, BT>(p.g.Ant.hi, p.g.Ant.lo, cidx * KD * BT, [&](int c, int i) {
     return -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c));
   });
@@ -984,7 +1010,7 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
   sc.rev = 1;
   sc.Wneg = bw.Wk; sc.U = bw.dU; sc.Kt = bw.Ant; sc.Gam = fw.Gam;
-  sc.At1 = bw.At1; sc.B1 = bw.B1t;
+  sc.At1 = bw.At1; sc.B1 = bw.B1t; sc.b1_exact = 1;  // B1t = raw keys, exact in bf16
   sc.Xs = bw.Lc; sc.wout = bw.dwC;
   sc.init = dC_T; sc.init_transposed = 1;
   sc.fin = dC0; sc.fin_transposed = 1;

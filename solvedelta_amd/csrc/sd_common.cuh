@@ -127,13 +127,15 @@ __device__ __forceinline__ void ld_row16(const __bf16* p, bool tv, int w, float 
   }
 }
 
-__device__ __forceinline__ void l2norm16(float (&x)[RQ]) {
+// Normalises one 16-lane row in place and returns its inverse norm.
+__device__ __forceinline__ float l2norm16(float (&x)[RQ]) {
   float ss = 0.f;
 #pragma unroll
   for (int q = 0; q < RQ; ++q) ss += x[q] * x[q];
   const float rs = rsqrtf(row16_sum(ss) + 1e-24f);
 #pragma unroll
   for (int q = 0; q < RQ; ++q) x[q] *= rs;
+  return rs;
 }
 
 __device__ __forceinline__ f4 zero4() { f4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
