@@ -179,6 +179,7 @@ struct StateSmem {
   float Xf[KD][XFS];
   float wf[BT][XFS];
   float Uf[BT][XFS];  // U tile, staged from one 16-byte load per thread
+  float Gf[KD];       // chunk decay, staged from one 16-byte load per lane of wave 0
 };
 
 template <bool INJ>
@@ -188,7 +189,7 @@ struct StateFrags {
   Frag A1[INJ ? SRB : 1][2];
   Frag B1[INJ ? HALVES : 1][2];
   float4 U4;  // U tile piece: token threadIdx / (SCOLS / 4), columns 4 (threadIdx % (SCOLS / 4))
-  float4 gam[SRB];
+  float4 G4;  // chunk decay, columns 4 (threadIdx % 32) .. +3 (every wave loads all 128)
 };
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -222,8 +223,7 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
     static_assert(BT * C4 == STHREADS, "one U piece per thread");
     f.U4 = ld4(p.U + (rowbase + threadIdx.x / C4) * KD + tile * SCOLS + (threadIdx.x % C4) * 4);
   }
-#pragma unroll
-  for (int q = 0; q < SRB; ++q) f.gam[q] = ld4(p.Gam + cidx * KD + (SRB * w + q) * 16 + (l >> 4) * 4);
+  f.G4 = ld4(p.Gam + cidx * KD + (l & 31) * 4);
   if constexpr (INJ) {
 #pragma unroll
     for (int q = 0; q < SRB; ++q)
@@ -279,6 +279,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
       stage_split4(&s.Xh[h * 16 + m][row0], &s.Xl[h * 16 + m][row0], X[q][h]);
     }
   *reinterpret_cast<float4*>(&s.Uf[threadIdx.x / (SCOLS / 4)][(threadIdx.x % (SCOLS / 4)) * 4]) = cur.U4;
+  if (threadIdx.x < KD / 4) *reinterpret_cast<float4*>(&s.Gf[threadIdx.x * 4]) = cur.G4;
   __syncthreads();
   if (p.Xs) {  // slot write-back: 128 rows x SCOLS columns as float4 pieces
     constexpr int C4 = SCOLS / 4;
@@ -308,7 +309,8 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
     }
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
-    const float gv[4] = {cur.gam[q].x, cur.gam[q].y, cur.gam[q].z, cur.gam[q].w};
+    const float4 g4 = *reinterpret_cast<const float4*>(&s.Gf[(SRB * w + q) * 16 + r4]);
+    const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
 #pragma unroll
     for (int h = 0; h < HALVES; ++h) {
       for (int e = 0; e < 4; ++e) X[q][h][e] *= gv[e];
