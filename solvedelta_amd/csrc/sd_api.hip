@@ -67,7 +67,7 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.Ant = c.take_sp(panel);
   float** panels[] = {&w.dU, &w.B1, &w.dwS, &w.dwC, &w.de, &w.dchi,
                       &w.dd, &w.dgS, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
-                      &w.dgC, &w.uh};
+                      &w.uh};
   for (float** pp : panels) *pp = c.take<float>(panel);
   if (total) *total = c.off + 256;
   return w;

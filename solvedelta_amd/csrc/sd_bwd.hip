@@ -841,7 +841,6 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) Sx[J][e] = s.gam[J * BS + r4 + e] * Su[J][e];
   SD_MARK(3, 5);
-  float* dg = p.g.dgC + rowbase * KD;
   // chunk-uniform output bases, 32-bit lane offsets (keeps addresses out of VGPR pairs)
   float* const dx_b = p.g.dxC + rowbase * KD;
   float* const dk_b = p.g.dkC + rowbase * KD;
@@ -865,12 +864,24 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       vv[I][e] = So[I][e] * Sdd[I][e] - Su[I][e] * dk + xs[I][e];
     }
   }
+  // the S side's closed decay gradient (loaded here: held through the loop above
+  // it would push the kernel past its registers)
+  float Sg[NB][4];
+  load_slab(Sg, p.g.dgS + rowbase * KD, cb);
   // dg_i = rowsum + sum_{i' >= i} dg_i' + sum_{i' > i} xdx_i'
   close_decay_column(vv, s.rsum, cb);
+  // the log-decay gradient, complete: this C-side closure plus the S side's
+  {
+    float* const dgo = p.dg + ((long long)b * p.T * p.H + hh) * p.r + c;
+    const long long tstride = (long long)p.H * p.r;
 #pragma unroll
-  for (int I = 0; I < NB; ++I)
+    for (int I = 0; I < NB; ++I)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dg[(unsigned)((I * BS + r4 + e) * KD + c)] = vv[I][e] - xs[I][e];
+      for (int e = 0; e < 4; ++e) {
+        const int t = t0 + I * BS + r4 + e;
+        if (t < p.T && c < p.r) dgo[t * tstride] = vv[I][e] - xs[I][e] + Sg[I][e];
+      }
+  }
   SD_MARK(3, 6);
   __syncthreads();  // M1 free: P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) into M1
   decayed_gram<false>(
@@ -960,13 +971,11 @@ __global__ __launch_bounds__(NTHREADS) void k_final(BwdParams p) {
     p.du[tok * r + l] = f2bf((du0 - ud * u0) * ru);
     p.dk[tok * r + l] = f2bf((dk0 - kd * k0) * rk);
     p.dh[tok * r + l] = f2bf(gm * dv0);
-    p.dg[tok * r + l] = p.g.dgS[row + l] + p.g.dgC[row + l];
   }
   if (l + 64 < r) {
     p.du[tok * r + l + 64] = f2bf((du1 - ud * u1) * ru);
     p.dk[tok * r + l + 64] = f2bf((dk1 - kd * k1) * rk);
     p.dh[tok * r + l + 64] = f2bf(gm * dv1);
-    p.dg[tok * r + l + 64] = p.g.dgS[row + l + 64] + p.g.dgC[row + l + 64];
   }
   if (l == 0) p.dgam[tok] = dgam;
 }

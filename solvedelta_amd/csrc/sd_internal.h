@@ -121,7 +121,7 @@ struct BwdWs {
   float* dwS; float* dwC;          // dw of each op           [n][Tp][128]
   float* de; float* dchi; float* dd; float* dgS;
   float* ddelta; float* du_src; float* dk_src;
-  float* dkC; float* dxC; float* dqC; float* dgC;
+  float* dkC; float* dxC; float* dqC;
   float* uh;  // normalised u
 };
 
