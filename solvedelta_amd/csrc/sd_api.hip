@@ -66,7 +66,7 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.B1t = c.take_sp(panel);
   w.Ant = c.take_sp(panel);
   float** panels[] = {&w.dU, &w.B1, &w.dwS, &w.dwC, &w.de, &w.dchi,
-                      &w.dd, &w.dgS, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
+                      &w.dd, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
                       &w.uh};
   for (float** pp : panels) *pp = c.take<float>(panel);
   if (total) *total = c.off + 256;

@@ -424,7 +424,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   auto D = [&](int j, int cc) { return dd_[j * KD + cc]; };
   auto E = [&](int j, int cc) { return ee[j * KD + cc]; };
   auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
-  float* dg = p.g.dgS + rowbase * KD;
   Tab1 t1;
   RowF rf;
   ColF cf;
@@ -492,13 +491,17 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
       }
     }
     close_decay_column(pdg, s.rsum, cb);
+    // the S side's log-decay gradient goes straight to the output; the C side's
+    // chunk gradient adds its own part to it
+    float* const dgo = p.dg + ((long long)b * p.T * p.H + hh) * p.r + c;
+    const long long tstride = (long long)p.H * p.r;
 #pragma unroll
     for (int I = 0; I < NB; ++I)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const unsigned o = (unsigned)((I * BS + r4 + e) * KD + c);
-        dd_b[o] = kl[I][e];
-        dg[o] = pdg[I][e];
+        const int i = I * BS + r4 + e, t = t0 + i;
+        dd_b[(unsigned)(i * KD + c)] = kl[I][e];
+        if (t < p.T && c < p.r) dgo[t * tstride] = pdg[I][e];
       }
   }
   SD_MARK(7, 6);
@@ -864,13 +867,12 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       vv[I][e] = So[I][e] * Sdd[I][e] - Su[I][e] * dk + xs[I][e];
     }
   }
-  // the S side's closed decay gradient (loaded here: held through the loop above
-  // it would push the kernel past its registers)
-  float Sg[NB][4];
-  load_slab(Sg, p.g.dgS + rowbase * KD, cb);
   // dg_i = rowsum + sum_{i' >= i} dg_i' + sum_{i' > i} xdx_i'
   close_decay_column(vv, s.rsum, cb);
-  // the log-decay gradient, complete: this C-side closure plus the S side's
+  // the C side's part of the log-decay gradient, added to the S side's (written
+  // by the S chunk gradient) with a return-free atomic: the add happens in L2, so
+  // nothing is loaded here, and with exactly one add per element on top of one
+  // store the sum is deterministic
   {
     float* const dgo = p.dg + ((long long)b * p.T * p.H + hh) * p.r + c;
     const long long tstride = (long long)p.H * p.r;
@@ -879,7 +881,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = t0 + I * BS + r4 + e;
-        if (t < p.T && c < p.r) dgo[t * tstride] = vv[I][e] - xs[I][e] + Sg[I][e];
+        if (t < p.T && c < p.r) unsafeAtomicAdd(&dgo[t * tstride], vv[I][e] - xs[I][e]);
       }
   }
   SD_MARK(3, 6);

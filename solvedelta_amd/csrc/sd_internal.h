@@ -119,7 +119,7 @@ struct BwdWs {
   float* Ls;   // S-op chunk-end cotangents
   float* dU; SP Wk; SP At1; float* B1; SP B1t; SP Ant;  // reverse-pass panels (reused)
   float* dwS; float* dwC;          // dw of each op           [n][Tp][128]
-  float* de; float* dchi; float* dd; float* dgS;
+  float* de; float* dchi; float* dd;
   float* ddelta; float* du_src; float* dk_src;
   float* dkC; float* dxC; float* dqC;
   float* uh;  // normalised u
