@@ -67,13 +67,13 @@ BYTES_PER_CHUNK = {
     "state_s_fwd": 3 * _P + (_S + _P),                      # W,U,K -> state slot, w
     "k_out_s": (_S + 2 * _P + _A) + _IN,                    # X0,w,Q,P -> out
     "k_bprep_s": (2 * _A + 5 * _P) + 5 * _P,                # A,P,e,k,decay,K,Q -> dU,Wk,At1,B1t,Ant
-    "state_s_bwd": 5 * _P + (_S + _P),                      # Wk,dU,Ant,At1,B1t -> lambda slot, dw
-    "state_c_bwd": 5 * _P + (_S + _P),
+    "state_s_bwd": 4 * _P + _IN + (_S + _P),                # Wk,dU,Ant,At1, B1t (bf16) -> lambda slot, dw
+    "state_c_bwd": 4 * _P + _IN + (_S + _P),
     "k_grad_s": (6 * _P + _IN + 3 * _S) + 4 * _P,           # dw,w,d,e,chi,decay,dO,X0,XC,lambda -> dchi,dd,de,dg
     "k_src_bwd": (6 * _IN + 5 * _P) + (3 * _P + 4 * _IN),   # inputs,delta,d*,dw -> du,dk,ddelta,dq,dv,der,dwr
     "k_bprep_c": (_A + 2 * _IN + 4 * _P) + 7 * _P,          # A,u,k,decay,K,dd,ddelta -> k,dU,u,Ant,At1,B1t,Wk
-    "k_grad_c": (7 * _P + 3 * _S) + 4 * _P,                 # dw,delta,dd,k,u,d,decay,X0,XC,lambda -> dx,dk,dg,dq
-    "k_final": (3 * _IN + 8 * _P) + (3 * _IN + _P),         # u,h,k, 8 partial grads -> du,dh,dk,dlog_decay
+    "k_grad_c": (8 * _P + 3 * _S) + 4 * _P,                 # dw,delta,dd,k,u,d,decay,dg(S),X0,XC,lambda -> dx,dk,dq,dg
+    "k_final": (3 * _IN + 6 * _P) + 3 * _IN,                # u,h,k, 6 partial grads -> du,dh,dk
 }
 
 # HBM bytes per dispatch of each kernel at this workload, from rocprofv3 counter
