@@ -654,6 +654,23 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   // panels that read d and chi as they are, then d's Gram form staged once for
   // both decayed Grams below (in d's own storage; the wild fix-ups read the
   // global copy of d)
+  // the decayed keys K^ = d e^{G_C - G} (chunk-transposed, fragment order) are
+  // formed from d while it is still in LDS and stored after the P Gram
+  constexpr int KPC = KD * BT / 8 / CT;  // pieces per thread
+  bf16x8 ksh[KPC], ksl[KPC];
+#pragma unroll
+  for (int q = 0; q < KPC; ++q) {
+    const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
+    const int c = (block / (BT / 32)) * 16 + (lane & 15);
+    const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 a, b2;
+      split_bf(s.Pc[i0 + e][c] * __expf(cd.G[BT - 1][c] - cd.G[i0 + e][c]), a, b2);
+      ksh[q][e] = a;
+      ksl[q][e] = b2;
+    }
+  }
   stage_ytilde(s.Kp, cd, [&](int j, int c) { return s.Pc[j][c]; });
   const float* const dg_ = p.d + rowbase * KD;
   auto Draw = [&](int j, int c) { return dg_[j * KD + c]; };
@@ -661,9 +678,12 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pb[i][c]; }, s.Kp, Draw, false, s.M);
   store_frag_panel<BT, BT>(p.Ps.hi, p.Ps.lo, cidx * BT * BT,
                            [&](int i, int j) { return s.M[i * LS + j]; });
-  store_frag_panel<KD, BT>(p.Ks.hi, p.Ks.lo, cidx * KD * BT, [&](int c, int i) {
-    return dg_[i * KD + c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
-  });
+#pragma unroll
+  for (int q = 0; q < KPC; ++q) {
+    const long long o = cidx * KD * BT + (long long)(threadIdx.x + q * CT) * 8;
+    *reinterpret_cast<bf16x8*>(p.Ks.hi + o) = ksh[q];
+    *reinterpret_cast<bf16x8*>(p.Ks.lo + o) = ksl[q];
+  }
   store_frag_panel<BT, KD>(p.Qs.hi, p.Qs.lo, rowbase * KD,
                            [&](int i, int c) { return s.Pb[i][c] * __expf(cd.G[i][c]); });
   __syncthreads();
