@@ -82,10 +82,10 @@ BYTES_PER_CHUNK = {
 # profiles/fwd_bwd_B4_T2048_H8_d128_hbm_traffic.txt.  Static figures: a kernel
 # change needs a new counter run.
 TRAFFIC_MB = {
-    "k_prep_c": 185.8, "state_c_fwd": 207.1, "k_prep_s": 556.6, "state_s_fwd": 207.1,
-    "k_out_s": 163.7, "k_bprep_s": 366.9, "state_s_bwd": 271.3, "state_c_bwd": 271.3,
-    "k_grad_s": 554.3, "k_src_bwd": 436.3, "k_bprep_c": 453.7, "k_grad_c": 735.1,
-    "k_final": 403.6,
+    "k_prep_c": 185.8, "state_c_fwd": 207.1, "k_prep_s": 527.5, "state_s_fwd": 207.1,
+    "k_out_s": 163.7, "k_bprep_s": 350.1, "state_s_bwd": 254.5, "state_c_bwd": 254.5,
+    "k_grad_s": 554.3, "k_src_bwd": 436.3, "k_bprep_c": 453.7, "k_grad_c": 715.7,
+    "k_final": 302.8,
 }
 
 
