@@ -466,12 +466,10 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   const float* g = (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
                    (long long)hh * in.log_decay.sh;
   SD_MARK(2, 0);
-  build_decay(s.cd, g, in.log_decay.st, t0, T, r);
-  SD_MARK(2, 1);
-  const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id();
-{
-    const int cl = l & 15;  // every row's loads first (see k_prep_c)
+  {
+    const int cl = l & 15;
+    // the rows' u / k loads are issued first: their latency overlaps the decay build
     float ux[2][RQ], kx[2][RQ];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -479,6 +477,8 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       load_row16(in.u, b, t, hh, T, r, ux[g]);
       load_row16(in.k, b, t, hh, T, r, kx[g]);
     }
+    build_decay(s.cd, g, in.log_decay.st, t0, T, r);
+    SD_MARK(2, 1);
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
@@ -493,6 +493,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   }
   __syncthreads();
   SD_MARK(2, 2);
+  const ChunkDecay& cd = s.cd;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long cidx = (long long)n * p.NT + ch;
   const float* delta = p.delta + rowbase * KD;
