@@ -273,32 +273,41 @@ struct ChunkDecay {
 
 // Loads g (fp32, [B,T,H,r] strided, token stride st, row pointer base at
 // token t0) and builds G, R and the wild lists.  Tokens >= T load 0 (neutral).
-__device__ __forceinline__ void build_decay(ChunkDecay& cd, const float* g, long long st, int t0, int T,
-                                   int r) {
-  const int tid = threadIdx.x;
-  if (tid < KD) {
-    const int c = tid;
-    float x[BT];
+// The chunk's log-decays in registers: thread (J, c) = (tid / 128, tid % 128)
+// holds rows J*16 .. J*16+15 of column c (clamped addresses + select: a guarded
+// load would branch and wait).
+__device__ __forceinline__ void decay_load(const float* g, long long st, int t0, int T, int r,
+                                           float (&x)[BS]) {
+  const int c = threadIdx.x & (KD - 1), J = threadIdx.x / KD;
 #pragma unroll
-    for (int i = 0; i < BT; ++i) {  // all loads in flight before the scan
-      const int t = t0 + i;
-      // clamped address + select (a guarded load would branch and wait)
-      const float v = g[(long long)(t < T ? t : T - 1) * st + (c < r ? c : r - 1)];
-      x[i] = keep_if(t < T && c < r, v);
-    }
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < BT; ++i) {
-      acc += x[i];
-      cd.G[i][c] = acc;
-    }
-    cd.R[0][c] = 0.f;
-    for (int J = 1; J < NB; ++J) cd.R[J][c] = cd.G[J * BS - 1][c];
-    for (int J = 0; J < NB; ++J) {
-      float drop = cd.R[J][c] - cd.G[J * BS + BS - 1][c];
-      cd.wild[J][c] = drop > TAU ? 1 : 0;
-    }
+  for (int i = 0; i < BS; ++i) {
+    const int t = t0 + J * BS + i;
+    const float v = g[(long long)(t < T ? t : T - 1) * st + (c < r ? c : r - 1)];
+    x[i] = keep_if(t < T && c < r, v);
   }
+}
+
+// Prefix tables from decay_load's registers: each thread scans its 16 rows, the
+// four block totals of a column give each block's offset.
+__device__ __forceinline__ void decay_build(ChunkDecay& cd, float (&x)[BS]) {
+  static_assert(CT == NB * KD, "one thread per (block, column)");
+  const int tid = threadIdx.x, c = tid & (KD - 1), J = tid / KD;
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < BS; ++i) {
+    acc += x[i];
+    x[i] = acc;
+  }
+  cd.R[J][c] = acc;  // block totals for now
+  __syncthreads();
+  float off = 0.f;
+#pragma unroll
+  for (int K = 0; K < NB - 1; ++K) off += K < J ? cd.R[K][c] : 0.f;
+  __syncthreads();  // every total read
+#pragma unroll
+  for (int i = 0; i < BS; ++i) cd.G[J * BS + i][c] = off + x[i];
+  cd.R[J][c] = off;
+  cd.wild[J][c] = off - (off + x[BS - 1]) > TAU ? 1 : 0;
   __syncthreads();
   {  // wild lists: wave J scans block J's coordinates with ballots
     const int w = tid >> 6, l = tid & 63;
@@ -313,6 +322,13 @@ __device__ __forceinline__ void build_decay(ChunkDecay& cd, const float* g, long
     }
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ void build_decay(ChunkDecay& cd, const float* g, long long st, int t0, int T,
+                                            int r) {
+  float x[BS];
+  decay_load(g, st, t0, T, r, x);
+  decay_build(cd, x);
 }
 
 // exp(x) on a non-wild coordinate, 0 on a wild one, without a branch (a
@@ -405,6 +421,7 @@ __device__ __forceinline__ f4 mma16s(const float* av, const float* bv, f4 acc) {
 // Diagonal 16x16 blocks by forward substitution (one lane per column), then
 // off-diagonal blocks A_IJ = -A_II * sum_{K=J}^{I-1} L_IK A_KJ by distance.
 // tmp: 64 x LS scratch.
+template <int MS = -1>
 __device__ void unit_lower_inverse(float* L, float* tmp) {
   const int tid = threadIdx.x;
   // Phase 0: diagonal blocks.  Thread (B, j): block B = tid/16 (tid < 64), column j.
@@ -419,12 +436,14 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
       col[i] = (i >= j) ? s : 0.f;
     }
   }
+  if constexpr (MS >= 0) SD_MARK(MS, 20);
   __syncthreads();
   if (tid < NB * BS) {
     const int B = tid / BS, j = tid % BS, B0 = B * BS;
     for (int i = 0; i < BS; ++i) tmp[(B0 + i) * LS + B0 + j] = col[i];
   }
   __syncthreads();
+  if constexpr (MS >= 0) SD_MARK(MS, 21);
   // tmp holds the diagonal inverses; L still holds the strict lower part.
   // Off-diagonal blocks by distance, one wave per block, on the K=16 MFMA:
   //   T = sum_{K=J}^{I-1} L_IK A_KJ,   A_IJ = -A_II T.
@@ -456,6 +475,7 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
       for (int e = 0; e < 4; ++e) tmp[(I * BS + r4 + e) * LS + J * BS + m] = -a[e];
     }
     __syncthreads();
+    if constexpr (MS >= 0) SD_MARK(MS, 21 + dist);
   }
   // Copy back: A lower (incl. diagonal), zero upper.
   for (int idx = tid; idx < BT * BT; idx += CT) {

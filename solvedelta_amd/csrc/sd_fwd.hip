@@ -68,7 +68,9 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   const sd_inputs& in = p.in;
   const float* g = (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
                    (long long)hh * in.log_decay.sh;
+  SD_MARK(0, 0);
   build_decay(s.cd, g, in.log_decay.st, t0, T, r);
+  SD_MARK(0, 1);
   const int w = wave_id(), l = lane_id();
   if (threadIdx.x < BT) {  // branch-free: clamped token, then select
     const int t = t0 + threadIdx.x;
@@ -98,13 +100,16 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     }
   }
   __syncthreads();
+  SD_MARK(0, 2);
   const ChunkDecay& cd = s.cd;
   // L_ij = gamma_i sum_c u_ic u_jc exp(G_{i-1,c} - G_jc), j < i
   stage_ytilde(s.Yt, cd, [&](int j, int c) { return s.Uh[j][c]; });
   decayed_gram_yt<true>(
       cd, [&](int i, int c) { return s.gam[i] * s.Uh[i][c]; }, s.Yt,
       [&](int j, int c) { return s.Uh[j][c]; }, true, s.M);
-  unit_lower_inverse(s.M, s.tmp);
+  SD_MARK(0, 3);
+  unit_lower_inverse<0>(s.M, s.tmp);
+  SD_MARK(0, 4);
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.Ac[((long long)n * p.NT + ch) * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
   // W = A diag(gamma) (u e^{Gexcl}),  U = A diag(gamma) h
@@ -129,12 +134,14 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
       }
     }
   }
+  SD_MARK(0, 5);
   // decayed keys (transposed per chunk) and chunk decay
   const long long cbase = ((long long)n * p.NT + ch);
   store_frag_panel<KD, BT>(p.Kc.hi, p.Kc.lo, cbase * KD * BT, [&](int c, int i) {
     return s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
   });
   if (threadIdx.x < KD) p.Gam[cbase * KD + threadIdx.x] = __expf(cd.G[BT - 1][threadIdx.x]);
+  SD_MARK(0, 6);
 }
 
 // ---------------------------------------------------------------------------

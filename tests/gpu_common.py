@@ -11,7 +11,9 @@ from oracle.sd_oracle import OracleState, solvedelta_oracle_raw
 def make_inputs(B, T, H, r, V, *, seed=0, device="cuda", decay="softplus", gamma=0.9,
                 gamma_shape="BTH", requires_grad=False, gate_scale=1.0):
     """Config-1 style inputs: u,h,q,k,v ~ N(0,1) bf16 (q,k per-head L2-normalised),
-    raw erase/write ~ N(0,1), log-decay = -softplus(N(0,1)), gamma constant."""
+    raw erase/write ~ N(0,1), log-decay = -softplus(N(0,1)), gamma constant.
+    Other decays: "small" (near 1), "extreme" (-100, every block wild), "mixed"
+    (wild and ordinary coordinates side by side), anything else zero."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     n = lambda *s: torch.randn(*s, generator=g)
     u, h = n(B, T, H, r), n(B, T, H, r)
@@ -25,6 +27,13 @@ def make_inputs(B, T, H, r, V, *, seed=0, device="cuda", decay="softplus", gamma
         gd = -0.02 * torch.rand(B, T, H, r, generator=g)
     elif decay == "extreme":
         gd = torch.full((B, T, H, r), -100.0)
+    elif decay == "mixed":
+        # three tiers of coordinates: x8 (16-token block drops ~100, always past
+        # the kernels' wild threshold of 30), x2.5 (drops ~32: wild in some blocks
+        # only) and x1 (~13, never), so exact wild fix-ups and ordinary
+        # coordinates meet in one block
+        fast = torch.tensor([8.0, 2.5, 1.0]).repeat(r // 3 + 1)[:r]
+        gd = -F.softplus(n(B, T, H, r)) * fast
     else:
         gd = torch.zeros(B, T, H, r)
     if gamma_shape == "BTH":

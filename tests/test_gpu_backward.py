@@ -55,6 +55,8 @@ def _report(tag, grads, rgrads, bound, names=None):
     (1, 200, 1, 128, 128, 5, "softplus"),
     (1, 19, 2, 16, 16, 6, "small"),
     (1, 70, 2, 20, 12, 8, "softplus"),   # widths not a multiple of 8: element-wise row loads
+    (1, 130, 2, 32, 24, 31, "mixed"),    # wild and ordinary coordinates in one block
+    (1, 128, 1, 128, 128, 32, "mixed"),
 ])
 def test_backward_matches_oracle(B, T, H, r, V, seed, decay):
     print(f"case B{B} T{T} H{H} r{r} V{V} {decay}", flush=True)

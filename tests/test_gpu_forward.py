@@ -36,6 +36,8 @@ def _check(out, st, eo, es, tag, frob=1e-2):
     (1, 19, 2, 16, 16, 6, "small", True),
     (1, 1, 2, 16, 16, 7, "small", True),
     (1, 70, 2, 20, 12, 8, "softplus", True),   # widths not a multiple of 8: element-wise row loads
+    (1, 130, 2, 32, 24, 31, "mixed", True),    # wild and ordinary coordinates in one block
+    (1, 128, 1, 128, 128, 32, "mixed", True),
 ])
 def test_forward_matches_oracle(B, T, H, r, V, seed, decay, with_state):
     args = make_inputs(B, T, H, r, V, seed=seed, decay=decay)
