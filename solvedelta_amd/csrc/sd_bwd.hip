@@ -5,12 +5,14 @@
 // d, e, chi, w).  For each op (S memory first, then C predictor):
 //   k_bprep_*   chunk-parallel: dU = (P A)^T rhs (+ A^T ext), Wk = A^T K^,
 //               and the reverse-pass injection panels;
-//   k_state<false> with rev = 1: lambda <- Gamma lambda + A1 B1 - x~^T dw,
+//   k_state<true, true> (rev = 1): lambda <- Gamma lambda + A1 B1 - x~^T dw,
 //               dw = dU + Wk lambda, storing the chunk-end cotangents;
 //   k_grad_*    chunk-parallel closed-form gradients of (k, x, v, q) and the
-//               in-chunk reverse cumulative sum that closes the decay gradient.
+//               in-chunk reverse cumulative sum that closes the decay gradient
+//               (k_grad_s writes the S side's log-decay gradient to the output,
+//               k_grad_c adds the C side's).
 // Between the ops k_src_bwd transposes the dual sources (phi, den, e, chi, z)
-// and the q/erase/write/value gates; k_final closes u, k, h, gamma, log-decay.
+// and the q/erase/write/value gates; k_final closes u, k, h and gamma.
 // The closed forms are the ones checked against FP64 autograd in
 // tests/chunk_model.py (Op.backward, sources_bwd, backward_seq).
 #include "sd_common.cuh"
@@ -942,7 +944,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Final closure: u, k, h, gamma, log-decay.  One wave per token.
+// Final closure: u, k, h, gamma.  One wave per token.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(NTHREADS) void k_final(BwdParams p) {
   const int n = blockIdx.y, b = n / p.H, hh = n % p.H;

@@ -3,11 +3,12 @@
 // Pipeline for one call (n = b*H + h sequences, NT chunks of 64 tokens):
 //   k_prep_c   (chunk-parallel) predictor C: norms, decayed Gram L_C, (I+L_C)^-1,
 //              WY panels W_C, U_C, decayed keys, chunk decay;
-//   k_state<false> (sequential per sequence x 16-column tile) C state pass:
-//              delta = U - W X0, X <- Gamma X + K^T delta (X = C^T);
+//   k_state<false, false> (sequential per sequence x 16-column tile) C state
+//              pass: delta = U - W X0, X <- Gamma X + K^T delta (X = C^T);
 //   k_prep_s   (chunk-parallel) primal d = k + C^T k, dual sources e, chi, z,
 //              then the S memory's Gram, inverse, WY panels and output pair P;
-//   k_state<true>  S state pass with the chunk output o = Q X0 + P w fused in.
+//   k_state<false, false> S state pass: chunk-entering slots and w;
+//   k_out_s    (chunk-parallel) readout o = Q~ X0 + P w from the saved slots.
 // The algebra is the generic pre-decay-read delta op: see the SolveDelta
 // chunk derivation restated in tests/chunk_model.py.
 #include "sd_common.cuh"
