@@ -754,12 +754,38 @@ struct OutParams {
   __bf16* out;      // [B,T,H,V]
 };
 
+// The chunk's Q~ and P panels, copied once (fragment order kept): every wave
+// reads all of their rows, so from L2 they would be fetched eight times.
+struct OutSmem {
+  __bf16 qh[BT * KD], ql[BT * KD];
+  __bf16 ph[BT * BT], pl[BT * BT];
+};
+
 __global__ __launch_bounds__(CT) void k_out_s(OutParams p) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  OutSmem& s = *reinterpret_cast<OutSmem*>(smem_raw);
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H;
   const int cb = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + ch * BT;
   const float* X0 = p.Xs + ((long long)n * (p.NT + 1) + ch) * KD * KD;
   const float* wv = p.w + rowbase * KD;
+  constexpr int QP = BT * KD / 8 / CT, PP = BT * BT / 8 / CT;  // 16-byte pieces per thread
+  bf16x8 vq[2][QP], vp[2][PP];  // loaded first, written to LDS after the X0 / w loads are issued
+  {
+    static_assert(QP * CT * 8 == BT * KD && PP * CT * 8 == BT * BT, "whole pieces");
+#pragma unroll
+    for (int q = 0; q < QP; ++q) {
+      const long long o = rowbase * KD + (long long)(threadIdx.x + q * CT) * 8;
+      vq[0][q] = *reinterpret_cast<const bf16x8*>(p.Q.hi + o);
+      vq[1][q] = *reinterpret_cast<const bf16x8*>(p.Q.lo + o);
+    }
+#pragma unroll
+    for (int q = 0; q < PP; ++q) {
+      const long long o = cidx * BT * BT + (long long)(threadIdx.x + q * CT) * 8;
+      vp[0][q] = *reinterpret_cast<const bf16x8*>(p.P.hi + o);
+      vp[1][q] = *reinterpret_cast<const bf16x8*>(p.P.lo + o);
+    }
+  }
   // B operands (column block cb): X0 over K = 128 state rows, w over the 64 tokens
   float xr[4][8], wr[2][8];
 #pragma unroll
@@ -770,6 +796,18 @@ __global__ __launch_bounds__(CT) void k_out_s(OutParams p) {
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
     for (int e = 0; e < 8; ++e) wr[ks][e] = wv[(ks * 32 + kq + e) * KD + cb * 16 + m];
+#pragma unroll
+  for (int q = 0; q < QP; ++q) {
+    const int o = (threadIdx.x + q * CT) * 8;
+    *reinterpret_cast<bf16x8*>(s.qh + o) = vq[0][q];
+    *reinterpret_cast<bf16x8*>(s.ql + o) = vq[1][q];
+  }
+#pragma unroll
+  for (int q = 0; q < PP; ++q) {
+    const int o = (threadIdx.x + q * CT) * 8;
+    *reinterpret_cast<bf16x8*>(s.ph + o) = vp[0][q];
+    *reinterpret_cast<bf16x8*>(s.pl + o) = vp[1][q];
+  }
   Frag bx[4], bw[2];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
@@ -790,13 +828,22 @@ __global__ __launch_bounds__(CT) void k_out_s(OutParams p) {
       bw[ks].l[e] = lo;
     }
   const int col = cb * 16 + m;
+  __syncthreads();  // Q~ and P staged
 #pragma unroll
   for (int I = 0; I < NB; ++I) {
     Frag q[4], pf[2];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) q[ks] = ldfrag(p.Q, rowbase * KD + frag_off(I * BS + m, ks * 32 + kq, KD));
+    for (int ks = 0; ks < 4; ++ks) {
+      const int o = (int)frag_off(I * BS + m, ks * 32 + kq, KD);
+      q[ks].h = *reinterpret_cast<const bf16x8*>(s.qh + o);
+      q[ks].l = *reinterpret_cast<const bf16x8*>(s.ql + o);
+    }
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) pf[ks] = ldfrag(p.P, cidx * BT * BT + frag_off(I * BS + m, ks * 32 + kq, BT));
+    for (int ks = 0; ks < 2; ++ks) {
+      const int o = (int)frag_off(I * BS + m, ks * 32 + kq, BT);
+      pf[ks].h = *reinterpret_cast<const bf16x8*>(s.ph + o);
+      pf[ks].l = *reinterpret_cast<const bf16x8*>(s.pl + o);
+    }
     f4 acc = zero4();
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mma3f(q[ks], bx[ks], acc);
@@ -852,7 +899,8 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   OutParams op{};
   op.H = in->H; op.T = in->T; op.NT = NT; op.Tp = Tp; op.V = in->V;
   op.Xs = w.Xs; op.w = w.wS; op.Q = w.Qs; op.P = w.Ps; op.out = (__bf16*)out;
-  SD_LAUNCH("k_out_s", k_out_s, dim3(NT, n), dim3(CT), 0, st, op);
+  SD_SMEM_ONCE(k_out_s, (int)sizeof(OutSmem));
+  SD_LAUNCH("k_out_s", k_out_s, dim3(NT, n), dim3(CT), sizeof(OutSmem), st, op);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 
