@@ -761,7 +761,7 @@ struct GradCSmem {
   float gam[BT];
   float rsum[4][KD];  // rowsum(X_C (.) lambda) partials
   LPanel PA;  // dw, then dd e^G
-  LPanel PW;  // delta
+  LPanel PW;  // delta, then the P' Gram's staged Y side
 };
 
 __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
@@ -869,6 +869,20 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       vv[I][e] = So[I][e] * Sdd[I][e] - Su[I][e] * dk + xs[I][e];
     }
   }
+  // the P' Gram's Y side (u e^{R_J - G}, 0 on wild coordinates), staged split
+  // from this wave's u slab into the dead delta panel (its last reader was the
+  // key product; dq gathers its delta operand from global memory)
+  LPanel& Yt = s.PW;
+#pragma unroll
+  for (int J = 0; J < NB; ++J)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = J * BS + r4 + e;
+      __bf16 hi, lo;
+      split_bf(Su[J][e] * exp_unless_wild(cd.wild[J][c] != 0, cd.R[J][c] - cd.G[j][c]), hi, lo);
+      Yt.h[j][c] = hi;
+      Yt.l[j][c] = lo;
+    }
   // dg_i = rowsum + sum_{i' >= i} dg_i' + sum_{i' > i} xdx_i'
   close_decay_column(vv, s.rsum, cb);
   // the C side's part of the log-decay gradient, added to the S side's (written
@@ -887,9 +901,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       }
   }
   SD_MARK(3, 6);
-  __syncthreads();  // M1 free: P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) into M1
-  decayed_gram<false>(
-      cd, [&](int i, int cc) { return ddp[i * KD + cc]; }, [&](int j, int cc) { return uh[j * KD + cc]; },
+  __syncthreads();  // M1 free, Yt staged: P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) into M1
+  decayed_gram_yt<false>(
+      cd, [&](int i, int cc) { return ddp[i * KD + cc]; }, Yt, [&](int j, int cc) { return uh[j * KD + cc]; },
       false, s.M1);
   SD_MARK(3, 7);
   // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
@@ -909,18 +923,17 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       }
       split_blk(raw, BX);
     }
-    // P' delta: the delta column block's stored hi / lo halves are the B operand
-    // as they are (gathered once for the four row blocks)
+    // P' delta: the delta column block gathered once for the four row blocks
     Frag pw[2];
     {
       const int m = l & 15, kq = (l >> 4) * 8;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks) {
+        float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pw[ks].h[e] = s.PW.h[ks * 32 + kq + e][cb * 16 + m];
-          pw[ks].l[e] = s.PW.l[ks * 32 + kq + e][cb * 16 + m];
-        }
+        for (int e = 0; e < 8; ++e) v[e] = wv[(ks * 32 + kq + e) * KD + cb * 16 + m];
+        pw[ks] = split8(v);
+      }
     }
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
