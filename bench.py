@@ -82,9 +82,9 @@ BYTES_PER_CHUNK = {
 # profiles/fwd_bwd_B4_T2048_H8_d128_hbm_traffic.txt.  Static figures: a kernel
 # change needs a new counter run.
 TRAFFIC_MB = {
-    "k_prep_c": 185.8, "state_c_fwd": 207.1, "k_prep_s": 527.5, "state_s_fwd": 207.1,
-    "k_out_s": 163.7, "k_bprep_s": 350.1, "state_s_bwd": 254.5, "state_c_bwd": 254.5,
-    "k_grad_s": 554.3, "k_src_bwd": 436.3, "k_bprep_c": 453.7, "k_grad_c": 715.7,
+    "k_prep_c": 185.7, "state_c_fwd": 207.1, "k_prep_s": 527.7, "state_s_fwd": 207.1,
+    "k_out_s": 167.9, "k_bprep_s": 350.3, "state_s_bwd": 254.5, "state_c_bwd": 254.5,
+    "k_grad_s": 554.2, "k_src_bwd": 436.3, "k_bprep_c": 453.6, "k_grad_c": 717.3,
     "k_final": 302.8,
 }
 
@@ -131,10 +131,13 @@ def cpu_baseline(budget_s=24.0):
         torch.autograd.grad(o, ins + st, dO.double())
         return time.perf_counter() - t0
 
-    tt, dt = 64, run(64)
-    while dt * 2.2 < budget_s and tt < T:
+    # the next doubling is predicted from the last one's growth (autograd over a
+    # token loop grows faster than linearly in T at the larger samples)
+    tt, dt, grow = 64, run(64), 2.2
+    while dt * grow < budget_s and tt < T:
         tt *= 2
-        dt = run(tt)
+        prev, dt = dt, run(tt)
+        grow = max(2.2, dt / prev)
     return {"value": B * tt / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"FP64 torch token-loop oracle F+VJP, B={B} H={H} r=V={R}, T={tt} "
                       f"({dt:.1f} s)"}
