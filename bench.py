@@ -71,8 +71,9 @@ BYTES_PER_CHUNK = {
     "state_c_bwd": 4 * _P + _IN + (_S + _P),
     "k_grad_s": (6 * _P + _IN + 3 * _S) + 4 * _P,           # dw,w,d,e,chi,decay,dO,X0,XC,lambda -> dchi,dd,de,dg
     "k_src_bwd": (6 * _IN + 5 * _P) + (3 * _P + 4 * _IN),   # inputs,delta,d*,dw -> du,dk,ddelta,dq,dv,der,dwr
-    "k_bprep_c": (_A + 2 * _IN + 4 * _P) + 7 * _P,          # A,u,k,decay,K,dd,ddelta -> k,dU,u,Ant,At1,B1t,Wk
-    "k_grad_c": (8 * _P + 3 * _S) + 4 * _P,                 # dw,delta,dd,k,u,d,decay,dg(S),X0,XC,lambda -> dx,dk,dq,dg
+    "k_bprep_c": (_A + 2 * _IN + 4 * _P) + (7 * _P + _A),   # A,u,k,decay,K,dd,ddelta -> k,dU,u,Ant,At1,B1t,Wk,P'
+
+    "k_grad_c": (8 * _P + 3 * _S + _A) + 4 * _P,            # dw,delta,dd,k,u,d,decay,dg(S),X0,XC,lambda,P' -> dx,dk,dq,dg
     "k_final": (3 * _IN + 6 * _P) + 3 * _IN,                # u,h,k, 6 partial grads -> du,dh,dk
 }
 

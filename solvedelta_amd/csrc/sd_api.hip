@@ -69,6 +69,7 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
                       &w.dd, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
                       &w.uh};
   for (float** pp : panels) *pp = c.take<float>(panel);
+  w.Pp = c.take<float>(n * NT * kBT * kBT);
   if (total) *total = c.off + 256;
   return w;
 }

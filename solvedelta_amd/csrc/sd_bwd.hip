@@ -656,6 +656,14 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       false, s.P);
   mat64_mul(s.P, s.A, s.N);
   __syncthreads();
+  // P' is also the C chunk gradient's dq operand: stored once here (upper
+  // blocks zero) instead of formed again there
+  for (int idx = threadIdx.x * 4; idx < BT * BT; idx += CT * 4) {
+    const int i = idx / BT, j = idx % BT;
+    const float4 v = *reinterpret_cast<const float4*>(&s.P[i * LS + j]);
+    *reinterpret_cast<float4*>(p.g.Pp + cidx * BT * BT + idx) =
+        (j / BS > i / BS) ? make_float4(0.f, 0.f, 0.f, 0.f) : v;
+  }
   const float* ddl = p.g.ddelta + rowbase * KD;
   const long long kbase = cidx * KD * BT;
   f4 wks[NB], dus[NB];
@@ -761,7 +769,7 @@ struct GradCSmem {
   float gam[BT];
   float rsum[4][KD];  // rowsum(X_C (.) lambda) partials
   LPanel PA;  // dw, then dd e^G
-  LPanel PW;  // delta, then the P' Gram's staged Y side
+  LPanel PW;  // delta
 };
 
 __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
@@ -846,6 +854,15 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) Sx[J][e] = s.gam[J * BS + r4 + e] * Su[J][e];
   SD_MARK(3, 5);
+  // P' (formed by the C chunk's backward prep): loaded now, written into M1 as
+  // soon as every apply below has read it, and used by the dq product at the end
+  constexpr int PPC = BT * BT / 4 / CT;
+  float4 ppv[PPC];
+  {
+    const float* const pp = p.g.Pp + ((long long)n * p.NT + ch) * BT * BT;
+#pragma unroll
+    for (int q = 0; q < PPC; ++q) ppv[q] = *reinterpret_cast<const float4*>(pp + (threadIdx.x + q * CT) * 4);
+  }
   // chunk-uniform output bases, 32-bit lane offsets (keeps addresses out of VGPR pairs)
   float* const dx_b = p.g.dxC + rowbase * KD;
   float* const dk_b = p.g.dkC + rowbase * KD;
@@ -869,20 +886,12 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       vv[I][e] = So[I][e] * Sdd[I][e] - Su[I][e] * dk + xs[I][e];
     }
   }
-  // the P' Gram's Y side (u e^{R_J - G}, 0 on wild coordinates), staged split
-  // from this wave's u slab into the dead delta panel (its last reader was the
-  // key product; dq gathers its delta operand from global memory)
-  LPanel& Yt = s.PW;
+  __syncthreads();  // every apply has read M1
 #pragma unroll
-  for (int J = 0; J < NB; ++J)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int j = J * BS + r4 + e;
-      __bf16 hi, lo;
-      split_bf(Su[J][e] * exp_unless_wild(cd.wild[J][c] != 0, cd.R[J][c] - cd.G[j][c]), hi, lo);
-      Yt.h[j][c] = hi;
-      Yt.l[j][c] = lo;
-    }
+  for (int q = 0; q < PPC; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 4;
+    *reinterpret_cast<float4*>(&s.M1[(idx / BT) * LS + idx % BT]) = ppv[q];
+  }
   // dg_i = rowsum + sum_{i' >= i} dg_i' + sum_{i' > i} xdx_i'
   close_decay_column(vv, s.rsum, cb);
   // the C side's part of the log-decay gradient, added to the S side's (written
@@ -901,10 +910,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       }
   }
   SD_MARK(3, 6);
-  __syncthreads();  // M1 free, Yt staged: P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) into M1
-  decayed_gram_yt<false>(
-      cd, [&](int i, int cc) { return ddp[i * KD + cc]; }, Yt, [&](int j, int cc) { return uh[j * KD + cc]; },
-      false, s.M1);
+  __syncthreads();  // P' in M1; PA (dd e^G) staged
   SD_MARK(3, 7);
   // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
   {
@@ -923,17 +929,18 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       }
       split_blk(raw, BX);
     }
-    // P' delta: the delta column block gathered once for the four row blocks
+    // P' delta: the delta column block's stored hi / lo halves are the B operand
+    // as they are (gathered once for the four row blocks)
     Frag pw[2];
     {
       const int m = l & 15, kq = (l >> 4) * 8;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        float v[8];
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = wv[(ks * 32 + kq + e) * KD + cb * 16 + m];
-        pw[ks] = split8(v);
-      }
+        for (int e = 0; e < 8; ++e) {
+          pw[ks].h[e] = s.PW.h[ks * 32 + kq + e][cb * 16 + m];
+          pw[ks].l[e] = s.PW.l[ks * 32 + kq + e][cb * 16 + m];
+        }
     }
 #pragma unroll
     for (int I = 0; I < NB; ++I) {

@@ -123,6 +123,7 @@ struct BwdWs {
   float* ddelta; float* du_src; float* dk_src;
   float* dkC; float* dxC; float* dqC;
   float* uh;  // normalised u
+  float* Pp;  // P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) of the C op  [n][NT][64][64]
 };
 
 int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void* dout,
