@@ -307,11 +307,8 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
 // the same elements of X_C, and leaves rowsum_c(X_C (.) lambda) partials (one
 // per 32-column lane group) in rsum[g][c], so the closure need not read either
 // 64 KiB block again.
-__device__ __forceinline__ void load_lam_rowsum(const float* lam, const float* XC, int cb, BlkS& BL,
-                                                float (*rsum)[KD]) {
-  Blk rl, rx;
-  load_blk(rl, lam + cb * 16 * KD, KD);
-  load_blk(rx, XC + cb * 16 * KD, KD);
+__device__ __forceinline__ void lam_rowsum(const Blk& rl, const Blk& rx, int cb, BlkS& BL,
+                                           float (*rsum)[KD]) {
   float acc = 0.f;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
@@ -322,6 +319,14 @@ __device__ __forceinline__ void load_lam_rowsum(const float* lam, const float* X
   const int l = lane_id();
   rsum[l >> 4][cb * 16 + (l & 15)] = acc;
   split_blk(rl, BL);
+}
+
+__device__ __forceinline__ void load_lam_rowsum(const float* lam, const float* XC, int cb, BlkS& BL,
+                                                float (*rsum)[KD]) {
+  Blk rl, rx;
+  load_blk(rl, lam + cb * 16 * KD, KD);
+  load_blk(rx, XC + cb * 16 * KD, KD);
+  lam_rowsum(rl, rx, cb, BL, rsum);
 }
 
 // Decay-gradient closure for this wave's 16 columns, in registers: v holds the
@@ -803,6 +808,12 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
   SD_MARK(3, 1);
   const ChunkDecay& cd = s.cd;
+  // this wave's X0, lambda and X_C row blocks: loads issued ahead of the two
+  // LDS Grams so their latency overlaps them
+  Blk bX0, bLam, bXC;
+  load_blk(bX0, X0 + cb * 16 * KD, KD);
+  load_blk(bLam, lam + cb * 16 * KD, KD);
+  load_blk(bXC, XC + cb * 16 * KD, KD);
   // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
   lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
   lds_pair(nullptr, kh, s.PW, s.M2, false);
@@ -810,8 +821,8 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   f4 a[NB], kl[NB];
   {
     BlkS BX, BL;
-    load_split_blk_g(X0 + cb * 16 * KD, BX);
-    load_lam_rowsum(lam, XC, cb, BL, s.rsum);
+    split_blk(bX0, BX);
+    lam_rowsum(bLam, bXC, cb, BL, s.rsum);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       BlkS A;
