@@ -83,9 +83,9 @@ BYTES_PER_CHUNK = {
 # profiles/fwd_bwd_B4_T2048_H8_d128_hbm_traffic.txt.  Static figures: a kernel
 # change needs a new counter run.
 TRAFFIC_MB = {
-    "k_prep_c": 185.7, "state_c_fwd": 207.1, "k_prep_s": 527.7, "state_s_fwd": 207.1,
-    "k_out_s": 167.9, "k_bprep_s": 350.3, "state_s_bwd": 254.5, "state_c_bwd": 254.5,
-    "k_grad_s": 554.2, "k_src_bwd": 436.3, "k_bprep_c": 453.6, "k_grad_c": 717.3,
+    "k_prep_c": 185.7, "state_c_fwd": 207.1, "k_prep_s": 524.6, "state_s_fwd": 207.1,
+    "k_out_s": 167.9, "k_bprep_s": 350.5, "state_s_bwd": 254.5, "state_c_bwd": 254.5,
+    "k_grad_s": 554.2, "k_src_bwd": 436.3, "k_bprep_c": 470.4, "k_grad_c": 708.1,
     "k_final": 302.8,
 }
 
