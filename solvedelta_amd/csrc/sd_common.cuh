@@ -188,6 +188,47 @@ __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
   return acc;
 }
 
+// Two products sharing the A operand (A B1 and A B2): A is gathered and split once.
+template <class FA, class FB1, class FB2>
+__device__ __forceinline__ void mma_k32x2(FA fa, FB1 fb1, FB2 fb2, int K, f4& acc1, f4& acc2) {
+  const int l = lane_id();
+  const int m = l & 15, kq = (l >> 4) * 8;
+  float av[4][8], b1[4][8], b2[4][8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks * 32 < K) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        av[ks][e] = fa(m, ks * 32 + kq + e);
+        b1[ks][e] = fb1(ks * 32 + kq + e, m);
+        b2[ks][e] = fb2(ks * 32 + kq + e, m);
+      }
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks * 32 < K) {
+      bf16x8 ah, al, ch, cl, dh, dl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        __bf16 h, lo;
+        split_bf(av[ks][e], h, lo);
+        ah[e] = h; al[e] = lo;
+        split_bf(b1[ks][e], h, lo);
+        ch[e] = h; cl[e] = lo;
+        split_bf(b2[ks][e], h, lo);
+        dh[e] = h; dl[e] = lo;
+      }
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ch, acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, dh, acc2, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, cl, acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dl, acc2, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ch, acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dh, acc2, 0, 0, 0);
+    }
+  }
+}
+
 // mma_k32 with the operand gathers split into a raw-load pass and a transform
 // pass: la(m, k) / lb(k, n) fetch the raw values (for global operands, every
 // load is issued before the first use), xa(m, k, x) / xb(k, n, x) turn them into

@@ -119,13 +119,13 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     for (int I = 0; I < NB; ++I) {
       const int K = I < 2 ? 32 : 64;
       auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k] * s.gam[k]; };
-      f4 aw = mma_k32(fa,
-                      [&](int k, int nn) {
-                        const int c = cb * 16 + nn;
-                        return s.Uh[k][c] * __expf(gx_excl(cd, k, c));
-                      },
-                      K, zero4());
-      f4 au = mma_k32(fa, [&](int k, int nn) { return bf2f(s.Hh[k][cb * 16 + nn]); }, K, zero4());
+      f4 aw = zero4(), au = zero4();
+      mma_k32x2(fa,
+                [&](int k, int nn) {
+                  const int c = cb * 16 + nn;
+                  return s.Uh[k][c] * __expf(gx_excl(cd, k, c));
+                },
+                [&](int k, int nn) { return bf2f(s.Hh[k][cb * 16 + nn]); }, K, aw, au);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
@@ -722,8 +722,9 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     for (int I = 0; I < NB; ++I) {
       const int K = I < 2 ? 32 : 64;
       auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k]; };
-      f4 aw = mma_k32(fa, [&](int k, int nn) { return s.Pa[k][cb * 16 + nn]; }, K, zero4());
-      f4 au = mma_k32(fa, [&](int k, int nn) { return s.Pb[k][cb * 16 + nn]; }, K, zero4());
+      f4 aw = zero4(), au = zero4();
+      mma_k32x2(fa, [&](int k, int nn) { return s.Pa[k][cb * 16 + nn]; },
+                [&](int k, int nn) { return s.Pb[k][cb * 16 + nn]; }, K, aw, au);
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
