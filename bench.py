@@ -162,8 +162,8 @@ def forward_bench(ins, st, steps, warmup):
 
 def refshape_bench(dev, steps, warmup):
     """Forward + full VJP at the shape the reference's own README quotes its core
-    F+B timing on (B=1 T=1024 H=8 r=V=128; 0.905 ms on an RTX 5070 Ti,
-    BASELINE.md): a like-for-like point beside the headline, not the metric."""
+    F+B timing on (B=1 T=1024 H=8 r=V=128; 0.905 ms on an RTX 5070 Ti, reference
+    README.md:270): a like-for-like point beside the headline, not the metric."""
     from solvedelta_amd import solvedelta_native
     ins, st, dO = make_inputs(dev, seed=5, b=1, t=1024)
     leaves = ins + list(st)
