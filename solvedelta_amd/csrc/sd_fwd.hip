@@ -275,6 +275,9 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
   const int tb = w;
   const long long sidx = (long long)n * NS + ch;
+  if (!p.rev && tile == 0 && n == 0) {  // per-step marks: C pass slot 6, S pass slot 4
+    if (p.init_transposed) SD_MARK(6, ch & 31); else SD_MARK(4, ch & 31);
+  }
   const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
   // save X0 and stage it split and transposed ([col][row]) for the B operand
 #pragma unroll
