@@ -237,7 +237,7 @@ def decode_bench(dev, steps=256, streams=64):
                                   + " the 256 MB last-level cache")}}
 
 
-def lm_bench(dev, steps=5, warmup=2):
+def lm_bench(dev, steps=5, warmup=2, graph=False):
     """Config 4: SolveDelta causal LM forward + backward, hidden 1024, 24 layers,
     H=8, r=V=128, vocab 32000, conv4, FP32 master weights under bf16 autocast,
     B=2, T=1024 uniform-random token ids with labels = inputs; eager steps and
@@ -267,15 +267,21 @@ def lm_bench(dev, steps=5, warmup=2):
         return (time.perf_counter() - t0) / steps
 
     t_eager = timed(eager)
-    step = SolveDeltaGraphedTrainingStep(model, ids, ids)
-    t_graph = timed(lambda: step(ids, ids).backward())
     ntok = 2 * 1024
-    return {"workload": "causal LM F+B, hidden 1024 x 24 layers, H=8 r=V=128, vocab 32000, "
-                        "B=2 T=1024, FP32 master weights + bf16 autocast",
-            "params": sum(p.numel() for p in model.parameters()),
-            "eager_ms_per_step": round(t_eager * 1e3, 3),
-            "graph_ms_per_step": round(t_graph * 1e3, 3),
-            "value": round(ntok / t_graph, 1), "unit": "tokens/s"}
+    res = {"workload": "causal LM F+B, hidden 1024 x 24 layers, H=8 r=V=128, vocab 32000, "
+                       "B=2 T=1024, FP32 master weights + bf16 autocast",
+           "params": sum(p.numel() for p in model.parameters()),
+           "eager_ms_per_step": round(t_eager * 1e3, 3)}
+    if graph:
+        step = SolveDeltaGraphedTrainingStep(model, ids, ids)
+        t_graph = timed(lambda: step(ids, ids).backward())
+        res["graph_ms_per_step"] = round(t_graph * 1e3, 3)
+        res.update(value=round(ntok / t_graph, 1), unit="tokens/s")
+    else:
+        # the full model's HIP-graph capture is off by default: one capture of it
+        # ended in a host segmentation fault whose cause is not known
+        res.update(value=round(ntok / t_eager, 1), unit="tokens/s", mode="eager")
+    return res
 
 
 def copy_calibration(dev, nbytes=1 << 30):
@@ -298,6 +304,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-lm", action="store_true")
+    ap.add_argument("--lm-graph", action="store_true",
+                    help="also time the causal LM step through its HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -373,7 +381,7 @@ def main():
         res["decode"] = decode_bench(dev)
         res["decode_uncached"] = decode_bench(dev, steps=32, streams=512)
     if not a.no_lm:
-        res["causal_lm"] = lm_bench(dev)
+        res["causal_lm"] = lm_bench(dev, graph=a.lm_graph)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)

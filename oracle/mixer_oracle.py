@@ -76,13 +76,15 @@ def rms_norm_gated(x, gate, weight, eps):
 
 def mixer_oracle(params: dict, hidden, *, heads, rk, rv, eps=1e-6, use_short_conv=True,
                  initial_state: Optional[tuple] = None, valid_mask=None, reset_mask=None,
-                 geometry_enabled=True, decay_enabled=True):
+                 geometry_enabled=True, decay_enabled=True, taps: Optional[list] = None):
     """One mixer layer in FP64.  ``params`` maps the reference module's parameter
     names (in_proj.weight, conv_weight, decay_proj.weight, output_gate_proj.weight/
     .bias, output_norm.weight, output_proj.weight, geometry_write_bias,
     associative_log_rate, associative_decay_bias; optional in_proj.bias /
     output_proj.bias) to tensors.  ``initial_state`` = ((C, S), conv) or None.
-    Returns (output [B,T,hidden], (C, S), conv_state)."""
+    Returns (output [B,T,hidden], (C, S), conv_state).  If ``taps`` is a list,
+    the log-decay tensor [B,T,H,r] is appended to it (for conditioning
+    estimates of the decay-rate gradient in tests)."""
     p = {k: v.double() for k, v in params.items()}
     hidden = hidden.double()
     B, T, _ = hidden.shape
@@ -105,6 +107,8 @@ def mixer_oracle(params: dict, hidden, *, heads, rk, rv, eps=1e-6, use_short_con
                           p["associative_log_rate"], p["associative_decay_bias"])
     if not decay_enabled:
         log_decay = torch.zeros_like(log_decay)
+    if taps is not None:
+        taps.append(log_decay)
     gamma = torch.sigmoid(geo + p["geometry_write_bias"].view(1, 1, heads))
     if not geometry_enabled:
         gamma = torch.zeros_like(gamma)

@@ -381,13 +381,11 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const float* X0 = p.f.Xs + sidx * KD * KD;
   const float* XC = X0 + KD * KD;
   const float* lam = p.g.Ls + sidx * KD * KD;
-  SD_MARK(7, 0);
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
-  SD_MARK(7, 1);
   // M1_ij = dw_i . w_j (j < i)
   lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
   // a = dw X0^T for this wave's column block (K = 128)
@@ -400,7 +398,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
     lblk(s.PA, I * BS, A);
     a[I] = mma_blks(A, BX, zero4());
   }
-  SD_MARK(7, 2);
   __syncthreads();  // PA free
   stage_dout_panel(s.PA, p, b, t0, hh);
   __syncthreads();
@@ -427,7 +424,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   for (int I = 0; I < NB; ++I)
 #pragma unroll
     for (int e = 0; e < 4; ++e) kl_park[(I * 4 + e) * CT + threadIdx.x] = kl[I][e];
-  SD_MARK(7, 3);
   auto D = [&](int j, int cc) { return dd_[j * KD + cc]; };
   auto E = [&](int j, int cc) { return ee[j * KD + cc]; };
   auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
@@ -443,7 +439,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   load_slab(Sd, dd_, cb);
   load_slab(Se, ee, cb);
   load_slab(Sq, chi, cb);
-  SD_MARK(7, 4);
   // Pass A: de = -(e^G (dw X0^T) + apply(M1, d)),  dchi = e^G (dO X0^T) + apply(M2, d);
   // the decay terms chi.dchi + e.de of dg
   // Chunk-uniform output bases with 32-bit lane offsets: 64-bit per-row
@@ -478,7 +473,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
         dchi_b[o] = bq[I][e];
       }
   }
-  SD_MARK(7, 5);
   // Pass B: dd = e^{G_C - G} (w lam^T) + apply_t(M2, chi) - apply_t(M1, e); dg -= d.dd
   {
 #pragma unroll
@@ -511,7 +505,6 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
         if (t < p.T && c < p.r) dgo[t * tstride] = pdg[I][e];
       }
   }
-  SD_MARK(7, 6);
 }
 
 // ---------------------------------------------------------------------------
@@ -802,11 +795,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       s.gam[threadIdx.x] = keep_if(t < p.T, gv);
     }
   }
-  SD_MARK(3, 0);
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
-  SD_MARK(3, 1);
   const ChunkDecay& cd = s.cd;
   // this wave's X0, lambda and X_C row blocks: loads issued ahead of the two
   // LDS Grams so their latency overlaps them
@@ -817,7 +808,6 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
   lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
   lds_pair(nullptr, kh, s.PW, s.M2, false);
-  SD_MARK(3, 2);
   f4 a[NB], kl[NB];
   {
     BlkS BX, BL;
@@ -832,7 +822,6 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       kl[I] = mma_blks(A, BL, zero4());
     }
   }
-  SD_MARK(3, 3);
   float Su[NB][4], Sdd[NB][4], So[NB][4];
   load_slab(Su, uh, cb);
   load_slab(Sdd, ddp, cb);
@@ -853,7 +842,6 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   make_rowf<false>(cd, cb, ri);
   make_colf(cd, cb, cf);
   __syncthreads();  // M1, M2 complete; PA free
-  SD_MARK(3, 4);
   // PA <- dd e^G for the dq product (staged now, consumed after the applies)
   stage_panel(s.PA, ddp, [&](int i, int cc) { return __expf(cd.G[i][cc]); });
   auto U = [&](int j, int cc) { return uh[j * KD + cc]; };
@@ -864,7 +852,6 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   for (int J = 0; J < NB; ++J)
 #pragma unroll
     for (int e = 0; e < 4; ++e) Sx[J][e] = s.gam[J * BS + r4 + e] * Su[J][e];
-  SD_MARK(3, 5);
   // P' (formed by the C chunk's backward prep): loaded now, written into M1 as
   // soon as every apply below has read it, and used by the dq product at the end
   constexpr int PPC = BT * BT / 4 / CT;
@@ -920,9 +907,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
         if (t < p.T && c < p.r) unsafeAtomicAdd(&dgo[t * tstride], vv[I][e] - xs[I][e]);
       }
   }
-  SD_MARK(3, 6);
   __syncthreads();  // P' in M1; PA (dd e^G) staged
-  SD_MARK(3, 7);
   // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
   {
     float* const dq_b = p.g.dqC + rowbase * KD;
@@ -971,7 +956,6 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       for (int e = 0; e < 4; ++e) dq_b[(unsigned)((I * BS + r4 + e) * KD + c)] = dq[e];
     }
   }
-  SD_MARK(3, 8);
 }
 
 // ---------------------------------------------------------------------------

@@ -17,31 +17,6 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
-// Compile-time section timer for kernel tuning (off unless SD_SECTION_TIMING is
-// defined): workgroup (0, SD_MARK_Y) thread 0 records s_memrealtime at marks 0..31.
-#ifdef SD_SECTION_TIMING
-#ifndef SD_MARK_Y
-#define SD_MARK_Y 0  // workgroup row whose chunk 0 is timed
-#endif
-static __device__ unsigned long long sd_section_ticks[8][32];
-#define SD_MARK(slot, idx)                                                              \
-  do {                                                                                  \
-    if (blockIdx.x == 0 && blockIdx.y == SD_MARK_Y && threadIdx.x == 0)                 \
-      sd_section_ticks[slot][idx] = __builtin_amdgcn_s_memrealtime();                   \
-  } while (0)
-// Per-workgroup start / end ticks of one kernel (tuning builds only).
-static __device__ unsigned long long sd_wg_ticks[2][4096];
-#define SD_WG_TRACE(end)                                                                \
-  do {                                                                                  \
-    if (threadIdx.x == 0)                                                               \
-      sd_wg_ticks[end][(blockIdx.y * gridDim.x + blockIdx.x) & 4095] =                  \
-          __builtin_amdgcn_s_memrealtime();                                             \
-  } while (0)
-#else
-#define SD_MARK(slot, idx) do { } while (0)
-#define SD_WG_TRACE(end) do { } while (0)
-#endif
-
 namespace sd {
 
 constexpr int BT = 64;     // chunk length
@@ -389,7 +364,7 @@ __device__ __forceinline__ float gx_excl(const ChunkDecay& cd, int i, int c) {
 // Decayed Gram M_ij = sum_c X_ic Y_jc exp(Gx_ic - G_jc), j<i (strict) or j<=i,
 // written to M (64 x LS, fp32); entries above the diagonal set to 0.
 // X(i,c), Y(j,c) are lambdas returning fp32; EXCL selects Gx.
-template <bool EXCL, int MS = -1, class FX, class FY>
+template <bool EXCL, class FX, class FY>
 __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, float* M,
                              int ldm = LS) {
   const int w = wave_id();
@@ -418,14 +393,12 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
       M[i * ldm + j] = keep ? acc[e] : 0.f;
     }
   }
-  if constexpr (MS >= 0) SD_MARK(MS, 13);
   // Zero the strictly-upper block pairs.
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
     const int i = idx / BT, j = idx % BT;
     if ((j / BS) > (i / BS)) M[i * ldm + j] = 0.f;
   }
   __syncthreads();
-  if constexpr (MS >= 0) SD_MARK(MS, 14);
   // Exact fix-up for wild coordinates.
   for (int J = 0; J < NB; ++J) {
     const int nw = cd.nwild[J];
@@ -462,7 +435,6 @@ __device__ __forceinline__ f4 mma16s(const float* av, const float* bv, f4 acc) {
 // Diagonal 16x16 blocks by forward substitution (one lane per column), then
 // off-diagonal blocks A_IJ = -A_II * sum_{K=J}^{I-1} L_IK A_KJ by distance.
 // tmp: 64 x LS scratch.
-template <int MS = -1>
 __device__ void unit_lower_inverse(float* L, float* tmp) {
   const int tid = threadIdx.x;
   // Phase 0: diagonal blocks.  Thread (B, j): block B = tid/16 (tid < 64), column j.
@@ -477,14 +449,12 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
       col[i] = (i >= j) ? s : 0.f;
     }
   }
-  if constexpr (MS >= 0) SD_MARK(MS, 20);
   __syncthreads();
   if (tid < NB * BS) {
     const int B = tid / BS, j = tid % BS, B0 = B * BS;
     for (int i = 0; i < BS; ++i) tmp[(B0 + i) * LS + B0 + j] = col[i];
   }
   __syncthreads();
-  if constexpr (MS >= 0) SD_MARK(MS, 21);
   // tmp holds the diagonal inverses; L still holds the strict lower part.
   // Off-diagonal blocks by distance, one wave per block, on the K=16 MFMA:
   //   T = sum_{K=J}^{I-1} L_IK A_KJ,   A_IJ = -A_II T.
@@ -516,7 +486,6 @@ __device__ void unit_lower_inverse(float* L, float* tmp) {
       for (int e = 0; e < 4; ++e) tmp[(I * BS + r4 + e) * LS + J * BS + m] = -a[e];
     }
     __syncthreads();
-    if constexpr (MS >= 0) SD_MARK(MS, 21 + dist);
   }
   // Copy back: A lower (incl. diagonal), zero upper.
   for (int idx = tid; idx < BT * BT; idx += CT) {

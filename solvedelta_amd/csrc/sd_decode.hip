@@ -106,7 +106,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
   const int n = blockIdx.x, b = n / in.H, hd = n % in.H;
   const int r = in.r, V = in.V, tid = threadIdx.x;
   const int cg = tid & 31, c0 = cg * 4, rg = tid >> 5, i0 = rg * 16;
-  SD_MARK(5, 0);
   auto ld = [&](const sd_view& v, int c, int w) -> float {
     if (!FULL && c >= w) return 0.f;
     return bf2f(((const __bf16*)v.data)[(long long)b * v.sb + (long long)hd * v.sh + c]);
@@ -138,7 +137,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
 #pragma unroll
   for (int a = 0; a < 16; ++a) sv[a] = ld4<FULL>(S0, i0 + a, c0, V, r, V);
   __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use
-  SD_MARK(5, 1);
   if (tid >= KD) uu = kk = qq = er = 0.f;
   if (tid < KD) {
     const int c = tid;
@@ -160,7 +158,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
 #pragma unroll
   for (int a = 0; a < 16; ++a) *reinterpret_cast<float4*>(&s.C[i0 + a][c0]) = cv[a];
   __syncthreads();
-  SD_MARK(5, 2);
   // delta_i = gamma (h_i - sum_j C_ij u_j): two threads per row
   {
     const int i = tid >> 1, half = tid & 1;
@@ -206,7 +203,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
       for (int m = 0; m < 4; ++m) s.d[c0 + m] = s.k[c0 + m] + f4get(dp, m);
     }
   }
-  SD_MARK(5, 3);
   // sources: phi = rho delta / sqrt(rho^2 + |u|^2 |delta|^2), den = 1 + phi.u
   const float dl = tid < KD ? s.delta[tid] : 0.f;
   float nrm[2] = {uu * uu, dl * dl};
@@ -223,7 +219,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
     s.chi[tid] = qq - phi * (pr2[1] / den);
   }
   __syncthreads();
-  SD_MARK(5, 4);
   // S' = D S + d (z - (D S)^T e)^T ;  o = S'^T chi
   {
     float4 pr = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -234,9 +229,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
       x.x *= g; x.y *= g; x.z *= g; x.w *= g;
       pr.x += x.x * ei; pr.y += x.y * ei; pr.z += x.z * ei; pr.w += x.w * ei;
     }
-    SD_MARK(5, 5);
     pr = col_sums(pr, s.part);
-    SD_MARK(5, 6);
     float upd[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) upd[m] = s.z[c0 + m] - f4get(pr, m);
@@ -253,7 +246,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
 #pragma unroll
       for (int a = 0; a < 16; ++a) st4<FULL>(Sn, i0 + a, c0, V, r, V, sv[a]);
     }
-    SD_MARK(5, 7);
     o = col_sums(o, s.part);
     if (rg == 0) {
 #pragma unroll
@@ -261,7 +253,6 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
         if (FULL || c0 + m < V) out[(long long)n * V + c0 + m] = f2bf(f4get(o, m));
     }
   }
-  SD_MARK(5, 8);
 }
 
 int launch_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, hipStream_t st) {

@@ -69,9 +69,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   const sd_inputs& in = p.in;
   const float* g = (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
                    (long long)hh * in.log_decay.sh;
-  SD_MARK(0, 0);
   build_decay(s.cd, g, in.log_decay.st, t0, T, r);
-  SD_MARK(0, 1);
   const int w = wave_id(), l = lane_id();
   if (threadIdx.x < BT) {  // branch-free: clamped token, then select
     const int t = t0 + threadIdx.x;
@@ -101,16 +99,13 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     }
   }
   __syncthreads();
-  SD_MARK(0, 2);
   const ChunkDecay& cd = s.cd;
   // L_ij = gamma_i sum_c u_ic u_jc exp(G_{i-1,c} - G_jc), j < i
   stage_ytilde(s.Yt, cd, [&](int j, int c) { return s.Uh[j][c]; });
   decayed_gram_yt<true>(
       cd, [&](int i, int c) { return s.gam[i] * s.Uh[i][c]; }, s.Yt,
       [&](int j, int c) { return s.Uh[j][c]; }, true, s.M);
-  SD_MARK(0, 3);
-  unit_lower_inverse<0>(s.M, s.tmp);
-  SD_MARK(0, 4);
+  unit_lower_inverse(s.M, s.tmp);
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.Ac[((long long)n * p.NT + ch) * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
   // W = A diag(gamma) (u e^{Gexcl}),  U = A diag(gamma) h
@@ -135,14 +130,12 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
       }
     }
   }
-  SD_MARK(0, 5);
   // decayed keys (transposed per chunk) and chunk decay
   const long long cbase = ((long long)n * p.NT + ch);
   store_frag_panel<KD, BT>(p.Kc.hi, p.Kc.lo, cbase * KD * BT, [&](int c, int i) {
     return s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
   });
   if (threadIdx.x < KD) p.Gam[cbase * KD + threadIdx.x] = __expf(cd.G[BT - 1][threadIdx.x]);
-  SD_MARK(0, 6);
 }
 
 // ---------------------------------------------------------------------------
@@ -276,7 +269,6 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
   const int tb = w;
   const long long sidx = (long long)n * NS + ch;
   if (!p.rev && tile == 0 && n == 0) {  // per-step marks: C pass slot 6, S pass slot 4
-    if (p.init_transposed) SD_MARK(6, ch & 31); else SD_MARK(4, ch & 31);
   }
   const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
   // save X0 and stage it split and transposed ([col][row]) for the B operand
@@ -469,14 +461,12 @@ struct PrepSSmem {
 __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepSSmem& s = *reinterpret_cast<PrepSSmem*>(smem_raw);
-  SD_WG_TRACE(0);
   const int ch = blockIdx.x, n = blockIdx.y;
   const int b = n / p.H, hh = n % p.H, t0 = ch * BT;
   const int T = p.T, r = p.r, V = p.V;
   const sd_inputs& in = p.in;
   const float* g = (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
                    (long long)hh * in.log_decay.sh;
-  SD_MARK(2, 0);
   const int w = wave_id(), l = lane_id();
   {
     const int cl = l & 15;
@@ -489,7 +479,6 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       load_row16(in.k, b, t, hh, T, r, kx[g]);
     }
     build_decay(s.cd, g, in.log_decay.st, t0, T, r);
-    SD_MARK(2, 1);
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
@@ -503,7 +492,6 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     }
   }
   __syncthreads();
-  SD_MARK(2, 2);
   const ChunkDecay& cd = s.cd;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long cidx = (long long)n * p.NT + ch;
@@ -546,7 +534,6 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     if ((j / BS) > (i / BS)) s.M[i * LS + j] = 0.f;
   }
   __syncthreads();
-  SD_MARK(2, 3);
   // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}  (this wave's column block)
   const float* X0 = p.Xc + ((long long)n * (p.NT + 1) + ch) * KD * KD;
   {
@@ -586,7 +573,6 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     }
   }
   __syncthreads();
-  SD_MARK(2, 4);
   // sources (16-lane row layout; e overwrites u, chi overwrites k).  Both row
   // groups' delta, q and erase are loaded before the first row is processed:
   // the rows' global stores would otherwise hold the next rows' loads behind them.
@@ -608,7 +594,6 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       load_row2(in.v, b, t0 + w + rr * CW, hh, T, V, vx[rr][0], vx[rr][1]);
       load_row2(in.write_raw, b, t0 + w + rr * CW, hh, T, V, wx[rr][0], wx[rr][1]);
     }
-    SD_MARK(2, 10);
     float* const e_b = p.e + rowbase * KD;
     float* const chi_b = p.chi + rowbase * KD;
 #pragma unroll
@@ -660,9 +645,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       zz[rr][1] = vx[rr][1] / (1.f + __expf(-wx[rr][1]));
     }
   }
-  SD_MARK(2, 12);
   __syncthreads();
-  SD_MARK(2, 5);
   // panels that read d and chi as they are, then d's Gram form staged once for
   // both decayed Grams below (in d's own storage; the wild fix-ups read the
   // global copy of d)
@@ -699,12 +682,9 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   store_frag_panel<BT, KD>(p.Qs.hi, p.Qs.lo, rowbase * KD,
                            [&](int i, int c) { return s.Pb[i][c] * __expf(cd.G[i][c]); });
   __syncthreads();
-  SD_MARK(2, 6);
   // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
   decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pa[i][c]; }, s.Kp, Draw, true, s.M);
-  SD_MARK(2, 7);
   unit_lower_inverse(s.M, &s.Pc[0][0]);
-  SD_MARK(2, 8);
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.As[cidx * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
   // WY operands staged once: Pa <- e e^G, Pb <- z = sigmoid(write_raw) v
@@ -738,8 +718,6 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   }
   __syncthreads();
   store_frag_panel<BT, KD>(p.Ws.hi, p.Ws.lo, rowbase * KD, [&](int i, int c) { return s.Pc[i][c]; });
-  SD_MARK(2, 9);
-  SD_WG_TRACE(1);
 }
 
 size_t prep_c_smem() { return sizeof(PrepCSmem); }

@@ -76,3 +76,36 @@ def max_rel(a, b):
     """max |a-b| / max |b| (max-norm relative error)."""
     a, b = a.detach().double().cpu(), b.detach().double().cpu()
     return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+
+
+def c_token_loop():
+    """The FP64/FP32 C token loop (oracle/sd_token_loop.c), built on demand."""
+    import ctypes
+    import os
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    so = os.path.join(root, "oracle", "libsd_token_loop.so")
+    if not os.path.exists(so):
+        subprocess.run(["make", "-C", os.path.join(root, "oracle")], check=True)
+    return ctypes.CDLL(so)
+
+
+def c_forward_f64(ins, state):
+    """Runs the C FP64 token loop on operator inputs (raw gates, any device) and an
+    initial (C, S); returns (out [B,T,H,V], C_T, S_T) as fp32 CPU tensors."""
+    import ctypes
+    import numpy as np
+    B, T, H, r = ins[0].shape
+    V = ins[4].shape[-1]
+    arr = lambda x: np.ascontiguousarray(
+        x.detach().float().cpu().numpy().reshape(*x.shape[:3], -1) if x.dim() == 5
+        else x.detach().float().cpu().numpy())
+    a = [arr(x) for x in ins]
+    C = np.ascontiguousarray(state[0].detach().float().cpu().numpy())
+    S = np.ascontiguousarray(state[1].detach().float().cpu().numpy())
+    o = np.zeros((B, T, H, V), np.float32)
+    ptr = lambda z: z.ctypes.data_as(ctypes.c_void_p)
+    rc = c_token_loop().sd_cpu_forward_f64(B, T, H, r, V, *(ptr(z) for z in a), ptr(C), ptr(S),
+                                           ptr(o))
+    assert rc == 0
+    return torch.from_numpy(o), torch.from_numpy(C), torch.from_numpy(S)

@@ -1,8 +1,8 @@
 """GPU parity of the HIP VJP against FP64 autograd through the oracle.
 
 Gate (reference tests/core/test_rebuild_semantics.py:540-597): every gradient's
-relative Frobenius error < 3e-2.  We also require < 1e-2 at the config-2 shape
-(B=1, T=512, H=8... reduced to H=2 for oracle time, r=V=128)."""
+relative Frobenius error < 3e-2.  The config-2 oracle shape itself (B=1, T=512,
+H=8, r=V=128, bound 1e-2, every cotangent pattern) is in test_gpu_configs.py."""
 import pytest
 import torch
 
@@ -62,12 +62,6 @@ def test_backward_matches_oracle(B, T, H, r, V, seed, decay):
     print(f"case B{B} T{T} H{H} r{r} V{V} {decay}", flush=True)
     grads, rgrads = _grads(B, T, H, r, V, seed, decay)
     _report(f"bwd T{T} r{r}", grads, rgrads, 3e-2)
-
-
-def test_backward_config2_shape_b1_t512():
-    """Config 2's oracle comparison shape (B=1, T=512, r=V=128), two heads."""
-    grads, rgrads = _grads(1, 512, 2, 128, 128, 77)
-    _report("bwd T512 r128", grads, rgrads, 1e-2)
 
 
 def test_backward_gamma_head_shape_and_no_state():

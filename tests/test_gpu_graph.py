@@ -59,3 +59,33 @@ def test_graphed_step_replays_match_eager():
     assert rel(loss.detach().float(), new_loss.float()) < 1e-5
     assert abs(new_loss.item() - ref_loss.item()) > 1e-4
     assert max(rel(p.grad, r) for p, r in zip(model.parameters(), new_grads)) < 1e-4
+
+
+def test_graphed_step_matches_fp64_lm_oracle():
+    """The captured training step against the FP64 LM oracle (not only against
+    eager): loss and every parameter gradient of a replay."""
+    from oracle.lm_oracle import lm_oracle
+    from solvedelta_amd.graph import SolveDeltaGraphedTrainingStep
+    model = _model(seed=4)
+    with torch.no_grad():
+        for n, p in model.named_parameters():
+            if n.endswith("norm.weight"):
+                p.uniform_(0.5, 1.5)
+    ids = torch.randint(0, 97, (2, 64), generator=torch.Generator().manual_seed(5)).cuda()
+    step = SolveDeltaGraphedTrainingStep(model, ids, ids)
+    for _ in range(2):
+        model.zero_grad(set_to_none=True)
+        loss = step(ids, ids)
+        loss.backward()
+    torch.cuda.synchronize()
+    names = [n for n, _ in model.named_parameters()]
+    params = {n: p.detach().double().cpu().requires_grad_() for n, p in model.named_parameters()}
+    ref_loss, _ = lm_oracle(params, ids.cpu(), ids.cpu(), layers=2, heads=2, rk=64, rv=64)
+    rgrads = torch.autograd.grad(ref_loss, [params[n] for n in names])
+    e_loss = abs(loss.item() - ref_loss.item()) / abs(ref_loss.item())
+    errs = {n: rel(p.grad.float(), rg) for (n, p), rg in zip(model.named_parameters(), rgrads)}
+    worst = max(errs, key=errs.get)
+    print(f"[graph vs oracle] rel loss {e_loss:.1e}; worst grad {worst} {errs[worst]:.2e}", flush=True)
+    assert e_loss < 5e-3
+    for n, e in errs.items():
+        assert e < 5e-2, (n, e)
