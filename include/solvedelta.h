@@ -67,6 +67,19 @@ int sd_bwd(const sd_inputs *in, const void *fwd_workspace, const void *dout, con
            void *dwrite, float *dlog_decay, float *dgamma, float *dC0, float *dS0,
            void *workspace, size_t workspace_bytes, void *stream);
 
+/* Forward without any allocation (no counterpart in the reference): the same
+ * kernels as sd_fwd, with the workspace in a device-resident static array of
+ * SD_NOALLOC_SCRATCH_BYTES per GPU instead of a caller buffer, for callers that
+ * cannot call hipMalloc (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  Inference only: the next call on the
+ * device overwrites the workspace, so there is no sd_bwd after it.  Shapes whose
+ * forward workspace (sd_fwd_workspace_bytes) exceeds the array return
+ * SD_ERR_WORKSPACE.  Calls that overlap on one GPU (two streams, two threads)
+ * share the array and race; serialise them. */
+#define SD_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+size_t sd_noalloc_scratch_bytes(void);
+int sd_fwd_noalloc(const sd_inputs *in, void *out, float *C_T, float *S_T, void *stream);
+
 /* One-token recurrent step (T must be 1). out: bf16 [B,1,H,V] contiguous.
  * C_T / S_T receive the advanced state; they may alias C0 / S0 (in place). */
 int sd_decode(const sd_inputs *in, void *out, float *C_T, float *S_T, void *stream);

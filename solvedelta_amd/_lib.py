@@ -38,6 +38,9 @@ EXPORTS = {
                + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "sd_profile_enable": (ctypes.c_int, [ctypes.c_int]),
     "sd_profile_read": (ctypes.c_size_t, [ctypes.c_char_p, ctypes.c_size_t]),
+    "sd_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "sd_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p]),
     "sd_decode": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
                                  ctypes.c_void_p, ctypes.c_void_p]),
     # mixer frontend / readout (include/solvedelta_mixer.h)

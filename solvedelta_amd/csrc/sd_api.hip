@@ -4,6 +4,8 @@
 #include "../../include/solvedelta.h"
 #include "sd_internal.h"
 
+#include <mutex>
+
 
 using namespace sd;
 
@@ -87,6 +89,31 @@ int check_inputs(const sd_inputs* in) {
   return SD_OK;
 }
 
+// Scratch of sd_fwd_noalloc: the forward workspace of callers that cannot
+// allocate.  Each device holds its own copy from module load to process end;
+// host code reaches it only through the address hipGetSymbolAddress returns
+// for the current device (the array's name on the host is not a device
+// address).  Every call on a device reuses that device's copy.
+static __device__ __align__(256) unsigned char scratch[SD_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up once per device).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SD_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SD_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SD_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -108,6 +135,22 @@ int sd_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* workspa
   size_t need = 0;
   FwdWs w = carve_fwd(workspace, in->B, in->T, in->H, &need);
   if (workspace_bytes < need) return SD_ERR_WORKSPACE;
+  return launch_fwd(in, out, C_T, S_T, w, (hipStream_t)stream);
+}
+
+size_t sd_noalloc_scratch_bytes(void) { return SD_NOALLOC_SCRATCH_BYTES; }
+
+int sd_fwd_noalloc(const sd_inputs* in, void* out, float* C_T, float* S_T, void* stream) {
+  int rc = check_inputs(in);
+  if (rc) return rc;
+  if (!out) return SD_ERR_ARG;
+  size_t need = 0;
+  carve_fwd(nullptr, in->B, in->T, in->H, &need);
+  if (need > SD_NOALLOC_SCRATCH_BYTES) return SD_ERR_WORKSPACE;
+  void* base = nullptr;
+  rc = scratch_for_current_device(&base);
+  if (rc) return rc;
+  FwdWs w = carve_fwd(base, in->B, in->T, in->H, nullptr);
   return launch_fwd(in, out, C_T, S_T, w, (hipStream_t)stream);
 }
 
