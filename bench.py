@@ -77,17 +77,46 @@ BYTES_PER_CHUNK = {
     "k_final": (3 * _IN + 6 * _P) + 3 * _IN,                # u,h,k, 6 partial grads -> du,dh,dk
 }
 
-# HBM bytes per dispatch of each kernel at this workload, from rocprofv3 counter
-# runs (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads for a
-# plain 1 GiB device copy: x2.0 and x1.0); the runs and the table are in
-# profiles/fwd_bwd_B4_T2048_H8_d128_hbm_traffic.txt.  Static figures: a kernel
-# change needs a new counter run.
-TRAFFIC_MB = {
-    "k_prep_c": 185.7, "state_c_fwd": 207.1, "k_prep_s": 524.6, "state_s_fwd": 207.1,
-    "k_out_s": 167.9, "k_bprep_s": 350.5, "state_s_bwd": 254.5, "state_c_bwd": 254.5,
-    "k_grad_s": 554.2, "k_src_bwd": 436.3, "k_bprep_c": 470.4, "k_grad_c": 708.1,
-    "k_final": 302.8,
+# Algorithmic bytes per token-head of each kernel in the sense of the
+# operator's own tensors (SURVEY-style accounting: the inputs it reads, the
+# outputs and gradients it writes, each once; workspace panels between kernels
+# are not algorithmic).  bf16 vector 2R = 256 B, fp32 log-decay / its gradient
+# 4R = 512 B, gamma 4 B.  State kernels touch only the boundary states
+# (64 KiB per sequence each), listed separately.
+_VEC, _DEC, _GAM = 2 * R, 4 * R, 4
+OP_BYTES_PER_TOKEN_HEAD = {
+    "k_prep_c": 2 * _VEC + _DEC + _GAM,                    # u, h, log-decay, gamma
+    "k_prep_s": 6 * _VEC + _DEC,                           # u, q, k, v, erase, write, log-decay
+    "k_out_s": _VEC,                                       # out
+    "k_bprep_s": _VEC + _DEC,                              # dO, log-decay
+    "k_grad_s": _VEC + 2 * _DEC,                           # dO, log-decay -> dlog_decay
+    "k_src_bwd": 6 * _VEC + 4 * _VEC,                      # u, k, q, erase, v, write -> dq, derase, dv, dwrite
+    "k_bprep_c": 2 * _VEC + _DEC + _GAM,                   # u, k, log-decay, gamma
+    "k_grad_c": _DEC + _GAM + _DEC,                        # log-decay, gamma -> dlog_decay (add)
+    "k_final": 3 * _VEC + _GAM + 3 * _VEC + _GAM,          # u, h, k, gamma -> du, dh, dk, dgamma
 }
+STATE_BYTES_PER_SEQ = {"state_c_fwd": R * R * 4, "state_s_fwd": R * V * 4,  # C0 / S0 read
+                       "state_c_bwd": R * R * 4, "state_s_bwd": R * V * 4}  # dC0 / dS0 write
+
+PROFILE_DIR = os.path.join(ROOT, "profiles")
+TRAFFIC_FILE = os.path.join(PROFILE_DIR, "fwd_bwd_B4_T2048_H8_d128_hbm_traffic.txt")
+COUNTER_FILE = os.path.join(PROFILE_DIR, "fwd_bwd_B4_T2048_H8_d128_mfma_valu_counters.txt")
+
+
+def profile_keys(path, key):
+    """Machine-readable lines `<key> <kernel> <value>` of a committed rocprofv3
+    summary (the counter runs of the current build that the file's header
+    names); {} if the file is absent."""
+    out = {}
+    try:
+        with open(path) as fh:
+            for line in fh:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == key:
+                    out[parts[1]] = float(parts[2])
+    except OSError:
+        pass
+    return out
 
 
 _NTH = B * T * H
@@ -140,8 +169,47 @@ def cpu_baseline(budget_s=24.0):
         prev, dt = dt, run(tt)
         grow = max(2.2, dt / prev)
     return {"value": B * tt / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu": cpu_model(),
             "sample": f"FP64 torch token-loop oracle F+VJP, B={B} H={H} r=V={R}, T={tt} "
                       f"({dt:.1f} s)"}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_forward_baseline():
+    """The C token loop (oracle/sd_token_loop.c, FP32, OpenMP over the 32 (b,h)
+    sequences) on config 1's full forward: the reference's CPU recurrence
+    (reference.py:156-227) as a compiled loop, timed on the host cores."""
+    import ctypes
+    import numpy as np
+    so = os.path.join(ROOT, "oracle", "libsd_token_loop.so")
+    if not os.path.exists(so):
+        return None
+    lib = ctypes.CDLL(so)
+    ins, st, _ = make_inputs("cpu", seed=2)
+    arr = lambda x: np.ascontiguousarray(x.detach().float().numpy().reshape(B, T, H, -1))
+    a = [arr(x) for x in ins[:8]] + [np.ascontiguousarray(ins[8].detach().float().numpy())]
+    C = np.ascontiguousarray(st[0].detach().numpy())
+    S = np.ascontiguousarray(st[1].detach().numpy())
+    o = np.zeros((B, T, H, V), np.float32)
+    ptr = lambda z: z.ctypes.data_as(ctypes.c_void_p)
+    t0 = time.perf_counter()
+    rc = lib.sd_cpu_forward_f32(B, T, H, R, V, *(ptr(z) for z in a), ptr(C), ptr(S), ptr(o))
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(B * T / dt, 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port", "ok": rc == 0, "cpu": cpu_model(),
+            "sample": f"C FP32 token loop forward, full config 1 (B={B} T={T} H={H} r=V={R}), "
+                      f"{dt:.2f} s"}
 
 
 def forward_bench(ins, st, steps, warmup):
@@ -180,9 +248,19 @@ def refshape_bench(dev, steps, warmup):
         step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / steps
+    # memory one F+B step allocates on top of its resident inputs (workspaces,
+    # output, the 11 gradients), against the reference's graph pool at this shape
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    grads = step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(dev) - base
+    del grads
     return {"workload": "operator forward + full VJP, B=1 T=1024 H=8 r=V=128",
             "value": round(1024 / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4),
-            "reference_published_ms": 0.905, "reference_hardware": "RTX 5070 Ti"}
+            "reference_published_ms": 0.905, "reference_hardware": "RTX 5070 Ti",
+            "step_alloc_mib": round(peak / 2 ** 20, 1),
+            "reference_graph_alloc_mib": 63.0}
 
 
 def decode_bench(dev, steps=256, streams=64):
@@ -343,28 +421,42 @@ def main():
     prof = _lib.profile_read()
     _lib.profile_enable(False)
     nchunks = B * H * (T // CH)
+    nth = B * T * H
+    us = {k: v[0] / v[1] * 1e3 for k, v in prof.items()}
     dom = max(prof, key=lambda k: prof[k][0])
-    tot_ms, cnt = prof[dom]
-    avg_s = tot_ms / cnt / 1e3
+    avg_s = us[dom] / 1e6
+    op_bytes = (OP_BYTES_PER_TOKEN_HEAD[dom] * nth if dom in OP_BYTES_PER_TOKEN_HEAD
+                else STATE_BYTES_PER_SEQ[dom] * B * H)
     flops = FLOPS_PER_CHUNK.get(dom, 0) * nchunks
-    nbytes = BYTES_PER_CHUNK[dom] * nchunks
-    # Arithmetic intensity flops/bytes of every kernel here is far below the
-    # MFMA/HBM ridge (2.5e15 / 8e12 = 312 flop/B), so HBM is the bounding roof.
-    gbs = nbytes / avg_s / 1e9
+    traffic = profile_keys(TRAFFIC_FILE, "traffic_bytes")
+    mfma_busy = profile_keys(COUNTER_FILE, "mfma_busy")
+    gbs = op_bytes / avg_s / 1e9
+    # every kernel's flops per algorithmic byte is far below the MFMA/HBM ridge
+    # (2.5e15 / 8e12 = 312 flop/B), so HBM is the roof that bounds it
     roof = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1),
             "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(gbs * 1e9 / PEAK_HBM, 4),
-            "algorithmic_bytes": nbytes, "intensity_flop_per_byte": round(flops / nbytes, 1),
-            "mfma_tflops": round(flops / avg_s / 1e12, 3),
-            "traffic": TRAFFIC_MB[dom] * 1e6 if dom in TRAFFIC_MB else None,
-            "traffic_unit": "bytes per launch",
+            "traffic": traffic.get(dom),
+            "traffic_unit": "HBM bytes per launch (FETCH_SIZE/WRITE_SIZE counter runs, "
+                            "profiles/fwd_bwd_B4_T2048_H8_d128_hbm_traffic.txt)",
+            "algorithmic_bytes": op_bytes,
             "avg_us": round(avg_s * 1e6, 2),
-            "kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in sorted(prof.items())},
-            # whole step against its own floor: each operator input, output and
-            # boundary state touched once (forward 2,564 B per token-head plus
-            # 256 KiB of C0/S0/C_T/S_T per sequence; backward re-reads the inputs
-            # and dO and writes the 11 cotangents)
-            "step_floor_us": round(STEP_FLOOR_BYTES / PEAK_HBM * 1e6, 1),
-            "step_frac": round(STEP_FLOOR_BYTES / PEAK_HBM / dt, 4)}
+            # the kernel's whole interface (operator tensors plus the workspace
+            # panels it reads and writes), each once: what it must move as built
+            "interface_bytes": BYTES_PER_CHUNK[dom] * nchunks if dom in BYTES_PER_CHUNK else None,
+            "interface_GBs": (round(BYTES_PER_CHUNK[dom] * nchunks / avg_s / 1e9, 1)
+                              if dom in BYTES_PER_CHUNK else None),
+            "mfma_tflops": round(flops / avg_s / 1e12, 3),
+            "mfma_frac": round(flops / avg_s / PEAK_MFMA_BF16, 5),
+            "kernels_us": {k: round(v, 2) for k, v in sorted(us.items())},
+            "kernels_mfma_busy": mfma_busy or None,
+            "kernels_traffic": traffic or None}
+    # every kernel runs once per step; the counter summary lists each by its event name
+    step_bytes = sum(traffic.get(k, 0.0) for k in us) if traffic else None
+    step = {"algorithmic_bytes": STEP_FLOOR_BYTES,
+            "floor_us": round(STEP_FLOOR_BYTES / PEAK_HBM * 1e6, 1),
+            "achieved_GBs": round(STEP_FLOOR_BYTES / dt / 1e9, 1),
+            "frac": round(STEP_FLOOR_BYTES / PEAK_HBM / dt, 4),
+            "traffic_bytes": step_bytes}
     res = {
         "metric": "SolveDelta layer fwd+bwd tokens/s @B4 T2048 H8 d128; % MFMA/HBM roofline",
         "value": round(B * T / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
@@ -374,6 +466,7 @@ def main():
                                "at configs[1] shape)", "global_batch": B, "seq_len": T,
                    "heads": H, "dk": R, "dv": V, "chunk": CH, "parallelism": "single-gpu"},
         "roofline": roof,
+        "step_roofline": step,
     }
     res["forward"] = forward_bench(ins, st, a.steps, a.warmup)
     res["reference_shape"] = refshape_bench(dev, a.steps, a.warmup)
@@ -384,6 +477,7 @@ def main():
         res["causal_lm"] = lm_bench(dev, graph=a.lm_graph)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
+        res["cpu_baseline_forward"] = cpu_forward_baseline()
     print(json.dumps(res), flush=True)
 
 

@@ -17,6 +17,12 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
+// Bf16 MFMA terms per product of two split (hi + lo) operands: 3 = hi*hi +
+// hi*lo + lo*hi (~16 mantissa bits), 2 = the A operand's high half only.
+#ifndef SD_CHUNK_TERMS
+#define SD_CHUNK_TERMS 3
+#endif
+
 namespace sd {
 
 constexpr int BT = 64;     // chunk length
@@ -155,8 +161,8 @@ __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
         split_bf(bv[ks][e], h, lo);
         bh[e] = h; bl[e] = lo;
       }
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+      if constexpr (SD_CHUNK_TERMS >= 3) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+      if constexpr (SD_CHUNK_TERMS >= 2) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
     }
   }
@@ -194,10 +200,14 @@ __device__ __forceinline__ void mma_k32x2(FA fa, FB1 fb1, FB2 fb2, int K, f4& ac
         split_bf(b2[ks][e], h, lo);
         dh[e] = h; dl[e] = lo;
       }
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ch, acc1, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, dh, acc2, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, cl, acc1, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dl, acc2, 0, 0, 0);
+      if constexpr (SD_CHUNK_TERMS >= 3) {
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ch, acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, dh, acc2, 0, 0, 0);
+      }
+      if constexpr (SD_CHUNK_TERMS >= 2) {
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, cl, acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dl, acc2, 0, 0, 0);
+      }
       acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ch, acc1, 0, 0, 0);
       acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dh, acc2, 0, 0, 0);
     }
@@ -540,9 +550,10 @@ namespace sd {
 // Pre-split (bf16 hi + lo) MFMA operand fragment and the 3-term product.
 struct Frag { bf16x8 h, l; };
 
+template <int TERMS = SD_CHUNK_TERMS>
 __device__ __forceinline__ f4 mma3f(const Frag& a, const Frag& b, f4 acc) {
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, acc, 0, 0, 0);
+  if constexpr (TERMS >= 3) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, acc, 0, 0, 0);
+  if constexpr (TERMS >= 2) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, acc, 0, 0, 0);
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, acc, 0, 0, 0);
 }
 

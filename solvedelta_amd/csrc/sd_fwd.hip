@@ -155,6 +155,9 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
 // token block w.  KD / SCOLS workgroups cover a sequence's state columns; every
 // one of them reads the chunk's full W and K panels, so wider tiles mean less
 // panel traffic per chunk step.
+#ifndef SD_STATE_TERMS
+#define SD_STATE_TERMS 3
+#endif
 constexpr int SCOLS = 16;
 constexpr int HALVES = SCOLS / 16;
 constexpr int SWAVES = 4;
@@ -308,7 +311,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
       Frag xb;
       xb.h = ldb8(&s.Xh[h * 16 + m][ks * 32 + kq]);
       xb.l = ldb8(&s.Xl[h * 16 + m][ks * 32 + kq]);
-      acc[h] = mma3f(cur.W[ks], xb, acc[h]);
+      acc[h] = mma3f<SD_STATE_TERMS>(cur.W[ks], xb, acc[h]);
     }
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
@@ -321,10 +324,11 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           if constexpr (B1X) {
-            X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks].l, cur.B1[h][ks].h, X[q][h], 0, 0, 0);
+            if constexpr (SD_STATE_TERMS >= 3)
+              X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks].l, cur.B1[h][ks].h, X[q][h], 0, 0, 0);
             X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks].h, cur.B1[h][ks].h, X[q][h], 0, 0, 0);
           } else {
-            X[q][h] = mma3f(cur.A1[q][ks], cur.B1[h][ks], X[q][h]);
+            X[q][h] = mma3f<SD_STATE_TERMS>(cur.A1[q][ks], cur.B1[h][ks], X[q][h]);
           }
         }
       }
@@ -356,7 +360,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
 #pragma unroll
     for (int q = 0; q < SRB; ++q)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) X[q][h] = mma3f(cur.K[q][ks], wf[ks], X[q][h]);
+      for (int ks = 0; ks < 2; ++ks) X[q][h] = mma3f<SD_STATE_TERMS>(cur.K[q][ks], wf[ks], X[q][h]);
   }
   __syncthreads();
 }

@@ -17,6 +17,10 @@ from . import _lib
 from .state import SolveDeltaState
 
 
+# widest key width r, and value group width, the HIP kernels take (include/solvedelta.h)
+_MAX_WIDTH = 128
+
+
 def _view(t: torch.Tensor) -> _lib.SdView:
     return _lib.SdView(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
 
@@ -178,8 +182,8 @@ def solvedelta_native(
         raise TypeError("associative_log_decay must be FP32")
     if geometry_write.dtype != torch.float32:
         raise TypeError("geometry_write must be FP32")
-    if r > 128 or V > 128:
-        raise ValueError("the MI355X path supports key and value widths up to 128")
+    if r > _MAX_WIDTH:
+        raise ValueError(f"the MI355X path supports key widths up to {_MAX_WIDTH}")
     if associative_log_decay.stride(-1) != 1:
         associative_log_decay = associative_log_decay.contiguous()
     if initial_state is not None:
@@ -189,18 +193,47 @@ def solvedelta_native(
         if any(s.dtype != torch.float32 for s in initial_state):
             raise TypeError("all continuation states must be FP32")
 
-    if T == 1 and not torch.is_grad_enabled():
+    if T == 1 and V <= _MAX_WIDTH and not torch.is_grad_enabled():
         return _decode(u, h, q, keys, values, associative_log_decay, erase_raw, write_raw,
                        geometry_write, initial_state, return_final_state)
 
     C0 = S0 = None
     if initial_state is not None:
         C0, S0 = (s.contiguous() for s in initial_state)
-    out, C_T, S_T = _SolveDeltaFn.apply(u, h, q, keys, values, associative_log_decay, erase_raw,
-                                        write_raw, geometry_write, C0, S0, return_final_state)
+    if V <= _MAX_WIDTH:
+        out, C_T, S_T = _SolveDeltaFn.apply(u, h, q, keys, values, associative_log_decay,
+                                            erase_raw, write_raw, geometry_write, C0, S0,
+                                            return_final_state)
+    else:
+        out, C_T, S_T = _value_groups(u, h, q, keys, values, associative_log_decay, erase_raw,
+                                      write_raw, geometry_write, C0, S0, return_final_state)
     if not return_final_state:
         return out, None
     return out, SolveDeltaState(C_T, S_T)
+
+
+def _value_groups(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,
+                  want_state):
+    """V > 128: the columns of S (and of the output) evolve independently given
+    the shared predictor C and the sources d, e, chi, so the value axis is cut
+    into groups of at most 128 columns, each run by the HIP path with the same
+    key-side inputs.  Every group recomputes the predictor identically; the
+    output and S are the groups' concatenation and C_T comes from the first
+    group, so autograd sums the shared inputs' gradients over the groups."""
+    V = values.shape[-1]
+    outs, S_parts, C_T = [], [], None
+    for g0 in range(0, V, _MAX_WIDTH):
+        g1 = min(V, g0 + _MAX_WIDTH)
+        S0g = None if S0 is None else S0[..., g0:g1].contiguous()
+        o, C, S = _SolveDeltaFn.apply(u, h, q, keys, values[..., g0:g1], log_decay, erase_raw,
+                                      write_raw[..., g0:g1], gamma, C0, S0g, want_state)
+        outs.append(o)
+        S_parts.append(S)
+        if g0 == 0:
+            C_T = C
+    out = torch.cat(outs, dim=-1)
+    S_T = torch.cat(S_parts, dim=-1) if want_state else None
+    return out, C_T, S_T
 
 
 __all__ = ["solvedelta_native"]

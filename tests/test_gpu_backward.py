@@ -100,3 +100,35 @@ def test_backward_strided_bitwise():
     g2 = torch.autograd.grad((o2, s2.predictor, s2.S), strided, cot)
     for a, b in zip(g1, g2):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("V,seed", [(256, 41), (200, 43)])
+def test_value_width_above_128_matches_oracle(V, seed):
+    """V > 128 runs as value groups of <= 128 columns (the columns of S are
+    independent given C, d, e, chi); forward, final states and all 11
+    gradients against the FP64 oracle.  The reference's Triton state pass
+    takes head widths up to 256 (residual_frame/common_left_h.py:140-151)."""
+    print(f"case V{V}", flush=True)
+    grads, rgrads = _grads(1, 96, 2, 64, V, seed)
+    _report(f"bwd V{V}", grads, rgrads, 3e-2)
+
+
+def test_value_width_above_128_forward_and_decode_dispatch():
+    """Forward states at V=256 and a T=1 no-grad call (which takes the chunked
+    path above 128 columns, as the reference does at residual_frame/operator.py:198-216)."""
+    from gpu_common import oracle_of
+    args = make_inputs(2, 70, 2, 32, 256, seed=47)
+    state = make_state(2, 2, 32, 256, seed=48)
+    with torch.no_grad():
+        out, st = _native()(*args, initial_state=state, return_final_state=True)
+        one = [a[:, :1] if a.ndim >= 3 else a for a in args]
+        o1, s1 = _native()(*one, initial_state=state, return_final_state=True)
+    eo, es = oracle_of(args, state)
+    eo1, es1 = oracle_of(one, state)
+    errs = [rel(out.float(), eo), rel(st.predictor, es.predictor), rel(st.S, es.S),
+            rel(o1.float(), eo1), rel(s1.S, es1.S)]
+    print("[V256 fwd/decode] " + " ".join(f"{e:.1e}" for e in errs), flush=True)
+    assert max(errs) < 1e-2
+    with pytest.raises(ValueError):
+        bad = make_inputs(1, 8, 1, 160, 16, seed=1)
+        _native()(*bad)
