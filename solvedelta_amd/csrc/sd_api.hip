@@ -43,13 +43,13 @@ FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
   w.delta = c.take<float>(panel);
   w.d = c.take<float>(panel);
   w.wS = c.take<float>(panel);
-  w.Wc = c.take_sp(panel);
+  w.Wc = c.take<_Float16>(panel);
   w.Uc = c.take<float>(panel);
-  w.Kc = c.take_sp(panel);
+  w.Kc = c.take<_Float16>(panel);
   w.Gam = c.take<float>(n * NT * kKD);
-  w.Ws = c.take_sp(panel);
+  w.Ws = c.take<_Float16>(panel);
   w.Us = c.take<float>(panel);
-  w.Ks = c.take_sp(panel);
+  w.Ks = c.take<_Float16>(panel);
   w.Qs = c.take_sp(panel);
   w.Ps = c.take_sp(n * NT * kBT * kBT);
   if (total) *total = c.off + 256;
@@ -63,10 +63,10 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   BwdWs w;
   w.Lc = c.take<float>(states);
   w.Ls = c.take<float>(states);
-  w.Wk = c.take_sp(panel);
-  w.At1 = c.take_sp(panel);
-  w.B1t = c.take_sp(panel);
-  w.Ant = c.take_sp(panel);
+  w.Wk = c.take<__bf16>(panel);
+  w.At1 = c.take<__bf16>(panel);
+  w.B1t = c.take<__bf16>(panel);
+  w.Ant = c.take<__bf16>(panel);
   float** panels[] = {&w.dU, &w.B1, &w.dwS, &w.dwC, &w.de, &w.dchi,
                       &w.dd, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
                       &w.uh};

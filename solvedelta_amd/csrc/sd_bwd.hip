@@ -157,10 +157,18 @@ struct BprepSSmem {
   SPanel64 At, Nt;   // A^T and N^T split once: the MFMA A operands of Wk and dU
 };
 
-__device__ __forceinline__ Frag ldfrag_g(const SP& sp, long long off) {
+// A fragment of an fp16 panel, re-split into bf16 high + low halves (exact:
+// fp16's 11-bit significand fits the two bf16 halves) for the 3-term product.
+__device__ __forceinline__ Frag ldfrag_h(const _Float16* p, long long off) {
+  const f16x8 v = *reinterpret_cast<const f16x8*>(p + off);
   Frag f;
-  f.h = *reinterpret_cast<const bf16x8*>(sp.hi + off);
-  f.l = *reinterpret_cast<const bf16x8*>(sp.lo + off);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    __bf16 a, b;
+    split_bf((float)v[e], a, b);
+    f.h[e] = a;
+    f.l[e] = b;
+  }
   return f;
 }
 static_assert(2 * BT * LS >= BT * KD, "P + N hold a 64 x 128 panel");
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       for (int e = 0; e < 8; ++e) r[e] = dout_raw(p, b, t0 + ks * 32 + kq + e, hh, cb * 16 + m);
 #pragma unroll
       for (int e = 0; e < 8; ++e) db[ks][e] = (__bf16)dout_val(r[e]);
-      kf[ks] = ldfrag_g(p.f.Ks, kbase + frag_off(cb * 16 + m, ks * 32 + kq, BT));
+      kf[ks] = ldfrag_h(p.f.Ks, kbase + frag_off(cb * 16 + m, ks * 32 + kq, BT));
     }
 #pragma unroll
     for (int Jb = 0; Jb < NB; ++Jb) {
@@ -255,7 +263,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) Wst[(Jb * BS + out_row(e)) * KD + w * 16 + out_col()] = wks[Jb][e];
     __syncthreads();
-    store_frag_panel<BT, KD>(p.g.Wk.hi, p.g.Wk.lo, rowbase * KD,
+    store_frag_panel1<BT, KD>(p.g.Wk, rowbase * KD,
                              [&](int i, int c) { return Wst[i * KD + c]; });
   }
   {  // chunk-transposed panels, fragment order: a thread's two pieces are
@@ -282,22 +290,17 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
       const int c = (block / (BT / 32)) * 16 + (lane & 15);
       const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
-      bf16x8 ah, al, qh, ql, dh;
+      bf16x8 ah, qh, dh;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        __bf16 x, y;
-        split_bf(-ev[q][e] * __expf(cd.G[i0 + e][c]), x, y);
-        ah[e] = x; al[e] = y;
-        qh[e] = qv[q][e].h;  // a transposed copy of an already split panel
-        ql[e] = qv[q][e].l;
-        dh[e] = (__bf16)dout_val(d[q][e]);  // exact in bf16: no low half is stored
+        ah[e] = (__bf16)(-ev[q][e] * __expf(cd.G[i0 + e][c]));
+        qh[e] = (__bf16)sp_val(qv[q][e]);   // a transposed, rounded copy of a split panel
+        dh[e] = (__bf16)dout_val(d[q][e]);  // exact in bf16
       }
       const long long ot = cidx * KD * BT + (long long)pc * 8;
-      *reinterpret_cast<bf16x8*>(p.g.Ant.hi + ot) = ah;
-      *reinterpret_cast<bf16x8*>(p.g.Ant.lo + ot) = al;
-      *reinterpret_cast<bf16x8*>(p.g.At1.hi + ot) = qh;
-      *reinterpret_cast<bf16x8*>(p.g.At1.lo + ot) = ql;
-      *reinterpret_cast<bf16x8*>(p.g.B1t.hi + ot) = dh;
+      *reinterpret_cast<bf16x8*>(p.g.Ant + ot) = ah;
+      *reinterpret_cast<bf16x8*>(p.g.At1 + ot) = qh;
+      *reinterpret_cast<bf16x8*>(p.g.B1t + ot) = dh;
     }
   }
 }
@@ -681,7 +684,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       }
       bd[ks] = split8(vd);
       bk[ks] = split8(vk);
-      kf[ks] = ldfrag_g(p.f.Kc, kbase + frag_off(cb * 16 + m, ks * 32 + kq, BT));
+      kf[ks] = ldfrag_h(p.f.Kc, kbase + frag_off(cb * 16 + m, ks * 32 + kq, BT));
     }
 #pragma unroll
     for (int Jb = 0; Jb < NB; ++Jb) {
@@ -716,7 +719,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) Wst[(Jb * BS + out_row(e)) * KD + w * 16 + out_col()] = wks[Jb][e];
     __syncthreads();
-    store_frag_panel<BT, KD>(p.g.Wk.hi, p.g.Wk.lo, rowbase * KD,
+    store_frag_panel1<BT, KD>(p.g.Wk, rowbase * KD,
                              [&](int i, int c) { return Wst[i * KD + c]; });
   }
   for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
@@ -728,7 +731,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   // The reverse pass's injection sum_i At1_ci Kh_i,col is formed as
   // sum_i (At1_ci / |k_i|) k_i,col: its B operand is then the raw key input,
   // exact in bf16, so only a high half is stored (and read).
-  store_frag_panel<KD, BT>(p.g.At1.hi, p.g.At1.lo, cidx * KD * BT, [&](int c, int i) {
+  store_frag_panel1<KD, BT>(p.g.At1, cidx * KD * BT, [&](int c, int i) {
     return ddp[i * KD + c] * __expf(cd.G[i][c]) * s.krs[i];
   });
   {
@@ -752,10 +755,10 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       bf16x8 h;
 #pragma unroll
       for (int e = 0; e < 8; ++e) h[e] = kr[q][e];
-      *reinterpret_cast<bf16x8*>(p.g.B1t.hi + cidx * KD * BT + (long long)(threadIdx.x + q * CT) * 8) = h;
+      *reinterpret_cast<bf16x8*>(p.g.B1t + cidx * KD * BT + (long long)(threadIdx.x + q * CT) * 8) = h;
     }
   }
-  store_frag_panel<KD, BT>(p.g.Ant.hi, p.g.Ant.lo, cidx * KD * BT, [&](int c, int i) {
+  store_frag_panel1<KD, BT>(p.g.Ant, cidx * KD * BT, [&](int c, int i) {
     return -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c));
   });
 }
@@ -1025,7 +1028,7 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
   ss.rev = 1;
   ss.Wneg = bw.Wk; ss.U = bw.dU; ss.Kt = bw.Ant; ss.Gam = fw.Gam;
-  ss.At1 = bw.At1; ss.B1 = bw.B1t; ss.b1_exact = 1;  // B1t = dO, exact in bf16
+  ss.At1 = bw.At1; ss.B1 = bw.B1t;  // B1t = dO, exact in bf16
   ss.Xs = bw.Ls; ss.wout = bw.dwS;
   ss.init = dS_T; ss.init_transposed = 0;
   ss.fin = dS0; ss.fin_transposed = 0;
@@ -1038,7 +1041,7 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
   sc.rev = 1;
   sc.Wneg = bw.Wk; sc.U = bw.dU; sc.Kt = bw.Ant; sc.Gam = fw.Gam;
-  sc.At1 = bw.At1; sc.B1 = bw.B1t; sc.b1_exact = 1;  // B1t = raw keys, exact in bf16
+  sc.At1 = bw.At1; sc.B1 = bw.B1t;  // B1t = raw keys, exact in bf16
   sc.Xs = bw.Lc; sc.wout = bw.dwC;
   sc.init = dC_T; sc.init_transposed = 1;
   sc.fin = dC0; sc.fin_transposed = 1;

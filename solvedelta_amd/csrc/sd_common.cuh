@@ -17,12 +17,6 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
-// Bf16 MFMA terms per product of two split (hi + lo) operands: 3 = hi*hi +
-// hi*lo + lo*hi (~16 mantissa bits), 2 = the A operand's high half only.
-#ifndef SD_CHUNK_TERMS
-#define SD_CHUNK_TERMS 3
-#endif
-
 namespace sd {
 
 constexpr int BT = 64;     // chunk length
@@ -39,6 +33,8 @@ constexpr int CW = CT / 64;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
@@ -161,8 +157,8 @@ __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
         split_bf(bv[ks][e], h, lo);
         bh[e] = h; bl[e] = lo;
       }
-      if constexpr (SD_CHUNK_TERMS >= 3) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-      if constexpr (SD_CHUNK_TERMS >= 2) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
     }
   }
@@ -200,14 +196,10 @@ __device__ __forceinline__ void mma_k32x2(FA fa, FB1 fb1, FB2 fb2, int K, f4& ac
         split_bf(b2[ks][e], h, lo);
         dh[e] = h; dl[e] = lo;
       }
-      if constexpr (SD_CHUNK_TERMS >= 3) {
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ch, acc1, 0, 0, 0);
-        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, dh, acc2, 0, 0, 0);
-      }
-      if constexpr (SD_CHUNK_TERMS >= 2) {
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, cl, acc1, 0, 0, 0);
-        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dl, acc2, 0, 0, 0);
-      }
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ch, acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, dh, acc2, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, cl, acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dl, acc2, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ch, acc1, 0, 0, 0);
       acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dh, acc2, 0, 0, 0);
     }
@@ -277,6 +269,26 @@ __device__ __forceinline__ void store_frag_panel(__bf16* hi, __bf16* lo, long lo
     }
     *reinterpret_cast<bf16x8*>(hi + base + (long long)pc * 8) = h;
     *reinterpret_cast<bf16x8*>(lo + base + (long long)pc * 8) = l;
+  }
+}
+
+// store_frag_panel for a panel kept in one 2-byte type E (fp16, or bf16 with
+// no low half): each piece is val rounded to E, one 16-byte store per lane.
+template <int R, int C, class E, class F>
+__device__ __forceinline__ void store_frag_panel1(E* dst, long long base, F val) {
+  typedef E V8 __attribute__((ext_vector_type(8)));
+  constexpr int PIECES = R * C / 8;
+#pragma unroll
+  for (int q = 0; q < (PIECES + CT - 1) / CT; ++q) {
+    const int pc = threadIdx.x + q * CT;
+    if (PIECES % CT != 0 && pc >= PIECES) break;
+    const int block = pc >> 6, lane = pc & 63;
+    const int row = (block / (C / 32)) * 16 + (lane & 15);
+    const int col0 = (block % (C / 32)) * 32 + (lane >> 4) * 8;
+    V8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (E)val(row, col0 + e);
+    *reinterpret_cast<V8*>(dst + base + (long long)pc * 8) = h;
   }
 }
 
@@ -550,10 +562,9 @@ namespace sd {
 // Pre-split (bf16 hi + lo) MFMA operand fragment and the 3-term product.
 struct Frag { bf16x8 h, l; };
 
-template <int TERMS = SD_CHUNK_TERMS>
 __device__ __forceinline__ f4 mma3f(const Frag& a, const Frag& b, f4 acc) {
-  if constexpr (TERMS >= 3) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, acc, 0, 0, 0);
-  if constexpr (TERMS >= 2) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.l, acc, 0, 0, 0);
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, acc, 0, 0, 0);
 }
 

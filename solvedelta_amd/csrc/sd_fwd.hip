@@ -125,14 +125,14 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
-        sp_store(p.Wc, rowbase * KD + frag_off(I * BS + out_row(e), c, KD), -aw[e]);
+        p.Wc[rowbase * KD + frag_off(I * BS + out_row(e), c, KD)] = (_Float16)(-aw[e]);
         p.Uc[row * KD + c] = au[e];
       }
     }
   }
   // decayed keys (transposed per chunk) and chunk decay
   const long long cbase = ((long long)n * p.NT + ch);
-  store_frag_panel<KD, BT>(p.Kc.hi, p.Kc.lo, cbase * KD * BT, [&](int c, int i) {
+  store_frag_panel1<KD, BT>(p.Kc, cbase * KD * BT, [&](int c, int i) {
     return s.Uh[i][c] * __expf(cd.G[BT - 1][c] - cd.G[i][c]);
   });
   if (threadIdx.x < KD) p.Gam[cbase * KD + threadIdx.x] = __expf(cd.G[BT - 1][threadIdx.x]);
@@ -155,9 +155,6 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
 // token block w.  KD / SCOLS workgroups cover a sequence's state columns; every
 // one of them reads the chunk's full W and K panels, so wider tiles mean less
 // panel traffic per chunk step.
-#ifndef SD_STATE_TERMS
-#define SD_STATE_TERMS 3
-#endif
 constexpr int SCOLS = 16;
 constexpr int HALVES = SCOLS / 16;
 constexpr int SWAVES = 4;
@@ -172,11 +169,39 @@ constexpr int PF = 3;
 // an MFMA output tile (rows 4 apart) land on distinct LDS banks.
 constexpr int XFS = SCOLS + 4;
 
+// Operand types of the two pass kinds.  Forward (REV false): the W and K panels
+// are fp16 (11-bit mantissa; both are bounded by construction: W = -(I+L)^-1
+// x~ and K = k e^{G_C - G} with unit-norm or decayed rows), the state X and w
+// are split into fp16 high + low halves (~22 bits), two f16 MFMAs per product.
+// Reverse (REV true): the panels are bf16 (the exponent range of bf16 keeps any
+// scale of the output cotangent representable), the cotangent state lambda and
+// dw split into bf16 halves, two bf16 MFMAs per product; the injection A1 B1 is
+// one bf16 MFMA (B1 is exact in bf16).
+template <bool REV> struct StateT;
+template <> struct StateT<false> {
+  using E = _Float16;
+  using V8 = f16x8;
+  using V4 = f16x4;
+  static __device__ __forceinline__ f4 mma(V8 a, V8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct StateT<true> {
+  using E = __bf16;
+  using V8 = bf16x8;
+  using V4 = bf16x4;
+  static __device__ __forceinline__ f4 mma(V8 a, V8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <bool REV>
 struct StateSmem {
-  __bf16 Xh[SCOLS][KD + 8];  // X0 tile, transposed [col][row], split hi / lo
-  __bf16 Xl[SCOLS][KD + 8];
-  __bf16 wh[SCOLS][BT + 8];  // w tile, transposed [col][token], split hi / lo
-  __bf16 wl[SCOLS][BT + 8];
+  using E = typename StateT<REV>::E;
+  E Xh[SCOLS][KD + 8];  // X0 tile, transposed [col][row], split high / low
+  E Xl[SCOLS][KD + 8];
+  E wh[SCOLS][BT + 8];  // w tile, transposed [col][token], split high / low
+  E wl[SCOLS][BT + 8];
   // fp32 copies of the X0 slot and the w tile, row-major, written back to global
   // memory as 16-byte pieces: a wave may hold at most 63 memory operations in
   // flight, and the prefetch ring needs that budget more than scalar stores do.
@@ -186,103 +211,100 @@ struct StateSmem {
   float Gf[KD];       // chunk decay, staged from one 16-byte load per lane of wave 0
 };
 
-template <bool INJ>
+template <bool REV>
 struct StateFrags {
-  Frag W[4];
-  Frag K[SRB][2];
-  Frag A1[INJ ? SRB : 1][2];
-  Frag B1[INJ ? HALVES : 1][2];
+  using V8 = typename StateT<REV>::V8;
+  V8 W[4];
+  V8 K[SRB][2];
+  bf16x8 A1[REV ? SRB : 1][2];
+  bf16x8 B1[REV ? HALVES : 1][2];
   float4 U4;  // U tile piece: token threadIdx / (SCOLS / 4), columns 4 (threadIdx % (SCOLS / 4))
   float4 G4;  // chunk decay, columns 4 (threadIdx % 32) .. +3 (every wave loads all 128)
 };
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ bf16x8 ldb8(const __bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
-__device__ __forceinline__ Frag ldfrag(const SP& sp, long long off) {
-  Frag f;
-  f.h = ldb8(sp.hi + off);
-  f.l = ldb8(sp.lo + off);
-  return f;
-}
+template <class V8, class E>
+__device__ __forceinline__ V8 ldv8(const E* p) { return *reinterpret_cast<const V8*>(p); }
 
-// B1X: the injection's B operand is exact in bf16 (its stored low half is zero),
-// so only the high half is loaded and multiplied.
-template <bool INJ, bool B1X>
+template <bool REV>
 __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
-                                                 StateFrags<INJ>& f) {
+                                                 StateFrags<REV>& f) {
+  using E = typename StateT<REV>::E;
+  using V8 = typename StateT<REV>::V8;
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
   const int tb = w;  // this wave's token block
   const long long cidx = (long long)n * p.NT + ch;
   const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
   const long long wb = rowbase * KD;
+  const E* Wp = static_cast<const E*>(p.Wneg);
+  const E* Kp = static_cast<const E*>(p.Kt);
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldfrag(p.Wneg, wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
+  for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldv8<V8>(Wp + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
 #pragma unroll
   for (int q = 0; q < SRB; ++q)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      f.K[q][ks] = ldfrag(p.Kt, cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
+      f.K[q][ks] = ldv8<V8>(Kp + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
   {
     constexpr int C4 = SCOLS / 4;
     static_assert(BT * C4 == STHREADS, "one U piece per thread");
     f.U4 = ld4(p.U + (rowbase + threadIdx.x / C4) * KD + tile * SCOLS + (threadIdx.x % C4) * 4);
   }
   f.G4 = ld4(p.Gam + cidx * KD + (l & 31) * 4);
-  if constexpr (INJ) {
+  if constexpr (REV) {
 #pragma unroll
     for (int q = 0; q < SRB; ++q)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        f.A1[q][ks] =
-            ldfrag(p.At1, cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
+        f.A1[q][ks] = ldb8(p.At1 + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
 #pragma unroll
     for (int h = 0; h < HALVES; ++h)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-      {
-        const long long o = cidx * KD * BT + frag_off(tile * SCOLS + h * 16 + m, ks * 32 + kq, BT);
-        if constexpr (B1X)
-          f.B1[h][ks].h = ldb8(p.B1.hi + o);
-        else
-          f.B1[h][ks] = ldfrag(p.B1, o);
-      }
+        f.B1[h][ks] =
+            ldb8(p.B1 + cidx * KD * BT + frag_off(tile * SCOLS + h * 16 + m, ks * 32 + kq, BT));
   }
 }
 
-__device__ __forceinline__ void stage_split4(__bf16* hi, __bf16* lo, f4 v) {
-  bf16x4 h, l;
+// Splits four fp32 values into high / low halves of type E and stores each as
+// one 8-byte piece.
+template <class E, class V4>
+__device__ __forceinline__ void stage_split4(E* hi, E* lo, f4 v) {
+  V4 h, l;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    __bf16 a, b;
-    split_bf(v[e], a, b);
+    const E a = (E)v[e];
     h[e] = a;
-    l[e] = b;
+    l[e] = (E)(v[e] - (float)a);
   }
-  *reinterpret_cast<bf16x4*>(hi) = h;
-  *reinterpret_cast<bf16x4*>(lo) = l;
+  *reinterpret_cast<V4*>(hi) = h;
+  *reinterpret_cast<V4*>(lo) = l;
 }
 
 // One chunk of the sequential pass with its operand fragments already in registers.
-template <bool INJ, bool B1X>
-__device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, int n, int ch, int tile,
-                                           const StateFrags<INJ>& cur,
+template <bool REV>
+__device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>& s, int n, int ch,
+                                           int tile, const StateFrags<REV>& cur,
                                            f4 (&X)[SRB][HALVES]) {
+  using T = StateT<REV>;
+  using E = typename T::E;
+  using V8 = typename T::V8;
+  using V4 = typename T::V4;
   const int NS = p.NT + 1;
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
   const int tb = w;
   const long long sidx = (long long)n * NS + ch;
-  if (!p.rev && tile == 0 && n == 0) {  // per-step marks: C pass slot 6, S pass slot 4
-  }
   const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
   // save X0 and stage it split and transposed ([col][row]) for the B operand
 #pragma unroll
   for (int q = 0; q < SRB; ++q)
 #pragma unroll
     for (int h = 0; h < HALVES; ++h) {
-      const int row0 = (SRB * w + q) * 16 + r4, col = tile * SCOLS + h * 16 + m;
+      const int row0 = (SRB * w + q) * 16 + r4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) s.Xf[row0 + e][h * 16 + m] = X[q][h][e];
-      stage_split4(&s.Xh[h * 16 + m][row0], &s.Xl[h * 16 + m][row0], X[q][h]);
+      stage_split4<E, V4>(&s.Xh[h * 16 + m][row0], &s.Xl[h * 16 + m][row0], X[q][h]);
     }
   *reinterpret_cast<float4*>(&s.Uf[threadIdx.x / (SCOLS / 4)][(threadIdx.x % (SCOLS / 4)) * 4]) = cur.U4;
   if (threadIdx.x < KD / 4) *reinterpret_cast<float4*>(&s.Gf[threadIdx.x * 4]) = cur.G4;
@@ -308,10 +330,10 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
     for (int h = 0; h < HALVES; ++h) {
-      Frag xb;
-      xb.h = ldb8(&s.Xh[h * 16 + m][ks * 32 + kq]);
-      xb.l = ldb8(&s.Xl[h * 16 + m][ks * 32 + kq]);
-      acc[h] = mma3f<SD_STATE_TERMS>(cur.W[ks], xb, acc[h]);
+      const V8 xh = ldv8<V8>(&s.Xh[h * 16 + m][ks * 32 + kq]);
+      const V8 xl = ldv8<V8>(&s.Xl[h * 16 + m][ks * 32 + kq]);
+      acc[h] = T::mma(cur.W[ks], xl, acc[h]);
+      acc[h] = T::mma(cur.W[ks], xh, acc[h]);
     }
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
@@ -320,17 +342,11 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
 #pragma unroll
     for (int h = 0; h < HALVES; ++h) {
       for (int e = 0; e < 4; ++e) X[q][h][e] *= gv[e];
-      if constexpr (INJ) {
+      if constexpr (REV) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          if constexpr (B1X) {
-            if constexpr (SD_STATE_TERMS >= 3)
-              X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks].l, cur.B1[h][ks].h, X[q][h], 0, 0, 0);
-            X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks].h, cur.B1[h][ks].h, X[q][h], 0, 0, 0);
-          } else {
-            X[q][h] = mma3f<SD_STATE_TERMS>(cur.A1[q][ks], cur.B1[h][ks], X[q][h]);
-          }
-        }
+        for (int ks = 0; ks < 2; ++ks)
+          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks], cur.B1[h][ks], X[q][h],
+                                                           0, 0, 0);
       }
     }
   }
@@ -338,7 +354,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
   for (int h = 0; h < HALVES; ++h) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) s.wf[tb * 16 + r4 + e][h * 16 + m] = acc[h][e];
-    stage_split4(&s.wh[h * 16 + m][tb * 16 + r4], &s.wl[h * 16 + m][tb * 16 + r4], acc[h]);
+    stage_split4<E, V4>(&s.wh[h * 16 + m][tb * 16 + r4], &s.wl[h * 16 + m][tb * 16 + r4], acc[h]);
   }
   __syncthreads();
   {  // w write-back: 64 tokens x SCOLS columns as float4 pieces
@@ -351,23 +367,26 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem& s, i
   // X += Kt w: the recurrence's critical path
 #pragma unroll
   for (int h = 0; h < HALVES; ++h) {
-    Frag wf[2];
+    V8 wh[2], wl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      wf[ks].h = ldb8(&s.wh[h * 16 + m][ks * 32 + kq]);
-      wf[ks].l = ldb8(&s.wl[h * 16 + m][ks * 32 + kq]);
+      wh[ks] = ldv8<V8>(&s.wh[h * 16 + m][ks * 32 + kq]);
+      wl[ks] = ldv8<V8>(&s.wl[h * 16 + m][ks * 32 + kq]);
     }
 #pragma unroll
     for (int q = 0; q < SRB; ++q)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) X[q][h] = mma3f<SD_STATE_TERMS>(cur.K[q][ks], wf[ks], X[q][h]);
+      for (int ks = 0; ks < 2; ++ks) {
+        X[q][h] = T::mma(cur.K[q][ks], wl[ks], X[q][h]);
+        X[q][h] = T::mma(cur.K[q][ks], wh[ks], X[q][h]);
+      }
   }
   __syncthreads();
 }
 
-template <bool INJ, bool B1X>
+template <bool REV>
 __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
-  __shared__ __align__(16) StateSmem s;
+  __shared__ __align__(16) StateSmem<REV> s;
   const int NS = p.NT + 1;  // state slots per sequence
   // Workgroups are dispatched round-robin over the 8 XCDs by linear id; when the
   // sequence count allows, map ids so that the column tiles of a sequence run
@@ -405,20 +424,20 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   // prefetches) so the compiler's wait counts only cover the buffer being
   // consumed; the last PF - 1 or fewer chunks run after the loop.
   auto clampc = [&](int it2) { return chunk_of(it2 < NT ? it2 : NT - 1); };
-  StateFrags<INJ> f[PF];
+  StateFrags<REV> f[PF];
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j) load_state_frags<INJ, B1X>(p, n, clampc(j), tile, f[j]);
+  for (int j = 0; j < PF - 1; ++j) load_state_frags<REV>(p, n, clampc(j), tile, f[j]);
   int it = 0;
   for (; it + PF - 1 < NT; it += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      load_state_frags<INJ, B1X>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
-      state_step<INJ, B1X>(p, s, n, chunk_of(it + j), tile, f[j], X);
+      load_state_frags<REV>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
+      state_step<REV>(p, s, n, chunk_of(it + j), tile, f[j], X);
     }
   }
 #pragma unroll
   for (int j = 0; j < PF - 1; ++j)
-    if (it + j < NT) state_step<INJ, B1X>(p, s, n, chunk_of(it + j), tile, f[j], X);
+    if (it + j < NT) state_step<REV>(p, s, n, chunk_of(it + j), tile, f[j], X);
   // final state (also kept as slot NT for the backward)
   for (int q = 0; q < SRB; ++q)
     for (int h = 0; h < HALVES; ++h)
@@ -438,12 +457,10 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
 
 void launch_state(const char* name, const StateParams& sp, int nseq, hipStream_t st) {
   const dim3 grid(STILES * nseq), blk(STHREADS);
-  if (sp.At1.hi && sp.b1_exact)
-    SD_LAUNCH(name, (k_state<true, true>), grid, blk, 0, st, sp);
-  else if (sp.At1.hi)
-    SD_LAUNCH(name, (k_state<true, false>), grid, blk, 0, st, sp);
+  if (sp.rev)
+    SD_LAUNCH(name, (k_state<true>), grid, blk, 0, st, sp);
   else
-    SD_LAUNCH(name, (k_state<false, false>), grid, blk, 0, st, sp);
+    SD_LAUNCH(name, (k_state<false>), grid, blk, 0, st, sp);
 }
 
 // ---------------------------------------------------------------------------
@@ -656,19 +673,15 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   // the decayed keys K^ = d e^{G_C - G} (chunk-transposed, fragment order) are
   // formed from d while it is still in LDS and stored after the P Gram
   constexpr int KPC = KD * BT / 8 / CT;  // pieces per thread
-  bf16x8 ksh[KPC], ksl[KPC];
+  f16x8 ksv[KPC];
 #pragma unroll
   for (int q = 0; q < KPC; ++q) {
     const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
     const int c = (block / (BT / 32)) * 16 + (lane & 15);
     const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      __bf16 a, b2;
-      split_bf(s.Pc[i0 + e][c] * __expf(cd.G[BT - 1][c] - cd.G[i0 + e][c]), a, b2);
-      ksh[q][e] = a;
-      ksl[q][e] = b2;
-    }
+    for (int e = 0; e < 8; ++e)
+      ksv[q][e] = (_Float16)(s.Pc[i0 + e][c] * __expf(cd.G[BT - 1][c] - cd.G[i0 + e][c]));
   }
   stage_ytilde(s.Kp, cd, [&](int j, int c) { return s.Pc[j][c]; });
   const float* const dg_ = p.d + rowbase * KD;
@@ -680,8 +693,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
 #pragma unroll
   for (int q = 0; q < KPC; ++q) {
     const long long o = cidx * KD * BT + (long long)(threadIdx.x + q * CT) * 8;
-    *reinterpret_cast<bf16x8*>(p.Ks.hi + o) = ksh[q];
-    *reinterpret_cast<bf16x8*>(p.Ks.lo + o) = ksl[q];
+    *reinterpret_cast<f16x8*>(p.Ks + o) = ksv[q];
   }
   store_frag_panel<BT, KD>(p.Qs.hi, p.Qs.lo, rowbase * KD,
                            [&](int i, int c) { return s.Pb[i][c] * __expf(cd.G[i][c]); });
@@ -721,7 +733,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     }
   }
   __syncthreads();
-  store_frag_panel<BT, KD>(p.Ws.hi, p.Ws.lo, rowbase * KD, [&](int i, int c) { return s.Pc[i][c]; });
+  store_frag_panel1<BT, KD>(p.Ws, rowbase * KD, [&](int i, int c) { return s.Pc[i][c]; });
 }
 
 size_t prep_c_smem() { return sizeof(PrepCSmem); }

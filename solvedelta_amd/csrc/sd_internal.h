@@ -53,27 +53,29 @@ struct FwdWs {
   float* delta;  // predictor write delta (C-op w)          [n][Tp][128]
   float* d;      // primal address d = k + C^T k            [n][Tp][128]
   float* wS;     // S-op w = z - S~^T e                     [n][Tp][128]
-  // transient panels
-  SP Wc; float* Uc; SP Kc; float* Gam;
-  SP Ws; float* Us; SP Ks; SP Qs; SP Ps;
+  // transient panels; the forward state passes' MFMA operands W (token-major)
+  // and K (chunk-transposed) are fp16 in fragment order
+  _Float16* Wc; float* Uc; _Float16* Kc; float* Gam;
+  _Float16* Ws; float* Us; _Float16* Ks; SP Qs; SP Ps;
 };
 
 struct FwdParams {
   sd_inputs in;
   int H, T, r, V, NT, Tp;
   float *Xc, *delta, *d, *Ac, *As, *e, *chi;
-  SP Wc; float* Uc; SP Kc; float* Gam;
-  SP Ws; float* Us; SP Ks; SP Qs; SP Ps;
+  _Float16* Wc; float* Uc; _Float16* Kc; float* Gam;
+  _Float16* Ws; float* Us; _Float16* Ks; SP Qs; SP Ps;
 };
 
-// Sequential chunk pass, forward (state X) or reverse (cotangent lambda):
-//   slot[ch] = X;  w = U + Wneg X;  X = Gamma X + Kt w (+ At1 B1)
-// Kt, At1 are chunk-transposed [128][64]; B1 is chunk-transposed [128 cols][64 tokens].
+// Sequential chunk pass, forward (state X) or reverse (cotangent lambda, rev):
+//   slot[ch] = X;  w = U + Wneg X;  X = Gamma X + Kt w (+ At1 B1 when rev)
+// Wneg token-major [Tp][128], Kt and At1 chunk-transposed [128][64], B1
+// chunk-transposed [128 cols][64 tokens], all in fragment order.  Wneg and Kt
+// are fp16 in forward passes and bf16 in reverse passes; At1 and B1 are bf16.
 struct StateParams {
   int H, T, NT, Tp, rows, cols, rev;
-  SP Wneg; const float* U; SP Kt; const float* Gam;
-  SP At1; SP B1;  // optional injection
-  int b1_exact;     // B1 is exact in bf16: its low half is zero and not read
+  const void* Wneg; const float* U; const void* Kt; const float* Gam;
+  const __bf16* At1; const __bf16* B1;  // reverse-pass injection
   float* Xs; float* wout;
   const float* init; int init_transposed;
   float* fin; int fin_transposed;
@@ -117,7 +119,8 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
 struct BwdWs {
   float* Lc;   // C-op chunk-end cotangents                [n][NT+1][128][128]
   float* Ls;   // S-op chunk-end cotangents
-  float* dU; SP Wk; SP At1; float* B1; SP B1t; SP Ant;  // reverse-pass panels (reused)
+  // reverse-pass panels (reused by both ops), bf16 in fragment order
+  float* dU; __bf16* Wk; __bf16* At1; float* B1; __bf16* B1t; __bf16* Ant;
   float* dwS; float* dwC;          // dw of each op           [n][Tp][128]
   float* de; float* dchi; float* dd;
   float* ddelta; float* du_src; float* dk_src;
