@@ -34,15 +34,15 @@ FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
   const size_t panel = n * Tp * kKD, states = n * (NT + 1) * kKD * kKD, amat = n * NT * kBT * kBT;
   Carver c{(char*)base};
   FwdWs w;
-  w.Xc = c.take<float>(states);
-  w.Xs = c.take<float>(states);
+  w.Xc = c.take<xslot_t>(states);
+  w.Xs = c.take<xslot_t>(states);
   w.Ac = c.take<float>(amat);
   w.As = c.take<float>(amat);
-  w.e = c.take<float>(panel);
-  w.chi = c.take<float>(panel);
-  w.delta = c.take<float>(panel);
-  w.d = c.take<float>(panel);
-  w.wS = c.take<float>(panel);
+  w.e = c.take<fpan_t>(panel);
+  w.chi = c.take<fpan_t>(panel);
+  w.delta = c.take<fpan_t>(panel);
+  w.d = c.take<fpan_t>(panel);
+  w.wS = c.take<fpan_t>(panel);
   w.Wc = c.take<_Float16>(panel);
   w.Uc = c.take<float>(panel);
   w.Kc = c.take<_Float16>(panel);
@@ -61,8 +61,8 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   const size_t panel = n * Tp * kKD, states = n * (NT + 1) * kKD * kKD;
   Carver c{(char*)base};
   BwdWs w;
-  w.Lc = c.take<float>(states);
-  w.Ls = c.take<float>(states);
+  w.Lc = c.take<lslot_t>(states);
+  w.Ls = c.take<lslot_t>(states);
   w.Wk = c.take<__bf16>(panel);
   w.At1 = c.take<__bf16>(panel);
   w.B1t = c.take<__bf16>(panel);

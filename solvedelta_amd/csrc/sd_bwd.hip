@@ -280,7 +280,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int i = i0 + e;
-        ev[q][e] = p.f.e[(rowbase + i) * KD + c];
+        ev[q][e] = (float)p.f.e[(rowbase + i) * KD + c];
         qv[q][e] = sp_raw(p.f.Qs, rowbase * KD + frag_off(i, c, KD));
         d[q][e] = dout_raw(p, b, t0 + i, hh, c);
       }
@@ -324,7 +324,7 @@ __device__ __forceinline__ void lam_rowsum(const Blk& rl, const Blk& rx, int cb,
   split_blk(rl, BL);
 }
 
-__device__ __forceinline__ void load_lam_rowsum(const float* lam, const float* XC, int cb, BlkS& BL,
+__device__ __forceinline__ void load_lam_rowsum(const lslot_t* lam, const xslot_t* XC, int cb, BlkS& BL,
                                                 float (*rsum)[KD]) {
   Blk rl, rx;
   load_blk(rl, lam + cb * 16 * KD, KD);
@@ -377,13 +377,13 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
   const float* dw = p.g.dwS + rowbase * KD;
-  const float* wv = p.f.wS + rowbase * KD;
-  const float* dd_ = p.f.d + rowbase * KD;
-  const float* ee = p.f.e + rowbase * KD;
-  const float* chi = p.f.chi + rowbase * KD;
-  const float* X0 = p.f.Xs + sidx * KD * KD;
-  const float* XC = X0 + KD * KD;
-  const float* lam = p.g.Ls + sidx * KD * KD;
+  const fpan_t* wv = p.f.wS + rowbase * KD;
+  const fpan_t* dd_ = p.f.d + rowbase * KD;
+  const fpan_t* ee = p.f.e + rowbase * KD;
+  const fpan_t* chi = p.f.chi + rowbase * KD;
+  const xslot_t* X0 = p.f.Xs + sidx * KD * KD;
+  const xslot_t* XC = X0 + KD * KD;
+  const lslot_t* lam = p.g.Ls + sidx * KD * KD;
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
@@ -427,9 +427,9 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   for (int I = 0; I < NB; ++I)
 #pragma unroll
     for (int e = 0; e < 4; ++e) kl_park[(I * 4 + e) * CT + threadIdx.x] = kl[I][e];
-  auto D = [&](int j, int cc) { return dd_[j * KD + cc]; };
-  auto E = [&](int j, int cc) { return ee[j * KD + cc]; };
-  auto Q = [&](int j, int cc) { return chi[j * KD + cc]; };
+  auto D = [&](int j, int cc) { return (float)dd_[j * KD + cc]; };
+  auto E = [&](int j, int cc) { return (float)ee[j * KD + cc]; };
+  auto Q = [&](int j, int cc) { return (float)chi[j * KD + cc]; };
   Tab1 t1;
   RowF rf;
   ColF cf;
@@ -529,7 +529,7 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   ldrow2(p.in.erase_raw, b, t, hh, p.T, r, e0, e1);
   ldrow2(p.in.write_raw, b, t, hh, p.T, V, w0, w1);
   ldrow2(p.in.v, b, t, hh, p.T, V, v0, v1);
-  const float d0 = p.f.delta[row + l], d1 = p.f.delta[row + l + 64];
+  const float d0 = (float)p.f.delta[row + l], d1 = (float)p.f.delta[row + l + 64];
   const float de0 = p.g.de[row + l], de1 = p.g.de[row + l + 64];
   const float dc0 = p.g.dchi[row + l], dc1 = p.g.dchi[row + l + 64];
   const float dz0 = p.g.dwS[row + l], dz1 = p.g.dwS[row + l + 64];
@@ -781,14 +781,14 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   const long long sidx = (long long)n * (p.NT + 1) + ch;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
   const float* dw = p.g.dwC + rowbase * KD;
-  const float* wv = p.f.delta + rowbase * KD;
+  const fpan_t* wv = p.f.delta + rowbase * KD;
   const float* ddp = p.g.dd + rowbase * KD;   // cotangent of the C-op output
   const float* kh = p.g.B1 + rowbase * KD;    // normalised keys
   const float* uh = p.g.uh + rowbase * KD;    // normalised u
-  const float* dprim = p.f.d + rowbase * KD;  // d = k + output
-  const float* X0 = p.f.Xc + sidx * KD * KD;
-  const float* XC = X0 + KD * KD;
-  const float* lam = p.g.Lc + sidx * KD * KD;
+  const fpan_t* dprim = p.f.d + rowbase * KD;  // d = k + output
+  const xslot_t* X0 = p.f.Xc + sidx * KD * KD;
+  const xslot_t* XC = X0 + KD * KD;
+  const lslot_t* lam = p.g.Lc + sidx * KD * KD;
   if (threadIdx.x < BT) {
     const int t = t0 + threadIdx.x;
     {  // clamped token, then select (a guarded load would branch and wait)
@@ -922,7 +922,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       for (int ks = 0; ks < 4; ++ks) {
         float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = X0[(ks * 32 + kq + e) * KD + c];
+        for (int e = 0; e < 8; ++e) v[e] = (float)X0[(ks * 32 + kq + e) * KD + c];
         raw.v[ks][0] = make_float4(v[0], v[1], v[2], v[3]);
         raw.v[ks][1] = make_float4(v[4], v[5], v[6], v[7]);
       }

@@ -536,22 +536,43 @@ struct Blk { float4 v[4][2]; };
 
 __device__ __forceinline__ float4 ld4g(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
-__device__ __forceinline__ void load_blk(Blk& b, const float* rows, int ld) {
-  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
-  const float* a = rows + (long long)m * ld + kq;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    b.v[ks][0] = ld4g(a + ks * 32);
-    b.v[ks][1] = ld4g(a + ks * 32 + 4);
-  }
+// Eight consecutive elements of a panel of element type E (fp32, or a 2-byte
+// type: one 16-byte load) as two float4.
+__device__ __forceinline__ void ld8f(const float* p, float4& a, float4& b) {
+  a = ld4g(p);
+  b = ld4g(p + 4);
+}
+template <class E>
+__device__ __forceinline__ void ld8f(const E* p, float4& a, float4& b) {
+  typedef E V8 __attribute__((ext_vector_type(8)));
+  const V8 v = *reinterpret_cast<const V8*>(p);
+  a = make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+  b = make_float4((float)v[4], (float)v[5], (float)v[6], (float)v[7]);
+}
+// Four consecutive elements as a float4.
+__device__ __forceinline__ float4 ld4f(const float* p) { return ld4g(p); }
+template <class E>
+__device__ __forceinline__ float4 ld4f(const E* p) {
+  typedef E V4 __attribute__((ext_vector_type(4)));
+  const V4 v = *reinterpret_cast<const V4*>(p);
+  return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
-__device__ __forceinline__ void load_slab(float (&s)[NB][4], const float* panel, int cb) {
+template <class E>
+__device__ __forceinline__ void load_blk(Blk& b, const E* rows, int ld) {
+  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+  const E* a = rows + (long long)m * ld + kq;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) ld8f(a + ks * 32, b.v[ks][0], b.v[ks][1]);
+}
+
+template <class E>
+__device__ __forceinline__ void load_slab(float (&s)[NB][4], const E* panel, int cb) {
   const int l = lane_id(), c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
 #pragma unroll
   for (int J = 0; J < NB; ++J)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s[J][e] = panel[(J * BS + r4 + e) * KD + c];
+    for (int e = 0; e < 4; ++e) s[J][e] = (float)panel[(J * BS + r4 + e) * KD + c];
 }
 
 
@@ -824,12 +845,12 @@ struct LPanel {
 
 // All CT threads: src is a [64][128] fp32 panel (row stride KD) in global memory;
 // optional scale(i, c) multiplies each element before the split.
-template <class FS>
-__device__ __forceinline__ void stage_panel(LPanel& P, const float* src, FS scale) {
+template <class E, class FS>
+__device__ __forceinline__ void stage_panel(LPanel& P, const E* src, FS scale) {
   constexpr int PER = BT * KD / 4 / CT;  // float4 per thread
   float4 v[PER];
 #pragma unroll
-  for (int q = 0; q < PER; ++q) v[q] = ld4g(src + (threadIdx.x + q * CT) * 4);
+  for (int q = 0; q < PER; ++q) v[q] = ld4f(src + (threadIdx.x + q * CT) * 4);
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
@@ -848,7 +869,8 @@ __device__ __forceinline__ void stage_panel(LPanel& P, const float* src, FS scal
   }
 }
 
-__device__ __forceinline__ void stage_panel(LPanel& P, const float* src) {
+template <class E>
+__device__ __forceinline__ void stage_panel(LPanel& P, const E* src) {
   stage_panel(P, src, [](int, int) { return 1.f; });
 }
 
@@ -862,7 +884,8 @@ __device__ __forceinline__ void lblk(const LPanel& P, int row0, BlkS& o) {
   }
 }
 
-__device__ __forceinline__ void load_split_blk_g(const float* rows, BlkS& o) {
+template <class E>
+__device__ __forceinline__ void load_split_blk_g(const E* rows, BlkS& o) {
   Blk raw;
   load_blk(raw, rows, KD);
   split_blk(raw, o);

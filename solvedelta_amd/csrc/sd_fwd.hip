@@ -179,6 +179,8 @@ constexpr int XFS = SCOLS + 4;
 // one bf16 MFMA (B1 is exact in bf16).
 template <bool REV> struct StateT;
 template <> struct StateT<false> {
+  using Slot = xslot_t;
+  using Wout = fpan_t;
   using E = _Float16;
   using V8 = f16x8;
   using V4 = f16x4;
@@ -187,6 +189,8 @@ template <> struct StateT<false> {
   }
 };
 template <> struct StateT<true> {
+  using Slot = lslot_t;
+  using Wout = float;
   using E = __bf16;
   using V8 = bf16x8;
   using V4 = bf16x4;
@@ -309,13 +313,18 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
   *reinterpret_cast<float4*>(&s.Uf[threadIdx.x / (SCOLS / 4)][(threadIdx.x % (SCOLS / 4)) * 4]) = cur.U4;
   if (threadIdx.x < KD / 4) *reinterpret_cast<float4*>(&s.Gf[threadIdx.x * 4]) = cur.G4;
   __syncthreads();
-  if (p.Xs) {  // slot write-back: 128 rows x SCOLS columns as float4 pieces
+  if (p.Xs) {  // slot write-back: 128 rows x SCOLS columns, four elements per piece
+    using S = typename StateT<REV>::Slot;
+    typedef S S4 __attribute__((ext_vector_type(4)));
     constexpr int C4 = SCOLS / 4;
 #pragma unroll
     for (int j = 0; j < KD * C4 / STHREADS; ++j) {
       const int idx = threadIdx.x + j * STHREADS, row = idx / C4, c4 = idx % C4;
-      *reinterpret_cast<float4*>(p.Xs + sidx * KD * KD + (long long)row * KD + tile * SCOLS + c4 * 4) =
-          *reinterpret_cast<const float4*>(&s.Xf[row][c4 * 4]);
+      const float4 v = *reinterpret_cast<const float4*>(&s.Xf[row][c4 * 4]);
+      S4 o;
+      o[0] = (S)v.x; o[1] = (S)v.y; o[2] = (S)v.z; o[3] = (S)v.w;
+      *reinterpret_cast<S4*>(static_cast<S*>(p.Xs) + sidx * KD * KD + (long long)row * KD +
+                             tile * SCOLS + c4 * 4) = o;
     }
   }
   // w = U + Wneg X0 (token block tb, each half).  The work that does not depend
@@ -361,8 +370,17 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
     constexpr int C4 = SCOLS / 4;
     static_assert(BT * C4 == STHREADS, "one w piece per thread");
     const int tok = threadIdx.x / C4, c4 = threadIdx.x % C4;
-    *reinterpret_cast<float4*>(p.wout + (rowbase + tok) * KD + tile * SCOLS + c4 * 4) =
-        *reinterpret_cast<const float4*>(&s.wf[tok][c4 * 4]);
+    using WO = typename StateT<REV>::Wout;
+    WO* dst = static_cast<WO*>(p.wout) + (rowbase + tok) * KD + tile * SCOLS + c4 * 4;
+    const float4 v = *reinterpret_cast<const float4*>(&s.wf[tok][c4 * 4]);
+    if constexpr (sizeof(WO) == 4) {
+      *reinterpret_cast<float4*>(dst) = v;
+    } else {
+      typedef WO W4 __attribute__((ext_vector_type(4)));
+      W4 o;
+      o[0] = (WO)v.x; o[1] = (WO)v.y; o[2] = (WO)v.z; o[3] = (WO)v.w;
+      *reinterpret_cast<W4*>(dst) = o;
+    }
   }
   // X += Kt w: the recurrence's critical path
 #pragma unroll
@@ -444,7 +462,8 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
       for (int e = 0; e < 4; ++e) {
         const int row = (SRB * w + q) * 16 + r4 + e, col = tile * SCOLS + h * 16 + m;
         if (p.Xs && !p.rev)
-          p.Xs[((long long)n * NS + p.NT) * KD * KD + (long long)row * KD + col] = X[q][h][e];
+          static_cast<xslot_t*>(p.Xs)[((long long)n * NS + p.NT) * KD * KD + (long long)row * KD + col] =
+              (xslot_t)X[q][h][e];
         if (p.fin && row < p.rows && col < p.cols) {
           const long long base = (long long)n * p.rows * p.cols;
           if (p.fin_transposed)
@@ -516,7 +535,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   const ChunkDecay& cd = s.cd;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long cidx = (long long)n * p.NT + ch;
-  const float* delta = p.delta + rowbase * KD;
+  const fpan_t* delta = p.delta + rowbase * KD;
   {  // keys split once into a shared panel (every wave would otherwise split all of them)
     constexpr int PER = BT * KD / 4 / CT;
 #pragma unroll
@@ -556,7 +575,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   }
   __syncthreads();
   // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}  (this wave's column block)
-  const float* X0 = p.Xc + ((long long)n * (p.NT + 1) + ch) * KD * KD;
+  const xslot_t* X0 = p.Xc + ((long long)n * (p.NT + 1) + ch) * KD * KD;
   {
     const int cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
     BlkS BX;
@@ -588,7 +607,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
         const float dv = s.Pb[i][c] + __expf(cd.G[i][c]) * a1[I][e] + ap[e];
-        p.d[(rowbase + i) * KD + c] = dv;
+        p.d[(rowbase + i) * KD + c] = (fpan_t)dv;
         s.Pc[i][c] = dv;
       }
     }
@@ -606,7 +625,7 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g), t = t0 + i;
 #pragma unroll
-      for (int q = 0; q < RQ; ++q) dq_[g][q] = delta[i * KD + cl + 16 * q];
+      for (int q = 0; q < RQ; ++q) dq_[g][q] = (float)delta[i * KD + cl + 16 * q];
       load_row16(in.q, b, t, hh, T, r, qq_[g]);
       load_row16(in.erase_raw, b, t, hh, T, r, er_[g]);
     }
@@ -615,8 +634,8 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       load_row2(in.v, b, t0 + w + rr * CW, hh, T, V, vx[rr][0], vx[rr][1]);
       load_row2(in.write_raw, b, t0 + w + rr * CW, hh, T, V, wx[rr][0], wx[rr][1]);
     }
-    float* const e_b = p.e + rowbase * KD;
-    float* const chi_b = p.chi + rowbase * KD;
+    fpan_t* const e_b = p.e + rowbase * KD;
+    fpan_t* const chi_b = p.chi + rowbase * KD;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
@@ -656,8 +675,8 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
         const float xv = in ? qq_[g][q] - pv[q] * uq : 0.f;
         s.Pa[i][c] = ev;
         s.Pb[i][c] = xv;
-        e_b[i * KD + c] = ev;
-        chi_b[i * KD + c] = xv;
+        e_b[i * KD + c] = (fpan_t)ev;
+        chi_b[i * KD + c] = (fpan_t)xv;
       }
     }
 #pragma unroll
@@ -684,8 +703,8 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       ksv[q][e] = (_Float16)(s.Pc[i0 + e][c] * __expf(cd.G[BT - 1][c] - cd.G[i0 + e][c]));
   }
   stage_ytilde(s.Kp, cd, [&](int j, int c) { return s.Pc[j][c]; });
-  const float* const dg_ = p.d + rowbase * KD;
-  auto Draw = [&](int j, int c) { return dg_[j * KD + c]; };
+  const fpan_t* const dg_ = p.d + rowbase * KD;
+  auto Draw = [&](int j, int c) { return (float)dg_[j * KD + c]; };
   // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i
   decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pb[i][c]; }, s.Kp, Draw, false, s.M);
   store_frag_panel<BT, BT>(p.Ps.hi, p.Ps.lo, cidx * BT * BT,
@@ -746,8 +765,8 @@ size_t prep_s_smem() { return sizeof(PrepSSmem); }
 // ---------------------------------------------------------------------------
 struct OutParams {
   int H, T, NT, Tp, V;
-  const float* Xs;  // [n][NT+1][128][128] chunk-entering S
-  const float* w;   // [n][Tp][128] S-op w
+  const xslot_t* Xs;  // [n][NT+1][128][128] chunk-entering S
+  const fpan_t* w;  // [n][Tp][128] S-op w
   SP Q, P;          // fragment-ordered Q~ [64][128] and P [64][64] per chunk
   __bf16* out;      // [B,T,H,V]
 };
@@ -765,8 +784,8 @@ __global__ __launch_bounds__(CT) void k_out_s(OutParams p) {
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H;
   const int cb = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + ch * BT;
-  const float* X0 = p.Xs + ((long long)n * (p.NT + 1) + ch) * KD * KD;
-  const float* wv = p.w + rowbase * KD;
+  const xslot_t* X0 = p.Xs + ((long long)n * (p.NT + 1) + ch) * KD * KD;
+  const fpan_t* wv = p.w + rowbase * KD;
   constexpr int QP = BT * KD / 8 / CT, PP = BT * BT / 8 / CT;  // 16-byte pieces per thread
   bf16x8 vq[2][QP], vp[2][PP];  // loaded first, written to LDS after the X0 / w loads are issued
   {
@@ -789,11 +808,11 @@ __global__ __launch_bounds__(CT) void k_out_s(OutParams p) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xr[ks][e] = X0[(ks * 32 + kq + e) * KD + cb * 16 + m];
+    for (int e = 0; e < 8; ++e) xr[ks][e] = (float)X0[(ks * 32 + kq + e) * KD + cb * 16 + m];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) wr[ks][e] = wv[(ks * 32 + kq + e) * KD + cb * 16 + m];
+    for (int e = 0; e < 8; ++e) wr[ks][e] = (float)wv[(ks * 32 + kq + e) * KD + cb * 16 + m];
 #pragma unroll
   for (int q = 0; q < QP; ++q) {
     const int o = (threadIdx.x + q * CT) * 8;

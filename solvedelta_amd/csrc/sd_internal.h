@@ -40,19 +40,39 @@ __device__ __forceinline__ SPRaw sp_raw(const SP& sp, long long i) { return {sp.
 __device__ __forceinline__ float sp_val(SPRaw r) { return (float)r.h + (float)r.l; }
 #endif
 
+// Chunk-boundary state slots saved for the backward, in a 2-byte type (the
+// final states handed to the caller stay fp32): forward states X (C^T and S)
+// and the reverse passes' cotangent states lambda.  bf16, as the reference
+// keeps its per-chunk S states (residual_frame/common_left_h.py:157): its
+// exponent range holds any state or cotangent scale.
+#ifndef SD_XSLOT_T
+#define SD_XSLOT_T _Float16
+#endif
+#ifndef SD_LSLOT_T
+#define SD_LSLOT_T __bf16
+#endif
+typedef SD_XSLOT_T xslot_t;
+// Forward token panels the backward reads (e, chi, delta, d and the S op's w):
+// fp16, like the forward state panels.
+#ifndef SD_FPAN_T
+#define SD_FPAN_T _Float16
+#endif
+typedef SD_FPAN_T fpan_t;
+typedef SD_LSLOT_T lslot_t;
+
 // Forward workspace: every buffer is [n][Tp][128] (token panels) or
 // [n][NT][...] (per-chunk), n = B*H, Tp = NT*64.
 struct FwdWs {
   // kept for the backward
-  float* Xc;     // C-op chunk-entering states X = C^T     [n][NT+1][128][128] (slot NT = final)
-  float* Xs;     // S-op chunk-entering states              [n][NT+1][128][128]
+  xslot_t* Xc;   // C-op chunk-entering states X = C^T     [n][NT+1][128][128] (slot NT = final)
+  xslot_t* Xs;   // S-op chunk-entering states              [n][NT+1][128][128]
   float* Ac;     // C-op (I+L)^-1 per chunk                 [n][NT][64][64]
   float* As;     // S-op (I+L)^-1 per chunk                 [n][NT][64][64]
-  float* e;      // dual erase source e                     [n][Tp][128]
-  float* chi;    // dual query chi                          [n][Tp][128]
-  float* delta;  // predictor write delta (C-op w)          [n][Tp][128]
-  float* d;      // primal address d = k + C^T k            [n][Tp][128]
-  float* wS;     // S-op w = z - S~^T e                     [n][Tp][128]
+  fpan_t* e;      // dual erase source e                     [n][Tp][128]
+  fpan_t* chi;    // dual query chi                          [n][Tp][128]
+  fpan_t* delta;  // predictor write delta (C-op w)          [n][Tp][128]
+  fpan_t* d;      // primal address d = k + C^T k            [n][Tp][128]
+  fpan_t* wS;     // S-op w = z - S~^T e                     [n][Tp][128]
   // transient panels; the forward state passes' MFMA operands W (token-major)
   // and K (chunk-transposed) are fp16 in fragment order
   _Float16* Wc; float* Uc; _Float16* Kc; float* Gam;
@@ -62,7 +82,9 @@ struct FwdWs {
 struct FwdParams {
   sd_inputs in;
   int H, T, r, V, NT, Tp;
-  float *Xc, *delta, *d, *Ac, *As, *e, *chi;
+  xslot_t* Xc;
+  fpan_t *delta, *d, *e, *chi;
+  float *Ac, *As;
   _Float16* Wc; float* Uc; _Float16* Kc; float* Gam;
   _Float16* Ws; float* Us; _Float16* Ks; SP Qs; SP Ps;
 };
@@ -76,7 +98,8 @@ struct StateParams {
   int H, T, NT, Tp, rows, cols, rev;
   const void* Wneg; const float* U; const void* Kt; const float* Gam;
   const __bf16* At1; const __bf16* B1;  // reverse-pass injection
-  float* Xs; float* wout;
+  void* Xs;  // state slots: xslot_t (forward) or lslot_t (reverse)
+  void* wout;  // w panel: fpan_t (forward) or float (reverse)
   const float* init; int init_transposed;
   float* fin; int fin_transposed;
 };
@@ -117,8 +140,8 @@ size_t prep_s_smem();
 int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const FwdWs& w,
                hipStream_t st);
 struct BwdWs {
-  float* Lc;   // C-op chunk-end cotangents                [n][NT+1][128][128]
-  float* Ls;   // S-op chunk-end cotangents
+  lslot_t* Lc;  // C-op chunk-end cotangents                [n][NT+1][128][128]
+  lslot_t* Ls;  // S-op chunk-end cotangents
   // reverse-pass panels (reused by both ops), bf16 in fragment order
   float* dU; __bf16* Wk; __bf16* At1; float* B1; __bf16* B1t; __bf16* Ant;
   float* dwS; float* dwC;          // dw of each op           [n][Tp][128]

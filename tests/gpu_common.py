@@ -109,3 +109,36 @@ def c_forward_f64(ins, state):
                                            ptr(o))
     assert rc == 0
     return torch.from_numpy(o), torch.from_numpy(C), torch.from_numpy(S)
+
+
+def check_lm_against_oracle(model, ids, loss, tag, layers, heads, rk, rv):
+    """Loss and every parameter gradient of a SolveDelta causal LM (grads already
+    in p.grad) against the FP64 LM oracle on the same parameters.  Bounds: loss
+    rel 5e-3; every gradient rel-Frobenius 5e-2, except the decay rates'
+    d loss / d log_rate[h] = sum over (b, t, c) of dlog_decay * log_decay, whose
+    terms cancel to ~1e-3 of their magnitude: it is bounded against the sum of
+    the terms' magnitudes (what carries over is each term's bf16 rounding)."""
+    from oracle.lm_oracle import lm_oracle
+    params = {n: p.detach().double().cpu().requires_grad_() for n, p in model.named_parameters()}
+    taps = []
+    ref_loss, _ = lm_oracle(params, ids.cpu(), ids.cpu(), layers=layers, heads=heads, rk=rk,
+                            rv=rv, taps=taps)
+    for t in taps:
+        t.retain_grad()
+    ref_loss.backward()
+    e_loss = abs(loss.item() - ref_loss.item()) / abs(ref_loss.item())
+    errs = {n: rel(p.grad.float(), params[n].grad) for n, p in model.named_parameters()}
+    print(f"[{tag}] loss {loss.item():.6f} oracle {ref_loss.item():.6f} rel {e_loss:.1e}",
+          flush=True)
+    for n, e in sorted(errs.items(), key=lambda kv: -kv[1])[:6]:
+        print(f"  {n} {e:.2e}", flush=True)
+    assert e_loss < 5e-3
+    for n, e in errs.items():
+        if not n.endswith("associative_log_rate"):
+            assert e < 5e-2, (n, e)
+    for i, ld in enumerate(taps):
+        scale = (ld.grad * ld).abs().sum(dim=(0, 1, 3)).detach()
+        n = f"model.layers.{i}.mixer.mixer.associative_log_rate"
+        err = (model.get_parameter(n).grad.double().cpu() - params[n].grad).abs()
+        print(f"  {n}: |err| {err.tolist()} vs sum|terms| {scale.tolist()}", flush=True)
+        assert torch.all(err < 5e-3 * scale), n

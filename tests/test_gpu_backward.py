@@ -73,12 +73,15 @@ def test_backward_gamma_head_shape_and_no_state():
 def test_backward_extreme_decay_finite():
     """test_rebuild_semantics.py:699-747: log-decay = -100 keeps every gradient finite."""
     grads, rgrads = _grads(1, 80, 1, 16, 16, 13, decay="extreme", state_scale=1.0)
-    # The exact log-decay gradient is ~1e-40 here (every retention is e^-100), so
-    # it is bounded absolutely (fp32 cancellation noise), the rest relatively.
+    # The exact log-decay gradient is ~1e-40 here (every retention is e^-100): its
+    # closure sums O(1) terms (unit-scale states and cotangents) that cancel
+    # exactly, so the kernel's value is the rounding noise of those terms, which
+    # pass through the 2-byte chunk-state slots (fp16 states, bf16 cotangents).
+    # It is bounded absolutely at 1 % of the terms' unit scale, the rest relatively.
     dg, rdg = grads[5], rgrads[5]
     print(f"[bwd extreme] |dlog_decay| max {dg.abs().max().item():.2e} (oracle "
           f"{rdg.abs().max().item():.2e})", flush=True)
-    assert torch.isfinite(dg).all() and (dg.double().cpu() - rdg).abs().max() < 1e-3
+    assert torch.isfinite(dg).all() and (dg.double().cpu() - rdg).abs().max() < 1e-2
     keep = [i for i in range(len(NAMES)) if i != 5]
     _report("bwd extreme", [grads[i] for i in keep], [rgrads[i] for i in keep], 3e-2,
             [NAMES[i] for i in keep])

@@ -22,7 +22,8 @@ import math
 import pytest
 import torch
 
-from gpu_common import c_forward_f64, make_inputs, make_state, oracle_of, rel
+from gpu_common import (c_forward_f64, check_lm_against_oracle, make_inputs, make_state,
+                        oracle_of, rel)
 
 pytestmark = pytest.mark.gpu
 
@@ -168,40 +169,13 @@ def _lm(hidden, H, r, layers, vocab, seed=0):
 def test_config4_small_lm_matches_fp64_lm_oracle():
     """Same structure as config 4 (conv4, FP32 master weights, bf16 autocast,
     labels = inputs) at hidden 128, 2 layers, H2, r=V=64, vocab 97, B2 T128."""
-    from oracle.lm_oracle import lm_oracle
     model = _lm(128, 2, 64, 2, 97, seed=3)
     g = torch.Generator().manual_seed(4)
     ids = torch.randint(0, 97, (2, 128), generator=g).cuda()
     with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
         loss, _, _ = model(ids, labels=ids)
     loss.backward()
-    params = {n: p.detach().double().cpu().requires_grad_() for n, p in model.named_parameters()}
-    taps = []
-    ref_loss, _ = lm_oracle(params, ids.cpu(), ids.cpu(), layers=2, heads=2, rk=64, rv=64,
-                            taps=taps)
-    for t in taps:
-        t.retain_grad()
-    ref_loss.backward()
-    e_loss = abs(loss.item() - ref_loss.item()) / abs(ref_loss.item())
-    errs = {n: rel(p.grad.float(), params[n].grad) for n, p in model.named_parameters()}
-    print(f"[config4 small] loss {loss.item():.6f} oracle {ref_loss.item():.6f} rel {e_loss:.1e}",
-          flush=True)
-    for n, e in sorted(errs.items(), key=lambda kv: -kv[1])[:8]:
-        print(f"  {n} {e:.2e}", flush=True)
-    assert e_loss < 5e-3
-    for n, e in errs.items():
-        if n.endswith("associative_log_rate"):
-            continue
-        assert e < 5e-2, (n, e)
-    # d loss / d log_rate[h] = sum over (b, t, c) of dlog_decay * log_decay: its terms
-    # cancel to ~1e-3 of their magnitude, so it is bounded against the sum of the
-    # terms' magnitudes (what carries over is the bf16 rounding of each term)
-    for i, ld in enumerate(taps):
-        scale = (ld.grad * ld).abs().sum(dim=(0, 1, 3)).detach()
-        n = f"model.layers.{i}.mixer.mixer.associative_log_rate"
-        err = (model.get_parameter(n).grad.double().cpu() - params[n].grad).abs()
-        print(f"  {n}: |err| {err.tolist()} vs sum|terms| {scale.tolist()}", flush=True)
-        assert torch.all(err < 5e-3 * scale), n
+    check_lm_against_oracle(model, ids, loss, "config4 small", layers=2, heads=2, rk=64, rv=64)
 
 
 def test_config4_mixer_layer_at_full_width_matches_oracle():

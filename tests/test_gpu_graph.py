@@ -7,7 +7,7 @@ inside and outside capture."""
 import pytest
 import torch
 
-from gpu_common import rel
+from gpu_common import check_lm_against_oracle, rel
 
 pytestmark = pytest.mark.gpu
 
@@ -64,7 +64,6 @@ def test_graphed_step_replays_match_eager():
 def test_graphed_step_matches_fp64_lm_oracle():
     """The captured training step against the FP64 LM oracle (not only against
     eager): loss and every parameter gradient of a replay."""
-    from oracle.lm_oracle import lm_oracle
     from solvedelta_amd.graph import SolveDeltaGraphedTrainingStep
     model = _model(seed=4)
     with torch.no_grad():
@@ -78,14 +77,4 @@ def test_graphed_step_matches_fp64_lm_oracle():
         loss = step(ids, ids)
         loss.backward()
     torch.cuda.synchronize()
-    names = [n for n, _ in model.named_parameters()]
-    params = {n: p.detach().double().cpu().requires_grad_() for n, p in model.named_parameters()}
-    ref_loss, _ = lm_oracle(params, ids.cpu(), ids.cpu(), layers=2, heads=2, rk=64, rv=64)
-    rgrads = torch.autograd.grad(ref_loss, [params[n] for n in names])
-    e_loss = abs(loss.item() - ref_loss.item()) / abs(ref_loss.item())
-    errs = {n: rel(p.grad.float(), rg) for (n, p), rg in zip(model.named_parameters(), rgrads)}
-    worst = max(errs, key=errs.get)
-    print(f"[graph vs oracle] rel loss {e_loss:.1e}; worst grad {worst} {errs[worst]:.2e}", flush=True)
-    assert e_loss < 5e-3
-    for n, e in errs.items():
-        assert e < 5e-2, (n, e)
+    check_lm_against_oracle(model, ids, loss, "graph vs oracle", layers=2, heads=2, rk=64, rv=64)
