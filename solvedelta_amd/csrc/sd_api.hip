@@ -67,10 +67,12 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.At1 = c.take<__bf16>(panel);
   w.B1t = c.take<__bf16>(panel);
   w.Ant = c.take<__bf16>(panel);
-  float** panels[] = {&w.dU, &w.B1, &w.dwS, &w.dwC, &w.de, &w.dchi,
-                      &w.dd, &w.ddelta, &w.du_src, &w.dk_src, &w.dkC, &w.dxC, &w.dqC,
-                      &w.uh};
-  for (float** pp : panels) *pp = c.take<float>(panel);
+  w.dU = c.take<float>(panel);
+  bpan_t** bpanels[] = {&w.dwS, &w.dwC, &w.de, &w.dchi, &w.dd, &w.ddelta, &w.du_src,
+                        &w.dk_src, &w.dkC, &w.dxC, &w.dqC};
+  for (bpan_t** pp : bpanels) *pp = c.take<bpan_t>(panel);
+  w.uh = c.take<fpan_t>(panel);
+  w.kh = c.take<fpan_t>(panel);
   w.Pp = c.take<float>(n * NT * kBT * kBT);
   if (total) *total = c.off + 256;
   return w;

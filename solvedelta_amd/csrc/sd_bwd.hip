@@ -376,7 +376,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
-  const float* dw = p.g.dwS + rowbase * KD;
+  const bpan_t* dw = p.g.dwS + rowbase * KD;
   const fpan_t* wv = p.f.wS + rowbase * KD;
   const fpan_t* dd_ = p.f.d + rowbase * KD;
   const fpan_t* ee = p.f.e + rowbase * KD;
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
   // M1_ij = dw_i . w_j (j < i)
-  lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
+  lds_pair(&s.PA, (const float*)nullptr, s.PW, s.M1, true);
   // a = dw X0^T for this wave's column block (K = 128)
   f4 a[NB], bq[NB], kl[NB];
   BlkS BX;
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   stage_dout_panel(s.PA, p, b, t0, hh);
   __syncthreads();
   // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T;  kl = w lam^T
-  lds_pair(&s.PA, nullptr, s.PW, s.M2, false);
+  lds_pair(&s.PA, (const float*)nullptr, s.PW, s.M2, false);
   {
     BlkS BL;
     load_lam_rowsum(lam, XC, cb, BL, s.rsum);
@@ -446,9 +446,9 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   // the decay terms chi.dchi + e.de of dg
   // Chunk-uniform output bases with 32-bit lane offsets: 64-bit per-row
   // addresses would not fit in registers beside the slabs.
-  float* const de_b = p.g.de + rowbase * KD;
-  float* const dchi_b = p.g.dchi + rowbase * KD;
-  float* const dd_b = p.g.dd + rowbase * KD;
+  bpan_t* const de_b = p.g.de + rowbase * KD;
+  bpan_t* const dchi_b = p.g.dchi + rowbase * KD;
+  bpan_t* const dd_b = p.g.dd + rowbase * KD;
   {
     __syncthreads();  // M1, M2 complete
 #pragma unroll
@@ -516,9 +516,14 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
 __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   const int n = blockIdx.y, b = n / p.H, hh = n % p.H;
   const int t = blockIdx.x * 4 + wave_id();
-  if (t >= p.T) return;
+  if (t >= p.Tp) return;
   const int l = lane_id(), r = p.r, V = p.V;
   const long long row = ((long long)n * p.Tp + t) * KD;
+  if (t >= p.T) {  // padded token: its ddelta row is read by the C chunk's backward prep
+    p.g.ddelta[row + l] = 0.f;
+    p.g.ddelta[row + l + 64] = 0.f;
+    return;
+  }
   float u0, u1, k0, k1, q0, q1, e0, e1, w0, w1, v0, v1;
   ldrow2(p.in.u, b, t, hh, p.T, r, u0, u1);
   norm2(u0, u1);
@@ -650,10 +655,10 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     s.A[(idx / BT) * LS + idx % BT] = p.f.Ac[cidx * BT * BT + idx];
   __syncthreads();
-  const float* ddp = p.g.dd + rowbase * KD;
+  const bpan_t* ddp = p.g.dd + rowbase * KD;
   // P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic}, i <= l
   decayed_gram<false>(
-      cd, [&](int i, int c) { return ddp[i * KD + c]; }, [&](int j, int c) { return s.Uh[j][c]; },
+      cd, [&](int i, int c) { return (float)ddp[i * KD + c]; }, [&](int j, int c) { return s.Uh[j][c]; },
       false, s.P);
   mat64_mul(s.P, s.A, s.N);
   __syncthreads();
@@ -665,7 +670,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     *reinterpret_cast<float4*>(p.g.Pp + cidx * BT * BT + idx) =
         (j / BS > i / BS) ? make_float4(0.f, 0.f, 0.f, 0.f) : v;
   }
-  const float* ddl = p.g.ddelta + rowbase * KD;
+  const bpan_t* ddl = p.g.ddelta + rowbase * KD;
   const long long kbase = cidx * KD * BT;
   f4 wks[NB], dus[NB];
   {
@@ -724,15 +729,15 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   }
   for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
     const int i = idx / KD, c = idx % KD;
-    p.g.B1[(rowbase + i) * KD + c] = s.Kh[i][c];
-    p.g.uh[(rowbase + i) * KD + c] = s.Uh[i][c];
+    p.g.kh[(rowbase + i) * KD + c] = (fpan_t)s.Kh[i][c];
+    p.g.uh[(rowbase + i) * KD + c] = (fpan_t)s.Uh[i][c];
   }
   // chunk-transposed panels, fragment order
   // The reverse pass's injection sum_i At1_ci Kh_i,col is formed as
   // sum_i (At1_ci / |k_i|) k_i,col: its B operand is then the raw key input,
   // exact in bf16, so only a high half is stored (and read).
   store_frag_panel1<KD, BT>(p.g.At1, cidx * KD * BT, [&](int c, int i) {
-    return ddp[i * KD + c] * __expf(cd.G[i][c]) * s.krs[i];
+    return (float)ddp[i * KD + c] * __expf(cd.G[i][c]) * s.krs[i];
   });
   {
     constexpr int PIECES = KD * BT / 8, PER = PIECES / CT;
@@ -780,11 +785,11 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   const long long rowbase = (long long)n * p.Tp + t0;
   const long long sidx = (long long)n * (p.NT + 1) + ch;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
-  const float* dw = p.g.dwC + rowbase * KD;
+  const bpan_t* dw = p.g.dwC + rowbase * KD;
   const fpan_t* wv = p.f.delta + rowbase * KD;
-  const float* ddp = p.g.dd + rowbase * KD;   // cotangent of the C-op output
-  const float* kh = p.g.B1 + rowbase * KD;    // normalised keys
-  const float* uh = p.g.uh + rowbase * KD;    // normalised u
+  const bpan_t* ddp = p.g.dd + rowbase * KD;  // cotangent of the C-op output
+  const fpan_t* kh = p.g.kh + rowbase * KD;  // normalised keys
+  const fpan_t* uh = p.g.uh + rowbase * KD;  // normalised u
   const fpan_t* dprim = p.f.d + rowbase * KD;  // d = k + output
   const xslot_t* X0 = p.f.Xc + sidx * KD * KD;
   const xslot_t* XC = X0 + KD * KD;
@@ -809,7 +814,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   load_blk(bLam, lam + cb * 16 * KD, KD);
   load_blk(bXC, XC + cb * 16 * KD, KD);
   // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
-  lds_pair(&s.PA, nullptr, s.PW, s.M1, true);
+  lds_pair(&s.PA, (const float*)nullptr, s.PW, s.M1, true);
   lds_pair(nullptr, kh, s.PW, s.M2, false);
   f4 a[NB], kl[NB];
   {
@@ -847,9 +852,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   __syncthreads();  // M1, M2 complete; PA free
   // PA <- dd e^G for the dq product (staged now, consumed after the applies)
   stage_panel(s.PA, ddp, [&](int i, int cc) { return __expf(cd.G[i][cc]); });
-  auto U = [&](int j, int cc) { return uh[j * KD + cc]; };
-  auto Xg = [&](int j, int cc) { return s.gam[j] * uh[j * KD + cc]; };
-  auto DO = [&](int j, int cc) { return ddp[j * KD + cc]; };
+  auto U = [&](int j, int cc) { return (float)uh[j * KD + cc]; };
+  auto Xg = [&](int j, int cc) { return s.gam[j] * (float)uh[j * KD + cc]; };
+  auto DO = [&](int j, int cc) { return (float)ddp[j * KD + cc]; };
   float Sx[NB][4];
 #pragma unroll
   for (int J = 0; J < NB; ++J)
@@ -865,8 +870,8 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     for (int q = 0; q < PPC; ++q) ppv[q] = *reinterpret_cast<const float4*>(pp + (threadIdx.x + q * CT) * 4);
   }
   // chunk-uniform output bases, 32-bit lane offsets (keeps addresses out of VGPR pairs)
-  float* const dx_b = p.g.dxC + rowbase * KD;
-  float* const dk_b = p.g.dkC + rowbase * KD;
+  bpan_t* const dx_b = p.g.dxC + rowbase * KD;
+  bpan_t* const dk_b = p.g.dkC + rowbase * KD;
   // decay cotangent: dg_i = o_i dd_i - u_i dk_i plus the shifted gamma u (.) dx
   // term, closed in registers below (v = dg + xdx, then dg = suffix(v) - xdx)
   float vv[NB][4], xs[NB][4];
@@ -913,7 +918,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   __syncthreads();  // P' in M1; PA (dd e^G) staged
   // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
   {
-    float* const dq_b = p.g.dqC + rowbase * KD;
+    bpan_t* const dq_b = p.g.dqC + rowbase * KD;
     BlkS BX;
     {
       const int kq = (l >> 4) * 8;

@@ -893,7 +893,8 @@ __device__ __forceinline__ void load_split_blk_g(const E* rows, BlkS& o) {
 
 // Pair matrix M = A Y^T over K = 128 (strict: j < i, else j <= i), Y from an LDS
 // panel and A from an LDS panel (Ag == nullptr) or a global fp32 panel.
-__device__ void lds_pair(const LPanel* A, const float* Ag, const LPanel& Y, float* M, bool strict) {
+template <class EG>
+__device__ void lds_pair(const LPanel* A, const EG* Ag, const LPanel& Y, float* M, bool strict) {
   const int w = wave_id();
   for (int pp = w; pp < 10; pp += CW) {
     int I = 0, J = pp;

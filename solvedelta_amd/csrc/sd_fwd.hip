@@ -190,7 +190,7 @@ template <> struct StateT<false> {
 };
 template <> struct StateT<true> {
   using Slot = lslot_t;
-  using Wout = float;
+  using Wout = bpan_t;
   using E = __bf16;
   using V8 = bf16x8;
   using V4 = bf16x4;

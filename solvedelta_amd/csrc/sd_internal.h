@@ -58,6 +58,12 @@ typedef SD_XSLOT_T xslot_t;
 #define SD_FPAN_T _Float16
 #endif
 typedef SD_FPAN_T fpan_t;
+// Backward token panels (partial gradients passed between the backward kernels):
+// bf16, whose exponent range holds any scale of the output cotangent.
+#ifndef SD_BPAN_T
+#define SD_BPAN_T __bf16
+#endif
+typedef SD_BPAN_T bpan_t;
 typedef SD_LSLOT_T lslot_t;
 
 // Forward workspace: every buffer is [n][Tp][128] (token panels) or
@@ -99,7 +105,7 @@ struct StateParams {
   const void* Wneg; const float* U; const void* Kt; const float* Gam;
   const __bf16* At1; const __bf16* B1;  // reverse-pass injection
   void* Xs;  // state slots: xslot_t (forward) or lslot_t (reverse)
-  void* wout;  // w panel: fpan_t (forward) or float (reverse)
+  void* wout;  // w panel: fpan_t (forward) or bpan_t (reverse)
   const float* init; int init_transposed;
   float* fin; int fin_transposed;
 };
@@ -143,12 +149,13 @@ struct BwdWs {
   lslot_t* Lc;  // C-op chunk-end cotangents                [n][NT+1][128][128]
   lslot_t* Ls;  // S-op chunk-end cotangents
   // reverse-pass panels (reused by both ops), bf16 in fragment order
-  float* dU; __bf16* Wk; __bf16* At1; float* B1; __bf16* B1t; __bf16* Ant;
-  float* dwS; float* dwC;          // dw of each op           [n][Tp][128]
-  float* de; float* dchi; float* dd;
-  float* ddelta; float* du_src; float* dk_src;
-  float* dkC; float* dxC; float* dqC;
-  float* uh;  // normalised u
+  float* dU; __bf16* Wk; __bf16* At1; __bf16* B1t; __bf16* Ant;
+  bpan_t* dwS; bpan_t* dwC;         // dw of each op           [n][Tp][128]
+  bpan_t* de; bpan_t* dchi; bpan_t* dd;
+  bpan_t* ddelta; bpan_t* du_src; bpan_t* dk_src;
+  bpan_t* dkC; bpan_t* dxC; bpan_t* dqC;
+  fpan_t* uh;  // normalised u
+  fpan_t* kh;  // normalised keys
   float* Pp;  // P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) of the C op  [n][NT][64][64]
 };
 
