@@ -384,6 +384,8 @@ def main():
     ap.add_argument("--no-lm", action="store_true")
     ap.add_argument("--lm-graph", action="store_true",
                     help="also time the causal LM step through its HIP graph")
+    ap.add_argument("--step-only", action="store_true",
+                    help="only the headline forward+VJP steps (counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -468,6 +470,9 @@ def main():
         "roofline": roof,
         "step_roofline": step,
     }
+    if a.step_only:
+        print(json.dumps(res), flush=True)
+        return
     res["forward"] = forward_bench(ins, st, a.steps, a.warmup)
     res["reference_shape"] = refshape_bench(dev, a.steps, a.warmup)
     if not a.no_decode:

@@ -399,7 +399,10 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
         X[q][h] = T::mma(cur.K[q][ks], wh[ks], X[q][h]);
       }
   }
-  __syncthreads();
+  // No closing barrier: the next step writes Xh / Xl / Xf / Uf / Gf, whose last
+  // readers all ran before this step's second barrier, and writes wh / wl / wf
+  // only after its own first barrier, which no wave passes before every wave
+  // has finished this step's reads of them.
 }
 
 template <bool REV>
