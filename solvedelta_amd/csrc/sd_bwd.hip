@@ -176,7 +176,9 @@ static_assert(2 * BT * LS >= BT * KD, "P + N hold a 64 x 128 panel");
 __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   BprepSSmem& s = *reinterpret_cast<BprepSSmem*>(smem_raw);
-  const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  // chunk-major dispatch, first chunk first: the last chunk, where the reverse
+  // state pass starts right after this kernel, is written last
+  const int n = blockIdx.x, ch = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
@@ -618,7 +620,9 @@ struct BprepCSmem {
 __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   BprepCSmem& s = *reinterpret_cast<BprepCSmem*>(smem_raw);
-  const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  // chunk-major dispatch, first chunk first: the last chunk, where the reverse
+  // state pass starts right after this kernel, is written last
+  const int n = blockIdx.x, ch = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
@@ -1028,7 +1032,8 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   SD_SMEM_ONCE(k_grad_c, (int)sizeof(GradCSmem));
   const dim3 chunks(NT, n), rows((Tp + 3) / 4, n), blk(NTHREADS), cblk(CT);
   // S memory
-  SD_LAUNCH("k_bprep_s", k_bprep_s, chunks, cblk, sizeof(BprepSSmem), st, p);
+  const dim3 chunks_cm(n, NT);  // chunk-major grid of the backward preps
+  SD_LAUNCH("k_bprep_s", k_bprep_s, chunks_cm, cblk, sizeof(BprepSSmem), st, p);
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
   ss.rev = 1;
@@ -1041,7 +1046,7 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   SD_LAUNCH("k_grad_s", k_grad_s, chunks, cblk, sizeof(GradSmem), st, p);
   SD_LAUNCH("k_src_bwd", k_src_bwd, rows, blk, 0, st, p);
   // C predictor
-  SD_LAUNCH("k_bprep_c", k_bprep_c, chunks, cblk, sizeof(BprepCSmem), st, p);
+  SD_LAUNCH("k_bprep_c", k_bprep_c, chunks_cm, cblk, sizeof(BprepCSmem), st, p);
   StateParams sc{};
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
   sc.rev = 1;

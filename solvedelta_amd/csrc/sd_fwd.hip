@@ -63,7 +63,9 @@ struct PrepCSmem {
 __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepCSmem& s = *reinterpret_cast<PrepCSmem*>(smem_raw);
-  const int ch = blockIdx.x, n = blockIdx.y;
+  // chunk-major dispatch, last chunk first (chunk 0, where the C state pass
+  // starts, is written last)
+  const int n = blockIdx.x, ch = gridDim.y - 1 - blockIdx.y;
   const int b = n / p.H, hh = n % p.H, t0 = ch * BT;
   const int T = p.T, r = p.r;
   const sd_inputs& in = p.in;
@@ -504,7 +506,9 @@ struct PrepSSmem {
 __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepSSmem& s = *reinterpret_cast<PrepSSmem*>(smem_raw);
-  const int ch = blockIdx.x, n = blockIdx.y;
+  // chunk-major dispatch, last chunk first: chunk 0 is written last, so the S
+  // state pass that starts on it right after this kernel finds it in cache
+  const int n = blockIdx.x, ch = gridDim.y - 1 - blockIdx.y;
   const int b = n / p.H, hh = n % p.H, t0 = ch * BT;
   const int T = p.T, r = p.r, V = p.V;
   const sd_inputs& in = p.in;
@@ -896,7 +900,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
 
   SD_SMEM_ONCE(k_prep_c, (int)prep_c_smem());
   SD_SMEM_ONCE(k_prep_s, (int)prep_s_smem());
-  SD_LAUNCH("k_prep_c", k_prep_c, dim3(NT, n), dim3(CT), prep_c_smem(), st, fp);
+  SD_LAUNCH("k_prep_c", k_prep_c, dim3(n, NT), dim3(CT), prep_c_smem(), st, fp);
 
   StateParams sc{};
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
@@ -906,7 +910,7 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   sc.fin = C_T; sc.fin_transposed = 1;
   launch_state("state_c_fwd", sc, n, st);
 
-  SD_LAUNCH("k_prep_s", k_prep_s, dim3(NT, n), dim3(CT), prep_s_smem(), st, fp);
+  SD_LAUNCH("k_prep_s", k_prep_s, dim3(n, NT), dim3(CT), prep_s_smem(), st, fp);
 
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
