@@ -54,28 +54,32 @@ FLOPS_PER_CHUNK = {
 }
 
 
-# Algorithmic bytes per (sequence, 64-token chunk) of each kernel: every global
-# tensor region the kernel's interface reads or writes, counted once.  Units:
-# a bf16 input/output panel [64 x 128] 16 KiB; an FP32 panel, or an FP32 panel
-# stored as bf16 hi + lo halves, 32 KiB; an FP32 chunk-boundary state
-# [128 x 128] 64 KiB; a 64 x 64 FP32 block 16 KiB.  Reads + writes:
-_IN, _P, _S, _A = 16384, 32768, 65536, 16384
+# Interface bytes per (sequence, 64-token chunk) of each kernel as built: every
+# global tensor region it reads or writes, counted once (operator tensors and
+# the workspace panels between kernels).  Units: a 2-byte token panel
+# [64 x 128] (bf16 input / fp16 or bf16 workspace panel) 16 KiB; an FP32 token
+# panel 32 KiB; a 2-byte chunk-state slot [128 x 128] 32 KiB; a 64 x 64 FP32
+# block 16 KiB.  Reads + writes:
+_H, _P, _S, _A = 16384, 32768, 32768, 16384
 BYTES_PER_CHUNK = {
-    "k_prep_c": (2 * _IN + _P) + (_A + 3 * _P),             # u,h,decay -> A,W,U,K
-    "state_c_fwd": 3 * _P + (_S + _P),                      # W,U,K -> state slot, delta
-    "k_prep_s": (6 * _IN + 2 * _P + _S) + (2 * _A + 7 * _P),  # inputs,decay,delta,C0 -> A,P,U,K,Q,W,chi,d,e
-    "state_s_fwd": 3 * _P + (_S + _P),                      # W,U,K -> state slot, w
-    "k_out_s": (_S + 2 * _P + _A) + _IN,                    # X0,w,Q,P -> out
-    "k_bprep_s": (2 * _A + 5 * _P) + 5 * _P,                # A,P,e,k,decay,K,Q -> dU,Wk,At1,B1t,Ant
-    "state_s_bwd": 4 * _P + _IN + (_S + _P),                # Wk,dU,Ant,At1, B1t (bf16) -> lambda slot, dw
-    "state_c_bwd": 4 * _P + _IN + (_S + _P),
-    "k_grad_s": (6 * _P + _IN + 3 * _S) + 4 * _P,           # dw,w,d,e,chi,decay,dO,X0,XC,lambda -> dchi,dd,de,dg
-    "k_src_bwd": (6 * _IN + 5 * _P) + (3 * _P + 4 * _IN),   # inputs,delta,d*,dw -> du,dk,ddelta,dq,dv,der,dwr
-    "k_bprep_c": (_A + 2 * _IN + 4 * _P) + (7 * _P + _A),   # A,u,k,decay,K,dd,ddelta -> k,dU,u,Ant,At1,B1t,Wk,P'
-
-    "k_grad_c": (8 * _P + 3 * _S + _A) + 4 * _P,            # dw,delta,dd,k,u,d,decay,dg(S),X0,XC,lambda,P' -> dx,dk,dq,dg
-    "k_final": (3 * _IN + 6 * _P) + 3 * _IN,                # u,h,k, 6 partial grads -> du,dh,dk
+    "k_prep_c": (2 * _H + _P) + (_A + 2 * _H + _P),           # u,h,decay -> A,W,K (fp16),U
+    "state_c_fwd": (2 * _H + _P) + (_S + _H),                # W,K,U -> slot, delta
+    "k_prep_s": (7 * _H + _P + _S) + (3 * _H + _H + _A + 2 * _H + _A + _P + _H),
+    # u,q,k,v,erase,write,delta,decay,C slot -> d,e,chi,K,P(split),Q(split),A,U,W
+    "state_s_fwd": (2 * _H + _P) + (_S + _H),                # W,K,U -> slot, w
+    "k_out_s": (_S + _H + 2 * _H + _A) + _H,                 # slot,w,Q,P -> out
+    "k_bprep_s": (_A + _A + 3 * _H + _P + 2 * _H) + (_P + 4 * _H),
+    # A,P,dO,K,e,decay,Q -> dU,Wk,Ant,At1,B1
+    "state_s_bwd": (4 * _H + _P) + (_S + _H),                # Wk,Ant,At1,B1,dU -> slot, dw
+    "state_c_bwd": (4 * _H + _P) + (_S + _H),
+    "k_grad_s": (6 * _H + _P + 3 * _S) + (3 * _H + _P),      # dw,w,d,e,chi,dO,decay,X0,XC,lam -> de,dchi,dd,dg
+    "k_src_bwd": (11 * _H) + (7 * _H),                       # 6 inputs,delta,de,dchi,dw,dd -> 4 grads,ddelta,du,dk
+    "k_bprep_c": (_A + 5 * _H + _P) + (_P + 6 * _H + _A),    # A,u,k,K,dd,ddelta,decay -> dU,Wk,kh,uh,At1,B1,Ant,P'
+    "k_grad_c": (6 * _H + _P + 3 * _S + _A + _P) + (3 * _H + _P),
+    # dw,delta,dd,kh,uh,d,decay,X0,XC,lam,P',dg -> dx,dk,dq,dg
+    "k_final": (9 * _H) + 3 * _H,                            # u,h,k,dx,dw,du,dk,dkC,dq -> du,dh,dk
 }
+
 
 # Algorithmic bytes per token-head of each kernel in the sense of the
 # operator's own tensors (SURVEY-style accounting: the inputs it reads, the
