@@ -15,7 +15,8 @@
  *   fp32 addressed as gamma[b*sb + t*st + h*sh] (strides 0 broadcast [H] / [1,H]);
  *   initial / final states: C [B,H,r,r] (prediction = C u) and S [B,H,r,V], fp32,
  *   contiguous.  Erase/write gates are raw logits; the sigmoid is applied inside.
- *   Widths: 1 <= r, V <= 128.  Any T >= 1 (tails are neutrally padded inside).
+ *   Widths: 1 <= r, V <= 128 (the Python operator runs V > 128 as groups of
+ *   <= 128 value columns).  Any T >= 1 (tails are neutrally padded inside).
  *
  * All entry points enqueue work on `stream` and never allocate or synchronise:
  * scratch comes from the caller's workspace, whose size the *_workspace_bytes
