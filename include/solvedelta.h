@@ -15,8 +15,14 @@
  *   fp32 addressed as gamma[b*sb + t*st + h*sh] (strides 0 broadcast [H] / [1,H]);
  *   initial / final states: C [B,H,r,r] (prediction = C u) and S [B,H,r,V], fp32,
  *   contiguous.  Erase/write gates are raw logits; the sigmoid is applied inside.
- *   Widths: 1 <= r, V <= 128 (the Python operator runs V > 128 as groups of
- *   <= 128 value columns).  Any T >= 1 (tails are neutrally padded inside).
+ *   Widths: 1 <= r, V <= 256, as the reference's state pass
+ *   (residual_frame/common_left_h.py:139-140).  r, V <= 128 run on the main
+ *   kernels (64-token chunks); a call with either width above 128 runs on the
+ *   wide-width kernels (32-token chunks, FP32 panels) with their own workspace
+ *   layout, which the *_workspace_bytes queries size from (r, V).  The Python
+ *   operator cuts wider value axes into groups.  sd_decode takes r, V <= 128
+ *   (wider T = 1 calls take the chunked path, as in the reference).
+ *   Any T >= 1 (tails are neutrally padded inside).
  *
  * All entry points enqueue work on `stream` and never allocate or synchronise:
  * scratch comes from the caller's workspace, whose size the *_workspace_bytes

@@ -83,7 +83,7 @@ bool view_ok(const sd_view& v) { return v.data != nullptr; }
 int check_inputs(const sd_inputs* in) {
   if (!in) return SD_ERR_ARG;
   if (in->B < 1 || in->T < 1 || in->H < 1 || in->r < 1 || in->V < 1) return SD_ERR_SHAPE;
-  if (in->r > kKD || in->V > kKD) return SD_ERR_SHAPE;
+  if (in->r > kWideMax || in->V > kWideMax) return SD_ERR_SHAPE;
   if (!view_ok(in->u) || !view_ok(in->h) || !view_ok(in->q) || !view_ok(in->k) ||
       !view_ok(in->v) || !view_ok(in->erase_raw) || !view_ok(in->write_raw) ||
       !view_ok(in->log_decay) || !view_ok(in->gamma))
@@ -123,7 +123,7 @@ extern "C" {
 const char* sd_version(void) { return "solvedelta_amd 0.1 (gfx950)"; }
 
 size_t sd_fwd_workspace_bytes(int B, int T, int H, int r, int V) {
-  (void)r; (void)V;
+  if (is_wide(r, V)) return wide_fwd_workspace_bytes(B, T, H, r, V);
   size_t total = 0;
   carve_fwd(nullptr, B, T, H, &total);
   return total;
@@ -135,6 +135,11 @@ int sd_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* workspa
   if (rc) return rc;
   if (!out || !workspace) return SD_ERR_ARG;
   size_t need = 0;
+  if (is_wide(in->r, in->V)) {
+    if (workspace_bytes < wide_fwd_workspace_bytes(in->B, in->T, in->H, in->r, in->V))
+      return SD_ERR_WORKSPACE;
+    return launch_wide_fwd(in, out, C_T, S_T, workspace, (hipStream_t)stream);
+  }
   FwdWs w = carve_fwd(workspace, in->B, in->T, in->H, &need);
   if (workspace_bytes < need) return SD_ERR_WORKSPACE;
   return launch_fwd(in, out, C_T, S_T, w, (hipStream_t)stream);
@@ -146,26 +151,30 @@ int sd_fwd_noalloc(const sd_inputs* in, void* out, float* C_T, float* S_T, void*
   int rc = check_inputs(in);
   if (rc) return rc;
   if (!out) return SD_ERR_ARG;
+  const bool wide = is_wide(in->r, in->V);
   size_t need = 0;
-  carve_fwd(nullptr, in->B, in->T, in->H, &need);
+  if (wide) need = wide_fwd_workspace_bytes(in->B, in->T, in->H, in->r, in->V);
+  else carve_fwd(nullptr, in->B, in->T, in->H, &need);
   if (need > SD_NOALLOC_SCRATCH_BYTES) return SD_ERR_WORKSPACE;
   void* base = nullptr;
   rc = scratch_for_current_device(&base);
   if (rc) return rc;
+  if (wide) return launch_wide_fwd(in, out, C_T, S_T, base, (hipStream_t)stream);
   FwdWs w = carve_fwd(base, in->B, in->T, in->H, nullptr);
   return launch_fwd(in, out, C_T, S_T, w, (hipStream_t)stream);
 }
 
 int sd_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, void* stream) {
+  // the decode kernel holds r, V <= 128 (wider states take the chunked path)
+  if (in && (in->T != 1 || in->r > kKD || in->V > kKD)) return SD_ERR_SHAPE;
   int rc = check_inputs(in);
   if (rc) return rc;
-  if (in->T != 1) return SD_ERR_SHAPE;
   if (!out) return SD_ERR_ARG;
   return launch_decode(in, out, C_T, S_T, (hipStream_t)stream);
 }
 
 size_t sd_bwd_workspace_bytes(int B, int T, int H, int r, int V) {
-  (void)r; (void)V;
+  if (is_wide(r, V)) return wide_bwd_workspace_bytes(B, T, H, r, V);
   size_t total = 0;
   carve_bwd(nullptr, B, T, H, &total);
   return total;
@@ -181,6 +190,12 @@ int sd_bwd(const sd_inputs* in, const void* fwd_workspace, const void* dout, con
       !dlog_decay || !dgamma)
     return SD_ERR_ARG;
   size_t need = 0;
+  if (is_wide(in->r, in->V)) {
+    if (workspace_bytes < wide_bwd_workspace_bytes(in->B, in->T, in->H, in->r, in->V))
+      return SD_ERR_WORKSPACE;
+    return launch_wide_bwd(in, fwd_workspace, workspace, dout, dC_T, dS_T, du, dh, dq, dk, dv,
+                           derase, dwrite, dlog_decay, dgamma, dC0, dS0, (hipStream_t)stream);
+  }
   BwdWs bw = carve_bwd(workspace, in->B, in->T, in->H, &need);
   if (workspace_bytes < need) return SD_ERR_WORKSPACE;
   FwdWs fw = carve_fwd((void*)fwd_workspace, in->B, in->T, in->H, nullptr);

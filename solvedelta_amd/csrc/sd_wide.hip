@@ -1,0 +1,1239 @@
+// Wide-width path of the SolveDelta recurrence: key widths 128 < r <= 256 and
+// value widths up to 256 (gfx950).
+//
+// The reference runs its state pass for head widths up to 256
+// (causallsso/ops/residual_frame/common_left_h.py:139-151).  The main kernels
+// hold a 64-token chunk's 128-wide panels in LDS; at 256 they would not fit, so
+// this path states the same chunked algebra (the generic pre-decay-read delta
+// op restated in tests/chunk_model.py) with 32-token chunks, runtime padded
+// widths KP, VP (multiples of 32, <= 256) and FP32 panels throughout:
+//
+//   k_w_tokens  (chunk-parallel)  in-chunk log-decay prefix G, L2 norms, gamma;
+//   per op (predictor C: X = C^T, erase read before the token's decay, row
+//   output; memory S: erase read after it, column output):
+//     k_w_prep    decayed Gram L, (I+L)^-1, WY panels W, U, decayed keys,
+//                 readout pair P (column output);
+//     k_w_state   sequential chunk pass over one 16-column state tile;
+//     k_w_out     chunk readout (row output also forms d = k^ + C^T k^);
+//   k_w_sources (per token)  dual sources e, chi and gated values z;
+// and backward, per op in reverse order:
+//     k_w_bprep   dU = A^T (dW + pair^T dO), W' = -A^T K^, K' = -x~, injection;
+//     k_w_state   reverse cotangent pass (lambda, dw);
+//     k_w_grad    closed-form chunk gradients dk, dx, dq and the decay closure;
+//   k_w_src_bwd, k_w_final (per token)  source and norm closures.
+//
+// Every decay factor is exp(a - b) with a <= b prefix sums inside one chunk (no
+// reciprocal decays), formed per element; padding tokens and coordinates are
+// zero and stay neutral.
+#include "sd_common.cuh"
+#include "sd_internal.h"
+
+namespace sd {
+namespace wide {
+
+constexpr int WBT = 32;    // chunk length
+constexpr int WMAX = 256;  // widest padded width
+constexpr int WT = 256;    // threads per workgroup
+constexpr int MS = WBT + 1;  // row stride of 32 x 32 LDS matrices
+constexpr int TILE = 16;   // state-pass column tile
+
+__device__ __forceinline__ const __bf16* wrow(const sd_view& v, int b, int t, int h) {
+  return (const __bf16*)v.data + (long long)b * v.sb + (long long)t * v.st + (long long)h * v.sh;
+}
+__device__ __forceinline__ float wgamma(const sd_view& g, int b, int t, int h) {
+  return ((const float*)g.data)[(long long)b * g.sb + (long long)t * g.st + (long long)h * g.sh];
+}
+
+// ---------------------------------------------------------------------------
+// Token preparation: G prefix, norms, gamma-scaled predictor operands.
+// ---------------------------------------------------------------------------
+struct TokParams {
+  sd_inputs in;
+  int NT, Tp, KP;
+  float *G, *uh, *kh, *qh, *xC, *vC, *gam, *rs;
+};
+
+__global__ __launch_bounds__(WT) void k_w_tokens(TokParams p) {
+  const int ch = blockIdx.x, s = blockIdx.y;
+  const int H = p.in.H, T = p.in.T, r = p.in.r, KP = p.KP;
+  const int b = s / H, h = s % H, t0 = ch * WBT;
+  const long long pb = (long long)s * p.Tp;
+  // in-chunk inclusive log-decay prefix, one coordinate per thread
+  const int c = threadIdx.x;
+  if (c < KP) {
+    const float* g = (const float*)p.in.log_decay.data + (long long)b * p.in.log_decay.sb +
+                     (long long)h * p.in.log_decay.sh + c;
+    float acc = 0.f;
+    for (int i = 0; i < WBT; ++i) {
+      const int t = t0 + i;
+      if (t < T && c < r) acc += g[(long long)t * p.in.log_decay.st];
+      p.G[(pb + t0 + i) * KP + c] = acc;
+    }
+  }
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  for (int i = w; i < WBT; i += WT / 64) {
+    const int t = t0 + i;
+    const bool tv = t < T;
+    const float gm = tv ? wgamma(p.in.gamma, b, t, h) : 0.f;
+    float uu[4], kk[4], qq[4], hv[4];
+    float su = 0.f, sk = 0.f, sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int cc = l + 64 * j;
+      const bool ok = tv && cc < r;
+      uu[j] = ok ? bf2f(wrow(p.in.u, b, t, h)[cc]) : 0.f;
+      kk[j] = ok ? bf2f(wrow(p.in.k, b, t, h)[cc]) : 0.f;
+      qq[j] = ok ? bf2f(wrow(p.in.q, b, t, h)[cc]) : 0.f;
+      hv[j] = ok ? bf2f(wrow(p.in.h, b, t, h)[cc]) : 0.f;
+      su += uu[j] * uu[j];
+      sk += kk[j] * kk[j];
+      sq += qq[j] * qq[j];
+    }
+    const float ru = rsqrtf(wave_sum(su) + 1e-24f);
+    const float rk = rsqrtf(wave_sum(sk) + 1e-24f);
+    const float rq = rsqrtf(wave_sum(sq) + 1e-24f);
+    const long long row = (pb + t) * KP;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int cc = l + 64 * j;
+      if (cc < KP) {
+        p.uh[row + cc] = uu[j] * ru;
+        p.kh[row + cc] = kk[j] * rk;
+        p.qh[row + cc] = qq[j] * rq;
+        p.xC[row + cc] = gm * uu[j] * ru;
+        p.vC[row + cc] = gm * hv[j];
+      }
+    }
+    if (l == 0) {
+      p.gam[pb + t] = gm;
+      p.rs[(pb + t) * 3 + 0] = ru;
+      p.rs[(pb + t) * 3 + 1] = rk;
+      p.rs[(pb + t) * 3 + 2] = rq;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One op (state X [kw x vw]) of the chunked recurrence.
+// ---------------------------------------------------------------------------
+struct OpParams {
+  int NT, Tp, kw, vw, excl, colout;
+  const float *k, *x, *v, *q, *G;  // k, x, G [Tp][kw]; v [Tp][vw]; q [Tp][kw] (col) / [Tp][vw] (row)
+  float *A, *P;                    // [NT][32][32]
+  float *W, *U, *Kh, *Qt, *Gam;    // W, Kh, Qt [Tp][kw]; U [Tp][vw]; Gam [NT][kw]
+};
+
+// G of the erase read for token i at coordinate c: the prefix before token i
+// (predictor) or through it (memory).
+__device__ __forceinline__ float gx_at(const float* Gs, int ld, int i, int c, int excl) {
+  if (!excl) return Gs[i * ld + c];
+  return i > 0 ? Gs[(i - 1) * ld + c] : 0.f;
+}
+
+// Entry e = threadIdx.x + 256 m of a 32 x 32 matrix: (i, j) = (e / 32, e % 32).
+__device__ __forceinline__ void entry(int m, int& i, int& j) {
+  const int e = threadIdx.x + WT * m;
+  i = e >> 5;
+  j = e & 31;
+}
+
+__global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
+  extern __shared__ __align__(16) float sm[];
+  const int ch = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw, ld = kw + 1;
+  float* xs = sm;                 // x  [32][kw+1]
+  float* ks = xs + WBT * ld;      // k
+  float* Gs = ks + WBT * ld;      // G
+  float* qs = Gs + WBT * ld;      // q (column output)
+  float* Ls = qs + WBT * ld;      // L, then A  [32][33]
+  float* Ps = Ls + WBT * MS;      // P
+  const long long tb = (long long)s * p.Tp + ch * WBT;
+  for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
+    const int i = idx / kw, c = idx % kw;
+    const long long o = (tb + i) * kw + c;
+    xs[i * ld + c] = p.x[o];
+    ks[i * ld + c] = p.k[o];
+    Gs[i * ld + c] = p.G[o];
+    if (p.colout) qs[i * ld + c] = p.q[o];
+  }
+  __syncthreads();
+  // L_ij = sum_c x_ic k_jc e^{Gx_ic - G_jc} (j < i); P_ij = sum_c q_ic k_jc e^{G_ic - G_jc} (j <= i)
+  for (int m = 0; m < WBT * WBT / WT; ++m) {
+    int i, j;
+    entry(m, i, j);
+    float l = 0.f, pp = 0.f;
+    if (j < i) {
+      for (int c = 0; c < kw; ++c)
+        l += xs[i * ld + c] * ks[j * ld + c] * __expf(gx_at(Gs, ld, i, c, p.excl) - Gs[j * ld + c]);
+    }
+    if (p.colout && j <= i) {
+      for (int c = 0; c < kw; ++c)
+        pp += qs[i * ld + c] * ks[j * ld + c] * __expf(Gs[i * ld + c] - Gs[j * ld + c]);
+    }
+    Ls[i * MS + j] = l;
+    Ps[i * MS + j] = pp;
+  }
+  __syncthreads();
+  // A = (I + L)^-1, one column per thread: a_i = [i == j] - sum_{m < i} L_im a_m
+  float acol[WBT];
+  if (threadIdx.x < WBT) {
+    const int j = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) {
+      float a = (i == j) ? 1.f : 0.f;
+#pragma unroll
+      for (int m = 0; m < i; ++m) a -= Ls[i * MS + m] * acol[m];
+      acol[i] = (i < j) ? 0.f : a;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < WBT) {
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) Ls[i * MS + threadIdx.x] = acol[i];
+  }
+  __syncthreads();
+  const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
+  for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) {
+    p.A[mb + idx] = Ls[(idx >> 5) * MS + (idx & 31)];
+    if (p.colout) p.P[mb + idx] = Ps[(idx >> 5) * MS + (idx & 31)];
+  }
+  // W = A x~, Kh, Qt, Gam: one key coordinate per thread
+  const int c = threadIdx.x;
+  if (c < kw) {
+    float xt[WBT];
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) xt[i] = xs[i * ld + c] * __expf(gx_at(Gs, ld, i, c, p.excl));
+    const float gl = Gs[(WBT - 1) * ld + c];
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int m = 0; m <= i; ++m) a += Ls[i * MS + m] * xt[m];
+      const long long o = (tb + i) * kw + c;
+      p.W[o] = a;
+      p.Kh[o] = ks[i * ld + c] * __expf(gl - Gs[i * ld + c]);
+      if (p.colout) p.Qt[o] = qs[i * ld + c] * __expf(Gs[i * ld + c]);
+    }
+    p.Gam[((long long)s * p.NT + ch) * kw + c] = __expf(gl);
+  }
+  // U = A v: one value column per thread
+  if (c < vw) {
+    float vv[WBT];
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) vv[i] = p.v[(tb + i) * vw + c];
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int m = 0; m <= i; ++m) a += Ls[i * MS + m] * vv[m];
+      p.U[(tb + i) * vw + c] = a;
+    }
+  }
+}
+
+constexpr size_t prep_smem(int kw) { return (size_t)(4 * WBT * (kw + 1) + 2 * WBT * MS) * sizeof(float); }
+
+// ---------------------------------------------------------------------------
+// Sequential chunk pass over a 16-column tile of X [kw x vw]:
+//   slot[ch] = X;  w = U - W X;  X = Gamma X + K^T w (+ Ia^T Ib)
+// forward (chunks ascending; slot NT = final state) or reverse (descending).
+// ---------------------------------------------------------------------------
+struct WStateParams {
+  int NT, Tp, kw, vw, rows, cols, rev;
+  const float *W, *U, *K, *Gam, *Ia, *Ib;
+  float *slots, *wout;
+  const float* init; int init_t;
+  float* fin; int fin_t;
+};
+
+__global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
+  __shared__ __align__(16) float Xl[WMAX][TILE + 1];
+  __shared__ __align__(16) float Wl[WBT][WMAX + 1];
+  __shared__ float wl[WBT][TILE + 1];
+  __shared__ float Il[WBT][TILE + 1];
+  const int tile = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw, c0 = tile * TILE;
+  const int r = threadIdx.x;
+  float X[TILE];
+#pragma unroll
+  for (int j = 0; j < TILE; ++j) {
+    const int c = c0 + j;
+    float v = 0.f;
+    if (p.init && r < p.rows && c < p.cols)
+      v = p.init_t ? p.init[((long long)s * p.cols + c) * p.rows + r]
+                   : p.init[((long long)s * p.rows + r) * p.cols + c];
+    X[j] = v;
+  }
+  const long long sb = (long long)s * (p.NT + 1) * kw * vw;
+  for (int step = 0; step < p.NT; ++step) {
+    const int ch = p.rev ? p.NT - 1 - step : step;
+    const long long tb = (long long)s * p.Tp + ch * WBT;
+    if (r < kw) {
+#pragma unroll
+      for (int j = 0; j < TILE; ++j) {
+        Xl[r][j] = X[j];
+        p.slots[sb + ((long long)ch * kw + r) * vw + c0 + j] = X[j];
+      }
+    }
+    for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
+      const int i = idx / kw, c = idx % kw;
+      Wl[i][c] = p.W[(tb + i) * kw + c];
+    }
+    if (p.Ib) {
+      for (int idx = threadIdx.x; idx < WBT * TILE; idx += WT) {
+        const int i = idx / TILE, j = idx % TILE;
+        Il[i][j] = p.Ib[(tb + i) * vw + c0 + j];
+      }
+    }
+    __syncthreads();
+    {
+      const int i = threadIdx.x >> 4, j = threadIdx.x & 15;
+      float a0 = p.U[(tb + i) * vw + c0 + j], a1 = p.U[(tb + i + 16) * vw + c0 + j];
+      for (int rr = 0; rr < kw; ++rr) {
+        const float xv = Xl[rr][j];
+        a0 -= Wl[i][rr] * xv;
+        a1 -= Wl[i + 16][rr] * xv;
+      }
+      wl[i][j] = a0;
+      wl[i + 16][j] = a1;
+      p.wout[(tb + i) * vw + c0 + j] = a0;
+      p.wout[(tb + i + 16) * vw + c0 + j] = a1;
+    }
+    __syncthreads();
+    if (r < kw) {
+      const float g = p.Gam[((long long)s * p.NT + ch) * kw + r];
+#pragma unroll
+      for (int j = 0; j < TILE; ++j) X[j] *= g;
+      for (int i = 0; i < WBT; ++i) {
+        const float kv = p.K[(tb + i) * kw + r];
+#pragma unroll
+        for (int j = 0; j < TILE; ++j) X[j] += kv * wl[i][j];
+      }
+      if (p.Ia) {
+        for (int i = 0; i < WBT; ++i) {
+          const float av = p.Ia[(tb + i) * kw + r];
+#pragma unroll
+          for (int j = 0; j < TILE; ++j) X[j] += av * Il[i][j];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (r < kw) {
+    if (!p.rev) {
+#pragma unroll
+      for (int j = 0; j < TILE; ++j)
+        p.slots[sb + ((long long)p.NT * kw + r) * vw + c0 + j] = X[j];
+    }
+    if (p.fin && r < p.rows) {
+#pragma unroll
+      for (int j = 0; j < TILE; ++j) {
+        const int c = c0 + j;
+        if (c < p.cols) {
+          if (p.fin_t) p.fin[((long long)s * p.cols + c) * p.rows + r] = X[j];
+          else p.fin[((long long)s * p.rows + r) * p.cols + c] = X[j];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Chunk readout.
+//   column output: o = Qt X0 + P w                       -> bf16 out [B,T,H,V]
+//   row output:    o_ir = e^{G_ir} (q X0^T)_ir + sum_{j<=i} (q_i.w_j) k_jr e^{G_ir - G_jr}
+//                  -> o panel and d = base + o
+// ---------------------------------------------------------------------------
+struct OutParams {
+  int NT, Tp, kw, vw, colout, H, T, V;
+  const float *slots, *w, *Qt, *P, *q, *k, *G, *base;
+  float *o, *d;
+  __bf16* out;
+};
+
+__global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
+  extern __shared__ __align__(16) float sm[];
+  const int ch = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw;
+  const long long tb = (long long)s * p.Tp + ch * WBT;
+  const float* X0 = p.slots + ((long long)s * (p.NT + 1) + ch) * kw * vw;
+  if (p.colout) {
+    const int ld = kw + 1;
+    float* Ql = sm;                 // [32][kw+1]
+    float* Pl = Ql + WBT * ld;      // [32][33]
+    for (int idx = threadIdx.x; idx < WBT * kw; idx += WT)
+      Ql[(idx / kw) * ld + idx % kw] = p.Qt[(tb + idx / kw) * kw + idx % kw];
+    const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
+    for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) Pl[(idx >> 5) * MS + (idx & 31)] = p.P[mb + idx];
+    __syncthreads();
+    const int c = threadIdx.x;
+    if (c >= vw) return;
+    float acc[WBT];
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
+    for (int rr = 0; rr < kw; ++rr) {
+      const float xv = X0[(long long)rr * vw + c];
+#pragma unroll
+      for (int i = 0; i < WBT; ++i) acc[i] += Ql[i * ld + rr] * xv;
+    }
+    float wc[WBT];
+#pragma unroll
+    for (int j = 0; j < WBT; ++j) wc[j] = p.w[(tb + j) * vw + c];
+    const int b = s / p.H, h = s % p.H;
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) {
+      float a = acc[i];
+#pragma unroll
+      for (int j = 0; j <= i; ++j) a += Pl[i * MS + j] * wc[j];
+      const int t = ch * WBT + i;
+      if (t < p.T && c < p.V) p.out[(((long long)b * p.T + t) * p.H + h) * p.V + c] = f2bf(a);
+    }
+    return;
+  }
+  // row output
+  const int lv = vw + 1;
+  float* ql = sm;               // q [32][vw+1]
+  float* wls = ql + WBT * lv;   // w [32][vw+1]
+  float* Ml = wls + WBT * lv;   // M [32][33]
+  float* Xb = Ml + WBT * MS;    // X0 column block [256][33]
+  for (int idx = threadIdx.x; idx < WBT * vw; idx += WT) {
+    const int i = idx / vw, c = idx % vw;
+    ql[i * lv + c] = p.q[(tb + i) * vw + c];
+    wls[i * lv + c] = p.w[(tb + i) * vw + c];
+  }
+  __syncthreads();
+  for (int m = 0; m < WBT * WBT / WT; ++m) {
+    int i, j;
+    entry(m, i, j);
+    float a = 0.f;
+    if (j <= i)
+      for (int c = 0; c < vw; ++c) a += ql[i * lv + c] * wls[j * lv + c];
+    Ml[i * MS + j] = a;
+  }
+  const int r = threadIdx.x;
+  float acc[WBT];
+#pragma unroll
+  for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
+  for (int cb = 0; cb < vw; cb += 32) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < kw * 32; idx += WT) {
+      const int rr = idx >> 5, cc = idx & 31;
+      Xb[rr * MS + cc] = X0[(long long)rr * vw + cb + cc];
+    }
+    __syncthreads();
+    if (r < kw) {
+      for (int cc = 0; cc < 32; ++cc) {
+        const float xv = Xb[r * MS + cc];
+#pragma unroll
+        for (int i = 0; i < WBT; ++i) acc[i] += ql[i * lv + cb + cc] * xv;
+      }
+    }
+  }
+  __syncthreads();
+  if (r >= kw) return;
+  float kr[WBT], Gr[WBT];
+#pragma unroll
+  for (int i = 0; i < WBT; ++i) {
+    kr[i] = p.k[(tb + i) * kw + r];
+    Gr[i] = p.G[(tb + i) * kw + r];
+  }
+#pragma unroll
+  for (int i = 0; i < WBT; ++i) {
+    float a = __expf(Gr[i]) * acc[i];
+#pragma unroll
+    for (int j = 0; j <= i; ++j) a += Ml[i * MS + j] * kr[j] * __expf(Gr[i] - Gr[j]);
+    const long long o = (tb + i) * kw + r;
+    p.o[o] = a;
+    p.d[o] = p.base[o] + a;
+  }
+}
+
+constexpr size_t out_smem(int kw, int vw, int colout) {
+  if (colout) return (size_t)(WBT * (kw + 1) + WBT * MS) * sizeof(float);
+  return (size_t)(2 * WBT * (vw + 1) + WBT * MS + WMAX * MS) * sizeof(float);
+}
+
+// ---------------------------------------------------------------------------
+// Dual sources (per token): phi, den, e, chi, z.
+// ---------------------------------------------------------------------------
+struct SrcParams {
+  sd_inputs in;
+  int Tp, KP, VP;
+  const float *uh, *delta, *kh, *qh;
+  float *e, *chi, *z;
+};
+
+__global__ __launch_bounds__(WT) void k_w_sources(SrcParams p) {
+  const int s = blockIdx.y, H = p.in.H, T = p.in.T, r = p.in.r, V = p.in.V;
+  const int b = s / H, h = s % H;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int t = blockIdx.x * (WT / 64) + w;
+  if (t >= p.Tp) return;
+  const bool tv = t < T;
+  const long long row = ((long long)s * p.Tp + t) * p.KP, vrow_ = ((long long)s * p.Tp + t) * p.VP;
+  float u[4], dl[4], k[4], q[4], er[4];
+  float usq = 0.f, dsq = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j;
+    const bool in = c < p.KP;
+    u[j] = in ? p.uh[row + c] : 0.f;
+    dl[j] = in ? p.delta[row + c] : 0.f;
+    k[j] = in ? p.kh[row + c] : 0.f;
+    q[j] = in ? p.qh[row + c] : 0.f;
+    er[j] = (tv && c < r) ? bf2f(wrow(p.in.erase_raw, b, t, h)[c]) : 0.f;
+    usq += u[j] * u[j];
+    dsq += dl[j] * dl[j];
+  }
+  usq = wave_sum(usq);
+  dsq = wave_sum(dsq);
+  const float sc = RHO / sqrtf(RHO * RHO + usq * dsq);
+  float phi[4], bb[4];
+  float pu = 0.f, ub = 0.f, uq = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    phi[j] = sc * dl[j];
+    bb[j] = k[j] / (1.f + __expf(-er[j]));
+    pu += phi[j] * u[j];
+    ub += u[j] * bb[j];
+    uq += u[j] * q[j];
+  }
+  const float den = 1.f + wave_sum(pu);
+  const float sb = wave_sum(ub) / den, sq = wave_sum(uq) / den;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j;
+    if (c < p.KP) {
+      p.e[row + c] = bb[j] - phi[j] * sb;
+      p.chi[row + c] = q[j] - phi[j] * sq;
+    }
+    if (c < p.VP) {
+      const bool ok = tv && c < V;
+      const float vv = ok ? bf2f(wrow(p.in.v, b, t, h)[c]) : 0.f;
+      const float wr = ok ? bf2f(wrow(p.in.write_raw, b, t, h)[c]) : 0.f;
+      p.z[vrow_ + c] = vv / (1.f + __expf(-wr));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward preparation of one op's reverse pass.
+//   column output: rhs = dW + P^T dO, injection Ia = q e^G, Ib = dO
+//   row output:    Pp_ij = sum_r dO_ir k_jr e^{G_ir - G_jr} (j <= i), rhs = dW + Pp^T q,
+//                  Ia = dO e^G, Ib = q
+//   dU = A^T rhs,  Wn = -A^T Kh,  Kn = -x~
+// ---------------------------------------------------------------------------
+struct BprepParams {
+  int NT, Tp, kw, vw, excl, colout;
+  const float *k, *x, *q, *G, *A, *P, *dO, *dW;
+  float *dU, *Wn, *Kn, *Ia, *Pp;
+};
+
+__global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
+  extern __shared__ __align__(16) float sm[];
+  const int ch = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw, ld = kw + 1;
+  const long long tb = (long long)s * p.Tp + ch * WBT;
+  const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
+  float* Al = sm;              // A [32][33]
+  float* Pl = Al + WBT * MS;   // P or Pp [32][33]
+  float* dOl = Pl + WBT * MS;  // row output: dO, k, G [32][kw+1]
+  float* kl = dOl + WBT * ld;
+  float* Gl = kl + WBT * ld;
+  // per-thread column vectors [32][256] (element i of thread t at i*256+t),
+  // over the row-output panels once the Pp Gram is done with them
+  float* cv = dOl;
+  float* cw = cv + WBT * WT;
+  const int tid = threadIdx.x;
+  for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) {
+    Al[(idx >> 5) * MS + (idx & 31)] = p.A[mb + idx];
+    if (p.colout) Pl[(idx >> 5) * MS + (idx & 31)] = p.P[mb + idx];
+  }
+  if (!p.colout) {
+    for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
+      const int i = idx / kw, c = idx % kw;
+      const long long o = (tb + i) * kw + c;
+      dOl[i * ld + c] = p.dO[o];
+      kl[i * ld + c] = p.k[o];
+      Gl[i * ld + c] = p.G[o];
+    }
+    __syncthreads();
+    for (int m = 0; m < WBT * WBT / WT; ++m) {
+      int i, j;
+      entry(m, i, j);
+      float a = 0.f;
+      if (j <= i)
+        for (int c = 0; c < kw; ++c)
+          a += dOl[i * ld + c] * kl[j * ld + c] * __expf(Gl[i * ld + c] - Gl[j * ld + c]);
+      Pl[i * MS + j] = a;
+      p.Pp[mb + i * WBT + j] = a;
+    }
+  }
+  __syncthreads();
+  // value side: rhs and dU, one value column per thread
+  const int c = threadIdx.x;
+  if (c < vw) {
+    for (int i = 0; i < WBT; ++i)
+      cv[i * WT + tid] = p.colout ? p.dO[(tb + i) * vw + c] : p.q[(tb + i) * vw + c];
+    for (int j = 0; j < WBT; ++j) {
+      float a = p.dW ? p.dW[(tb + j) * vw + c] : 0.f;
+      for (int i = j; i < WBT; ++i) a += Pl[i * MS + j] * cv[i * WT + tid];
+      cw[j * WT + tid] = a;
+    }
+    for (int m = 0; m < WBT; ++m) {
+      float a = 0.f;
+      for (int i = m; i < WBT; ++i) a += Al[i * MS + m] * cw[i * WT + tid];
+      p.dU[(tb + m) * vw + c] = a;
+    }
+  }
+  // key side: Wn, Kn, Ia, one key coordinate per thread
+  if (c < kw) {
+    const float gl = p.G[(tb + WBT - 1) * kw + c];
+    for (int i = 0; i < WBT; ++i) {
+      const long long o = (tb + i) * kw + c;
+      const float gi = p.G[o];
+      cv[i * WT + tid] = p.k[o] * __expf(gl - gi);
+      const float gx = p.excl ? (i > 0 ? p.G[o - kw] : 0.f) : gi;
+      p.Kn[o] = -p.x[o] * __expf(gx);
+      const float src = p.colout ? p.q[o] : p.dO[o];
+      p.Ia[o] = src * __expf(gi);
+    }
+    for (int m = 0; m < WBT; ++m) {
+      float a = 0.f;
+      for (int i = m; i < WBT; ++i) a += Al[i * MS + m] * cv[i * WT + tid];
+      p.Wn[(tb + m) * kw + c] = -a;
+    }
+  }
+}
+
+constexpr size_t bprep_smem(int kw) {
+  const size_t panels = 3 * WBT * (size_t)(kw + 1), cols = 2 * WBT * WT;
+  return (2 * WBT * MS + (panels > cols ? panels : cols)) * sizeof(float);
+}
+
+// ---------------------------------------------------------------------------
+// Closed-form chunk gradients of one op (tests/chunk_model.py Op.backward):
+//   M1_ij = dw_i.w_j (j < i);  M2_lj = Y_l.w_j (j <= l), Y = dO (column) / q (row)
+//   dx = -(e^{Gx} (dw X0^T) + apply(M1, k, Gx, G))
+//   dk = e^{G_C - G} (w lam^T) + apply_t(M2, Yk, G, G) - apply_t(M1, x, Gx, G)
+//        with Yk = q (column) / dO (row)
+//   dq = e^{G} (dO X0^T) + apply(M2, k, G, G)          (column)
+//   dq = (dO e^G) X0 + Pp w                             (row)
+//   dG = q dq - k dk (column) / o dO - k dk (row), + x dx (shifted one token
+//   earlier when the erase reads before the decay), last row + rowsum(X_C lam);
+//   dg = in-chunk reverse cumulative sum of dG.
+// ---------------------------------------------------------------------------
+struct GradParams {
+  int NT, Tp, kw, vw, excl, colout;
+  const float *k, *x, *q, *G, *dO, *o, *w, *dw, *Xslots, *Lslots, *Pp;
+  float *dk, *dx, *dq, *dg;
+};
+
+__global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
+  extern __shared__ __align__(16) float sm[];
+  const int ch = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw;
+  const long long tb = (long long)s * p.Tp + ch * WBT;
+  const long long slot = (long long)s * (p.NT + 1) + ch;
+  const float* X0 = p.Xslots + slot * kw * vw;
+  const float* XC = X0 + (long long)kw * vw;
+  const float* Lm = p.Lslots + slot * kw * vw;
+  // phase 1: column blocks of 32 value columns
+  float* dwb = sm;               // [32][33] each
+  float* wb = dwb + WBT * MS;
+  float* yb = wb + WBT * MS;
+  float* M1 = yb + WBT * MS;
+  float* M2 = M1 + WBT * MS;
+  float* X0b = M2 + WBT * MS;    // [256][33] each
+  float* Lb = X0b + WMAX * MS;
+  float* XCb = Lb + WMAX * MS;
+  const int r = threadIdx.x;
+  float dwX[WBT], wL[WBT], dOX[WBT];
+#pragma unroll
+  for (int i = 0; i < WBT; ++i) dwX[i] = wL[i] = dOX[i] = 0.f;
+  float rsum = 0.f;
+  float m1[4] = {0.f, 0.f, 0.f, 0.f}, m2[4] = {0.f, 0.f, 0.f, 0.f};
+  const float* Y = p.colout ? p.dO : p.q;  // [Tp][vw]
+  for (int cb = 0; cb < vw; cb += 32) {
+    for (int idx = threadIdx.x; idx < WBT * 32; idx += WT) {
+      const int i = idx >> 5, cc = idx & 31;
+      const long long o = (tb + i) * vw + cb + cc;
+      dwb[i * MS + cc] = p.dw[o];
+      wb[i * MS + cc] = p.w[o];
+      yb[i * MS + cc] = Y[o];
+    }
+    for (int idx = threadIdx.x; idx < kw * 32; idx += WT) {
+      const int rr = idx >> 5, cc = idx & 31;
+      const long long o = (long long)rr * vw + cb + cc;
+      X0b[rr * MS + cc] = X0[o];
+      Lb[rr * MS + cc] = Lm[o];
+      XCb[rr * MS + cc] = XC[o];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      int i, j;
+      entry(m, i, j);
+      float a1 = 0.f, a2 = 0.f;
+#pragma unroll 4
+      for (int cc = 0; cc < 32; ++cc) {
+        const float wj = wb[j * MS + cc];
+        a1 += dwb[i * MS + cc] * wj;
+        a2 += yb[i * MS + cc] * wj;
+      }
+      m1[m] += a1;
+      m2[m] += a2;
+    }
+    if (r < kw) {
+#pragma unroll 1
+      for (int cc = 0; cc < 32; ++cc) {
+        const float xv = X0b[r * MS + cc], lv = Lb[r * MS + cc];
+        rsum += XCb[r * MS + cc] * lv;
+#pragma unroll
+        for (int i = 0; i < WBT; ++i) {
+          dwX[i] += dwb[i * MS + cc] * xv;
+          wL[i] += wb[i * MS + cc] * lv;
+          dOX[i] += yb[i * MS + cc] * xv;  // dO X0^T (column output only)
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // the phase-1 row products go to this thread's own output columns, which
+  // phase 3 reads back and overwrites (no register arrays live across phases)
+  if (r < kw) {
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) {
+      const long long o = (tb + i) * kw + r;
+      p.dx[o] = dwX[i];
+      p.dk[o] = wL[i];
+      if (p.colout) p.dq[o] = dOX[i];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    int i, j;
+    entry(m, i, j);
+    M1[i * MS + j] = j < i ? m1[m] : 0.f;
+    M2[i * MS + j] = j <= i ? m2[m] : 0.f;
+  }
+  // phase 2 (row output): dq = (dO e^G) X0 + Pp w, one value column per thread
+  float* dOe = X0b;  // [32][kw+1]
+  float* Ppl = dOe + WBT * (kw + 1);
+  if (!p.colout) {
+    const int ld = kw + 1;
+    for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
+      const int i = idx / kw, c = idx % kw;
+      const long long o = (tb + i) * kw + c;
+      dOe[i * ld + c] = p.dO[o] * __expf(p.G[o]);
+    }
+    const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
+    for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) Ppl[(idx >> 5) * MS + (idx & 31)] = p.Pp[mb + idx];
+    __syncthreads();
+    const int c = threadIdx.x;
+    if (c < vw) {
+      float acc[WBT];
+#pragma unroll
+      for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
+      for (int rr = 0; rr < kw; ++rr) {
+        const float xv = X0[(long long)rr * vw + c];
+#pragma unroll
+        for (int i = 0; i < WBT; ++i) acc[i] += dOe[i * ld + rr] * xv;
+      }
+      float wc[WBT];
+#pragma unroll
+      for (int j = 0; j < WBT; ++j) wc[j] = p.w[(tb + j) * vw + c];
+#pragma unroll
+      for (int i = 0; i < WBT; ++i) {
+        float a = acc[i];
+#pragma unroll
+        for (int j = 0; j <= i; ++j) a += Ppl[i * MS + j] * wc[j];
+        p.dq[(tb + i) * vw + c] = a;
+      }
+    }
+  }
+  __syncthreads();
+  // phase 3: key-side gradients, one key coordinate per thread, its chunk
+  // columns staged in LDS [32][kw]
+  float* kL = X0b;
+  float* xL = kL + WBT * kw;
+  float* GL = xL + WBT * kw;
+  float* YL = GL + WBT * kw;
+  const float* Yk = p.colout ? p.q : p.dO;  // [Tp][kw]
+  for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
+    const int i = idx / kw, c = idx % kw;
+    const long long o = (tb + i) * kw + c;
+    kL[idx] = p.k[o];
+    xL[idx] = p.x[o];
+    GL[idx] = p.G[o];
+    YL[idx] = Yk[o];
+  }
+  __syncthreads();
+  if (r >= kw) return;
+  auto Gx = [&](int i) { return p.excl ? (i > 0 ? GL[(i - 1) * kw + r] : 0.f) : GL[i * kw + r]; };
+  const float gl = GL[(WBT - 1) * kw + r];
+  // dx = -(e^{Gx} (dw X0^T) + apply(M1, k, Gx, G))
+  for (int i = 0; i < WBT; ++i) {
+    const long long o = (tb + i) * kw + r;
+    const float gxi = Gx(i);
+    float a = __expf(gxi) * p.dx[o];
+    for (int j = 0; j < i; ++j) a += M1[i * MS + j] * kL[j * kw + r] * __expf(gxi - GL[j * kw + r]);
+    p.dx[o] = -a;
+  }
+  // dk = e^{G_C - G} (w lam^T) + apply_t(M2, Yk, G, G) - apply_t(M1, x, Gx, G)
+  for (int j = 0; j < WBT; ++j) {
+    const long long o = (tb + j) * kw + r;
+    const float gj = GL[j * kw + r];
+    float a = __expf(gl - gj) * p.dk[o];
+    for (int l = j; l < WBT; ++l) a += M2[l * MS + j] * YL[l * kw + r] * __expf(GL[l * kw + r] - gj);
+    for (int i = j + 1; i < WBT; ++i) a -= M1[i * MS + j] * xL[i * kw + r] * __expf(Gx(i) - gj);
+    p.dk[o] = a;
+  }
+  if (p.colout) {
+    // dq = e^G (dO X0^T) + apply(M2, k, G, G)
+    for (int i = 0; i < WBT; ++i) {
+      const long long o = (tb + i) * kw + r;
+      const float gi = GL[i * kw + r];
+      float a = __expf(gi) * p.dq[o];
+      for (int j = 0; j <= i; ++j) a += M2[i * MS + j] * kL[j * kw + r] * __expf(gi - GL[j * kw + r]);
+      p.dq[o] = a;
+    }
+  }
+  // decay closure: dG = q dq - k dk (column) / o dO - k dk (row) + x dx (one
+  // token earlier when the erase reads before the decay); the last row adds
+  // rowsum(X_C lam); dg is its in-chunk reverse cumulative sum.  dx, dk, dq are
+  // read back from this thread's own stores above.
+  float run = rsum;
+  for (int i = WBT - 1; i >= 0; --i) {
+    const long long o = (tb + i) * kw + r;
+    float dG = -kL[i * kw + r] * p.dk[o];
+    dG += p.colout ? YL[i * kw + r] * p.dq[o] : p.o[o] * p.dO[o];
+    const int ix = p.excl ? i + 1 : i;
+    if (ix < WBT) dG += xL[ix * kw + r] * p.dx[(tb + ix) * kw + r];
+    run += dG;
+    p.dg[o] = run;
+  }
+}
+
+constexpr size_t grad_smem(int kw) {
+  const size_t ph1 = 5 * WBT * MS + 3 * WMAX * MS;
+  const size_t ph3 = 5 * WBT * MS + 4 * WBT * (size_t)kw;
+  const size_t ph2 = 5 * WBT * MS + WBT * (kw + 1) + WBT * MS;
+  return (ph1 > ph3 ? (ph1 > ph2 ? ph1 : ph2) : (ph3 > ph2 ? ph3 : ph2)) * sizeof(float);
+}
+
+// ---------------------------------------------------------------------------
+// Source closure (per token): cotangents of e, chi, z back to u^, delta, k^, q^,
+// the raw gates and the values (tests/chunk_model.py sources_bwd).
+// ---------------------------------------------------------------------------
+struct SrcBwdParams {
+  sd_inputs in;
+  int Tp, KP, VP;
+  const float *uh, *delta, *kh, *qh, *de, *dchi, *dz;
+  float *duh, *ddelta, *dkh, *dqh;
+  __bf16 *derase, *dwrite, *dv;
+};
+
+__global__ __launch_bounds__(WT) void k_w_src_bwd(SrcBwdParams p) {
+  const int s = blockIdx.y, H = p.in.H, T = p.in.T, r = p.in.r, V = p.in.V;
+  const int b = s / H, h = s % H;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int t = blockIdx.x * (WT / 64) + w;
+  if (t >= p.Tp) return;
+  const bool tv = t < T;
+  const long long row = ((long long)s * p.Tp + t) * p.KP, vr = ((long long)s * p.Tp + t) * p.VP;
+  float u[4], dl[4], k[4], q[4], er[4], de[4], dc[4];
+  float usq = 0.f, dsq = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j;
+    const bool in = c < p.KP;
+    u[j] = in ? p.uh[row + c] : 0.f;
+    dl[j] = in ? p.delta[row + c] : 0.f;
+    k[j] = in ? p.kh[row + c] : 0.f;
+    q[j] = in ? p.qh[row + c] : 0.f;
+    de[j] = in ? p.de[row + c] : 0.f;
+    dc[j] = in ? p.dchi[row + c] : 0.f;
+    er[j] = (tv && c < r) ? bf2f(wrow(p.in.erase_raw, b, t, h)[c]) : 0.f;
+    usq += u[j] * u[j];
+    dsq += dl[j] * dl[j];
+  }
+  usq = wave_sum(usq);
+  dsq = wave_sum(dsq);
+  const float N = sqrtf(RHO * RHO + usq * dsq), sc = RHO / N;
+  float phi[4], se[4], bb[4];
+  float pu = 0.f, ub = 0.f, uq = 0.f, pde = 0.f, pdc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    phi[j] = sc * dl[j];
+    se[j] = 1.f / (1.f + __expf(-er[j]));
+    bb[j] = se[j] * k[j];
+    pu += phi[j] * u[j];
+    ub += u[j] * bb[j];
+    uq += u[j] * q[j];
+    pde += phi[j] * de[j];
+    pdc += phi[j] * dc[j];
+  }
+  const float den = 1.f + wave_sum(pu);
+  const float sb = wave_sum(ub) / den, sqv = wave_sum(uq) / den;
+  const float dsb = -wave_sum(pde), dsqv = -wave_sum(pdc);
+  const float dub = dsb / den, duq = dsqv / den;
+  const float dden = -(dsb * sb + dsqv * sqv) / den;
+  float dphi[4], duh[4], dqh[4], db[4];
+  float ds = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    dphi[j] = -sb * de[j] - sqv * dc[j] + dden * u[j];
+    duh[j] = dub * bb[j] + duq * q[j] + dden * phi[j];
+    db[j] = de[j] + dub * u[j];
+    dqh[j] = dc[j] + duq * u[j];
+    ds += dphi[j] * dl[j];
+  }
+  ds = wave_sum(ds);
+  const float dN2 = (-RHO * ds / (N * N)) / (2.f * N);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j;
+    if (c < p.KP) {
+      p.duh[row + c] = duh[j] + 2.f * dN2 * dsq * u[j];
+      p.ddelta[row + c] = sc * dphi[j] + 2.f * dN2 * usq * dl[j];
+      p.dkh[row + c] = db[j] * se[j];
+      p.dqh[row + c] = dqh[j];
+    }
+    const long long obase = ((long long)b * T + t) * H + h;
+    if (tv && c < r) p.derase[obase * r + c] = f2bf(db[j] * k[j] * se[j] * (1.f - se[j]));
+    if (tv && c < V) {
+      const float vv = bf2f(wrow(p.in.v, b, t, h)[c]);
+      const float wr = bf2f(wrow(p.in.write_raw, b, t, h)[c]);
+      const float sw = 1.f / (1.f + __expf(-wr));
+      const float dz = p.dz[vr + c];
+      p.dv[obase * V + c] = f2bf(sw * dz);
+      p.dwrite[obase * V + c] = f2bf(dz * vv * sw * (1.f - sw));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Final closure (per token): norms, gamma, and the two ops' decay gradients.
+// ---------------------------------------------------------------------------
+struct FinalParams {
+  sd_inputs in;
+  int Tp, KP;
+  const float *uh, *kh, *qh, *gam, *rs;
+  const float *duh, *dkh, *dqh, *dd, *dkC, *dxC, *dvC, *dqC, *dgS, *dgC;
+  __bf16 *du, *dh, *dq, *dk;
+  float *dlog_decay, *dgamma;
+};
+
+__global__ __launch_bounds__(WT) void k_w_final(FinalParams p) {
+  const int s = blockIdx.y, H = p.in.H, T = p.in.T, r = p.in.r;
+  const int b = s / H, h = s % H;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int t = blockIdx.x * (WT / 64) + w;
+  if (t >= T) return;
+  const long long tok = (long long)s * p.Tp + t, row = tok * p.KP;
+  const float gm = p.gam[tok];
+  float u[4], k[4], q[4], gu[4], gk[4], gq[4];
+  float su = 0.f, sk = 0.f, sq = 0.f, sg = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j;
+    const bool in = c < p.KP;
+    u[j] = in ? p.uh[row + c] : 0.f;
+    k[j] = in ? p.kh[row + c] : 0.f;
+    q[j] = in ? p.qh[row + c] : 0.f;
+    const float dxc = in ? p.dxC[row + c] : 0.f;
+    const float dvc = in ? p.dvC[row + c] : 0.f;
+    gu[j] = in ? p.duh[row + c] + p.dkC[row + c] + gm * dxc : 0.f;
+    gk[j] = in ? p.dkh[row + c] + p.dd[row + c] + p.dqC[row + c] : 0.f;
+    gq[j] = in ? p.dqh[row + c] : 0.f;
+    const float hv = c < r ? bf2f(wrow(p.in.h, b, t, h)[c]) : 0.f;
+    su += gu[j] * u[j];
+    sk += gk[j] * k[j];
+    sq += gq[j] * q[j];
+    sg += u[j] * dxc + hv * dvc;
+    const long long o = (((long long)b * T + t) * H + h) * r + c;
+    if (c < r) {
+      p.dh[o] = f2bf(gm * dvc);
+      p.dlog_decay[o] = p.dgS[row + c] + p.dgC[row + c];
+    }
+  }
+  su = wave_sum(su);
+  sk = wave_sum(sk);
+  sq = wave_sum(sq);
+  sg = wave_sum(sg);
+  const float ru = p.rs[tok * 3], rk = p.rs[tok * 3 + 1], rq = p.rs[tok * 3 + 2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j;
+    if (c < r) {
+      const long long o = (((long long)b * T + t) * H + h) * r + c;
+      p.du[o] = f2bf((gu[j] - su * u[j]) * ru);
+      p.dk[o] = f2bf((gk[j] - sk * k[j]) * rk);
+      p.dq[o] = f2bf((gq[j] - sq * q[j]) * rq);
+    }
+  }
+  if (l == 0) p.dgamma[((long long)b * T + t) * H + h] = sg;
+}
+
+// Output cotangent as an FP32 panel (zero when absent and on padded entries).
+struct DoutParams {
+  int H, T, V, Tp, VP;
+  const __bf16* dout;
+  float* dO;
+};
+__global__ __launch_bounds__(WT) void k_w_dout(DoutParams p) {
+  const int s = blockIdx.y, b = s / p.H, h = s % p.H;
+  const long long n = (long long)p.Tp * p.VP;
+  for (long long idx = (long long)blockIdx.x * WT + threadIdx.x; idx < n; idx += (long long)gridDim.x * WT) {
+    const int t = (int)(idx / p.VP), c = (int)(idx % p.VP);
+    float v = 0.f;
+    if (p.dout && t < p.T && c < p.V) v = bf2f(p.dout[(((long long)b * p.T + t) * p.H + h) * p.V + c]);
+    p.dO[(long long)s * n + idx] = v;
+  }
+}
+
+}  // namespace wide
+
+// ---------------------------------------------------------------------------
+// Host side: workspace layout and launch sequences.
+// ---------------------------------------------------------------------------
+namespace {
+
+using namespace wide;
+
+int pad32(int x) { return (x + 31) / 32 * 32; }
+
+struct WideDims {
+  int n, NT, Tp, KP, VP;
+};
+WideDims wide_dims(int B, int T, int H, int r, int V) {
+  WideDims d;
+  d.n = B * H;
+  d.NT = (T + WBT - 1) / WBT;
+  d.Tp = d.NT * WBT;
+  d.KP = pad32(r);
+  d.VP = pad32(V);
+  return d;
+}
+
+struct WCarver {
+  char* base;
+  size_t off = 0;
+  float* take(size_t count) {
+    off = (off + 255) & ~size_t(255);
+    float* p = base ? reinterpret_cast<float*>(base + off) : nullptr;
+    off += count * sizeof(float);
+    return p;
+  }
+};
+
+struct WideFwd {
+  float *G, *uh, *kh, *qh, *xC, *vC, *gam, *rs;
+  float *delta, *oC, *d, *e, *chi, *z, *wS;
+  float *AC, *AS, *PS, *XC, *XS;
+  float *W, *U, *Kh, *Qt, *Gam;
+};
+
+WideFwd carve_wide_fwd(void* base, const WideDims& d, size_t* total) {
+  WCarver c{(char*)base};
+  const size_t tok = (size_t)d.n * d.Tp, pk = tok * d.KP, pv = tok * d.VP;
+  const size_t mat = (size_t)d.n * d.NT * WBT * WBT;
+  WideFwd w;
+  w.G = c.take(pk); w.uh = c.take(pk); w.kh = c.take(pk); w.qh = c.take(pk);
+  w.xC = c.take(pk); w.vC = c.take(pk); w.gam = c.take(tok); w.rs = c.take(tok * 3);
+  w.delta = c.take(pk); w.oC = c.take(pk); w.d = c.take(pk); w.e = c.take(pk);
+  w.chi = c.take(pk); w.z = c.take(pv); w.wS = c.take(pv);
+  w.AC = c.take(mat); w.AS = c.take(mat); w.PS = c.take(mat);
+  w.XC = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.KP);
+  w.XS = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.VP);
+  const size_t pm = d.KP > d.VP ? pk : pv;
+  w.W = c.take(pk); w.U = c.take(pm); w.Kh = c.take(pk); w.Qt = c.take(pk);
+  w.Gam = c.take((size_t)d.n * d.NT * d.KP);
+  if (total) *total = c.off + 256;
+  return w;
+}
+
+struct WideBwd {
+  float *dO, *LC, *LS, *dU, *Wn, *Kn, *Ia, *Pp;
+  float *dwS, *dwC, *dd, *de, *dchi, *dgS;
+  float *duh, *ddelta, *dkh, *dqh, *dkC, *dxC, *dqC, *dgC;
+};
+
+WideBwd carve_wide_bwd(void* base, const WideDims& d, size_t* total) {
+  WCarver c{(char*)base};
+  const size_t tok = (size_t)d.n * d.Tp, pk = tok * d.KP, pv = tok * d.VP;
+  const size_t pm = d.KP > d.VP ? pk : pv;
+  WideBwd w;
+  w.dO = c.take(pv);
+  w.LC = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.KP);
+  w.LS = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.VP);
+  w.dU = c.take(pm); w.Wn = c.take(pk); w.Kn = c.take(pk); w.Ia = c.take(pk);
+  w.Pp = c.take((size_t)d.n * d.NT * WBT * WBT);
+  w.dwS = c.take(pv); w.dwC = c.take(pk);
+  w.dd = c.take(pk); w.de = c.take(pk); w.dchi = c.take(pk); w.dgS = c.take(pk);
+  w.duh = c.take(pk); w.ddelta = c.take(pk); w.dkh = c.take(pk); w.dqh = c.take(pk);
+  w.dkC = c.take(pk); w.dxC = c.take(pk); w.dqC = c.take(pk); w.dgC = c.take(pk);
+  if (total) *total = c.off + 256;
+  return w;
+}
+
+constexpr size_t kMaxLds = 160 * 1024;  // LDS of one gfx950 CU
+static_assert(prep_smem(WMAX) <= kMaxLds && out_smem(WMAX, WMAX, 0) <= kMaxLds &&
+                  out_smem(WMAX, WMAX, 1) <= kMaxLds && bprep_smem(WMAX) <= kMaxLds &&
+                  grad_smem(WMAX) <= kMaxLds,
+              "a wide kernel's LDS exceeds the CU");
+
+void launch_wprep(const OpParams& op, int n, hipStream_t st) {
+  const size_t sm = prep_smem(op.kw);
+  SD_SMEM_ONCE(k_w_prep, (int)prep_smem(WMAX));
+  SD_LAUNCH("k_w_prep", k_w_prep, dim3(op.NT, n), dim3(WT), sm, st, op);
+}
+
+void launch_wstate(const char* name, const WStateParams& sp, int n, hipStream_t st) {
+  SD_LAUNCH(name, k_w_state, dim3(sp.vw / TILE, n), dim3(WT), 0, st, sp);
+}
+
+}  // namespace
+
+size_t wide_fwd_workspace_bytes(int B, int T, int H, int r, int V) {
+  size_t total = 0;
+  carve_wide_fwd(nullptr, wide_dims(B, T, H, r, V), &total);
+  return total;
+}
+
+size_t wide_bwd_workspace_bytes(int B, int T, int H, int r, int V) {
+  size_t total = 0;
+  carve_wide_bwd(nullptr, wide_dims(B, T, H, r, V), &total);
+  return total;
+}
+
+int launch_wide_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* ws,
+                    hipStream_t st) {
+  const WideDims d = wide_dims(in->B, in->T, in->H, in->r, in->V);
+  const WideFwd w = carve_wide_fwd(ws, d, nullptr);
+
+  TokParams tp{};
+  tp.in = *in; tp.NT = d.NT; tp.Tp = d.Tp; tp.KP = d.KP;
+  tp.G = w.G; tp.uh = w.uh; tp.kh = w.kh; tp.qh = w.qh; tp.xC = w.xC; tp.vC = w.vC;
+  tp.gam = w.gam; tp.rs = w.rs;
+  SD_LAUNCH("k_w_tokens", k_w_tokens, dim3(d.NT, d.n), dim3(WT), 0, st, tp);
+
+  // predictor C: X = C^T, k = u^, x = gamma u^, v = gamma h, q = k^, row output
+  OpParams oc{};
+  oc.NT = d.NT; oc.Tp = d.Tp; oc.kw = d.KP; oc.vw = d.KP; oc.excl = 1; oc.colout = 0;
+  oc.k = w.uh; oc.x = w.xC; oc.v = w.vC; oc.q = w.kh; oc.G = w.G;
+  oc.A = w.AC; oc.P = w.PS; oc.W = w.W; oc.U = w.U; oc.Kh = w.Kh; oc.Qt = w.Qt; oc.Gam = w.Gam;
+  launch_wprep(oc, d.n, st);
+  WStateParams sc{};
+  sc.NT = d.NT; sc.Tp = d.Tp; sc.kw = d.KP; sc.vw = d.KP; sc.rows = in->r; sc.cols = in->r;
+  sc.W = w.W; sc.U = w.U; sc.K = w.Kh; sc.Gam = w.Gam;
+  sc.slots = w.XC; sc.wout = w.delta;
+  sc.init = in->C0; sc.init_t = 1; sc.fin = C_T; sc.fin_t = 1;
+  launch_wstate("w_state_c_fwd", sc, d.n, st);
+  OutParams orow{};
+  orow.NT = d.NT; orow.Tp = d.Tp; orow.kw = d.KP; orow.vw = d.KP; orow.colout = 0;
+  orow.slots = w.XC; orow.w = w.delta; orow.q = w.kh; orow.k = w.uh; orow.G = w.G;
+  orow.base = w.kh; orow.o = w.oC; orow.d = w.d;
+  SD_SMEM_ONCE(k_w_out, (int)out_smem(WMAX, WMAX, 0));
+  SD_LAUNCH("k_w_out_c", k_w_out, dim3(d.NT, d.n), dim3(WT), out_smem(d.KP, d.KP, 0), st, orow);
+
+  SrcParams sp{};
+  sp.in = *in; sp.Tp = d.Tp; sp.KP = d.KP; sp.VP = d.VP;
+  sp.uh = w.uh; sp.delta = w.delta; sp.kh = w.kh; sp.qh = w.qh;
+  sp.e = w.e; sp.chi = w.chi; sp.z = w.z;
+  SD_LAUNCH("k_w_sources", k_w_sources, dim3(d.Tp / (WT / 64), d.n), dim3(WT), 0, st, sp);
+
+  // memory S: k = d, x = e, v = z, q = chi, column output
+  OpParams os{};
+  os.NT = d.NT; os.Tp = d.Tp; os.kw = d.KP; os.vw = d.VP; os.excl = 0; os.colout = 1;
+  os.k = w.d; os.x = w.e; os.v = w.z; os.q = w.chi; os.G = w.G;
+  os.A = w.AS; os.P = w.PS; os.W = w.W; os.U = w.U; os.Kh = w.Kh; os.Qt = w.Qt; os.Gam = w.Gam;
+  launch_wprep(os, d.n, st);
+  WStateParams ss{};
+  ss.NT = d.NT; ss.Tp = d.Tp; ss.kw = d.KP; ss.vw = d.VP; ss.rows = in->r; ss.cols = in->V;
+  ss.W = w.W; ss.U = w.U; ss.K = w.Kh; ss.Gam = w.Gam;
+  ss.slots = w.XS; ss.wout = w.wS;
+  ss.init = in->S0; ss.init_t = 0; ss.fin = S_T; ss.fin_t = 0;
+  launch_wstate("w_state_s_fwd", ss, d.n, st);
+  OutParams ocol{};
+  ocol.NT = d.NT; ocol.Tp = d.Tp; ocol.kw = d.KP; ocol.vw = d.VP; ocol.colout = 1;
+  ocol.H = in->H; ocol.T = in->T; ocol.V = in->V;
+  ocol.slots = w.XS; ocol.w = w.wS; ocol.Qt = w.Qt; ocol.P = w.PS; ocol.out = (__bf16*)out;
+  SD_LAUNCH("k_w_out_s", k_w_out, dim3(d.NT, d.n), dim3(WT), out_smem(d.KP, d.VP, 1), st, ocol);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void* dout,
+                    const float* dC_T, const float* dS_T, void* du, void* dh, void* dq, void* dk,
+                    void* dv, void* derase, void* dwrite, float* dlog_decay, float* dgamma,
+                    float* dC0, float* dS0, hipStream_t st) {
+  const WideDims d = wide_dims(in->B, in->T, in->H, in->r, in->V);
+  const WideFwd f = carve_wide_fwd((void*)fws, d, nullptr);
+  const WideBwd w = carve_wide_bwd(bws, d, nullptr);
+  // The forward's Gam panel holds exp(G_C) of the last op it ran; both ops share
+  // the log-decay, so it serves both reverse passes.
+
+  DoutParams dp{};
+  dp.H = in->H; dp.T = in->T; dp.V = in->V; dp.Tp = d.Tp; dp.VP = d.VP;
+  dp.dout = (const __bf16*)dout; dp.dO = w.dO;
+  SD_LAUNCH("k_w_dout", k_w_dout, dim3(64, d.n), dim3(WT), 0, st, dp);
+
+  SD_SMEM_ONCE(k_w_bprep, (int)bprep_smem(WMAX));
+  SD_SMEM_ONCE(k_w_grad, (int)grad_smem(WMAX));
+
+  // ---- memory S op ----
+  BprepParams bs{};
+  bs.NT = d.NT; bs.Tp = d.Tp; bs.kw = d.KP; bs.vw = d.VP; bs.excl = 0; bs.colout = 1;
+  bs.k = f.d; bs.x = f.e; bs.q = f.chi; bs.G = f.G; bs.A = f.AS; bs.P = f.PS;
+  bs.dO = w.dO; bs.dW = nullptr;
+  bs.dU = w.dU; bs.Wn = w.Wn; bs.Kn = w.Kn; bs.Ia = w.Ia; bs.Pp = w.Pp;
+  SD_LAUNCH("k_w_bprep_s", k_w_bprep, dim3(d.NT, d.n), dim3(WT), bprep_smem(d.KP), st, bs);
+  WStateParams rs{};
+  rs.NT = d.NT; rs.Tp = d.Tp; rs.kw = d.KP; rs.vw = d.VP; rs.rows = in->r; rs.cols = in->V; rs.rev = 1;
+  rs.W = w.Wn; rs.U = w.dU; rs.K = w.Kn; rs.Gam = f.Gam; rs.Ia = w.Ia; rs.Ib = w.dO;
+  rs.slots = w.LS; rs.wout = w.dwS;
+  rs.init = dS_T; rs.init_t = 0; rs.fin = dS0; rs.fin_t = 0;
+  launch_wstate("w_state_s_bwd", rs, d.n, st);
+  GradParams gs{};
+  gs.NT = d.NT; gs.Tp = d.Tp; gs.kw = d.KP; gs.vw = d.VP; gs.excl = 0; gs.colout = 1;
+  gs.k = f.d; gs.x = f.e; gs.q = f.chi; gs.G = f.G; gs.dO = w.dO; gs.o = nullptr;
+  gs.w = f.wS; gs.dw = w.dwS; gs.Xslots = f.XS; gs.Lslots = w.LS; gs.Pp = nullptr;
+  gs.dk = w.dd; gs.dx = w.de; gs.dq = w.dchi; gs.dg = w.dgS;
+  SD_LAUNCH("k_w_grad_s", k_w_grad, dim3(d.NT, d.n), dim3(WT), grad_smem(d.KP), st, gs);
+
+  SrcBwdParams sb{};
+  sb.in = *in; sb.Tp = d.Tp; sb.KP = d.KP; sb.VP = d.VP;
+  sb.uh = f.uh; sb.delta = f.delta; sb.kh = f.kh; sb.qh = f.qh;
+  sb.de = w.de; sb.dchi = w.dchi; sb.dz = w.dwS;
+  sb.duh = w.duh; sb.ddelta = w.ddelta; sb.dkh = w.dkh; sb.dqh = w.dqh;
+  sb.derase = (__bf16*)derase; sb.dwrite = (__bf16*)dwrite; sb.dv = (__bf16*)dv;
+  SD_LAUNCH("k_w_src_bwd", k_w_src_bwd, dim3(d.Tp / (WT / 64), d.n), dim3(WT), 0, st, sb);
+
+  // ---- predictor C op: output cotangent dd (d = k^ + o_C), dW = ddelta ----
+  BprepParams bc{};
+  bc.NT = d.NT; bc.Tp = d.Tp; bc.kw = d.KP; bc.vw = d.KP; bc.excl = 1; bc.colout = 0;
+  bc.k = f.uh; bc.x = f.xC; bc.q = f.kh; bc.G = f.G; bc.A = f.AC; bc.P = nullptr;
+  bc.dO = w.dd; bc.dW = w.ddelta;
+  bc.dU = w.dU; bc.Wn = w.Wn; bc.Kn = w.Kn; bc.Ia = w.Ia; bc.Pp = w.Pp;
+  SD_LAUNCH("k_w_bprep_c", k_w_bprep, dim3(d.NT, d.n), dim3(WT), bprep_smem(d.KP), st, bc);
+  WStateParams rc{};
+  rc.NT = d.NT; rc.Tp = d.Tp; rc.kw = d.KP; rc.vw = d.KP; rc.rows = in->r; rc.cols = in->r; rc.rev = 1;
+  rc.W = w.Wn; rc.U = w.dU; rc.K = w.Kn; rc.Gam = f.Gam; rc.Ia = w.Ia; rc.Ib = f.kh;
+  rc.slots = w.LC; rc.wout = w.dwC;
+  rc.init = dC_T; rc.init_t = 1; rc.fin = dC0; rc.fin_t = 1;
+  launch_wstate("w_state_c_bwd", rc, d.n, st);
+  GradParams gc{};
+  gc.NT = d.NT; gc.Tp = d.Tp; gc.kw = d.KP; gc.vw = d.KP; gc.excl = 1; gc.colout = 0;
+  gc.k = f.uh; gc.x = f.xC; gc.q = f.kh; gc.G = f.G; gc.dO = w.dd; gc.o = f.oC;
+  gc.w = f.delta; gc.dw = w.dwC; gc.Xslots = f.XC; gc.Lslots = w.LC; gc.Pp = w.Pp;
+  gc.dk = w.dkC; gc.dx = w.dxC; gc.dq = w.dqC; gc.dg = w.dgC;
+  SD_LAUNCH("k_w_grad_c", k_w_grad, dim3(d.NT, d.n), dim3(WT), grad_smem(d.KP), st, gc);
+
+  FinalParams fp{};
+  fp.in = *in; fp.Tp = d.Tp; fp.KP = d.KP;
+  fp.uh = f.uh; fp.kh = f.kh; fp.qh = f.qh; fp.gam = f.gam; fp.rs = f.rs;
+  fp.duh = w.duh; fp.dkh = w.dkh; fp.dqh = w.dqh; fp.dd = w.dd;
+  fp.dkC = w.dkC; fp.dxC = w.dxC; fp.dvC = w.dwC; fp.dqC = w.dqC; fp.dgS = w.dgS; fp.dgC = w.dgC;
+  fp.du = (__bf16*)du; fp.dh = (__bf16*)dh; fp.dq = (__bf16*)dq; fp.dk = (__bf16*)dk;
+  fp.dlog_decay = dlog_decay; fp.dgamma = dgamma;
+  SD_LAUNCH("k_w_final", k_w_final, dim3(d.Tp / (WT / 64), d.n), dim3(WT), 0, st, fp);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+}  // namespace sd

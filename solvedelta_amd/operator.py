@@ -17,8 +17,11 @@ from . import _lib
 from .state import SolveDeltaState
 
 
-# widest key width r, and value group width, the HIP kernels take (include/solvedelta.h)
+# widest key and value widths of the main kernels; widths up to _WIDE_MAX run on
+# the library's wide-width kernels (include/solvedelta.h), as the reference's
+# state pass takes head widths up to 256 (residual_frame/common_left_h.py:139-140)
 _MAX_WIDTH = 128
+_WIDE_MAX = 256
 
 
 def _view(t: torch.Tensor) -> _lib.SdView:
@@ -182,8 +185,9 @@ def solvedelta_native(
         raise TypeError("associative_log_decay must be FP32")
     if geometry_write.dtype != torch.float32:
         raise TypeError("geometry_write must be FP32")
-    if r > _MAX_WIDTH:
-        raise ValueError(f"the MI355X path supports key widths up to {_MAX_WIDTH}")
+    if r > _WIDE_MAX:
+        # residual_frame/common_left_h.py:140 asserts the same bound
+        raise AssertionError("current kernel does not support head dimension larger than 256.")
     if associative_log_decay.stride(-1) != 1:
         associative_log_decay = associative_log_decay.contiguous()
     if initial_state is not None:
@@ -193,37 +197,38 @@ def solvedelta_native(
         if any(s.dtype != torch.float32 for s in initial_state):
             raise TypeError("all continuation states must be FP32")
 
-    if T == 1 and V <= _MAX_WIDTH and not torch.is_grad_enabled():
+    if T == 1 and r <= _MAX_WIDTH and V <= _MAX_WIDTH and not torch.is_grad_enabled():
         return _decode(u, h, q, keys, values, associative_log_decay, erase_raw, write_raw,
                        geometry_write, initial_state, return_final_state)
 
     C0 = S0 = None
     if initial_state is not None:
         C0, S0 = (s.contiguous() for s in initial_state)
-    if V <= _MAX_WIDTH:
+    group = _MAX_WIDTH if r <= _MAX_WIDTH else _WIDE_MAX
+    if V <= group:
         out, C_T, S_T = _SolveDeltaFn.apply(u, h, q, keys, values, associative_log_decay,
                                             erase_raw, write_raw, geometry_write, C0, S0,
                                             return_final_state)
     else:
         out, C_T, S_T = _value_groups(u, h, q, keys, values, associative_log_decay, erase_raw,
-                                      write_raw, geometry_write, C0, S0, return_final_state)
+                                      write_raw, geometry_write, C0, S0, return_final_state, group)
     if not return_final_state:
         return out, None
     return out, SolveDeltaState(C_T, S_T)
 
 
 def _value_groups(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,
-                  want_state):
-    """V > 128: the columns of S (and of the output) evolve independently given
+                  want_state, group):
+    """V above the kernels' value width (128, or 256 on the wide kernels): the columns of S (and of the output) evolve independently given
     the shared predictor C and the sources d, e, chi, so the value axis is cut
-    into groups of at most 128 columns, each run by the HIP path with the same
+    into groups of at most `group` columns, each run by the HIP path with the same
     key-side inputs.  Every group recomputes the predictor identically; the
     output and S are the groups' concatenation and C_T comes from the first
     group, so autograd sums the shared inputs' gradients over the groups."""
     V = values.shape[-1]
     outs, S_parts, C_T = [], [], None
-    for g0 in range(0, V, _MAX_WIDTH):
-        g1 = min(V, g0 + _MAX_WIDTH)
+    for g0 in range(0, V, group):
+        g1 = min(V, g0 + group)
         S0g = None if S0 is None else S0[..., g0:g1].contiguous()
         o, C, S = _SolveDeltaFn.apply(u, h, q, keys, values[..., g0:g1], log_decay, erase_raw,
                                       write_raw[..., g0:g1], gamma, C0, S0g, want_state)

@@ -37,9 +37,17 @@ def test_workspace_queries_and_argument_rejection():
     big = lib.sd_fwd_workspace_bytes(4, 2048, 8, 128, 128)
     assert 0 < small < big
     assert lib.sd_bwd_workspace_bytes(4, 2048, 8, 128, 128) > 0
+    # key widths 129..256 take the wide-width kernels' own (larger) layout
+    wide = lib.sd_fwd_workspace_bytes(1, 64, 1, 200, 16)
+    assert wide > small and lib.sd_bwd_workspace_bytes(1, 64, 1, 200, 256) > 0
     ins = _lib.SdInputs()
-    ins.B, ins.T, ins.H, ins.r, ins.V = 1, 4, 1, 200, 16  # r > 128
+    ins.B, ins.T, ins.H, ins.r, ins.V = 1, 4, 1, 264, 16  # r > 256
     assert lib.sd_fwd(ctypes.byref(ins), None, None, None, None, 0, None) == _lib.SD_ERR_SHAPE
+    ins.r, ins.V = 16, 300  # one call takes at most 256 value columns
+    assert lib.sd_fwd(ctypes.byref(ins), None, None, None, None, 0, None) == _lib.SD_ERR_SHAPE
+    ins.r, ins.V, ins.T = 200, 16, 1  # decode kernel: r, V <= 128
+    assert lib.sd_decode(ctypes.byref(ins), None, None, None, None) == _lib.SD_ERR_SHAPE
+    ins.T, ins.V = 4, 16
     ins.r = 16  # null operand pointers
     assert lib.sd_fwd(ctypes.byref(ins), None, None, None, None, 0, None) == _lib.SD_ERR_ARG
 
