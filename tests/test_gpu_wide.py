@@ -135,3 +135,18 @@ def test_wide_strided_bitwise_and_split_continuation():
     e = [rel(split.float(), o1.float()), rel(sb.S, s1.S), rel(sb.predictor, s1.predictor)]
     print("[wide split] " + " ".join(f"{x:.1e}" for x in e), flush=True)
     assert max(e) < 1e-5
+
+
+def test_wide_larger_forward_matches_fp64_token_loop():
+    """B=2, T=1024, H=4 at r = V = 256 against the FP64 C token loop
+    (oracle/sd_token_loop.c), with the north-star's state bound 1e-3."""
+    from gpu_common import c_forward_f64
+    args = make_inputs(2, 1024, 4, 256, 256, seed=71)
+    state = make_state(2, 4, 256, 256, seed=72)
+    with torch.no_grad():
+        out, st = _native()(*args, initial_state=state, return_final_state=True)
+    torch.cuda.synchronize()
+    eo, eC, eS = c_forward_f64(args, state)
+    errs = [rel(out.float(), eo), rel(st.predictor, eC), rel(st.S, eS)]
+    print("[wide B2 T1024 H4 r256] " + " ".join(f"{e:.1e}" for e in errs), flush=True)
+    assert errs[0] < 5e-3 and errs[1] < 1e-3 and errs[2] < 1e-3
