@@ -55,6 +55,11 @@ typedef struct {
   sd_view log_decay;                           /* fp32 */
   sd_view gamma;                               /* fp32, no channel axis */
   const float *C0, *S0;                        /* nullable initial state */
+  sd_view fresh; /* uint8 [B,T] at data[b*sb + t*st], nullable: a nonzero entry marks a
+                  * token whose predictor residual reads a zero state (the predictor's
+                  * erase read is dropped).  With log-decay <= -200 on that token, which
+                  * zeroes both states before its write, this is the reference's reset
+                  * (reference.py:156-227); solvedelta_amd.masks composes the two. */
 } sd_inputs;
 
 /* Forward. out: bf16 [B,T,H,V] contiguous. C_T / S_T nullable.

@@ -4,6 +4,7 @@ around it (conv4 frontend, decay gate, gated-RMSNorm readout), the
 recurrent cache, a causal LM shell and the Hugging Face ``SolveDeltaConfig``."""
 from .operator import solvedelta_native
 from .segments import PackedSegments, build_packed_segments, solvedelta_segmented_native
+from .masks import solvedelta_masked_native
 from .state import RELATIVE_FRAME_RADIUS, SolveDeltaState, solvedelta_zero_state
 from .mixer import (RMSNormGated, SolveDelta, SolveDeltaLayerState, SolveDeltaMixerConfig,
                     conv4_silu, kda_decay_gate)
@@ -20,7 +21,8 @@ def __getattr__(name):
     raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
 
 
-__all__ = ["solvedelta_native", "solvedelta_segmented_native", "build_packed_segments",
+__all__ = ["solvedelta_native", "solvedelta_segmented_native", "solvedelta_masked_native",
+           "build_packed_segments",
            "PackedSegments", "SolveDeltaState", "solvedelta_zero_state",
            "RELATIVE_FRAME_RADIUS", "SolveDelta", "SolveDeltaLayerState",
            "SolveDeltaMixerConfig", "RMSNormGated", "conv4_silu", "kda_decay_gate",

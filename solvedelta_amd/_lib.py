@@ -24,7 +24,8 @@ class SdInputs(ctypes.Structure):
                 ("r", ctypes.c_int), ("V", ctypes.c_int),
                 ("u", SdView), ("h", SdView), ("q", SdView), ("k", SdView), ("v", SdView),
                 ("erase_raw", SdView), ("write_raw", SdView), ("log_decay", SdView),
-                ("gamma", SdView), ("C0", ctypes.c_void_p), ("S0", ctypes.c_void_p)]
+                ("gamma", SdView), ("C0", ctypes.c_void_p), ("S0", ctypes.c_void_p),
+                ("fresh", SdView)]
 
 
 EXPORTS = {

@@ -613,7 +613,7 @@ struct BprepCSmem {
   float N[BT * LS];
   float Uh[BT][GS];
   float Kh[BT][GS];
-  float gam[BT];
+  float gam[BT];   // erase-side gamma: 0 on fresh tokens
   float krs[BT];  // 1 / |k_i|
 };
 
@@ -632,7 +632,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     const float gv = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
                                                     (long long)(t < p.T ? t : p.T - 1) * p.in.gamma.st +
                                                     (long long)hh * p.in.gamma.sh];
-    s.gam[threadIdx.x] = keep_if(t < p.T, gv);
+    s.gam[threadIdx.x] = keep_if(t < p.T, gv) * erase_keep(p.in, b, t < p.T ? t : p.T - 1);
   }
 {
     const int cl = l & 15;  // 16-lane rows: every row's loads before the first reduction
@@ -776,7 +776,7 @@ struct GradCSmem {
   ChunkDecay cd;
   float M1[BT * LS];
   float M2[BT * LS];
-  float gam[BT];
+  float gam[BT];      // erase-side gamma: 0 on fresh tokens
   float rsum[4][KD];  // rowsum(X_C (.) lambda) partials
   LPanel PA;  // dw, then dd e^G
   LPanel PW;  // delta
@@ -804,7 +804,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       const float gv = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
                                                       (long long)(t < p.T ? t : p.T - 1) * p.in.gamma.st +
                                                       (long long)hh * p.in.gamma.sh];
-      s.gam[threadIdx.x] = keep_if(t < p.T, gv);
+      s.gam[threadIdx.x] = keep_if(t < p.T, gv) * erase_keep(p.in, b, t < p.T ? t : p.T - 1);
     }
   }
   stage_panel(s.PA, dw);
@@ -988,7 +988,10 @@ __global__ __launch_bounds__(NTHREADS) void k_final(BwdParams p) {
   const float gm = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
                                                    (long long)t * p.in.gamma.st +
                                                    (long long)hh * p.in.gamma.sh];
-  const float dx0 = p.g.dxC[row + l], dx1 = p.g.dxC[row + l + 64];
+  // the erase read x = gamma u^ is dropped on fresh tokens: its cotangent dx
+  // reaches neither u nor gamma there
+  const float xk = erase_keep(p.in, b, t);
+  const float dx0 = xk * p.g.dxC[row + l], dx1 = xk * p.g.dxC[row + l + 64];
   const float dv0 = p.g.dwC[row + l], dv1 = p.g.dwC[row + l + 64];
   const float du0 = p.g.du_src[row + l] + p.g.dkC[row + l] + gm * dx0;
   const float du1 = p.g.du_src[row + l + 64] + p.g.dkC[row + l + 64] + gm * dx1;

@@ -169,7 +169,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
       acc += c.x * s.u[j] + c.y * s.u[j + 1] + c.z * s.u[j + 2] + c.w * s.u[j + 3];
     }
     acc += __shfl_xor(acc, 1, 64);
-    if (half == 0) s.delta[i] = gam * (s.hh[i] - acc);
+    if (half == 0) s.delta[i] = gam * (s.hh[i] - erase_keep(in, b, 0) * acc);
   }
   __syncthreads();
   // C' = C diag(e^g) + delta u^T in registers; d_j = k_j + sum_i C'_ij k_i

@@ -57,6 +57,7 @@ struct PrepCSmem {
   float Uh[BT][GS];   // normalised u
   __bf16 Hh[BT][PS];  // h (raw bf16, exact)
   float gam[BT];
+  float xm[BT];       // 1, or 0 on fresh tokens (no erase read)
   LPanel Yt;          // the L Gram's Y side (u), transformed and split once
 };
 
@@ -77,6 +78,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     const int t = t0 + threadIdx.x;
     const float gv = gamma_at(in.gamma, b, t < T ? t : T - 1, hh);
     s.gam[threadIdx.x] = keep_if(t < T, gv);
+    s.xm[threadIdx.x] = erase_keep(in, b, t < T ? t : T - 1);
   }
 {
     // every row's loads first: a row's reduction would otherwise hold the next
@@ -105,12 +107,12 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   // L_ij = gamma_i sum_c u_ic u_jc exp(G_{i-1,c} - G_jc), j < i
   stage_ytilde(s.Yt, cd, [&](int j, int c) { return s.Uh[j][c]; });
   decayed_gram_yt<true>(
-      cd, [&](int i, int c) { return s.gam[i] * s.Uh[i][c]; }, s.Yt,
+      cd, [&](int i, int c) { return s.gam[i] * s.xm[i] * s.Uh[i][c]; }, s.Yt,
       [&](int j, int c) { return s.Uh[j][c]; }, true, s.M);
   unit_lower_inverse(s.M, s.tmp);
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.Ac[((long long)n * p.NT + ch) * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
-  // W = A diag(gamma) (u e^{Gexcl}),  U = A diag(gamma) h
+  // W = A diag(gamma) (u e^{Gexcl} masked on fresh tokens),  U = A diag(gamma) h
   const long long rowbase = (long long)n * p.Tp + t0;
   for (int cb = w; cb < w + 1; ++cb) {
     for (int I = 0; I < NB; ++I) {
@@ -120,7 +122,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
       mma_k32x2(fa,
                 [&](int k, int nn) {
                   const int c = cb * 16 + nn;
-                  return s.Uh[k][c] * __expf(gx_excl(cd, k, c));
+                  return s.xm[k] * s.Uh[k][c] * __expf(gx_excl(cd, k, c));
                 },
                 [&](int k, int nn) { return bf2f(s.Hh[k][cb * 16 + nn]); }, K, aw, au);
 #pragma unroll

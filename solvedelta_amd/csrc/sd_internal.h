@@ -38,6 +38,15 @@ struct SPRaw {
 };
 __device__ __forceinline__ SPRaw sp_raw(const SP& sp, long long i) { return {sp.hi[i], sp.lo[i]}; }
 __device__ __forceinline__ float sp_val(SPRaw r) { return (float)r.h + (float)r.l; }
+
+// 0 on a token flagged fresh (its predictor residual reads a zero state: the
+// erase read x = gamma u^ of the C op is dropped), 1 otherwise.  t must be a
+// valid token index.
+__device__ __forceinline__ float erase_keep(const sd_inputs& in, int b, int t) {
+  if (!in.fresh.data) return 1.f;
+  const uint8_t f = ((const uint8_t*)in.fresh.data)[(long long)b * in.fresh.sb + (long long)t * in.fresh.st];
+  return f ? 0.f : 1.f;
+}
 #endif
 
 // Chunk-boundary state slots saved for the backward, in a 2-byte type (the

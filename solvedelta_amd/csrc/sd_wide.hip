@@ -75,6 +75,7 @@ __global__ __launch_bounds__(WT) void k_w_tokens(TokParams p) {
     const int t = t0 + i;
     const bool tv = t < T;
     const float gm = tv ? wgamma(p.in.gamma, b, t, h) : 0.f;
+    const float gx = tv ? gm * erase_keep(p.in, b, t) : 0.f;  // erase side: 0 on fresh tokens
     float uu[4], kk[4], qq[4], hv[4];
     float su = 0.f, sk = 0.f, sq = 0.f;
 #pragma unroll
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(WT) void k_w_tokens(TokParams p) {
         p.uh[row + cc] = uu[j] * ru;
         p.kh[row + cc] = kk[j] * rk;
         p.qh[row + cc] = qq[j] * rq;
-        p.xC[row + cc] = gm * uu[j] * ru;
+        p.xC[row + cc] = gx * uu[j] * ru;
         p.vC[row + cc] = gm * hv[j];
       }
     }
@@ -928,6 +929,7 @@ __global__ __launch_bounds__(WT) void k_w_final(FinalParams p) {
   if (t >= T) return;
   const long long tok = (long long)s * p.Tp + t, row = tok * p.KP;
   const float gm = p.gam[tok];
+  const float xk = erase_keep(p.in, b, t);  // fresh tokens: dx reaches neither u nor gamma
   float u[4], k[4], q[4], gu[4], gk[4], gq[4];
   float su = 0.f, sk = 0.f, sq = 0.f, sg = 0.f;
 #pragma unroll
@@ -937,7 +939,7 @@ __global__ __launch_bounds__(WT) void k_w_final(FinalParams p) {
     u[j] = in ? p.uh[row + c] : 0.f;
     k[j] = in ? p.kh[row + c] : 0.f;
     q[j] = in ? p.qh[row + c] : 0.f;
-    const float dxc = in ? p.dxC[row + c] : 0.f;
+    const float dxc = in ? xk * p.dxC[row + c] : 0.f;
     const float dvc = in ? p.dvC[row + c] : 0.f;
     gu[j] = in ? p.duh[row + c] + p.dkC[row + c] + gm * dxc : 0.f;
     gk[j] = in ? p.dkh[row + c] + p.dd[row + c] + p.dqC[row + c] : 0.f;

@@ -36,13 +36,20 @@ def _gamma_view(g: torch.Tensor, B: int, T: int, H: int) -> _lib.SdView:
     return _lib.SdView(g.data_ptr(), g.stride(0), g.stride(1), g.stride(2))
 
 
-def _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0):
+def _fresh_view(fresh: Optional[torch.Tensor]) -> _lib.SdView:
+    if fresh is None:
+        return _lib.SdView(None, 0, 0, 0)
+    return _lib.SdView(fresh.data_ptr(), fresh.stride(0), fresh.stride(1), 0)
+
+
+def _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0, fresh=None):
     B, T, H, r = u.shape
     V = values.shape[-1]
     return _lib.SdInputs(
         B, T, H, r, V, _view(u), _view(h), _view(q), _view(keys), _view(values),
         _view(erase_raw), _view(write_raw), _view(log_decay), _gamma_view(gamma, B, T, H),
-        None if C0 is None else C0.data_ptr(), None if S0 is None else S0.data_ptr())
+        None if C0 is None else C0.data_ptr(), None if S0 is None else S0.data_ptr(),
+        _fresh_view(fresh))
 
 
 def _stream(device) -> int:
@@ -56,12 +63,12 @@ def _ptr(t: Optional[torch.Tensor]):
 class _SolveDeltaFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,
-                want_state: bool):
+                want_state: bool, fresh=None):
         lib = _lib.load()
         B, T, H, r = u.shape
         V = values.shape[-1]
         dev = u.device
-        ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0)
+        ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0, fresh)
         out = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
         C_T = torch.empty(B, H, r, r, dtype=torch.float32, device=dev) if want_state else None
         S_T = torch.empty(B, H, r, V, dtype=torch.float32, device=dev) if want_state else None
@@ -72,9 +79,11 @@ class _SolveDeltaFn(torch.autograd.Function):
         _lib.check(rc, "sd_fwd")
         ctx.set_materialize_grads(False)
         ctx.has_C0, ctx.has_S0 = C0 is not None, S0 is not None
+        ctx.has_fresh = fresh is not None
         empty = u.new_empty(0)
         ctx.save_for_backward(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma,
-                              C0 if C0 is not None else empty, S0 if S0 is not None else empty, ws)
+                              C0 if C0 is not None else empty, S0 if S0 is not None else empty, ws,
+                              fresh if fresh is not None else empty)
         if want_state:
             return out, C_T, S_T
         return out, None, None
@@ -83,13 +92,14 @@ class _SolveDeltaFn(torch.autograd.Function):
     def backward(ctx, dout, dC, dS):
         lib = _lib.load()
         (u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,
-         ws) = ctx.saved_tensors
+         ws, fresh) = ctx.saved_tensors
         C0 = C0 if ctx.has_C0 else None
         S0 = S0 if ctx.has_S0 else None
+        fresh = fresh if ctx.has_fresh else None
         B, T, H, r = u.shape
         V = values.shape[-1]
         dev = u.device
-        ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0)
+        ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0, fresh)
         dout = None if dout is None else dout.to(torch.bfloat16).contiguous()
         dC = None if dC is None else dC.float().contiguous()
         dS = None if dS is None else dS.float().contiguous()
@@ -112,11 +122,11 @@ class _SolveDeltaFn(torch.autograd.Function):
             dgam = dgam.sum(dim=(0, 1)).reshape(gamma.shape)
         return (du.to(u.dtype), dh.to(h.dtype), dq.to(q.dtype), dk.to(keys.dtype),
                 dv.to(values.dtype), dg.to(log_decay.dtype), der.to(erase_raw.dtype),
-                dwr.to(write_raw.dtype), dgam.to(gamma.dtype), dC0, dS0, None)
+                dwr.to(write_raw.dtype), dgam.to(gamma.dtype), dC0, dS0, None, None)
 
 
 def _decode(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, initial_state,
-            return_final_state):
+            return_final_state, fresh=None):
     """T = 1 recurrent step (reference: residual_frame/recurrent.py:188-327)."""
     lib = _lib.load()
     B, T, H, r = u.shape
@@ -125,7 +135,7 @@ def _decode(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, initi
     C0 = S0 = None
     if initial_state is not None:
         C0, S0 = (s.contiguous() for s in initial_state)
-    ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0)
+    ins = _inputs(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0, fresh)
     out = torch.empty(B, 1, H, V, dtype=torch.bfloat16, device=dev)
     C_T = torch.empty(B, H, r, r, dtype=torch.float32, device=dev) if return_final_state else None
     S_T = torch.empty(B, H, r, V, dtype=torch.float32, device=dev) if return_final_state else None
@@ -136,25 +146,11 @@ def _decode(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, initi
     return out, SolveDeltaState(C_T, S_T)
 
 
-def solvedelta_native(
-    u: torch.Tensor,
-    h: torch.Tensor,
-    q: torch.Tensor,
-    keys: torch.Tensor,
-    values: torch.Tensor,
-    associative_log_decay: torch.Tensor,
-    erase_raw: torch.Tensor,
-    write_raw: torch.Tensor,
-    geometry_write: torch.Tensor,
-    *,
-    initial_state: Optional[SolveDeltaState] = None,
-    return_final_state: bool = False,
-) -> tuple[torch.Tensor, Optional[SolveDeltaState]]:
-    """Dense K=1 SolveDelta from raw fused-projection views.
-
-    Checks follow ops/operator.py:28-40 then residual_frame/operator.py:169-196
-    and :251-261 in that order; raw erase/write logits are activated inside.
-    """
+def _validate(u, h, q, keys, values, associative_log_decay, erase_raw, write_raw,
+              geometry_write, initial_state):
+    """The reference's operand checks (ops/operator.py:28-40, then
+    residual_frame/operator.py:169-196 and :251-261, in that order); returns
+    the log-decay with a unit inner stride."""
     if u.device.type != "cuda" or u.dtype != torch.bfloat16:
         raise TypeError("solvedelta_native requires BF16 CUDA activations")
     if keys.ndim != 5 or keys.shape[-2] != 1:
@@ -196,31 +192,64 @@ def solvedelta_native(
             raise ValueError("initial_state shapes do not match the input geometry")
         if any(s.dtype != torch.float32 for s in initial_state):
             raise TypeError("all continuation states must be FP32")
+    return associative_log_decay
 
+
+def solvedelta_native(
+    u: torch.Tensor,
+    h: torch.Tensor,
+    q: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    associative_log_decay: torch.Tensor,
+    erase_raw: torch.Tensor,
+    write_raw: torch.Tensor,
+    geometry_write: torch.Tensor,
+    *,
+    initial_state: Optional[SolveDeltaState] = None,
+    return_final_state: bool = False,
+) -> tuple[torch.Tensor, Optional[SolveDeltaState]]:
+    """Dense K=1 SolveDelta from raw fused-projection views.
+
+    Checks follow ops/operator.py:28-40 then residual_frame/operator.py:169-196
+    and :251-261 in that order; raw erase/write logits are activated inside.
+    """
+    associative_log_decay = _validate(u, h, q, keys, values, associative_log_decay, erase_raw,
+                                      write_raw, geometry_write, initial_state)
+    return _dispatch(u, h, q, keys, values, associative_log_decay, erase_raw, write_raw,
+                     geometry_write, initial_state, return_final_state)
+
+
+def _dispatch(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, initial_state,
+              return_final_state, fresh=None):
+    """Validated operands -> decode kernel (T = 1, no grad, r, V <= 128, as
+    residual_frame/operator.py:198-216) or the chunked kernels, in value groups
+    above the kernels' value width.  `fresh` is an optional uint8 [B,T] mask of
+    tokens whose predictor residual reads a zero state (include/solvedelta.h)."""
+    B, T, H, r = u.shape
+    V = values.shape[-1]
     if T == 1 and r <= _MAX_WIDTH and V <= _MAX_WIDTH and not torch.is_grad_enabled():
-        return _decode(u, h, q, keys, values, associative_log_decay, erase_raw, write_raw,
-                       geometry_write, initial_state, return_final_state)
-
+        return _decode(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma,
+                       initial_state, return_final_state, fresh)
     C0 = S0 = None
     if initial_state is not None:
         C0, S0 = (s.contiguous() for s in initial_state)
     group = _MAX_WIDTH if r <= _MAX_WIDTH else _WIDE_MAX
     if V <= group:
-        out, C_T, S_T = _SolveDeltaFn.apply(u, h, q, keys, values, associative_log_decay,
-                                            erase_raw, write_raw, geometry_write, C0, S0,
-                                            return_final_state)
+        out, C_T, S_T = _SolveDeltaFn.apply(u, h, q, keys, values, log_decay, erase_raw,
+                                            write_raw, gamma, C0, S0, return_final_state, fresh)
     else:
-        out, C_T, S_T = _value_groups(u, h, q, keys, values, associative_log_decay, erase_raw,
-                                      write_raw, geometry_write, C0, S0, return_final_state, group)
+        out, C_T, S_T = _value_groups(u, h, q, keys, values, log_decay, erase_raw, write_raw,
+                                      gamma, C0, S0, return_final_state, group, fresh)
     if not return_final_state:
         return out, None
     return out, SolveDeltaState(C_T, S_T)
 
 
 def _value_groups(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,
-                  want_state, group):
-    """V above the kernels' value width (128, or 256 on the wide kernels): the columns of S (and of the output) evolve independently given
-    the shared predictor C and the sources d, e, chi, so the value axis is cut
+                  want_state, group, fresh=None):
+    """V above the kernels' value width (128, or 256 on the wide kernels): the
+    columns of S (and of the output) evolve independently given the shared predictor C and the sources d, e, chi, so the value axis is cut
     into groups of at most `group` columns, each run by the HIP path with the same
     key-side inputs.  Every group recomputes the predictor identically; the
     output and S are the groups' concatenation and C_T comes from the first
@@ -231,7 +260,7 @@ def _value_groups(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma,
         g1 = min(V, g0 + group)
         S0g = None if S0 is None else S0[..., g0:g1].contiguous()
         o, C, S = _SolveDeltaFn.apply(u, h, q, keys, values[..., g0:g1], log_decay, erase_raw,
-                                      write_raw[..., g0:g1], gamma, C0, S0g, want_state)
+                                      write_raw[..., g0:g1], gamma, C0, S0g, want_state, fresh)
         outs.append(o)
         S_parts.append(S)
         if g0 == 0:

@@ -1,0 +1,118 @@
+"""Masks and resets on the dense batch (solvedelta_amd.masks: neutral invalid
+tokens, reset = log-decay kill + fresh predictor read, no repacking and no host
+sync) against the FP64 oracle with the same valid / reset masks (reference
+tests/core/test_rebuild_semantics.py:932-1039: outputs 2e-2, states rtol 1e-2 /
+atol 3e-2, gradients rel-Frobenius < 3e-2), and against the segmented path."""
+import pytest
+import torch
+
+from gpu_common import make_inputs, make_state, rel
+from oracle.sd_oracle import OracleState, solvedelta_oracle_raw
+
+pytestmark = pytest.mark.gpu
+
+
+def _masks(B, T, seed, p_valid=0.8, p_reset=0.03):
+    g = torch.Generator().manual_seed(seed)
+    valid = torch.rand(B, T, generator=g) < p_valid
+    reset = torch.rand(B, T, generator=g) < p_reset
+    return valid, reset
+
+
+def _run(B, T, H, r, V, valid, reset, seed, gamma_shape="BTH", with_state=True, grad=True):
+    from solvedelta_amd import solvedelta_masked_native
+    print(f"case masked B{B} T{T} H{H} r{r} V{V} seed {seed}", flush=True)
+    args = make_inputs(B, T, H, r, V, seed=seed, requires_grad=grad, gamma_shape=gamma_shape)
+    state = make_state(B, H, r, V, seed=seed + 1, requires_grad=grad) if with_state else None
+    valid, reset = valid.cuda(), reset.cuda()
+    out, st = solvedelta_masked_native(*args, valid, reset, initial_state=state,
+                                       return_final_state=True)
+    leaves = list(args) + (list(state) if with_state else [])
+    ref = [a.detach().double().cpu().requires_grad_(grad) for a in leaves]
+    ro, rs = solvedelta_oracle_raw(*ref[:9], initial_state=OracleState(ref[9], ref[10])
+                                   if with_state else None,
+                                   valid_mask=valid.cpu(), reset_mask=reset.cpu())
+    errs = {"out": rel(out.float(), ro), "C": rel(st.predictor, rs.predictor), "S": rel(st.S, rs.S)}
+    torch.testing.assert_close(out.float().cpu(), ro.float(), rtol=2e-2, atol=2e-2)
+    for a, b in zip(st, rs):
+        torch.testing.assert_close(a.cpu(), b.float(), rtol=1e-2, atol=3e-2)
+    assert torch.equal(out[~valid], torch.zeros_like(out[~valid]))   # invalid tokens emit 0
+    if grad:
+        g = torch.Generator().manual_seed(seed + 2)
+        cot = [torch.randn(x.shape, generator=g) for x in (out, st.predictor, st.S)]
+        grads = torch.autograd.grad((out, st.predictor, st.S), leaves,
+                                    [c.to(x.device, x.dtype) for c, x in
+                                     zip(cot, (out, st.predictor, st.S))])
+        rg = torch.autograd.grad((ro, rs.predictor, rs.S), ref, [c.double() for c in cot])
+        for i, (a, b) in enumerate(zip(grads, rg)):
+            assert torch.isfinite(a).all(), i
+            errs[f"g{i}"] = rel(a.float(), b)
+    print("  " + " ".join(f"{k}={v:.1e}" for k, v in errs.items()), flush=True)
+    for k, v in errs.items():
+        assert v < 3e-2, (k, v)
+
+
+def test_masked_short_rows():
+    """An invalid token inside the first row, a reset at 8, a row with no valid
+    token (its final state is the initial state)."""
+    valid = torch.tensor([[1, 1, 0, 1, 1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1],
+                          [0] * 19], dtype=torch.bool)
+    reset = torch.zeros_like(valid)
+    reset[0, 8] = True
+    reset[1, 3] = True   # a reset on an invalid token is ignored
+    _run(2, 19, 1, 16, 16, valid, reset, seed=149)
+
+
+@pytest.mark.parametrize("B,T,H,r,V,seed", [
+    (3, 150, 2, 32, 32, 151),
+    (2, 200, 2, 128, 128, 153),   # resets inside and at the edges of 64-token chunks
+    (1, 90, 2, 160, 96, 155),     # wide kernels
+])
+def test_masked_long_rows_several_resets(B, T, H, r, V, seed):
+    valid, reset = _masks(B, T, seed)
+    reset[0, 0] = True                      # a reset on the first token drops the initial state
+    if T > 130:
+        reset[-1, 64] = True                # on a chunk boundary
+        reset[-1, 127] = True               # on a chunk's last token
+        reset[-1, 128] = reset[-1, 129] = True   # consecutive resets
+        valid[-1, 64] = valid[-1, 127:130] = True
+    _run(B, T, H, r, V, valid, reset, seed, gamma_shape="H" if seed % 2 else "BTH")
+
+
+def test_masked_without_initial_state_and_all_valid_equals_dense():
+    """No masks set: the masked entry equals the dense operator bitwise."""
+    from solvedelta_amd import solvedelta_masked_native, solvedelta_native
+    args = make_inputs(2, 70, 2, 32, 24, seed=157)
+    valid = torch.ones(2, 70, dtype=torch.bool, device="cuda")
+    reset = torch.zeros_like(valid)
+    with torch.no_grad():
+        o1, s1 = solvedelta_masked_native(*args, valid, reset, return_final_state=True)
+        o2, s2 = solvedelta_native(*args, return_final_state=True)
+    assert torch.equal(o1, o2) and torch.equal(s1.S, s2.S) and torch.equal(s1.predictor, s2.predictor)
+    _run(1, 40, 1, 16, 16, *_masks(1, 40, 158), seed=158, with_state=False)
+
+
+def test_masked_decode_step():
+    """T = 1 through the decode kernel: a reset row restarts from zero, an
+    invalid row emits 0 and keeps its state."""
+    valid = torch.tensor([[True], [False], [True], [True]])
+    reset = torch.tensor([[True], [False], [False], [True]])
+    with torch.no_grad():
+        _run(4, 1, 2, 64, 64, valid, reset, seed=159, grad=False)
+
+
+def test_masked_matches_segmented_path():
+    from solvedelta_amd import (build_packed_segments, solvedelta_masked_native,
+                                solvedelta_segmented_native)
+    valid, reset = _masks(2, 130, 161, p_reset=0.05)
+    valid, reset = valid.cuda(), reset.cuda()
+    args = make_inputs(2, 130, 2, 64, 64, seed=161)
+    state = make_state(2, 2, 64, 64, seed=162)
+    with torch.no_grad():
+        o1, s1 = solvedelta_masked_native(*args, valid, reset, initial_state=state,
+                                          return_final_state=True)
+        o2, s2 = solvedelta_segmented_native(*args, build_packed_segments(valid, reset),
+                                             initial_state=state, return_final_state=True)
+    e = [rel(o1.float(), o2.float()), rel(s1.predictor, s2.predictor), rel(s1.S, s2.S)]
+    print("[masked vs segmented] " + " ".join(f"{x:.1e}" for x in e), flush=True)
+    assert max(e) < 5e-3

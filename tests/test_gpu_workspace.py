@@ -47,7 +47,8 @@ def _run(B, T, H, r, V, fill, seed):
     return [out, C_T, S_T, du, dh, dq, dk, dv, der, dwr, dg, dgam, dC0, dS0]
 
 
-@pytest.mark.parametrize("B,T,H,r,V", [(1, 200, 2, 128, 128), (2, 128, 1, 40, 24), (1, 19, 1, 16, 16)])
+@pytest.mark.parametrize("B,T,H,r,V", [(1, 200, 2, 128, 128), (2, 128, 1, 40, 24), (1, 19, 1, 16, 16),
+                                       (1, 70, 2, 256, 200), (1, 33, 1, 136, 40)])  # last two: wide kernels
 def test_results_do_not_depend_on_workspace_contents(B, T, H, r, V):
     print(f"case workspace fill B{B} T{T} H{H} r{r} V{V}", flush=True)
     a = _run(B, T, H, r, V, 0xFF, 61)
