@@ -42,6 +42,24 @@ int sd_conv4_silu_bwd(int B, int T, int D, const void *x, int64_t x_sb, int64_t 
                       void *dx, float *dw, float *dinit, void *workspace,
                       size_t workspace_bytes, void *stream);
 
+/* conv4 + SiLU under valid / reset masks (uint8 [B,T], element (b,t) at
+ * m[b*m_sb + t*m_st], each nullable), the reference's CPU loop
+ * (causallsso/model.py:146-164) that its varlen path reproduces by repacking
+ * (model.py:166-220, packing.py:130-132): a reset on a valid token zeroes the
+ * state first, an invalid token emits 0 and keeps the state, a valid token
+ * emits silu(w . [state, x_t]) and shifts x_t in.  No repacking, no host sync.
+ * Other arguments as sd_conv4_silu_fwd / _bwd; dx of invalid tokens is 0. */
+int sd_conv4_silu_masked_fwd(int B, int T, int D, const void *x, int64_t x_sb, int64_t x_st,
+                             const float *w, const void *init, const uint8_t *valid,
+                             const uint8_t *reset, int64_t m_sb, int64_t m_st, void *y,
+                             void *final_state, void *stream);
+size_t sd_conv4_masked_workspace_bytes(int B, int D);
+int sd_conv4_silu_masked_bwd(int B, int T, int D, const void *x, int64_t x_sb, int64_t x_st,
+                             const float *w, const void *init, const uint8_t *valid,
+                             const uint8_t *reset, int64_t m_sb, int64_t m_st, const void *dy,
+                             const void *dfinal, void *dx, float *dw, float *dinit,
+                             void *workspace, size_t workspace_bytes, void *stream);
+
 /* KDA decay gate over N rows of H*r columns:
  *   out[n,h*r+c] = -exp(log_rate[h]) * softplus(raw[n*raw_row_stride + h*r+c] + bias[h*r+c])
  * (softplus(x) = x above 20).  raw: bf16; out: fp32 [N][H*r]. */

@@ -51,6 +51,13 @@ EXPORTS = {
     "sd_conv4_silu_bwd": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64,
                                          ctypes.c_int64] + [ctypes.c_void_p] * 8
                           + [ctypes.c_size_t, ctypes.c_void_p]),
+    "sd_conv4_masked_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 2),
+    "sd_conv4_silu_masked_fwd": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64,
+                                 ctypes.c_int64] + [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 2
+                                 + [ctypes.c_void_p] * 3),
+    "sd_conv4_silu_masked_bwd": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64,
+                                 ctypes.c_int64] + [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 2
+                                 + [ctypes.c_void_p] * 6 + [ctypes.c_size_t, ctypes.c_void_p]),
     "sd_kda_gate_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 3),
     "sd_kda_gate_fwd": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64]
                         + [ctypes.c_void_p] * 4),

@@ -323,6 +323,147 @@ __global__ __launch_bounds__(RMS_ROWS * 64) void k_rms_bwd(int N, int D, float e
 
 static inline int cdiv(long long a, int b) { return (int)((a + b - 1) / b); }
 
+
+// ---------------------------------------------------------------------------
+// conv4 + SiLU under valid / reset masks, the CPU loop's semantics
+// (model.py:146-164): a reset on a valid token zeroes the 3-token state first;
+// an invalid token emits 0 and leaves the state; a valid token emits
+// silu(w . [state, x_t]) and shifts x_t into the state.  One thread per
+// (channel, batch row) walks the row, 8 tokens' loads issued at a time: the
+// masks make each window depend on the row's whole history, so the row is not
+// cut into chunks.
+// ---------------------------------------------------------------------------
+struct ConvMask {
+  const uint8_t* __restrict__ valid;  // [B,T] at b*sb + t*st, nullable (all valid)
+  const uint8_t* __restrict__ reset;  // nullable (no reset)
+  long long sb, st;
+};
+constexpr int MCONV_U = 8;
+
+__device__ __forceinline__ void conv_mask_at(const ConvMask& m, int b, int t, bool& v, bool& r) {
+  const long long o = (long long)b * m.sb + (long long)t * m.st;
+  v = m.valid ? m.valid[o] != 0 : true;
+  r = v && m.reset && m.reset[o] != 0;
+}
+
+__global__ __launch_bounds__(NTHREADS) void k_conv_masked_fwd(ConvArgs a, ConvMask m,
+                                                              __bf16* __restrict__ y,
+                                                              __bf16* __restrict__ fin) {
+  const int d = blockIdx.x * NTHREADS + threadIdx.x, b = blockIdx.y;
+  if (d >= a.D) return;
+  const int T = a.T;
+  const float w0 = a.w[d * 4], w1 = a.w[d * 4 + 1], w2 = a.w[d * 4 + 2], w3 = a.w[d * 4 + 3];
+  float s0 = conv_x(a, b, -3, d), s1 = conv_x(a, b, -2, d), s2 = conv_x(a, b, -1, d);
+  for (int t0 = 0; t0 < T; t0 += MCONV_U) {
+    float xv[MCONV_U];
+    bool vv[MCONV_U], rr[MCONV_U];
+#pragma unroll
+    for (int j = 0; j < MCONV_U; ++j) {
+      const int t = t0 + j < T ? t0 + j : T - 1;
+      xv[j] = bf2f(a.x[(long long)b * a.sb + (long long)t * a.st + d]);
+      conv_mask_at(m, b, t, vv[j], rr[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < MCONV_U; ++j) {
+      const int t = t0 + j;
+      if (t < T) {
+        if (rr[j]) s0 = s1 = s2 = 0.f;
+        const float acc = w0 * s0 + w1 * s1 + w2 * s2 + w3 * xv[j];
+        y[((long long)b * T + t) * a.D + d] = f2bf(vv[j] ? silu(acc) : 0.f);
+        if (vv[j]) {
+          s0 = s1;
+          s1 = s2;
+          s2 = xv[j];
+        }
+      }
+    }
+  }
+  if (fin) {
+    __bf16* f = fin + ((long long)b * a.D + d) * 3;
+    f[0] = f2bf(s0);
+    f[1] = f2bf(s1);
+    f[2] = f2bf(s2);
+  }
+}
+
+// Backward in one forward walk.  Each window slot carries its owner (a token
+// t >= 0, an initial-state slot -1..-3, or kNoOwner after a reset) and the
+// cotangent gathered for it so far; a slot's cotangent is complete when its
+// value leaves the window (shift, reset, or the end of the row, where the
+// final-state cotangent joins it) and is written to dx / dinit then.  Invalid
+// tokens get dx = 0.  dw partials per (row, channel) go to the workspace.
+constexpr int kNoOwner = -1000;
+
+__device__ __forceinline__ void conv_flush(int owner, float g, __bf16* __restrict__ dx,
+                                           float* __restrict__ dinit, int b, int T, int D, int d) {
+  if (owner >= 0) dx[((long long)b * T + owner) * D + d] = f2bf(g);
+  else if (owner > kNoOwner && dinit) dinit[((long long)b * D + d) * 3 + (-owner - 1)] = g;
+}
+
+__global__ __launch_bounds__(NTHREADS) void k_conv_masked_bwd(ConvArgs a, ConvMask m,
+                                                              const __bf16* __restrict__ dy,
+                                                              const __bf16* __restrict__ dfin,
+                                                              __bf16* __restrict__ dx,
+                                                              float* __restrict__ dinit,
+                                                              float* __restrict__ dw_part) {
+  const int d = blockIdx.x * NTHREADS + threadIdx.x, b = blockIdx.y;
+  if (d >= a.D) return;
+  const int T = a.T, D = a.D;
+  const float w0 = a.w[d * 4], w1 = a.w[d * 4 + 1], w2 = a.w[d * 4 + 2], w3 = a.w[d * 4 + 3];
+  float s0 = conv_x(a, b, -3, d), s1 = conv_x(a, b, -2, d), s2 = conv_x(a, b, -1, d);
+  int o0 = a.init ? -1 : kNoOwner, o1 = a.init ? -2 : kNoOwner, o2 = a.init ? -3 : kNoOwner;
+  float p0 = 0.f, p1 = 0.f, p2 = 0.f;
+  float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f;
+  for (int t0 = 0; t0 < T; t0 += MCONV_U) {
+    float xv[MCONV_U], gv[MCONV_U];
+    bool vv[MCONV_U], rr[MCONV_U];
+#pragma unroll
+    for (int j = 0; j < MCONV_U; ++j) {
+      const int t = t0 + j < T ? t0 + j : T - 1;
+      xv[j] = bf2f(a.x[(long long)b * a.sb + (long long)t * a.st + d]);
+      gv[j] = bf2f(dy[((long long)b * T + t) * D + d]);
+      conv_mask_at(m, b, t, vv[j], rr[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < MCONV_U; ++j) {
+      const int t = t0 + j;
+      if (t >= T) continue;
+      if (!vv[j]) {
+        dx[((long long)b * T + t) * D + d] = f2bf(0.f);
+        continue;
+      }
+      if (rr[j]) {
+        conv_flush(o0, p0, dx, dinit, b, T, D, d);
+        conv_flush(o1, p1, dx, dinit, b, T, D, d);
+        conv_flush(o2, p2, dx, dinit, b, T, D, d);
+        s0 = s1 = s2 = 0.f;
+        p0 = p1 = p2 = 0.f;
+        o0 = o1 = o2 = kNoOwner;
+      }
+      const float acc = w0 * s0 + w1 * s1 + w2 * s2 + w3 * xv[j];
+      const float sg = sigm(acc);
+      const float da = gv[j] * sg * (1.f + acc * (1.f - sg));
+      g0 += da * s0; g1 += da * s1; g2 += da * s2; g3 += da * xv[j];
+      p0 += da * w0; p1 += da * w1; p2 += da * w2;
+      conv_flush(o0, p0, dx, dinit, b, T, D, d);  // slot 0 leaves the window
+      s0 = s1; o0 = o1; p0 = p1;
+      s1 = s2; o1 = o2; p1 = p2;
+      s2 = xv[j]; o2 = t; p2 = da * w3;
+    }
+  }
+  if (dfin) {
+    const __bf16* f = dfin + ((long long)b * D + d) * 3;
+    p0 += bf2f(f[0]);
+    p1 += bf2f(f[1]);
+    p2 += bf2f(f[2]);
+  }
+  conv_flush(o0, p0, dx, dinit, b, T, D, d);
+  conv_flush(o1, p1, dx, dinit, b, T, D, d);
+  conv_flush(o2, p2, dx, dinit, b, T, D, d);
+  float* wp = dw_part + ((long long)b * D + d) * 4;
+  wp[0] = g0; wp[1] = g1; wp[2] = g2; wp[3] = g3;
+}
+
 }  // namespace sd
 
 using namespace sd;
@@ -359,6 +500,43 @@ int sd_conv4_silu_bwd(int B, int T, int D, const void* x, int64_t x_sb, int64_t 
             (const __bf16*)dy, (const __bf16*)dfinal, (__bf16*)dx, dinit, (float*)workspace);
   SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(4LL * D, 32)), dim3(NTHREADS), 0, st,
             (const float*)workspace, B * nch, 4 * D, dw);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+size_t sd_conv4_masked_workspace_bytes(int B, int D) {
+  if (B <= 0 || D <= 0) return 0;
+  return (size_t)B * D * 4 * sizeof(float);
+}
+
+int sd_conv4_silu_masked_fwd(int B, int T, int D, const void* x, int64_t x_sb, int64_t x_st,
+                             const float* w, const void* init, const uint8_t* valid,
+                             const uint8_t* reset, int64_t m_sb, int64_t m_st, void* y,
+                             void* final_state, void* stream) {
+  if (B <= 0 || T <= 0 || D <= 0) return SD_ERR_SHAPE;
+  if (!x || !w || !y) return SD_ERR_ARG;
+  ConvArgs a{B, T, D, (const __bf16*)x, x_sb, x_st, w, (const __bf16*)init};
+  ConvMask m{valid, reset, m_sb, m_st};
+  SD_LAUNCH("k_conv_masked_fwd", k_conv_masked_fwd, dim3(cdiv(D, NTHREADS), B), dim3(NTHREADS), 0,
+            (hipStream_t)stream, a, m, (__bf16*)y, (__bf16*)final_state);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+int sd_conv4_silu_masked_bwd(int B, int T, int D, const void* x, int64_t x_sb, int64_t x_st,
+                             const float* w, const void* init, const uint8_t* valid,
+                             const uint8_t* reset, int64_t m_sb, int64_t m_st, const void* dy,
+                             const void* dfinal, void* dx, float* dw, float* dinit,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  if (B <= 0 || T <= 0 || D <= 0) return SD_ERR_SHAPE;
+  if (!x || !w || !dy || !dx || !dw || !workspace) return SD_ERR_ARG;
+  if (workspace_bytes < sd_conv4_masked_workspace_bytes(B, D)) return SD_ERR_WORKSPACE;
+  ConvArgs a{B, T, D, (const __bf16*)x, x_sb, x_st, w, (const __bf16*)init};
+  ConvMask m{valid, reset, m_sb, m_st};
+  hipStream_t st = (hipStream_t)stream;
+  SD_LAUNCH("k_conv_masked_bwd", k_conv_masked_bwd, dim3(cdiv(D, NTHREADS), B), dim3(NTHREADS), 0,
+            st, a, m, (const __bf16*)dy, (const __bf16*)dfinal, (__bf16*)dx, dinit,
+            (float*)workspace);
+  SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(4LL * D, 32)), dim3(NTHREADS), 0, st,
+            (const float*)workspace, B, 4 * D, dw);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 

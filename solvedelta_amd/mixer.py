@@ -29,8 +29,7 @@ from torch import nn
 
 from . import _lib
 from .operator import _ptr, _stream, solvedelta_native
-from .segments import (PackedSegments, _from_segments, _to_segments, build_packed_segments,
-                       solvedelta_segmented_native)
+from .masks import solvedelta_masked_native
 from .state import SolveDeltaState
 
 
@@ -140,47 +139,79 @@ class _Conv4SiluFn(torch.autograd.Function):
         return dx, dw.to(ctx.wdtype), None if dinit is None else dinit.to(ctx.idtype), None
 
 
+class _Conv4SiluMaskedFn(torch.autograd.Function):
+    """conv4 + SiLU under valid / reset masks on the dense batch (the CPU
+    loop's semantics, model.py:146-164), without repacking."""
+
+    @staticmethod
+    def forward(ctx, x, weight, init, valid, reset, want_final: bool):
+        lib = _lib.load()
+        B, T, D = x.shape
+        if x.dtype != torch.bfloat16 or x.stride(2) != 1:
+            raise ValueError("conv4 input must be bf16 [B,T,D] with unit channel stride")
+        if weight.shape != (D, 4):
+            raise ValueError("conv weight must have shape [D,4]")
+        w32 = weight.detach().float().contiguous()
+        init_dtype = None if init is None else init.dtype
+        if init is not None:
+            if init.shape != (B, D, 3):
+                raise ValueError("conv initial state must have shape [B,D,3]")
+            init = init.to(torch.bfloat16).contiguous()
+        valid = valid.to(torch.uint8).contiguous()
+        reset = reset.to(torch.uint8).contiguous()
+        y = torch.empty(B, T, D, dtype=torch.bfloat16, device=x.device)
+        fin = torch.empty(B, D, 3, dtype=torch.bfloat16, device=x.device) if want_final else None
+        rc = lib.sd_conv4_silu_masked_fwd(B, T, D, x.data_ptr(), x.stride(0), x.stride(1),
+                                          w32.data_ptr(), _ptr(init), valid.data_ptr(),
+                                          reset.data_ptr(), T, 1, y.data_ptr(), _ptr(fin),
+                                          _stream(x.device))
+        _lib.check(rc, "sd_conv4_silu_masked_fwd")
+        ctx.save_for_backward(x, w32, init if init is not None else x.new_empty(0), valid, reset)
+        ctx.has_init = init is not None
+        ctx.wdtype = weight.dtype
+        ctx.idtype = init_dtype
+        ctx.set_materialize_grads(False)
+        return y, fin
+
+    @staticmethod
+    def backward(ctx, dy, dfin):
+        lib = _lib.load()
+        x, w32, init, valid, reset = ctx.saved_tensors
+        init = init if ctx.has_init else None
+        B, T, D = x.shape
+        if dy is None and dfin is None:
+            return None, None, None, None, None, None
+        dy = (torch.zeros(B, T, D, dtype=torch.bfloat16, device=x.device) if dy is None
+              else dy.to(torch.bfloat16).contiguous())
+        dfin = None if dfin is None else dfin.to(torch.bfloat16).contiguous()
+        dx = torch.empty(B, T, D, dtype=torch.bfloat16, device=x.device)
+        dw = torch.empty(D, 4, dtype=torch.float32, device=x.device)
+        dinit = torch.empty(B, D, 3, dtype=torch.float32, device=x.device) if init is not None else None
+        nb = lib.sd_conv4_masked_workspace_bytes(B, D)
+        ws = torch.empty(nb, dtype=torch.uint8, device=x.device)
+        rc = lib.sd_conv4_silu_masked_bwd(B, T, D, x.data_ptr(), x.stride(0), x.stride(1),
+                                          w32.data_ptr(), _ptr(init), valid.data_ptr(),
+                                          reset.data_ptr(), T, 1, dy.data_ptr(), _ptr(dfin),
+                                          dx.data_ptr(), dw.data_ptr(), _ptr(dinit), ws.data_ptr(),
+                                          nb, _stream(x.device))
+        _lib.check(rc, "sd_conv4_silu_masked_bwd")
+        return (dx, dw.to(ctx.wdtype), None if dinit is None else dinit.to(ctx.idtype), None,
+                None, None)
+
+
+def conv4_silu_masked(x, weight, valid_mask, reset_mask, initial_state=None,
+                      return_final_state=False):
+    """conv4 + SiLU under bool [B,T] valid / reset masks (model.py:146-164)."""
+    _require_device(x, weight, initial_state, valid_mask, reset_mask)
+    return _Conv4SiluMaskedFn.apply(x, weight, initial_state, valid_mask, reset_mask,
+                                    return_final_state)
+
+
 def conv4_silu(x, weight, initial_state=None, return_final_state=False):
     """causal_conv1d_fn(x^T, weight, initial_states, return_final_states,
     activation="silu") on [B,T,D] activations (model.py:119-136)."""
     _require_device(x, weight, initial_state)
     return _Conv4SiluFn.apply(x, weight, initial_state, return_final_state)
-
-
-def _conv4_segments(x, weight, initial_state, plan: PackedSegments, return_final_state):
-    """conv4 over reset-free packed segments (the CPU loop's mask/reset
-    semantics, model.py:146-164): invalid tokens emit 0 and keep the state, a
-    valid reset starts from a zero state."""
-    B, T, D = x.shape
-    base = initial_state if initial_state is not None else x.new_zeros(B, D, 3)
-    if plan.num_tokens == 0:
-        return x.new_zeros(B, T, D), (base if return_final_state else None)
-    padded = plan.max_seqlen
-    xs = _to_segments(x, plan, padded)                                 # [S, P, D]
-    seg_init = None
-    if initial_state is not None:
-        keep = plan.use_initial[:, None, None]
-        sel = initial_state.index_select(0, plan.segment_batch)
-        seg_init = torch.where(keep, sel, torch.zeros_like(sel))
-    y_seg, _ = _Conv4SiluFn.apply(xs, weight, seg_init, False)
-    y = _from_segments(y_seg, plan)
-    if not return_final_state:
-        return y, None
-    # final state of a row: the last three of (segment init, segment tokens)
-    has = plan.last_segment >= 0
-    s = plan.last_segment.clamp_min(0)
-    L = plan.segment_lengths.long()[s]                                # [B]
-    m = torch.arange(3, device=x.device)
-    pos = L[:, None] - 3 + m[None, :]                                  # [B, 3]
-    tok = xs[s[:, None], pos.clamp_min(0)]                             # [B, 3, D]
-    if seg_init is not None:
-        pre = seg_init[s].transpose(1, 2)                              # [B, 3, D]
-        pre = pre.gather(1, (pos + 3).clamp(0, 2)[:, :, None].expand(B, 3, D))
-    else:
-        pre = torch.zeros_like(tok)
-    fin = torch.where((pos >= 0)[:, :, None], tok, pre.to(tok.dtype)).transpose(1, 2)
-    fin = torch.where(has[:, None, None], fin, base.to(fin.dtype))
-    return y, fin
 
 
 # --------------------------------------------------------------------------
@@ -436,15 +467,19 @@ class SolveDelta(nn.Module):
         if proj.dtype != torch.bfloat16:
             raise TypeError("the native SolveDelta mixer needs bf16 activations "
                             "(a bf16 module or autocast)")
-        plan = None
-        if valid_mask is not None or reset_mask is not None:
+        # masks run on the dense batch (conv4 under masks, then the operator with
+        # neutral invalid tokens and reset tokens): no repacking, no host sync
+        masked = valid_mask is not None or reset_mask is not None
+        if masked:
             if valid_mask is None:
                 valid_mask = torch.ones(B, T, dtype=torch.bool, device=hidden_states.device)
             if reset_mask is None:
                 reset_mask = torch.zeros(B, T, dtype=torch.bool, device=hidden_states.device)
             if valid_mask.device != hidden_states.device or reset_mask.device != hidden_states.device:
                 raise ValueError("masks must share the activation device")
-            plan = build_packed_segments(valid_mask, reset_mask)
+            if (valid_mask.shape != (B, T) or reset_mask.shape != (B, T)
+                    or valid_mask.dtype != torch.bool or reset_mask.dtype != torch.bool):
+                raise ValueError("valid_mask and reset_mask must be bool [B,T]")
         conv_state = initial_state.conv if initial_state is not None else None
         sizes = self.projection_sizes
         final_conv = None
@@ -453,12 +488,12 @@ class SolveDelta(nn.Module):
             qkv_proj, *rest = _SplitColumns.apply(proj, (qkv_w,) + tuple(sizes[3:]))
             if conv_state is not None and (conv_state.shape != (B, qkv_w, 3)):
                 raise ValueError("conv initial state must have shape [B,D,3]")
-            if plan is None:
+            if not masked:
                 qkv, final_conv = conv4_silu(qkv_proj, self.conv_weight, conv_state,
                                              return_final_state)
             else:
-                qkv, final_conv = _conv4_segments(qkv_proj, self.conv_weight, conv_state, plan,
-                                                  return_final_state)
+                qkv, final_conv = conv4_silu_masked(qkv_proj, self.conv_weight, valid_mask,
+                                                    reset_mask, conv_state, return_final_state)
             q_raw, k_raw, v_raw = qkv.split(sizes[:3], dim=-1)
         else:
             parts = _SplitColumns.apply(proj, tuple(sizes))
@@ -481,9 +516,9 @@ class SolveDelta(nn.Module):
         op_init = initial_state.operator if initial_state is not None else None
         erase = erase_raw.view(B, T, H, 1, rk)
         write = write_raw.view(B, T, H, 1, rv)
-        if plan is not None:
-            out, op_state = solvedelta_segmented_native(
-                u, h, q, keys, values, log_decay, erase, write, gamma, plan,
+        if masked:
+            out, op_state = solvedelta_masked_native(
+                u, h, q, keys, values, log_decay, erase, write, gamma, valid_mask, reset_mask,
                 initial_state=op_init, return_final_state=return_final_state)
         else:
             out, op_state = solvedelta_native(
@@ -498,4 +533,4 @@ class SolveDelta(nn.Module):
 
 
 __all__ = ["SolveDelta", "SolveDeltaLayerState", "SolveDeltaMixerConfig", "RMSNormGated",
-           "conv4_silu", "kda_decay_gate"]
+           "conv4_silu", "conv4_silu_masked", "kda_decay_gate"]

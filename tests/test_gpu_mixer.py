@@ -199,3 +199,71 @@ def test_mixer_masks_resets_and_continuation():
     assert rel(torch.cat((y1, y2), 1).float(), yf.float()) < 1e-2
     assert torch.equal(s2.conv, sf.conv)
     assert rel(s2.operator.S, sf.operator.S) < 1e-2
+
+
+@pytest.mark.parametrize("with_init", [True, False])
+def test_conv4_masked_matches_oracle_loop_with_grads(with_init):
+    """conv4 + SiLU under valid / reset masks (no repacking) against the FP64
+    CPU loop (oracle conv4_loop, model.py:146-164): output, final state and the
+    gradients of x, the weight and the initial state."""
+    from oracle.mixer_oracle import conv4_loop
+    from solvedelta_amd.mixer import conv4_silu_masked
+    g = torch.Generator().manual_seed(31)
+    B, T, D = 3, 77, 200
+    x = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    w = 0.5 * torch.randn(D, 4, generator=g)
+    init = torch.randn(B, D, 3, generator=g).to(torch.bfloat16) if with_init else None
+    valid = torch.rand(B, T, generator=g) > 0.25
+    reset = torch.rand(B, T, generator=g) > 0.9
+    reset[0, 0] = True
+    valid[2, :] = False            # a row with no valid token keeps its initial state
+    valid[1, 70:] = False
+    xc = x.cuda().requires_grad_()
+    wc = w.cuda().requires_grad_()
+    ic = init.cuda().float().requires_grad_() if with_init else None
+    y, fin = conv4_silu_masked(xc, wc, valid.cuda(), reset.cuda(), ic, True)
+    xr = x.double().requires_grad_()
+    wr = w.double().requires_grad_()
+    ir = init.double().requires_grad_() if with_init else None
+    yo, fo = conv4_loop(xr, wr, ir, valid_mask=valid, reset_mask=reset)
+    assert torch.all(y[~valid.cuda()] == 0)
+    cy = torch.randn(B, T, D, generator=g)
+    cf = torch.randn(B, D, 3, generator=g)
+    grads = torch.autograd.grad((y, fin), [xc, wc] + ([ic] if with_init else []),
+                                (cy.to(torch.bfloat16).cuda(), cf.to(torch.bfloat16).cuda()))
+    rg = torch.autograd.grad((yo, fo), [xr, wr] + ([ir] if with_init else []),
+                             (cy.to(torch.bfloat16).double(), cf.to(torch.bfloat16).double()))
+    errs = [rel(y.float(), yo), rel(fin.float(), fo)] + [rel(a.float(), b) for a, b in zip(grads, rg)]
+    print(f"[conv masked init={with_init}] " + " ".join(f"{e:.1e}" for e in errs), flush=True)
+    assert errs[1] == 0.0          # the final state is a copy of bf16 inputs
+    assert max(errs) < 5e-3
+    assert torch.all(grads[0][~valid.cuda()] == 0)
+
+
+def test_mixer_masks_backward_matches_oracle():
+    """The masked mixer (masked conv4 + masked operator, no repacking) forward and
+    every parameter / input gradient against the FP64 mixer oracle."""
+    mx = _mx()
+    layer = _layer(hidden=128, H=2, r=32, seed=3)
+    g = torch.Generator().manual_seed(7)
+    B, T = 2, 70
+    x = torch.randn(B, T, 128, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    valid = torch.rand(B, T, generator=g) > 0.2
+    reset = torch.rand(B, T, generator=g) > 0.93
+    y = layer(x, valid_mask=valid.cuda(), reset_mask=reset.cuda())
+    params = _params(layer)
+    for p in params.values():
+        p.requires_grad_()
+    xd = _d(x).requires_grad_()
+    yo, _, _ = mixer_oracle(params, xd, heads=2, rk=32, rv=32, valid_mask=valid, reset_mask=reset)
+    cot = torch.randn(y.shape, generator=g)
+    names = [n for n, _ in layer.named_parameters()]
+    grads = torch.autograd.grad(y, [x] + [p for _, p in layer.named_parameters()],
+                                cot.to(y.device, y.dtype))
+    rg = torch.autograd.grad(yo, [xd] + [params[n] for n in names], cot.double())
+    errs = {"y": rel(y.float(), yo), "x": rel(grads[0].float(), rg[0])}
+    for n, a, b in zip(names, grads[1:], rg[1:]):
+        errs[n] = rel(a.float(), b)
+    print("[mixer masks bwd] " + " ".join(f"{k}={v:.1e}" for k, v in errs.items()), flush=True)
+    for k, v in errs.items():
+        assert v < 3e-2, (k, v)
