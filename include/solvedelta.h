@@ -63,10 +63,18 @@ typedef struct {
 } sd_inputs;
 
 /* Forward. out: bf16 [B,T,H,V] contiguous. C_T / S_T nullable.
- * The workspace also holds what sd_bwd needs; keep it alive until then. */
+ * The workspace is two regions: the first sd_fwd_saved_bytes hold what sd_bwd
+ * reads (pass that region, or the whole workspace, to sd_bwd and keep it alive
+ * until then); the rest is forward-only scratch.  sd_fwd_split takes the two
+ * regions as separate buffers, so a caller can release the scratch as soon as
+ * the forward has run (the saved region is what an autograd graph holds). */
 size_t sd_fwd_workspace_bytes(int B, int T, int H, int r, int V);
+size_t sd_fwd_saved_bytes(int B, int T, int H, int r, int V);
+size_t sd_fwd_scratch_bytes(int B, int T, int H, int r, int V);
 int sd_fwd(const sd_inputs *in, void *out, float *C_T, float *S_T, void *workspace,
            size_t workspace_bytes, void *stream);
+int sd_fwd_split(const sd_inputs *in, void *out, float *C_T, float *S_T, void *saved,
+                 size_t saved_bytes, void *scratch, size_t scratch_bytes, void *stream);
 
 /* Backward of sd_fwd with the same inputs and the forward's workspace.
  * dout: bf16 [B,T,H,V] contiguous (nullable = zero); dC_T, dS_T fp32 (nullable).

@@ -31,6 +31,11 @@ class SdInputs(ctypes.Structure):
 EXPORTS = {
     "sd_version": (ctypes.c_char_p, []),
     "sd_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 5),
+    "sd_fwd_saved_bytes": (ctypes.c_size_t, [ctypes.c_int] * 5),
+    "sd_fwd_scratch_bytes": (ctypes.c_size_t, [ctypes.c_int] * 5),
+    "sd_fwd_split": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                    ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "sd_fwd": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "sd_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 5),

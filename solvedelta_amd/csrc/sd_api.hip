@@ -29,10 +29,15 @@ struct Carver {
   }
 };
 
-FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
+// The forward workspace is two regions: `saved` holds what sd_bwd reads (chunk
+// states, inverses, forward token panels, the state passes' key panels, the
+// readout panels and the chunk decay); `scratch` holds the panels only the
+// forward's state passes read (W, U of both ops), free once sd_fwd returns.
+FwdWs carve_fwd(void* saved, void* scratch, int B, int T, int H, size_t* saved_bytes,
+                size_t* scratch_bytes) {
   const size_t n = (size_t)B * H, NT = (T + kBT - 1) / kBT, Tp = NT * kBT;
   const size_t panel = n * Tp * kKD, states = n * (NT + 1) * kKD * kKD, amat = n * NT * kBT * kBT;
-  Carver c{(char*)base};
+  Carver c{(char*)saved};
   FwdWs w;
   w.Xc = c.take<xslot_t>(states);
   w.Xs = c.take<xslot_t>(states);
@@ -43,17 +48,37 @@ FwdWs carve_fwd(void* base, int B, int T, int H, size_t* total) {
   w.delta = c.take<fpan_t>(panel);
   w.d = c.take<fpan_t>(panel);
   w.wS = c.take<fpan_t>(panel);
-  w.Wc = c.take<_Float16>(panel);
-  w.Uc = c.take<float>(panel);
   w.Kc = c.take<_Float16>(panel);
   w.Gam = c.take<float>(n * NT * kKD);
-  w.Ws = c.take<_Float16>(panel);
-  w.Us = c.take<float>(panel);
   w.Ks = c.take<_Float16>(panel);
   w.Qs = c.take_sp(panel);
   w.Ps = c.take_sp(n * NT * kBT * kBT);
-  if (total) *total = c.off + 256;
+  if (saved_bytes) *saved_bytes = c.off + 256;
+  Carver t{(char*)scratch};
+  w.Wc = t.take<_Float16>(panel);
+  w.Uc = t.take<float>(panel);
+  w.Ws = t.take<_Float16>(panel);
+  w.Us = t.take<float>(panel);
+  if (scratch_bytes) *scratch_bytes = t.off + 256;
   return w;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Saved / scratch sizes of either kernel family.
+void fwd_sizes(int B, int T, int H, int r, int V, size_t* saved, size_t* scratch) {
+  if (is_wide(r, V)) {
+    wide_fwd_sizes(B, T, H, r, V, saved, scratch);
+    return;
+  }
+  carve_fwd(nullptr, nullptr, B, T, H, saved, scratch);
+}
+
+int fwd_launch(const sd_inputs* in, void* out, float* C_T, float* S_T, void* saved,
+               void* scratch, hipStream_t st) {
+  if (is_wide(in->r, in->V)) return launch_wide_fwd(in, out, C_T, S_T, saved, scratch, st);
+  FwdWs w = carve_fwd(saved, scratch, in->B, in->T, in->H, nullptr, nullptr);
+  return launch_fwd(in, out, C_T, S_T, w, st);
 }
 
 BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
@@ -122,11 +147,22 @@ extern "C" {
 
 const char* sd_version(void) { return "solvedelta_amd 0.1 (gfx950)"; }
 
+size_t sd_fwd_saved_bytes(int B, int T, int H, int r, int V) {
+  size_t saved = 0, scratch = 0;
+  fwd_sizes(B, T, H, r, V, &saved, &scratch);
+  return saved;
+}
+
+size_t sd_fwd_scratch_bytes(int B, int T, int H, int r, int V) {
+  size_t saved = 0, scratch = 0;
+  fwd_sizes(B, T, H, r, V, &saved, &scratch);
+  return scratch;
+}
+
 size_t sd_fwd_workspace_bytes(int B, int T, int H, int r, int V) {
-  if (is_wide(r, V)) return wide_fwd_workspace_bytes(B, T, H, r, V);
-  size_t total = 0;
-  carve_fwd(nullptr, B, T, H, &total);
-  return total;
+  size_t saved = 0, scratch = 0;
+  fwd_sizes(B, T, H, r, V, &saved, &scratch);
+  return align256(saved) + scratch;
 }
 
 int sd_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* workspace,
@@ -134,15 +170,22 @@ int sd_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* workspa
   int rc = check_inputs(in);
   if (rc) return rc;
   if (!out || !workspace) return SD_ERR_ARG;
-  size_t need = 0;
-  if (is_wide(in->r, in->V)) {
-    if (workspace_bytes < wide_fwd_workspace_bytes(in->B, in->T, in->H, in->r, in->V))
-      return SD_ERR_WORKSPACE;
-    return launch_wide_fwd(in, out, C_T, S_T, workspace, (hipStream_t)stream);
-  }
-  FwdWs w = carve_fwd(workspace, in->B, in->T, in->H, &need);
-  if (workspace_bytes < need) return SD_ERR_WORKSPACE;
-  return launch_fwd(in, out, C_T, S_T, w, (hipStream_t)stream);
+  size_t saved = 0, scratch = 0;
+  fwd_sizes(in->B, in->T, in->H, in->r, in->V, &saved, &scratch);
+  if (workspace_bytes < align256(saved) + scratch) return SD_ERR_WORKSPACE;
+  return fwd_launch(in, out, C_T, S_T, workspace, (char*)workspace + align256(saved),
+                    (hipStream_t)stream);
+}
+
+int sd_fwd_split(const sd_inputs* in, void* out, float* C_T, float* S_T, void* saved,
+                 size_t saved_bytes, void* scratch, size_t scratch_bytes, void* stream) {
+  int rc = check_inputs(in);
+  if (rc) return rc;
+  if (!out || !saved || !scratch) return SD_ERR_ARG;
+  size_t need_saved = 0, need_scratch = 0;
+  fwd_sizes(in->B, in->T, in->H, in->r, in->V, &need_saved, &need_scratch);
+  if (saved_bytes < need_saved || scratch_bytes < need_scratch) return SD_ERR_WORKSPACE;
+  return fwd_launch(in, out, C_T, S_T, saved, scratch, (hipStream_t)stream);
 }
 
 size_t sd_noalloc_scratch_bytes(void) { return SD_NOALLOC_SCRATCH_BYTES; }
@@ -151,17 +194,13 @@ int sd_fwd_noalloc(const sd_inputs* in, void* out, float* C_T, float* S_T, void*
   int rc = check_inputs(in);
   if (rc) return rc;
   if (!out) return SD_ERR_ARG;
-  const bool wide = is_wide(in->r, in->V);
-  size_t need = 0;
-  if (wide) need = wide_fwd_workspace_bytes(in->B, in->T, in->H, in->r, in->V);
-  else carve_fwd(nullptr, in->B, in->T, in->H, &need);
-  if (need > SD_NOALLOC_SCRATCH_BYTES) return SD_ERR_WORKSPACE;
+  size_t saved = 0, scratch_b = 0;
+  fwd_sizes(in->B, in->T, in->H, in->r, in->V, &saved, &scratch_b);
+  if (align256(saved) + scratch_b > SD_NOALLOC_SCRATCH_BYTES) return SD_ERR_WORKSPACE;
   void* base = nullptr;
   rc = scratch_for_current_device(&base);
   if (rc) return rc;
-  if (wide) return launch_wide_fwd(in, out, C_T, S_T, base, (hipStream_t)stream);
-  FwdWs w = carve_fwd(base, in->B, in->T, in->H, nullptr);
-  return launch_fwd(in, out, C_T, S_T, w, (hipStream_t)stream);
+  return fwd_launch(in, out, C_T, S_T, base, (char*)base + align256(saved), (hipStream_t)stream);
 }
 
 int sd_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, void* stream) {
@@ -198,7 +237,7 @@ int sd_bwd(const sd_inputs* in, const void* fwd_workspace, const void* dout, con
   }
   BwdWs bw = carve_bwd(workspace, in->B, in->T, in->H, &need);
   if (workspace_bytes < need) return SD_ERR_WORKSPACE;
-  FwdWs fw = carve_fwd((void*)fwd_workspace, in->B, in->T, in->H, nullptr);
+  FwdWs fw = carve_fwd((void*)fwd_workspace, nullptr, in->B, in->T, in->H, nullptr, nullptr);
   return launch_bwd(in, fw, bw, dout, dC_T, dS_T, du, dh, dq, dk, dv, derase, dwrite, dlog_decay,
                     dgamma, dC0, dS0, (hipStream_t)stream);
 }

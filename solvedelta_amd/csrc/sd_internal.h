@@ -178,10 +178,10 @@ int launch_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, hipStr
 // workspace layout and kernels (sd_wide.hip).
 constexpr int kWideMax = 256;
 inline bool is_wide(int r, int V) { return r > 128 || V > 128; }
-size_t wide_fwd_workspace_bytes(int B, int T, int H, int r, int V);
+void wide_fwd_sizes(int B, int T, int H, int r, int V, size_t* saved, size_t* scratch);
 size_t wide_bwd_workspace_bytes(int B, int T, int H, int r, int V);
-int launch_wide_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* ws,
-                    hipStream_t st);
+int launch_wide_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* saved,
+                    void* scratch, hipStream_t st);
 int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void* dout,
                     const float* dC_T, const float* dS_T, void* du, void* dh, void* dq, void* dk,
                     void* dv, void* derase, void* dwrite, float* dlog_decay, float* dgamma,

@@ -1032,22 +1032,28 @@ struct WideFwd {
   float *W, *U, *Kh, *Qt, *Gam;
 };
 
-WideFwd carve_wide_fwd(void* base, const WideDims& d, size_t* total) {
-  WCarver c{(char*)base};
+// saved: what the backward reads; scratch: the forward-only panels (the C op's
+// gamma h, the S op's z, and both ops' W, U, K^, Q~).
+WideFwd carve_wide_fwd(void* saved, void* scratch, const WideDims& d, size_t* saved_bytes,
+                       size_t* scratch_bytes) {
+  WCarver c{(char*)saved};
   const size_t tok = (size_t)d.n * d.Tp, pk = tok * d.KP, pv = tok * d.VP;
   const size_t mat = (size_t)d.n * d.NT * WBT * WBT;
   WideFwd w;
   w.G = c.take(pk); w.uh = c.take(pk); w.kh = c.take(pk); w.qh = c.take(pk);
-  w.xC = c.take(pk); w.vC = c.take(pk); w.gam = c.take(tok); w.rs = c.take(tok * 3);
+  w.xC = c.take(pk); w.gam = c.take(tok); w.rs = c.take(tok * 3);
   w.delta = c.take(pk); w.oC = c.take(pk); w.d = c.take(pk); w.e = c.take(pk);
-  w.chi = c.take(pk); w.z = c.take(pv); w.wS = c.take(pv);
+  w.chi = c.take(pk); w.wS = c.take(pv);
   w.AC = c.take(mat); w.AS = c.take(mat); w.PS = c.take(mat);
   w.XC = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.KP);
   w.XS = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.VP);
-  const size_t pm = d.KP > d.VP ? pk : pv;
-  w.W = c.take(pk); w.U = c.take(pm); w.Kh = c.take(pk); w.Qt = c.take(pk);
   w.Gam = c.take((size_t)d.n * d.NT * d.KP);
-  if (total) *total = c.off + 256;
+  if (saved_bytes) *saved_bytes = c.off + 256;
+  WCarver t{(char*)scratch};
+  const size_t pm = d.KP > d.VP ? pk : pv;
+  w.vC = t.take(pk); w.z = t.take(pv);
+  w.W = t.take(pk); w.U = t.take(pm); w.Kh = t.take(pk); w.Qt = t.take(pk);
+  if (scratch_bytes) *scratch_bytes = t.off + 256;
   return w;
 }
 
@@ -1093,10 +1099,8 @@ void launch_wstate(const char* name, const WStateParams& sp, int n, hipStream_t 
 
 }  // namespace
 
-size_t wide_fwd_workspace_bytes(int B, int T, int H, int r, int V) {
-  size_t total = 0;
-  carve_wide_fwd(nullptr, wide_dims(B, T, H, r, V), &total);
-  return total;
+void wide_fwd_sizes(int B, int T, int H, int r, int V, size_t* saved, size_t* scratch) {
+  carve_wide_fwd(nullptr, nullptr, wide_dims(B, T, H, r, V), saved, scratch);
 }
 
 size_t wide_bwd_workspace_bytes(int B, int T, int H, int r, int V) {
@@ -1105,10 +1109,10 @@ size_t wide_bwd_workspace_bytes(int B, int T, int H, int r, int V) {
   return total;
 }
 
-int launch_wide_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* ws,
-                    hipStream_t st) {
+int launch_wide_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void* saved,
+                    void* scratch, hipStream_t st) {
   const WideDims d = wide_dims(in->B, in->T, in->H, in->r, in->V);
-  const WideFwd w = carve_wide_fwd(ws, d, nullptr);
+  const WideFwd w = carve_wide_fwd(saved, scratch, d, nullptr, nullptr);
 
   TokParams tp{};
   tp.in = *in; tp.NT = d.NT; tp.Tp = d.Tp; tp.KP = d.KP;
@@ -1166,7 +1170,7 @@ int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void*
                     void* dv, void* derase, void* dwrite, float* dlog_decay, float* dgamma,
                     float* dC0, float* dS0, hipStream_t st) {
   const WideDims d = wide_dims(in->B, in->T, in->H, in->r, in->V);
-  const WideFwd f = carve_wide_fwd((void*)fws, d, nullptr);
+  const WideFwd f = carve_wide_fwd((void*)fws, nullptr, d, nullptr, nullptr);
   const WideBwd w = carve_wide_bwd(bws, d, nullptr);
   // The forward's Gam panel holds exp(G_C) of the last op it ran; both ops share
   // the log-decay, so it serves both reverse passes.

@@ -72,11 +72,16 @@ class _SolveDeltaFn(torch.autograd.Function):
         out = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
         C_T = torch.empty(B, H, r, r, dtype=torch.float32, device=dev) if want_state else None
         S_T = torch.empty(B, H, r, V, dtype=torch.float32, device=dev) if want_state else None
-        nbytes = lib.sd_fwd_workspace_bytes(B, T, H, r, V)
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        rc = lib.sd_fwd(ctypes.byref(ins), out.data_ptr(), _ptr(C_T), _ptr(S_T), ws.data_ptr(),
-                        nbytes, _stream(dev))
-        _lib.check(rc, "sd_fwd")
+        # the saved region is held for the backward; the scratch region (panels
+        # only the forward's state passes read) returns to the allocator here
+        nsaved = lib.sd_fwd_saved_bytes(B, T, H, r, V)
+        nscratch = lib.sd_fwd_scratch_bytes(B, T, H, r, V)
+        ws = torch.empty(nsaved, dtype=torch.uint8, device=dev)
+        scratch = torch.empty(nscratch, dtype=torch.uint8, device=dev)
+        rc = lib.sd_fwd_split(ctypes.byref(ins), out.data_ptr(), _ptr(C_T), _ptr(S_T),
+                              ws.data_ptr(), nsaved, scratch.data_ptr(), nscratch, _stream(dev))
+        _lib.check(rc, "sd_fwd_split")
+        del scratch
         ctx.set_materialize_grads(False)
         ctx.has_C0, ctx.has_S0 = C0 is not None, S0 is not None
         ctx.has_fresh = fresh is not None

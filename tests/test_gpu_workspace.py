@@ -12,7 +12,7 @@ from gpu_common import make_inputs, make_state
 pytestmark = pytest.mark.gpu
 
 
-def _run(B, T, H, r, V, fill, seed):
+def _run(B, T, H, r, V, fill, seed, split=False):
     from solvedelta_amd import _lib
     from solvedelta_amd.operator import _inputs
     lib = _lib.load()
@@ -30,8 +30,18 @@ def _run(B, T, H, r, V, fill, seed):
     bws = torch.full((nb,), fill, dtype=torch.uint8, device=dev)
     out = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
     C_T, S_T = torch.empty_like(C0), torch.empty_like(S0)
-    assert lib.sd_fwd(ctypes.byref(ins), out.data_ptr(), C_T.data_ptr(), S_T.data_ptr(),
-                      fws.data_ptr(), nf, st) == 0
+    if split:
+        # saved and scratch regions as separate buffers; the backward gets an
+        # exactly sized saved region, the scratch is released before it runs
+        ns, nx = lib.sd_fwd_saved_bytes(B, T, H, r, V), lib.sd_fwd_scratch_bytes(B, T, H, r, V)
+        fws = torch.full((ns,), fill, dtype=torch.uint8, device=dev)
+        scratch = torch.full((nx,), fill, dtype=torch.uint8, device=dev)
+        assert lib.sd_fwd_split(ctypes.byref(ins), out.data_ptr(), C_T.data_ptr(), S_T.data_ptr(),
+                                fws.data_ptr(), ns, scratch.data_ptr(), nx, st) == 0
+        scratch.fill_(0xFF)   # the backward reads nothing from it
+    else:
+        assert lib.sd_fwd(ctypes.byref(ins), out.data_ptr(), C_T.data_ptr(), S_T.data_ptr(),
+                          fws.data_ptr(), nf, st) == 0
     bf = dict(dtype=torch.bfloat16, device=dev)
     grads = [torch.empty(B, T, H, r, **bf) for _ in range(4)] + \
             [torch.empty(B, T, H, V, **bf) for _ in range(2)] + [torch.empty(B, T, H, r, **bf)]
@@ -55,4 +65,15 @@ def test_results_do_not_depend_on_workspace_contents(B, T, H, r, V):
     z = _run(B, T, H, r, V, 0x00, 61)
     for i, (x, y) in enumerate(zip(a, z)):
         assert torch.isfinite(x.float()).all(), i
+        assert torch.equal(x, y), i
+
+
+@pytest.mark.parametrize("B,T,H,r,V", [(1, 200, 2, 128, 128), (1, 70, 2, 256, 200)])
+def test_split_workspace_equals_single_workspace(B, T, H, r, V):
+    """sd_fwd_split with separate saved / scratch buffers (the scratch overwritten
+    before the backward) gives bitwise the single-workspace results."""
+    print(f"case split workspace B{B} T{T} H{H} r{r} V{V}", flush=True)
+    a = _run(B, T, H, r, V, 0x00, 63, split=True)
+    z = _run(B, T, H, r, V, 0x00, 63)
+    for i, (x, y) in enumerate(zip(a, z)):
         assert torch.equal(x, y), i
