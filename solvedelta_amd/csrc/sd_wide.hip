@@ -246,103 +246,275 @@ struct WStateParams {
   float* fin; int fin_t;
 };
 
-__global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
-  __shared__ __align__(16) float Xl[WMAX][TILE + 1];
-  __shared__ __align__(16) float Wl[WBT][WMAX + 1];
-  __shared__ float wl[WBT][TILE + 1];
-  __shared__ float Il[WBT][TILE + 1];
-  const int tile = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw, c0 = tile * TILE;
-  const int r = threadIdx.x;
-  float X[TILE];
+// Matrix-core form.  A workgroup owns a 32-column tile (two 16-column
+// halves).  The tile's rows are cut into 16-row blocks dealt round-robin to
+// the 4 waves (up to 4 per wave), each half held as an FP32 MFMA accumulator
+// (lane (g, n) holds rows 4g..4g+3 of column n).  Every product runs on
+// v_mfma_f32_16x16x4f32 with the sum index k = 4g + e carried by MFMA e and
+// lane group g, so an accumulator block is a B operand as it stands (no
+// transpose):
+//   w = U - W X0:      each wave sums its own row blocks, partials reduced
+//                      across the waves through LDS;
+//   X = Gamma X + K^T w (+ A^T B): the w accumulators are again B operands.
+// W is staged row-major [32][kw+4], K (and the injection A) transposed
+// [kw][36], the injection B tile transposed [32][36].  The next chunk's W, K
+// and A are loaded into registers while the current chunk computes.
+constexpr int WRB = WMAX / 16 / 4;  // row blocks per wave
+constexpr int LDT = WBT + 4;        // row stride of the transposed panels
+constexpr int STILE = 32;           // state columns per workgroup
+constexpr int NSUB = STILE / 16;
+constexpr int PFQ = WBT * WMAX / 4 / WT;  // 16-byte pieces of one [32][kw] panel per thread (kw = 256)
+constexpr size_t state_smem(int kw, bool inj) {
+  return (size_t)(WBT * (kw + 4) + kw * LDT + (inj ? kw * LDT + STILE * LDT : 0) +
+                  4 * NSUB * 2 * 4 * 64) * sizeof(float);
+}
+
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Registers <-> one [32 tokens][kw] panel: piece q of thread t is element
+// (i, 4 c4) with i = (t + 256 q) % 32, c4 = (t + 256 q) / 32, so a wave's
+// transposed LDS writes land on consecutive tokens (distinct banks).
+struct PanelRegs {
+  float4 v[PFQ];
+};
+__device__ __forceinline__ void panel_load(PanelRegs& r, const float* src, int kw) {
 #pragma unroll
-  for (int j = 0; j < TILE; ++j) {
-    const int c = c0 + j;
-    float v = 0.f;
-    if (p.init && r < p.rows && c < p.cols)
-      v = p.init_t ? p.init[((long long)s * p.cols + c) * p.rows + r]
-                   : p.init[((long long)s * p.rows + r) * p.cols + c];
-    X[j] = v;
+  for (int q = 0; q < PFQ; ++q) {
+    const int idx = threadIdx.x + WT * q, i = idx & 31, c = (idx >> 5) * 4;
+    r.v[q] = c < kw ? *reinterpret_cast<const float4*>(src + (long long)i * kw + c)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+__device__ __forceinline__ void panel_store_rows(const PanelRegs& r, float* dst, int ld, int kw) {
+#pragma unroll
+  for (int q = 0; q < PFQ; ++q) {
+    const int idx = threadIdx.x + WT * q, i = idx & 31, c = (idx >> 5) * 4;
+    if (c < kw) *reinterpret_cast<float4*>(dst + i * ld + c) = r.v[q];
+  }
+}
+__device__ __forceinline__ void panel_store_t(const PanelRegs& r, float* dst, int kw) {
+#pragma unroll
+  for (int q = 0; q < PFQ; ++q) {
+    const int idx = threadIdx.x + WT * q, i = idx & 31, c = (idx >> 5) * 4;
+    if (c < kw) {
+      dst[c * LDT + i] = r.v[q].x;
+      dst[(c + 1) * LDT + i] = r.v[q].y;
+      dst[(c + 2) * LDT + i] = r.v[q].z;
+      dst[(c + 3) * LDT + i] = r.v[q].w;
+    }
+  }
+}
+
+__global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
+  extern __shared__ __align__(16) float sm[];
+  const int tile = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw, c0 = tile * STILE;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
+  const int nrb = kw / 16, ldw = kw + 4;
+  const bool inj = p.Ia != nullptr;
+  float* Wl = sm;                       // W [32][kw+4]
+  float* Kt = Wl + WBT * ldw;           // K^T [kw][LDT]
+  float* At = Kt + kw * LDT;            // injection A^T [kw][LDT]
+  float* Bt = At + (inj ? kw * LDT : 0);  // injection B^T [32][LDT]
+  float* red = Bt + (inj ? STILE * LDT : 0);  // w partials [4 waves][NSUB][2][4][64]
+  f4 X[WRB][NSUB];
+#pragma unroll
+  for (int q = 0; q < WRB; ++q) {
+    const int rb = w + 4 * q;
+#pragma unroll
+    for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = rb * 16 + 4 * g + e, col = c0 + h * 16 + m;
+        float v = 0.f;
+        if (rb < nrb && p.init && row < p.rows && col < p.cols)
+          v = p.init_t ? p.init[((long long)s * p.cols + col) * p.rows + row]
+                       : p.init[((long long)s * p.rows + row) * p.cols + col];
+        X[q][h][e] = v;
+      }
   }
   const long long sb = (long long)s * (p.NT + 1) * kw * vw;
+  auto tok0 = [&](int step) {
+    return (long long)s * p.Tp + (long long)(p.rev ? p.NT - 1 - step : step) * WBT;
+  };
+  PanelRegs nW, nK, nA;
+  panel_load(nW, p.W + tok0(0) * kw, kw);
+  panel_load(nK, p.K + tok0(0) * kw, kw);
+  if (inj) panel_load(nA, p.Ia + tok0(0) * kw, kw);
   for (int step = 0; step < p.NT; ++step) {
     const int ch = p.rev ? p.NT - 1 - step : step;
-    const long long tb = (long long)s * p.Tp + ch * WBT;
-    if (r < kw) {
+    const long long tb = tok0(step);
+    panel_store_rows(nW, Wl, ldw, kw);
+    panel_store_t(nK, Kt, kw);
+    if (inj) {
+      panel_store_t(nA, At, kw);
+      for (int q = threadIdx.x; q < WBT * STILE; q += WT) {
+        const int i = q & 31, n = q >> 5;
+        Bt[n * LDT + i] = p.Ib[(tb + i) * vw + c0 + n];
+      }
+    }
+    // this step's U and chunk decay, loaded ahead of their use
+    f4 uv[NSUB][2];
 #pragma unroll
-      for (int j = 0; j < TILE; ++j) {
-        Xl[r][j] = X[j];
-        p.slots[sb + ((long long)ch * kw + r) * vw + c0 + j] = X[j];
+    for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) uv[h][t2][e] = p.U[(tb + t2 * 16 + 4 * g + e) * vw + c0 + h * 16 + m];
+    float gv[WRB][4];
+#pragma unroll
+    for (int q = 0; q < WRB; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rb = w + 4 * q;
+        gv[q][e] = rb < nrb ? p.Gam[((long long)s * p.NT + ch) * kw + rb * 16 + 4 * g + e] : 0.f;
       }
-    }
-    for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
-      const int i = idx / kw, c = idx % kw;
-      Wl[i][c] = p.W[(tb + i) * kw + c];
-    }
-    if (p.Ib) {
-      for (int idx = threadIdx.x; idx < WBT * TILE; idx += WT) {
-        const int i = idx / TILE, j = idx % TILE;
-        Il[i][j] = p.Ib[(tb + i) * vw + c0 + j];
-      }
+#pragma unroll
+    for (int q = 0; q < WRB; ++q) {  // slot[ch] = X0
+      const int rb = w + 4 * q;
+      if (rb < nrb)
+#pragma unroll
+        for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            p.slots[sb + ((long long)ch * kw + rb * 16 + 4 * g + e) * vw + c0 + h * 16 + m] = X[q][h][e];
     }
     __syncthreads();
+    // the next chunk's panels load while this one computes (clamped at the end)
     {
-      const int i = threadIdx.x >> 4, j = threadIdx.x & 15;
-      float a0 = p.U[(tb + i) * vw + c0 + j], a1 = p.U[(tb + i + 16) * vw + c0 + j];
-      for (int rr = 0; rr < kw; ++rr) {
-        const float xv = Xl[rr][j];
-        a0 -= Wl[i][rr] * xv;
-        a1 -= Wl[i + 16][rr] * xv;
-      }
-      wl[i][j] = a0;
-      wl[i + 16][j] = a1;
-      p.wout[(tb + i) * vw + c0 + j] = a0;
-      p.wout[(tb + i + 16) * vw + c0 + j] = a1;
+      const int nx = step + 1 < p.NT ? step + 1 : step;
+      panel_load(nW, p.W + tok0(nx) * kw, kw);
+      panel_load(nK, p.K + tok0(nx) * kw, kw);
+      if (inj) panel_load(nA, p.Ia + tok0(nx) * kw, kw);
     }
-    __syncthreads();
-    if (r < kw) {
-      const float g = p.Gam[((long long)s * p.NT + ch) * kw + r];
+    // partial w = W X0 over this wave's row blocks
+    f4 pw[NSUB][2];
 #pragma unroll
-      for (int j = 0; j < TILE; ++j) X[j] *= g;
-      for (int i = 0; i < WBT; ++i) {
-        const float kv = p.K[(tb + i) * kw + r];
+    for (int h = 0; h < NSUB; ++h) pw[h][0] = pw[h][1] = zero4();
 #pragma unroll
-        for (int j = 0; j < TILE; ++j) X[j] += kv * wl[i][j];
-      }
-      if (p.Ia) {
-        for (int i = 0; i < WBT; ++i) {
-          const float av = p.Ia[(tb + i) * kw + r];
+    for (int q = 0; q < WRB; ++q) {
+      const int rb = w + 4 * q;
+      if (rb < nrb) {
 #pragma unroll
-          for (int j = 0; j < TILE; ++j) X[j] += av * Il[i][j];
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const float4 a = *reinterpret_cast<const float4*>(Wl + (t2 * 16 + m) * ldw + rb * 16 + 4 * g);
+#pragma unroll
+          for (int h = 0; h < NSUB; ++h) {
+            pw[h][t2] = mfma4(a.x, X[q][h][0], pw[h][t2]);
+            pw[h][t2] = mfma4(a.y, X[q][h][1], pw[h][t2]);
+            pw[h][t2] = mfma4(a.z, X[q][h][2], pw[h][t2]);
+            pw[h][t2] = mfma4(a.w, X[q][h][3], pw[h][t2]);
+          }
         }
       }
     }
+#pragma unroll
+    for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[(((w * NSUB + h) * 2 + t2) * 4 + e) * 64 + l] = pw[h][t2][e];
     __syncthreads();
+    f4 wv[NSUB][2];
+#pragma unroll
+    for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float a = uv[h][t2][e];
+#pragma unroll
+          for (int w2 = 0; w2 < 4; ++w2) a -= red[(((w2 * NSUB + h) * 2 + t2) * 4 + e) * 64 + l];
+          wv[h][t2][e] = a;
+        }
+    if (w == 0)
+#pragma unroll
+      for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            p.wout[(tb + t2 * 16 + 4 * g + e) * vw + c0 + h * 16 + m] = wv[h][t2][e];
+    // X = Gamma X + K^T w (+ A^T B)
+#pragma unroll
+    for (int q = 0; q < WRB; ++q) {
+      const int rb = w + 4 * q;
+      if (rb < nrb) {
+#pragma unroll
+        for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) X[q][h][e] *= gv[q][e];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const float4 kk = *reinterpret_cast<const float4*>(Kt + (rb * 16 + m) * LDT + t2 * 16 + 4 * g);
+#pragma unroll
+          for (int h = 0; h < NSUB; ++h) {
+            X[q][h] = mfma4(kk.x, wv[h][t2][0], X[q][h]);
+            X[q][h] = mfma4(kk.y, wv[h][t2][1], X[q][h]);
+            X[q][h] = mfma4(kk.z, wv[h][t2][2], X[q][h]);
+            X[q][h] = mfma4(kk.w, wv[h][t2][3], X[q][h]);
+          }
+          if (inj) {
+            const float4 aa = *reinterpret_cast<const float4*>(At + (rb * 16 + m) * LDT + t2 * 16 + 4 * g);
+#pragma unroll
+            for (int h = 0; h < NSUB; ++h) {
+              const float4 bb = *reinterpret_cast<const float4*>(Bt + (h * 16 + m) * LDT + t2 * 16 + 4 * g);
+              X[q][h] = mfma4(aa.x, bb.x, X[q][h]);
+              X[q][h] = mfma4(aa.y, bb.y, X[q][h]);
+              X[q][h] = mfma4(aa.z, bb.z, X[q][h]);
+              X[q][h] = mfma4(aa.w, bb.w, X[q][h]);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next step restages the panels
   }
-  if (r < kw) {
-    if (!p.rev) {
 #pragma unroll
-      for (int j = 0; j < TILE; ++j)
-        p.slots[sb + ((long long)p.NT * kw + r) * vw + c0 + j] = X[j];
-    }
-    if (p.fin && r < p.rows) {
+  for (int q = 0; q < WRB; ++q) {
+    const int rb = w + 4 * q;
+    if (rb >= nrb) continue;
 #pragma unroll
-      for (int j = 0; j < TILE; ++j) {
-        const int c = c0 + j;
-        if (c < p.cols) {
-          if (p.fin_t) p.fin[((long long)s * p.cols + c) * p.rows + r] = X[j];
-          else p.fin[((long long)s * p.rows + r) * p.cols + c] = X[j];
+    for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = rb * 16 + 4 * g + e, col = c0 + h * 16 + m;
+        if (!p.rev) p.slots[sb + ((long long)p.NT * kw + row) * vw + col] = X[q][h][e];
+        if (p.fin && row < p.rows && col < p.cols) {
+          if (p.fin_t) p.fin[((long long)s * p.cols + col) * p.rows + row] = X[q][h][e];
+          else p.fin[((long long)s * p.rows + row) * p.cols + col] = X[q][h][e];
         }
+      }
+  }
+}
+
+// acc[i] += sum_r A[i][r] X[r][c] over r < kw for this thread's value column
+// c = threadIdx.x (< vw): X [kw][vw] (global) is staged through LDS in 32-row
+// blocks with 16-byte loads; A [32][lda] is in LDS.  Every thread of the
+// workgroup must call it (it synchronises).
+__device__ __forceinline__ void rows_times_x(const float* A, int lda, const float* X, int kw,
+                                             int vw, float* buf, float (&acc)[WBT]) {
+  const int c = threadIdx.x, lb = vw + 4;
+  for (int rb = 0; rb < kw; rb += 32) {
+    __syncthreads();
+    for (int q = threadIdx.x; q < 32 * vw / 4; q += WT) {
+      const int i = (q * 4) / vw, cc = (q * 4) % vw;
+      *reinterpret_cast<float4*>(buf + i * lb + cc) =
+          *reinterpret_cast<const float4*>(X + (long long)(rb + i) * vw + cc);
+    }
+    __syncthreads();
+    if (c < vw) {
+#pragma unroll 4
+      for (int k = 0; k < 32; ++k) {
+        const float x = buf[k * lb + c];
+#pragma unroll
+        for (int i = 0; i < WBT; ++i) acc[i] += A[i * lda + rb + k] * x;
       }
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// Chunk readout.
-//   column output: o = Qt X0 + P w                       -> bf16 out [B,T,H,V]
-//   row output:    o_ir = e^{G_ir} (q X0^T)_ir + sum_{j<=i} (q_i.w_j) k_jr e^{G_ir - G_jr}
-//                  -> o panel and d = base + o
-// ---------------------------------------------------------------------------
 struct OutParams {
   int NT, Tp, kw, vw, colout, H, T, V;
   const float *slots, *w, *Qt, *P, *q, *k, *G, *base;
@@ -359,21 +531,17 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
     const int ld = kw + 1;
     float* Ql = sm;                 // [32][kw+1]
     float* Pl = Ql + WBT * ld;      // [32][33]
+    float* Xb = Pl + WBT * MS;      // X0 row block [32][vw+4]
     for (int idx = threadIdx.x; idx < WBT * kw; idx += WT)
       Ql[(idx / kw) * ld + idx % kw] = p.Qt[(tb + idx / kw) * kw + idx % kw];
     const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
     for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) Pl[(idx >> 5) * MS + (idx & 31)] = p.P[mb + idx];
-    __syncthreads();
-    const int c = threadIdx.x;
-    if (c >= vw) return;
     float acc[WBT];
 #pragma unroll
     for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
-    for (int rr = 0; rr < kw; ++rr) {
-      const float xv = X0[(long long)rr * vw + c];
-#pragma unroll
-      for (int i = 0; i < WBT; ++i) acc[i] += Ql[i * ld + rr] * xv;
-    }
+    rows_times_x(Ql, ld, X0, kw, vw, Xb, acc);  // Q~ X0 (synchronises first)
+    const int c = threadIdx.x;
+    if (c >= vw) return;
     float wc[WBT];
 #pragma unroll
     for (int j = 0; j < WBT; ++j) wc[j] = p.w[(tb + j) * vw + c];
@@ -447,7 +615,7 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
 }
 
 constexpr size_t out_smem(int kw, int vw, int colout) {
-  if (colout) return (size_t)(WBT * (kw + 1) + WBT * MS) * sizeof(float);
+  if (colout) return (size_t)(WBT * (kw + 1) + WBT * MS + WBT * (vw + 4)) * sizeof(float);
   return (size_t)(2 * WBT * (vw + 1) + WBT * MS + WMAX * MS) * sizeof(float);
 }
 
@@ -726,16 +894,12 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
     const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
     for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) Ppl[(idx >> 5) * MS + (idx & 31)] = p.Pp[mb + idx];
     __syncthreads();
+    float acc[WBT];
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
+    rows_times_x(dOe, ld, X0, kw, vw, Ppl + WBT * MS, acc);  // (dO e^G) X0
     const int c = threadIdx.x;
     if (c < vw) {
-      float acc[WBT];
-#pragma unroll
-      for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
-      for (int rr = 0; rr < kw; ++rr) {
-        const float xv = X0[(long long)rr * vw + c];
-#pragma unroll
-        for (int i = 0; i < WBT; ++i) acc[i] += dOe[i * ld + rr] * xv;
-      }
       float wc[WBT];
 #pragma unroll
       for (int j = 0; j < WBT; ++j) wc[j] = p.w[(tb + j) * vw + c];
@@ -814,7 +978,7 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
 constexpr size_t grad_smem(int kw) {
   const size_t ph1 = 5 * WBT * MS + 3 * WMAX * MS;
   const size_t ph3 = 5 * WBT * MS + 4 * WBT * (size_t)kw;
-  const size_t ph2 = 5 * WBT * MS + WBT * (kw + 1) + WBT * MS;
+  const size_t ph2 = 5 * WBT * MS + WBT * (kw + 1) + WBT * MS + WBT * (size_t)(WMAX + 4);
   return (ph1 > ph3 ? (ph1 > ph2 ? ph1 : ph2) : (ph3 > ph2 ? ph3 : ph2)) * sizeof(float);
 }
 
@@ -1082,7 +1246,7 @@ WideBwd carve_wide_bwd(void* base, const WideDims& d, size_t* total) {
 }
 
 constexpr size_t kMaxLds = 160 * 1024;  // LDS of one gfx950 CU
-static_assert(prep_smem(WMAX) <= kMaxLds && out_smem(WMAX, WMAX, 0) <= kMaxLds &&
+static_assert(prep_smem(WMAX) <= kMaxLds && state_smem(WMAX, true) <= kMaxLds && out_smem(WMAX, WMAX, 0) <= kMaxLds &&
                   out_smem(WMAX, WMAX, 1) <= kMaxLds && bprep_smem(WMAX) <= kMaxLds &&
                   grad_smem(WMAX) <= kMaxLds,
               "a wide kernel's LDS exceeds the CU");
@@ -1094,7 +1258,9 @@ void launch_wprep(const OpParams& op, int n, hipStream_t st) {
 }
 
 void launch_wstate(const char* name, const WStateParams& sp, int n, hipStream_t st) {
-  SD_LAUNCH(name, k_w_state, dim3(sp.vw / TILE, n), dim3(WT), 0, st, sp);
+  SD_SMEM_ONCE(k_w_state, (int)state_smem(WMAX, true));
+  SD_LAUNCH(name, k_w_state, dim3(sp.vw / STILE, n), dim3(WT), state_smem(sp.kw, sp.Ia != nullptr),
+            st, sp);
 }
 
 }  // namespace
