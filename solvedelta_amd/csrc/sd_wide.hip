@@ -802,114 +802,147 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
   const float* X0 = p.Xslots + slot * kw * vw;
   const float* XC = X0 + (long long)kw * vw;
   const float* Lm = p.Lslots + slot * kw * vw;
-  // phase 1: column blocks of 32 value columns
-  float* dwb = sm;               // [32][33] each
-  float* wb = dwb + WBT * MS;
-  float* yb = wb + WBT * MS;
-  float* M1 = yb + WBT * MS;
+  // LDS: M1, M2 [32][33], then phase 3's panels
+  float* M1 = sm;
   float* M2 = M1 + WBT * MS;
-  float* X0b = M2 + WBT * MS;    // [256][33] each
-  float* Lb = X0b + WMAX * MS;
-  float* XCb = Lb + WMAX * MS;
+  float* X0b = M2 + WBT * MS;
   const int r = threadIdx.x;
-  float dwX[WBT], wL[WBT], dOX[WBT];
-#pragma unroll
-  for (int i = 0; i < WBT; ++i) dwX[i] = wL[i] = dOX[i] = 0.f;
-  float rsum = 0.f;
-  float m1[4] = {0.f, 0.f, 0.f, 0.f}, m2[4] = {0.f, 0.f, 0.f, 0.f};
+  const int wv_ = r >> 6, l = r & 63, g = l >> 4, m = l & 15;
+  const int nrb = kw / 16, nvb = vw / 16;
   const float* Y = p.colout ? p.dO : p.q;  // [Tp][vw]
-  for (int cb = 0; cb < vw; cb += 32) {
-    for (int idx = threadIdx.x; idx < WBT * 32; idx += WT) {
-      const int i = idx >> 5, cc = idx & 31;
-      const long long o = (tb + i) * vw + cb + cc;
-      dwb[i * MS + cc] = p.dw[o];
-      wb[i * MS + cc] = p.w[o];
-      yb[i * MS + cc] = Y[o];
-    }
-    for (int idx = threadIdx.x; idx < kw * 32; idx += WT) {
-      const int rr = idx >> 5, cc = idx & 31;
-      const long long o = (long long)rr * vw + cb + cc;
-      X0b[rr * MS + cc] = X0[o];
-      Lb[rr * MS + cc] = Lm[o];
-      XCb[rr * MS + cc] = XC[o];
-    }
-    __syncthreads();
+  // phase 1 on FP32 matrix cores (sum index c = 16 cb + 4 g + e: MFMA e, lane
+  // group g): the row products dwX = dw X0^T, wL = w lam^T, dOX = dO X0^T
+  // (column output) over this wave's 16-row blocks of the state, and the token
+  // Grams M1 = dw w^T, M2 = Y w^T (one 16 x 16 block of each per wave), all
+  // from 16-byte global loads of the rows involved.
+  {
+    f4 aX[WRB][2], aL[WRB][2], aO[WRB][2];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      int i, j;
-      entry(m, i, j);
-      float a1 = 0.f, a2 = 0.f;
-#pragma unroll 4
-      for (int cc = 0; cc < 32; ++cc) {
-        const float wj = wb[j * MS + cc];
-        a1 += dwb[i * MS + cc] * wj;
-        a2 += yb[i * MS + cc] * wj;
+    for (int q = 0; q < WRB; ++q)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) aX[q][t2] = aL[q][t2] = aO[q][t2] = zero4();
+    f4 m1a = zero4(), m2a = zero4();
+    const int bi = wv_ >> 1, bj = wv_ & 1;
+    for (int cb = 0; cb < vw; cb += 16) {
+      float4 adw[2], aw[2], ay[2];
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const long long o = (tb + t2 * 16 + m) * vw + cb + 4 * g;
+        adw[t2] = *reinterpret_cast<const float4*>(p.dw + o);
+        aw[t2] = *reinterpret_cast<const float4*>(p.w + o);
+        ay[t2] = *reinterpret_cast<const float4*>(Y + o);
       }
-      m1[m] += a1;
-      m2[m] += a2;
-    }
-    if (r < kw) {
-#pragma unroll 1
-      for (int cc = 0; cc < 32; ++cc) {
-        const float xv = X0b[r * MS + cc], lv = Lb[r * MS + cc];
-        rsum += XCb[r * MS + cc] * lv;
 #pragma unroll
-        for (int i = 0; i < WBT; ++i) {
-          dwX[i] += dwb[i * MS + cc] * xv;
-          wL[i] += wb[i * MS + cc] * lv;
-          dOX[i] += yb[i * MS + cc] * xv;  // dO X0^T (column output only)
+      for (int q = 0; q < WRB; ++q) {
+        const int rb = wv_ + 4 * q;
+        if (rb < nrb) {
+          const long long o = (long long)(rb * 16 + m) * vw + cb + 4 * g;
+          const float4 bx = *reinterpret_cast<const float4*>(X0 + o);
+          const float4 bl = *reinterpret_cast<const float4*>(Lm + o);
+#pragma unroll
+          for (int t2 = 0; t2 < 2; ++t2) {
+            aX[q][t2] = mfma4(adw[t2].x, bx.x, aX[q][t2]);
+            aX[q][t2] = mfma4(adw[t2].y, bx.y, aX[q][t2]);
+            aX[q][t2] = mfma4(adw[t2].z, bx.z, aX[q][t2]);
+            aX[q][t2] = mfma4(adw[t2].w, bx.w, aX[q][t2]);
+            aL[q][t2] = mfma4(aw[t2].x, bl.x, aL[q][t2]);
+            aL[q][t2] = mfma4(aw[t2].y, bl.y, aL[q][t2]);
+            aL[q][t2] = mfma4(aw[t2].z, bl.z, aL[q][t2]);
+            aL[q][t2] = mfma4(aw[t2].w, bl.w, aL[q][t2]);
+            if (p.colout) {
+              aO[q][t2] = mfma4(ay[t2].x, bx.x, aO[q][t2]);
+              aO[q][t2] = mfma4(ay[t2].y, bx.y, aO[q][t2]);
+              aO[q][t2] = mfma4(ay[t2].z, bx.z, aO[q][t2]);
+              aO[q][t2] = mfma4(ay[t2].w, bx.w, aO[q][t2]);
+            }
+          }
         }
       }
+      m1a = mfma4(adw[bi].x, aw[bj].x, m1a);
+      m1a = mfma4(adw[bi].y, aw[bj].y, m1a);
+      m1a = mfma4(adw[bi].z, aw[bj].z, m1a);
+      m1a = mfma4(adw[bi].w, aw[bj].w, m1a);
+      m2a = mfma4(ay[bi].x, aw[bj].x, m2a);
+      m2a = mfma4(ay[bi].y, aw[bj].y, m2a);
+      m2a = mfma4(ay[bi].z, aw[bj].z, m2a);
+      m2a = mfma4(ay[bi].w, aw[bj].w, m2a);
     }
-    __syncthreads();
+    // the row products go to the output panels, which phase 3 reads back per
+    // key coordinate and overwrites
+#pragma unroll
+    for (int q = 0; q < WRB; ++q) {
+      const int rb = wv_ + 4 * q;
+      if (rb < nrb)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const long long o = (tb + t2 * 16 + 4 * g + e) * kw + rb * 16 + m;
+            p.dx[o] = aX[q][t2][e];
+            p.dk[o] = aL[q][t2][e];
+            if (p.colout) p.dq[o] = aO[q][t2][e];
+          }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = bi * 16 + 4 * g + e, j = bj * 16 + m;
+      M1[i * MS + j] = j < i ? m1a[e] : 0.f;
+      M2[i * MS + j] = j <= i ? m2a[e] : 0.f;
+    }
   }
-  // the phase-1 row products go to this thread's own output columns, which
-  // phase 3 reads back and overwrites (no register arrays live across phases)
+  // rowsum(X_C (.) lam) for this thread's key coordinate
+  float rsum = 0.f;
   if (r < kw) {
-#pragma unroll
-    for (int i = 0; i < WBT; ++i) {
-      const long long o = (tb + i) * kw + r;
-      p.dx[o] = dwX[i];
-      p.dk[o] = wL[i];
-      if (p.colout) p.dq[o] = dOX[i];
+    const float* xr = XC + (long long)r * vw;
+    const float* lr = Lm + (long long)r * vw;
+    for (int c = 0; c < vw; c += 4) {
+      const float4 a4 = *reinterpret_cast<const float4*>(xr + c);
+      const float4 b4 = *reinterpret_cast<const float4*>(lr + c);
+      rsum += a4.x * b4.x + a4.y * b4.y + a4.z * b4.z + a4.w * b4.w;
     }
   }
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    int i, j;
-    entry(m, i, j);
-    M1[i * MS + j] = j < i ? m1[m] : 0.f;
-    M2[i * MS + j] = j <= i ? m2[m] : 0.f;
-  }
-  // phase 2 (row output): dq = (dO e^G) X0 + Pp w, one value column per thread
-  float* dOe = X0b;  // [32][kw+1]
-  float* Ppl = dOe + WBT * (kw + 1);
+  // phase 2 (row output): dq = (dO e^G) X0 + Pp w on matrix cores, this wave's
+  // 16-column blocks of the value axis
   if (!p.colout) {
-    const int ld = kw + 1;
-    for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
-      const int i = idx / kw, c = idx % kw;
-      const long long o = (tb + i) * kw + c;
-      dOe[i * ld + c] = p.dO[o] * __expf(p.G[o]);
-    }
     const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
-    for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) Ppl[(idx >> 5) * MS + (idx & 31)] = p.Pp[mb + idx];
-    __syncthreads();
-    float acc[WBT];
 #pragma unroll
-    for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
-    rows_times_x(dOe, ld, X0, kw, vw, Ppl + WBT * MS, acc);  // (dO e^G) X0
-    const int c = threadIdx.x;
-    if (c < vw) {
-      float wc[WBT];
+    for (int q = 0; q < WRB; ++q) {
+      const int nb = wv_ + 4 * q;
+      if (nb >= nvb) continue;
+      f4 acc[2] = {zero4(), zero4()};
+      for (int rb = 0; rb < nrb; ++rb) {
+        float bx[4];
 #pragma unroll
-      for (int j = 0; j < WBT; ++j) wc[j] = p.w[(tb + j) * vw + c];
+        for (int e = 0; e < 4; ++e) bx[e] = X0[(long long)(rb * 16 + 4 * g + e) * vw + nb * 16 + m];
 #pragma unroll
-      for (int i = 0; i < WBT; ++i) {
-        float a = acc[i];
-#pragma unroll
-        for (int j = 0; j <= i; ++j) a += Ppl[i * MS + j] * wc[j];
-        p.dq[(tb + i) * vw + c] = a;
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const long long o = (tb + t2 * 16 + m) * kw + rb * 16 + 4 * g;
+          const float4 d4 = *reinterpret_cast<const float4*>(p.dO + o);
+          const float4 g4 = *reinterpret_cast<const float4*>(p.G + o);
+          acc[t2] = mfma4(d4.x * __expf(g4.x), bx[0], acc[t2]);
+          acc[t2] = mfma4(d4.y * __expf(g4.y), bx[1], acc[t2]);
+          acc[t2] = mfma4(d4.z * __expf(g4.z), bx[2], acc[t2]);
+          acc[t2] = mfma4(d4.w * __expf(g4.w), bx[3], acc[t2]);
+        }
       }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        float bw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bw[e] = p.w[(tb + kb * 16 + 4 * g + e) * vw + nb * 16 + m];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const float4 a4 = *reinterpret_cast<const float4*>(p.Pp + mb + (t2 * 16 + m) * WBT + kb * 16 + 4 * g);
+          acc[t2] = mfma4(a4.x, bw[0], acc[t2]);
+          acc[t2] = mfma4(a4.y, bw[1], acc[t2]);
+          acc[t2] = mfma4(a4.z, bw[2], acc[t2]);
+          acc[t2] = mfma4(a4.w, bw[3], acc[t2]);
+        }
+      }
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p.dq[(tb + t2 * 16 + 4 * g + e) * vw + nb * 16 + m] = acc[t2][e];
     }
   }
   __syncthreads();
@@ -975,12 +1008,7 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
   }
 }
 
-constexpr size_t grad_smem(int kw) {
-  const size_t ph1 = 5 * WBT * MS + 3 * WMAX * MS;
-  const size_t ph3 = 5 * WBT * MS + 4 * WBT * (size_t)kw;
-  const size_t ph2 = 5 * WBT * MS + WBT * (kw + 1) + WBT * MS + WBT * (size_t)(WMAX + 4);
-  return (ph1 > ph3 ? (ph1 > ph2 ? ph1 : ph2) : (ph3 > ph2 ? ph3 : ph2)) * sizeof(float);
-}
+constexpr size_t grad_smem(int kw) { return (2 * WBT * MS + 4 * WBT * (size_t)kw) * sizeof(float); }
 
 // ---------------------------------------------------------------------------
 // Source closure (per token): cotangents of e, chi, z back to u^, delta, k^, q^,
