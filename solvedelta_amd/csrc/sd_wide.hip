@@ -138,6 +138,57 @@ __device__ __forceinline__ void entry(int m, int& i, int& j) {
   j = e & 31;
 }
 
+// Decay factors of the matrix-core Grams and applies are factored per
+// coordinate c as exp(Ga_i) * exp(-Gb_j), both prefixes inside the chunk.  That
+// is exact up to rounding while the coordinate's decay over the chunk,
+// -G_{31,c}, stays at most WILD (exp(WILD) is far inside FP32); "wild"
+// coordinates beyond it are left out of the factored product and their terms
+// added exactly.
+constexpr float WILD = 60.f;
+
+// The chunk's wild coordinates in increasing order (deterministic: wave
+// ballots and a prefix over the four waves), from the last row of the in-chunk
+// prefix G (row stride ld).  Every thread must call it; returns the count.
+__device__ __forceinline__ int wild_list(const float* Gs, int ld, int kw, int* wl, int* cnt) {
+  const int c = threadIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const bool f = c < kw && -Gs[(WBT - 1) * ld + c] > WILD;
+  const unsigned long long mask = __ballot(f);
+  if (l == 0) cnt[w] = __popcll(mask);
+  __syncthreads();
+  int off = 0;
+  for (int v = 0; v < w; ++v) off += cnt[v];
+  if (f) wl[off + __popcll(mask & ((1ull << l) - 1ull))] = c;
+  const int total = cnt[0] + cnt[1] + cnt[2] + cnt[3];
+  __syncthreads();
+  return total;
+}
+
+// M[i][j] = sum_c A(i, c) B(j, c) exp(Ga(i, c) - Gb(j, c)) for i, j < 32, kept
+// where keep(i, j), on FP32 matrix cores: wave w forms the 16 x 16 block
+// (w >> 1, w & 1) from fa(i, c) = A e^{Ga} and fb(j, c) = B e^{-Gb} (zero on
+// wild coordinates), then adds the wild coordinates' exact terms fx(i, j, c).
+template <class FA, class FB, class FX, class KEEP>
+__device__ __forceinline__ void gram_mfma(int kw, const int* wl, int nw, FA fa, FB fb, FX fx,
+                                          KEEP keep, float* M) {
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
+  const int bi = w >> 1, bj = w & 1;
+  f4 acc = zero4();
+  for (int kb = 0; kb < kw; kb += 16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = kb + 4 * g + e;
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa(bi * 16 + m, c), fb(bj * 16 + m, c), acc, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int i = bi * 16 + 4 * g + e, j = bj * 16 + m;
+    float v = acc[e];
+    for (int t = 0; t < nw; ++t) v += fx(i, j, wl[t]);
+    M[i * MS + j] = keep(i, j) ? v : 0.f;
+  }
+}
+
 __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
   extern __shared__ __align__(16) float sm[];
   const int ch = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw, ld = kw + 1;
@@ -158,21 +209,24 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
   }
   __syncthreads();
   // L_ij = sum_c x_ic k_jc e^{Gx_ic - G_jc} (j < i); P_ij = sum_c q_ic k_jc e^{G_ic - G_jc} (j <= i)
-  for (int m = 0; m < WBT * WBT / WT; ++m) {
-    int i, j;
-    entry(m, i, j);
-    float l = 0.f, pp = 0.f;
-    if (j < i) {
-      for (int c = 0; c < kw; ++c)
-        l += xs[i * ld + c] * ks[j * ld + c] * __expf(gx_at(Gs, ld, i, c, p.excl) - Gs[j * ld + c]);
-    }
-    if (p.colout && j <= i) {
-      for (int c = 0; c < kw; ++c)
-        pp += qs[i * ld + c] * ks[j * ld + c] * __expf(Gs[i * ld + c] - Gs[j * ld + c]);
-    }
-    Ls[i * MS + j] = l;
-    Ps[i * MS + j] = pp;
-  }
+  int* wl = reinterpret_cast<int*>(Ps + WBT * MS);
+  const int nw = wild_list(Gs, ld, kw, wl, wl + WMAX);
+  auto wild = [&](int c) { return -Gs[(WBT - 1) * ld + c] > WILD; };
+  auto kb = [&](int j, int c) { return wild(c) ? 0.f : ks[j * ld + c] * __expf(-Gs[j * ld + c]); };
+  gram_mfma(
+      kw, wl, nw,
+      [&](int i, int c) { return xs[i * ld + c] * __expf(gx_at(Gs, ld, i, c, p.excl)); }, kb,
+      [&](int i, int j, int c) {
+        return xs[i * ld + c] * ks[j * ld + c] * __expf(gx_at(Gs, ld, i, c, p.excl) - Gs[j * ld + c]);
+      },
+      [](int i, int j) { return j < i; }, Ls);
+  if (p.colout)
+    gram_mfma(
+        kw, wl, nw, [&](int i, int c) { return qs[i * ld + c] * __expf(Gs[i * ld + c]); }, kb,
+        [&](int i, int j, int c) {
+          return qs[i * ld + c] * ks[j * ld + c] * __expf(Gs[i * ld + c] - Gs[j * ld + c]);
+        },
+        [](int i, int j) { return j <= i; }, Ps);
   __syncthreads();
   // A = (I + L)^-1, one column per thread: a_i = [i == j] - sum_{m < i} L_im a_m
   float acol[WBT];
@@ -231,7 +285,9 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
   }
 }
 
-constexpr size_t prep_smem(int kw) { return (size_t)(4 * WBT * (kw + 1) + 2 * WBT * MS) * sizeof(float); }
+constexpr size_t prep_smem(int kw) {
+  return (size_t)(4 * WBT * (kw + 1) + 2 * WBT * MS + WMAX + 4) * sizeof(float);  // + wild list
+}
 
 // ---------------------------------------------------------------------------
 // Sequential chunk pass over a 16-column tile of X [kw x vw]:
@@ -802,27 +858,28 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
   const float* X0 = p.Xslots + slot * kw * vw;
   const float* XC = X0 + (long long)kw * vw;
   const float* Lm = p.Lslots + slot * kw * vw;
-  // LDS: M1, M2 [32][33], then phase 3's panels
+  // LDS: the token Grams M1, M2 [32][33]
   float* M1 = sm;
   float* M2 = M1 + WBT * MS;
-  float* X0b = M2 + WBT * MS;
   const int r = threadIdx.x;
   const int wv_ = r >> 6, l = r & 63, g = l >> 4, m = l & 15;
   const int nrb = kw / 16, nvb = vw / 16;
   const float* Y = p.colout ? p.dO : p.q;  // [Tp][vw]
   // phase 1 on FP32 matrix cores (sum index c = 16 cb + 4 g + e: MFMA e, lane
   // group g): the row products dwX = dw X0^T, wL = w lam^T, dOX = dO X0^T
-  // (column output) over this wave's 16-row blocks of the state, and the token
-  // Grams M1 = dw w^T, M2 = Y w^T (one 16 x 16 block of each per wave), all
-  // from 16-byte global loads of the rows involved.
+  // (column output) over this wave's 16-row blocks of the state, kept in
+  // accumulators (lane (g, n): tokens 4g..4g+3 of state row 16 rb + n) for
+  // phase 3, and the token Grams M1 = dw w^T, M2 = Y w^T (one 16 x 16 block of
+  // each per wave), all from 16-byte global loads of the rows involved.
+  f4 aX[WRB][2], aL[WRB][2], aO[WRB][2];
+#pragma unroll
+  for (int q = 0; q < WRB; ++q)
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) aX[q][t2] = aL[q][t2] = aO[q][t2] = zero4();
   {
-    f4 aX[WRB][2], aL[WRB][2], aO[WRB][2];
-#pragma unroll
-    for (int q = 0; q < WRB; ++q)
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) aX[q][t2] = aL[q][t2] = aO[q][t2] = zero4();
     f4 m1a = zero4(), m2a = zero4();
     const int bi = wv_ >> 1, bj = wv_ & 1;
+#pragma unroll 2
     for (int cb = 0; cb < vw; cb += 16) {
       float4 adw[2], aw[2], ay[2];
 #pragma unroll
@@ -867,22 +924,6 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
       m2a = mfma4(ay[bi].z, aw[bj].z, m2a);
       m2a = mfma4(ay[bi].w, aw[bj].w, m2a);
     }
-    // the row products go to the output panels, which phase 3 reads back per
-    // key coordinate and overwrites
-#pragma unroll
-    for (int q = 0; q < WRB; ++q) {
-      const int rb = wv_ + 4 * q;
-      if (rb < nrb)
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const long long o = (tb + t2 * 16 + 4 * g + e) * kw + rb * 16 + m;
-            p.dx[o] = aX[q][t2][e];
-            p.dk[o] = aL[q][t2][e];
-            if (p.colout) p.dq[o] = aO[q][t2][e];
-          }
-    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = bi * 16 + 4 * g + e, j = bj * 16 + m;
@@ -895,6 +936,7 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
   if (r < kw) {
     const float* xr = XC + (long long)r * vw;
     const float* lr = Lm + (long long)r * vw;
+#pragma unroll 8
     for (int c = 0; c < vw; c += 4) {
       const float4 a4 = *reinterpret_cast<const float4*>(xr + c);
       const float4 b4 = *reinterpret_cast<const float4*>(lr + c);
@@ -945,70 +987,106 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
         for (int e = 0; e < 4; ++e) p.dq[(tb + t2 * 16 + 4 * g + e) * vw + nb * 16 + m] = acc[t2][e];
     }
   }
-  __syncthreads();
-  // phase 3: key-side gradients, one key coordinate per thread, its chunk
-  // columns staged in LDS [32][kw]
-  float* kL = X0b;
-  float* xL = kL + WBT * kw;
-  float* GL = xL + WBT * kw;
-  float* YL = GL + WBT * kw;
+  __syncthreads();  // M1, M2 complete
+  // phase 3: the in-chunk applies on matrix cores, decay factored per state
+  // row r as e^{Ga_i} e^{-Gb_j} (exact while r's decay over the chunk is at
+  // most WILD; wild rows take the exact per-term sums):
+  //   dx = -e^{Gx} (dwX + M1 k~),               k~_jr = k_jr e^{-G_jr}
+  //   dk = e^{-G} (e^{G_C} wL + M2^T Y~ - M1^T x~),  Y~ = Yk e^{G}, x~ = x e^{Gx}
+  //   dq = e^{G} (dOX + M2 k~)                   (column output)
   const float* Yk = p.colout ? p.q : p.dO;  // [Tp][kw]
-  for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
-    const int i = idx / kw, c = idx % kw;
-    const long long o = (tb + i) * kw + c;
-    kL[idx] = p.k[o];
-    xL[idx] = p.x[o];
-    GL[idx] = p.G[o];
-    YL[idx] = Yk[o];
-  }
-  __syncthreads();
-  if (r >= kw) return;
-  auto Gx = [&](int i) { return p.excl ? (i > 0 ? GL[(i - 1) * kw + r] : 0.f) : GL[i * kw + r]; };
-  const float gl = GL[(WBT - 1) * kw + r];
-  // dx = -(e^{Gx} (dw X0^T) + apply(M1, k, Gx, G))
-  for (int i = 0; i < WBT; ++i) {
-    const long long o = (tb + i) * kw + r;
-    const float gxi = Gx(i);
-    float a = __expf(gxi) * p.dx[o];
-    for (int j = 0; j < i; ++j) a += M1[i * MS + j] * kL[j * kw + r] * __expf(gxi - GL[j * kw + r]);
-    p.dx[o] = -a;
-  }
-  // dk = e^{G_C - G} (w lam^T) + apply_t(M2, Yk, G, G) - apply_t(M1, x, Gx, G)
-  for (int j = 0; j < WBT; ++j) {
-    const long long o = (tb + j) * kw + r;
-    const float gj = GL[j * kw + r];
-    float a = __expf(gl - gj) * p.dk[o];
-    for (int l = j; l < WBT; ++l) a += M2[l * MS + j] * YL[l * kw + r] * __expf(GL[l * kw + r] - gj);
-    for (int i = j + 1; i < WBT; ++i) a -= M1[i * MS + j] * xL[i * kw + r] * __expf(Gx(i) - gj);
-    p.dk[o] = a;
-  }
-  if (p.colout) {
-    // dq = e^G (dO X0^T) + apply(M2, k, G, G)
-    for (int i = 0; i < WBT; ++i) {
-      const long long o = (tb + i) * kw + r;
-      const float gi = GL[i * kw + r];
-      float a = __expf(gi) * p.dq[o];
-      for (int j = 0; j <= i; ++j) a += M2[i * MS + j] * kL[j * kw + r] * __expf(gi - GL[j * kw + r]);
-      p.dq[o] = a;
+  auto gx_g = [&](int i, int rr) {
+    return p.excl ? (i > 0 ? p.G[(tb + i - 1) * kw + rr] : 0.f) : p.G[(tb + i) * kw + rr];
+  };
+#pragma unroll
+  for (int q = 0; q < WRB; ++q) {
+    const int rb = wv_ + 4 * q;
+    if (rb >= nrb) continue;
+    const int rr = rb * 16 + m;  // this lane's state row (output column)
+    const float gl = p.G[(tb + WBT - 1) * kw + rr];
+    const bool wild = -gl > WILD;
+    float kt[2][4], yt[2][4], xt[2][4];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = jb * 16 + 4 * g + e;
+        const long long o = (tb + j) * kw + rr;
+        const float gj = p.G[o];
+        kt[jb][e] = wild ? 0.f : p.k[o] * __expf(-gj);
+        yt[jb][e] = wild ? 0.f : Yk[o] * __expf(gj);
+        xt[jb][e] = wild ? 0.f : p.x[o] * __expf(gx_g(j, rr));
+      }
+    const float egl = __expf(gl);
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      f4 ax = aX[q][t2], aq = aO[q][t2], ak;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ak[e] = egl * aL[q][t2][e];
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int jj = jb * 16 + 4 * g + e, ii = t2 * 16 + m;
+          ax = mfma4(M1[ii * MS + jj], kt[jb][e], ax);
+          ak = mfma4(M2[jj * MS + ii], yt[jb][e], ak);
+          ak = mfma4(-M1[jj * MS + ii], xt[jb][e], ak);
+          if (p.colout) aq = mfma4(M2[ii * MS + jj], kt[jb][e], aq);
+        }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = t2 * 16 + 4 * g + e;
+        const long long o = (tb + i) * kw + rr;
+        const float gi = p.G[o], gxi = gx_g(i, rr);
+        float dx, dk, dq = 0.f;
+        if (!wild) {
+          dx = -__expf(gxi) * ax[e];
+          dk = __expf(-gi) * ak[e];
+          dq = __expf(gi) * aq[e];
+        } else {
+          float a = __expf(gxi) * aX[q][t2][e];
+          for (int j = 0; j < i; ++j)
+            a += M1[i * MS + j] * p.k[(tb + j) * kw + rr] * __expf(gxi - p.G[(tb + j) * kw + rr]);
+          dx = -a;
+          float b = __expf(gl - gi) * aL[q][t2][e];
+          for (int j = i; j < WBT; ++j)
+            b += M2[j * MS + i] * Yk[(tb + j) * kw + rr] * __expf(p.G[(tb + j) * kw + rr] - gi);
+          for (int j = i + 1; j < WBT; ++j)
+            b -= M1[j * MS + i] * p.x[(tb + j) * kw + rr] * __expf(gx_g(j, rr) - gi);
+          dk = b;
+          if (p.colout) {
+            float c2 = __expf(gi) * aO[q][t2][e];
+            for (int j = 0; j <= i; ++j)
+              c2 += M2[i * MS + j] * p.k[(tb + j) * kw + rr] * __expf(gi - p.G[(tb + j) * kw + rr]);
+            dq = c2;
+          }
+        }
+        p.dx[o] = dx;
+        p.dk[o] = dk;
+        if (p.colout) p.dq[o] = dq;
+      }
     }
   }
-  // decay closure: dG = q dq - k dk (column) / o dO - k dk (row) + x dx (one
-  // token earlier when the erase reads before the decay); the last row adds
-  // rowsum(X_C lam); dg is its in-chunk reverse cumulative sum.  dx, dk, dq are
-  // read back from this thread's own stores above.
+  __syncthreads();  // dx, dk, dq of the whole chunk written
+  // phase 4, one key coordinate per thread: decay closure dG = q dq - k dk
+  // (column) / o dO - k dk (row) + x dx (one token earlier when the erase reads
+  // before the decay); the last row adds rowsum(X_C lam); dg is its in-chunk
+  // reverse cumulative sum.
+  if (r >= kw) return;
   float run = rsum;
+#pragma unroll 8
   for (int i = WBT - 1; i >= 0; --i) {
     const long long o = (tb + i) * kw + r;
-    float dG = -kL[i * kw + r] * p.dk[o];
-    dG += p.colout ? YL[i * kw + r] * p.dq[o] : p.o[o] * p.dO[o];
+    float dG = -p.k[o] * p.dk[o];
+    dG += p.colout ? Yk[o] * p.dq[o] : p.o[o] * p.dO[o];
     const int ix = p.excl ? i + 1 : i;
-    if (ix < WBT) dG += xL[ix * kw + r] * p.dx[(tb + ix) * kw + r];
+    if (ix < WBT) dG += p.x[(tb + ix) * kw + r] * p.dx[(tb + ix) * kw + r];
     run += dG;
     p.dg[o] = run;
   }
 }
 
-constexpr size_t grad_smem(int kw) { return (2 * WBT * MS + 4 * WBT * (size_t)kw) * sizeof(float); }
+constexpr size_t grad_smem(int) { return 2 * WBT * MS * sizeof(float); }
 
 // ---------------------------------------------------------------------------
 // Source closure (per token): cotangents of e, chi, z back to u^, delta, k^, q^,
