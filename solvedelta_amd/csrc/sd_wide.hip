@@ -612,67 +612,83 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
     }
     return;
   }
-  // row output
-  const int lv = vw + 1;
-  float* ql = sm;               // q [32][vw+1]
-  float* wls = ql + WBT * lv;   // w [32][vw+1]
-  float* Ml = wls + WBT * lv;   // M [32][33]
-  float* Xb = Ml + WBT * MS;    // X0 column block [256][33]
-  for (int idx = threadIdx.x; idx < WBT * vw; idx += WT) {
-    const int i = idx / vw, c = idx % vw;
-    ql[i * lv + c] = p.q[(tb + i) * vw + c];
-    wls[i * lv + c] = p.w[(tb + i) * vw + c];
+  // row output on matrix cores: M = q w^T (j <= i), then
+  //   o_ir = e^{G_ir} ((q X0^T)_ir + (M k~)_ir),  k~_jr = k_jr e^{-G_jr}
+  // with the decay factored per state row r (wild rows: exact per-term sum).
+  float* Ml = sm;  // [32][33]
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
+  {
+    const int bi = w >> 1, bj = w & 1;
+    f4 acc = zero4();
+    for (int cb = 0; cb < vw; cb += 16) {
+      const float4 a4 = *reinterpret_cast<const float4*>(p.q + (tb + bi * 16 + m) * vw + cb + 4 * g);
+      const float4 b4 = *reinterpret_cast<const float4*>(p.w + (tb + bj * 16 + m) * vw + cb + 4 * g);
+      acc = mfma4(a4.x, b4.x, acc);
+      acc = mfma4(a4.y, b4.y, acc);
+      acc = mfma4(a4.z, b4.z, acc);
+      acc = mfma4(a4.w, b4.w, acc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = bi * 16 + 4 * g + e, j = bj * 16 + m;
+      Ml[i * MS + j] = j <= i ? acc[e] : 0.f;
+    }
   }
   __syncthreads();
-  for (int m = 0; m < WBT * WBT / WT; ++m) {
-    int i, j;
-    entry(m, i, j);
-    float a = 0.f;
-    if (j <= i)
-      for (int c = 0; c < vw; ++c) a += ql[i * lv + c] * wls[j * lv + c];
-    Ml[i * MS + j] = a;
-  }
-  const int r = threadIdx.x;
-  float acc[WBT];
+  const int nrb = kw / 16;
 #pragma unroll
-  for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
-  for (int cb = 0; cb < vw; cb += 32) {
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < kw * 32; idx += WT) {
-      const int rr = idx >> 5, cc = idx & 31;
-      Xb[rr * MS + cc] = X0[(long long)rr * vw + cb + cc];
-    }
-    __syncthreads();
-    if (r < kw) {
-      for (int cc = 0; cc < 32; ++cc) {
-        const float xv = Xb[r * MS + cc];
+  for (int q = 0; q < WRB; ++q) {
+    const int rb = w + 4 * q;
+    if (rb >= nrb) continue;
+    const int rr = rb * 16 + m;
+    const bool wild = -p.G[(tb + WBT - 1) * kw + rr] > WILD;
+    f4 acc[2] = {zero4(), zero4()};
+#pragma unroll 2
+    for (int cb = 0; cb < vw; cb += 16) {
+      const float4 bx = *reinterpret_cast<const float4*>(X0 + (long long)rr * vw + cb + 4 * g);
 #pragma unroll
-        for (int i = 0; i < WBT; ++i) acc[i] += ql[i * lv + cb + cc] * xv;
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const float4 a4 = *reinterpret_cast<const float4*>(p.q + (tb + t2 * 16 + m) * vw + cb + 4 * g);
+        acc[t2] = mfma4(a4.x, bx.x, acc[t2]);
+        acc[t2] = mfma4(a4.y, bx.y, acc[t2]);
+        acc[t2] = mfma4(a4.z, bx.z, acc[t2]);
+        acc[t2] = mfma4(a4.w, bx.w, acc[t2]);
       }
     }
-  }
-  __syncthreads();
-  if (r >= kw) return;
-  float kr[WBT], Gr[WBT];
+    float kt[2][4];
 #pragma unroll
-  for (int i = 0; i < WBT; ++i) {
-    kr[i] = p.k[(tb + i) * kw + r];
-    Gr[i] = p.G[(tb + i) * kw + r];
-  }
+    for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-  for (int i = 0; i < WBT; ++i) {
-    float a = __expf(Gr[i]) * acc[i];
+      for (int e = 0; e < 4; ++e) {
+        const long long o = (tb + jb * 16 + 4 * g + e) * kw + rr;
+        kt[jb][e] = wild ? 0.f : p.k[o] * __expf(-p.G[o]);
+      }
 #pragma unroll
-    for (int j = 0; j <= i; ++j) a += Ml[i * MS + j] * kr[j] * __expf(Gr[i] - Gr[j]);
-    const long long o = (tb + i) * kw + r;
-    p.o[o] = a;
-    p.d[o] = p.base[o] + a;
+    for (int t2 = 0; t2 < 2; ++t2) {
+      f4 a = acc[t2];
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a = mfma4(Ml[(t2 * 16 + m) * MS + jb * 16 + 4 * g + e], kt[jb][e], a);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = t2 * 16 + 4 * g + e;
+        const long long o = (tb + i) * kw + rr;
+        const float gi = p.G[o];
+        float v = __expf(gi) * a[e];
+        if (wild)
+          for (int j = 0; j <= i; ++j)
+            v += Ml[i * MS + j] * p.k[(tb + j) * kw + rr] * __expf(gi - p.G[(tb + j) * kw + rr]);
+        p.o[o] = v;
+        p.d[o] = p.base[o] + v;
+      }
+    }
   }
 }
 
 constexpr size_t out_smem(int kw, int vw, int colout) {
   if (colout) return (size_t)(WBT * (kw + 1) + WBT * MS + WBT * (vw + 4)) * sizeof(float);
-  return (size_t)(2 * WBT * (vw + 1) + WBT * MS + WMAX * MS) * sizeof(float);
+  return (size_t)(WBT * MS) * sizeof(float);
 }
 
 // ---------------------------------------------------------------------------
@@ -779,16 +795,20 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
       Gl[i * ld + c] = p.G[o];
     }
     __syncthreads();
-    for (int m = 0; m < WBT * WBT / WT; ++m) {
-      int i, j;
-      entry(m, i, j);
-      float a = 0.f;
-      if (j <= i)
-        for (int c = 0; c < kw; ++c)
-          a += dOl[i * ld + c] * kl[j * ld + c] * __expf(Gl[i * ld + c] - Gl[j * ld + c]);
-      Pl[i * MS + j] = a;
-      p.Pp[mb + i * WBT + j] = a;
-    }
+    int* wl = reinterpret_cast<int*>(Gl + WBT * ld);
+    const int nw = wild_list(Gl, ld, kw, wl, wl + WMAX);
+    gram_mfma(
+        kw, wl, nw, [&](int i, int c) { return dOl[i * ld + c] * __expf(Gl[i * ld + c]); },
+        [&](int j, int c) {
+          return -Gl[(WBT - 1) * ld + c] > WILD ? 0.f : kl[j * ld + c] * __expf(-Gl[j * ld + c]);
+        },
+        [&](int i, int j, int c) {
+          return dOl[i * ld + c] * kl[j * ld + c] * __expf(Gl[i * ld + c] - Gl[j * ld + c]);
+        },
+        [](int i, int j) { return j <= i; }, Pl);
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT)
+      p.Pp[mb + idx] = Pl[(idx >> 5) * MS + (idx & 31)];
   }
   __syncthreads();
   // value side: rhs and dU, one value column per thread
@@ -828,7 +848,7 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
 }
 
 constexpr size_t bprep_smem(int kw) {
-  const size_t panels = 3 * WBT * (size_t)(kw + 1), cols = 2 * WBT * WT;
+  const size_t panels = 3 * WBT * (size_t)(kw + 1) + WMAX + 4, cols = 2 * WBT * WT;
   return (2 * WBT * MS + (panels > cols ? panels : cols)) * sizeof(float);
 }
 
