@@ -455,7 +455,11 @@ def main():
             "mfma_frac": round(flops / avg_s / PEAK_MFMA_BF16, 5),
             "kernels_us": {k: round(v, 2) for k, v in sorted(us.items())},
             "kernels_mfma_busy": mfma_busy or None,
-            "kernels_traffic": traffic or None}
+            "kernels_traffic": traffic or None,
+            # each kernel's counter-measured HBM bytes over its event-timed duration
+            # (the state passes' and per-token closures' bandwidth against 8 TB/s)
+            "kernels_traffic_GBs": ({k: round(traffic[k] / (us[k] * 1e-6) / 1e9, 1)
+                                     for k in sorted(us) if k in traffic} if traffic else None)}
     # every kernel runs once per step; the counter summary lists each by its event name
     step_bytes = sum(traffic.get(k, 0.0) for k in us) if traffic else None
     step = {"algorithmic_bytes": STEP_FLOOR_BYTES,
