@@ -232,6 +232,44 @@ def forward_bench(ins, st, steps, warmup):
             "value": round(B * T / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4)}
 
 
+def variant_bench(dev, steps, warmup, *, r=R, v=V, masked=False):
+    """F+B at the headline's B, T, H on a variant of the path: key / value widths
+    above 128 (the wide-width kernels), or the masked operator with 10 % invalid
+    tokens and 1 % resets on the dense batch.  Reported beside the headline."""
+    import torch.nn.functional as F
+    from solvedelta_amd import solvedelta_masked_native, solvedelta_native
+    g = torch.Generator().manual_seed(7)
+    n = lambda *sh: torch.randn(*sh, generator=g)
+    bf = lambda x: x.to(torch.bfloat16).to(dev).requires_grad_()
+    ins = [bf(n(B, T, H, r)), bf(n(B, T, H, r)), bf(F.normalize(n(B, T, H, r), dim=-1)),
+           bf(F.normalize(n(B, T, H, 1, r), dim=-1)), bf(n(B, T, H, 1, v)),
+           (-F.softplus(n(B, T, H, r))).to(dev).requires_grad_(), bf(n(B, T, H, 1, r)),
+           bf(n(B, T, H, 1, v)), torch.full((B, T, H), 0.9, device=dev).requires_grad_()]
+    dO = n(B, T, H, v).to(torch.bfloat16).to(dev)
+    valid = (torch.rand(B, T, generator=g) > 0.1).to(dev)
+    reset = (torch.rand(B, T, generator=g) < 0.01).to(dev)
+
+    def step():
+        if masked:
+            out, _ = solvedelta_masked_native(*ins, valid, reset)
+        else:
+            out, _ = solvedelta_native(*ins)
+        return torch.autograd.grad(out, ins, dO)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    what = ("masked operator, 10 % invalid tokens and 1 % resets" if masked
+            else f"wide-width kernels, r={r} V={v}")
+    return {"workload": f"operator forward + full VJP, B={B} T={T} H={H}, {what}",
+            "value": round(B * T / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4)}
+
+
 def refshape_bench(dev, steps, warmup):
     """Forward + full VJP at the shape the reference's own README quotes its core
     F+B timing on (B=1 T=1024 H=8 r=V=128; 0.905 ms on an RTX 5070 Ti, reference
@@ -483,6 +521,8 @@ def main():
         return
     res["forward"] = forward_bench(ins, st, a.steps, a.warmup)
     res["reference_shape"] = refshape_bench(dev, a.steps, a.warmup)
+    res["wide"] = variant_bench(dev, 5, 2, r=256, v=256)
+    res["masked"] = variant_bench(dev, 10, 3, masked=True)
     if not a.no_decode:
         res["decode"] = decode_bench(dev)
         res["decode_uncached"] = decode_bench(dev, steps=32, streams=512)

@@ -100,6 +100,25 @@ int sd_bwd(const sd_inputs *in, const void *fwd_workspace, const void *dout, con
 size_t sd_noalloc_scratch_bytes(void);
 int sd_fwd_noalloc(const sd_inputs *in, void *out, float *C_T, float *S_T, void *stream);
 
+/* Row masking for masked batches on the dense layout (no counterpart in the
+ * reference, whose masked path repacks valid tokens into segments with a host
+ * sync, causallsso/ops/packing.py:43-150): one launch copies up to eight
+ * [B,T,H,width] tensors into contiguous outputs, keeping the rows of valid
+ * tokens and zeroing the others; on valid reset tokens rows with reset_fill
+ * set take reset_value.  flags: uint8 [B,T] at flags[b*flags_sb + t*flags_st],
+ * bit 0 valid, bit 1 reset.  Used forward (operands: zero invalid tokens, kill
+ * the log-decay of reset tokens) and backward (gradients: zero on invalid
+ * tokens, zero log-decay gradient on reset tokens). */
+typedef struct {
+  const void *src; /* element (b,t,h,c) at src[b*sb + t*st + h*sh + c] */
+  int64_t sb, st, sh;
+  void *dst;       /* contiguous [B,T,H,width] */
+  int width, is_fp32, reset_fill;
+  float reset_value;
+} sd_mask_tensor;
+int sd_mask_rows(int B, int T, int H, const uint8_t *flags, int64_t flags_sb, int64_t flags_st,
+                 const sd_mask_tensor *tensors, int n, void *stream);
+
 /* One-token recurrent step (T must be 1). out: bf16 [B,1,H,V] contiguous.
  * C_T / S_T receive the advanced state; they may alias C0 / S0 (in place). */
 int sd_decode(const sd_inputs *in, void *out, float *C_T, float *S_T, void *stream);

@@ -28,6 +28,13 @@ class SdInputs(ctypes.Structure):
                 ("fresh", SdView)]
 
 
+class SdMaskTensor(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("sb", ctypes.c_int64), ("st", ctypes.c_int64),
+                ("sh", ctypes.c_int64), ("dst", ctypes.c_void_p), ("width", ctypes.c_int),
+                ("is_fp32", ctypes.c_int), ("reset_fill", ctypes.c_int),
+                ("reset_value", ctypes.c_float)]
+
+
 EXPORTS = {
     "sd_version": (ctypes.c_char_p, []),
     "sd_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int] * 5),
@@ -47,6 +54,9 @@ EXPORTS = {
     "sd_noalloc_scratch_bytes": (ctypes.c_size_t, []),
     "sd_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
                                       ctypes.c_void_p, ctypes.c_void_p]),
+    "sd_mask_rows": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64,
+                                    ctypes.c_int64, ctypes.POINTER(SdMaskTensor), ctypes.c_int,
+                                    ctypes.c_void_p]),
     "sd_decode": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
                                  ctypes.c_void_p, ctypes.c_void_p]),
     # mixer frontend / readout (include/solvedelta_mixer.h)

@@ -1,0 +1,105 @@
+// Row masking for the dense-batch masked operator (valid / reset masks without
+// repacking): one launch copies up to eight [B,T,H,w] tensors, keeping the
+// rows of valid tokens, zeroing the others, and giving the log-decay rows of
+// reset tokens a fixed value.  The same kernel masks the gradients on the way
+// back (zero on invalid tokens, zero log-decay gradient on reset tokens).
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include "../../include/solvedelta.h"
+#include "sd_internal.h"
+
+namespace sd {
+namespace {
+
+constexpr int kMaxMasked = 8;
+
+struct MaskJob {
+  int n;
+  sd_mask_tensor t[kMaxMasked];
+};
+
+// One thread per 16 bytes of one row of one tensor when the tensor's rows are
+// 16-byte aligned on both sides (vec), else per 4 elements.
+struct MaskJobExt {
+  MaskJob job;
+  int vec[kMaxMasked];
+};
+
+__global__ __launch_bounds__(256) void k_mask_rows(MaskJobExt jx, int B, int T, int H,
+                                                   const uint8_t* __restrict__ flags,
+                                                   long long f_sb, long long f_st) {
+  const sd_mask_tensor& m = jx.job.t[blockIdx.y];
+  const int esz = m.is_fp32 ? 4 : 2, w = m.width;
+  const int per = jx.vec[blockIdx.y] ? 16 / esz : 4;  // elements per thread
+  const int q = (w + per - 1) / per;
+  const long long rows = (long long)B * T * H;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * q) return;
+  const long long row = idx / q;
+  const int c0 = (int)(idx % q) * per;
+  const int hh = (int)(row % H), t = (int)((row / H) % T), b = (int)(row / ((long long)H * T));
+  const uint8_t f = flags[(long long)b * f_sb + (long long)t * f_st];
+  const bool valid = f & 1, reset = (f & 2) != 0;
+  const long long so = (long long)b * m.sb + (long long)t * m.st + (long long)hh * m.sh;
+  const long long dof = row * w;
+  if (jx.vec[blockIdx.y]) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (valid) v = *reinterpret_cast<const uint4*>((const char*)m.src + (so + c0) * esz);
+    if (valid && reset && m.reset_fill) {
+      if (m.is_fp32) {
+        const unsigned r = __float_as_uint(m.reset_value);
+        v = make_uint4(r, r, r, r);
+      } else {
+        const __bf16 r = (__bf16)m.reset_value;
+        const unsigned short rb = *reinterpret_cast<const unsigned short*>(&r);
+        const unsigned r2 = (unsigned)rb | ((unsigned)rb << 16);
+        v = make_uint4(r2, r2, r2, r2);
+      }
+    }
+    *reinterpret_cast<uint4*>((char*)m.dst + (dof + c0) * esz) = v;
+    return;
+  }
+  for (int c = c0; c < c0 + per && c < w; ++c) {
+    if (m.is_fp32) {
+      float v = valid ? ((const float*)m.src)[so + c] : 0.f;
+      if (valid && reset && m.reset_fill) v = m.reset_value;
+      ((float*)m.dst)[dof + c] = v;
+    } else {
+      __bf16 v = valid ? ((const __bf16*)m.src)[so + c] : (__bf16)0.f;
+      if (valid && reset && m.reset_fill) v = (__bf16)m.reset_value;
+      ((__bf16*)m.dst)[dof + c] = v;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace sd
+
+using namespace sd;
+
+extern "C" int sd_mask_rows(int B, int T, int H, const uint8_t* flags, int64_t flags_sb,
+                            int64_t flags_st, const sd_mask_tensor* tensors, int n,
+                            void* stream) {
+  if (B < 1 || T < 1 || H < 1 || n < 1 || n > kMaxMasked) return SD_ERR_SHAPE;
+  if (!flags || !tensors) return SD_ERR_ARG;
+  MaskJobExt jx{};
+  jx.job.n = n;
+  long long work = 0;
+  for (int i = 0; i < n; ++i) {
+    const sd_mask_tensor& m = tensors[i];
+    jx.job.t[i] = m;
+    if (!m.src || !m.dst || m.width < 1) return SD_ERR_ARG;
+    const long long esz = m.is_fp32 ? 4 : 2;
+    const bool vec = ((uintptr_t)m.src % 16 == 0) && ((uintptr_t)m.dst % 16 == 0) &&
+                     (m.width * esz) % 16 == 0 && (m.sb * esz) % 16 == 0 &&
+                     (m.st * esz) % 16 == 0 && (m.sh * esz) % 16 == 0;
+    jx.vec[i] = vec;
+    const long long per = vec ? 16 / esz : 4;
+    const long long items = (long long)B * T * H * ((m.width + per - 1) / per);
+    work = items > work ? items : work;
+  }
+  const dim3 grid((unsigned)((work + 255) / 256), (unsigned)n);
+  SD_LAUNCH("k_mask_rows", k_mask_rows, grid, dim3(256), 0, (hipStream_t)stream, jx, B, T, H,
+            flags, (long long)flags_sb, (long long)flags_st);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}

@@ -18,18 +18,26 @@ kernels unchanged in shape:
   predictor's residual is taken before forgetting (h - C_{t-1} u), so the
   decay alone would not reset it.
 
-Gradients reach the masked operands through torch.where, so invalid tokens'
-inputs and reset tokens' log-decay get zero gradient, as when the reference
-leaves them out of its segments.  Everything is elementwise on the device and
-capturable in a HIP graph.
+The masking is one HIP launch each way (sd_mask_rows): the forward copies
+u, h, q, keys, values and the log-decay with invalid rows zeroed and reset rows'
+log-decay killed; the backward zeroes the same rows of their gradients (and the
+reset tokens' log-decay gradient), so invalid tokens' inputs and reset tokens'
+log-decay get zero gradient, as when the reference leaves them out of its
+segments.  erase_raw, write_raw and gamma need no masking: on an invalid token
+their only partners (the normalised key, the values, u and h) are zero, so
+their forward effect and gradients vanish by themselves.  Everything stays on
+the device and is capturable in a HIP graph.
 """
 from __future__ import annotations
 
 from typing import Optional
 
+import ctypes
+
 import torch
 
-from .operator import _dispatch, _validate
+from . import _lib
+from .operator import _dispatch, _stream, _validate
 from .state import SolveDeltaState
 
 # log-decay of a reset token: exp(-200) underflows to 0 in FP32 (the smallest
@@ -50,6 +58,50 @@ def _check_masks(valid_mask, reset_mask, B, T, device):
     return valid_mask, reset_mask
 
 
+def _mask_tensor(src: torch.Tensor, dst: torch.Tensor, reset_fill: bool, reset_value: float):
+    return _lib.SdMaskTensor(src.data_ptr(), src.stride(0), src.stride(1), src.stride(2),
+                             dst.data_ptr(), src.shape[-1], int(src.dtype == torch.float32),
+                             int(reset_fill), reset_value)
+
+
+def _mask_rows(flags, srcs, decay_last: bool, reset_value: float):
+    """Masked contiguous copies of srcs ([B,T,H,...,w] views, unit inner stride);
+    the last one is the log-decay (or its gradient) when decay_last."""
+    B, T, H = srcs[0].shape[:3]
+    outs = [torch.empty(x.shape, dtype=x.dtype, device=x.device) for x in srcs]
+    arr = (_lib.SdMaskTensor * len(srcs))(*[
+        _mask_tensor(x, o, decay_last and i == len(srcs) - 1, reset_value)
+        for i, (x, o) in enumerate(zip(srcs, outs))])
+    rc = _lib.load().sd_mask_rows(B, T, H, flags.data_ptr(), flags.stride(0), flags.stride(1),
+                                  arr, len(srcs), _stream(srcs[0].device))
+    _lib.check(rc, "sd_mask_rows")
+    return outs
+
+
+class _MaskOperands(torch.autograd.Function):
+    """u, h, q, keys, values, log-decay -> copies with invalid tokens zeroed and
+    reset tokens' log-decay set to RESET_LOG_DECAY; the backward masks the
+    gradients the same way (zero log-decay gradient on reset tokens)."""
+
+    @staticmethod
+    def forward(ctx, flags, u, h, q, keys, values, log_decay):
+        ctx.save_for_backward(flags)
+        return tuple(_mask_rows(flags, [u, h, q, keys, values, log_decay], True,
+                                RESET_LOG_DECAY))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        (flags,) = ctx.saved_tensors
+        live = [i for i, g in enumerate(grads) if g is not None]
+        out = [None] * len(grads)
+        if live:
+            srcs = [grads[i] if grads[i].stride(-1) == 1 else grads[i].contiguous() for i in live]
+            masked = _mask_rows(flags, srcs, live[-1] == len(grads) - 1, 0.0)
+            for i, m in zip(live, masked):
+                out[i] = m
+        return (None, *out)
+
+
 def solvedelta_masked_native(u, h, q, keys, values, associative_log_decay, erase_raw,
                              write_raw, geometry_write, valid_mask=None, reset_mask=None, *,
                              initial_state: Optional[SolveDeltaState] = None,
@@ -62,15 +114,9 @@ def solvedelta_masked_native(u, h, q, keys, values, associative_log_decay, erase
     B, T = u.shape[:2]
     valid_mask, reset_mask = _check_masks(valid_mask, reset_mask, B, T, u.device)
     reset = reset_mask & valid_mask
-    m4 = valid_mask[:, :, None, None]
-    m5 = valid_mask[:, :, None, None, None]
-    zero = lambda x: torch.where(m4 if x.ndim == 4 else m5, x, torch.zeros((), dtype=x.dtype,
-                                                                           device=x.device))
-    u, h, q = zero(u), zero(h), zero(q)
-    keys, values, erase_raw, write_raw = zero(keys), zero(values), zero(erase_raw), zero(write_raw)
-    g = torch.where(reset[:, :, None, None],
-                    torch.full((), RESET_LOG_DECAY, dtype=torch.float32, device=u.device),
-                    zero(associative_log_decay))
+    flags = (valid_mask.to(torch.uint8) | (reset.to(torch.uint8) << 1)).contiguous()
+    u, h, q, keys, values, g = _MaskOperands.apply(flags, u, h, q, keys, values,
+                                                   associative_log_decay)
     fresh = reset.to(torch.uint8)
     return _dispatch(u, h, q, keys, values, g, erase_raw, write_raw, geometry_write,
                      initial_state, return_final_state, fresh)
