@@ -24,7 +24,10 @@ constexpr int BS = 16;     // block length inside a chunk
 constexpr int NB = BT / BS;
 constexpr int KD = 128;    // padded key width
 constexpr int VD = 128;    // padded value width
-constexpr float TAU = 30.f;
+// The block factor exp(R_J - G_j) stays below exp(TAU); a factor exp(Gx_i - R_J)
+// that underflows FP32 (below exp(-87)) then drops a term below exp(TAU - 87)
+// ~ 2e-12 of its operands' product, far under FP32 rounding of the terms kept.
+constexpr float TAU = 60.f;
 constexpr float RHO = 0.625f;
 constexpr int NTHREADS = 256;  // sequential / per-token kernels
 constexpr int CT = 512;        // chunk-parallel kernels: 8 waves, one 16-column block each
@@ -374,7 +377,7 @@ __device__ __forceinline__ void build_decay(ChunkDecay& cd, const float* g, long
 // wild coordinate's argument can exceed the fp32 exp range, so it is clamped
 // before the mask; a non-wild argument is at most TAU and is left unchanged.
 __device__ __forceinline__ float exp_unless_wild(bool wild, float x) {
-  return keep_if(!wild, __expf(fminf(x, 2.f * TAU)));
+  return keep_if(!wild, __expf(fminf(x, TAU)));
 }
 
 // Gx for the erase side: inclusive (G_i) or exclusive (G_{i-1} = G_i - g_i).

@@ -11,11 +11,16 @@ kernels unchanged in shape:
   gives zero, so the predictor's write, the dual sources and the primal address
   are zero), so it emits 0 and keeps both states -- the reference's semantics
   (reference.py:156-227);
-* a reset on a valid token zeroes both states before that token: its
-  log-decay is replaced by RESET_LOG_DECAY (exp underflows to exactly 0 in
-  FP32, so D C and D S vanish), and the token is flagged *fresh* for the
-  kernels, which drops the predictor's erase read x = gamma u^ on it -- the
-  predictor's residual is taken before forgetting (h - C_{t-1} u), so the
+* a reset on a valid token clears both states before that token: its
+  log-decay is replaced by RESET_LOG_DECAY, so D C and D S keep exp(-20) ~
+  2e-9 of the old states -- below FP32 rounding (6e-8) of the terms that
+  follow -- while the chunk kernels keep the token on their factored
+  (matrix-core) decay path: a 16-token block whose decay exceeds their wild
+  threshold of 60 (an exact exp(-inf) kill would, and so would three such
+  resets in one block) takes the exact per-coordinate fix-up, several times
+  slower, and the slowest block sets each round's time.  The token is also flagged *fresh* for the
+  kernels, which drops the predictor's erase read x = gamma u^ on it exactly --
+  the predictor's residual is taken before forgetting (h - C_{t-1} u), so the
   decay alone would not reset it.
 
 The masking is one HIP launch each way (sd_mask_rows): the forward copies
@@ -40,9 +45,11 @@ from . import _lib
 from .operator import _dispatch, _stream, _validate
 from .state import SolveDeltaState
 
-# log-decay of a reset token: exp(-200) underflows to 0 in FP32 (the smallest
-# subnormal is exp(-103.3)); the kernels take any finite decay exactly
-RESET_LOG_DECAY = -200.0
+# log-decay of a reset token: the old states survive as exp(-20) ~ 2e-9 of
+# their value, under FP32's 6e-8 rounding of the new terms; two resets and up
+# to 20 of ordinary decay fit in one 16-token block before it leaves the
+# kernels' factored path (see the module docstring for why not an exact kill)
+RESET_LOG_DECAY = -20.0
 
 
 def _check_masks(valid_mask, reset_mask, B, T, device):

@@ -21,7 +21,7 @@ import torch
 
 BT = 64
 BS = 16
-TAU = 30.0
+TAU = 60.0
 RHO = 5.0 / 8.0
 
 

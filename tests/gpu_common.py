@@ -29,10 +29,10 @@ def make_inputs(B, T, H, r, V, *, seed=0, device="cuda", decay="softplus", gamma
         gd = torch.full((B, T, H, r), -100.0)
     elif decay == "mixed":
         # three tiers of coordinates: x8 (16-token block drops ~100, always past
-        # the kernels' wild threshold of 30), x2.5 (drops ~32: wild in some blocks
-        # only) and x1 (~13, never), so exact wild fix-ups and ordinary
+        # the kernels' wild threshold of 60), x4.5 (drops ~58: wild in some
+        # blocks only) and x1 (~13, never), so exact wild fix-ups and ordinary
         # coordinates meet in one block
-        fast = torch.tensor([8.0, 2.5, 1.0]).repeat(r // 3 + 1)[:r]
+        fast = torch.tensor([8.0, 4.5, 1.0]).repeat(r // 3 + 1)[:r]
         gd = -F.softplus(n(B, T, H, r)) * fast
     else:
         gd = torch.zeros(B, T, H, r)
