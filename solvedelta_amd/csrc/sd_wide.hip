@@ -37,6 +37,39 @@ constexpr int WT = 256;    // threads per workgroup
 constexpr int MS = WBT + 1;  // row stride of 32 x 32 LDS matrices
 constexpr int TILE = 16;   // state-pass column tile
 
+// Chunk-boundary state slots in a 2-byte type, as in the main kernels: the
+// forward states X (C^T and S) in fp16, the reverse passes' cotangent states
+// lambda in bf16.  The final states handed to the caller stay FP32.
+using xs_t = xslot_t;
+using ls_t = lslot_t;
+__device__ __forceinline__ float4 ld4s(const _Float16* p) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 v = *reinterpret_cast<const h4*>(p);
+  return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+__device__ __forceinline__ float4 ld4s(const __bf16* p) {
+  typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+  const b4 v = *reinterpret_cast<const b4*>(p);
+  return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+
+// Workgroup ids are dealt round-robin over the 8 XCDs (each with its own L2).
+// Maps a linear id over (inner, outer) = (L % inner, L / inner) so that, when the
+// outer count is a multiple of 8, the inner indices of one outer index run on
+// one XCD in consecutive order: the state pass's column tiles of a sequence
+// share its L2 copy of the chunk panels, and the chunk gradients of neighbouring
+// chunks share the state slot between them.
+__device__ __forceinline__ void xcd_map(int L, int inner, int outer, int& in, int& out) {
+  if (outer % 8 == 0) {
+    const int x = L % 8, j = L / 8;
+    in = j % inner;
+    out = (j / inner) * 8 + x;
+  } else {
+    in = L % inner;
+    out = L / inner;
+  }
+}
+
 __device__ __forceinline__ const __bf16* wrow(const sd_view& v, int b, int t, int h) {
   return (const __bf16*)v.data + (long long)b * v.sb + (long long)t * v.st + (long long)h * v.sh;
 }
@@ -297,14 +330,16 @@ constexpr size_t prep_smem(int kw) {
 struct WStateParams {
   int NT, Tp, kw, vw, rows, cols, rev;
   const float *W, *U, *K, *Gam, *Ia, *Ib;
-  float *slots, *wout;
+  void* slots;  // xs_t (forward) or ls_t (reverse)
+  float* wout;
   const float* init; int init_t;
   float* fin; int fin_t;
 };
 
 // Matrix-core form.  A workgroup owns a 32-column tile (two 16-column
 // halves).  The tile's rows are cut into 16-row blocks dealt round-robin to
-// the 4 waves (up to 4 per wave), each half held as an FP32 MFMA accumulator
+// the 8 waves (up to 2 per wave, two waves per SIMD so that one wave's LDS and
+// memory waits overlap the other's matrix work), each half held as an FP32 MFMA accumulator
 // (lane (g, n) holds rows 4g..4g+3 of column n).  Every product runs on
 // v_mfma_f32_16x16x4f32 with the sum index k = 4g + e carried by MFMA e and
 // lane group g, so an accumulator block is a B operand as it stands (no
@@ -315,14 +350,20 @@ struct WStateParams {
 // W is staged row-major [32][kw+4], K (and the injection A) transposed
 // [kw][36], the injection B tile transposed [32][36].  The next chunk's W, K
 // and A are loaded into registers while the current chunk computes.
-constexpr int WRB = WMAX / 16 / 4;  // row blocks per wave
+constexpr int WRB = WMAX / 16 / 4;  // row blocks per wave (four-wave kernels)
+constexpr int SW = 8;               // state-pass waves: two per SIMD
+constexpr int ST = SW * 64;
+constexpr int SRB = WMAX / 16 / SW;  // state-pass row blocks per wave
 constexpr int LDT = WBT + 4;        // row stride of the transposed panels
 constexpr int STILE = 32;           // state columns per workgroup
 constexpr int NSUB = STILE / 16;
-constexpr int PFQ = WBT * WMAX / 4 / WT;  // 16-byte pieces of one [32][kw] panel per thread (kw = 256)
+constexpr int NCMB = NSUB * 2 * 4;  // w values per lane: (half, token block, element)
+constexpr int CPW = NCMB / SW;      // of which each wave reduces CPW
+static_assert(NCMB % SW == 0, "w values split evenly over the waves");
+constexpr int PFQ = WBT * WMAX / 4 / ST;  // 16-byte pieces of one [32][kw] panel per thread (kw = 256)
 constexpr size_t state_smem(int kw, bool inj) {
   return (size_t)(WBT * (kw + 4) + kw * LDT + (inj ? kw * LDT + STILE * LDT : 0) +
-                  4 * NSUB * 2 * 4 * 64) * sizeof(float);
+                  (SW + 1) * NCMB * 64) * sizeof(float);
 }
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
@@ -338,7 +379,7 @@ struct PanelRegs {
 __device__ __forceinline__ void panel_load(PanelRegs& r, const float* src, int kw) {
 #pragma unroll
   for (int q = 0; q < PFQ; ++q) {
-    const int idx = threadIdx.x + WT * q, i = idx & 31, c = (idx >> 5) * 4;
+    const int idx = threadIdx.x + ST * q, i = idx & 31, c = (idx >> 5) * 4;
     r.v[q] = c < kw ? *reinterpret_cast<const float4*>(src + (long long)i * kw + c)
                     : make_float4(0.f, 0.f, 0.f, 0.f);
   }
@@ -346,14 +387,14 @@ __device__ __forceinline__ void panel_load(PanelRegs& r, const float* src, int k
 __device__ __forceinline__ void panel_store_rows(const PanelRegs& r, float* dst, int ld, int kw) {
 #pragma unroll
   for (int q = 0; q < PFQ; ++q) {
-    const int idx = threadIdx.x + WT * q, i = idx & 31, c = (idx >> 5) * 4;
+    const int idx = threadIdx.x + ST * q, i = idx & 31, c = (idx >> 5) * 4;
     if (c < kw) *reinterpret_cast<float4*>(dst + i * ld + c) = r.v[q];
   }
 }
 __device__ __forceinline__ void panel_store_t(const PanelRegs& r, float* dst, int kw) {
 #pragma unroll
   for (int q = 0; q < PFQ; ++q) {
-    const int idx = threadIdx.x + WT * q, i = idx & 31, c = (idx >> 5) * 4;
+    const int idx = threadIdx.x + ST * q, i = idx & 31, c = (idx >> 5) * 4;
     if (c < kw) {
       dst[c * LDT + i] = r.v[q].x;
       dst[(c + 1) * LDT + i] = r.v[q].y;
@@ -363,9 +404,11 @@ __device__ __forceinline__ void panel_store_t(const PanelRegs& r, float* dst, in
   }
 }
 
-__global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
+__global__ __launch_bounds__(ST) void k_w_state(WStateParams p) {
   extern __shared__ __align__(16) float sm[];
-  const int tile = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw, c0 = tile * STILE;
+  int tile, s;
+  xcd_map(blockIdx.x, p.vw / STILE, gridDim.x / (p.vw / STILE), tile, s);
+  const int kw = p.kw, vw = p.vw, c0 = tile * STILE;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
   const int nrb = kw / 16, ldw = kw + 4;
   const bool inj = p.Ia != nullptr;
@@ -373,11 +416,12 @@ __global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
   float* Kt = Wl + WBT * ldw;           // K^T [kw][LDT]
   float* At = Kt + kw * LDT;            // injection A^T [kw][LDT]
   float* Bt = At + (inj ? kw * LDT : 0);  // injection B^T [32][LDT]
-  float* red = Bt + (inj ? STILE * LDT : 0);  // w partials [4 waves][NSUB][2][4][64]
-  f4 X[WRB][NSUB];
+  float* red = Bt + (inj ? STILE * LDT : 0);  // w partials [SW waves][NCMB][64]
+  float* wred = red + SW * NCMB * 64;          // reduced w [NCMB][64]
+  f4 X[SRB][NSUB];
 #pragma unroll
-  for (int q = 0; q < WRB; ++q) {
-    const int rb = w + 4 * q;
+  for (int q = 0; q < SRB; ++q) {
+    const int rb = w + SW * q;
 #pragma unroll
     for (int h = 0; h < NSUB; ++h)
 #pragma unroll
@@ -405,36 +449,41 @@ __global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
     panel_store_t(nK, Kt, kw);
     if (inj) {
       panel_store_t(nA, At, kw);
-      for (int q = threadIdx.x; q < WBT * STILE; q += WT) {
+      for (int q = threadIdx.x; q < WBT * STILE; q += ST) {
         const int i = q & 31, n = q >> 5;
         Bt[n * LDT + i] = p.Ib[(tb + i) * vw + c0 + n];
       }
     }
-    // this step's U and chunk decay, loaded ahead of their use
-    f4 uv[NSUB][2];
+    // this step's U (the w values this wave reduces) and chunk decay, loaded
+    // ahead of their use
+    float uq[CPW];
 #pragma unroll
-    for (int h = 0; h < NSUB; ++h)
+    for (int j = 0; j < CPW; ++j) {
+      const int k = w * CPW + j, h = k >> 3, t2 = (k >> 2) & 1, e = k & 3;
+      uq[j] = p.U[(tb + t2 * 16 + 4 * g + e) * vw + c0 + h * 16 + m];
+    }
+    float gv[SRB][4];
 #pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) uv[h][t2][e] = p.U[(tb + t2 * 16 + 4 * g + e) * vw + c0 + h * 16 + m];
-    float gv[WRB][4];
-#pragma unroll
-    for (int q = 0; q < WRB; ++q)
+    for (int q = 0; q < SRB; ++q)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int rb = w + 4 * q;
+        const int rb = w + SW * q;
         gv[q][e] = rb < nrb ? p.Gam[((long long)s * p.NT + ch) * kw + rb * 16 + 4 * g + e] : 0.f;
       }
 #pragma unroll
-    for (int q = 0; q < WRB; ++q) {  // slot[ch] = X0
-      const int rb = w + 4 * q;
+    for (int q = 0; q < SRB; ++q) {  // slot[ch] = X0
+      const int rb = w + SW * q;
       if (rb < nrb)
 #pragma unroll
         for (int h = 0; h < NSUB; ++h)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            p.slots[sb + ((long long)ch * kw + rb * 16 + 4 * g + e) * vw + c0 + h * 16 + m] = X[q][h][e];
+          for (int e = 0; e < 4; ++e) {
+            const long long o = sb + ((long long)ch * kw + rb * 16 + 4 * g + e) * vw + c0 + h * 16 + m;
+            if (p.rev)
+              static_cast<ls_t*>(p.slots)[o] = (ls_t)X[q][h][e];
+            else
+              static_cast<xs_t*>(p.slots)[o] = (xs_t)X[q][h][e];
+          }
     }
     __syncthreads();
     // the next chunk's panels load while this one computes (clamped at the end)
@@ -449,8 +498,8 @@ __global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
 #pragma unroll
     for (int h = 0; h < NSUB; ++h) pw[h][0] = pw[h][1] = zero4();
 #pragma unroll
-    for (int q = 0; q < WRB; ++q) {
-      const int rb = w + 4 * q;
+    for (int q = 0; q < SRB; ++q) {
+      const int rb = w + SW * q;
       if (rb < nrb) {
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2) {
@@ -472,30 +521,29 @@ __global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) red[(((w * NSUB + h) * 2 + t2) * 4 + e) * 64 + l] = pw[h][t2][e];
     __syncthreads();
+    // each wave finishes CPW of the lane's NCMB w values (U minus the eight
+    // waves' partials, in wave order) and shares them through LDS
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int k = w * CPW + j, h = k >> 3, t2 = (k >> 2) & 1, e = k & 3;
+      float a = uq[j];
+#pragma unroll
+      for (int w2 = 0; w2 < SW; ++w2) a -= red[(w2 * NCMB + k) * 64 + l];
+      wred[k * 64 + l] = a;
+      p.wout[(tb + t2 * 16 + 4 * g + e) * vw + c0 + h * 16 + m] = a;
+    }
+    __syncthreads();
     f4 wv[NSUB][2];
 #pragma unroll
     for (int h = 0; h < NSUB; ++h)
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float a = uv[h][t2][e];
-#pragma unroll
-          for (int w2 = 0; w2 < 4; ++w2) a -= red[(((w2 * NSUB + h) * 2 + t2) * 4 + e) * 64 + l];
-          wv[h][t2][e] = a;
-        }
-    if (w == 0)
-#pragma unroll
-      for (int h = 0; h < NSUB; ++h)
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            p.wout[(tb + t2 * 16 + 4 * g + e) * vw + c0 + h * 16 + m] = wv[h][t2][e];
+        for (int e = 0; e < 4; ++e) wv[h][t2][e] = wred[((h * 2 + t2) * 4 + e) * 64 + l];
     // X = Gamma X + K^T w (+ A^T B)
 #pragma unroll
-    for (int q = 0; q < WRB; ++q) {
-      const int rb = w + 4 * q;
+    for (int q = 0; q < SRB; ++q) {
+      const int rb = w + SW * q;
       if (rb < nrb) {
 #pragma unroll
         for (int h = 0; h < NSUB; ++h)
@@ -528,15 +576,15 @@ __global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
     __syncthreads();  // the next step restages the panels
   }
 #pragma unroll
-  for (int q = 0; q < WRB; ++q) {
-    const int rb = w + 4 * q;
+  for (int q = 0; q < SRB; ++q) {
+    const int rb = w + SW * q;
     if (rb >= nrb) continue;
 #pragma unroll
     for (int h = 0; h < NSUB; ++h)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = rb * 16 + 4 * g + e, col = c0 + h * 16 + m;
-        if (!p.rev) p.slots[sb + ((long long)p.NT * kw + row) * vw + col] = X[q][h][e];
+        if (!p.rev) static_cast<xs_t*>(p.slots)[sb + ((long long)p.NT * kw + row) * vw + col] = (xs_t)X[q][h][e];
         if (p.fin && row < p.rows && col < p.cols) {
           if (p.fin_t) p.fin[((long long)s * p.cols + col) * p.rows + row] = X[q][h][e];
           else p.fin[((long long)s * p.rows + row) * p.cols + col] = X[q][h][e];
@@ -549,15 +597,14 @@ __global__ __launch_bounds__(WT) void k_w_state(WStateParams p) {
 // c = threadIdx.x (< vw): X [kw][vw] (global) is staged through LDS in 32-row
 // blocks with 16-byte loads; A [32][lda] is in LDS.  Every thread of the
 // workgroup must call it (it synchronises).
-__device__ __forceinline__ void rows_times_x(const float* A, int lda, const float* X, int kw,
+__device__ __forceinline__ void rows_times_x(const float* A, int lda, const xs_t* X, int kw,
                                              int vw, float* buf, float (&acc)[WBT]) {
   const int c = threadIdx.x, lb = vw + 4;
   for (int rb = 0; rb < kw; rb += 32) {
     __syncthreads();
     for (int q = threadIdx.x; q < 32 * vw / 4; q += WT) {
       const int i = (q * 4) / vw, cc = (q * 4) % vw;
-      *reinterpret_cast<float4*>(buf + i * lb + cc) =
-          *reinterpret_cast<const float4*>(X + (long long)(rb + i) * vw + cc);
+      *reinterpret_cast<float4*>(buf + i * lb + cc) = ld4s(X + (long long)(rb + i) * vw + cc);
     }
     __syncthreads();
     if (c < vw) {
@@ -573,7 +620,8 @@ __device__ __forceinline__ void rows_times_x(const float* A, int lda, const floa
 
 struct OutParams {
   int NT, Tp, kw, vw, colout, H, T, V;
-  const float *slots, *w, *Qt, *P, *q, *k, *G, *base;
+  const xs_t* slots;
+  const float *w, *Qt, *P, *q, *k, *G, *base;
   float *o, *d;
   __bf16* out;
 };
@@ -582,7 +630,7 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
   extern __shared__ __align__(16) float sm[];
   const int ch = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw;
   const long long tb = (long long)s * p.Tp + ch * WBT;
-  const float* X0 = p.slots + ((long long)s * (p.NT + 1) + ch) * kw * vw;
+  const xs_t* X0 = p.slots + ((long long)s * (p.NT + 1) + ch) * kw * vw;
   if (p.colout) {
     const int ld = kw + 1;
     float* Ql = sm;                 // [32][kw+1]
@@ -645,7 +693,7 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
     f4 acc[2] = {zero4(), zero4()};
 #pragma unroll 2
     for (int cb = 0; cb < vw; cb += 16) {
-      const float4 bx = *reinterpret_cast<const float4*>(X0 + (long long)rr * vw + cb + 4 * g);
+      const float4 bx = ld4s(X0 + (long long)rr * vw + cb + 4 * g);
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
         const float4 a4 = *reinterpret_cast<const float4*>(p.q + (tb + t2 * 16 + m) * vw + cb + 4 * g);
@@ -866,21 +914,32 @@ constexpr size_t bprep_smem(int kw) {
 // ---------------------------------------------------------------------------
 struct GradParams {
   int NT, Tp, kw, vw, excl, colout;
-  const float *k, *x, *q, *G, *dO, *o, *w, *dw, *Xslots, *Lslots, *Pp;
+  const float *k, *x, *q, *G, *dO, *o, *w, *dw, *Pp;
+  const xs_t* Xslots;
+  const ls_t* Lslots;
   float *dk, *dx, *dq, *dg;
 };
 
-__global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
+// Eight waves (two per SIMD, so one wave's loads overlap another's matrix
+// work), each owning the 16-row blocks rb = wave + 8 q of the state.
+constexpr int GW = 8;
+constexpr int GT = GW * 64;
+constexpr int GRB = WMAX / 16 / GW;
+
+__global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   extern __shared__ __align__(16) float sm[];
-  const int ch = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw;
+  int ch, s;
+  xcd_map(blockIdx.x, p.NT, gridDim.x / p.NT, ch, s);
+  const int kw = p.kw, vw = p.vw;
   const long long tb = (long long)s * p.Tp + ch * WBT;
   const long long slot = (long long)s * (p.NT + 1) + ch;
-  const float* X0 = p.Xslots + slot * kw * vw;
-  const float* XC = X0 + (long long)kw * vw;
-  const float* Lm = p.Lslots + slot * kw * vw;
-  // LDS: the token Grams M1, M2 [32][33]
+  const xs_t* X0 = p.Xslots + slot * kw * vw;
+  const xs_t* XC = X0 + (long long)kw * vw;
+  const ls_t* Lm = p.Lslots + slot * kw * vw;
+  // LDS: the token Grams M1, M2 [32][33], rowsum(X_C (.) lam) [kw]
   float* M1 = sm;
   float* M2 = M1 + WBT * MS;
+  float* RS = M2 + WBT * MS;
   const int r = threadIdx.x;
   const int wv_ = r >> 6, l = r & 63, g = l >> 4, m = l & 15;
   const int nrb = kw / 16, nvb = vw / 16;
@@ -890,15 +949,20 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
   // (column output) over this wave's 16-row blocks of the state, kept in
   // accumulators (lane (g, n): tokens 4g..4g+3 of state row 16 rb + n) for
   // phase 3, and the token Grams M1 = dw w^T, M2 = Y w^T (one 16 x 16 block of
-  // each per wave), all from 16-byte global loads of the rows involved.
-  f4 aX[WRB][2], aL[WRB][2], aO[WRB][2];
+  // each per wave of the first four), all from 16-byte global loads of the
+  // rows involved.
+  f4 aX[GRB][2], aL[GRB][2], aO[GRB][2];
+  float rs[GRB];  // partial rowsum(X_C (.) lam) of state row 16 rb + m over this lane's columns
 #pragma unroll
-  for (int q = 0; q < WRB; ++q)
+  for (int q = 0; q < GRB; ++q) {
+    rs[q] = 0.f;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) aX[q][t2] = aL[q][t2] = aO[q][t2] = zero4();
+  }
   {
     f4 m1a = zero4(), m2a = zero4();
-    const int bi = wv_ >> 1, bj = wv_ & 1;
+    const int bi = (wv_ >> 1) & 1, bj = wv_ & 1;
+    const bool gram = wv_ < 4;  // one 16 x 16 block of M1 and M2 per wave of the first four
 #pragma unroll 2
     for (int cb = 0; cb < vw; cb += 16) {
       float4 adw[2], aw[2], ay[2];
@@ -910,12 +974,14 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
         ay[t2] = *reinterpret_cast<const float4*>(Y + o);
       }
 #pragma unroll
-      for (int q = 0; q < WRB; ++q) {
-        const int rb = wv_ + 4 * q;
+      for (int q = 0; q < GRB; ++q) {
+        const int rb = wv_ + GW * q;
         if (rb < nrb) {
           const long long o = (long long)(rb * 16 + m) * vw + cb + 4 * g;
-          const float4 bx = *reinterpret_cast<const float4*>(X0 + o);
-          const float4 bl = *reinterpret_cast<const float4*>(Lm + o);
+          const float4 bx = ld4s(X0 + o);
+          const float4 bl = ld4s(Lm + o);
+          const float4 bc = ld4s(XC + o);
+          rs[q] += bc.x * bl.x + bc.y * bl.y + bc.z * bl.z + bc.w * bl.w;
 #pragma unroll
           for (int t2 = 0; t2 < 2; ++t2) {
             aX[q][t2] = mfma4(adw[t2].x, bx.x, aX[q][t2]);
@@ -935,47 +1001,47 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
           }
         }
       }
-      m1a = mfma4(adw[bi].x, aw[bj].x, m1a);
-      m1a = mfma4(adw[bi].y, aw[bj].y, m1a);
-      m1a = mfma4(adw[bi].z, aw[bj].z, m1a);
-      m1a = mfma4(adw[bi].w, aw[bj].w, m1a);
-      m2a = mfma4(ay[bi].x, aw[bj].x, m2a);
-      m2a = mfma4(ay[bi].y, aw[bj].y, m2a);
-      m2a = mfma4(ay[bi].z, aw[bj].z, m2a);
-      m2a = mfma4(ay[bi].w, aw[bj].w, m2a);
+if (gram) {
+              m1a = mfma4(adw[bi].x, aw[bj].x, m1a);
+        m1a = mfma4(adw[bi].y, aw[bj].y, m1a);
+        m1a = mfma4(adw[bi].z, aw[bj].z, m1a);
+        m1a = mfma4(adw[bi].w, aw[bj].w, m1a);
+        m2a = mfma4(ay[bi].x, aw[bj].x, m2a);
+        m2a = mfma4(ay[bi].y, aw[bj].y, m2a);
+        m2a = mfma4(ay[bi].z, aw[bj].z, m2a);
+        m2a = mfma4(ay[bi].w, aw[bj].w, m2a);
+      }
     }
+    if (gram)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = bi * 16 + 4 * g + e, j = bj * 16 + m;
-      M1[i * MS + j] = j < i ? m1a[e] : 0.f;
-      M2[i * MS + j] = j <= i ? m2a[e] : 0.f;
-    }
+      for (int e = 0; e < 4; ++e) {
+        const int i = bi * 16 + 4 * g + e, j = bj * 16 + m;
+        M1[i * MS + j] = j < i ? m1a[e] : 0.f;
+        M2[i * MS + j] = j <= i ? m2a[e] : 0.f;
+      }
   }
-  // rowsum(X_C (.) lam) for this thread's key coordinate
-  float rsum = 0.f;
-  if (r < kw) {
-    const float* xr = XC + (long long)r * vw;
-    const float* lr = Lm + (long long)r * vw;
-#pragma unroll 8
-    for (int c = 0; c < vw; c += 4) {
-      const float4 a4 = *reinterpret_cast<const float4*>(xr + c);
-      const float4 b4 = *reinterpret_cast<const float4*>(lr + c);
-      rsum += a4.x * b4.x + a4.y * b4.y + a4.z * b4.z + a4.w * b4.w;
-    }
+  // rowsum(X_C (.) lam): the four lane groups' partials of each state row
+#pragma unroll
+  for (int q = 0; q < GRB; ++q) {
+    float v = rs[q];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    const int rb = wv_ + GW * q;
+    if (rb < nrb && g == 0) RS[rb * 16 + m] = v;
   }
   // phase 2 (row output): dq = (dO e^G) X0 + Pp w on matrix cores, this wave's
   // 16-column blocks of the value axis
   if (!p.colout) {
     const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
 #pragma unroll
-    for (int q = 0; q < WRB; ++q) {
-      const int nb = wv_ + 4 * q;
+    for (int q = 0; q < GRB; ++q) {
+      const int nb = wv_ + GW * q;
       if (nb >= nvb) continue;
       f4 acc[2] = {zero4(), zero4()};
       for (int rb = 0; rb < nrb; ++rb) {
         float bx[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bx[e] = X0[(long long)(rb * 16 + 4 * g + e) * vw + nb * 16 + m];
+        for (int e = 0; e < 4; ++e) bx[e] = (float)X0[(long long)(rb * 16 + 4 * g + e) * vw + nb * 16 + m];
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2) {
           const long long o = (tb + t2 * 16 + m) * kw + rb * 16 + 4 * g;
@@ -1019,8 +1085,8 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
     return p.excl ? (i > 0 ? p.G[(tb + i - 1) * kw + rr] : 0.f) : p.G[(tb + i) * kw + rr];
   };
 #pragma unroll
-  for (int q = 0; q < WRB; ++q) {
-    const int rb = wv_ + 4 * q;
+  for (int q = 0; q < GRB; ++q) {
+    const int rb = wv_ + GW * q;
     if (rb >= nrb) continue;
     const int rr = rb * 16 + m;  // this lane's state row (output column)
     const float gl = p.G[(tb + WBT - 1) * kw + rr];
@@ -1093,7 +1159,7 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
   // before the decay); the last row adds rowsum(X_C lam); dg is its in-chunk
   // reverse cumulative sum.
   if (r >= kw) return;
-  float run = rsum;
+  float run = RS[r];
 #pragma unroll 8
   for (int i = WBT - 1; i >= 0; --i) {
     const long long o = (tb + i) * kw + r;
@@ -1106,7 +1172,7 @@ __global__ __launch_bounds__(WT) void k_w_grad(GradParams p) {
   }
 }
 
-constexpr size_t grad_smem(int) { return 2 * WBT * MS * sizeof(float); }
+constexpr size_t grad_smem(int kw) { return (2 * WBT * MS + kw) * sizeof(float); }
 
 // ---------------------------------------------------------------------------
 // Source closure (per token): cotangents of e, chi, z back to u^, delta, k^, q^,
@@ -1307,10 +1373,11 @@ WideDims wide_dims(int B, int T, int H, int r, int V) {
 struct WCarver {
   char* base;
   size_t off = 0;
-  float* take(size_t count) {
+  template <class T = float>
+  T* take(size_t count) {
     off = (off + 255) & ~size_t(255);
-    float* p = base ? reinterpret_cast<float*>(base + off) : nullptr;
-    off += count * sizeof(float);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += count * sizeof(T);
     return p;
   }
 };
@@ -1318,7 +1385,8 @@ struct WCarver {
 struct WideFwd {
   float *G, *uh, *kh, *qh, *xC, *vC, *gam, *rs;
   float *delta, *oC, *d, *e, *chi, *z, *wS;
-  float *AC, *AS, *PS, *XC, *XS;
+  float *AC, *AS, *PS;
+  xs_t *XC, *XS;
   float *W, *U, *Kh, *Qt, *Gam;
 };
 
@@ -1335,8 +1403,8 @@ WideFwd carve_wide_fwd(void* saved, void* scratch, const WideDims& d, size_t* sa
   w.delta = c.take(pk); w.oC = c.take(pk); w.d = c.take(pk); w.e = c.take(pk);
   w.chi = c.take(pk); w.wS = c.take(pv);
   w.AC = c.take(mat); w.AS = c.take(mat); w.PS = c.take(mat);
-  w.XC = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.KP);
-  w.XS = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.VP);
+  w.XC = c.take<xs_t>((size_t)d.n * (d.NT + 1) * d.KP * d.KP);
+  w.XS = c.take<xs_t>((size_t)d.n * (d.NT + 1) * d.KP * d.VP);
   w.Gam = c.take((size_t)d.n * d.NT * d.KP);
   if (saved_bytes) *saved_bytes = c.off + 256;
   WCarver t{(char*)scratch};
@@ -1348,7 +1416,9 @@ WideFwd carve_wide_fwd(void* saved, void* scratch, const WideDims& d, size_t* sa
 }
 
 struct WideBwd {
-  float *dO, *LC, *LS, *dU, *Wn, *Kn, *Ia, *Pp;
+  float* dO;
+  ls_t *LC, *LS;
+  float *dU, *Wn, *Kn, *Ia, *Pp;
   float *dwS, *dwC, *dd, *de, *dchi, *dgS;
   float *duh, *ddelta, *dkh, *dqh, *dkC, *dxC, *dqC, *dgC;
 };
@@ -1359,8 +1429,8 @@ WideBwd carve_wide_bwd(void* base, const WideDims& d, size_t* total) {
   const size_t pm = d.KP > d.VP ? pk : pv;
   WideBwd w;
   w.dO = c.take(pv);
-  w.LC = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.KP);
-  w.LS = c.take((size_t)d.n * (d.NT + 1) * d.KP * d.VP);
+  w.LC = c.take<ls_t>((size_t)d.n * (d.NT + 1) * d.KP * d.KP);
+  w.LS = c.take<ls_t>((size_t)d.n * (d.NT + 1) * d.KP * d.VP);
   w.dU = c.take(pm); w.Wn = c.take(pk); w.Kn = c.take(pk); w.Ia = c.take(pk);
   w.Pp = c.take((size_t)d.n * d.NT * WBT * WBT);
   w.dwS = c.take(pv); w.dwC = c.take(pk);
@@ -1385,7 +1455,7 @@ void launch_wprep(const OpParams& op, int n, hipStream_t st) {
 
 void launch_wstate(const char* name, const WStateParams& sp, int n, hipStream_t st) {
   SD_SMEM_ONCE(k_w_state, (int)state_smem(WMAX, true));
-  SD_LAUNCH(name, k_w_state, dim3(sp.vw / STILE, n), dim3(WT), state_smem(sp.kw, sp.Ia != nullptr),
+  SD_LAUNCH(name, k_w_state, dim3(sp.vw / STILE * n), dim3(ST), state_smem(sp.kw, sp.Ia != nullptr),
             st, sp);
 }
 
@@ -1493,7 +1563,7 @@ int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void*
   gs.k = f.d; gs.x = f.e; gs.q = f.chi; gs.G = f.G; gs.dO = w.dO; gs.o = nullptr;
   gs.w = f.wS; gs.dw = w.dwS; gs.Xslots = f.XS; gs.Lslots = w.LS; gs.Pp = nullptr;
   gs.dk = w.dd; gs.dx = w.de; gs.dq = w.dchi; gs.dg = w.dgS;
-  SD_LAUNCH("k_w_grad_s", k_w_grad, dim3(d.NT, d.n), dim3(WT), grad_smem(d.KP), st, gs);
+  SD_LAUNCH("k_w_grad_s", k_w_grad, dim3(d.NT * d.n), dim3(GT), grad_smem(d.KP), st, gs);
 
   SrcBwdParams sb{};
   sb.in = *in; sb.Tp = d.Tp; sb.KP = d.KP; sb.VP = d.VP;
@@ -1521,7 +1591,7 @@ int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void*
   gc.k = f.uh; gc.x = f.xC; gc.q = f.kh; gc.G = f.G; gc.dO = w.dd; gc.o = f.oC;
   gc.w = f.delta; gc.dw = w.dwC; gc.Xslots = f.XC; gc.Lslots = w.LC; gc.Pp = w.Pp;
   gc.dk = w.dkC; gc.dx = w.dxC; gc.dq = w.dqC; gc.dg = w.dgC;
-  SD_LAUNCH("k_w_grad_c", k_w_grad, dim3(d.NT, d.n), dim3(WT), grad_smem(d.KP), st, gc);
+  SD_LAUNCH("k_w_grad_c", k_w_grad, dim3(d.NT * d.n), dim3(GT), grad_smem(d.KP), st, gc);
 
   FinalParams fp{};
   fp.in = *in; fp.Tp = d.Tp; fp.KP = d.KP;
