@@ -240,6 +240,13 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
     Gs[i * ld + c] = p.G[o];
     if (p.colout) qs[i * ld + c] = p.q[o];
   }
+  // this thread's value column for U = A v, loaded before any store of the
+  // kernel (a load issued after a store waits for it: one counter retires both)
+  const int c = threadIdx.x;
+  float vv[WBT];
+  if (c < vw)
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) vv[i] = p.v[(tb + i) * vw + c];
   __syncthreads();
   // L_ij = sum_c x_ic k_jc e^{Gx_ic - G_jc} (j < i); P_ij = sum_c q_ic k_jc e^{G_ic - G_jc} (j <= i)
   int* wl = reinterpret_cast<int*>(Ps + WBT * MS);
@@ -285,7 +292,6 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
     if (p.colout) p.P[mb + idx] = Ps[(idx >> 5) * MS + (idx & 31)];
   }
   // W = A x~, Kh, Qt, Gam: one key coordinate per thread
-  const int c = threadIdx.x;
   if (c < kw) {
     float xt[WBT];
 #pragma unroll
@@ -305,9 +311,6 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
   }
   // U = A v: one value column per thread
   if (c < vw) {
-    float vv[WBT];
-#pragma unroll
-    for (int i = 0; i < WBT; ++i) vv[i] = p.v[(tb + i) * vw + c];
 #pragma unroll
     for (int i = 0; i < WBT; ++i) {
       float a = 0.f;
@@ -684,6 +687,7 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
   }
   __syncthreads();
   const int nrb = kw / 16;
+  float ro[WRB][2][4], rbase[WRB][2][4];
 #pragma unroll
   for (int q = 0; q < WRB; ++q) {
     const int rb = w + 4 * q;
@@ -727,10 +731,24 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
         if (wild)
           for (int j = 0; j <= i; ++j)
             v += Ml[i * MS + j] * p.k[(tb + j) * kw + rr] * __expf(gi - p.G[(tb + j) * kw + rr]);
-        p.o[o] = v;
-        p.d[o] = p.base[o] + v;
+        ro[q][t2][e] = v;
+        rbase[q][t2][e] = p.base[o];
       }
     }
+  }
+  // stores after every row block's loads (a load issued after a store waits for it)
+#pragma unroll
+  for (int q = 0; q < WRB; ++q) {
+    const int rb = w + 4 * q;
+    if (rb >= nrb) continue;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const long long o = (tb + t2 * 16 + 4 * g + e) * kw + rb * 16 + m;
+        p.o[o] = ro[q][t2][e];
+        p.d[o] = rbase[q][t2][e] + ro[q][t2][e];
+      }
   }
 }
 
@@ -859,8 +877,20 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
       p.Pp[mb + idx] = Pl[(idx >> 5) * MS + (idx & 31)];
   }
   __syncthreads();
-  // value side: rhs and dU, one value column per thread
+  // The key side's inputs are loaded first, before any store of the value
+  // side: a load issued after a store waits for it (one counter retires both).
   const int c = threadIdx.x;
+  float kg[WBT], kk[WBT], kx[WBT], ks2[WBT];
+  if (c < kw)
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) {
+      const long long o = (tb + i) * kw + c;
+      kg[i] = p.G[o];
+      kk[i] = p.k[o];
+      kx[i] = p.x[o];
+      ks2[i] = p.colout ? p.q[o] : p.dO[o];
+    }
+  // value side: rhs and dU, one value column per thread
   if (c < vw) {
     for (int i = 0; i < WBT; ++i)
       cv[i * WT + tid] = p.colout ? p.dO[(tb + i) * vw + c] : p.q[(tb + i) * vw + c];
@@ -877,15 +907,15 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
   }
   // key side: Wn, Kn, Ia, one key coordinate per thread
   if (c < kw) {
-    const float gl = p.G[(tb + WBT - 1) * kw + c];
+    const float gl = kg[WBT - 1];
+#pragma unroll
     for (int i = 0; i < WBT; ++i) {
       const long long o = (tb + i) * kw + c;
-      const float gi = p.G[o];
-      cv[i * WT + tid] = p.k[o] * __expf(gl - gi);
-      const float gx = p.excl ? (i > 0 ? p.G[o - kw] : 0.f) : gi;
-      p.Kn[o] = -p.x[o] * __expf(gx);
-      const float src = p.colout ? p.q[o] : p.dO[o];
-      p.Ia[o] = src * __expf(gi);
+      const float gi = kg[i];
+      cv[i * WT + tid] = kk[i] * __expf(gl - gi);
+      const float gx = p.excl ? (i > 0 ? kg[i - 1] : 0.f) : gi;
+      p.Kn[o] = -kx[i] * __expf(gx);
+      p.Ia[o] = ks2[i] * __expf(gi);
     }
     for (int m = 0; m < WBT; ++m) {
       float a = 0.f;
@@ -936,10 +966,9 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   const xs_t* X0 = p.Xslots + slot * kw * vw;
   const xs_t* XC = X0 + (long long)kw * vw;
   const ls_t* Lm = p.Lslots + slot * kw * vw;
-  // LDS: the token Grams M1, M2 [32][33], rowsum(X_C (.) lam) [kw]
+  // LDS: the token Grams M1, M2 [32][33]
   float* M1 = sm;
   float* M2 = M1 + WBT * MS;
-  float* RS = M2 + WBT * MS;
   const int r = threadIdx.x;
   const int wv_ = r >> 6, l = r & 63, g = l >> 4, m = l & 15;
   const int nrb = kw / 16, nvb = vw / 16;
@@ -1021,13 +1050,11 @@ if (gram) {
       }
   }
   // rowsum(X_C (.) lam): the four lane groups' partials of each state row
+  // (every lane of the row ends with the total)
 #pragma unroll
   for (int q = 0; q < GRB; ++q) {
-    float v = rs[q];
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    const int rb = wv_ + GW * q;
-    if (rb < nrb && g == 0) RS[rb * 16 + m] = v;
+    rs[q] += __shfl_xor(rs[q], 16);
+    rs[q] += __shfl_xor(rs[q], 32);
   }
   // phase 2 (row output): dq = (dO e^G) X0 + Pp w on matrix cores, this wave's
   // 16-column blocks of the value axis
@@ -1084,6 +1111,7 @@ if (gram) {
   auto gx_g = [&](int i, int rr) {
     return p.excl ? (i > 0 ? p.G[(tb + i - 1) * kw + rr] : 0.f) : p.G[(tb + i) * kw + rr];
   };
+  float rdx[GRB][2][4], rdk[GRB][2][4], rdq[GRB][2][4], rdg[GRB][2][4];
 #pragma unroll
   for (int q = 0; q < GRB; ++q) {
     const int rb = wv_ + GW * q;
@@ -1091,7 +1119,10 @@ if (gram) {
     const int rr = rb * 16 + m;  // this lane's state row (output column)
     const float gl = p.G[(tb + WBT - 1) * kw + rr];
     const bool wild = -gl > WILD;
-    float kt[2][4], yt[2][4], xt[2][4];
+    // the lane's operands at tokens jb * 16 + 4 g + e of row rr: the same
+    // tokens its outputs (t2 = jb) cover, so the decay closure below needs no
+    // further loads
+    float kt[2][4], yt[2][4], xt[2][4], kr[2][4], yr[2][4], xr[2][4], orw[2][4];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
@@ -1099,9 +1130,13 @@ if (gram) {
         const int j = jb * 16 + 4 * g + e;
         const long long o = (tb + j) * kw + rr;
         const float gj = p.G[o];
-        kt[jb][e] = wild ? 0.f : p.k[o] * __expf(-gj);
-        yt[jb][e] = wild ? 0.f : Yk[o] * __expf(gj);
-        xt[jb][e] = wild ? 0.f : p.x[o] * __expf(gx_g(j, rr));
+        kr[jb][e] = p.k[o];
+        yr[jb][e] = Yk[o];
+        xr[jb][e] = p.x[o];
+        orw[jb][e] = p.colout ? 0.f : p.o[o];
+        kt[jb][e] = wild ? 0.f : kr[jb][e] * __expf(-gj);
+        yt[jb][e] = wild ? 0.f : yr[jb][e] * __expf(gj);
+        xt[jb][e] = wild ? 0.f : xr[jb][e] * __expf(gx_g(j, rr));
       }
     const float egl = __expf(gl);
 #pragma unroll
@@ -1147,32 +1182,77 @@ if (gram) {
             dq = c2;
           }
         }
-        p.dx[o] = dx;
-        p.dk[o] = dk;
-        if (p.colout) p.dq[o] = dq;
+        rdx[q][t2][e] = dx;
+        rdk[q][t2][e] = dk;
+        rdq[q][t2][e] = dq;
       }
     }
+    // decay closure of row rr: dG = q dq - k dk (column) / o dO - k dk (row)
+    // + x dx (of the next token when the erase reads before the decay), and
+    // dg = rowsum(X_C lam) + the in-chunk reverse cumulative sum of dG.  The
+    // lane holds tokens t2 * 16 + 4 g + e; the next token of e = 3 sits in lane
+    // group g + 1 (g = 3, t2 = 0: group 0 of t2 = 1).
+    float dG[2][4], xd[2][4];
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dG[t2][e] = -kr[t2][e] * rdk[q][t2][e] +
+                    (p.colout ? yr[t2][e] * rdq[q][t2][e] : orw[t2][e] * yr[t2][e]);
+        xd[t2][e] = xr[t2][e] * rdx[q][t2][e];
+      }
+    if (p.excl) {
+      const int src = g < 3 ? l + 16 : l - 48;
+      const float n0 = __shfl(xd[0][0], src), n1 = __shfl(xd[1][0], src);
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int e = 0; e < 3; ++e) dG[t2][e] += xd[t2][e + 1];
+      dG[0][3] += g < 3 ? n0 : n1;
+      dG[1][3] += g < 3 ? n1 : 0.f;
+    } else {
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dG[t2][e] += xd[t2][e];
+    }
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int e = 2; e >= 0; --e) dG[t2][e] += dG[t2][e + 1];  // suffix within the lane
+    float later[2], total1 = 0.f;  // sums of the later lane groups' tokens, per t2
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      const float s1 = __shfl(dG[t2][0], (l + 16) & 63), s2 = __shfl(dG[t2][0], (l + 32) & 63),
+                  s3 = __shfl(dG[t2][0], (l + 48) & 63);
+      later[t2] = (g < 3 ? s1 : 0.f) + (g < 2 ? s2 : 0.f) + (g < 1 ? s3 : 0.f);
+      if (t2 == 1) total1 = dG[1][0] + s1 + s2 + s3;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      rdg[q][1][e] = rs[q] + dG[1][e] + later[1];
+      rdg[q][0][e] = rs[q] + dG[0][e] + later[0] + total1;
+    }
   }
-  __syncthreads();  // dx, dk, dq of the whole chunk written
-  // phase 4, one key coordinate per thread: decay closure dG = q dq - k dk
-  // (column) / o dO - k dk (row) + x dx (one token earlier when the erase reads
-  // before the decay); the last row adds rowsum(X_C lam); dg is its in-chunk
-  // reverse cumulative sum.
-  if (r >= kw) return;
-  float run = RS[r];
-#pragma unroll 8
-  for (int i = WBT - 1; i >= 0; --i) {
-    const long long o = (tb + i) * kw + r;
-    float dG = -p.k[o] * p.dk[o];
-    dG += p.colout ? Yk[o] * p.dq[o] : p.o[o] * p.dO[o];
-    const int ix = p.excl ? i + 1 : i;
-    if (ix < WBT) dG += p.x[(tb + ix) * kw + r] * p.dx[(tb + ix) * kw + r];
-    run += dG;
-    p.dg[o] = run;
+  // stores after every row block's loads (a load issued after a store waits for it)
+#pragma unroll
+  for (int q = 0; q < GRB; ++q) {
+    const int rb = wv_ + GW * q;
+    if (rb >= nrb) continue;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const long long o = (tb + t2 * 16 + 4 * g + e) * kw + rb * 16 + m;
+        p.dx[o] = rdx[q][t2][e];
+        p.dk[o] = rdk[q][t2][e];
+        if (p.colout) p.dq[o] = rdq[q][t2][e];
+        p.dg[o] = rdg[q][t2][e];
+      }
   }
 }
 
-constexpr size_t grad_smem(int kw) { return (2 * WBT * MS + kw) * sizeof(float); }
+constexpr size_t grad_smem(int) { return 2 * WBT * MS * sizeof(float); }
 
 // ---------------------------------------------------------------------------
 // Source closure (per token): cotangents of e, chi, z back to u^, delta, k^, q^,

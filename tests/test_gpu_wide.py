@@ -64,6 +64,7 @@ def _check_fb(B, T, H, r, V, seed, decay="softplus", with_state=True, cot="all",
     (2, 33, 1, 200, 136, 53, "softplus"),   # widths not a multiple of 32
     (1, 100, 2, 160, 64, 55, "mixed"),      # wide keys, narrow values; strongly decaying coordinates
     (1, 64, 1, 144, 144, 57, "small"),
+    (2, 70, 4, 160, 144, 59, "softplus"),  # B*H = 8: the XCD-grouped workgroup mapping
 ])
 def test_wide_forward_backward_matches_oracle(B, T, H, r, V, seed, decay):
     _check_fb(B, T, H, r, V, seed, decay)
