@@ -1030,15 +1030,16 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
           }
         }
       }
-if (gram) {
-              m1a = mfma4(adw[bi].x, aw[bj].x, m1a);
-        m1a = mfma4(adw[bi].y, aw[bj].y, m1a);
-        m1a = mfma4(adw[bi].z, aw[bj].z, m1a);
-        m1a = mfma4(adw[bi].w, aw[bj].w, m1a);
-        m2a = mfma4(ay[bi].x, aw[bj].x, m2a);
-        m2a = mfma4(ay[bi].y, aw[bj].y, m2a);
-        m2a = mfma4(ay[bi].z, aw[bj].z, m2a);
-        m2a = mfma4(ay[bi].w, aw[bj].w, m2a);
+      if (gram) {  // selects, not indexing: a runtime index would put the arrays in scratch
+        const float4 da = bi ? adw[1] : adw[0], ya = bi ? ay[1] : ay[0], wb = bj ? aw[1] : aw[0];
+        m1a = mfma4(da.x, wb.x, m1a);
+        m1a = mfma4(da.y, wb.y, m1a);
+        m1a = mfma4(da.z, wb.z, m1a);
+        m1a = mfma4(da.w, wb.w, m1a);
+        m2a = mfma4(ya.x, wb.x, m2a);
+        m2a = mfma4(ya.y, wb.y, m2a);
+        m2a = mfma4(ya.z, wb.z, m2a);
+        m2a = mfma4(ya.w, wb.w, m2a);
       }
     }
     if (gram)
