@@ -25,6 +25,8 @@
 // Every decay factor is exp(a - b) with a <= b prefix sums inside one chunk (no
 // reciprocal decays), formed per element; padding tokens and coordinates are
 // zero and stay neutral.
+#include <type_traits>
+
 #include "sd_common.cuh"
 #include "sd_internal.h"
 
@@ -154,7 +156,8 @@ struct OpParams {
   int NT, Tp, kw, vw, excl, colout;
   const float *k, *x, *v, *q, *G;  // k, x, G [Tp][kw]; v [Tp][vw]; q [Tp][kw] (col) / [Tp][vw] (row)
   float *A, *P;                    // [NT][32][32]
-  float *W, *U, *Kh, *Qt, *Gam;    // W, Kh, Qt [Tp][kw]; U [Tp][vw]; Gam [NT][kw]
+  _Float16 *Wneg, *Kt;             // state-pass panels: -W [Tp][kw], K^ transposed per chunk [NT][kw][32]
+  float *U, *Qt, *Gam;             // Qt [Tp][kw]; U [Tp][vw]; Gam [NT][kw]
 };
 
 // G of the erase read for token i at coordinate c: the prefix before token i
@@ -291,8 +294,11 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
     p.A[mb + idx] = Ls[(idx >> 5) * MS + (idx & 31)];
     if (p.colout) p.P[mb + idx] = Ps[(idx >> 5) * MS + (idx & 31)];
   }
-  // W = A x~, Kh, Qt, Gam: one key coordinate per thread
+  // W = A x~, K^, Qt, Gam: one key coordinate per thread (-W and K^ in fp16 for
+  // the state pass, K^ transposed per chunk: this thread's 32 tokens contiguous)
   if (c < kw) {
+    _Float16* const kt = p.Kt + (((long long)s * p.NT + ch) * kw + c) * WBT;
+    f16x8 kv;
     float xt[WBT];
 #pragma unroll
     for (int i = 0; i < WBT; ++i) xt[i] = xs[i * ld + c] * __expf(gx_at(Gs, ld, i, c, p.excl));
@@ -303,8 +309,9 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
 #pragma unroll
       for (int m = 0; m <= i; ++m) a += Ls[i * MS + m] * xt[m];
       const long long o = (tb + i) * kw + c;
-      p.W[o] = a;
-      p.Kh[o] = ks[i * ld + c] * __expf(gl - Gs[i * ld + c]);
+      p.Wneg[o] = (_Float16)(-a);
+      kv[i & 7] = (_Float16)(ks[i * ld + c] * __expf(gl - Gs[i * ld + c]));
+      if ((i & 7) == 7) *reinterpret_cast<f16x8*>(kt + i - 7) = kv;
       if (p.colout) p.Qt[o] = qs[i * ld + c] * __expf(Gs[i * ld + c]);
     }
     p.Gam[((long long)s * p.NT + ch) * kw + c] = __expf(gl);
@@ -326,101 +333,247 @@ constexpr size_t prep_smem(int kw) {
 }
 
 // ---------------------------------------------------------------------------
-// Sequential chunk pass over a 16-column tile of X [kw x vw]:
-//   slot[ch] = X;  w = U - W X;  X = Gamma X + K^T w (+ Ia^T Ib)
+// Sequential chunk pass over a 32-column tile of X [kw x vw]:
+//   slot[ch] = X;  w = U + Wneg X;  X = Gamma X + K^T w (+ At^T Ib)
 // forward (chunks ascending; slot NT = final state) or reverse (descending).
 // ---------------------------------------------------------------------------
 struct WStateParams {
   int NT, Tp, kw, vw, rows, cols, rev;
-  const float *W, *U, *K, *Gam, *Ia, *Ib;
+  const void* Wneg;  // -W, token-major [Tp][kw] (fp16 forward, bf16 reverse)
+  const void* Kt;    // K^T per chunk [NT][kw][32] (fp16 forward, bf16 reverse)
+  const __bf16* At;  // injection A^T per chunk [NT][kw][32] (reverse only; nullable)
+  const float *U, *Gam, *Ib;  // U, Ib [Tp][vw]; Gam [NT][kw]
   void* slots;  // xs_t (forward) or ls_t (reverse)
   float* wout;
   const float* init; int init_t;
   float* fin; int fin_t;
 };
 
-// Matrix-core form.  A workgroup owns a 32-column tile (two 16-column
-// halves).  The tile's rows are cut into 16-row blocks dealt round-robin to
-// the 8 waves (up to 2 per wave, two waves per SIMD so that one wave's LDS and
-// memory waits overlap the other's matrix work), each half held as an FP32 MFMA accumulator
-// (lane (g, n) holds rows 4g..4g+3 of column n).  Every product runs on
-// v_mfma_f32_16x16x4f32 with the sum index k = 4g + e carried by MFMA e and
-// lane group g, so an accumulator block is a B operand as it stands (no
-// transpose):
-//   w = U - W X0:      each wave sums its own row blocks, partials reduced
-//                      across the waves through LDS;
-//   X = Gamma X + K^T w (+ A^T B): the w accumulators are again B operands.
-// W is staged row-major [32][kw+4], K (and the injection A) transposed
-// [kw][36], the injection B tile transposed [32][36].  The next chunk's W, K
-// and A are loaded into registers while the current chunk computes.
-constexpr int WRB = WMAX / 16 / 4;  // row blocks per wave (four-wave kernels)
-constexpr int SW = 8;               // state-pass waves: two per SIMD
+// Matrix-core form on 16-bit MFMAs (v_mfma_f32_16x16x32_{f16,bf16}), as the
+// main kernels' state pass: a workgroup of 8 waves owns a 32-column tile of the
+// state, wave w holding the 16-row blocks w and w + 8 of both 16-column halves
+// in FP32 accumulators.  Per chunk step:
+//   the state X0 is staged into LDS split into high and low 16-bit halves,
+//   transposed ([column][row]), as the B operand of w = U + Wneg X0, which
+//   waves 0-3 form (one 16-token x 16-column tile each, over all kw rows);
+//   w is staged split the same way ([column][token]) as the B operand of
+//   X = Gamma X + K^T w (+ At^T Ib, reverse), which every wave forms for its
+//   own rows.
+// The panels Wneg, K^T and At are stored 16-bit by the prep kernels in the
+// order the MFMA operands read them, so each lane's fragment is one 16-byte
+// load; they, U, Gamma and Ib are fetched PF - 1 chunks ahead into a ring of
+// registers.  Forward: panels fp16 (W and K are bounded by construction), X
+// and w split into fp16 halves (~22 bits).  Reverse: bf16 throughout (its
+// exponent range keeps any scale of the cotangent), lambda, dw and Ib split
+// into bf16 halves.  Two barriers per step: the next step writes the X0
+// staging only after this step's second barrier (its readers, the w tiles,
+// are done), and the w staging only after its own first barrier.
+constexpr int WRB = WMAX / 16 / 4;   // row blocks per wave (four-wave kernels)
+constexpr int SW = 8;                // state-pass waves: two per SIMD
 constexpr int ST = SW * 64;
 constexpr int SRB = WMAX / 16 / SW;  // state-pass row blocks per wave
-constexpr int LDT = WBT + 4;        // row stride of the transposed panels
-constexpr int STILE = 32;           // state columns per workgroup
+constexpr int STILE = 32;            // state columns per workgroup
 constexpr int NSUB = STILE / 16;
-constexpr int NCMB = NSUB * 2 * 4;  // w values per lane: (half, token block, element)
-constexpr int CPW = NCMB / SW;      // of which each wave reduces CPW
-static_assert(NCMB % SW == 0, "w values split evenly over the waves");
-constexpr int PFQ = WBT * WMAX / 4 / ST;  // 16-byte pieces of one [32][kw] panel per thread (kw = 256)
-constexpr size_t state_smem(int kw, bool inj) {
-  return (size_t)(WBT * (kw + 4) + kw * LDT + (inj ? kw * LDT + STILE * LDT : 0) +
-                  (SW + 1) * NCMB * 64) * sizeof(float);
-}
+constexpr int WKS = WMAX / 32;       // K = 32 steps of the w product
+constexpr int SPF = 2;               // prefetch ring depth (chunks)
+constexpr int XLD = WMAX + 8;        // row stride (16-bit) of the staged X0
+constexpr int WLD = WBT + 8;         // row stride (16-bit) of the staged w
+constexpr size_t state_smem() { return (size_t)(2 * STILE * XLD + 2 * STILE * WLD) * 2; }
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Registers <-> one [32 tokens][kw] panel: piece q of thread t is element
-// (i, 4 c4) with i = (t + 256 q) % 32, c4 = (t + 256 q) / 32, so a wave's
-// transposed LDS writes land on consecutive tokens (distinct banks).
-struct PanelRegs {
-  float4 v[PFQ];
+template <bool REV> struct WStateT;
+template <> struct WStateT<false> {
+  using E = _Float16;
+  using V8 = f16x8;
+  using V4 = f16x4;
+  static __device__ __forceinline__ f4 mma(V8 a, V8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
 };
-__device__ __forceinline__ void panel_load(PanelRegs& r, const float* src, int kw) {
-#pragma unroll
-  for (int q = 0; q < PFQ; ++q) {
-    const int idx = threadIdx.x + ST * q, i = idx & 31, c = (idx >> 5) * 4;
-    r.v[q] = c < kw ? *reinterpret_cast<const float4*>(src + (long long)i * kw + c)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
+template <> struct WStateT<true> {
+  using E = __bf16;
+  using V8 = bf16x8;
+  using V4 = bf16x4;
+  static __device__ __forceinline__ f4 mma(V8 a, V8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
-}
-__device__ __forceinline__ void panel_store_rows(const PanelRegs& r, float* dst, int ld, int kw) {
+};
+
+template <bool REV>
+struct WFrags {
+  using V8 = typename WStateT<REV>::V8;
+  V8 W[WKS];                      // waves 0-3: Wneg rows of token block w & 1
+  V8 K[SRB];                      // K^T rows of this wave's row blocks, the chunk's 32 tokens
+  bf16x8 A[REV ? SRB : 1];        // At rows (reverse)
+  bf16x8 Bh[REV ? NSUB : 1], Bl[REV ? NSUB : 1];  // Ib columns, split (reverse)
+  f4 U;                           // waves 0-3: U tile (C-operand layout)
+  float4 G[SRB];                  // Gamma of this wave's rows 16 rb + 4 g .. + 3
+};
+
+// Chunk-uniform bases with 32-bit lane offsets throughout: 64-bit per-lane
+// addresses for the ~20 fragment loads of a chunk would not fit in registers
+// beside the prefetch ring.
+template <bool REV>
+__device__ __forceinline__ void wstate_load(const WStateParams& p, int s, int ch, int c0,
+                                            WFrags<REV>& f) {
+  using E = typename WStateT<REV>::E;
+  using V8 = typename WStateT<REV>::V8;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15, kq = g * 8;
+  const int kw = p.kw, vw = p.vw, nrb = kw / 16;
+  const long long tb = (long long)s * p.Tp + (long long)ch * WBT;
+  const long long cb = ((long long)s * p.NT + ch) * kw;  // chunk base of [kw][32] and [kw] panels
+  if (w < 4) {
+    const int tbk = w & 1, hh = w >> 1;
+    const E* Wc = static_cast<const E*>(p.Wneg) + tb * kw;
+    const unsigned wo = (unsigned)((tbk * 16 + m) * kw + kq);
 #pragma unroll
-  for (int q = 0; q < PFQ; ++q) {
-    const int idx = threadIdx.x + ST * q, i = idx & 31, c = (idx >> 5) * 4;
-    if (c < kw) *reinterpret_cast<float4*>(dst + i * ld + c) = r.v[q];
+    for (int ks = 0; ks < WKS; ++ks)
+      if (ks * 32 < kw) f.W[ks] = *reinterpret_cast<const V8*>(Wc + wo + ks * 32);
+    const float* Uc = p.U + tb * vw + c0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f.U[e] = Uc[(unsigned)((tbk * 16 + 4 * g + e) * vw + hh * 16 + m)];
   }
-}
-__device__ __forceinline__ void panel_store_t(const PanelRegs& r, float* dst, int kw) {
+  const E* Kc = static_cast<const E*>(p.Kt) + cb * WBT;
+  const float* Gc = p.Gam + cb;
 #pragma unroll
-  for (int q = 0; q < PFQ; ++q) {
-    const int idx = threadIdx.x + ST * q, i = idx & 31, c = (idx >> 5) * 4;
-    if (c < kw) {
-      dst[c * LDT + i] = r.v[q].x;
-      dst[(c + 1) * LDT + i] = r.v[q].y;
-      dst[(c + 2) * LDT + i] = r.v[q].z;
-      dst[(c + 3) * LDT + i] = r.v[q].w;
+  for (int q = 0; q < SRB; ++q) {
+    const int rb = w + SW * q;
+    if (rb < nrb) {
+      const unsigned ko = (unsigned)((rb * 16 + m) * WBT + kq);
+      f.K[q] = *reinterpret_cast<const V8*>(Kc + ko);
+      f.G[q] = *reinterpret_cast<const float4*>(Gc + (unsigned)(rb * 16 + 4 * g));
+      if constexpr (REV)
+        if (p.At) f.A[q] = *reinterpret_cast<const bf16x8*>(p.At + cb * WBT + ko);
+    }
+  }
+  if constexpr (REV) {
+    if (p.At) {
+      const float* Ic = p.Ib + tb * vw + c0;
+#pragma unroll
+      for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float x = Ic[(unsigned)((kq + j) * vw + h * 16 + m)];
+          const __bf16 hi = (__bf16)x;
+          f.Bh[h][j] = hi;
+          f.Bl[h][j] = (__bf16)(x - (float)hi);
+        }
     }
   }
 }
 
+// Four 16-bit values split from an FP32 accumulator fragment, stored as two
+// 8-byte pieces (high and low halves).
+template <class E, class V4>
+__device__ __forceinline__ void wsplit4(E* hi, E* lo, f4 v) {
+  V4 h, o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const E a = (E)v[e];
+    h[e] = a;
+    o[e] = (E)(v[e] - (float)a);
+  }
+  *reinterpret_cast<V4*>(hi) = h;
+  *reinterpret_cast<V4*>(lo) = o;
+}
+
+template <bool REV>
+__device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch, int c0,
+                                            const WFrags<REV>& f, f4 (&X)[SRB][NSUB], unsigned char* sm) {
+  using T = WStateT<REV>;
+  using E = typename T::E;
+  using V8 = typename T::V8;
+  using V4 = typename T::V4;
+  using S = typename std::conditional<REV, ls_t, xs_t>::type;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15, kq = g * 8;
+  const int kw = p.kw, vw = p.vw, nrb = kw / 16;
+  const long long tb = (long long)s * p.Tp + (long long)ch * WBT;
+  E* Xh = reinterpret_cast<E*>(sm);  // X0 [32 columns][XLD], high and low halves
+  E* Xl = Xh + STILE * XLD;
+  E* wh = Xl + STILE * XLD;          // w [32 columns][WLD]
+  E* wl = wh + STILE * WLD;
+  S* slot = static_cast<S*>(p.slots) + ((long long)s * (p.NT + 1) + ch) * kw * vw;
+  // slot[ch] = X0; X0 staged split and transposed for the w product
+#pragma unroll
+  for (int q = 0; q < SRB; ++q) {
+    const int rb = w + SW * q;
+    if (rb >= nrb) continue;
+#pragma unroll
+    for (int h = 0; h < NSUB; ++h) {
+      const int col = h * 16 + m, row = rb * 16 + 4 * g;
+      wsplit4<E, V4>(Xh + col * XLD + row, Xl + col * XLD + row, X[q][h]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) slot[(unsigned)((row + e) * vw + c0 + col)] = (S)X[q][h][e];
+    }
+  }
+  __syncthreads();
+  // w = U + Wneg X0 (waves 0-3, one 16 x 16 tile each; high and low halves of
+  // X0 in two accumulators so the two dependent chains interleave)
+  if (w < 4) {
+    const int tbk = w & 1, hh = w >> 1;
+    f4 a0 = f.U, a1 = zero4();
+    const E* bh = Xh + (hh * 16 + m) * XLD + kq;
+    const E* bl = Xl + (hh * 16 + m) * XLD + kq;
+#pragma unroll
+    for (int ks = 0; ks < WKS; ++ks)
+      if (ks * 32 < kw) {
+        a1 = T::mma(f.W[ks], *reinterpret_cast<const V8*>(bl + ks * 32), a1);
+        a0 = T::mma(f.W[ks], *reinterpret_cast<const V8*>(bh + ks * 32), a0);
+      }
+    f4 wv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[e] = a0[e] + a1[e];
+    const int col = hh * 16 + m, tok = tbk * 16 + 4 * g;
+    wsplit4<E, V4>(wh + col * WLD + tok, wl + col * WLD + tok, wv);
+    float* const wo = p.wout + tb * vw + c0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wo[(unsigned)((tok + e) * vw + col)] = wv[e];
+  }
+  // X = Gamma X (+ At^T Ib): independent of w, so it overlaps the w tiles
+#pragma unroll
+  for (int q = 0; q < SRB; ++q) {
+    const int rb = w + SW * q;
+    if (rb >= nrb) continue;
+    const float gv[4] = {f.G[q].x, f.G[q].y, f.G[q].z, f.G[q].w};
+#pragma unroll
+    for (int h = 0; h < NSUB; ++h) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) X[q][h][e] *= gv[e];
+      if constexpr (REV) {
+        if (p.At) {
+          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.A[q], f.Bl[h], X[q][h], 0, 0, 0);
+          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.A[q], f.Bh[h], X[q][h], 0, 0, 0);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // X += K^T w
+#pragma unroll
+  for (int h = 0; h < NSUB; ++h) {
+    const V8 whv = *reinterpret_cast<const V8*>(wh + (h * 16 + m) * WLD + kq);
+    const V8 wlv = *reinterpret_cast<const V8*>(wl + (h * 16 + m) * WLD + kq);
+#pragma unroll
+    for (int q = 0; q < SRB; ++q) {
+      const int rb = w + SW * q;
+      if (rb >= nrb) continue;
+      X[q][h] = T::mma(f.K[q], wlv, X[q][h]);
+      X[q][h] = T::mma(f.K[q], whv, X[q][h]);
+    }
+  }
+}
+
+template <bool REV>
 __global__ __launch_bounds__(ST) void k_w_state(WStateParams p) {
-  extern __shared__ __align__(16) float sm[];
+  extern __shared__ __align__(16) unsigned char wsm[];
   int tile, s;
   xcd_map(blockIdx.x, p.vw / STILE, gridDim.x / (p.vw / STILE), tile, s);
-  const int kw = p.kw, vw = p.vw, c0 = tile * STILE;
+  const int kw = p.kw, c0 = tile * STILE, NT = p.NT;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
-  const int nrb = kw / 16, ldw = kw + 4;
-  const bool inj = p.Ia != nullptr;
-  float* Wl = sm;                       // W [32][kw+4]
-  float* Kt = Wl + WBT * ldw;           // K^T [kw][LDT]
-  float* At = Kt + kw * LDT;            // injection A^T [kw][LDT]
-  float* Bt = At + (inj ? kw * LDT : 0);  // injection B^T [32][LDT]
-  float* red = Bt + (inj ? STILE * LDT : 0);  // w partials [SW waves][NCMB][64]
-  float* wred = red + SW * NCMB * 64;          // reduced w [NCMB][64]
+  const int nrb = kw / 16;
   f4 X[SRB][NSUB];
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
@@ -437,147 +590,27 @@ __global__ __launch_bounds__(ST) void k_w_state(WStateParams p) {
         X[q][h][e] = v;
       }
   }
-  const long long sb = (long long)s * (p.NT + 1) * kw * vw;
-  auto tok0 = [&](int step) {
-    return (long long)s * p.Tp + (long long)(p.rev ? p.NT - 1 - step : step) * WBT;
-  };
-  PanelRegs nW, nK, nA;
-  panel_load(nW, p.W + tok0(0) * kw, kw);
-  panel_load(nK, p.K + tok0(0) * kw, kw);
-  if (inj) panel_load(nA, p.Ia + tok0(0) * kw, kw);
-  for (int step = 0; step < p.NT; ++step) {
-    const int ch = p.rev ? p.NT - 1 - step : step;
-    const long long tb = tok0(step);
-    panel_store_rows(nW, Wl, ldw, kw);
-    panel_store_t(nK, Kt, kw);
-    if (inj) {
-      panel_store_t(nA, At, kw);
-      for (int q = threadIdx.x; q < WBT * STILE; q += ST) {
-        const int i = q & 31, n = q >> 5;
-        Bt[n * LDT + i] = p.Ib[(tb + i) * vw + c0 + n];
-      }
+  auto chunk_of = [&](int it) { return REV ? NT - 1 - it : it; };
+  auto clampc = [&](int it) { return chunk_of(it < NT ? it : NT - 1); };
+  // Straight-line ring (no breaks; clamped, unconditional prefetches) so the
+  // compiler's wait counts only cover the buffer being consumed; the last
+  // SPF - 1 or fewer chunks run after the loop.
+  WFrags<REV> f[SPF];
+#pragma unroll
+  for (int j = 0; j < SPF - 1; ++j) wstate_load<REV>(p, s, clampc(j), c0, f[j]);
+  int it = 0;
+  for (; it + SPF - 1 < NT; it += SPF) {
+#pragma unroll
+    for (int j = 0; j < SPF; ++j) {
+      wstate_load<REV>(p, s, clampc(it + j + SPF - 1), c0, f[(j + SPF - 1) % SPF]);
+      wstate_step<REV>(p, s, chunk_of(it + j), c0, f[j], X, wsm);
     }
-    // this step's U (the w values this wave reduces) and chunk decay, loaded
-    // ahead of their use
-    float uq[CPW];
-#pragma unroll
-    for (int j = 0; j < CPW; ++j) {
-      const int k = w * CPW + j, h = k >> 3, t2 = (k >> 2) & 1, e = k & 3;
-      uq[j] = p.U[(tb + t2 * 16 + 4 * g + e) * vw + c0 + h * 16 + m];
-    }
-    float gv[SRB][4];
-#pragma unroll
-    for (int q = 0; q < SRB; ++q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int rb = w + SW * q;
-        gv[q][e] = rb < nrb ? p.Gam[((long long)s * p.NT + ch) * kw + rb * 16 + 4 * g + e] : 0.f;
-      }
-#pragma unroll
-    for (int q = 0; q < SRB; ++q) {  // slot[ch] = X0
-      const int rb = w + SW * q;
-      if (rb < nrb)
-#pragma unroll
-        for (int h = 0; h < NSUB; ++h)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const long long o = sb + ((long long)ch * kw + rb * 16 + 4 * g + e) * vw + c0 + h * 16 + m;
-            if (p.rev)
-              static_cast<ls_t*>(p.slots)[o] = (ls_t)X[q][h][e];
-            else
-              static_cast<xs_t*>(p.slots)[o] = (xs_t)X[q][h][e];
-          }
-    }
-    __syncthreads();
-    // the next chunk's panels load while this one computes (clamped at the end)
-    {
-      const int nx = step + 1 < p.NT ? step + 1 : step;
-      panel_load(nW, p.W + tok0(nx) * kw, kw);
-      panel_load(nK, p.K + tok0(nx) * kw, kw);
-      if (inj) panel_load(nA, p.Ia + tok0(nx) * kw, kw);
-    }
-    // partial w = W X0 over this wave's row blocks
-    f4 pw[NSUB][2];
-#pragma unroll
-    for (int h = 0; h < NSUB; ++h) pw[h][0] = pw[h][1] = zero4();
-#pragma unroll
-    for (int q = 0; q < SRB; ++q) {
-      const int rb = w + SW * q;
-      if (rb < nrb) {
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          const float4 a = *reinterpret_cast<const float4*>(Wl + (t2 * 16 + m) * ldw + rb * 16 + 4 * g);
-#pragma unroll
-          for (int h = 0; h < NSUB; ++h) {
-            pw[h][t2] = mfma4(a.x, X[q][h][0], pw[h][t2]);
-            pw[h][t2] = mfma4(a.y, X[q][h][1], pw[h][t2]);
-            pw[h][t2] = mfma4(a.z, X[q][h][2], pw[h][t2]);
-            pw[h][t2] = mfma4(a.w, X[q][h][3], pw[h][t2]);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < NSUB; ++h)
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[(((w * NSUB + h) * 2 + t2) * 4 + e) * 64 + l] = pw[h][t2][e];
-    __syncthreads();
-    // each wave finishes CPW of the lane's NCMB w values (U minus the eight
-    // waves' partials, in wave order) and shares them through LDS
-#pragma unroll
-    for (int j = 0; j < CPW; ++j) {
-      const int k = w * CPW + j, h = k >> 3, t2 = (k >> 2) & 1, e = k & 3;
-      float a = uq[j];
-#pragma unroll
-      for (int w2 = 0; w2 < SW; ++w2) a -= red[(w2 * NCMB + k) * 64 + l];
-      wred[k * 64 + l] = a;
-      p.wout[(tb + t2 * 16 + 4 * g + e) * vw + c0 + h * 16 + m] = a;
-    }
-    __syncthreads();
-    f4 wv[NSUB][2];
-#pragma unroll
-    for (int h = 0; h < NSUB; ++h)
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) wv[h][t2][e] = wred[((h * 2 + t2) * 4 + e) * 64 + l];
-    // X = Gamma X + K^T w (+ A^T B)
-#pragma unroll
-    for (int q = 0; q < SRB; ++q) {
-      const int rb = w + SW * q;
-      if (rb < nrb) {
-#pragma unroll
-        for (int h = 0; h < NSUB; ++h)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) X[q][h][e] *= gv[q][e];
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          const float4 kk = *reinterpret_cast<const float4*>(Kt + (rb * 16 + m) * LDT + t2 * 16 + 4 * g);
-#pragma unroll
-          for (int h = 0; h < NSUB; ++h) {
-            X[q][h] = mfma4(kk.x, wv[h][t2][0], X[q][h]);
-            X[q][h] = mfma4(kk.y, wv[h][t2][1], X[q][h]);
-            X[q][h] = mfma4(kk.z, wv[h][t2][2], X[q][h]);
-            X[q][h] = mfma4(kk.w, wv[h][t2][3], X[q][h]);
-          }
-          if (inj) {
-            const float4 aa = *reinterpret_cast<const float4*>(At + (rb * 16 + m) * LDT + t2 * 16 + 4 * g);
-#pragma unroll
-            for (int h = 0; h < NSUB; ++h) {
-              const float4 bb = *reinterpret_cast<const float4*>(Bt + (h * 16 + m) * LDT + t2 * 16 + 4 * g);
-              X[q][h] = mfma4(aa.x, bb.x, X[q][h]);
-              X[q][h] = mfma4(aa.y, bb.y, X[q][h]);
-              X[q][h] = mfma4(aa.z, bb.z, X[q][h]);
-              X[q][h] = mfma4(aa.w, bb.w, X[q][h]);
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();  // the next step restages the panels
   }
+#pragma unroll
+  for (int j = 0; j < SPF - 1; ++j)
+    if (it + j < NT) wstate_step<REV>(p, s, chunk_of(it + j), c0, f[j], X, wsm);
+  // final state (forward: also slot NT for the backward)
+  using S = typename std::conditional<REV, ls_t, xs_t>::type;
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
     const int rb = w + SW * q;
@@ -587,7 +620,9 @@ __global__ __launch_bounds__(ST) void k_w_state(WStateParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int row = rb * 16 + 4 * g + e, col = c0 + h * 16 + m;
-        if (!p.rev) static_cast<xs_t*>(p.slots)[sb + ((long long)p.NT * kw + row) * vw + col] = (xs_t)X[q][h][e];
+        if (!REV)
+          static_cast<S*>(p.slots)[((long long)s * (p.NT + 1) + p.NT) * kw * p.vw + (long long)row * p.vw + col] =
+              (S)X[q][h][e];
         if (p.fin && row < p.rows && col < p.cols) {
           if (p.fin_t) p.fin[((long long)s * p.cols + col) * p.rows + row] = X[q][h][e];
           else p.fin[((long long)s * p.rows + row) * p.cols + col] = X[q][h][e];
@@ -825,12 +860,14 @@ __global__ __launch_bounds__(WT) void k_w_sources(SrcParams p) {
 //   column output: rhs = dW + P^T dO, injection Ia = q e^G, Ib = dO
 //   row output:    Pp_ij = sum_r dO_ir k_jr e^{G_ir - G_jr} (j <= i), rhs = dW + Pp^T q,
 //                  Ia = dO e^G, Ib = q
-//   dU = A^T rhs,  Wn = -A^T Kh,  Kn = -x~
+//   dU = A^T rhs,  Wn = -A^T Kh,  Kn = -x~  (Wn, Kn, Ia stored bf16 for the
+//   reverse pass: -Wn token-major, Kn and Ia transposed per chunk)
 // ---------------------------------------------------------------------------
 struct BprepParams {
   int NT, Tp, kw, vw, excl, colout;
   const float *k, *x, *q, *G, *A, *P, *dO, *dW;
-  float *dU, *Wn, *Kn, *Ia, *Pp;
+  float *dU, *Pp;
+  __bf16 *Wneg, *Kt, *At;  // reverse-pass panels: -Wn [Tp][kw]; Kn, Ia transposed per chunk [NT][kw][32]
 };
 
 __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
@@ -908,19 +945,24 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
   // key side: Wn, Kn, Ia, one key coordinate per thread
   if (c < kw) {
     const float gl = kg[WBT - 1];
+    const long long cb = (((long long)s * p.NT + ch) * kw + c) * WBT;
+    bf16x8 kv, av;
 #pragma unroll
     for (int i = 0; i < WBT; ++i) {
-      const long long o = (tb + i) * kw + c;
       const float gi = kg[i];
       cv[i * WT + tid] = kk[i] * __expf(gl - gi);
       const float gx = p.excl ? (i > 0 ? kg[i - 1] : 0.f) : gi;
-      p.Kn[o] = -kx[i] * __expf(gx);
-      p.Ia[o] = ks2[i] * __expf(gi);
+      kv[i & 7] = (__bf16)(-kx[i] * __expf(gx));
+      av[i & 7] = (__bf16)(ks2[i] * __expf(gi));
+      if ((i & 7) == 7) {
+        *reinterpret_cast<bf16x8*>(p.Kt + cb + i - 7) = kv;
+        *reinterpret_cast<bf16x8*>(p.At + cb + i - 7) = av;
+      }
     }
     for (int m = 0; m < WBT; ++m) {
       float a = 0.f;
       for (int i = m; i < WBT; ++i) a += Al[i * MS + m] * cv[i * WT + tid];
-      p.Wn[(tb + m) * kw + c] = -a;
+      p.Wneg[(tb + m) * kw + c] = (__bf16)a;
     }
   }
 }
@@ -1468,7 +1510,8 @@ struct WideFwd {
   float *delta, *oC, *d, *e, *chi, *z, *wS;
   float *AC, *AS, *PS;
   xs_t *XC, *XS;
-  float *W, *U, *Kh, *Qt, *Gam;
+  _Float16 *Wneg, *Kt;
+  float *U, *Qt, *Gam;
 };
 
 // saved: what the backward reads; scratch: the forward-only panels (the C op's
@@ -1491,7 +1534,7 @@ WideFwd carve_wide_fwd(void* saved, void* scratch, const WideDims& d, size_t* sa
   WCarver t{(char*)scratch};
   const size_t pm = d.KP > d.VP ? pk : pv;
   w.vC = t.take(pk); w.z = t.take(pv);
-  w.W = t.take(pk); w.U = t.take(pm); w.Kh = t.take(pk); w.Qt = t.take(pk);
+  w.Wneg = t.take<_Float16>(pk); w.U = t.take(pm); w.Kt = t.take<_Float16>(pk); w.Qt = t.take(pk);
   if (scratch_bytes) *scratch_bytes = t.off + 256;
   return w;
 }
@@ -1499,7 +1542,8 @@ WideFwd carve_wide_fwd(void* saved, void* scratch, const WideDims& d, size_t* sa
 struct WideBwd {
   float* dO;
   ls_t *LC, *LS;
-  float *dU, *Wn, *Kn, *Ia, *Pp;
+  float *dU, *Pp;
+  __bf16 *Wneg, *Kt, *At;
   float *dwS, *dwC, *dd, *de, *dchi, *dgS;
   float *duh, *ddelta, *dkh, *dqh, *dkC, *dxC, *dqC, *dgC;
 };
@@ -1512,7 +1556,7 @@ WideBwd carve_wide_bwd(void* base, const WideDims& d, size_t* total) {
   w.dO = c.take(pv);
   w.LC = c.take<ls_t>((size_t)d.n * (d.NT + 1) * d.KP * d.KP);
   w.LS = c.take<ls_t>((size_t)d.n * (d.NT + 1) * d.KP * d.VP);
-  w.dU = c.take(pm); w.Wn = c.take(pk); w.Kn = c.take(pk); w.Ia = c.take(pk);
+  w.dU = c.take(pm); w.Wneg = c.take<__bf16>(pk); w.Kt = c.take<__bf16>(pk); w.At = c.take<__bf16>(pk);
   w.Pp = c.take((size_t)d.n * d.NT * WBT * WBT);
   w.dwS = c.take(pv); w.dwC = c.take(pk);
   w.dd = c.take(pk); w.de = c.take(pk); w.dchi = c.take(pk); w.dgS = c.take(pk);
@@ -1523,7 +1567,7 @@ WideBwd carve_wide_bwd(void* base, const WideDims& d, size_t* total) {
 }
 
 constexpr size_t kMaxLds = 160 * 1024;  // LDS of one gfx950 CU
-static_assert(prep_smem(WMAX) <= kMaxLds && state_smem(WMAX, true) <= kMaxLds && out_smem(WMAX, WMAX, 0) <= kMaxLds &&
+static_assert(prep_smem(WMAX) <= kMaxLds && state_smem() <= kMaxLds && out_smem(WMAX, WMAX, 0) <= kMaxLds &&
                   out_smem(WMAX, WMAX, 1) <= kMaxLds && bprep_smem(WMAX) <= kMaxLds &&
                   grad_smem(WMAX) <= kMaxLds,
               "a wide kernel's LDS exceeds the CU");
@@ -1535,9 +1579,11 @@ void launch_wprep(const OpParams& op, int n, hipStream_t st) {
 }
 
 void launch_wstate(const char* name, const WStateParams& sp, int n, hipStream_t st) {
-  SD_SMEM_ONCE(k_w_state, (int)state_smem(WMAX, true));
-  SD_LAUNCH(name, k_w_state, dim3(sp.vw / STILE * n), dim3(ST), state_smem(sp.kw, sp.Ia != nullptr),
-            st, sp);
+  const dim3 grid(sp.vw / STILE * n), blk(ST);
+  if (sp.rev)
+    SD_LAUNCH(name, k_w_state<true>, grid, blk, state_smem(), st, sp);
+  else
+    SD_LAUNCH(name, k_w_state<false>, grid, blk, state_smem(), st, sp);
 }
 
 }  // namespace
@@ -1567,11 +1613,11 @@ int launch_wide_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void
   OpParams oc{};
   oc.NT = d.NT; oc.Tp = d.Tp; oc.kw = d.KP; oc.vw = d.KP; oc.excl = 1; oc.colout = 0;
   oc.k = w.uh; oc.x = w.xC; oc.v = w.vC; oc.q = w.kh; oc.G = w.G;
-  oc.A = w.AC; oc.P = w.PS; oc.W = w.W; oc.U = w.U; oc.Kh = w.Kh; oc.Qt = w.Qt; oc.Gam = w.Gam;
+  oc.A = w.AC; oc.P = w.PS; oc.Wneg = w.Wneg; oc.U = w.U; oc.Kt = w.Kt; oc.Qt = w.Qt; oc.Gam = w.Gam;
   launch_wprep(oc, d.n, st);
   WStateParams sc{};
   sc.NT = d.NT; sc.Tp = d.Tp; sc.kw = d.KP; sc.vw = d.KP; sc.rows = in->r; sc.cols = in->r;
-  sc.W = w.W; sc.U = w.U; sc.K = w.Kh; sc.Gam = w.Gam;
+  sc.Wneg = w.Wneg; sc.U = w.U; sc.Kt = w.Kt; sc.Gam = w.Gam;
   sc.slots = w.XC; sc.wout = w.delta;
   sc.init = in->C0; sc.init_t = 1; sc.fin = C_T; sc.fin_t = 1;
   launch_wstate("w_state_c_fwd", sc, d.n, st);
@@ -1592,11 +1638,11 @@ int launch_wide_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void
   OpParams os{};
   os.NT = d.NT; os.Tp = d.Tp; os.kw = d.KP; os.vw = d.VP; os.excl = 0; os.colout = 1;
   os.k = w.d; os.x = w.e; os.v = w.z; os.q = w.chi; os.G = w.G;
-  os.A = w.AS; os.P = w.PS; os.W = w.W; os.U = w.U; os.Kh = w.Kh; os.Qt = w.Qt; os.Gam = w.Gam;
+  os.A = w.AS; os.P = w.PS; os.Wneg = w.Wneg; os.U = w.U; os.Kt = w.Kt; os.Qt = w.Qt; os.Gam = w.Gam;
   launch_wprep(os, d.n, st);
   WStateParams ss{};
   ss.NT = d.NT; ss.Tp = d.Tp; ss.kw = d.KP; ss.vw = d.VP; ss.rows = in->r; ss.cols = in->V;
-  ss.W = w.W; ss.U = w.U; ss.K = w.Kh; ss.Gam = w.Gam;
+  ss.Wneg = w.Wneg; ss.U = w.U; ss.Kt = w.Kt; ss.Gam = w.Gam;
   ss.slots = w.XS; ss.wout = w.wS;
   ss.init = in->S0; ss.init_t = 0; ss.fin = S_T; ss.fin_t = 0;
   launch_wstate("w_state_s_fwd", ss, d.n, st);
@@ -1631,11 +1677,11 @@ int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void*
   bs.NT = d.NT; bs.Tp = d.Tp; bs.kw = d.KP; bs.vw = d.VP; bs.excl = 0; bs.colout = 1;
   bs.k = f.d; bs.x = f.e; bs.q = f.chi; bs.G = f.G; bs.A = f.AS; bs.P = f.PS;
   bs.dO = w.dO; bs.dW = nullptr;
-  bs.dU = w.dU; bs.Wn = w.Wn; bs.Kn = w.Kn; bs.Ia = w.Ia; bs.Pp = w.Pp;
+  bs.dU = w.dU; bs.Wneg = w.Wneg; bs.Kt = w.Kt; bs.At = w.At; bs.Pp = w.Pp;
   SD_LAUNCH("k_w_bprep_s", k_w_bprep, dim3(d.NT, d.n), dim3(WT), bprep_smem(d.KP), st, bs);
   WStateParams rs{};
   rs.NT = d.NT; rs.Tp = d.Tp; rs.kw = d.KP; rs.vw = d.VP; rs.rows = in->r; rs.cols = in->V; rs.rev = 1;
-  rs.W = w.Wn; rs.U = w.dU; rs.K = w.Kn; rs.Gam = f.Gam; rs.Ia = w.Ia; rs.Ib = w.dO;
+  rs.Wneg = w.Wneg; rs.U = w.dU; rs.Kt = w.Kt; rs.Gam = f.Gam; rs.At = w.At; rs.Ib = w.dO;
   rs.slots = w.LS; rs.wout = w.dwS;
   rs.init = dS_T; rs.init_t = 0; rs.fin = dS0; rs.fin_t = 0;
   launch_wstate("w_state_s_bwd", rs, d.n, st);
@@ -1659,11 +1705,11 @@ int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void*
   bc.NT = d.NT; bc.Tp = d.Tp; bc.kw = d.KP; bc.vw = d.KP; bc.excl = 1; bc.colout = 0;
   bc.k = f.uh; bc.x = f.xC; bc.q = f.kh; bc.G = f.G; bc.A = f.AC; bc.P = nullptr;
   bc.dO = w.dd; bc.dW = w.ddelta;
-  bc.dU = w.dU; bc.Wn = w.Wn; bc.Kn = w.Kn; bc.Ia = w.Ia; bc.Pp = w.Pp;
+  bc.dU = w.dU; bc.Wneg = w.Wneg; bc.Kt = w.Kt; bc.At = w.At; bc.Pp = w.Pp;
   SD_LAUNCH("k_w_bprep_c", k_w_bprep, dim3(d.NT, d.n), dim3(WT), bprep_smem(d.KP), st, bc);
   WStateParams rc{};
   rc.NT = d.NT; rc.Tp = d.Tp; rc.kw = d.KP; rc.vw = d.KP; rc.rows = in->r; rc.cols = in->r; rc.rev = 1;
-  rc.W = w.Wn; rc.U = w.dU; rc.K = w.Kn; rc.Gam = f.Gam; rc.Ia = w.Ia; rc.Ib = f.kh;
+  rc.Wneg = w.Wneg; rc.U = w.dU; rc.Kt = w.Kt; rc.Gam = f.Gam; rc.At = w.At; rc.Ib = f.kh;
   rc.slots = w.LC; rc.wout = w.dwC;
   rc.init = dC_T; rc.init_t = 1; rc.fin = dC0; rc.fin_t = 1;
   launch_wstate("w_state_c_bwd", rc, d.n, st);
