@@ -225,6 +225,37 @@ __device__ __forceinline__ void gram_mfma(int kw, const int* wl, int nw, FA fa, 
   }
 }
 
+// Stages NA [32][kw] FP32 token panels (rows from token tb) into LDS panels of
+// row stride ld.  Every thread's 16-byte loads of all of them are issued before
+// its first LDS write, so the staging costs one memory latency, not one per row.
+template <int NA>
+__device__ __forceinline__ void stage_panels(const float* const (&src)[NA], float* const (&dst)[NA],
+                                             long long tb, int kw, int ld) {
+  constexpr int PQ = WBT * WMAX / 4 / WT;  // 16-byte pieces per thread and panel at kw = 256
+  const int npc = WBT * kw / 4;
+  float4 v[NA][PQ];
+#pragma unroll
+  for (int q = 0; q < PQ; ++q) {
+    const int idx = threadIdx.x + WT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
+    if (idx < npc)
+#pragma unroll
+      for (int a = 0; a < NA; ++a) v[a][q] = *reinterpret_cast<const float4*>(src[a] + (tb + i) * kw + c);
+  }
+#pragma unroll
+  for (int q = 0; q < PQ; ++q) {
+    const int idx = threadIdx.x + WT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
+    if (idx < npc)
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+        float* d = dst[a] + i * ld + c;
+        d[0] = v[a][q].x;
+        d[1] = v[a][q].y;
+        d[2] = v[a][q].z;
+        d[3] = v[a][q].w;
+      }
+  }
+}
+
 __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
   extern __shared__ __align__(16) float sm[];
   const int ch = blockIdx.x, s = blockIdx.y, kw = p.kw, vw = p.vw, ld = kw + 1;
@@ -235,13 +266,14 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
   float* Ls = qs + WBT * ld;      // L, then A  [32][33]
   float* Ps = Ls + WBT * MS;      // P
   const long long tb = (long long)s * p.Tp + ch * WBT;
-  for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
-    const int i = idx / kw, c = idx % kw;
-    const long long o = (tb + i) * kw + c;
-    xs[i * ld + c] = p.x[o];
-    ks[i * ld + c] = p.k[o];
-    Gs[i * ld + c] = p.G[o];
-    if (p.colout) qs[i * ld + c] = p.q[o];
+  if (p.colout) {
+    const float* const src[4] = {p.x, p.k, p.G, p.q};
+    float* const dst[4] = {xs, ks, Gs, qs};
+    stage_panels<4>(src, dst, tb, kw, ld);
+  } else {
+    const float* const src[3] = {p.x, p.k, p.G};
+    float* const dst[3] = {xs, ks, Gs};
+    stage_panels<3>(src, dst, tb, kw, ld);
   }
   // this thread's value column for U = A v, loaded before any store of the
   // kernel (a load issued after a store waits for it: one counter retires both)
@@ -638,13 +670,26 @@ __global__ __launch_bounds__(ST) void k_w_state(WStateParams p) {
 __device__ __forceinline__ void rows_times_x(const float* A, int lda, const xs_t* X, int kw,
                                              int vw, float* buf, float (&acc)[WBT]) {
   const int c = threadIdx.x, lb = vw + 4;
+  constexpr int PQ = 32 * WMAX / 4 / WT;  // 4-element pieces per thread of a 32-row block
+  const int npc = 32 * vw / 4;
+  float4 nx[PQ];  // the next row block, loaded while the current one is used
+  auto fetch = [&](int rb) {
+#pragma unroll
+    for (int q = 0; q < PQ; ++q) {
+      const int idx = threadIdx.x + WT * q, i = (idx * 4) / vw, cc = (idx * 4) % vw;
+      if (idx < npc) nx[q] = ld4s(X + (long long)(rb + i) * vw + cc);
+    }
+  };
+  fetch(0);
   for (int rb = 0; rb < kw; rb += 32) {
     __syncthreads();
-    for (int q = threadIdx.x; q < 32 * vw / 4; q += WT) {
-      const int i = (q * 4) / vw, cc = (q * 4) % vw;
-      *reinterpret_cast<float4*>(buf + i * lb + cc) = ld4s(X + (long long)(rb + i) * vw + cc);
+#pragma unroll
+    for (int q = 0; q < PQ; ++q) {
+      const int idx = threadIdx.x + WT * q, i = (idx * 4) / vw, cc = (idx * 4) % vw;
+      if (idx < npc) *reinterpret_cast<float4*>(buf + i * lb + cc) = nx[q];
     }
     __syncthreads();
+    if (rb + 32 < kw) fetch(rb + 32);
     if (c < vw) {
 #pragma unroll 4
       for (int k = 0; k < 32; ++k) {
@@ -674,8 +719,11 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
     float* Ql = sm;                 // [32][kw+1]
     float* Pl = Ql + WBT * ld;      // [32][33]
     float* Xb = Pl + WBT * MS;      // X0 row block [32][vw+4]
-    for (int idx = threadIdx.x; idx < WBT * kw; idx += WT)
-      Ql[(idx / kw) * ld + idx % kw] = p.Qt[(tb + idx / kw) * kw + idx % kw];
+    {
+      const float* const src[1] = {p.Qt};
+      float* const dst[1] = {Ql};
+      stage_panels<1>(src, dst, tb, kw, ld);
+    }
     const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
     for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) Pl[(idx >> 5) * MS + (idx & 31)] = p.P[mb + idx];
     float acc[WBT];
@@ -890,12 +938,10 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
     if (p.colout) Pl[(idx >> 5) * MS + (idx & 31)] = p.P[mb + idx];
   }
   if (!p.colout) {
-    for (int idx = threadIdx.x; idx < WBT * kw; idx += WT) {
-      const int i = idx / kw, c = idx % kw;
-      const long long o = (tb + i) * kw + c;
-      dOl[i * ld + c] = p.dO[o];
-      kl[i * ld + c] = p.k[o];
-      Gl[i * ld + c] = p.G[o];
+    {
+      const float* const src[3] = {p.dO, p.k, p.G};
+      float* const dst[3] = {dOl, kl, Gl};
+      stage_panels<3>(src, dst, tb, kw, ld);
     }
     __syncthreads();
     int* wl = reinterpret_cast<int*>(Gl + WBT * ld);
