@@ -1054,9 +1054,10 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   const xs_t* X0 = p.Xslots + slot * kw * vw;
   const xs_t* XC = X0 + (long long)kw * vw;
   const ls_t* Lm = p.Lslots + slot * kw * vw;
-  // LDS: the token Grams M1, M2 [32][33]
+  // LDS: the token Grams M1, M2 [32][33]; row output: dO e^G [32][kw+4]
   float* M1 = sm;
   float* M2 = M1 + WBT * MS;
+  float* DG = M2 + WBT * MS;
   const int r = threadIdx.x;
   const int wv_ = r >> 6, l = r & 63, g = l >> 4, m = l & 15;
   const int nrb = kw / 16, nvb = vw / 16;
@@ -1146,27 +1147,48 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
     rs[q] += __shfl_xor(rs[q], 32);
   }
   // phase 2 (row output): dq = (dO e^G) X0 + Pp w on matrix cores, this wave's
-  // 16-column blocks of the value axis
+  // 16-column blocks of the value axis; dO e^G is formed once into LDS
   if (!p.colout) {
     const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
+    const int la = kw + 4;
+    {
+      constexpr int PQ = WBT * WMAX / 4 / GT;
+      float4 d4[PQ], g4[PQ];
+#pragma unroll
+      for (int q = 0; q < PQ; ++q) {
+        const int idx = threadIdx.x + GT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
+        if (idx < WBT * kw / 4) {
+          d4[q] = *reinterpret_cast<const float4*>(p.dO + (tb + i) * kw + c);
+          g4[q] = *reinterpret_cast<const float4*>(p.G + (tb + i) * kw + c);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < PQ; ++q) {
+        const int idx = threadIdx.x + GT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
+        if (idx < WBT * kw / 4)
+          *reinterpret_cast<float4*>(DG + i * la + c) =
+              make_float4(d4[q].x * __expf(g4[q].x), d4[q].y * __expf(g4[q].y),
+                          d4[q].z * __expf(g4[q].z), d4[q].w * __expf(g4[q].w));
+      }
+    }
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < GRB; ++q) {
       const int nb = wv_ + GW * q;
       if (nb >= nvb) continue;
       f4 acc[2] = {zero4(), zero4()};
+#pragma unroll 4
       for (int rb = 0; rb < nrb; ++rb) {
         float bx[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) bx[e] = (float)X0[(long long)(rb * 16 + 4 * g + e) * vw + nb * 16 + m];
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2) {
-          const long long o = (tb + t2 * 16 + m) * kw + rb * 16 + 4 * g;
-          const float4 d4 = *reinterpret_cast<const float4*>(p.dO + o);
-          const float4 g4 = *reinterpret_cast<const float4*>(p.G + o);
-          acc[t2] = mfma4(d4.x * __expf(g4.x), bx[0], acc[t2]);
-          acc[t2] = mfma4(d4.y * __expf(g4.y), bx[1], acc[t2]);
-          acc[t2] = mfma4(d4.z * __expf(g4.z), bx[2], acc[t2]);
-          acc[t2] = mfma4(d4.w * __expf(g4.w), bx[3], acc[t2]);
+          const float4 a4 = *reinterpret_cast<const float4*>(DG + (t2 * 16 + m) * la + rb * 16 + 4 * g);
+          acc[t2] = mfma4(a4.x, bx[0], acc[t2]);
+          acc[t2] = mfma4(a4.y, bx[1], acc[t2]);
+          acc[t2] = mfma4(a4.z, bx[2], acc[t2]);
+          acc[t2] = mfma4(a4.w, bx[3], acc[t2]);
         }
       }
 #pragma unroll
@@ -1341,7 +1363,7 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   }
 }
 
-constexpr size_t grad_smem(int) { return 2 * WBT * MS * sizeof(float); }
+constexpr size_t grad_smem(int kw) { return (2 * WBT * MS + WBT * (kw + 4)) * sizeof(float); }
 
 // ---------------------------------------------------------------------------
 // Source closure (per token): cotangents of e, chi, z back to u^, delta, k^, q^,
