@@ -1054,10 +1054,12 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   const xs_t* X0 = p.Xslots + slot * kw * vw;
   const xs_t* XC = X0 + (long long)kw * vw;
   const ls_t* Lm = p.Lslots + slot * kw * vw;
-  // LDS: the token Grams M1, M2 [32][33]; row output: dO e^G [32][kw+4]
+  // LDS: the token Grams M1, M2 [32][33]; the rows dw, w, Y [3][32][vw+4]
+  // (first pass), then for the row output dO e^G [32][kw+4]
   float* M1 = sm;
   float* M2 = M1 + WBT * MS;
-  float* DG = M2 + WBT * MS;
+  float* TR = M2 + WBT * MS;
+  float* DG = TR;
   const int r = threadIdx.x;
   const int wv_ = r >> 6, l = r & 63, g = l >> 4, m = l & 15;
   const int nrb = kw / 16, nvb = vw / 16;
@@ -1077,6 +1079,22 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) aX[q][t2] = aL[q][t2] = aO[q][t2] = zero4();
   }
+  // the chunk's dw, w, Y rows staged once into LDS (every wave reads all of them)
+  const int lt = vw + 4;
+#pragma unroll
+  for (int q = 0; q < WBT * WMAX / 4 / GT; ++q) {
+    const int idx = threadIdx.x + GT * q, i = (idx * 4) / vw, c = (idx * 4) % vw;
+    if (idx < WBT * vw / 4) {
+      const long long o = (tb + i) * vw + c;
+      const float4 a0 = *reinterpret_cast<const float4*>(p.dw + o);
+      const float4 a1 = *reinterpret_cast<const float4*>(p.w + o);
+      const float4 a2 = *reinterpret_cast<const float4*>(Y + o);
+      *reinterpret_cast<float4*>(TR + i * lt + c) = a0;
+      *reinterpret_cast<float4*>(TR + (WBT + i) * lt + c) = a1;
+      *reinterpret_cast<float4*>(TR + (2 * WBT + i) * lt + c) = a2;
+    }
+  }
+  __syncthreads();
   {
     f4 m1a = zero4(), m2a = zero4();
     const int bi = (wv_ >> 1) & 1, bj = wv_ & 1;
@@ -1086,10 +1104,10 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
       float4 adw[2], aw[2], ay[2];
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
-        const long long o = (tb + t2 * 16 + m) * vw + cb + 4 * g;
-        adw[t2] = *reinterpret_cast<const float4*>(p.dw + o);
-        aw[t2] = *reinterpret_cast<const float4*>(p.w + o);
-        ay[t2] = *reinterpret_cast<const float4*>(Y + o);
+        const int o = (t2 * 16 + m) * lt + cb + 4 * g;
+        adw[t2] = *reinterpret_cast<const float4*>(TR + o);
+        aw[t2] = *reinterpret_cast<const float4*>(TR + WBT * lt + o);
+        ay[t2] = *reinterpret_cast<const float4*>(TR + 2 * WBT * lt + o);
       }
 #pragma unroll
       for (int q = 0; q < GRB; ++q) {
@@ -1151,24 +1169,15 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   if (!p.colout) {
     const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
     const int la = kw + 4;
-    {
-      constexpr int PQ = WBT * WMAX / 4 / GT;
-      float4 d4[PQ], g4[PQ];
+    __syncthreads();  // every wave is done reading the rows DG overwrites
 #pragma unroll
-      for (int q = 0; q < PQ; ++q) {
-        const int idx = threadIdx.x + GT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
-        if (idx < WBT * kw / 4) {
-          d4[q] = *reinterpret_cast<const float4*>(p.dO + (tb + i) * kw + c);
-          g4[q] = *reinterpret_cast<const float4*>(p.G + (tb + i) * kw + c);
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < PQ; ++q) {
-        const int idx = threadIdx.x + GT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
-        if (idx < WBT * kw / 4)
-          *reinterpret_cast<float4*>(DG + i * la + c) =
-              make_float4(d4[q].x * __expf(g4[q].x), d4[q].y * __expf(g4[q].y),
-                          d4[q].z * __expf(g4[q].z), d4[q].w * __expf(g4[q].w));
+    for (int q = 0; q < WBT * WMAX / 4 / GT; ++q) {
+      const int idx = threadIdx.x + GT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
+      if (idx < WBT * kw / 4) {
+        const float4 d4 = *reinterpret_cast<const float4*>(p.dO + (tb + i) * kw + c);
+        const float4 g4 = *reinterpret_cast<const float4*>(p.G + (tb + i) * kw + c);
+        *reinterpret_cast<float4*>(DG + i * la + c) =
+            make_float4(d4.x * __expf(g4.x), d4.y * __expf(g4.y), d4.z * __expf(g4.z), d4.w * __expf(g4.w));
       }
     }
     __syncthreads();
@@ -1363,7 +1372,7 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   }
 }
 
-constexpr size_t grad_smem(int kw) { return (2 * WBT * MS + WBT * (kw + 4)) * sizeof(float); }
+constexpr size_t grad_smem(int w) { return (2 * WBT * MS + 3 * WBT * (w + 4)) * sizeof(float); }
 
 // ---------------------------------------------------------------------------
 // Source closure (per token): cotangents of e, chi, z back to u^, delta, k^, q^,
@@ -1758,7 +1767,7 @@ int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void*
   gs.k = f.d; gs.x = f.e; gs.q = f.chi; gs.G = f.G; gs.dO = w.dO; gs.o = nullptr;
   gs.w = f.wS; gs.dw = w.dwS; gs.Xslots = f.XS; gs.Lslots = w.LS; gs.Pp = nullptr;
   gs.dk = w.dd; gs.dx = w.de; gs.dq = w.dchi; gs.dg = w.dgS;
-  SD_LAUNCH("k_w_grad_s", k_w_grad, dim3(d.NT * d.n), dim3(GT), grad_smem(d.KP), st, gs);
+  SD_LAUNCH("k_w_grad_s", k_w_grad, dim3(d.NT * d.n), dim3(GT), grad_smem(d.KP > d.VP ? d.KP : d.VP), st, gs);
 
   SrcBwdParams sb{};
   sb.in = *in; sb.Tp = d.Tp; sb.KP = d.KP; sb.VP = d.VP;
@@ -1786,7 +1795,7 @@ int launch_wide_bwd(const sd_inputs* in, const void* fws, void* bws, const void*
   gc.k = f.uh; gc.x = f.xC; gc.q = f.kh; gc.G = f.G; gc.dO = w.dd; gc.o = f.oC;
   gc.w = f.delta; gc.dw = w.dwC; gc.Xslots = f.XC; gc.Lslots = w.LC; gc.Pp = w.Pp;
   gc.dk = w.dkC; gc.dx = w.dxC; gc.dq = w.dqC; gc.dg = w.dgC;
-  SD_LAUNCH("k_w_grad_c", k_w_grad, dim3(d.NT * d.n), dim3(GT), grad_smem(d.KP), st, gc);
+  SD_LAUNCH("k_w_grad_c", k_w_grad, dim3(d.NT * d.n), dim3(GT), grad_smem(d.KP > d.VP ? d.KP : d.VP), st, gc);
 
   FinalParams fp{};
   fp.in = *in; fp.Tp = d.Tp; fp.KP = d.KP;
