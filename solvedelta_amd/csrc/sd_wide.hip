@@ -393,8 +393,9 @@ struct WStateParams {
 //   own rows.
 // The panels Wneg, K^T and At are stored 16-bit by the prep kernels in the
 // order the MFMA operands read them, so each lane's fragment is one 16-byte
-// load; they, U, Gamma and Ib are fetched PF - 1 chunks ahead into a ring of
-// registers.  Forward: panels fp16 (W and K are bounded by construction), X
+// load; they, U, Gamma and Ib are fetched SPF - 1 chunks ahead into a ring of
+// registers (Ib as two FP32 elements per thread, staged split through LDS like
+// w).  Forward: panels fp16 (W and K are bounded by construction), X
 // and w split into fp16 halves (~22 bits).  Reverse: bf16 throughout (its
 // exponent range keeps any scale of the cotangent), lambda, dw and Ib split
 // into bf16 halves.  Two barriers per step: the next step writes the X0
@@ -410,7 +411,7 @@ constexpr int WKS = WMAX / 32;       // K = 32 steps of the w product
 constexpr int SPF = 2;               // prefetch ring depth (chunks)
 constexpr int XLD = WMAX + 8;        // row stride (16-bit) of the staged X0
 constexpr int WLD = WBT + 8;         // row stride (16-bit) of the staged w
-constexpr size_t state_smem() { return (size_t)(2 * STILE * XLD + 2 * STILE * WLD) * 2; }
+constexpr size_t state_smem() { return (size_t)(2 * STILE * XLD + 4 * STILE * WLD) * 2; }
 
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -440,7 +441,7 @@ struct WFrags {
   V8 W[WKS];                      // waves 0-3: Wneg rows of token block w & 1
   V8 K[SRB];                      // K^T rows of this wave's row blocks, the chunk's 32 tokens
   bf16x8 A[REV ? SRB : 1];        // At rows (reverse)
-  bf16x8 Bh[REV ? NSUB : 1], Bl[REV ? NSUB : 1];  // Ib columns, split (reverse)
+  float2 ib;                      // reverse: this thread's two elements of the Ib tile
   f4 U;                           // waves 0-3: U tile (C-operand layout)
   float4 G[SRB];                  // Gamma of this wave's rows 16 rb + 4 g .. + 3
 };
@@ -482,17 +483,10 @@ __device__ __forceinline__ void wstate_load(const WStateParams& p, int s, int ch
     }
   }
   if constexpr (REV) {
+    static_assert(WBT * STILE == 2 * ST, "two Ib elements per thread");
     if (p.At) {
-      const float* Ic = p.Ib + tb * vw + c0;
-#pragma unroll
-      for (int h = 0; h < NSUB; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float x = Ic[(unsigned)((kq + j) * vw + h * 16 + m)];
-          const __bf16 hi = (__bf16)x;
-          f.Bh[h][j] = hi;
-          f.Bl[h][j] = (__bf16)(x - (float)hi);
-        }
+      const int tok = threadIdx.x / (STILE / 2), col = (threadIdx.x % (STILE / 2)) * 2;
+      f.ib = *reinterpret_cast<const float2*>(p.Ib + tb * vw + c0 + (unsigned)(tok * vw + col));
     }
   }
 }
@@ -527,6 +521,8 @@ __device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch
   E* Xl = Xh + STILE * XLD;
   E* wh = Xl + STILE * XLD;          // w [32 columns][WLD]
   E* wl = wh + STILE * WLD;
+  E* ih = wl + STILE * WLD;          // reverse: the injection's Ib tile [32 columns][WLD]
+  E* il = ih + STILE * WLD;
   S* slot = static_cast<S*>(p.slots) + ((long long)s * (p.NT + 1) + ch) * kw * vw;
   // slot[ch] = X0; X0 staged split and transposed for the w product
 #pragma unroll
@@ -539,6 +535,18 @@ __device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch
       wsplit4<E, V4>(Xh + col * XLD + row, Xl + col * XLD + row, X[q][h]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) slot[(unsigned)((row + e) * vw + c0 + col)] = (S)X[q][h][e];
+    }
+  }
+  if constexpr (REV) {
+    if (p.At) {  // the Ib tile staged split and transposed ([column][token])
+      const int tok = threadIdx.x / (STILE / 2), col = (threadIdx.x % (STILE / 2)) * 2;
+      const float v2[2] = {f.ib.x, f.ib.y};
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const E hi = (E)v2[j];
+        ih[(col + j) * WLD + tok] = hi;
+        il[(col + j) * WLD + tok] = (E)(v2[j] - (float)hi);
+      }
     }
   }
   __syncthreads();
@@ -576,8 +584,10 @@ __device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch
       for (int e = 0; e < 4; ++e) X[q][h][e] *= gv[e];
       if constexpr (REV) {
         if (p.At) {
-          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.A[q], f.Bl[h], X[q][h], 0, 0, 0);
-          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.A[q], f.Bh[h], X[q][h], 0, 0, 0);
+          const bf16x8 bh = *reinterpret_cast<const bf16x8*>(ih + (h * 16 + m) * WLD + kq);
+          const bf16x8 bl = *reinterpret_cast<const bf16x8*>(il + (h * 16 + m) * WLD + kq);
+          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.A[q], bl, X[q][h], 0, 0, 0);
+          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.A[q], bh, X[q][h], 0, 0, 0);
         }
       }
     }
