@@ -6,14 +6,15 @@
 // hold a 64-token chunk's 128-wide panels in LDS; at 256 they would not fit, so
 // this path states the same chunked algebra (the generic pre-decay-read delta
 // op restated in tests/chunk_model.py) with 32-token chunks, runtime padded
-// widths KP, VP (multiples of 32, <= 256) and FP32 panels throughout:
+// widths KP, VP (multiples of 32, <= 256), FP32 token panels and a 16-bit
+// matrix-core state pass (its panels and the chunk states in fp16 / bf16):
 //
 //   k_w_tokens  (chunk-parallel)  in-chunk log-decay prefix G, L2 norms, gamma;
 //   per op (predictor C: X = C^T, erase read before the token's decay, row
 //   output; memory S: erase read after it, column output):
 //     k_w_prep    decayed Gram L, (I+L)^-1, WY panels W, U, decayed keys,
 //                 readout pair P (column output);
-//     k_w_state   sequential chunk pass over one 16-column state tile;
+//     k_w_state   sequential chunk pass over one 32-column state tile;
 //     k_w_out     chunk readout (row output also forms d = k^ + C^T k^);
 //   k_w_sources (per token)  dual sources e, chi and gated values z;
 // and backward, per op in reverse order:

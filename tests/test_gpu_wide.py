@@ -4,10 +4,10 @@ width up to 256 per call) against the FP64 oracle.
 The reference's state pass takes head widths up to 256
 (causallsso/ops/residual_frame/common_left_h.py:139-151); the main kernels
 stop at 128, so these widths run on the library's wide-width kernels (32-token
-chunks, FP32 panels).  Gates as for the main path (reference
+chunks, FP32 token panels, 16-bit state pass).  Gates as for the main path (reference
 tests/core/test_rebuild_semantics.py:540-597): output rtol/atol 2e-2, final
 states and every gradient's relative Frobenius error well inside 3e-2; the
-FP32 wide path is held to 1e-2."""
+wide path is held to 1e-2."""
 import pytest
 import torch
 
