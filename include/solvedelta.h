@@ -108,11 +108,13 @@ int sd_fwd_noalloc(const sd_inputs *in, void *out, float *C_T, float *S_T, void 
  * set take reset_value.  flags: uint8 [B,T] at flags[b*flags_sb + t*flags_st],
  * bit 0 valid, bit 1 reset.  Used forward (operands: zero invalid tokens, kill
  * the log-decay of reset tokens) and backward (gradients: zero on invalid
- * tokens, zero log-decay gradient on reset tokens). */
+ * tokens, zero log-decay gradient on reset tokens).  dst == src masks in place
+ * (src must then be contiguous): only the rows that change are written.
+ * Returns SD_ERR_ARG for dst == src with a non-contiguous src. */
 typedef struct {
   const void *src; /* element (b,t,h,c) at src[b*sb + t*st + h*sh + c] */
   int64_t sb, st, sh;
-  void *dst;       /* contiguous [B,T,H,width] */
+  void *dst;       /* contiguous [B,T,H,width]; or src itself (in place) */
   int width, is_fp32, reset_fill;
   float reset_value;
 } sd_mask_tensor;

@@ -2,7 +2,9 @@
 // repacking): one launch copies up to eight [B,T,H,w] tensors, keeping the
 // rows of valid tokens, zeroing the others, and giving the log-decay rows of
 // reset tokens a fixed value.  The same kernel masks the gradients on the way
-// back (zero on invalid tokens, zero log-decay gradient on reset tokens).
+// back (zero on invalid tokens, zero log-decay gradient on reset tokens), in
+// place when the destination is the (contiguous) source: then only the rows it
+// changes are written and nothing is read but the flags.
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
 #include "../../include/solvedelta.h"
@@ -23,6 +25,7 @@ struct MaskJob {
 struct MaskJobExt {
   MaskJob job;
   int vec[kMaxMasked];
+  int inplace[kMaxMasked];
 };
 
 __global__ __launch_bounds__(256) void k_mask_rows(MaskJobExt jx, int B, int T, int H,
@@ -40,12 +43,14 @@ __global__ __launch_bounds__(256) void k_mask_rows(MaskJobExt jx, int B, int T, 
   const int hh = (int)(row % H), t = (int)((row / H) % T), b = (int)(row / ((long long)H * T));
   const uint8_t f = flags[(long long)b * f_sb + (long long)t * f_st];
   const bool valid = f & 1, reset = (f & 2) != 0;
+  const bool fill = valid && reset && m.reset_fill;
+  if (jx.inplace[blockIdx.y] && valid && !fill) return;  // the row keeps its values
   const long long so = (long long)b * m.sb + (long long)t * m.st + (long long)hh * m.sh;
   const long long dof = row * w;
   if (jx.vec[blockIdx.y]) {
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (valid) v = *reinterpret_cast<const uint4*>((const char*)m.src + (so + c0) * esz);
-    if (valid && reset && m.reset_fill) {
+    if (valid && !fill) v = *reinterpret_cast<const uint4*>((const char*)m.src + (so + c0) * esz);
+    if (fill) {
       if (m.is_fp32) {
         const unsigned r = __float_as_uint(m.reset_value);
         v = make_uint4(r, r, r, r);
@@ -94,6 +99,10 @@ extern "C" int sd_mask_rows(int B, int T, int H, const uint8_t* flags, int64_t f
                      (m.width * esz) % 16 == 0 && (m.sb * esz) % 16 == 0 &&
                      (m.st * esz) % 16 == 0 && (m.sh * esz) % 16 == 0;
     jx.vec[i] = vec;
+    // in place: the destination is the source itself, stored contiguously
+    jx.inplace[i] = m.src == m.dst && m.sh == m.width && m.st == (int64_t)H * m.width &&
+                    m.sb == (int64_t)T * H * m.width;
+    if (m.src == m.dst && !jx.inplace[i]) return SD_ERR_ARG;
     const long long per = vec ? 16 / esz : 4;
     const long long items = (long long)B * T * H * ((m.width + per - 1) / per);
     work = items > work ? items : work;

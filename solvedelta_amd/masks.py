@@ -71,11 +71,13 @@ def _mask_tensor(src: torch.Tensor, dst: torch.Tensor, reset_fill: bool, reset_v
                              int(reset_fill), reset_value)
 
 
-def _mask_rows(flags, srcs, decay_last: bool, reset_value: float):
-    """Masked contiguous copies of srcs ([B,T,H,...,w] views, unit inner stride);
+def _mask_rows(flags, srcs, decay_last: bool, reset_value: float, inplace: bool = False):
+    """Masked contiguous copies of srcs ([B,T,H,...,w] views, unit inner stride),
+    or, with inplace, srcs themselves masked in place (each must be contiguous);
     the last one is the log-decay (or its gradient) when decay_last."""
     B, T, H = srcs[0].shape[:3]
-    outs = [torch.empty(x.shape, dtype=x.dtype, device=x.device) for x in srcs]
+    outs = list(srcs) if inplace else [torch.empty(x.shape, dtype=x.dtype, device=x.device)
+                                       for x in srcs]
     arr = (_lib.SdMaskTensor * len(srcs))(*[
         _mask_tensor(x, o, decay_last and i == len(srcs) - 1, reset_value)
         for i, (x, o) in enumerate(zip(srcs, outs))])
@@ -102,8 +104,11 @@ class _MaskOperands(torch.autograd.Function):
         live = [i for i, g in enumerate(grads) if g is not None]
         out = [None] * len(grads)
         if live:
-            srcs = [grads[i] if grads[i].stride(-1) == 1 else grads[i].contiguous() for i in live]
-            masked = _mask_rows(flags, srcs, live[-1] == len(grads) - 1, 0.0)
+            # The incoming gradients are this function's alone (the masked
+            # operands feed only the operator), so they are masked in place:
+            # only invalid rows (and reset tokens' log-decay rows) are written.
+            srcs = [grads[i].contiguous() for i in live]
+            masked = _mask_rows(flags, srcs, live[-1] == len(grads) - 1, 0.0, inplace=True)
             for i, m in zip(live, masked):
                 out[i] = m
         return (None, *out)

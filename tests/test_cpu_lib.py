@@ -108,3 +108,26 @@ def test_packed_segment_plan_on_cpu():
     assert plan.max_seqlen == 5
     with pytest.raises(ValueError):
         build_packed_segments(valid.int(), reset)
+
+
+def test_mask_rows_argument_rejection():
+    """sd_mask_rows checks its arguments before any launch: in-place masking
+    (dst == src) needs a contiguous source, and at most eight tensors."""
+    from solvedelta_amd import _lib
+    lib = _lib.load()
+    flags = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails its checks
+    B, T, H, w = 2, 5, 3, 8
+    fake = 0x2000
+
+    def call(sb, st, sh, dst, n=1):
+        arr = (_lib.SdMaskTensor * 9)(*[_lib.SdMaskTensor(fake, sb, st, sh, dst, w, 0, 0, 0.0)
+                                        for _ in range(9)])
+        return lib.sd_mask_rows(B, T, H, flags, T, 1, arr, n, None)
+
+    # in place over a strided (non-contiguous) source
+    assert call(2 * T * H * w, 2 * H * w, w, fake) == _lib.SD_ERR_ARG
+    assert call(T * H * w, H * w, 2 * w, fake) == _lib.SD_ERR_ARG
+    # null destination, too many tensors, empty shape
+    assert call(T * H * w, H * w, w, 0) == _lib.SD_ERR_ARG
+    assert call(T * H * w, H * w, w, 0x3000, n=9) == _lib.SD_ERR_SHAPE
+    assert lib.sd_mask_rows(0, T, H, flags, T, 1, None, 1, None) == _lib.SD_ERR_SHAPE
