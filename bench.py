@@ -428,6 +428,8 @@ def main():
                     help="also time the causal LM step through its HIP graph")
     ap.add_argument("--step-only", action="store_true",
                     help="only the headline forward+VJP steps (counter runs)")
+    ap.add_argument("--variant", choices=["wide", "masked"],
+                    help="only that variant's F+B line (its kernel profiles)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration)")
     a = ap.parse_args()
@@ -439,6 +441,10 @@ def main():
     dev = torch.device("cuda:0")
     if a.copy_calibration:
         copy_calibration(dev)
+        return
+    if a.variant:
+        kw = dict(r=256, v=256) if a.variant == "wide" else dict(masked=True)
+        print(json.dumps({a.variant: variant_bench(dev, a.steps, a.warmup, **kw)}), flush=True)
         return
     from solvedelta_amd import _lib, solvedelta_native
     ins, st, dO = make_inputs(dev)
