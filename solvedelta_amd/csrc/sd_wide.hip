@@ -674,44 +674,6 @@ __global__ __launch_bounds__(ST) void k_w_state(WStateParams p) {
   }
 }
 
-// acc[i] += sum_r A[i][r] X[r][c] over r < kw for this thread's value column
-// c = threadIdx.x (< vw): X [kw][vw] (global) is staged through LDS in 32-row
-// blocks with 16-byte loads; A [32][lda] is in LDS.  Every thread of the
-// workgroup must call it (it synchronises).
-__device__ __forceinline__ void rows_times_x(const float* A, int lda, const xs_t* X, int kw,
-                                             int vw, float* buf, float (&acc)[WBT]) {
-  const int c = threadIdx.x, lb = vw + 4;
-  constexpr int PQ = 32 * WMAX / 4 / WT;  // 4-element pieces per thread of a 32-row block
-  const int npc = 32 * vw / 4;
-  float4 nx[PQ];  // the next row block, loaded while the current one is used
-  auto fetch = [&](int rb) {
-#pragma unroll
-    for (int q = 0; q < PQ; ++q) {
-      const int idx = threadIdx.x + WT * q, i = (idx * 4) / vw, cc = (idx * 4) % vw;
-      if (idx < npc) nx[q] = ld4s(X + (long long)(rb + i) * vw + cc);
-    }
-  };
-  fetch(0);
-  for (int rb = 0; rb < kw; rb += 32) {
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < PQ; ++q) {
-      const int idx = threadIdx.x + WT * q, i = (idx * 4) / vw, cc = (idx * 4) % vw;
-      if (idx < npc) *reinterpret_cast<float4*>(buf + i * lb + cc) = nx[q];
-    }
-    __syncthreads();
-    if (rb + 32 < kw) fetch(rb + 32);
-    if (c < vw) {
-#pragma unroll 4
-      for (int k = 0; k < 32; ++k) {
-        const float x = buf[k * lb + c];
-#pragma unroll
-        for (int i = 0; i < WBT; ++i) acc[i] += A[i * lda + rb + k] * x;
-      }
-    }
-  }
-}
-
 struct OutParams {
   int NT, Tp, kw, vw, colout, H, T, V;
   const xs_t* slots;
@@ -726,34 +688,127 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
   const long long tb = (long long)s * p.Tp + ch * WBT;
   const xs_t* X0 = p.slots + ((long long)s * (p.NT + 1) + ch) * kw * vw;
   if (p.colout) {
-    const int ld = kw + 1;
-    float* Ql = sm;                 // [32][kw+1]
-    float* Pl = Ql + WBT * ld;      // [32][33]
-    float* Xb = Pl + WBT * MS;      // X0 row block [32][vw+4]
-    {
-      const float* const src[1] = {p.Qt};
-      float* const dst[1] = {Ql};
-      stage_panels<1>(src, dst, tb, kw, ld);
+    // Column output on matrix cores: o = Q~ X0 + P w.
+    //   Q~ X0 on v_mfma_f32_16x16x32_f16: Q~ (|Q~| <= 1) split into fp16 high and
+    //   low halves, X0 exact in its fp16 slot; the slot is row-major, so each
+    //   32-row block is staged transposed ([column][row]) through LDS, the
+    //   next block's loads in flight while the current one is used;
+    //   P w (32 tokens) on v_mfma_f32_16x16x4f32 from FP32 P and w.
+    // Wave w owns output tiles (token block t2, column block w + 4 j).
+    using h8 = f16x8;
+    constexpr int QLD = WMAX + 8, XTL = WBT + 8, PLD = WBT + 4, NJ = WMAX / 16 / 4;
+    _Float16* Qh = reinterpret_cast<_Float16*>(sm);  // Q~ high / low [32][QLD]
+    _Float16* Qo = Qh + WBT * QLD;
+    _Float16* Xt = Qo + WBT * QLD;                   // X0 row block, transposed [vw][XTL]
+    float* Pl = reinterpret_cast<float*>(Xt + WMAX * XTL);  // P [32][PLD]
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15, kq = g * 8;
+    const int nvb = vw / 16;
+    // this lane's w values for the P w product: B[k = 4 g + e][n = m] of token block kb
+    float wb[NJ][2][4];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int nb = w + 4 * j;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          wb[j][kb][e] = nb < nvb ? p.w[(tb + kb * 16 + 4 * g + e) * vw + nb * 16 + m] : 0.f;
     }
-    const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
-    for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) Pl[(idx >> 5) * MS + (idx & 31)] = p.P[mb + idx];
-    float acc[WBT];
+    // X0 row-block staging: task (column c, 8-row group rg), 8 rows of one column
+    constexpr int XQ = WMAX * 4 / WT;  // tasks per thread at vw = 256
+    h8 xr[XQ];
+    auto fetch = [&](int rb) {
 #pragma unroll
-    for (int i = 0; i < WBT; ++i) acc[i] = 0.f;
-    rows_times_x(Ql, ld, X0, kw, vw, Xb, acc);  // Q~ X0 (synchronises first)
-    const int c = threadIdx.x;
-    if (c >= vw) return;
-    float wc[WBT];
+      for (int q = 0; q < XQ; ++q) {
+        const int task = threadIdx.x + WT * q, c = task % vw, rg = task / vw;
+        if (task < vw * 4)
 #pragma unroll
-    for (int j = 0; j < WBT; ++j) wc[j] = p.w[(tb + j) * vw + c];
+          for (int j = 0; j < 8; ++j) xr[q][j] = X0[(long long)(rb + rg * 8 + j) * vw + c];
+      }
+    };
+    fetch(0);
+    // Q~ split into LDS; P into LDS
+    {
+      const long long mb = ((long long)s * p.NT + ch) * WBT * WBT;
+      for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) Pl[(idx >> 5) * PLD + (idx & 31)] = p.P[mb + idx];
+      constexpr int PQ = WBT * WMAX / 4 / WT;
+      float4 qv[PQ];
+#pragma unroll
+      for (int q = 0; q < PQ; ++q) {
+        const int idx = threadIdx.x + WT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
+        if (idx < WBT * kw / 4) qv[q] = *reinterpret_cast<const float4*>(p.Qt + (tb + i) * kw + c);
+      }
+#pragma unroll
+      for (int q = 0; q < PQ; ++q) {
+        const int idx = threadIdx.x + WT * q, i = (idx * 4) / kw, c = (idx * 4) % kw;
+        if (idx < WBT * kw / 4) {
+          f4 v = {qv[q].x, qv[q].y, qv[q].z, qv[q].w};
+          f16x4 hi, lo;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            hi[e] = (_Float16)v[e];
+            lo[e] = (_Float16)(v[e] - (float)hi[e]);
+          }
+          *reinterpret_cast<f16x4*>(Qh + i * QLD + c) = hi;
+          *reinterpret_cast<f16x4*>(Qo + i * QLD + c) = lo;
+        }
+      }
+    }
+    f4 acc[2][NJ];
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[t2][j] = zero4();
+    for (int rb = 0; rb < kw; rb += 32) {
+      __syncthreads();  // the previous block's readers are done
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) {
+        const int task = threadIdx.x + WT * q, c = task % vw, rg = task / vw;
+        if (task < vw * 4) *reinterpret_cast<h8*>(Xt + c * XTL + rg * 8) = xr[q];
+      }
+      __syncthreads();
+      if (rb + 32 < kw) fetch(rb + 32);
+      h8 ah[2], al[2];
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        ah[t2] = *reinterpret_cast<const h8*>(Qh + (t2 * 16 + m) * QLD + rb + kq);
+        al[t2] = *reinterpret_cast<const h8*>(Qo + (t2 * 16 + m) * QLD + rb + kq);
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int nb = w + 4 * j;
+        if (nb >= nvb) continue;
+        const h8 bx = *reinterpret_cast<const h8*>(Xt + (nb * 16 + m) * XTL + kq);
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          acc[t2][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t2], bx, acc[t2][j], 0, 0, 0);
+          acc[t2][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t2], bx, acc[t2][j], 0, 0, 0);
+        }
+      }
+    }
+    // + P w, then the bf16 output
     const int b = s / p.H, h = s % p.H;
 #pragma unroll
-    for (int i = 0; i < WBT; ++i) {
-      float a = acc[i];
+    for (int j = 0; j < NJ; ++j) {
+      const int nb = w + 4 * j;
+      if (nb >= nvb) continue;
 #pragma unroll
-      for (int j = 0; j <= i; ++j) a += Pl[i * MS + j] * wc[j];
-      const int t = ch * WBT + i;
-      if (t < p.T && c < p.V) p.out[(((long long)b * p.T + t) * p.H + h) * p.V + c] = f2bf(a);
+      for (int t2 = 0; t2 < 2; ++t2) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const float4 a4 = *reinterpret_cast<const float4*>(Pl + (t2 * 16 + m) * PLD + kb * 16 + 4 * g);
+          acc[t2][j] = mfma4(a4.x, wb[j][kb][0], acc[t2][j]);
+          acc[t2][j] = mfma4(a4.y, wb[j][kb][1], acc[t2][j]);
+          acc[t2][j] = mfma4(a4.z, wb[j][kb][2], acc[t2][j]);
+          acc[t2][j] = mfma4(a4.w, wb[j][kb][3], acc[t2][j]);
+        }
+        const int c = nb * 16 + m;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = ch * WBT + t2 * 16 + 4 * g + e;
+          if (t < p.T && c < p.V) p.out[(((long long)b * p.T + t) * p.H + h) * p.V + c] = f2bf(acc[t2][j][e]);
+        }
+      }
     }
     return;
   }
@@ -847,7 +902,8 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
 }
 
 constexpr size_t out_smem(int kw, int vw, int colout) {
-  if (colout) return (size_t)(WBT * (kw + 1) + WBT * MS + WBT * (vw + 4)) * sizeof(float);
+  // column output: Q~ high / low [32][WMAX+8] and X0 block [WMAX][40] fp16, P [32][36]
+  if (colout) return (size_t)(2 * WBT * (WMAX + 8) + WMAX * (WBT + 8)) * 2 + WBT * (WBT + 4) * sizeof(float);
   return (size_t)(WBT * MS) * sizeof(float);
 }
 
