@@ -815,8 +815,38 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
   // row output on matrix cores: M = q w^T (j <= i), then
   //   o_ir = e^{G_ir} ((q X0^T)_ir + (M k~)_ir),  k~_jr = k_jr e^{-G_jr}
   // with the decay factored per state row r (wild rows: exact per-term sum).
+  // q X0^T runs on v_mfma_f32_16x16x32_f16: q (unit rows) split into fp16 high
+  // and low halves in LDS, X0 exact in its fp16 slot (the contraction runs
+  // along the slot's rows, so each lane's fragment is one 16-byte load).
+  constexpr int QLD = WMAX + 8;
   float* Ml = sm;  // [32][33]
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
+  _Float16* Qh = reinterpret_cast<_Float16*>(Ml + WBT * MS);  // q high / low [32][QLD]
+  _Float16* Qo = Qh + WBT * QLD;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15, kq = g * 8;
+  {
+    constexpr int PQ = WBT * WMAX / 4 / WT;
+    float4 qv[PQ];
+#pragma unroll
+    for (int q = 0; q < PQ; ++q) {
+      const int idx = threadIdx.x + WT * q, i = (idx * 4) / vw, c = (idx * 4) % vw;
+      if (idx < WBT * vw / 4) qv[q] = *reinterpret_cast<const float4*>(p.q + (tb + i) * vw + c);
+    }
+#pragma unroll
+    for (int q = 0; q < PQ; ++q) {
+      const int idx = threadIdx.x + WT * q, i = (idx * 4) / vw, c = (idx * 4) % vw;
+      if (idx < WBT * vw / 4) {
+        f4 v = {qv[q].x, qv[q].y, qv[q].z, qv[q].w};
+        f16x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hi[e] = (_Float16)v[e];
+          lo[e] = (_Float16)(v[e] - (float)hi[e]);
+        }
+        *reinterpret_cast<f16x4*>(Qh + i * QLD + c) = hi;
+        *reinterpret_cast<f16x4*>(Qo + i * QLD + c) = lo;
+      }
+    }
+  }
   {
     const int bi = w >> 1, bj = w & 1;
     f4 acc = zero4();
@@ -844,16 +874,15 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
     const int rr = rb * 16 + m;
     const bool wild = -p.G[(tb + WBT - 1) * kw + rr] > WILD;
     f4 acc[2] = {zero4(), zero4()};
-#pragma unroll 2
-    for (int cb = 0; cb < vw; cb += 16) {
-      const float4 bx = ld4s(X0 + (long long)rr * vw + cb + 4 * g);
+#pragma unroll 4
+    for (int cb = 0; cb < vw; cb += 32) {
+      const f16x8 bx = *reinterpret_cast<const f16x8*>(X0 + (long long)rr * vw + cb + kq);
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
-        const float4 a4 = *reinterpret_cast<const float4*>(p.q + (tb + t2 * 16 + m) * vw + cb + 4 * g);
-        acc[t2] = mfma4(a4.x, bx.x, acc[t2]);
-        acc[t2] = mfma4(a4.y, bx.y, acc[t2]);
-        acc[t2] = mfma4(a4.z, bx.z, acc[t2]);
-        acc[t2] = mfma4(a4.w, bx.w, acc[t2]);
+        const f16x8 ah = *reinterpret_cast<const f16x8*>(Qh + (t2 * 16 + m) * QLD + cb + kq);
+        const f16x8 al = *reinterpret_cast<const f16x8*>(Qo + (t2 * 16 + m) * QLD + cb + kq);
+        acc[t2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bx, acc[t2], 0, 0, 0);
+        acc[t2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bx, acc[t2], 0, 0, 0);
       }
     }
     float kt[2][4];
@@ -904,7 +933,7 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
 constexpr size_t out_smem(int kw, int vw, int colout) {
   // column output: Q~ high / low [32][WMAX+8] and X0 block [WMAX][40] fp16, P [32][36]
   if (colout) return (size_t)(2 * WBT * (WMAX + 8) + WMAX * (WBT + 8)) * 2 + WBT * (WBT + 4) * sizeof(float);
-  return (size_t)(WBT * MS) * sizeof(float);
+  return (size_t)(WBT * MS) * sizeof(float) + (size_t)2 * WBT * (WMAX + 8) * 2;  // M; q high / low
 }
 
 // ---------------------------------------------------------------------------
@@ -1769,7 +1798,7 @@ int launch_wide_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, void
   orow.NT = d.NT; orow.Tp = d.Tp; orow.kw = d.KP; orow.vw = d.KP; orow.colout = 0;
   orow.slots = w.XC; orow.w = w.delta; orow.q = w.kh; orow.k = w.uh; orow.G = w.G;
   orow.base = w.kh; orow.o = w.oC; orow.d = w.d;
-  SD_SMEM_ONCE(k_w_out, (int)out_smem(WMAX, WMAX, 0));
+  SD_SMEM_ONCE(k_w_out, (int)(out_smem(WMAX, WMAX, 0) > out_smem(WMAX, WMAX, 1) ? out_smem(WMAX, WMAX, 0) : out_smem(WMAX, WMAX, 1)));
   SD_LAUNCH("k_w_out_c", k_w_out, dim3(d.NT, d.n), dim3(WT), out_smem(d.KP, d.KP, 0), st, orow);
 
   SrcParams sp{};
