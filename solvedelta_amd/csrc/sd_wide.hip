@@ -1160,13 +1160,12 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   const int wv_ = r >> 6, l = r & 63, g = l >> 4, m = l & 15;
   const int nrb = kw / 16, nvb = vw / 16;
   const float* Y = p.colout ? p.dO : p.q;  // [Tp][vw]
-  // phase 1 on FP32 matrix cores (sum index c = 16 cb + 4 g + e: MFMA e, lane
-  // group g): the row products dwX = dw X0^T, wL = w lam^T, dOX = dO X0^T
+  // phase 1 on matrix cores: the row products dwX = dw X0^T, wL = w lam^T, dOX = dO X0^T
   // (column output) over this wave's 16-row blocks of the state, kept in
   // accumulators (lane (g, n): tokens 4g..4g+3 of state row 16 rb + n) for
   // phase 3, and the token Grams M1 = dw w^T, M2 = Y w^T (one 16 x 16 block of
-  // each per wave of the first four), all from 16-byte global loads of the
-  // rows involved.
+  // each per wave of the first four); the rows from LDS, the state slots by
+  // 16-byte global loads.
   f4 aX[GRB][2], aL[GRB][2], aO[GRB][2];
   float rs[GRB];  // partial rowsum(X_C (.) lam) of state row 16 rb + m over this lane's columns
 #pragma unroll
@@ -1195,54 +1194,78 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
     f4 m1a = zero4(), m2a = zero4();
     const int bi = (wv_ >> 1) & 1, bj = wv_ & 1;
     const bool gram = wv_ < 4;  // one 16 x 16 block of M1 and M2 per wave of the first four
+    const int kq = g * 8;
+    // 16-bit matrix cores over K = 32 columns per step (bf16: the cotangents
+    // may take any scale).  The FP32 rows dw, w, Y and the fp16 state X0 enter
+    // split into bf16 high and low halves (three MFMAs per product: hi.hi,
+    // hi.lo, lo.hi); lambda is exact in its bf16 slot (two MFMAs).
+    auto split8 = [](const float* v, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const __bf16 h = (__bf16)v[j];
+        hi[j] = h;
+        lo[j] = (__bf16)(v[j] - (float)h);
+      }
+    };
+    auto mma = [](bf16x8 a, bf16x8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); };
 #pragma unroll 2
-    for (int cb = 0; cb < vw; cb += 16) {
-      float4 adw[2], aw[2], ay[2];
+    for (int cb = 0; cb < vw; cb += 32) {
+      bf16x8 dwh[2], dwl[2], wh[2], wl[2], yh[2], yl[2];
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
-        const int o = (t2 * 16 + m) * lt + cb + 4 * g;
-        adw[t2] = *reinterpret_cast<const float4*>(TR + o);
-        aw[t2] = *reinterpret_cast<const float4*>(TR + WBT * lt + o);
-        ay[t2] = *reinterpret_cast<const float4*>(TR + 2 * WBT * lt + o);
+        const int o = (t2 * 16 + m) * lt + cb + kq;
+        float v[8];
+        *reinterpret_cast<float4*>(v) = *reinterpret_cast<const float4*>(TR + o);
+        *reinterpret_cast<float4*>(v + 4) = *reinterpret_cast<const float4*>(TR + o + 4);
+        split8(v, dwh[t2], dwl[t2]);
+        *reinterpret_cast<float4*>(v) = *reinterpret_cast<const float4*>(TR + WBT * lt + o);
+        *reinterpret_cast<float4*>(v + 4) = *reinterpret_cast<const float4*>(TR + WBT * lt + o + 4);
+        split8(v, wh[t2], wl[t2]);
+        *reinterpret_cast<float4*>(v) = *reinterpret_cast<const float4*>(TR + 2 * WBT * lt + o);
+        *reinterpret_cast<float4*>(v + 4) = *reinterpret_cast<const float4*>(TR + 2 * WBT * lt + o + 4);
+        split8(v, yh[t2], yl[t2]);
       }
 #pragma unroll
       for (int q = 0; q < GRB; ++q) {
         const int rb = wv_ + GW * q;
         if (rb < nrb) {
-          const long long o = (long long)(rb * 16 + m) * vw + cb + 4 * g;
-          const float4 bx = ld4s(X0 + o);
-          const float4 bl = ld4s(Lm + o);
-          const float4 bc = ld4s(XC + o);
-          rs[q] += bc.x * bl.x + bc.y * bl.y + bc.z * bl.z + bc.w * bl.w;
+          const long long o = (long long)(rb * 16 + m) * vw + cb + kq;
+          const f16x8 x8 = *reinterpret_cast<const f16x8*>(X0 + o);
+          const f16x8 c8 = *reinterpret_cast<const f16x8*>(XC + o);
+          const bf16x8 lb = *reinterpret_cast<const bf16x8*>(Lm + o);
+          float xv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            xv[j] = (float)x8[j];
+            rs[q] += (float)c8[j] * (float)lb[j];
+          }
+          bf16x8 xh, xl;
+          split8(xv, xh, xl);
 #pragma unroll
           for (int t2 = 0; t2 < 2; ++t2) {
-            aX[q][t2] = mfma4(adw[t2].x, bx.x, aX[q][t2]);
-            aX[q][t2] = mfma4(adw[t2].y, bx.y, aX[q][t2]);
-            aX[q][t2] = mfma4(adw[t2].z, bx.z, aX[q][t2]);
-            aX[q][t2] = mfma4(adw[t2].w, bx.w, aX[q][t2]);
-            aL[q][t2] = mfma4(aw[t2].x, bl.x, aL[q][t2]);
-            aL[q][t2] = mfma4(aw[t2].y, bl.y, aL[q][t2]);
-            aL[q][t2] = mfma4(aw[t2].z, bl.z, aL[q][t2]);
-            aL[q][t2] = mfma4(aw[t2].w, bl.w, aL[q][t2]);
+            aX[q][t2] = mma(dwl[t2], xh, aX[q][t2]);
+            aX[q][t2] = mma(dwh[t2], xl, aX[q][t2]);
+            aX[q][t2] = mma(dwh[t2], xh, aX[q][t2]);
+            aL[q][t2] = mma(wl[t2], lb, aL[q][t2]);
+            aL[q][t2] = mma(wh[t2], lb, aL[q][t2]);
             if (p.colout) {
-              aO[q][t2] = mfma4(ay[t2].x, bx.x, aO[q][t2]);
-              aO[q][t2] = mfma4(ay[t2].y, bx.y, aO[q][t2]);
-              aO[q][t2] = mfma4(ay[t2].z, bx.z, aO[q][t2]);
-              aO[q][t2] = mfma4(ay[t2].w, bx.w, aO[q][t2]);
+              aO[q][t2] = mma(yl[t2], xh, aO[q][t2]);
+              aO[q][t2] = mma(yh[t2], xl, aO[q][t2]);
+              aO[q][t2] = mma(yh[t2], xh, aO[q][t2]);
             }
           }
         }
       }
       if (gram) {  // selects, not indexing: a runtime index would put the arrays in scratch
-        const float4 da = bi ? adw[1] : adw[0], ya = bi ? ay[1] : ay[0], wb = bj ? aw[1] : aw[0];
-        m1a = mfma4(da.x, wb.x, m1a);
-        m1a = mfma4(da.y, wb.y, m1a);
-        m1a = mfma4(da.z, wb.z, m1a);
-        m1a = mfma4(da.w, wb.w, m1a);
-        m2a = mfma4(ya.x, wb.x, m2a);
-        m2a = mfma4(ya.y, wb.y, m2a);
-        m2a = mfma4(ya.z, wb.z, m2a);
-        m2a = mfma4(ya.w, wb.w, m2a);
+        const bf16x8 dah = bi ? dwh[1] : dwh[0], dal = bi ? dwl[1] : dwl[0];
+        const bf16x8 yah = bi ? yh[1] : yh[0], yal = bi ? yl[1] : yl[0];
+        const bf16x8 wbh = bj ? wh[1] : wh[0], wbl = bj ? wl[1] : wl[0];
+        m1a = mma(dal, wbh, m1a);
+        m1a = mma(dah, wbl, m1a);
+        m1a = mma(dah, wbh, m1a);
+        m2a = mma(yal, wbh, m2a);
+        m2a = mma(yah, wbl, m2a);
+        m2a = mma(yah, wbh, m2a);
       }
     }
     if (gram)
