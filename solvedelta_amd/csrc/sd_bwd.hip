@@ -255,6 +255,26 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       wks[Jb] = wk;
     }
   }
+  // The chunk-transposed panels' loads are issued before the dU and Wk stores
+  // below (a load issued after a store waits for it: one counter retires both).
+  // Fragment order: a thread's two pieces are (state row c, tokens i0 .. i0+7).
+  constexpr int NPC = KD * BT / 8 / CT;
+  float ev[NPC][8];
+  SPRaw qv[NPC][8];
+  DoutRaw d[NPC][8];
+#pragma unroll
+  for (int q = 0; q < NPC; ++q) {
+    const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
+    const int c = (block / (BT / 32)) * 16 + (lane & 15);
+    const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = i0 + e;
+      ev[q][e] = (float)p.f.e[(rowbase + i) * KD + c];
+      qv[q][e] = sp_raw(p.f.Qs, rowbase * KD + frag_off(i, c, KD));
+      d[q][e] = dout_raw(p, b, t0 + i, hh, c);
+    }
+  }
   store_du_slab(p.g.dU + rowbase * KD, dus);
   // Wk staged in the free P / N rows, then stored in fragment order
   __syncthreads();
@@ -268,25 +288,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
     store_frag_panel1<BT, KD>(p.g.Wk, rowbase * KD,
                              [&](int i, int c) { return Wst[i * KD + c]; });
   }
-  {  // chunk-transposed panels, fragment order: a thread's two pieces are
-     // (state row c, tokens i0 .. i0+7); all their loads are issued first
-    constexpr int NPC = KD * BT / 8 / CT;
-    float ev[NPC][8];
-    SPRaw qv[NPC][8];
-    DoutRaw d[NPC][8];
-#pragma unroll
-    for (int q = 0; q < NPC; ++q) {
-      const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
-      const int c = (block / (BT / 32)) * 16 + (lane & 15);
-      const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = i0 + e;
-        ev[q][e] = (float)p.f.e[(rowbase + i) * KD + c];
-        qv[q][e] = sp_raw(p.f.Qs, rowbase * KD + frag_off(i, c, KD));
-        d[q][e] = dout_raw(p, b, t0 + i, hh, c);
-      }
-    }
+  {
 #pragma unroll
     for (int q = 0; q < NPC; ++q) {
       const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
@@ -540,6 +542,7 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   const float de0 = p.g.de[row + l], de1 = p.g.de[row + l + 64];
   const float dc0 = p.g.dchi[row + l], dc1 = p.g.dchi[row + l + 64];
   const float dz0 = p.g.dwS[row + l], dz1 = p.g.dwS[row + l + 64];
+  const float dd0 = p.g.dd[row + l], dd1 = p.g.dd[row + l + 64];  // loaded before any store
   const float usq = wave_sum(u0 * u0 + u1 * u1);
   const float dsq = wave_sum(d0 * d0 + d1 * d1);
   const float N = sqrtf(RHO * RHO + usq * dsq);
@@ -594,7 +597,6 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
     p.dv[tok * V + l + 64] = f2bf(dv1);
     p.dwr[tok * V + l + 64] = f2bf(dwr1);
   }
-  const float dd0 = p.g.dd[row + l], dd1 = p.g.dd[row + l + 64];
   p.g.ddelta[row + l] = l < r ? ddl0 : 0.f;
   p.g.ddelta[row + l + 64] = l + 64 < r ? ddl1 : 0.f;
   p.g.du_src[row + l] = duh0;
@@ -666,14 +668,6 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       false, s.P);
   mat64_mul(s.P, s.A, s.N);
   __syncthreads();
-  // P' is also the C chunk gradient's dq operand: stored once here (upper
-  // blocks zero) instead of formed again there
-  for (int idx = threadIdx.x * 4; idx < BT * BT; idx += CT * 4) {
-    const int i = idx / BT, j = idx % BT;
-    const float4 v = *reinterpret_cast<const float4*>(&s.P[i * LS + j]);
-    *reinterpret_cast<float4*>(p.g.Pp + cidx * BT * BT + idx) =
-        (j / BS > i / BS) ? make_float4(0.f, 0.f, 0.f, 0.f) : v;
-  }
   const bpan_t* ddl = p.g.ddelta + rowbase * KD;
   const long long kbase = cidx * KD * BT;
   f4 wks[NB], dus[NB];
@@ -719,6 +713,35 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       wks[Jb] = wk;
     }
   }
+  // The global inputs of the chunk-transposed panels below (dd for At1, the
+  // raw keys for B1t) are loaded before this kernel's stores: a load issued
+  // after a store waits for it (one counter retires both).  Fragment order: a
+  // thread's pieces are (state row c, tokens i0 .. i0+7).
+  constexpr int PIECES = KD * BT / 8, PER = PIECES / CT;
+  static_assert(PIECES % CT == 0, "whole pieces per thread");
+  float ddv[PER][8];
+  __bf16 kr[PER][8];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
+    const int c = (block / (BT / 32)) * 16 + (lane & 15);
+    const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {  // clamped address + mask: no guarded load
+      const int t = t0 + i0 + e;
+      ddv[q][e] = (float)ddp[(i0 + e) * KD + c];
+      const float v = bf2f(brow(p.in.k, b, t < p.T ? t : p.T - 1, hh)[c < p.r ? c : p.r - 1]);
+      kr[q][e] = (__bf16)keep_if(t < p.T && c < p.r, v);
+    }
+  }
+  // P' is also the C chunk gradient's dq operand: stored once here (upper
+  // blocks zero) instead of formed again there, after every load of the kernel
+  for (int idx = threadIdx.x * 4; idx < BT * BT; idx += CT * 4) {
+    const int i = idx / BT, j = idx % BT;
+    const float4 v = *reinterpret_cast<const float4*>(&s.P[i * LS + j]);
+    *reinterpret_cast<float4*>(p.g.Pp + cidx * BT * BT + idx) =
+        (j / BS > i / BS) ? make_float4(0.f, 0.f, 0.f, 0.f) : v;
+  }
   store_du_slab(p.g.dU + rowbase * KD, dus);
   __syncthreads();
   {
@@ -740,32 +763,19 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   // The reverse pass's injection sum_i At1_ci Kh_i,col is formed as
   // sum_i (At1_ci / |k_i|) k_i,col: its B operand is then the raw key input,
   // exact in bf16, so only a high half is stored (and read).
-  store_frag_panel1<KD, BT>(p.g.At1, cidx * KD * BT, [&](int c, int i) {
-    return (float)ddp[i * KD + c] * __expf(cd.G[i][c]) * s.krs[i];
-  });
-  {
-    constexpr int PIECES = KD * BT / 8, PER = PIECES / CT;
-    static_assert(PIECES % CT == 0, "whole pieces per thread");
-    __bf16 kr[PER][8];
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
-      const int c = (block / (BT / 32)) * 16 + (lane & 15);
-      const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
+  for (int q = 0; q < PER; ++q) {
+    const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
+    const int c = (block / (BT / 32)) * 16 + (lane & 15);
+    const int i0 = (block % (BT / 32)) * 32 + (lane >> 4) * 8;
+    bf16x8 a, h;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {  // clamped address + mask: no guarded load
-        const int t = t0 + i0 + e;
-        const float v = bf2f(brow(p.in.k, b, t < p.T ? t : p.T - 1, hh)[c < p.r ? c : p.r - 1]);
-        kr[q][e] = (__bf16)keep_if(t < p.T && c < p.r, v);
-      }
+    for (int e = 0; e < 8; ++e) {
+      a[e] = (__bf16)(ddv[q][e] * __expf(cd.G[i0 + e][c]) * s.krs[i0 + e]);
+      h[e] = kr[q][e];
     }
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      bf16x8 h;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = kr[q][e];
-      *reinterpret_cast<bf16x8*>(p.g.B1t + cidx * KD * BT + (long long)(threadIdx.x + q * CT) * 8) = h;
-    }
+    *reinterpret_cast<bf16x8*>(p.g.At1 + cidx * KD * BT + (long long)pc * 8) = a;
+    *reinterpret_cast<bf16x8*>(p.g.B1t + cidx * KD * BT + (long long)pc * 8) = h;
   }
   store_frag_panel1<KD, BT>(p.g.Ant, cidx * KD * BT, [&](int c, int i) {
     return -s.gam[i] * s.Uh[i][c] * __expf(gx_excl(cd, i, c));

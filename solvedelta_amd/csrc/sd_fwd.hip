@@ -616,7 +616,6 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       for (int e = 0; e < 4; ++e) {
         const int i = I * BS + r4 + e;
         const float dv = s.Pb[i][c] + __expf(cd.G[i][c]) * a1[I][e] + ap[e];
-        p.d[(rowbase + i) * KD + c] = (fpan_t)dv;
         s.Pc[i][c] = dv;
       }
     }
@@ -642,6 +641,18 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     for (int rr = 0; rr < RPW; ++rr) {
       load_row2(in.v, b, t0 + w + rr * CW, hh, T, V, vx[rr][0], vx[rr][1]);
       load_row2(in.write_raw, b, t0 + w + rr * CW, hh, T, V, wx[rr][0], wx[rr][1]);
+    }
+    {  // d to global memory only now, from this thread's own LDS entries: stored
+       // before the loads above, it would have held them (one counter retires both)
+      const int c = w * 16 + (l & 15), r4 = (l >> 4) * 4;
+      fpan_t* const d_b = p.d + rowbase * KD;
+#pragma unroll
+      for (int I = 0; I < NB; ++I)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = I * BS + r4 + e;
+          d_b[i * KD + c] = (fpan_t)s.Pc[i][c];
+        }
     }
     fpan_t* const e_b = p.e + rowbase * KD;
     fpan_t* const chi_b = p.chi + rowbase * KD;
