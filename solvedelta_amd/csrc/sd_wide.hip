@@ -1024,10 +1024,9 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
   float* dOl = Pl + WBT * MS;  // row output: dO, k, G [32][kw+1]
   float* kl = dOl + WBT * ld;
   float* Gl = kl + WBT * ld;
-  // per-thread column vectors [32][256] (element i of thread t at i*256+t),
-  // over the row-output panels once the Pp Gram is done with them
+  // column vectors [32][256] (element i of column t at i*256+t), over the
+  // row-output panels once the Pp Gram is done with them
   float* cv = dOl;
-  float* cw = cv + WBT * WT;
   const int tid = threadIdx.x;
   for (int idx = threadIdx.x; idx < WBT * WBT; idx += WT) {
     Al[(idx >> 5) * MS + (idx & 31)] = p.A[mb + idx];
@@ -1069,22 +1068,53 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
       kx[i] = p.x[o];
       ks2[i] = p.colout ? p.q[o] : p.dO[o];
     }
-  // value side: rhs and dU, one value column per thread
-  if (c < vw) {
+  // value side: rhs = dW + P^T Y and dU = A^T rhs on FP32 matrix cores (the sum
+  // index k = 4 g + e carried by MFMA e and lane group g, so the rhs
+  // accumulators are the B operands of the dU product as they stand); Y's
+  // columns are staged in LDS by one thread per value column
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
+  constexpr int NJ = WMAX / 16 / 4;  // column blocks per wave
+  if (c < vw)
     for (int i = 0; i < WBT; ++i)
       cv[i * WT + tid] = p.colout ? p.dO[(tb + i) * vw + c] : p.q[(tb + i) * vw + c];
-    for (int j = 0; j < WBT; ++j) {
-      float a = p.dW ? p.dW[(tb + j) * vw + c] : 0.f;
-      for (int i = j; i < WBT; ++i) a += Pl[i * MS + j] * cv[i * WT + tid];
-      cw[j * WT + tid] = a;
-    }
-    for (int m = 0; m < WBT; ++m) {
-      float a = 0.f;
-      for (int i = m; i < WBT; ++i) a += Al[i * MS + m] * cw[i * WT + tid];
-      p.dU[(tb + m) * vw + c] = a;
+  f4 rhs[2][NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int nb = w + 4 * j;
+        rhs[t2][j][e] = (p.dW && nb * 16 < vw) ? p.dW[(tb + t2 * 16 + 4 * g + e) * vw + nb * 16 + m] : 0.f;
+      }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int nb = w + 4 * j;
+    if (nb * 16 >= vw) continue;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          rhs[t2][j] = mfma4(Pl[(kb * 16 + 4 * g + e) * MS + t2 * 16 + m],
+                             cv[(kb * 16 + 4 * g + e) * WT + nb * 16 + m], rhs[t2][j]);
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      f4 du = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          du = mfma4(Al[(kb * 16 + 4 * g + e) * MS + t2 * 16 + m], rhs[kb][j][e], du);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p.dU[(tb + t2 * 16 + 4 * g + e) * vw + nb * 16 + m] = du[e];
     }
   }
-  // key side: Wn, Kn, Ia, one key coordinate per thread
+  __syncthreads();  // cv is reused for the decayed keys
+  // key side: Kn, Ia (transposed per chunk, one key coordinate per thread) and
+  // the decayed keys' columns for Wn = -A^T K^ (matrix cores, as dU)
   if (c < kw) {
     const float gl = kg[WBT - 1];
     const long long cb = (((long long)s * p.NT + ch) * kw + c) * WBT;
@@ -1101,16 +1131,29 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
         *reinterpret_cast<bf16x8*>(p.At + cb + i - 7) = av;
       }
     }
-    for (int m = 0; m < WBT; ++m) {
-      float a = 0.f;
-      for (int i = m; i < WBT; ++i) a += Al[i * MS + m] * cv[i * WT + tid];
-      p.Wneg[(tb + m) * kw + c] = (__bf16)a;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int nb = w + 4 * j;
+    if (nb * 16 >= kw) continue;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      f4 a = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          a = mfma4(Al[(kb * 16 + 4 * g + e) * MS + t2 * 16 + m],
+                    cv[(kb * 16 + 4 * g + e) * WT + nb * 16 + m], a);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p.Wneg[(tb + t2 * 16 + 4 * g + e) * kw + nb * 16 + m] = (__bf16)a[e];
     }
   }
 }
 
 constexpr size_t bprep_smem(int kw) {
-  const size_t panels = 3 * WBT * (size_t)(kw + 1) + WMAX + 4, cols = 2 * WBT * WT;
+  const size_t panels = 3 * WBT * (size_t)(kw + 1) + WMAX + 4, cols = (size_t)WBT * WT;
   return (2 * WBT * MS + (panels > cols ? panels : cols)) * sizeof(float);
 }
 
