@@ -183,6 +183,15 @@ __device__ __forceinline__ void entry(int m, int& i, int& j) {
 // added exactly.
 constexpr float WILD = 60.f;
 
+// v_mfma_f32_16x16x4f32: used with the sum index k = 4 g + e carried by MFMA e
+// (e = 0..3) and lane group g = lane / 16, so an accumulator (lane (g, n)
+// holding rows 4g..4g+3 of column n) is the B operand of a following product
+// as it stands.
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+
 // The chunk's wild coordinates in increasing order (deterministic: wave
 // ballots and a prefix over the four waves), from the last row of the in-chunk
 // prefix G (row stride ld).  Every thread must call it; returns the count.
@@ -276,13 +285,22 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
     float* const dst[3] = {xs, ks, Gs};
     stage_panels<3>(src, dst, tb, kw, ld);
   }
-  // this thread's value column for U = A v, loaded before any store of the
-  // kernel (a load issued after a store waits for it: one counter retires both)
+  // this lane's values for U = A v (the MFMA B operand: tokens kb * 16 + 4 g + e
+  // of column block w + 4 j), loaded before any store of the kernel (a load
+  // issued after a store waits for it: one counter retires both)
   const int c = threadIdx.x;
-  float vv[WBT];
-  if (c < vw)
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
+  constexpr int NJ = WMAX / 16 / 4;
+  float vb[NJ][2][4];
 #pragma unroll
-    for (int i = 0; i < WBT; ++i) vv[i] = p.v[(tb + i) * vw + c];
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int nb = w + 4 * j;
+        vb[j][kb][e] = nb * 16 < vw ? p.v[(tb + kb * 16 + 4 * g + e) * vw + nb * 16 + m] : 0.f;
+      }
   __syncthreads();
   // L_ij = sum_c x_ic k_jc e^{Gx_ic - G_jc} (j < i); P_ij = sum_c q_ic k_jc e^{G_ic - G_jc} (j <= i)
   int* wl = reinterpret_cast<int*>(Ps + WBT * MS);
@@ -327,37 +345,50 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
     p.A[mb + idx] = Ls[(idx >> 5) * MS + (idx & 31)];
     if (p.colout) p.P[mb + idx] = Ps[(idx >> 5) * MS + (idx & 31)];
   }
-  // W = A x~, K^, Qt, Gam: one key coordinate per thread (-W and K^ in fp16 for
-  // the state pass, K^ transposed per chunk: this thread's 32 tokens contiguous)
+  // W = A x~ and U = A v on FP32 matrix cores (the sum index k = 4 g + e carried
+  // by MFMA e and lane group g); -W stored fp16 for the state pass
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int nb = w + 4 * j;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      if (nb * 16 < kw) {
+        f4 a = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int k = kb * 16 + 4 * g + e, cc = nb * 16 + m;
+            a = mfma4(Ls[(t2 * 16 + m) * MS + k], xs[k * ld + cc] * __expf(gx_at(Gs, ld, k, cc, p.excl)), a);
+          }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p.Wneg[(tb + t2 * 16 + 4 * g + e) * kw + nb * 16 + m] = (_Float16)(-a[e]);
+      }
+      if (nb * 16 < vw) {
+        f4 a = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a = mfma4(Ls[(t2 * 16 + m) * MS + kb * 16 + 4 * g + e], vb[j][kb][e], a);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p.U[(tb + t2 * 16 + 4 * g + e) * vw + nb * 16 + m] = a[e];
+      }
+    }
+  }
+  // K^, Qt, Gam: one key coordinate per thread (K^ in fp16 for the state pass,
+  // transposed per chunk: this thread's 32 tokens contiguous)
   if (c < kw) {
     _Float16* const kt = p.Kt + (((long long)s * p.NT + ch) * kw + c) * WBT;
     f16x8 kv;
-    float xt[WBT];
-#pragma unroll
-    for (int i = 0; i < WBT; ++i) xt[i] = xs[i * ld + c] * __expf(gx_at(Gs, ld, i, c, p.excl));
     const float gl = Gs[(WBT - 1) * ld + c];
 #pragma unroll
     for (int i = 0; i < WBT; ++i) {
-      float a = 0.f;
-#pragma unroll
-      for (int m = 0; m <= i; ++m) a += Ls[i * MS + m] * xt[m];
       const long long o = (tb + i) * kw + c;
-      p.Wneg[o] = (_Float16)(-a);
       kv[i & 7] = (_Float16)(ks[i * ld + c] * __expf(gl - Gs[i * ld + c]));
       if ((i & 7) == 7) *reinterpret_cast<f16x8*>(kt + i - 7) = kv;
       if (p.colout) p.Qt[o] = qs[i * ld + c] * __expf(Gs[i * ld + c]);
     }
     p.Gam[((long long)s * p.NT + ch) * kw + c] = __expf(gl);
-  }
-  // U = A v: one value column per thread
-  if (c < vw) {
-#pragma unroll
-    for (int i = 0; i < WBT; ++i) {
-      float a = 0.f;
-#pragma unroll
-      for (int m = 0; m <= i; ++m) a += Ls[i * MS + m] * vv[m];
-      p.U[(tb + i) * vw + c] = a;
-    }
   }
 }
 
@@ -413,10 +444,6 @@ constexpr int SPF = 2;               // prefetch ring depth (chunks)
 constexpr int XLD = WMAX + 8;        // row stride (16-bit) of the staged X0
 constexpr int WLD = WBT + 8;         // row stride (16-bit) of the staged w
 constexpr size_t state_smem() { return (size_t)(2 * STILE * XLD + 4 * STILE * WLD) * 2; }
-
-__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 template <bool REV> struct WStateT;
 template <> struct WStateT<false> {
