@@ -17,11 +17,6 @@ struct SP {
 };
 
 #ifdef __HIPCC__
-__device__ __forceinline__ void sp_store(const SP& sp, long long i, float x) {
-  const __bf16 h = (__bf16)x;
-  sp.hi[i] = h;
-  sp.lo[i] = (__bf16)(x - (float)h);
-}
 // Fragment order of a per-chunk split panel of R rows x C columns (C = 64 or
 // 128): each 16-row x 32-column MFMA operand block is 512 consecutive
 // elements, lane-major (lane = 16 * ((col % 32) / 8) + row % 16, 8 elements

@@ -38,7 +38,6 @@ constexpr int WBT = 32;    // chunk length
 constexpr int WMAX = 256;  // widest padded width
 constexpr int WT = 256;    // threads per workgroup
 constexpr int MS = WBT + 1;  // row stride of 32 x 32 LDS matrices
-constexpr int TILE = 16;   // state-pass column tile
 
 // Chunk-boundary state slots in a 2-byte type, as in the main kernels: the
 // forward states X (C^T and S) in fp16, the reverse passes' cotangent states
@@ -166,13 +165,6 @@ struct OpParams {
 __device__ __forceinline__ float gx_at(const float* Gs, int ld, int i, int c, int excl) {
   if (!excl) return Gs[i * ld + c];
   return i > 0 ? Gs[(i - 1) * ld + c] : 0.f;
-}
-
-// Entry e = threadIdx.x + 256 m of a 32 x 32 matrix: (i, j) = (e / 32, e % 32).
-__device__ __forceinline__ void entry(int m, int& i, int& j) {
-  const int e = threadIdx.x + WT * m;
-  i = e >> 5;
-  j = e & 31;
 }
 
 // Decay factors of the matrix-core Grams and applies are factored per
