@@ -163,8 +163,10 @@ struct OpParams {
 // G of the erase read for token i at coordinate c: the prefix before token i
 // (predictor) or through it (memory).
 __device__ __forceinline__ float gx_at(const float* Gs, int ld, int i, int c, int excl) {
-  if (!excl) return Gs[i * ld + c];
-  return i > 0 ? Gs[(i - 1) * ld + c] : 0.f;
+  // branch-free: the read is unconditional (a branch around it would serialise
+  // every operand behind its own LDS wait), the first token's value selected away
+  const float v = Gs[(excl && i > 0 ? i - 1 : i) * ld + c];
+  return excl && i == 0 ? 0.f : v;
 }
 
 // Decay factors of the matrix-core Grams and applies are factored per
@@ -174,6 +176,16 @@ __device__ __forceinline__ float gx_at(const float* Gs, int ld, int i, int c, in
 // coordinates beyond it are left out of the factored product and their terms
 // added exactly.
 constexpr float WILD = 60.f;
+
+// x * e^{g} for a factored decay operand, zero on a wild coordinate.  Both
+// sides are evaluated (the operands are loaded unconditionally by the caller;
+// a branch around them would serialise every operand behind its own memory
+// wait), the exponent clamped so a wild coordinate's factor stays finite
+// before the select drops it.
+__device__ __forceinline__ float keep_exp(bool keep, float x, float g) {
+  const float v = x * __expf(fminf(g, 80.f));
+  return keep ? v : 0.f;
+}
 
 // v_mfma_f32_16x16x4f32: used with the sum index k = 4 g + e carried by MFMA e
 // (e = 0..3) and lane group g = lane / 16, so an accumulator (lane (g, n)
@@ -211,6 +223,7 @@ __device__ __forceinline__ void gram_mfma(int kw, const int* wl, int nw, FA fa, 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4, m = l & 15;
   const int bi = w >> 1, bj = w & 1;
   f4 acc = zero4();
+#pragma unroll 4
   for (int kb = 0; kb < kw; kb += 16) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -298,7 +311,7 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
   int* wl = reinterpret_cast<int*>(Ps + WBT * MS);
   const int nw = wild_list(Gs, ld, kw, wl, wl + WMAX);
   auto wild = [&](int c) { return -Gs[(WBT - 1) * ld + c] > WILD; };
-  auto kb = [&](int j, int c) { return wild(c) ? 0.f : ks[j * ld + c] * __expf(-Gs[j * ld + c]); };
+  auto kb = [&](int j, int c) { return keep_exp(!wild(c), ks[j * ld + c], -Gs[j * ld + c]); };
   gram_mfma(
       kw, wl, nw,
       [&](int i, int c) { return xs[i * ld + c] * __expf(gx_at(Gs, ld, i, c, p.excl)); }, kb,
@@ -910,7 +923,7 @@ __global__ __launch_bounds__(WT) void k_w_out(OutParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long o = (tb + jb * 16 + 4 * g + e) * kw + rr;
-        kt[jb][e] = wild ? 0.f : p.k[o] * __expf(-p.G[o]);
+        kt[jb][e] = keep_exp(!wild, p.k[o], -p.G[o]);
       }
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
@@ -1063,7 +1076,7 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
     gram_mfma(
         kw, wl, nw, [&](int i, int c) { return dOl[i * ld + c] * __expf(Gl[i * ld + c]); },
         [&](int j, int c) {
-          return -Gl[(WBT - 1) * ld + c] > WILD ? 0.f : kl[j * ld + c] * __expf(-Gl[j * ld + c]);
+          return keep_exp(-Gl[(WBT - 1) * ld + c] <= WILD, kl[j * ld + c], -Gl[j * ld + c]);
         },
         [&](int i, int j, int c) {
           return dOl[i * ld + c] * kl[j * ld + c] * __expf(Gl[i * ld + c] - Gl[j * ld + c]);
@@ -1409,8 +1422,9 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
   //   dk = e^{-G} (e^{G_C} wL + M2^T Y~ - M1^T x~),  Y~ = Yk e^{G}, x~ = x e^{Gx}
   //   dq = e^{G} (dOX + M2 k~)                   (column output)
   const float* Yk = p.colout ? p.q : p.dO;  // [Tp][kw]
-  auto gx_g = [&](int i, int rr) {
-    return p.excl ? (i > 0 ? p.G[(tb + i - 1) * kw + rr] : 0.f) : p.G[(tb + i) * kw + rr];
+  auto gx_g = [&](int i, int rr) {  // branch-free, as gx_at
+    const float v = p.G[(tb + (p.excl && i > 0 ? i - 1 : i)) * kw + rr];
+    return p.excl && i == 0 ? 0.f : v;
   };
   float rdx[GRB][2][4], rdk[GRB][2][4], rdq[GRB][2][4], rdg[GRB][2][4];
 #pragma unroll
@@ -1435,9 +1449,9 @@ __global__ __launch_bounds__(GT) void k_w_grad(GradParams p) {
         yr[jb][e] = Yk[o];
         xr[jb][e] = p.x[o];
         orw[jb][e] = p.colout ? 0.f : p.o[o];
-        kt[jb][e] = wild ? 0.f : kr[jb][e] * __expf(-gj);
-        yt[jb][e] = wild ? 0.f : yr[jb][e] * __expf(gj);
-        xt[jb][e] = wild ? 0.f : xr[jb][e] * __expf(gx_g(j, rr));
+        kt[jb][e] = keep_exp(!wild, kr[jb][e], -gj);
+        yt[jb][e] = keep_exp(!wild, yr[jb][e], gj);
+        xt[jb][e] = keep_exp(!wild, xr[jb][e], gx_g(j, rr));
       }
     const float egl = __expf(gl);
 #pragma unroll
