@@ -6,11 +6,15 @@ reset-free segments, which needs the segment lengths on the host
 ops/operator.py:96-193).  Here the dense [B,T] batch runs through the same
 kernels unchanged in shape:
 
-* an invalid token becomes neutral: u, h, q, keys, values = 0 and log-decay 0.
-  Its erase read, write and readout vanish exactly (normalising a zero vector
-  gives zero, so the predictor's write, the dual sources and the primal address
-  are zero), so it emits 0 and keeps both states -- the reference's semantics
-  (reference.py:156-227);
+* an invalid token becomes neutral: its gamma, q, keys and log-decay are zeroed.
+  gamma = 0 makes the predictor's write delta = gamma (h - C u) and its erase
+  read x = gamma u^ vanish (so the dual sources' phi, and with keys = 0 the
+  primal address d = k + C^T k and the erase source e, are zero: no memory
+  write), q = 0 makes the readout vanish, and log-decay 0 keeps both states: the
+  token emits 0 and leaves both states as they were -- the reference's
+  semantics (reference.py:156-227).  u, h and the values need no masking: each
+  of their effects passes through delta, x, d or the token's write, all zero,
+  so their gradients on the token are exactly zero as well;
 * a reset on a valid token clears both states before that token: its
   log-decay is replaced by RESET_LOG_DECAY, so D C and D S keep exp(-20) ~
   2e-9 of the old states -- below FP32 rounding (6e-8) of the terms that
@@ -23,15 +27,15 @@ kernels unchanged in shape:
   the predictor's residual is taken before forgetting (h - C_{t-1} u), so the
   decay alone would not reset it.
 
-The masking is one HIP launch each way (sd_mask_rows): the forward copies
-u, h, q, keys, values and the log-decay with invalid rows zeroed and reset rows'
-log-decay killed; the backward zeroes the same rows of their gradients (and the
-reset tokens' log-decay gradient), so invalid tokens' inputs and reset tokens'
-log-decay get zero gradient, as when the reference leaves them out of its
-segments.  erase_raw, write_raw and gamma need no masking: on an invalid token
-their only partners (the normalised key, the values, u and h) are zero, so
-their forward effect and gradients vanish by themselves.  Everything stays on
-the device and is capturable in a HIP graph.
+The masking is one HIP launch each way (sd_mask_rows): the forward copies q,
+keys, the log-decay and gamma (broadcast to [B,T,H]) with invalid rows zeroed
+and reset rows' log-decay killed; the backward zeroes the same rows of their
+gradients in place (and the reset tokens' log-decay gradient), so invalid
+tokens' inputs and reset tokens' log-decay get zero gradient, as when the
+reference leaves them out of its segments.  erase_raw and write_raw need no
+masking either: their partners on an invalid token (the key, and the write
+through d) are zero.  Everything stays on the device and is capturable in a
+HIP graph.
 """
 from __future__ import annotations
 
@@ -71,15 +75,16 @@ def _mask_tensor(src: torch.Tensor, dst: torch.Tensor, reset_fill: bool, reset_v
                              int(reset_fill), reset_value)
 
 
-def _mask_rows(flags, srcs, decay_last: bool, reset_value: float, inplace: bool = False):
+def _mask_rows(flags, srcs, decay_idx, reset_value: float, inplace: bool = False):
     """Masked contiguous copies of srcs ([B,T,H,...,w] views, unit inner stride),
     or, with inplace, srcs themselves masked in place (each must be contiguous);
-    the last one is the log-decay (or its gradient) when decay_last."""
+    srcs[decay_idx] (if not None) is the log-decay or its gradient, whose reset
+    rows take reset_value."""
     B, T, H = srcs[0].shape[:3]
     outs = list(srcs) if inplace else [torch.empty(x.shape, dtype=x.dtype, device=x.device)
                                        for x in srcs]
     arr = (_lib.SdMaskTensor * len(srcs))(*[
-        _mask_tensor(x, o, decay_last and i == len(srcs) - 1, reset_value)
+        _mask_tensor(x, o, i == decay_idx, reset_value)
         for i, (x, o) in enumerate(zip(srcs, outs))])
     rc = _lib.load().sd_mask_rows(B, T, H, flags.data_ptr(), flags.stride(0), flags.stride(1),
                                   arr, len(srcs), _stream(srcs[0].device))
@@ -87,16 +92,18 @@ def _mask_rows(flags, srcs, decay_last: bool, reset_value: float, inplace: bool 
     return outs
 
 
+_DECAY = 2  # position of the log-decay among the masked operands
+
+
 class _MaskOperands(torch.autograd.Function):
-    """u, h, q, keys, values, log-decay -> copies with invalid tokens zeroed and
-    reset tokens' log-decay set to RESET_LOG_DECAY; the backward masks the
+    """q, keys, log-decay, gamma ([B,T,H,1]) -> copies with invalid tokens zeroed
+    and reset tokens' log-decay set to RESET_LOG_DECAY; the backward masks the
     gradients the same way (zero log-decay gradient on reset tokens)."""
 
     @staticmethod
-    def forward(ctx, flags, u, h, q, keys, values, log_decay):
+    def forward(ctx, flags, q, keys, log_decay, gamma):
         ctx.save_for_backward(flags)
-        return tuple(_mask_rows(flags, [u, h, q, keys, values, log_decay], True,
-                                RESET_LOG_DECAY))
+        return tuple(_mask_rows(flags, [q, keys, log_decay, gamma], _DECAY, RESET_LOG_DECAY))
 
     @staticmethod
     def backward(ctx, *grads):
@@ -108,7 +115,8 @@ class _MaskOperands(torch.autograd.Function):
             # operands feed only the operator), so they are masked in place:
             # only invalid rows (and reset tokens' log-decay rows) are written.
             srcs = [grads[i].contiguous() for i in live]
-            masked = _mask_rows(flags, srcs, live[-1] == len(grads) - 1, 0.0, inplace=True)
+            decay = live.index(_DECAY) if _DECAY in live else None
+            masked = _mask_rows(flags, srcs, decay, 0.0, inplace=True)
             for i, m in zip(live, masked):
                 out[i] = m
         return (None, *out)
@@ -127,10 +135,12 @@ def solvedelta_masked_native(u, h, q, keys, values, associative_log_decay, erase
     valid_mask, reset_mask = _check_masks(valid_mask, reset_mask, B, T, u.device)
     reset = reset_mask & valid_mask
     flags = (valid_mask.to(torch.uint8) | (reset.to(torch.uint8) << 1)).contiguous()
-    u, h, q, keys, values, g = _MaskOperands.apply(flags, u, h, q, keys, values,
-                                                   associative_log_decay)
+    H = u.shape[2]
+    gamma = geometry_write if geometry_write.dim() == 3 else geometry_write.reshape(1, 1, H)
+    gamma = gamma.expand(B, T, H).unsqueeze(-1)
+    q, keys, g, gamma = _MaskOperands.apply(flags, q, keys, associative_log_decay, gamma)
     fresh = reset.to(torch.uint8)
-    return _dispatch(u, h, q, keys, values, g, erase_raw, write_raw, geometry_write,
+    return _dispatch(u, h, q, keys, values, g, erase_raw, write_raw, gamma.squeeze(-1),
                      initial_state, return_final_state, fresh)
 
 

@@ -47,6 +47,13 @@ def _run(B, T, H, r, V, valid, reset, seed, gamma_shape="BTH", with_state=True, 
         for i, (a, b) in enumerate(zip(grads, rg)):
             assert torch.isfinite(a).all(), i
             errs[f"g{i}"] = rel(a.float(), b)
+        # invalid tokens' per-token inputs get exactly zero gradient, as when the
+        # reference leaves them out (u, h and the values included: they are not
+        # masked, every path from them through the token carries a zero factor)
+        inv = (~valid).cuda()
+        for i in range(9):
+            if grads[i].dim() >= 3 and grads[i].shape[:2] == (B, T):
+                assert grads[i][inv].abs().max().item() == 0.0 if inv.any() else True, i
     print("  " + " ".join(f"{k}={v:.1e}" for k, v in errs.items()), flush=True)
     for k, v in errs.items():
         assert v < 3e-2, (k, v)
