@@ -14,7 +14,8 @@ kernels unchanged in shape:
   token emits 0 and leaves both states as they were -- the reference's
   semantics (reference.py:156-227).  u, h and the values need no masking: each
   of their effects passes through delta, x, d or the token's write, all zero,
-  so their gradients on the token are exactly zero as well;
+  so their gradients on the token are exactly zero as well (they, like the
+  gate logits, must be finite there: zero times a NaN is not zero);
 * a reset on a valid token clears both states before that token: its
   log-decay is replaced by RESET_LOG_DECAY, so D C and D S keep exp(-20) ~
   2e-9 of the old states -- below FP32 rounding (6e-8) of the terms that
