@@ -156,8 +156,8 @@ struct OpParams {
   int NT, Tp, kw, vw, excl, colout;
   const float *k, *x, *v, *q, *G;  // k, x, G [Tp][kw]; v [Tp][vw]; q [Tp][kw] (col) / [Tp][vw] (row)
   float *A, *P;                    // [NT][32][32]
-  _Float16 *Wneg, *Kt;             // state-pass panels: -W [Tp][kw], K^ transposed per chunk [NT][kw][32]
-  float *U, *Qt, *Gam;             // Qt [Tp][kw]; U [Tp][vw]; Gam [NT][kw]
+  _Float16 *Wneg, *Kt;             // state-pass panels: -W [Tp][kw] (fragment order), K^ transposed per chunk [NT][kw][32]
+  float *U, *Qt, *Gam;             // Qt [Tp][kw]; U [Tp][vw] (accumulator order); Gam [NT][kw]
 };
 
 // G of the erase read for token i at coordinate c: the prefix before token i
@@ -175,6 +175,13 @@ __device__ __forceinline__ float gx_at(const float* Gs, int ld, int i, int c, in
 // -G_{31,c}, stays at most WILD (exp(WILD) is far inside FP32); "wild"
 // coordinates beyond it are left out of the factored product and their terms
 // added exactly.
+// Accumulator order of a chunk's [32 tokens][C] FP32 panel (U, dU): the 16 x 16
+// tile (token block tb, column block cb) is 64 lanes x 4 elements, lane (g, m)
+// holding tokens 16 tb + 4 g .. + 3 of column 16 cb + m, as an MFMA writes it.
+__device__ __forceinline__ unsigned acc_off(int tb, int cb, int lane, int C) {
+  return (unsigned)(((tb * (C >> 4) + cb) * 64 + lane) * 4);
+}
+
 constexpr float WILD = 60.f;
 
 // x * e^{g} for a factored decay operand, zero on a wild coordinate.  Both
@@ -367,7 +374,7 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
             a = mfma4(Ls[(t2 * 16 + m) * MS + k], xs[k * ld + cc] * __expf(gx_at(Gs, ld, k, cc, p.excl)), a);
           }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) p.Wneg[(tb + t2 * 16 + 4 * g + e) * kw + nb * 16 + m] = (_Float16)(-a[e]);
+        for (int e = 0; e < 4; ++e) p.Wneg[tb * kw + frag_off(t2 * 16 + 4 * g + e, nb * 16 + m, kw)] = (_Float16)(-a[e]);
       }
       if (nb * 16 < vw) {
         f4 a = zero4();
@@ -375,8 +382,7 @@ __global__ __launch_bounds__(WT) void k_w_prep(OpParams p) {
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) a = mfma4(Ls[(t2 * 16 + m) * MS + kb * 16 + 4 * g + e], vb[j][kb][e], a);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) p.U[(tb + t2 * 16 + 4 * g + e) * vw + nb * 16 + m] = a[e];
+        *reinterpret_cast<f4*>(p.U + tb * vw + acc_off(t2, nb, l, vw)) = a;
       }
     }
   }
@@ -408,10 +414,10 @@ constexpr size_t prep_smem(int kw) {
 // ---------------------------------------------------------------------------
 struct WStateParams {
   int NT, Tp, kw, vw, rows, cols, rev;
-  const void* Wneg;  // -W, token-major [Tp][kw] (fp16 forward, bf16 reverse)
+  const void* Wneg;  // -W [Tp][kw] in fragment order (frag_off; fp16 forward, bf16 reverse)
   const void* Kt;    // K^T per chunk [NT][kw][32] (fp16 forward, bf16 reverse)
   const __bf16* At;  // injection A^T per chunk [NT][kw][32] (reverse only; nullable)
-  const float *U, *Gam, *Ib;  // U, Ib [Tp][vw]; Gam [NT][kw]
+  const float *U, *Gam, *Ib;  // U [Tp][vw] (accumulator order), Ib [Tp][vw]; Gam [NT][kw]
   void* slots;  // xs_t (forward) or ls_t (reverse)
   float* wout;
   const float* init; int init_t;
@@ -448,7 +454,11 @@ constexpr int WKS = WMAX / 32;       // K = 32 steps of the w product
 constexpr int SPF = 2;               // prefetch ring depth (chunks)
 constexpr int XLD = WMAX + 8;        // row stride (16-bit) of the staged X0
 constexpr int WLD = WBT + 8;         // row stride (16-bit) of the staged w
-constexpr size_t state_smem() { return (size_t)(2 * STILE * XLD + 4 * STILE * WLD) * 2; }
+constexpr int XRS = STILE + 8;       // row stride (16-bit) of the row-major slot copy
+constexpr int WFS = WBT + 4;         // row stride (FP32) of the w tile
+constexpr size_t state_smem() {
+  return (size_t)(2 * STILE * XLD + 4 * STILE * WLD + WMAX * XRS) * 2 + (size_t)STILE * WFS * 4;
+}
 
 template <bool REV> struct WStateT;
 template <> struct WStateT<false> {
@@ -471,17 +481,22 @@ template <> struct WStateT<true> {
 template <bool REV>
 struct WFrags {
   using V8 = typename WStateT<REV>::V8;
-  V8 W[WKS];                      // waves 0-3: Wneg rows of token block w & 1
+  V8 W[WKS];                      // Wneg rows of token block w & 1
   V8 K[SRB];                      // K^T rows of this wave's row blocks, the chunk's 32 tokens
   bf16x8 A[REV ? SRB : 1];        // At rows (reverse)
   float2 ib;                      // reverse: this thread's two elements of the Ib tile
-  f4 U;                           // waves 0-3: U tile (C-operand layout)
+  f4 U;                           // U tile (C-operand layout)
   float4 G[SRB];                  // Gamma of this wave's rows 16 rb + 4 g .. + 3
 };
 
 // Chunk-uniform bases with 32-bit lane offsets throughout: 64-bit per-lane
 // addresses for the ~20 fragment loads of a chunk would not fit in registers
-// beside the prefetch ring.
+// beside the prefetch ring.  Every load is unconditional (indices clamped into
+// the panel; a null At replaced by a panel of the same shape): a memory
+// operation under a branch gives the two paths different counts of
+// operations in flight, and the compiler then waits for all of them (the
+// ring's prefetches included) wherever the paths meet.  Waves 4-7 fetch the
+// W and U fragments waves 0-3 use, for the same reason.
 template <bool REV>
 __device__ __forceinline__ void wstate_load(const WStateParams& p, int s, int ch, int c0,
                                             WFrags<REV>& f) {
@@ -491,36 +506,34 @@ __device__ __forceinline__ void wstate_load(const WStateParams& p, int s, int ch
   const int kw = p.kw, vw = p.vw, nrb = kw / 16;
   const long long tb = (long long)s * p.Tp + (long long)ch * WBT;
   const long long cb = ((long long)s * p.NT + ch) * kw;  // chunk base of [kw][32] and [kw] panels
-  if (w < 4) {
-    const int tbk = w & 1, hh = w >> 1;
+  {
+    const int tbk = w & 1, hh = (w >> 1) & 1, nks = kw >> 5;
     const E* Wc = static_cast<const E*>(p.Wneg) + tb * kw;
-    const unsigned wo = (unsigned)((tbk * 16 + m) * kw + kq);
+    // fragment order: a K = 32 step of a 16-token block is 1 KiB, lane-contiguous
+    const unsigned wo = (unsigned)(tbk * nks * 512 + l * 8);
 #pragma unroll
     for (int ks = 0; ks < WKS; ++ks)
-      if (ks * 32 < kw) f.W[ks] = *reinterpret_cast<const V8*>(Wc + wo + ks * 32);
-    const float* Uc = p.U + tb * vw + c0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) f.U[e] = Uc[(unsigned)((tbk * 16 + 4 * g + e) * vw + hh * 16 + m)];
+      f.W[ks] = *reinterpret_cast<const V8*>(Wc + wo + min(ks, nks - 1) * 512);
+    f.U = *reinterpret_cast<const f4*>(p.U + tb * vw + acc_off(tbk, (c0 >> 4) + hh, l, vw));
   }
   const E* Kc = static_cast<const E*>(p.Kt) + cb * WBT;
   const float* Gc = p.Gam + cb;
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
-    const int rb = w + SW * q;
-    if (rb < nrb) {
-      const unsigned ko = (unsigned)((rb * 16 + m) * WBT + kq);
-      f.K[q] = *reinterpret_cast<const V8*>(Kc + ko);
-      f.G[q] = *reinterpret_cast<const float4*>(Gc + (unsigned)(rb * 16 + 4 * g));
-      if constexpr (REV)
-        if (p.At) f.A[q] = *reinterpret_cast<const bf16x8*>(p.At + cb * WBT + ko);
+    const int rb = min(w + SW * q, nrb - 1);
+    const unsigned ko = (unsigned)((rb * 16 + m) * WBT + kq);
+    f.K[q] = *reinterpret_cast<const V8*>(Kc + ko);
+    f.G[q] = *reinterpret_cast<const float4*>(Gc + (unsigned)(rb * 16 + 4 * g));
+    if constexpr (REV) {
+      const __bf16* Ap = p.At ? p.At : static_cast<const __bf16*>(p.Kt);
+      f.A[q] = *reinterpret_cast<const bf16x8*>(Ap + cb * WBT + ko);
     }
   }
   if constexpr (REV) {
     static_assert(WBT * STILE == 2 * ST, "two Ib elements per thread");
-    if (p.At) {
-      const int tok = threadIdx.x / (STILE / 2), col = (threadIdx.x % (STILE / 2)) * 2;
-      f.ib = *reinterpret_cast<const float2*>(p.Ib + tb * vw + c0 + (unsigned)(tok * vw + col));
-    }
+    const float* Ip = p.At ? p.Ib : p.U;  // both [Tp][vw]
+    const int tok = threadIdx.x / (STILE / 2), col = (threadIdx.x % (STILE / 2)) * 2;
+    f.ib = *reinterpret_cast<const float2*>(Ip + tb * vw + c0 + (unsigned)(tok * vw + col));
   }
 }
 
@@ -556,8 +569,10 @@ __device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch
   E* wl = wh + STILE * WLD;
   E* ih = wl + STILE * WLD;          // reverse: the injection's Ib tile [32 columns][WLD]
   E* il = ih + STILE * WLD;
-  S* slot = static_cast<S*>(p.slots) + ((long long)s * (p.NT + 1) + ch) * kw * vw;
-  // slot[ch] = X0; X0 staged split and transposed for the w product
+  E* Xr = il + STILE * WLD;          // X0 row-major [rows][XRS]: the slot, written back below
+  float* wf = reinterpret_cast<float*>(Xr + WMAX * XRS);  // w FP32 [32 columns][WFS]
+  static_assert(std::is_same<S, E>::value, "the slot holds the staged high half");
+  // X0 staged split and transposed for the w product, and row-major for the slot
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
     const int rb = w + SW * q;
@@ -567,7 +582,7 @@ __device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch
       const int col = h * 16 + m, row = rb * 16 + 4 * g;
       wsplit4<E, V4>(Xh + col * XLD + row, Xl + col * XLD + row, X[q][h]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) slot[(unsigned)((row + e) * vw + c0 + col)] = (S)X[q][h][e];
+      for (int e = 0; e < 4; ++e) Xr[(row + e) * XRS + col] = (E)X[q][h][e];
     }
   }
   if constexpr (REV) {
@@ -583,6 +598,18 @@ __device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch
     }
   }
   __syncthreads();
+  {  // slot[ch] = X0: 16 columns of one row per thread, two 16-byte pieces
+    static_assert(WMAX * 2 == ST && STILE == 32, "one half row of the slot tile per thread");
+    // (rows past kw repeat row kw - 1: same values, and no store under a branch)
+    const int row = min(threadIdx.x >> 1, kw - 1), c = (threadIdx.x & 1) * 16;
+    typedef E E8 __attribute__((ext_vector_type(8)));
+    const E8 v0 = *reinterpret_cast<const E8*>(Xr + row * XRS + c);
+    const E8 v1 = *reinterpret_cast<const E8*>(Xr + row * XRS + c + 8);
+    S* dst = static_cast<S*>(p.slots) + ((long long)s * (p.NT + 1) + ch) * kw * vw + c0 +
+             (unsigned)(row * vw + c);
+    *reinterpret_cast<E8*>(dst) = v0;
+    *reinterpret_cast<E8*>(dst + 8) = v1;
+  }
   // w = U + Wneg X0 (waves 0-3, one 16 x 16 tile each; high and low halves of
   // X0 in two accumulators so the two dependent chains interleave)
   if (w < 4) {
@@ -601,9 +628,7 @@ __device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch
     for (int e = 0; e < 4; ++e) wv[e] = a0[e] + a1[e];
     const int col = hh * 16 + m, tok = tbk * 16 + 4 * g;
     wsplit4<E, V4>(wh + col * WLD + tok, wl + col * WLD + tok, wv);
-    float* const wo = p.wout + tb * vw + c0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) wo[(unsigned)((tok + e) * vw + col)] = wv[e];
+    *reinterpret_cast<f4*>(wf + col * WFS + tok) = wv;
   }
   // X = Gamma X (+ At^T Ib): independent of w, so it overlaps the w tiles
 #pragma unroll
@@ -626,6 +651,12 @@ __device__ __forceinline__ void wstate_step(const WStateParams& p, int s, int ch
     }
   }
   __syncthreads();
+  {  // w to global memory, two elements per thread
+    static_assert(WBT * STILE == 2 * ST, "two w elements per thread");
+    const int tok = threadIdx.x / (STILE / 2), col = (threadIdx.x % (STILE / 2)) * 2;
+    const float2 v = make_float2(wf[col * WFS + tok], wf[(col + 1) * WFS + tok]);
+    *reinterpret_cast<float2*>(p.wout + tb * vw + c0 + (unsigned)(tok * vw + col)) = v;
+  }
   // X += K^T w
 #pragma unroll
   for (int h = 0; h < NSUB; ++h) {
@@ -1042,8 +1073,8 @@ __global__ __launch_bounds__(WT) void k_w_sources(SrcParams p) {
 struct BprepParams {
   int NT, Tp, kw, vw, excl, colout;
   const float *k, *x, *q, *G, *A, *P, *dO, *dW;
-  float *dU, *Pp;
-  __bf16 *Wneg, *Kt, *At;  // reverse-pass panels: -Wn [Tp][kw]; Kn, Ia transposed per chunk [NT][kw][32]
+  float *dU, *Pp;  // dU [Tp][vw] in accumulator order (acc_off)
+  __bf16 *Wneg, *Kt, *At;  // reverse-pass panels: -Wn [Tp][kw] (fragment order); Kn, Ia transposed per chunk [NT][kw][32]
 };
 
 __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
@@ -1140,8 +1171,7 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           du = mfma4(Al[(kb * 16 + 4 * g + e) * MS + t2 * 16 + m], rhs[kb][j][e], du);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) p.dU[(tb + t2 * 16 + 4 * g + e) * vw + nb * 16 + m] = du[e];
+      *reinterpret_cast<f4*>(p.dU + tb * vw + acc_off(t2, nb, l, vw)) = du;
     }
   }
   __syncthreads();  // cv is reused for the decayed keys
@@ -1179,7 +1209,7 @@ __global__ __launch_bounds__(WT) void k_w_bprep(BprepParams p) {
           a = mfma4(Al[(kb * 16 + 4 * g + e) * MS + t2 * 16 + m],
                     cv[(kb * 16 + 4 * g + e) * WT + nb * 16 + m], a);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) p.Wneg[(tb + t2 * 16 + 4 * g + e) * kw + nb * 16 + m] = (__bf16)a[e];
+      for (int e = 0; e < 4; ++e) p.Wneg[tb * kw + frag_off(t2 * 16 + 4 * g + e, nb * 16 + m, kw)] = (__bf16)a[e];
     }
   }
 }
