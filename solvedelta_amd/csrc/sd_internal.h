@@ -37,10 +37,14 @@ __device__ __forceinline__ float sp_val(SPRaw r) { return (float)r.h + (float)r.
 // 0 on a token flagged fresh (its predictor residual reads a zero state: the
 // erase read x = gamma u^ of the C op is dropped), 1 otherwise.  t must be a
 // valid token index.
+// The flag's address is selected, not branched on: a load under a branch would
+// wait for every load issued before it.
+static __device__ const uint8_t sd_no_fresh = 0;  // the flag read when no flags are given
 __device__ __forceinline__ float erase_keep(const sd_inputs& in, int b, int t) {
-  if (!in.fresh.data) return 1.f;
-  const uint8_t f = ((const uint8_t*)in.fresh.data)[(long long)b * in.fresh.sb + (long long)t * in.fresh.st];
-  return f ? 0.f : 1.f;
+  const uint8_t* fl = in.fresh.data
+                          ? (const uint8_t*)in.fresh.data + (long long)b * in.fresh.sb + (long long)t * in.fresh.st
+                          : &sd_no_fresh;
+  return *fl ? 0.f : 1.f;
 }
 #endif
 

@@ -88,63 +88,94 @@ struct TokParams {
   float *G, *uh, *kh, *qh, *xC, *vC, *gam, *rs;
 };
 
+// Loads here are unconditional (indices clamped into the row, invalid values
+// masked afterwards by a select): a load under a branch waits for every load
+// issued before it, so guarded loads would run one round trip at a time.
 __global__ __launch_bounds__(WT) void k_w_tokens(TokParams p) {
   const int ch = blockIdx.x, s = blockIdx.y;
   const int H = p.in.H, T = p.in.T, r = p.in.r, KP = p.KP;
   const int b = s / H, h = s % H, t0 = ch * WBT;
   const long long pb = (long long)s * p.Tp;
-  // in-chunk inclusive log-decay prefix, one coordinate per thread
+  // in-chunk inclusive log-decay prefix, one coordinate per thread: the chunk's
+  // 32 values are loaded first, then summed
   const int c = threadIdx.x;
   if (c < KP) {
     const float* g = (const float*)p.in.log_decay.data + (long long)b * p.in.log_decay.sb +
-                     (long long)h * p.in.log_decay.sh + c;
+                     (long long)h * p.in.log_decay.sh + min(c, r - 1);
+    float gv[WBT];
+#pragma unroll
+    for (int i = 0; i < WBT; ++i) gv[i] = g[(long long)min(t0 + i, T - 1) * p.in.log_decay.st];
     float acc = 0.f;
+#pragma unroll
     for (int i = 0; i < WBT; ++i) {
-      const int t = t0 + i;
-      if (t < T && c < r) acc += g[(long long)t * p.in.log_decay.st];
+      acc += (t0 + i < T && c < r) ? gv[i] : 0.f;
       p.G[(pb + t0 + i) * KP + c] = acc;
     }
   }
+  // per token: norms and the gamma-scaled predictor operands, two tokens per
+  // wave at a time with all their loads in flight together
+  constexpr int NW = WT / 64, TU = 2;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  for (int i = w; i < WBT; i += WT / 64) {
-    const int t = t0 + i;
-    const bool tv = t < T;
-    const float gm = tv ? wgamma(p.in.gamma, b, t, h) : 0.f;
-    const float gx = tv ? gm * erase_keep(p.in, b, t) : 0.f;  // erase side: 0 on fresh tokens
-    float uu[4], kk[4], qq[4], hv[4];
-    float su = 0.f, sk = 0.f, sq = 0.f;
+  static_assert(WBT % (NW * TU) == 0, "tokens per wave");
+  for (int i0 = w; i0 < WBT; i0 += NW * TU) {
+    float uu[TU][4], kk[TU][4], qq[TU][4], hv[TU][4], gm[TU], ek[TU];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int cc = l + 64 * j;
-      const bool ok = tv && cc < r;
-      uu[j] = ok ? bf2f(wrow(p.in.u, b, t, h)[cc]) : 0.f;
-      kk[j] = ok ? bf2f(wrow(p.in.k, b, t, h)[cc]) : 0.f;
-      qq[j] = ok ? bf2f(wrow(p.in.q, b, t, h)[cc]) : 0.f;
-      hv[j] = ok ? bf2f(wrow(p.in.h, b, t, h)[cc]) : 0.f;
-      su += uu[j] * uu[j];
-      sk += kk[j] * kk[j];
-      sq += qq[j] * qq[j];
-    }
-    const float ru = rsqrtf(wave_sum(su) + 1e-24f);
-    const float rk = rsqrtf(wave_sum(sk) + 1e-24f);
-    const float rq = rsqrtf(wave_sum(sq) + 1e-24f);
-    const long long row = (pb + t) * KP;
+    for (int u = 0; u < TU; ++u) {
+      const int tc = min(t0 + i0 + u * NW, T - 1);
+      gm[u] = wgamma(p.in.gamma, b, tc, h);
+      ek[u] = erase_keep(p.in, b, tc);
+      const __bf16* ur = wrow(p.in.u, b, tc, h);
+      const __bf16* kr = wrow(p.in.k, b, tc, h);
+      const __bf16* qr = wrow(p.in.q, b, tc, h);
+      const __bf16* hr = wrow(p.in.h, b, tc, h);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int cc = l + 64 * j;
-      if (cc < KP) {
-        p.uh[row + cc] = uu[j] * ru;
-        p.kh[row + cc] = kk[j] * rk;
-        p.qh[row + cc] = qq[j] * rq;
-        p.xC[row + cc] = gx * uu[j] * ru;
-        p.vC[row + cc] = gm * hv[j];
+      for (int j = 0; j < 4; ++j) {
+        const int cc = min(l + 64 * j, r - 1);
+        uu[u][j] = bf2f(ur[cc]);
+        kk[u][j] = bf2f(kr[cc]);
+        qq[u][j] = bf2f(qr[cc]);
+        hv[u][j] = bf2f(hr[cc]);
       }
     }
-    if (l == 0) {
-      p.gam[pb + t] = gm;
-      p.rs[(pb + t) * 3 + 0] = ru;
-      p.rs[(pb + t) * 3 + 1] = rk;
-      p.rs[(pb + t) * 3 + 2] = rq;
+#pragma unroll
+    for (int u = 0; u < TU; ++u) {
+      const int t = t0 + i0 + u * NW;
+      const bool tv = t < T;
+      const float g1 = tv ? gm[u] : 0.f;
+      const float gx = tv ? g1 * ek[u] : 0.f;  // erase side: 0 on fresh tokens
+      float su = 0.f, sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = tv && l + 64 * j < r;
+        uu[u][j] = ok ? uu[u][j] : 0.f;
+        kk[u][j] = ok ? kk[u][j] : 0.f;
+        qq[u][j] = ok ? qq[u][j] : 0.f;
+        hv[u][j] = ok ? hv[u][j] : 0.f;
+        su += uu[u][j] * uu[u][j];
+        sk += kk[u][j] * kk[u][j];
+        sq += qq[u][j] * qq[u][j];
+      }
+      const float ru = rsqrtf(wave_sum(su) + 1e-24f);
+      const float rk = rsqrtf(wave_sum(sk) + 1e-24f);
+      const float rq = rsqrtf(wave_sum(sq) + 1e-24f);
+      const long long row = (pb + t) * KP;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cc = l + 64 * j;
+        if (cc < KP) {
+          p.uh[row + cc] = uu[u][j] * ru;
+          p.kh[row + cc] = kk[u][j] * rk;
+          p.qh[row + cc] = qq[u][j] * rq;
+          p.xC[row + cc] = gx * uu[u][j] * ru;
+          p.vC[row + cc] = g1 * hv[u][j];
+        }
+      }
+      if (l == 0) {
+        p.gam[pb + t] = g1;
+        p.rs[(pb + t) * 3 + 0] = ru;
+        p.rs[(pb + t) * 3 + 1] = rk;
+        p.rs[(pb + t) * 3 + 2] = rq;
+      }
     }
   }
 }
@@ -1017,17 +1048,32 @@ __global__ __launch_bounds__(WT) void k_w_sources(SrcParams p) {
   if (t >= p.Tp) return;
   const bool tv = t < T;
   const long long row = ((long long)s * p.Tp + t) * p.KP, vrow_ = ((long long)s * p.Tp + t) * p.VP;
-  float u[4], dl[4], k[4], q[4], er[4];
+  // every load first, at clamped indices (masked below): no load under a branch
+  const int tc = min(t, T - 1);
+  const __bf16 *err = wrow(p.in.erase_raw, b, tc, h), *vr = wrow(p.in.v, b, tc, h),
+               *wrr = wrow(p.in.write_raw, b, tc, h);
+  float u[4], dl[4], k[4], q[4], er[4], vv[4], wr[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j, ck = min(c, p.KP - 1);
+    u[j] = p.uh[row + ck];
+    dl[j] = p.delta[row + ck];
+    k[j] = p.kh[row + ck];
+    q[j] = p.qh[row + ck];
+    er[j] = bf2f(err[min(c, r - 1)]);
+    vv[j] = bf2f(vr[min(c, V - 1)]);
+    wr[j] = bf2f(wrr[min(c, V - 1)]);
+  }
   float usq = 0.f, dsq = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = l + 64 * j;
     const bool in = c < p.KP;
-    u[j] = in ? p.uh[row + c] : 0.f;
-    dl[j] = in ? p.delta[row + c] : 0.f;
-    k[j] = in ? p.kh[row + c] : 0.f;
-    q[j] = in ? p.qh[row + c] : 0.f;
-    er[j] = (tv && c < r) ? bf2f(wrow(p.in.erase_raw, b, t, h)[c]) : 0.f;
+    u[j] = in ? u[j] : 0.f;
+    dl[j] = in ? dl[j] : 0.f;
+    k[j] = in ? k[j] : 0.f;
+    q[j] = in ? q[j] : 0.f;
+    er[j] = (tv && c < r) ? er[j] : 0.f;
     usq += u[j] * u[j];
     dsq += dl[j] * dl[j];
   }
@@ -1055,9 +1101,7 @@ __global__ __launch_bounds__(WT) void k_w_sources(SrcParams p) {
     }
     if (c < p.VP) {
       const bool ok = tv && c < V;
-      const float vv = ok ? bf2f(wrow(p.in.v, b, t, h)[c]) : 0.f;
-      const float wr = ok ? bf2f(wrow(p.in.write_raw, b, t, h)[c]) : 0.f;
-      p.z[vrow_ + c] = vv / (1.f + __expf(-wr));
+      p.z[vrow_ + c] = ok ? vv[j] / (1.f + __expf(-wr[j])) : 0.f;
     }
   }
 }
@@ -1619,19 +1663,37 @@ __global__ __launch_bounds__(WT) void k_w_src_bwd(SrcBwdParams p) {
   if (t >= p.Tp) return;
   const bool tv = t < T;
   const long long row = ((long long)s * p.Tp + t) * p.KP, vr = ((long long)s * p.Tp + t) * p.VP;
-  float u[4], dl[4], k[4], q[4], er[4], de[4], dc[4];
+  // every load first, at clamped indices (masked below): no load under a branch
+  const int tc = min(t, T - 1);
+  const __bf16 *err = wrow(p.in.erase_raw, b, tc, h), *vrow = wrow(p.in.v, b, tc, h),
+               *wrr = wrow(p.in.write_raw, b, tc, h);
+  float u[4], dl[4], k[4], q[4], er[4], de[4], dc[4], vv[4], wr[4], dzv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j, ck = min(c, p.KP - 1), cv = min(c, V - 1);
+    u[j] = p.uh[row + ck];
+    dl[j] = p.delta[row + ck];
+    k[j] = p.kh[row + ck];
+    q[j] = p.qh[row + ck];
+    de[j] = p.de[row + ck];
+    dc[j] = p.dchi[row + ck];
+    er[j] = bf2f(err[min(c, r - 1)]);
+    vv[j] = bf2f(vrow[cv]);
+    wr[j] = bf2f(wrr[cv]);
+    dzv[j] = p.dz[vr + cv];
+  }
   float usq = 0.f, dsq = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = l + 64 * j;
     const bool in = c < p.KP;
-    u[j] = in ? p.uh[row + c] : 0.f;
-    dl[j] = in ? p.delta[row + c] : 0.f;
-    k[j] = in ? p.kh[row + c] : 0.f;
-    q[j] = in ? p.qh[row + c] : 0.f;
-    de[j] = in ? p.de[row + c] : 0.f;
-    dc[j] = in ? p.dchi[row + c] : 0.f;
-    er[j] = (tv && c < r) ? bf2f(wrow(p.in.erase_raw, b, t, h)[c]) : 0.f;
+    u[j] = in ? u[j] : 0.f;
+    dl[j] = in ? dl[j] : 0.f;
+    k[j] = in ? k[j] : 0.f;
+    q[j] = in ? q[j] : 0.f;
+    de[j] = in ? de[j] : 0.f;
+    dc[j] = in ? dc[j] : 0.f;
+    er[j] = (tv && c < r) ? er[j] : 0.f;
     usq += u[j] * u[j];
     dsq += dl[j] * dl[j];
   }
@@ -1680,12 +1742,9 @@ __global__ __launch_bounds__(WT) void k_w_src_bwd(SrcBwdParams p) {
     const long long obase = ((long long)b * T + t) * H + h;
     if (tv && c < r) p.derase[obase * r + c] = f2bf(db[j] * k[j] * se[j] * (1.f - se[j]));
     if (tv && c < V) {
-      const float vv = bf2f(wrow(p.in.v, b, t, h)[c]);
-      const float wr = bf2f(wrow(p.in.write_raw, b, t, h)[c]);
-      const float sw = 1.f / (1.f + __expf(-wr));
-      const float dz = p.dz[vr + c];
-      p.dv[obase * V + c] = f2bf(sw * dz);
-      p.dwrite[obase * V + c] = f2bf(dz * vv * sw * (1.f - sw));
+      const float sw = 1.f / (1.f + __expf(-wr[j]));
+      p.dv[obase * V + c] = f2bf(sw * dzv[j]);
+      p.dwrite[obase * V + c] = f2bf(dzv[j] * vv[j] * sw * (1.f - sw));
     }
   }
 }
@@ -1711,36 +1770,57 @@ __global__ __launch_bounds__(WT) void k_w_final(FinalParams p) {
   const long long tok = (long long)s * p.Tp + t, row = tok * p.KP;
   const float gm = p.gam[tok];
   const float xk = erase_keep(p.in, b, t);  // fresh tokens: dx reaches neither u nor gamma
-  float u[4], k[4], q[4], gu[4], gk[4], gq[4];
+  // every load first, at clamped indices (masked below): no load under a branch,
+  // and none issued after a store
+  const __bf16* hr = wrow(p.in.h, b, t, h);
+  const float ru = p.rs[tok * 3], rk = p.rs[tok * 3 + 1], rq = p.rs[tok * 3 + 2];
+  float u[4], k[4], q[4], dxc[4], dvc[4], gu[4], gk[4], gq[4], hv[4], dgl[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j, ck = min(c, p.KP - 1);
+    u[j] = p.uh[row + ck];
+    k[j] = p.kh[row + ck];
+    q[j] = p.qh[row + ck];
+    dxc[j] = p.dxC[row + ck];
+    dvc[j] = p.dvC[row + ck];
+    gu[j] = p.duh[row + ck] + p.dkC[row + ck];
+    gk[j] = p.dkh[row + ck] + p.dd[row + ck] + p.dqC[row + ck];
+    gq[j] = p.dqh[row + ck];
+    hv[j] = bf2f(hr[min(c, r - 1)]);
+    dgl[j] = p.dgS[row + ck] + p.dgC[row + ck];
+  }
   float su = 0.f, sk = 0.f, sq = 0.f, sg = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = l + 64 * j;
     const bool in = c < p.KP;
-    u[j] = in ? p.uh[row + c] : 0.f;
-    k[j] = in ? p.kh[row + c] : 0.f;
-    q[j] = in ? p.qh[row + c] : 0.f;
-    const float dxc = in ? xk * p.dxC[row + c] : 0.f;
-    const float dvc = in ? p.dvC[row + c] : 0.f;
-    gu[j] = in ? p.duh[row + c] + p.dkC[row + c] + gm * dxc : 0.f;
-    gk[j] = in ? p.dkh[row + c] + p.dd[row + c] + p.dqC[row + c] : 0.f;
-    gq[j] = in ? p.dqh[row + c] : 0.f;
-    const float hv = c < r ? bf2f(wrow(p.in.h, b, t, h)[c]) : 0.f;
+    u[j] = in ? u[j] : 0.f;
+    k[j] = in ? k[j] : 0.f;
+    q[j] = in ? q[j] : 0.f;
+    dxc[j] = in ? xk * dxc[j] : 0.f;
+    dvc[j] = in ? dvc[j] : 0.f;
+    gu[j] = in ? gu[j] + gm * dxc[j] : 0.f;
+    gk[j] = in ? gk[j] : 0.f;
+    gq[j] = in ? gq[j] : 0.f;
+    hv[j] = c < r ? hv[j] : 0.f;
     su += gu[j] * u[j];
     sk += gk[j] * k[j];
     sq += gq[j] * q[j];
-    sg += u[j] * dxc + hv * dvc;
-    const long long o = (((long long)b * T + t) * H + h) * r + c;
+    sg += u[j] * dxc[j] + hv[j] * dvc[j];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = l + 64 * j;
     if (c < r) {
-      p.dh[o] = f2bf(gm * dvc);
-      p.dlog_decay[o] = p.dgS[row + c] + p.dgC[row + c];
+      const long long o = (((long long)b * T + t) * H + h) * r + c;
+      p.dh[o] = f2bf(gm * dvc[j]);
+      p.dlog_decay[o] = dgl[j];
     }
   }
   su = wave_sum(su);
   sk = wave_sum(sk);
   sq = wave_sum(sq);
   sg = wave_sum(sg);
-  const float ru = p.rs[tok * 3], rk = p.rs[tok * 3 + 1], rq = p.rs[tok * 3 + 2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = l + 64 * j;
