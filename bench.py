@@ -43,8 +43,7 @@ FLOPS_PER_CHUNK = {
     "k_prep_c": 3 * _T,                          # L, W, U
     "state_c_fwd": 2 * _G,                       # w = U - W X, X += K^T w
     "k_prep_s": 6 * _T + _G,                     # k.delta, apply, P, L, W, U; K X0^T
-    "state_s_fwd": 2 * _G,                       # w = U - W X, X += K^T w
-    "k_out_s": _G + _T,                          # o = Q X0 + P w
+    "state_s_fwd": 3 * _G + _T,                  # w = U - W X, X += K^T w; o = Q X0 + P w
     "k_bprep_s": 2 * 64 ** 3 // 2 + 2 * _T * 2 // 2 + _T,  # N = P A, dU, Wk
     "state_s_bwd": 3 * _G,                       # dw, injection, lambda update
     "k_grad_s": 3 * _G + 6 * _T,                 # dw X0, dO X0, w lam; M1, M2, 2 apply, 2 apply_t
@@ -64,11 +63,10 @@ _H, _P, _S, _A = 16384, 32768, 32768, 16384
 BYTES_PER_CHUNK = {
     "k_prep_c": (2 * _H + _P) + (_A + 2 * _H + _P),           # u,h,decay -> A,W,K (fp16),U
     "state_c_fwd": (2 * _H + _P) + (_S + _H),                # W,K,U -> slot, delta
-    "k_prep_s": (7 * _H + _P + _S) + (3 * _H + _H + _A + 2 * _H + _A + _P + _H),
-    # u,q,k,v,erase,write,delta,decay,C slot -> d,e,chi,K,P(split),Q(split),A,U,W
-    "state_s_fwd": (2 * _H + _P) + (_S + _H),                # W,K,U -> slot, w
-    "k_out_s": (_S + _H + 2 * _H + _A) + _H,                 # slot,w,Q,P -> out
-    "k_bprep_s": (_A + _A + 3 * _H + _P + 2 * _H) + (_P + 4 * _H),
+    "k_prep_s": (7 * _H + _P + _S) + (3 * _H + _H + _A // 2 + _H + _A + _P + _H),
+    # u,q,k,v,erase,write,delta,decay,C slot -> d,e,chi,K,P,Q,A,U,W
+    "state_s_fwd": (3 * _H + _P + _A // 2) + (_S + 2 * _H),  # W,K,U,Q,P -> slot, w, out
+    "k_bprep_s": (_A + _A // 2 + 3 * _H + _P + _H) + (_P + 4 * _H),
     # A,P,dO,K,e,decay,Q -> dU,Wk,Ant,At1,B1
     "state_s_bwd": (4 * _H + _P) + (_S + _H),                # Wk,Ant,At1,B1,dU -> slot, dw
     "state_c_bwd": (4 * _H + _P) + (_S + _H),
@@ -91,7 +89,7 @@ _VEC, _DEC, _GAM = 2 * R, 4 * R, 4
 OP_BYTES_PER_TOKEN_HEAD = {
     "k_prep_c": 2 * _VEC + _DEC + _GAM,                    # u, h, log-decay, gamma
     "k_prep_s": 6 * _VEC + _DEC,                           # u, q, k, v, erase, write, log-decay
-    "k_out_s": _VEC,                                       # out
+    "state_s_fwd": _VEC,                                   # out (plus the states below)
     "k_bprep_s": _VEC + _DEC,                              # dO, log-decay
     "k_grad_s": _VEC + 2 * _DEC,                           # dO, log-decay -> dlog_decay
     "k_src_bwd": 6 * _VEC + 4 * _VEC,                      # u, k, q, erase, v, write -> dq, derase, dv, dwrite
@@ -475,8 +473,8 @@ def main():
     us = {k: v[0] / v[1] * 1e3 for k, v in prof.items()}
     dom = max(prof, key=lambda k: prof[k][0])
     avg_s = us[dom] / 1e6
-    op_bytes = (OP_BYTES_PER_TOKEN_HEAD[dom] * nth if dom in OP_BYTES_PER_TOKEN_HEAD
-                else STATE_BYTES_PER_SEQ[dom] * B * H)
+    op_bytes = (OP_BYTES_PER_TOKEN_HEAD.get(dom, 0) * nth +
+                STATE_BYTES_PER_SEQ.get(dom, 0) * B * H)
     flops = FLOPS_PER_CHUNK.get(dom, 0) * nchunks
     traffic = profile_keys(TRAFFIC_FILE, "traffic_bytes")
     mfma_busy = profile_keys(COUNTER_FILE, "mfma_busy")

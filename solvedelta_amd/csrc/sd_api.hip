@@ -21,12 +21,6 @@ struct Carver {
     off += count * sizeof(T);
     return p;
   }
-  SP take_sp(size_t count) {
-    SP s;
-    s.hi = take<__bf16>(count);
-    s.lo = take<__bf16>(count);
-    return s;
-  }
 };
 
 // The forward workspace is two regions: `saved` holds what sd_bwd reads (chunk
@@ -51,8 +45,8 @@ FwdWs carve_fwd(void* saved, void* scratch, int B, int T, int H, size_t* saved_b
   w.Kc = c.take<_Float16>(panel);
   w.Gam = c.take<float>(n * NT * kKD);
   w.Ks = c.take<_Float16>(panel);
-  w.Qs = c.take_sp(panel);
-  w.Ps = c.take_sp(n * NT * kBT * kBT);
+  w.Qs = c.take<_Float16>(panel);
+  w.Ps = c.take<_Float16>(n * NT * kBT * kBT);
   if (saved_bytes) *saved_bytes = c.off + 256;
   Carver t{(char*)scratch};
   w.Wc = t.take<_Float16>(panel);

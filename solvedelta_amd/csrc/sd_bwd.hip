@@ -185,18 +185,18 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   {
     constexpr int PA = BT * BT / CT;
     float av[PA];
-    SPRaw pv[PA];
+    _Float16 pv[PA];
 #pragma unroll
     for (int q = 0; q < PA; ++q) {
       av[q] = p.f.As[cidx * BT * BT + threadIdx.x + q * CT];
       const int idx = threadIdx.x + q * CT;
-      pv[q] = sp_raw(p.f.Ps, cidx * BT * BT + frag_off(idx / BT, idx % BT, BT));
+      pv[q] = p.f.Ps[cidx * BT * BT + frag_off(idx / BT, idx % BT, BT)];
     }
 #pragma unroll
     for (int q = 0; q < PA; ++q) {
       const int idx = threadIdx.x + q * CT;
       s.A[(idx / BT) * LS + idx % BT] = av[q];
-      s.P[(idx / BT) * LS + idx % BT] = sp_val(pv[q]);
+      s.P[(idx / BT) * LS + idx % BT] = (float)pv[q];
     }
   }
   __syncthreads();
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   // Fragment order: a thread's two pieces are (state row c, tokens i0 .. i0+7).
   constexpr int NPC = KD * BT / 8 / CT;
   float ev[NPC][8];
-  SPRaw qv[NPC][8];
+  _Float16 qv[NPC][8];
   DoutRaw d[NPC][8];
 #pragma unroll
   for (int q = 0; q < NPC; ++q) {
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
     for (int e = 0; e < 8; ++e) {
       const int i = i0 + e;
       ev[q][e] = (float)p.f.e[(rowbase + i) * KD + c];
-      qv[q][e] = sp_raw(p.f.Qs, rowbase * KD + frag_off(i, c, KD));
+      qv[q][e] = p.f.Qs[rowbase * KD + frag_off(i, c, KD)];
       d[q][e] = dout_raw(p, b, t0 + i, hh, c);
     }
   }
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         ah[e] = (__bf16)(-ev[q][e] * __expf(cd.G[i0 + e][c]));
-        qh[e] = (__bf16)sp_val(qv[q][e]);   // a transposed, rounded copy of a split panel
+        qh[e] = (__bf16)(float)qv[q][e];    // a transposed bf16 copy of the fp16 panel
         dh[e] = (__bf16)dout_val(d[q][e]);  // exact in bf16
       }
       const long long ot = cidx * KD * BT + (long long)pc * 8;

@@ -247,36 +247,12 @@ __device__ __forceinline__ f4 mma_k32_lx(LA la, XA xa, LB lb, XB xb, int K, f4 a
                  [&](int k, int nn) { return bv[k >> 5][k & 7]; }, K, acc);
 }
 
-// Writes a per-chunk R x C panel (C = 64 or 128) split into bf16 hi / lo halves
-// in fragment order (see frag_off): each piece is one lane's 16 bytes of one
-// 16 x 32 operand block -- a fixed row and 8 consecutive columns -- produced
-// from val(row, col) and stored with one 16-byte store per half, so a wave's
-// stores are contiguous.  All CT threads of the workgroup take part.
-template <int R, int C, class F>
-__device__ __forceinline__ void store_frag_panel(__bf16* hi, __bf16* lo, long long base, F val) {
-  constexpr int PIECES = R * C / 8;
-#pragma unroll
-  for (int q = 0; q < (PIECES + CT - 1) / CT; ++q) {
-    const int pc = threadIdx.x + q * CT;
-    if (PIECES % CT != 0 && pc >= PIECES) break;
-    const int block = pc >> 6, lane = pc & 63;
-    const int row = (block / (C / 32)) * 16 + (lane & 15);
-    const int col0 = (block % (C / 32)) * 32 + (lane >> 4) * 8;
-    bf16x8 h, l;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      __bf16 a, b;
-      split_bf(val(row, col0 + e), a, b);
-      h[e] = a;
-      l[e] = b;
-    }
-    *reinterpret_cast<bf16x8*>(hi + base + (long long)pc * 8) = h;
-    *reinterpret_cast<bf16x8*>(lo + base + (long long)pc * 8) = l;
-  }
-}
-
-// store_frag_panel for a panel kept in one 2-byte type E (fp16, or bf16 with
-// no low half): each piece is val rounded to E, one 16-byte store per lane.
+// Writes a per-chunk R x C panel (C = 64 or 128) kept in one 2-byte type E
+// (fp16, or bf16 with no low half) in fragment order (see frag_off): each piece
+// is one lane's 16 bytes of one 16 x 32 operand block -- a fixed row and 8
+// consecutive columns -- produced from val(row, col), rounded to E and stored
+// with one 16-byte store, so a wave's stores are contiguous.  All CT threads of
+// the workgroup take part.
 template <int R, int C, class E, class F>
 __device__ __forceinline__ void store_frag_panel1(E* dst, long long base, F val) {
   typedef E V8 __attribute__((ext_vector_type(8)));

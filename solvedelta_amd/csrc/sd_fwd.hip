@@ -7,8 +7,8 @@
 //              pass: delta = U - W X0, X <- Gamma X + K^T delta (X = C^T);
 //   k_prep_s   (chunk-parallel) primal d = k + C^T k, dual sources e, chi, z,
 //              then the S memory's Gram, inverse, WY panels and output pair P;
-//   k_state<false, false> S state pass: chunk-entering slots and w;
-//   k_out_s    (chunk-parallel) readout o = Q~ X0 + P w from the saved slots.
+//   k_state<false, true> S state pass: chunk-entering slots and w, and the
+//              readout o = Q~ X0 + P w of each chunk from the same X0 and w.
 // The algebra is the generic pre-decay-read delta op: see the SolveDelta
 // chunk derivation restated in tests/chunk_model.py.
 #include "sd_common.cuh"
@@ -216,13 +216,16 @@ struct StateSmem {
   float Xf[KD][XFS];
   float wf[BT][XFS];
   float Uf[BT][XFS];  // U tile, staged from one 16-byte load per thread
+  float of[BT][XFS];  // readout tile of the previous chunk (forward S pass), stored one step later
   float Gf[KD];       // chunk decay, staged from one 16-byte load per lane of wave 0
 };
 
-template <bool REV>
+template <bool REV, bool OUT>
 struct StateFrags {
   using V8 = typename StateT<REV>::V8;
   V8 W[4];
+  V8 Q[OUT ? 4 : 1];  // readout operands (forward S pass): Q~ rows of this wave's token block
+  V8 P[OUT ? 2 : 1];  // and the same rows of P
   V8 K[SRB][2];
   bf16x8 A1[REV ? SRB : 1][2];
   bf16x8 B1[REV ? HALVES : 1][2];
@@ -235,9 +238,9 @@ __device__ __forceinline__ bf16x8 ldb8(const __bf16* p) { return *reinterpret_ca
 template <class V8, class E>
 __device__ __forceinline__ V8 ldv8(const E* p) { return *reinterpret_cast<const V8*>(p); }
 
-template <bool REV>
+template <bool REV, bool OUT>
 __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
-                                                 StateFrags<REV>& f) {
+                                                 StateFrags<REV, OUT>& f) {
   using E = typename StateT<REV>::E;
   using V8 = typename StateT<REV>::V8;
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
@@ -249,6 +252,14 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
   const E* Kp = static_cast<const E*>(p.Kt);
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldv8<V8>(Wp + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
+  if constexpr (OUT) {
+    static_assert(!REV, "the readout runs in the forward S pass");
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) f.Q[ks] = ldv8<V8>(p.Q + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      f.P[ks] = ldv8<V8>(p.P + cidx * BT * BT + frag_off(tb * 16 + m, ks * 32 + kq, BT));
+  }
 #pragma unroll
   for (int q = 0; q < SRB; ++q)
 #pragma unroll
@@ -290,11 +301,39 @@ __device__ __forceinline__ void stage_split4(E* hi, E* lo, f4 v) {
   *reinterpret_cast<V4*>(lo) = l;
 }
 
-// One chunk of the sequential pass with its operand fragments already in registers.
+// Stores the readout tile a step staged in s.of (chunk ch, 64 tokens x 16
+// columns) as bf16: one 16-byte piece per thread of the first 128 when the
+// output rows allow it (p.out_vec: V a multiple of 8 and a 16-byte aligned
+// base), element by element otherwise.  Called after a barrier that follows
+// the staging writes and precedes the next ones.
 template <bool REV>
+__device__ __forceinline__ void store_readout(const StateParams& p, const StateSmem<REV>& s, int n,
+                                              int ch, int tile) {
+  const int b = n / p.H, hh = n % p.H;
+  if (threadIdx.x >= BT * 2) return;
+  const int tok = threadIdx.x >> 1, c8 = (threadIdx.x & 1) * 8, t = ch * BT + tok;
+  const int col = tile * SCOLS + c8;
+  if (t >= p.T) return;
+  __bf16* dst = p.out + (((long long)b * p.T + t) * p.H + hh) * p.cols + col;
+  if (p.out_vec && col + 8 <= p.cols) {
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = f2bf(s.of[tok][c8 + e]);
+    *reinterpret_cast<bf16x8*>(dst) = v;
+  } else {
+    for (int e = 0; e < 8 && col + e < p.cols; ++e) dst[e] = f2bf(s.of[tok][c8 + e]);
+  }
+}
+
+// One chunk of the sequential pass with its operand fragments already in registers.
+// With OUT (forward S pass) the step also forms the chunk's readout
+// o = Q~ X0 + P w for its 16 columns: wave w's token block, from the X0 and w
+// fragments the recurrence loads anyway; o is off the recurrence's critical path.
+template <bool REV, bool OUT>
 __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>& s, int n, int ch,
-                                           int tile, const StateFrags<REV>& cur,
+                                           int tile, const StateFrags<REV, OUT>& cur,
                                            f4 (&X)[SRB][HALVES]) {
+  static_assert(!OUT || HALVES == 1, "readout tiles are 16 columns wide");
   using T = StateT<REV>;
   using E = typename T::E;
   using V8 = typename T::V8;
@@ -331,10 +370,13 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
                              tile * SCOLS + c4 * 4) = o;
     }
   }
+  if constexpr (OUT) {
+    if (ch > 0) store_readout(p, s, n, ch - 1, tile);
+  }
   // w = U + Wneg X0 (token block tb, each half).  The work that does not depend
   // on this chunk's w -- Gamma X (+ At1 B1) -- is issued alongside so the
   // independent MFMA chains overlap.
-  f4 acc[HALVES];
+  f4 acc[HALVES], ao = zero4();
 #pragma unroll
   for (int h = 0; h < HALVES; ++h)
     acc[h] = {s.Uf[tb * 16 + r4][h * 16 + m], s.Uf[tb * 16 + r4 + 1][h * 16 + m],
@@ -346,7 +388,9 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
       const V8 xh = ldv8<V8>(&s.Xh[h * 16 + m][ks * 32 + kq]);
       const V8 xl = ldv8<V8>(&s.Xl[h * 16 + m][ks * 32 + kq]);
       acc[h] = T::mma(cur.W[ks], xl, acc[h]);
+      if constexpr (OUT) ao = T::mma(cur.Q[ks], xl, ao);
       acc[h] = T::mma(cur.W[ks], xh, acc[h]);
+      if constexpr (OUT) ao = T::mma(cur.Q[ks], xh, ao);
     }
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
@@ -402,6 +446,17 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
         X[q][h] = T::mma(cur.K[q][ks], wl[ks], X[q][h]);
         X[q][h] = T::mma(cur.K[q][ks], wh[ks], X[q][h]);
       }
+    if constexpr (OUT) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        ao = T::mma(cur.P[ks], wl[ks], ao);
+        ao = T::mma(cur.P[ks], wh[ks], ao);
+      }
+    }
+  }
+  if constexpr (OUT) {  // o rows of token block tb, staged for the next step's store
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s.of[tb * 16 + r4 + e][m] = ao[e];
   }
   // No closing barrier: the next step writes Xh / Xl / Xf / Uf / Gf, whose last
   // readers all ran before this step's second barrier, and writes wh / wl / wf
@@ -409,7 +464,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
   // has finished this step's reads of them.
 }
 
-template <bool REV>
+template <bool REV, bool OUT>
 __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   __shared__ __align__(16) StateSmem<REV> s;
   const int NS = p.NT + 1;  // state slots per sequence
@@ -449,20 +504,24 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   // prefetches) so the compiler's wait counts only cover the buffer being
   // consumed; the last PF - 1 or fewer chunks run after the loop.
   auto clampc = [&](int it2) { return chunk_of(it2 < NT ? it2 : NT - 1); };
-  StateFrags<REV> f[PF];
+  StateFrags<REV, OUT> f[PF];
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j) load_state_frags<REV>(p, n, clampc(j), tile, f[j]);
+  for (int j = 0; j < PF - 1; ++j) load_state_frags<REV, OUT>(p, n, clampc(j), tile, f[j]);
   int it = 0;
   for (; it + PF - 1 < NT; it += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      load_state_frags<REV>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
-      state_step<REV>(p, s, n, chunk_of(it + j), tile, f[j], X);
+      load_state_frags<REV, OUT>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
+      state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X);
     }
   }
 #pragma unroll
   for (int j = 0; j < PF - 1; ++j)
-    if (it + j < NT) state_step<REV>(p, s, n, chunk_of(it + j), tile, f[j], X);
+    if (it + j < NT) state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X);
+  if constexpr (OUT) {  // the last chunk's readout
+    __syncthreads();
+    store_readout(p, s, n, NT - 1, tile);
+  }
   // final state (also kept as slot NT for the backward)
   for (int q = 0; q < SRB; ++q)
     for (int h = 0; h < HALVES; ++h)
@@ -484,9 +543,11 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
 void launch_state(const char* name, const StateParams& sp, int nseq, hipStream_t st) {
   const dim3 grid(STILES * nseq), blk(STHREADS);
   if (sp.rev)
-    SD_LAUNCH(name, (k_state<true>), grid, blk, 0, st, sp);
+    SD_LAUNCH(name, (k_state<true, false>), grid, blk, 0, st, sp);
+  else if (sp.out)
+    SD_LAUNCH(name, (k_state<false, true>), grid, blk, 0, st, sp);
   else
-    SD_LAUNCH(name, (k_state<false>), grid, blk, 0, st, sp);
+    SD_LAUNCH(name, (k_state<false, false>), grid, blk, 0, st, sp);
 }
 
 // ---------------------------------------------------------------------------
@@ -727,15 +788,14 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   auto Draw = [&](int j, int c) { return (float)dg_[j * KD + c]; };
   // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i
   decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pb[i][c]; }, s.Kp, Draw, false, s.M);
-  store_frag_panel<BT, BT>(p.Ps.hi, p.Ps.lo, cidx * BT * BT,
-                           [&](int i, int j) { return s.M[i * LS + j]; });
+  store_frag_panel1<BT, BT>(p.Ps, cidx * BT * BT, [&](int i, int j) { return s.M[i * LS + j]; });
 #pragma unroll
   for (int q = 0; q < KPC; ++q) {
     const long long o = cidx * KD * BT + (long long)(threadIdx.x + q * CT) * 8;
     *reinterpret_cast<f16x8*>(p.Ks + o) = ksv[q];
   }
-  store_frag_panel<BT, KD>(p.Qs.hi, p.Qs.lo, rowbase * KD,
-                           [&](int i, int c) { return s.Pb[i][c] * __expf(cd.G[i][c]); });
+  store_frag_panel1<BT, KD>(p.Qs, rowbase * KD,
+                            [&](int i, int c) { return s.Pb[i][c] * __expf(cd.G[i][c]); });
   __syncthreads();
   // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
   decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pa[i][c]; }, s.Kp, Draw, true, s.M);
@@ -778,126 +838,6 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
 size_t prep_c_smem() { return sizeof(PrepCSmem); }
 size_t prep_s_smem() { return sizeof(PrepSSmem); }
 
-// ---------------------------------------------------------------------------
-// k_out_s: the S memory's readout o = Q~ X0 + P w for every chunk in parallel,
-// from the chunk-entering states the sequential pass saved (so the pass itself
-// carries no output work).  One wave per 16-column block of the output.
-// ---------------------------------------------------------------------------
-struct OutParams {
-  int H, T, NT, Tp, V;
-  const xslot_t* Xs;  // [n][NT+1][128][128] chunk-entering S
-  const fpan_t* w;  // [n][Tp][128] S-op w
-  SP Q, P;          // fragment-ordered Q~ [64][128] and P [64][64] per chunk
-  __bf16* out;      // [B,T,H,V]
-};
-
-// The chunk's Q~ and P panels, copied once (fragment order kept): every wave
-// reads all of their rows, so from L2 they would be fetched eight times.
-struct OutSmem {
-  __bf16 qh[BT * KD], ql[BT * KD];
-  __bf16 ph[BT * BT], pl[BT * BT];
-};
-
-__global__ __launch_bounds__(CT) void k_out_s(OutParams p) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  OutSmem& s = *reinterpret_cast<OutSmem*>(smem_raw);
-  const int ch = blockIdx.x, n = blockIdx.y, b = n / p.H, hh = n % p.H;
-  const int cb = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
-  const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + ch * BT;
-  const xslot_t* X0 = p.Xs + ((long long)n * (p.NT + 1) + ch) * KD * KD;
-  const fpan_t* wv = p.w + rowbase * KD;
-  constexpr int QP = BT * KD / 8 / CT, PP = BT * BT / 8 / CT;  // 16-byte pieces per thread
-  bf16x8 vq[2][QP], vp[2][PP];  // loaded first, written to LDS after the X0 / w loads are issued
-  {
-    static_assert(QP * CT * 8 == BT * KD && PP * CT * 8 == BT * BT, "whole pieces");
-#pragma unroll
-    for (int q = 0; q < QP; ++q) {
-      const long long o = rowbase * KD + (long long)(threadIdx.x + q * CT) * 8;
-      vq[0][q] = *reinterpret_cast<const bf16x8*>(p.Q.hi + o);
-      vq[1][q] = *reinterpret_cast<const bf16x8*>(p.Q.lo + o);
-    }
-#pragma unroll
-    for (int q = 0; q < PP; ++q) {
-      const long long o = cidx * BT * BT + (long long)(threadIdx.x + q * CT) * 8;
-      vp[0][q] = *reinterpret_cast<const bf16x8*>(p.P.hi + o);
-      vp[1][q] = *reinterpret_cast<const bf16x8*>(p.P.lo + o);
-    }
-  }
-  // B operands (column block cb): X0 over K = 128 state rows, w over the 64 tokens
-  float xr[4][8], wr[2][8];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) xr[ks][e] = (float)X0[(ks * 32 + kq + e) * KD + cb * 16 + m];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) wr[ks][e] = (float)wv[(ks * 32 + kq + e) * KD + cb * 16 + m];
-#pragma unroll
-  for (int q = 0; q < QP; ++q) {
-    const int o = (threadIdx.x + q * CT) * 8;
-    *reinterpret_cast<bf16x8*>(s.qh + o) = vq[0][q];
-    *reinterpret_cast<bf16x8*>(s.ql + o) = vq[1][q];
-  }
-#pragma unroll
-  for (int q = 0; q < PP; ++q) {
-    const int o = (threadIdx.x + q * CT) * 8;
-    *reinterpret_cast<bf16x8*>(s.ph + o) = vp[0][q];
-    *reinterpret_cast<bf16x8*>(s.pl + o) = vp[1][q];
-  }
-  Frag bx[4], bw[2];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      __bf16 h, lo;
-      split_bf(xr[ks][e], h, lo);
-      bx[ks].h[e] = h;
-      bx[ks].l[e] = lo;
-    }
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      __bf16 h, lo;
-      split_bf(wr[ks][e], h, lo);
-      bw[ks].h[e] = h;
-      bw[ks].l[e] = lo;
-    }
-  const int col = cb * 16 + m;
-  __syncthreads();  // Q~ and P staged
-#pragma unroll
-  for (int I = 0; I < NB; ++I) {
-    Frag q[4], pf[2];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int o = (int)frag_off(I * BS + m, ks * 32 + kq, KD);
-      q[ks].h = *reinterpret_cast<const bf16x8*>(s.qh + o);
-      q[ks].l = *reinterpret_cast<const bf16x8*>(s.ql + o);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int o = (int)frag_off(I * BS + m, ks * 32 + kq, BT);
-      pf[ks].h = *reinterpret_cast<const bf16x8*>(s.ph + o);
-      pf[ks].l = *reinterpret_cast<const bf16x8*>(s.pl + o);
-    }
-    f4 acc = zero4();
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mma3f(q[ks], bx[ks], acc);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (ks == 1 && I < 2) break;  // P is lower triangular: tokens 32.. only reach rows 32..
-      acc = mma3f(pf[ks], bw[ks], acc);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = ch * BT + I * BS + r4 + e;
-      if (t < p.T && col < p.V)
-        p.out[(((long long)b * p.T + t) * p.H + hh) * p.V + col] = f2bf(acc[e]);
-    }
-  }
-}
-
 int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const FwdWs& w,
                hipStream_t st) {
   
@@ -931,13 +871,9 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   ss.Xs = w.Xs; ss.wout = w.wS;
   ss.init = in->S0; ss.init_transposed = 0;
   ss.fin = S_T; ss.fin_transposed = 0;
+  ss.Q = w.Qs; ss.P = w.Ps; ss.out = (__bf16*)out;
+  ss.out_vec = in->V % 8 == 0 && ((uintptr_t)out & 15) == 0;
   launch_state("state_s_fwd", ss, n, st);
-
-  OutParams op{};
-  op.H = in->H; op.T = in->T; op.NT = NT; op.Tp = Tp; op.V = in->V;
-  op.Xs = w.Xs; op.w = w.wS; op.Q = w.Qs; op.P = w.Ps; op.out = (__bf16*)out;
-  SD_SMEM_ONCE(k_out_s, (int)sizeof(OutSmem));
-  SD_LAUNCH("k_out_s", k_out_s, dim3(NT, n), dim3(CT), sizeof(OutSmem), st, op);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 

@@ -8,16 +8,8 @@
 
 namespace sd {
 
-// A "split panel": an fp32 panel stored as bf16 high part + bf16 residual
-// (same bytes as fp32, ~16 mantissa bits).  MFMA consumers load both halves as
-// ready-made bf16 fragments instead of converting fp32 operands on every use.
-struct SP {
-  __bf16* hi;
-  __bf16* lo;
-};
-
 #ifdef __HIPCC__
-// Fragment order of a per-chunk split panel of R rows x C columns (C = 64 or
+// Fragment order of a per-chunk panel of R rows x C columns (C = 64 or
 // 128): each 16-row x 32-column MFMA operand block is 512 consecutive
 // elements, lane-major (lane = 16 * ((col % 32) / 8) + row % 16, 8 elements
 // per lane), so the sequential state pass reads a fragment as one contiguous
@@ -26,13 +18,6 @@ __device__ __forceinline__ long long frag_off(int row, int col, int C) {
   return ((long long)(row >> 4) * (C >> 5) + (col >> 5)) * 512 +
          ((((col & 31) >> 3) << 4) + (row & 15)) * 8 + (col & 7);
 }
-
-// Raw halves of a split value (load now, combine later with sp_val).
-struct SPRaw {
-  __bf16 h, l;
-};
-__device__ __forceinline__ SPRaw sp_raw(const SP& sp, long long i) { return {sp.hi[i], sp.lo[i]}; }
-__device__ __forceinline__ float sp_val(SPRaw r) { return (float)r.h + (float)r.l; }
 
 // 0 on a token flagged fresh (its predictor residual reads a zero state: the
 // erase read x = gamma u^ of the C op is dropped), 1 otherwise.  t must be a
@@ -88,9 +73,10 @@ struct FwdWs {
   fpan_t* d;      // primal address d = k + C^T k            [n][Tp][128]
   fpan_t* wS;     // S-op w = z - S~^T e                     [n][Tp][128]
   // transient panels; the forward state passes' MFMA operands W (token-major)
-  // and K (chunk-transposed) are fp16 in fragment order
+  // and K (chunk-transposed) are fp16 in fragment order, as are the S readout's
+  // Q~ (token-major) and P ([64][64] per chunk)
   _Float16* Wc; float* Uc; _Float16* Kc; float* Gam;
-  _Float16* Ws; float* Us; _Float16* Ks; SP Qs; SP Ps;
+  _Float16* Ws; float* Us; _Float16* Ks; _Float16* Qs; _Float16* Ps;
 };
 
 struct FwdParams {
@@ -100,7 +86,7 @@ struct FwdParams {
   fpan_t *delta, *d, *e, *chi;
   float *Ac, *As;
   _Float16* Wc; float* Uc; _Float16* Kc; float* Gam;
-  _Float16* Ws; float* Us; _Float16* Ks; SP Qs; SP Ps;
+  _Float16* Ws; float* Us; _Float16* Ks; _Float16* Qs; _Float16* Ps;
 };
 
 // Sequential chunk pass, forward (state X) or reverse (cotangent lambda, rev):
@@ -116,6 +102,10 @@ struct StateParams {
   void* wout;  // w panel: fpan_t (forward) or bpan_t (reverse)
   const float* init; int init_transposed;
   float* fin; int fin_transposed;
+  // forward S pass only: the readout o = Q~ X0 + P w of every chunk, formed
+  // from the staged X0 and w tiles and written to out [B,T,H,V] (bf16)
+  const _Float16* Q; const _Float16* P; __bf16* out;
+  int out_vec;  // rows of out take 16-byte stores (V % 8 == 0, aligned base)
 };
 
 void prof_begin(const char* name, hipStream_t st);
