@@ -663,9 +663,8 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   __syncthreads();
   const bpan_t* ddp = p.g.dd + rowbase * KD;
   // P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic}, i <= l
-  decayed_gram<false>(
-      cd, [&](int i, int c) { return (float)ddp[i * KD + c]; }, [&](int j, int c) { return s.Uh[j][c]; },
-      false, s.P);
+  static_assert(sizeof(bpan_t) == 2, "dd is a bf16 panel");
+  decayed_gram_gx<false>(cd, ddp, [&](int j, int c) { return s.Uh[j][c]; }, false, s.P);
   mat64_mul(s.P, s.A, s.N);
   __syncthreads();
   const bpan_t* ddl = p.g.ddelta + rowbase * KD;
@@ -754,10 +753,17 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     store_frag_panel1<BT, KD>(p.g.Wk, rowbase * KD,
                              [&](int i, int c) { return Wst[i * KD + c]; });
   }
-  for (int idx = threadIdx.x; idx < BT * KD; idx += CT) {
+  for (int idx = threadIdx.x * 8; idx < BT * KD; idx += CT * 8) {  // 16-byte pieces
     const int i = idx / KD, c = idx % KD;
-    p.g.kh[(rowbase + i) * KD + c] = (fpan_t)s.Kh[i][c];
-    p.g.uh[(rowbase + i) * KD + c] = (fpan_t)s.Uh[i][c];
+    typedef fpan_t P8 __attribute__((ext_vector_type(8)));
+    P8 kv, uv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      kv[e] = (fpan_t)s.Kh[i][c + e];
+      uv[e] = (fpan_t)s.Uh[i][c + e];
+    }
+    *reinterpret_cast<P8*>(p.g.kh + (rowbase + i) * KD + c) = kv;
+    *reinterpret_cast<P8*>(p.g.uh + (rowbase + i) * KD + c) = uv;
   }
   // chunk-transposed panels, fragment order
   // The reverse pass's injection sum_i At1_ci Kh_i,col is formed as

@@ -422,6 +422,68 @@ __device__ void decayed_gram(const ChunkDecay& cd, FX X, FY Y, bool strict, floa
   __syncthreads();
 }
 
+// decayed_gram with the X side a 64 x 128 bf16 panel in global memory (row
+// stride KD): each lane's 8-column slice of its row is one 16-byte load, all
+// four issued before the first use (the per-element form makes 32 two-byte
+// loads per block pair).
+template <bool EXCL, class FY>
+__device__ void decayed_gram_gx(const ChunkDecay& cd, const __bf16* Xg, FY Y, bool strict, float* M,
+                                int ldm = LS) {
+  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+  for (int p = w; p < 10; p += CW) {
+    int I = 0, J = p;
+    while (J > I) { J -= I + 1; ++I; }  // p -> (I, J) with J <= I
+    const int I0 = I * BS, J0 = J * BS;
+    const float* RJ = cd.R[J];
+    bf16x8 xr[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      xr[ks] = *reinterpret_cast<const bf16x8*>(Xg + (I0 + m) * KD + ks * 32 + kq);
+    f4 acc = mma_k32_lx(
+        [&](int mm, int c) { return (float)xr[c >> 5][c & 7]; },
+        [&](int mm, int c, float x) {
+          const int i = I0 + mm;
+          const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+          return x * __expf(gx - RJ[c]);
+        },
+        [&](int c, int n) { return Y(J0 + n, c); },
+        [&](int c, int n, float y) {
+          return y * exp_unless_wild(cd.wild[J][c] != 0, RJ[c] - cd.G[J0 + n][c]);
+        },
+        KD, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I0 + out_row(e), j = J0 + out_col();
+      const bool keep = strict ? (j < i) : (j <= i);
+      M[i * ldm + j] = keep ? acc[e] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) M[i * ldm + j] = 0.f;
+  }
+  __syncthreads();
+  for (int J = 0; J < NB; ++J) {  // exact fix-up for wild coordinates
+    const int nw = cd.nwild[J];
+    if (nw == 0) continue;
+    const int J0 = J * BS;
+    const int npairs = (BT - J0) * BS;
+    for (int idx = threadIdx.x; idx < npairs; idx += CT) {
+      const int i = J0 + idx / BS, j = J0 + idx % BS;
+      const bool keep = strict ? (j < i) : (j <= i);
+      if (!keep) continue;
+      float s = 0.f;
+      for (int q = 0; q < nw; ++q) {
+        const int c = cd.wlist[J][q];
+        const float gx = EXCL ? gx_excl(cd, i, c) : cd.G[i][c];
+        s += (float)Xg[i * KD + c] * Y(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      }
+      M[i * ldm + j] += s;
+    }
+  }
+  __syncthreads();
+}
+
 // D(16x16) += A(16x16) B(16x16) with lane (g = l >> 4, m = l & 15) holding
 // av[e] = A[m][4g + e] and bv[e] = B[4g + e][m]: four fp32 16x16x4 MFMAs, one per
 // e, each summing over g.  Exact fp32 products and no operand conversions, which
