@@ -46,6 +46,25 @@ __device__ __forceinline__ float conv_x(const ConvArgs& a, int b, int t, int d) 
   return bf2f(a.init[((long long)b * a.D + d) * 3 + (t + 3)]);
 }
 
+// xs[t0 - 3 + j] for j < N: every load reads a clamped, valid token and is
+// issued before the first use (a guarded load would branch and wait for the
+// loads before it); tokens past T read 0, and the three halo tokens of the
+// first chunk come from the initial state (zeros when absent).
+template <int N>
+__device__ __forceinline__ void conv_window(const ConvArgs& a, int b, int t0, int d, float (&xv)[N]) {
+  const __bf16* xb = a.x + (long long)b * a.sb + d;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int t = t0 - 3 + j, tc = t < 0 ? 0 : (t < a.T ? t : a.T - 1);
+    xv[j] = keep_if(t < a.T, bf2f(xb[(long long)tc * a.st]));
+  }
+  if (t0 == 0) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      xv[j] = a.init ? bf2f(a.init[((long long)b * a.D + d) * 3 + j]) : 0.f;
+  }
+}
+
 __global__ __launch_bounds__(NTHREADS) void k_conv_fwd(ConvArgs a, __bf16* __restrict__ y,
                                                        __bf16* __restrict__ fin) {
   const int d = blockIdx.x * NTHREADS + threadIdx.x, b = blockIdx.z;
@@ -53,8 +72,7 @@ __global__ __launch_bounds__(NTHREADS) void k_conv_fwd(ConvArgs a, __bf16* __res
   const int t0 = blockIdx.y * CONV_TC;
   const float w0 = a.w[d * 4], w1 = a.w[d * 4 + 1], w2 = a.w[d * 4 + 2], w3 = a.w[d * 4 + 3];
   float xv[CONV_TC + 3];
-#pragma unroll
-  for (int j = 0; j < CONV_TC + 3; ++j) xv[j] = conv_x(a, b, t0 - 3 + j, d);
+  conv_window(a, b, t0, d, xv);
 #pragma unroll
   for (int j = 0; j < CONV_TC; ++j) {
     const int t = t0 + j;
@@ -85,12 +103,11 @@ __global__ __launch_bounds__(NTHREADS) void k_conv_bwd(ConvArgs a, const __bf16*
   constexpr int NX = CONV_TC + 6, NA = CONV_TC + 3;
   float xv[NX];   // xs[t0-3 .. t0+CONV_TC+2]
   float gv[NA];   // dy[t0 .. t0+CONV_TC+2]
+  conv_window(a, b, t0, d, xv);
 #pragma unroll
-  for (int j = 0; j < NX; ++j) xv[j] = conv_x(a, b, t0 - 3 + j, d);
-#pragma unroll
-  for (int j = 0; j < NA; ++j) {
+  for (int j = 0; j < NA; ++j) {  // clamped token, then select
     const int t = t0 + j;
-    gv[j] = t < T ? bf2f(dy[((long long)b * T + t) * a.D + d]) : 0.f;
+    gv[j] = keep_if(t < T, bf2f(dy[((long long)b * T + (t < T ? t : T - 1)) * a.D + d]));
   }
   float df[3] = {0.f, 0.f, 0.f};  // dfinal_m is the cotangent of xs[T-3+m]
   if (dfin)
@@ -199,7 +216,8 @@ __global__ __launch_bounds__(NTHREADS) void k_gate_bwd(int N, int H, int r, cons
   part[(long long)blockIdx.y * 2 * HR + HR + c] = dl;
 }
 
-// One workgroup per head: dbias[c] for the head's columns, dlog_rate[h].
+// One workgroup per head: dbias[c] for the head's columns, dlog_rate[h], from
+// nparts partial rows (the backward passes the one row of column sums).
 __global__ __launch_bounds__(NTHREADS) void k_gate_reduce(int H, int r, int nparts,
                                                           const float* part, float* dbias,
                                                           float* dlog_rate) {
@@ -237,12 +255,12 @@ __device__ __forceinline__ void rms_row(const __bf16* x, const __bf16* g, const 
                                         float (&xv)[4], float (&gv)[4], float (&wv)[4]) {
   const int l = lane_id();
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int c = l + 64 * m;
+  for (int m = 0; m < 4; ++m) {  // clamped column, then select: no branch around the loads
+    const int c = l + 64 * m, cc = c < D ? c : D - 1;
     const bool ok = c < D;
-    xv[m] = ok ? bf2f(x[c]) : 0.f;
-    gv[m] = ok ? bf2f(g[c]) : 0.f;
-    wv[m] = ok ? w[c] : 0.f;
+    xv[m] = keep_if(ok, bf2f(x[cc]));
+    gv[m] = keep_if(ok, bf2f(g[cc]));
+    wv[m] = keep_if(ok, w[cc]);
   }
 }
 
@@ -267,46 +285,71 @@ __global__ __launch_bounds__(RMS_ROWS * 64) void k_rms_fwd(int N, int D, float e
 
 // dx = rstd (gy - xhat mean(gy xhat)), gy = dy w s;  dg = dy xhat w s (1 - s);
 // dw_c = sum dy xhat s;  y (recomputed for the projection's weight gradient).
+// Each wave takes RMS_U rows at a time, every row's loads issued before the
+// first row's reductions (rows past N read row N - 1 and store nothing).
+constexpr int RMS_U = 4;
+static_assert(RMS_PART % (RMS_ROWS * RMS_U) == 0, "whole row groups per workgroup");
+
 __global__ __launch_bounds__(RMS_ROWS * 64) void k_rms_bwd(int N, int D, float eps,
-                                                           const __bf16* x, const __bf16* g,
-                                                           const float* w, const __bf16* dy,
-                                                           __bf16* dx, __bf16* dg, __bf16* y,
-                                                           float* part) {
+                                                           const __bf16* __restrict__ x,
+                                                           const __bf16* __restrict__ g,
+                                                           const float* __restrict__ w,
+                                                           const __bf16* __restrict__ dy,
+                                                           __bf16* __restrict__ dx,
+                                                           __bf16* __restrict__ dg,
+                                                           __bf16* __restrict__ y,
+                                                           float* __restrict__ part) {
   __shared__ float pw[RMS_ROWS][256];
   const int l = lane_id(), wv_ = wave_id();
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float wv[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int c = l + 64 * m;
+    wv[m] = keep_if(c < D, w[c < D ? c : D - 1]);
+  }
   // a workgroup covers RMS_PART rows: each wave walks RMS_PART / RMS_ROWS of them
   const int base = blockIdx.x * RMS_PART;
-  for (int rr = wv_; rr < RMS_PART; rr += RMS_ROWS) {
-    const int n = base + rr;
-    if (n >= N) break;
-    float xv[4], gv[4], wv[4], dv[4];
-    rms_row(x + (long long)n * D, g + (long long)n * D, w, D, xv, gv, wv);
+  for (int r0 = wv_; r0 < RMS_PART; r0 += RMS_ROWS * RMS_U) {
+    if (base + r0 >= N) break;
+    float xv[RMS_U][4], gv[RMS_U][4], dv[RMS_U][4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int c = l + 64 * m;
-      dv[m] = c < D ? bf2f(dy[(long long)n * D + c]) : 0.f;
+    for (int u = 0; u < RMS_U; ++u) {
+      const int n = base + r0 + u * RMS_ROWS, nc = n < N ? n : N - 1;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int c = l + 64 * m, cc = c < D ? c : D - 1;
+        const long long o = (long long)nc * D + cc;
+        xv[u][m] = keep_if(c < D, bf2f(x[o]));
+        gv[u][m] = keep_if(c < D, bf2f(g[o]));
+        dv[u][m] = keep_if(c < D && n < N, bf2f(dy[o]));
+      }
     }
-    const float ss = wave_sum(xv[0] * xv[0] + xv[1] * xv[1] + xv[2] * xv[2] + xv[3] * xv[3]);
-    const float rs = rsqrtf(ss / D + eps);
-    float gy[4], xh[4], sg[4], dot = 0.f;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      sg[m] = sigm(gv[m]);
-      xh[m] = xv[m] * rs;
-      gy[m] = dv[m] * wv[m] * sg[m];
-      dot += gy[m] * xh[m];
-    }
-    dot = wave_sum(dot) / D;
+    for (int u = 0; u < RMS_U; ++u) {
+      const int n = base + r0 + u * RMS_ROWS;
+      const float ss = wave_sum(xv[u][0] * xv[u][0] + xv[u][1] * xv[u][1] + xv[u][2] * xv[u][2] +
+                                xv[u][3] * xv[u][3]);
+      const float rs = rsqrtf(ss / D + eps);
+      float gy[4], xh[4], sg[4], dot = 0.f;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int c = l + 64 * m;
-      if (c < D) {
-        const long long o = (long long)n * D + c;
-        dx[o] = f2bf(rs * (gy[m] - xh[m] * dot));
-        dg[o] = f2bf(dv[m] * xh[m] * wv[m] * sg[m] * (1.f - sg[m]));
-        if (y) y[o] = f2bf(xh[m] * wv[m] * sg[m]);
-        acc[m] += dv[m] * xh[m] * sg[m];
+      for (int m = 0; m < 4; ++m) {
+        sg[m] = sigm(gv[u][m]);
+        xh[m] = xv[u][m] * rs;
+        gy[m] = dv[u][m] * wv[m] * sg[m];
+        dot += gy[m] * xh[m];
+      }
+      dot = wave_sum(dot) / D;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int c = l + 64 * m;
+        acc[m] += dv[u][m] * xh[m] * sg[m];  // 0 on rows past N (dv = 0)
+        if (c < D && n < N) {
+          const long long o = (long long)n * D + c;
+          dx[o] = f2bf(rs * (gy[m] - xh[m] * dot));
+          dg[o] = f2bf(dv[u][m] * xh[m] * wv[m] * sg[m] * (1.f - sg[m]));
+          if (y) y[o] = f2bf(xh[m] * wv[m] * sg[m]);
+        }
       }
     }
   }
@@ -540,9 +583,10 @@ int sd_conv4_silu_masked_bwd(int B, int T, int D, const void* x, int64_t x_sb, i
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 
+// Workspace: the [np][2][H*r] per-workgroup partials, then their [2][H*r] column sums.
 size_t sd_kda_gate_workspace_bytes(int N, int H, int r) {
   if (N <= 0 || H <= 0 || r <= 0) return 0;
-  return (size_t)cdiv(N, GATE_TR) * 2 * H * r * sizeof(float);
+  return (size_t)(cdiv(N, GATE_TR) + 1) * 2 * H * r * sizeof(float);
 }
 
 int sd_kda_gate_fwd(int N, int H, int r, const void* raw, int64_t raw_row_stride,
@@ -568,8 +612,13 @@ int sd_kda_gate_bwd(int N, int H, int r, const void* raw, int64_t raw_row_stride
   SD_LAUNCH("k_gate_bwd", k_gate_bwd, dim3(cdiv(H * r, NTHREADS), np), dim3(NTHREADS), 0, st, N,
             H, r, (const __bf16*)raw, raw_row_stride, log_rate, bias, dout, (__bf16*)draw,
             (float*)workspace);
-  SD_LAUNCH("k_gate_reduce", k_gate_reduce, dim3(H), dim3(NTHREADS), 0, st, H, r, np,
-            (const float*)workspace, dbias, dlog_rate);
+  // column sums over the partial rows spread over many workgroups (a per-head
+  // walk over every partial row kept only H workgroups busy), then per head
+  float* colsum = (float*)workspace + (size_t)np * 2 * H * r;
+  SD_LAUNCH("k_sum_parts", k_sum_parts, dim3(cdiv(2 * H * r, 32)), dim3(NTHREADS), 0, st,
+            (const float*)workspace, np, 2 * H * r, colsum);
+  SD_LAUNCH("k_gate_reduce", k_gate_reduce, dim3(H), dim3(NTHREADS), 0, st, H, r, 1,
+            (const float*)colsum, dbias, dlog_rate);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 
