@@ -77,3 +77,32 @@ def test_split_workspace_equals_single_workspace(B, T, H, r, V):
     z = _run(B, T, H, r, V, 0x00, 63)
     for i, (x, y) in enumerate(zip(a, z)):
         assert torch.equal(x, y), i
+
+
+@pytest.mark.parametrize("B,T,H,r,V", [(1, 130, 2, 64, 64), (1, 70, 2, 32, 40)])
+def test_unaligned_output_pointer_bitwise(B, T, H, r, V):
+    """The S pass stores its readout as 16-byte pieces only when the output's
+    rows allow it; an output base 2 bytes off a 16-byte boundary takes the
+    element-wise path and must give bitwise the aligned result."""
+    from solvedelta_amd import _lib
+    from solvedelta_amd.operator import _inputs
+    lib = _lib.load()
+    args = make_inputs(B, T, H, r, V, seed=41)
+    C0, S0 = make_state(B, H, r, V, seed=42)
+    ins = _inputs(*args, C0, S0)
+    dev = args[0].device
+    st = torch.cuda.current_stream(dev).cuda_stream
+    nf = lib.sd_fwd_workspace_bytes(B, T, H, r, V)
+    fws = torch.empty(nf, dtype=torch.uint8, device=dev)
+    n = B * T * H * V
+    outs = []
+    for off in (0, 1):
+        buf = torch.full((n + 8,), float("nan"), dtype=torch.bfloat16, device=dev)
+        out = buf[off:off + n]
+        print(f"case B{B} T{T} H{H} r{r} V{V} output offset {off}", flush=True)
+        assert lib.sd_fwd(ctypes.byref(ins), out.data_ptr(), None, None, fws.data_ptr(), nf,
+                          st) == 0
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all()
+        outs.append(out.clone())
+    assert torch.equal(outs[0], outs[1])
