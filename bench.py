@@ -21,6 +21,7 @@ Prints ONE JSON line (rank 0).  Besides the throughput it reports:
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -523,14 +524,23 @@ def main():
     if a.step_only:
         print(json.dumps(res), flush=True)
         return
+    # each section starts from a collected heap: cyclic garbage left by the
+    # previous sections (and the device memory it holds) otherwise slows the
+    # launch-bound config-4 step by a third
+    gc.collect()
     res["forward"] = forward_bench(ins, st, a.steps, a.warmup)
+    gc.collect()
     res["reference_shape"] = refshape_bench(dev, a.steps, a.warmup)
+    gc.collect()
     res["wide"] = variant_bench(dev, 5, 2, r=256, v=256)
+    gc.collect()
     res["masked"] = variant_bench(dev, 10, 3, masked=True)
     if not a.no_decode:
+        gc.collect()
         res["decode"] = decode_bench(dev)
         res["decode_uncached"] = decode_bench(dev, steps=32, streams=512)
     if not a.no_lm:
+        gc.collect()
         res["causal_lm"] = lm_bench(dev, graph=a.lm_graph)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
