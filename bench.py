@@ -371,6 +371,9 @@ def lm_bench(dev, steps=5, warmup=2, graph=False):
     ids = torch.randint(0, 32000, (2, 1024), generator=g).to(dev)
 
     def eager():
+        # a fresh step's gradients (as after an optimizer's zero_grad), not an
+        # accumulation onto the previous step's
+        model.zero_grad(set_to_none=True)
         with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
             loss, _, _ = model(ids, labels=ids)
         loss.backward()
