@@ -528,13 +528,12 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
     p.g.ddelta[row + l + 64] = 0.f;
     return;
   }
+  // every row of the token is loaded before the first reduction: a load issued
+  // after a cross-lane sum waits for it, which made three memory round trips
   float u0, u1, k0, k1, q0, q1, e0, e1, w0, w1, v0, v1;
   ldrow2(p.in.u, b, t, hh, p.T, r, u0, u1);
-  norm2(u0, u1);
   ldrow2(p.in.k, b, t, hh, p.T, r, k0, k1);
-  norm2(k0, k1);
   ldrow2(p.in.q, b, t, hh, p.T, r, q0, q1);
-  const float rq = norm2(q0, q1);
   ldrow2(p.in.erase_raw, b, t, hh, p.T, r, e0, e1);
   ldrow2(p.in.write_raw, b, t, hh, p.T, V, w0, w1);
   ldrow2(p.in.v, b, t, hh, p.T, V, v0, v1);
@@ -543,6 +542,9 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   const float dc0 = p.g.dchi[row + l], dc1 = p.g.dchi[row + l + 64];
   const float dz0 = p.g.dwS[row + l], dz1 = p.g.dwS[row + l + 64];
   const float dd0 = p.g.dd[row + l], dd1 = p.g.dd[row + l + 64];  // loaded before any store
+  norm2(u0, u1);
+  norm2(k0, k1);
+  const float rq = norm2(q0, q1);
   const float usq = wave_sum(u0 * u0 + u1 * u1);
   const float dsq = wave_sum(d0 * d0 + d1 * d1);
   const float N = sqrtf(RHO * RHO + usq * dsq);
@@ -995,11 +997,9 @@ __global__ __launch_bounds__(NTHREADS) void k_final(BwdParams p) {
   if (t >= p.T) return;
   const int l = lane_id(), r = p.r;
   const long long row = ((long long)n * p.Tp + t) * KD;
-  float u0, u1, k0, k1, h0, h1;
+  float u0, u1, k0, k1, h0, h1;  // rows loaded before the norms' cross-lane sums
   ldrow2(p.in.u, b, t, hh, p.T, r, u0, u1);
-  const float ru = norm2(u0, u1);
   ldrow2(p.in.k, b, t, hh, p.T, r, k0, k1);
-  const float rk = norm2(k0, k1);
   ldrow2(p.in.h, b, t, hh, p.T, r, h0, h1);
   const float gm = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
                                                    (long long)t * p.in.gamma.st +
@@ -1013,6 +1013,8 @@ __global__ __launch_bounds__(NTHREADS) void k_final(BwdParams p) {
   const float du1 = p.g.du_src[row + l + 64] + p.g.dkC[row + l + 64] + gm * dx1;
   const float dk0 = p.g.dk_src[row + l] + p.g.dqC[row + l];
   const float dk1 = p.g.dk_src[row + l + 64] + p.g.dqC[row + l + 64];
+  const float ru = norm2(u0, u1);
+  const float rk = norm2(k0, k1);
   const float dgam = wave_sum(u0 * dx0 + u1 * dx1 + h0 * dv0 + h1 * dv1);
   const float ud = wave_sum(du0 * u0 + du1 * u1);
   const float kd = wave_sum(dk0 * k0 + dk1 * k1);
