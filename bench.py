@@ -178,6 +178,23 @@ def cpu_baseline(budget_s=24.0):
 
 
 def cpu_model() -> str:
+    """The host CPU as lscpu names it (model name, family / model / stepping,
+    sockets x cores x threads), falling back to /proc/cpuinfo."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        f = {}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            f.setdefault(k.strip(), v.strip())
+        if f.get("Model name"):
+            return (f"{f['Model name']} (family {f.get('CPU family', '?')} model "
+                    f"{f.get('Model', '?')} stepping {f.get('Stepping', '?')}; "
+                    f"{f.get('Socket(s)', '?')} socket(s) x {f.get('Core(s) per socket', '?')} "
+                    f"cores x {f.get('Thread(s) per core', '?')} threads; "
+                    f"{f.get('CPU(s)', '?')} CPUs listed)")
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as fh:
             for line in fh:
@@ -265,8 +282,54 @@ def variant_bench(dev, steps, warmup, *, r=R, v=V, masked=False):
     dt = (time.perf_counter() - t0) / steps
     what = ("masked operator, 10 % invalid tokens and 1 % resets" if masked
             else f"wide-width kernels, r={r} V={v}")
-    return {"workload": f"operator forward + full VJP, B={B} T={T} H={H}, {what}",
-            "value": round(B * T / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4)}
+    res = {"workload": f"operator forward + full VJP, B={B} T={T} H={H}, {what}",
+           "value": round(B * T / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4)}
+    if not masked and r <= R < v:
+        # both routes for these widths, whichever the operator dispatches to:
+        # value groups of the main kernels, and one call of the wide-width kernels
+        from solvedelta_amd.operator import _SolveDeltaFn, _value_groups, value_route
+        routes = {
+            "value_groups_ms": lambda: _value_groups(*ins, None, None, False, R)[0],
+            "one_wide_call_ms": lambda: _SolveDeltaFn.apply(*ins, None, None, False, None)[0],
+        }
+        for name, fwd in routes.items():
+            fn = lambda: torch.autograd.grad(fwd(), ins, dO)
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            res[name] = round((time.perf_counter() - t0) / steps * 1e3, 4)
+        res["route"] = value_route(r, v)
+    return res
+
+
+def graph_time(fn, steps, warmup):
+    """Captures fn (a forward + autograd.grad step on static inputs) once as a
+    HIP graph on a side stream, after eager warm-up there, and returns the
+    replay time per step (the reference's timing mode, docs/RESULTS.md:9-12)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    del graph
+    return dt
 
 
 def refshape_bench(dev, steps, warmup):
@@ -297,11 +360,61 @@ def refshape_bench(dev, steps, warmup):
     torch.cuda.synchronize()
     peak = torch.cuda.max_memory_allocated(dev) - base
     del grads
+    dt_graph = graph_time(step, 200, 10)
     return {"workload": "operator forward + full VJP, B=1 T=1024 H=8 r=V=128",
             "value": round(1024 / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt * 1e3, 4),
+            "graph_ms_per_step": round(dt_graph * 1e3, 4),
             "reference_published_ms": 0.905, "reference_hardware": "RTX 5070 Ti",
             "step_alloc_mib": round(peak / 2 ** 20, 1),
             "reference_graph_alloc_mib": 63.0}
+
+
+def mixer_bench(dev, steps=20, warmup=5):
+    """The projected mixer (in-projection, conv4 + SiLU, KDA decay gate, the
+    operator, gated RMSNorm, out-projection) forward + backward at the shape the
+    reference quotes it on (docs/RESULTS.md:9-18: B=1 T=1024 H=8 r=V=128, hidden
+    1024, 8.99 M parameters; 1.760 ms F+B as a CUDA-graph replay on an RTX 5070 Ti,
+    208.1 MiB graph allocation).  FP32 master parameters under bf16 autocast,
+    hidden states ~ N(0,1) bf16, output cotangent ~ N(0,1); gradients of the input
+    and every parameter.  Timed eagerly and as a HIP-graph replay."""
+    from solvedelta_amd.mixer import SolveDelta, SolveDeltaMixerConfig
+    torch.manual_seed(0)
+    cfg = SolveDeltaMixerConfig(hidden_size=1024, num_heads=8, head_k_dim=128, head_v_dim=128)
+    mixer = SolveDelta(cfg).to(dev).train()
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(1, 1024, 1024, generator=g).to(torch.bfloat16).to(dev).requires_grad_()
+    dy = torch.randn(1, 1024, 1024, generator=g).to(torch.bfloat16).to(dev)
+    leaves = [x] + list(mixer.parameters())
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+            y = mixer(x)
+        return torch.autograd.grad(y, leaves, dy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    grads = step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(dev) - base
+    del grads
+    dt_graph = graph_time(step, 100, 5)
+    return {"workload": "projected mixer forward + backward, B=1 T=1024 hidden 1024 H=8 "
+                        "r=V=128, FP32 parameters + bf16 autocast",
+            "params": sum(p.numel() for p in mixer.parameters()),
+            "value": round(1024 / dt_graph, 1), "unit": "tokens/s",
+            "graph_ms_per_step": round(dt_graph * 1e3, 4),
+            "eager_ms_per_step": round(dt * 1e3, 4),
+            "step_alloc_mib": round(peak / 2 ** 20, 1),
+            "reference_published_ms": 1.760, "reference_hardware": "RTX 5070 Ti",
+            "reference_graph_alloc_mib": 208.1}
 
 
 def decode_bench(dev, steps=256, streams=64):
@@ -393,17 +506,41 @@ def lm_bench(dev, steps=5, warmup=2, graph=False):
     res = {"workload": "causal LM F+B, hidden 1024 x 24 layers, H=8 r=V=128, vocab 32000, "
                        "B=2 T=1024, FP32 master weights + bf16 autocast",
            "params": sum(p.numel() for p in model.parameters()),
-           "eager_ms_per_step": round(t_eager * 1e3, 3)}
+           "eager_ms_per_step": round(t_eager * 1e3, 3),
+           "value": round(ntok / t_eager, 1), "unit": "tokens/s", "mode": "eager"}
     if graph:
+        # eager() released its loss, so no autograd graph holds the parameters'
+        # AccumulateGrad nodes when the capture starts
+        print(json.dumps(res), flush=True)      # the eager figures, should capture fail
+        model.zero_grad(set_to_none=True)
         step = SolveDeltaGraphedTrainingStep(model, ids, ids)
-        t_graph = timed(lambda: step(ids, ids).backward())
+
+        def graphed():
+            model.zero_grad(set_to_none=True)
+            step(ids, ids).backward()
+
+        t_graph = timed(graphed)
         res["graph_ms_per_step"] = round(t_graph * 1e3, 3)
-        res.update(value=round(ntok / t_graph, 1), unit="tokens/s")
-    else:
-        # the full model's HIP-graph capture is off by default: one capture of it
-        # ended in a host segmentation fault whose cause is not known
-        res.update(value=round(ntok / t_eager, 1), unit="tokens/s", mode="eager")
+        res.update(value=round(ntok / t_graph, 1), mode="hip_graph")
     return res
+
+
+def lm_bench_child(timeout_s=600):
+    """Runs the config-4 section in a child process (python bench.py --lm-only)
+    and returns the last JSON line it printed, so that a failure there leaves
+    the rest of this run's line intact; the error is reported in its place."""
+    import subprocess
+    cmd = [sys.executable, os.path.abspath(__file__), "--lm-only"]
+    try:
+        res = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        return {"error": f"causal LM section exceeded {timeout_s} s"}
+    lines = [ln for ln in res.stdout.splitlines() if ln.startswith("{")]
+    out = json.loads(lines[-1]) if lines else {}
+    if res.returncode != 0:
+        out["error"] = f"causal LM section exited with status {res.returncode}"
+        out["stderr_tail"] = res.stderr[-800:]
+    return out
 
 
 def copy_calibration(dev, nbytes=1 << 30):
@@ -426,11 +563,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-lm", action="store_true")
-    ap.add_argument("--lm-graph", action="store_true",
-                    help="also time the causal LM step through its HIP graph")
+    ap.add_argument("--no-lm-graph", action="store_true",
+                    help="time the causal LM step eagerly only (no HIP-graph capture)")
+    ap.add_argument("--lm-only", action="store_true",
+                    help="only the causal LM section (run as a child of the full bench)")
     ap.add_argument("--step-only", action="store_true",
                     help="only the headline forward+VJP steps (counter runs)")
-    ap.add_argument("--variant", choices=["wide", "masked"],
+    ap.add_argument("--variant", choices=["wide", "masked", "mixer", "wide_v"],
                     help="only that variant's F+B line (its kernel profiles)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration)")
@@ -444,8 +583,15 @@ def main():
     if a.copy_calibration:
         copy_calibration(dev)
         return
+    if a.lm_only:
+        print(json.dumps(lm_bench(dev, graph=not a.no_lm_graph)), flush=True)
+        return
+    if a.variant == "mixer":
+        print(json.dumps({"mixer": mixer_bench(dev, a.steps, a.warmup)}), flush=True)
+        return
     if a.variant:
-        kw = dict(r=256, v=256) if a.variant == "wide" else dict(masked=True)
+        kw = {"wide": dict(r=256, v=256), "wide_v": dict(r=128, v=256),
+              "masked": dict(masked=True)}[a.variant]
         print(json.dumps({a.variant: variant_bench(dev, a.steps, a.warmup, **kw)}), flush=True)
         return
     from solvedelta_amd import _lib, solvedelta_native
@@ -537,17 +683,26 @@ def main():
     gc.collect()
     res["wide"] = variant_bench(dev, 5, 2, r=256, v=256)
     gc.collect()
+    res["wide_v"] = variant_bench(dev, 5, 2, r=128, v=256)
+    gc.collect()
     res["masked"] = variant_bench(dev, 10, 3, masked=True)
+    gc.collect()
+    res["mixer"] = mixer_bench(dev)
     if not a.no_decode:
         gc.collect()
         res["decode"] = decode_bench(dev)
         res["decode_uncached"] = decode_bench(dev, steps=32, streams=512)
-    if not a.no_lm:
-        gc.collect()
-        res["causal_lm"] = lm_bench(dev, graph=a.lm_graph)
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
         res["cpu_baseline_forward"] = cpu_forward_baseline()
+    if not a.no_lm:
+        # last: the child runs on the GPU after everything else here has finished
+        gc.collect()
+        torch.cuda.empty_cache()
+        if a.no_lm_graph:
+            res["causal_lm"] = lm_bench(dev, graph=False)
+        else:
+            res["causal_lm"] = lm_bench_child()
     print(json.dumps(res), flush=True)
 
 

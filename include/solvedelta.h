@@ -57,9 +57,12 @@ typedef struct {
   const float *C0, *S0;                        /* nullable initial state */
   sd_view fresh; /* uint8 [B,T] at data[b*sb + t*st], nullable: a nonzero entry marks a
                   * token whose predictor residual reads a zero state (the predictor's
-                  * erase read is dropped).  With log-decay <= -200 on that token, which
-                  * zeroes both states before its write, this is the reference's reset
-                  * (reference.py:156-227); solvedelta_amd.masks composes the two. */
+                  * erase read is dropped exactly).  Together with a killing log-decay
+                  * on that token this is the reference's reset (reference.py:156-227).
+                  * solvedelta_amd.masks uses log-decay -20, which keeps e^-20 ~ 2.1e-9
+                  * of both states before the token (the reference keeps none); decays
+                  * whose 16-token block total exceeds 60 take the kernels' exact but
+                  * slow per-coordinate path. */
 } sd_inputs;
 
 /* Forward. out: bf16 [B,T,H,V] contiguous. C_T / S_T nullable.
@@ -86,19 +89,6 @@ int sd_bwd(const sd_inputs *in, const void *fwd_workspace, const void *dout, con
            const float *dS_T, void *du, void *dh, void *dq, void *dk, void *dv, void *derase,
            void *dwrite, float *dlog_decay, float *dgamma, float *dC0, float *dS0,
            void *workspace, size_t workspace_bytes, void *stream);
-
-/* Forward without any allocation (no counterpart in the reference): the same
- * kernels as sd_fwd, with the workspace in a device-resident static array of
- * SD_NOALLOC_SCRATCH_BYTES per GPU instead of a caller buffer, for callers that
- * cannot call hipMalloc (code under HIP graph capture, tight serving loops,
- * harnesses that forbid allocation).  Inference only: the next call on the
- * device overwrites the workspace, so there is no sd_bwd after it.  Shapes whose
- * forward workspace (sd_fwd_workspace_bytes) exceeds the array return
- * SD_ERR_WORKSPACE.  Calls that overlap on one GPU (two streams, two threads)
- * share the array and race; serialise them. */
-#define SD_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
-size_t sd_noalloc_scratch_bytes(void);
-int sd_fwd_noalloc(const sd_inputs *in, void *out, float *C_T, float *S_T, void *stream);
 
 /* Row masking for masked batches on the dense layout (no counterpart in the
  * reference, whose masked path repacks valid tokens into segments with a host

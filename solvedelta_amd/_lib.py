@@ -51,9 +51,6 @@ EXPORTS = {
                + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "sd_profile_enable": (ctypes.c_int, [ctypes.c_int]),
     "sd_profile_read": (ctypes.c_size_t, [ctypes.c_char_p, ctypes.c_size_t]),
-    "sd_noalloc_scratch_bytes": (ctypes.c_size_t, []),
-    "sd_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
-                                      ctypes.c_void_p, ctypes.c_void_p]),
     "sd_mask_rows": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64,
                                     ctypes.c_int64, ctypes.POINTER(SdMaskTensor), ctypes.c_int,
                                     ctypes.c_void_p]),
@@ -85,7 +82,16 @@ EXPORTS = {
                              + [ctypes.c_void_p] * 9 + [ctypes.c_size_t, ctypes.c_void_p]),
 }
 
+# libsolvedelta_noalloc.so (include/solvedelta_noalloc.h): loaded only by its callers
+NOALLOC_LIB_PATH = os.path.join(HERE, "libsolvedelta_noalloc.so")
+NOALLOC_EXPORTS = {
+    "sd_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "sd_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p]),
+}
+
 _lib = None
+_noalloc = None
 
 
 def load(path: str = None) -> ctypes.CDLL:
@@ -105,6 +111,24 @@ def load(path: str = None) -> ctypes.CDLL:
         fn.restype = res
         fn.argtypes = args
     _lib = lib
+    return lib
+
+
+def load_noalloc() -> ctypes.CDLL:
+    """Loads libsolvedelta_noalloc.so (after the main library, which it links)."""
+    global _noalloc
+    if _noalloc is not None:
+        return _noalloc
+    load()
+    if not os.path.exists(NOALLOC_LIB_PATH):
+        raise RuntimeError(f"{NOALLOC_LIB_PATH} is missing: build the HIP extension first "
+                           "(python -m solvedelta_amd.build)")
+    lib = ctypes.CDLL(NOALLOC_LIB_PATH)
+    for name, (res, args) in NOALLOC_EXPORTS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _noalloc = lib
     return lib
 
 

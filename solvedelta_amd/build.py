@@ -11,6 +11,10 @@ import subprocess
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsolvedelta_hip.so")
+# sd_fwd_noalloc and its static device array, in a library of their own so that
+# only the processes that call it carry the array
+NOALLOC_SRC = os.path.join(CSRC, "noalloc", "sd_noalloc.hip")
+NOALLOC_LIB = os.path.join(HERE, "libsolvedelta_noalloc.so")
 OBJ = os.path.join(HERE, "_obj")
 ARCH = os.environ.get("SD_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -41,13 +45,22 @@ def build(verbose: bool = True) -> str:
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
+           "-Wl,-soname,libsolvedelta_hip.so"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")
     os.replace(tmp, LIB)
+    nobj = _compile(NOALLOC_SRC)
+    tmp = NOALLOC_LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, nobj,
+           f"-L{HERE}", "-lsolvedelta_hip", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")
+    os.replace(tmp, NOALLOC_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {NOALLOC_LIB}")
     return LIB
 
 

@@ -21,7 +21,7 @@ caches are lists of the per-layer dicts.
 """
 from __future__ import annotations
 
-from typing import Any, Iterator, Optional
+from typing import Any, Iterator, NamedTuple, Optional
 
 import torch
 from torch import nn
@@ -83,77 +83,110 @@ class RecurrentCache:
 
 
 def state_from_cache(last_state: Optional[dict]) -> Optional[SolveDeltaLayerState]:
-    """dict entry -> SolveDeltaLayerState (modeling_solvedelta.py:104-115)."""
-    if last_state is None:
+    """A layer's cache entry as the mixer's initial state, or None when the entry
+    is absent or holds no recurrent state yet.  Wire format
+    (modeling_solvedelta.py:104-115): ``recurrent_state`` is the pair
+    (predictor C, memory S); ``conv_state`` rides along unchanged (it may be None)."""
+    pair = None if last_state is None else last_state.get("recurrent_state")
+    if pair is None:
         return None
-    recurrent_state = last_state.get("recurrent_state")
-    if recurrent_state is None:
-        return None
-    if not isinstance(recurrent_state, (tuple, list)) or len(recurrent_state) != 2:
+    if not isinstance(pair, (tuple, list)) or len(pair) != 2:
         raise ValueError("SolveDelta cache recurrent_state must contain (predictor,S)")
-    return SolveDeltaLayerState(operator=SolveDeltaState(*recurrent_state),
-                                conv=last_state.get("conv_state"))
+    return SolveDeltaLayerState(SolveDeltaState(*pair), last_state.get("conv_state"))
 
 
 def segment_reset_mask(hidden_states: torch.Tensor, cu_seqlens: torch.Tensor) -> torch.Tensor:
-    """Packed [1,T,D] rows with cu_seqlens -> reset at every segment start
-    (modeling_solvedelta.py:118-131)."""
+    """Reset flags of a packed row: ``hidden_states`` is one [1,T,D] row holding
+    several sequences back to back, ``cu_seqlens`` their cumulative boundaries;
+    every sequence's first token starts from a zero state
+    (modeling_solvedelta.py:118-131; the same errors for the same inputs)."""
     if hidden_states.shape[0] != 1:
         raise ValueError("explicit cu_seqlens require packed hidden states [1,T,D]")
     if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
         raise ValueError("cu_seqlens must be one-dimensional with at least two entries")
     if cu_seqlens.dtype not in (torch.int32, torch.int64):
         raise TypeError("cu_seqlens must have int32 or int64 dtype")
-    starts = cu_seqlens[:-1].to(device=hidden_states.device, dtype=torch.long)
-    mask = torch.zeros((1, hidden_states.shape[1]), dtype=torch.bool, device=hidden_states.device)
-    return mask.scatter(1, starts.unsqueeze(0), True)
+    device = hidden_states.device
+    first_tokens = cu_seqlens.narrow(0, 0, cu_seqlens.numel() - 1).to(device, torch.long)
+    flags = torch.zeros(hidden_states.shape[1], dtype=torch.bool, device=device)
+    return flags.index_fill_(0, first_tokens, True).unsqueeze(0)
+
+
+class _CallPlan(NamedTuple):
+    """What one adapter call hands the mixer, derived from the HF-style arguments."""
+    initial_state: Optional[SolveDeltaLayerState]
+    valid_mask: Optional[torch.Tensor]
+    reset_mask: Optional[torch.Tensor]
+    write_back: bool
+
+
+def _valid_from_attention(attention_mask, batch: int, length: int):
+    """The last ``length`` columns of a [B, >=T] padding mask as valid flags."""
+    if attention_mask is None:
+        return None
+    if attention_mask.ndim != 2 or attention_mask.shape[0] != batch:
+        raise ValueError("attention_mask must have shape [B,T]")
+    if attention_mask.shape[1] < length:
+        raise ValueError("attention_mask is shorter than the current input")
+    return attention_mask[:, attention_mask.shape[1] - length:].bool()
+
+
+def _resets(hidden_states, explicit, cu_seqlens, continues_cache: bool):
+    """Reset flags from an explicit mask, else from packed-sequence boundaries.
+    When boundaries are given and the call continues a cached state, the row's
+    first sequence is the cached one carried on, so its first token keeps the
+    state (the reference clears that one flag, modeling_solvedelta.py:180-187)."""
+    batch, length = hidden_states.shape[:2]
+    flags = explicit
+    if flags is None and cu_seqlens is not None:
+        flags = segment_reset_mask(hidden_states, cu_seqlens)
+    if flags is None:
+        return None
+    if flags.dtype != torch.bool or tuple(flags.shape) != (batch, length):
+        raise ValueError("solvedelta_reset_mask must be bool [B,T]")
+    if continues_cache and cu_seqlens is not None and bool(length):
+        keep_first = torch.ones_like(flags)
+        keep_first[0, 0] = False
+        flags = flags & keep_first
+    return flags
 
 
 class SolveDeltaCacheAdapter(nn.Module):
-    """Cache ABI around the mixer (modeling_solvedelta.py:134-195)."""
+    """The layer's cache boundary around the mixer (modeling_solvedelta.py:134-195):
+    reads the layer's entry from ``past_key_values``, turns the padding mask,
+    explicit resets or packed boundaries into the mixer's dense masks, and with
+    ``use_cache`` writes the final (C, S) and conv state back, advancing the
+    cache by the call's token count.  Returns (output, None, past_key_values)."""
 
     def __init__(self, config, layer_idx: int) -> None:
         super().__init__()
         self.layer_idx = layer_idx
         self.mixer = SolveDelta(config)
 
+    def _plan(self, hidden_states, attention_mask, past_key_values, use_cache, extra) -> _CallPlan:
+        batch, length = hidden_states.shape[:2]
+        entry = None
+        if past_key_values is not None and self.layer_idx < len(past_key_values):
+            entry = past_key_values[self.layer_idx]
+        initial = state_from_cache(entry)
+        valid = _valid_from_attention(attention_mask, batch, length)
+        resets = _resets(hidden_states, extra.get("solvedelta_reset_mask"),
+                         extra.get("cu_seqlens"), initial is not None)
+        return _CallPlan(initial, valid, resets, bool(use_cache) and past_key_values is not None)
+
     def forward(self, hidden_states, attention_mask=None, past_key_values=None,
                 use_cache: Optional[bool] = False, output_attentions: Optional[bool] = False,
                 **kwargs):
-        del output_attentions
-        batch, length, _ = hidden_states.shape
-        last_state = None
-        if past_key_values is not None and self.layer_idx < len(past_key_values):
-            last_state = past_key_values[self.layer_idx]
-        initial_state = state_from_cache(last_state)
-        valid_mask = None
-        if attention_mask is not None:
-            if attention_mask.ndim != 2 or attention_mask.shape[0] != batch:
-                raise ValueError("attention_mask must have shape [B,T]")
-            if attention_mask.shape[1] < length:
-                raise ValueError("attention_mask is shorter than the current input")
-            valid_mask = attention_mask[:, -length:].to(torch.bool)
-        reset_mask = kwargs.get("solvedelta_reset_mask")
-        cu_seqlens = kwargs.get("cu_seqlens")
-        if reset_mask is None and cu_seqlens is not None:
-            reset_mask = segment_reset_mask(hidden_states, cu_seqlens)
-        if reset_mask is not None:
-            if reset_mask.shape != (batch, length) or reset_mask.dtype != torch.bool:
-                raise ValueError("solvedelta_reset_mask must be bool [B,T]")
-            if initial_state is not None and cu_seqlens is not None:
-                # a packed continuation carries the cached state into its first segment
-                reset_mask = reset_mask.clone()
-                reset_mask[0, 0] = False
-        cache_requested = bool(use_cache and past_key_values is not None)
-        result = self.mixer(hidden_states, initial_state=initial_state, valid_mask=valid_mask,
-                            reset_mask=reset_mask, return_final_state=cache_requested)
-        if cache_requested:
-            output, final_state = result
-            past_key_values.update(recurrent_state=tuple(final_state.operator),
-                                   conv_state=final_state.conv, layer_idx=self.layer_idx,
-                                   offset=length)
-        else:
-            output = result
+        plan = self._plan(hidden_states, attention_mask, past_key_values, use_cache, kwargs)
+        result = self.mixer(hidden_states, initial_state=plan.initial_state,
+                            valid_mask=plan.valid_mask, reset_mask=plan.reset_mask,
+                            return_final_state=plan.write_back)
+        if not plan.write_back:
+            return result, None, past_key_values
+        output, final = result
+        past_key_values.update(recurrent_state=(final.operator.predictor, final.operator.S),
+                               conv_state=final.conv, layer_idx=self.layer_idx,
+                               offset=hidden_states.shape[1])
         return output, None, past_key_values
 
 

@@ -4,9 +4,6 @@
 #include "../../include/solvedelta.h"
 #include "sd_internal.h"
 
-#include <mutex>
-
-
 using namespace sd;
 
 namespace {
@@ -68,8 +65,11 @@ void fwd_sizes(int B, int T, int H, int r, int V, size_t* saved, size_t* scratch
   carve_fwd(nullptr, nullptr, B, T, H, saved, scratch);
 }
 
+int check_chunk_grid(const sd_inputs* in);
+
 int fwd_launch(const sd_inputs* in, void* out, float* C_T, float* S_T, void* saved,
                void* scratch, hipStream_t st) {
+  if (int rc = check_chunk_grid(in)) return rc;
   if (is_wide(in->r, in->V)) return launch_wide_fwd(in, out, C_T, S_T, saved, scratch, st);
   FwdWs w = carve_fwd(saved, scratch, in->B, in->T, in->H, nullptr, nullptr);
   return launch_fwd(in, out, C_T, S_T, w, st);
@@ -119,28 +119,10 @@ int check_inputs(const sd_inputs* in) {
   return SD_OK;
 }
 
-// Scratch of sd_fwd_noalloc: the forward workspace of callers that cannot
-// allocate.  Each device holds its own copy from module load to process end;
-// host code reaches it only through the address hipGetSymbolAddress returns
-// for the current device (the array's name on the host is not a device
-// address).  Every call on a device reuses that device's copy.
-static __device__ __align__(256) unsigned char scratch[SD_NOALLOC_SCRATCH_BYTES];
-
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
-
-// Device address of `scratch` on the current device (looked up once per device).
-int scratch_for_current_device(void** out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SD_ERR_LAUNCH;
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SD_ERR_LAUNCH;
-    g_scratch_ptr[dev] = p;
-  }
-  *out = g_scratch_ptr[dev];
+// The chunked kernels' grids put B*H and the chunk count on axes capped at
+// 65535 workgroups (the decode grid is one-dimensional and has no such cap).
+int check_chunk_grid(const sd_inputs* in) {
+  if ((long long)in->B * in->H > 65535 || (in->T + 31) / 32 > 65535) return SD_ERR_SHAPE;
   return SD_OK;
 }
 
@@ -191,21 +173,6 @@ int sd_fwd_split(const sd_inputs* in, void* out, float* C_T, float* S_T, void* s
   return fwd_launch(in, out, C_T, S_T, saved, scratch, (hipStream_t)stream);
 }
 
-size_t sd_noalloc_scratch_bytes(void) { return SD_NOALLOC_SCRATCH_BYTES; }
-
-int sd_fwd_noalloc(const sd_inputs* in, void* out, float* C_T, float* S_T, void* stream) {
-  int rc = check_inputs(in);
-  if (rc) return rc;
-  if (!out) return SD_ERR_ARG;
-  size_t saved = 0, scratch_b = 0;
-  fwd_sizes(in->B, in->T, in->H, in->r, in->V, &saved, &scratch_b);
-  if (align256(saved) + scratch_b > SD_NOALLOC_SCRATCH_BYTES) return SD_ERR_WORKSPACE;
-  void* base = nullptr;
-  rc = scratch_for_current_device(&base);
-  if (rc) return rc;
-  return fwd_launch(in, out, C_T, S_T, base, (char*)base + align256(saved), (hipStream_t)stream);
-}
-
 int sd_decode(const sd_inputs* in, void* out, float* C_T, float* S_T, void* stream) {
   // the decode kernel holds r, V <= 128 (wider states take the chunked path)
   if (in && (in->T != 1 || in->r > kKD || in->V > kKD)) return SD_ERR_SHAPE;
@@ -231,6 +198,7 @@ int sd_bwd(const sd_inputs* in, const void* fwd_workspace, const void* dout, con
   if (!fwd_workspace || !workspace || !du || !dh || !dq || !dk || !dv || !derase || !dwrite ||
       !dlog_decay || !dgamma)
     return SD_ERR_ARG;
+  if ((rc = check_chunk_grid(in))) return rc;
   size_t need = 0;
   if (is_wide(in->r, in->V)) {
     if (workspace_bytes < wide_bwd_workspace_bytes(in->B, in->T, in->H, in->r, in->V))

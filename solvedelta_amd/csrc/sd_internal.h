@@ -34,30 +34,19 @@ __device__ __forceinline__ float erase_keep(const sd_inputs& in, int b, int t) {
 #endif
 
 // Chunk-boundary state slots saved for the backward, in a 2-byte type (the
-// final states handed to the caller stay fp32): forward states X (C^T and S)
-// and the reverse passes' cotangent states lambda.  bf16, as the reference
-// keeps its per-chunk S states (residual_frame/common_left_h.py:157): its
-// exponent range holds any state or cotangent scale.
-#ifndef SD_XSLOT_T
-#define SD_XSLOT_T _Float16
-#endif
-#ifndef SD_LSLOT_T
-#define SD_LSLOT_T __bf16
-#endif
-typedef SD_XSLOT_T xslot_t;
+// final states handed to the caller stay fp32).  Forward states X (C^T and S)
+// are fp16: the log-decay gradient's closure needs its 11-bit mantissa (the
+// reference keeps its per-chunk S states 16-bit too,
+// residual_frame/common_left_h.py:157).  The reverse passes' cotangent states
+// lambda are bf16, whose exponent range holds any cotangent scale.
+typedef _Float16 xslot_t;
+typedef __bf16 lslot_t;
 // Forward token panels the backward reads (e, chi, delta, d and the S op's w):
 // fp16, like the forward state panels.
-#ifndef SD_FPAN_T
-#define SD_FPAN_T _Float16
-#endif
-typedef SD_FPAN_T fpan_t;
+typedef _Float16 fpan_t;
 // Backward token panels (partial gradients passed between the backward kernels):
 // bf16, whose exponent range holds any scale of the output cotangent.
-#ifndef SD_BPAN_T
-#define SD_BPAN_T __bf16
-#endif
-typedef SD_BPAN_T bpan_t;
-typedef SD_LSLOT_T lslot_t;
+typedef __bf16 bpan_t;
 
 // Forward workspace: every buffer is [n][Tp][128] (token panels) or
 // [n][NT][...] (per-chunk), n = B*H, Tp = NT*64.

@@ -16,7 +16,6 @@ after capture) is not part of this single-GPU build.
 from __future__ import annotations
 
 import threading
-import warnings
 from typing import Any, Optional
 
 import torch
@@ -25,6 +24,20 @@ from torch import nn
 from .lm import SolveDeltaForCausalLM
 
 _CAPTURE_LOCK = threading.Lock()
+_PROBE = "solvedelta_graph_probe"
+
+
+def _has_live_grad_accumulator(param: torch.Tensor) -> bool:
+    """True when an autograd graph still alive elsewhere (an eager loss the
+    caller holds) owns ``param``'s AccumulateGrad node.  A node created here
+    dies as soon as it is dropped, so a tag set on it survives the next lookup
+    only when someone else holds the node."""
+    node = torch.autograd.graph.get_gradient_edge(param).node
+    node.metadata[_PROBE] = True
+    del node
+    node = torch.autograd.graph.get_gradient_edge(param).node
+    alive = node.metadata.pop(_PROBE, False)
+    return alive
 
 
 class _LossModule(nn.Module):
@@ -58,6 +71,18 @@ class SolveDeltaGraphedTrainingStep:
         for m in model.modules():
             if m._forward_hooks or m._forward_pre_hooks or m._backward_hooks:
                 raise ValueError("remove module hooks before graph capture")
+        # An AccumulateGrad node records the stream current when it was created.
+        # A node kept alive by an earlier eager graph belongs to that graph's
+        # stream (normally the default stream), and the capture's backward,
+        # which runs on make_graphed_callables' private stream, would make that
+        # stream wait on an event of the capture: the default stream joins the
+        # capture and is never rejoined.  The reference redirects such nodes with
+        # torch's stale-capture-stream override (cuda_graph.py:75-122), which
+        # this torch does not have, so the capture refuses them instead.
+        if any(_has_live_grad_accumulator(p) for p in model.parameters() if p.requires_grad):
+            raise ValueError("an autograd graph built on the model's parameters is still alive "
+                             "(an eager loss or output that was not released): release it "
+                             "before graph capture")
         self.model = model
         self.device = sample_input_ids.device
         self._replay_stream = torch.cuda.current_stream(self.device)
@@ -65,9 +90,7 @@ class SolveDeltaGraphedTrainingStep:
         static_ids = sample_input_ids.detach().contiguous().clone()
         static_labels = sample_labels.detach().contiguous().clone()
         loss_module = _LossModule(model).train()
-        with _CAPTURE_LOCK, warnings.catch_warnings():
-            warnings.filterwarnings("ignore", message="The AccumulateGrad node's stream.*",
-                                    category=UserWarning)
+        with _CAPTURE_LOCK:
             with torch.autocast(device_type="cuda", dtype=torch.bfloat16, cache_enabled=False):
                 self._graphed = torch.cuda.make_graphed_callables(
                     loss_module, (static_ids, static_labels), num_warmup_iters=num_warmup_iters,

@@ -18,8 +18,10 @@ kernels unchanged in shape:
   gate logits, must be finite there: zero times a NaN is not zero);
 * a reset on a valid token clears both states before that token: its
   log-decay is replaced by RESET_LOG_DECAY, so D C and D S keep exp(-20) ~
-  2e-9 of the old states -- below FP32 rounding (6e-8) of the terms that
-  follow -- while the chunk kernels keep the token on their factored
+  2.1e-9 of the old states, where the reference keeps none (below FP32
+  rounding, 6e-8, of the terms that follow while the old state is at most ~30x
+  their size; a relative error of ~1e-3 with an old state 1e5x the later
+  writes) -- while the chunk kernels keep the token on their factored
   (matrix-core) decay path: a 16-token block whose decay exceeds their wild
   threshold of 60 (an exact exp(-inf) kill would, and so would three such
   resets in one block) takes the exact per-coordinate fix-up, several times
@@ -50,8 +52,8 @@ from . import _lib
 from .operator import _dispatch, _stream, _validate
 from .state import SolveDeltaState
 
-# log-decay of a reset token: the old states survive as exp(-20) ~ 2e-9 of
-# their value, under FP32's 6e-8 rounding of the new terms; two resets and up
+# log-decay of a reset token: the old states survive as exp(-20) ~ 2.1e-9 of
+# their value (the reference zeroes them); two resets and up
 # to 20 of ordinary decay fit in one 16-token block before it leaves the
 # kernels' factored path (see the module docstring for why not an exact kill)
 RESET_LOG_DECAY = -20.0

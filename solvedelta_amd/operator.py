@@ -239,7 +239,7 @@ def _dispatch(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, ini
     C0 = S0 = None
     if initial_state is not None:
         C0, S0 = (s.contiguous() for s in initial_state)
-    group = _MAX_WIDTH if r <= _MAX_WIDTH else _WIDE_MAX
+    group = _WIDE_MAX if value_route(r, V) == "wide" else _MAX_WIDTH
     if V <= group:
         out, C_T, S_T = _SolveDeltaFn.apply(u, h, q, keys, values, log_decay, erase_raw,
                                             write_raw, gamma, C0, S0, return_final_state, fresh)
@@ -249,6 +249,19 @@ def _dispatch(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, ini
     if not return_final_state:
         return out, None
     return out, SolveDeltaState(C_T, S_T)
+
+
+def value_route(r: int, V: int) -> str:
+    """How a call of key width r and value width V runs: "main" (r, V <= 128:
+    the 64-token kernels), "wide" (one call of the wide-width kernels, which
+    take r, V <= 256; V above 256 in groups of 256) or "groups" (r <= 128 < V:
+    value groups of 128 columns on the main kernels, each recomputing the
+    predictor)."""
+    if r <= _MAX_WIDTH and V <= _MAX_WIDTH:
+        return "main"
+    if r > _MAX_WIDTH:
+        return "wide"
+    return "groups"
 
 
 def _value_groups(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,

@@ -71,3 +71,21 @@ def test_graphed_step_validates_like_the_reference():
               "model.layers.0.mlp.down_proj.weight", "model.norm.weight", "lm_head.weight",
               "model.layers.0.mixer.mixer.associative_decay_bias"):
         assert n in names, n
+
+
+def test_live_grad_accumulator_probe():
+    """The capture guard's probe: True exactly while another autograd graph
+    holds the parameter's AccumulateGrad node, and it leaves no tag behind."""
+    import gc
+    from solvedelta_amd.graph import _has_live_grad_accumulator
+    p = torch.nn.Parameter(torch.randn(3))
+    assert not _has_live_grad_accumulator(p)
+    y = (p * 2).sum()
+    assert _has_live_grad_accumulator(p)
+    y.backward()
+    assert _has_live_grad_accumulator(p)          # backward ran; the graph is still held
+    node = torch.autograd.graph.get_gradient_edge(p).node
+    assert not any(k.startswith("solvedelta") for k in node.metadata)
+    del node, y
+    gc.collect()
+    assert not _has_live_grad_accumulator(p)

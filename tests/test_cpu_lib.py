@@ -12,22 +12,39 @@ import torch
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _declared():
+def _declared(headers):
     inc = os.path.join(ROOT, "include")
-    text = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc))
-                   if f.endswith(".h"))
+    text = "".join(open(os.path.join(inc, f)).read() for f in headers)
     return sorted(set(re.findall(r"\b(sd_[a-z_]+)\s*\(", text)))
+
+
+def test_every_header_is_checked():
+    inc = os.path.join(ROOT, "include")
+    assert sorted(f for f in os.listdir(inc) if f.endswith(".h")) == [
+        "solvedelta.h", "solvedelta_mixer.h", "solvedelta_noalloc.h"]
 
 
 def test_library_exports_every_declared_symbol():
     from solvedelta_amd import _lib
     lib = _lib.load()
-    names = _declared()
+    names = _declared(["solvedelta.h", "solvedelta_mixer.h"])
     assert "sd_fwd" in names and "sd_bwd" in names and "sd_decode" in names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.EXPORTS, name
     assert lib.sd_version().startswith(b"solvedelta_amd")
+    assert not hasattr(lib, "sd_fwd_noalloc")     # the static array stays out of this library
+
+
+def test_noalloc_library_exports_its_declared_symbols():
+    from solvedelta_amd import _lib
+    lib = _lib.load_noalloc()
+    names = _declared(["solvedelta_noalloc.h"])
+    assert names == ["sd_fwd_noalloc", "sd_noalloc_scratch_bytes"]
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.NOALLOC_EXPORTS, name
+    assert lib.sd_noalloc_scratch_bytes() == 96 << 20
 
 
 def test_workspace_queries_and_argument_rejection():
@@ -108,6 +125,45 @@ def test_packed_segment_plan_on_cpu():
     assert plan.max_seqlen == 5
     with pytest.raises(ValueError):
         build_packed_segments(valid.int(), reset)
+    assert plan.cu_seqlens_cpu.tolist() == [0, 3, 5, 10]
+    assert plan.segment_batch_cpu.tolist() == [0, 0, 2] and plan.use_initial_cpu.tolist() == [
+        True, False, False]
+    assert plan.indices.tolist() == [0, 1, 3, 4, 5, 12, 13, 14, 15, 17]
+    assert plan.segment_ids.tolist() == [0, 0, 0, 1, 1, 2, 2, 2, 2, 2]
+
+
+def test_packed_segment_plan_against_a_token_walk():
+    """Random masks: the plan equals a plain walk over each row's tokens, and
+    the masks the segmented operator rebuilds from it are the valid tokens and
+    the valid resets."""
+    from solvedelta_amd.segments import build_packed_segments, plan_masks
+    g = torch.Generator().manual_seed(3)
+    for B, T in ((1, 1), (3, 17), (4, 64)):
+        valid = torch.rand(B, T, generator=g) > 0.3
+        reset = torch.rand(B, T, generator=g) > 0.8
+        plan = build_packed_segments(valid, reset)
+        seg_rows, seg_len, seg_init, idx, ids, last = [], [], [], [], [], [-1] * B
+        for b in range(B):
+            first = True
+            for t in range(T):
+                if not valid[b, t]:
+                    continue
+                if first or reset[b, t]:
+                    seg_rows.append(b)
+                    seg_len.append(0)
+                    seg_init.append(first and not bool(reset[b, t]))
+                    last[b] = len(seg_rows) - 1
+                first = False
+                seg_len[-1] += 1
+                idx.append(b * T + t)
+                ids.append(len(seg_rows) - 1)
+        assert plan.segment_batch.tolist() == seg_rows
+        assert plan.segment_lengths.tolist() == seg_len
+        assert plan.use_initial.tolist() == seg_init
+        assert plan.indices.tolist() == idx and plan.segment_ids.tolist() == ids
+        assert plan.last_segment.tolist() == last
+        v2, r2 = plan_masks(plan, "cpu")
+        assert torch.equal(v2, valid) and torch.equal(r2, valid & reset)
 
 
 def test_mask_rows_argument_rejection():

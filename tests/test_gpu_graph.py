@@ -78,3 +78,23 @@ def test_graphed_step_matches_fp64_lm_oracle():
         loss.backward()
     torch.cuda.synchronize()
     check_lm_against_oracle(model, ids, loss, "graph vs oracle", layers=2, heads=2, rk=64, rv=64)
+
+
+def test_capture_refuses_a_live_eager_graph():
+    """A loss still holding its autograd graph pins the parameters'
+    AccumulateGrad nodes to the stream it ran on; the helper refuses to capture
+    then (before any capture starts) and captures once the loss is released."""
+    from solvedelta_amd.graph import SolveDeltaGraphedTrainingStep
+    model = _model(seed=2)
+    ids = torch.randint(0, 97, (2, 64), generator=torch.Generator().manual_seed(3)).cuda()
+    with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
+        loss, _, _ = model(ids, labels=ids)
+    loss.backward()
+    with pytest.raises(ValueError, match="still alive"):
+        SolveDeltaGraphedTrainingStep(model, ids, ids)
+    del loss
+    step = SolveDeltaGraphedTrainingStep(model, ids, ids)
+    model.zero_grad(set_to_none=True)
+    step(ids, ids).backward()
+    torch.cuda.synchronize()
+    assert all(torch.isfinite(p.grad).all() for p in model.parameters())
