@@ -74,9 +74,8 @@ BYTES_PER_CHUNK = {
     "k_grad_s": (6 * _H + _P + 3 * _S) + (3 * _H + _P),      # dw,w,d,e,chi,dO,decay,X0,XC,lam -> de,dchi,dd,dg
     "k_src_bwd": (11 * _H) + (7 * _H),                       # 6 inputs,delta,de,dchi,dw,dd -> 4 grads,ddelta,du,dk
     "k_bprep_c": (_A + 5 * _H + _P) + (_P + 6 * _H + _A),    # A,u,k,K,dd,ddelta,decay -> dU,Wk,kh,uh,At1,B1,Ant,P'
-    "k_grad_c": (6 * _H + _P + 3 * _S + _A + _P) + (3 * _H + _P),
-    # dw,delta,dd,kh,uh,d,decay,X0,XC,lam,P',dg -> dx,dk,dq,dg
-    "k_final": (9 * _H) + 3 * _H,                            # u,h,k,dx,dw,du,dk,dkC,dq -> du,dh,dk
+    "k_grad_c": (6 * _H + _P + 3 * _S + _A + _P + 5 * _H) + (3 * _H + _P),
+    # dw,delta,dd,kh,uh,d,decay,X0,XC,lam,P',dg, tail: u,k,h,du_src,dk_src -> du,dk,dh,dg
 }
 
 
@@ -95,8 +94,8 @@ OP_BYTES_PER_TOKEN_HEAD = {
     "k_grad_s": _VEC + 2 * _DEC,                           # dO, log-decay -> dlog_decay
     "k_src_bwd": 6 * _VEC + 4 * _VEC,                      # u, k, q, erase, v, write -> dq, derase, dv, dwrite
     "k_bprep_c": 2 * _VEC + _DEC + _GAM,                   # u, k, log-decay, gamma
-    "k_grad_c": _DEC + _GAM + _DEC,                        # log-decay, gamma -> dlog_decay (add)
-    "k_final": 3 * _VEC + _GAM + 3 * _VEC + _GAM,          # u, h, k, gamma -> du, dh, dk, dgamma
+    "k_grad_c": _DEC + _GAM + _DEC + 3 * _VEC + 3 * _VEC + _GAM,
+    # log-decay, gamma, u, k, h -> dlog_decay (add), du, dk, dh, dgamma
 }
 STATE_BYTES_PER_SEQ = {"state_c_fwd": R * R * 4, "state_s_fwd": R * V * 4,  # C0 / S0 read
                        "state_c_bwd": R * R * 4, "state_s_bwd": R * V * 4}  # dC0 / dS0 write

@@ -81,11 +81,10 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   Carver c{(char*)base};
   BwdWs w;
   // Buffers whose last reader runs before the first writer of another share
-  // its storage (kernel order: bprep_s, state_s, grad_s, src_bwd, bprep_c,
-  // state_c, grad_c, final): the C op's cotangent slots take the S op's (last
-  // read by grad_s), dw_C takes dw_S (last read by src_bwd), grad_c's dk / dx
-  // take de / dchi (last read by src_bwd) and its dq takes the injection panel
-  // B1 (last read by the C reverse pass).
+  // its storage (kernel order: bprep_s, state_s, grad_s, bprep_c (its head
+  // transposes the sources), state_c, grad_c (its tail closes u, k, h, gamma)):
+  // the C op's cotangent slots take the S op's (last read by grad_s) and dw_C
+  // takes dw_S (last read by bprep_c's head).
   w.Ls = c.take<lslot_t>(states);
   w.Lc = w.Ls;
   w.Wk = c.take<__bf16>(panel);
@@ -96,9 +95,6 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   bpan_t** bpanels[] = {&w.dwS, &w.de, &w.dchi, &w.dd, &w.ddelta, &w.du_src, &w.dk_src};
   for (bpan_t** pp : bpanels) *pp = c.take<bpan_t>(panel);
   w.dwC = w.dwS;
-  w.dkC = w.de;
-  w.dxC = w.dchi;
-  w.dqC = w.B1t;
   w.uh = c.take<fpan_t>(panel);
   w.kh = c.take<fpan_t>(panel);
   w.Pp = c.take<float>(n * NT * kBT * kBT);

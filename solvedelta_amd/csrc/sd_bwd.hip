@@ -11,8 +11,9 @@
 //               in-chunk reverse cumulative sum that closes the decay gradient
 //               (k_grad_s writes the S side's log-decay gradient to the output,
 //               k_grad_c adds the C side's).
-// Between the ops k_src_bwd transposes the dual sources (phi, den, e, chi, z)
-// and the q/erase/write/value gates; k_final closes u, k, h and gamma.
+// Between the ops k_src_bwd transposes the dual sources (phi, den, e, chi, z
+// and the q / erase / write / value gates); the C chunk gradient closes with u,
+// k, h and gamma.
 // The closed forms are the ones checked against FP64 autograd in
 // tests/chunk_model.py (Op.backward, sources_bwd, backward_seq).
 #include "sd_common.cuh"
@@ -790,6 +791,79 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   });
 }
 
+// ---------------------------------------------------------------------------
+// Final closure of a four-token group (16-lane row layout, rows i = row16(w, g)):
+// u, k, h and gamma, from the C chunk gradient's dx, dk, dq rows (bf16, in its
+// LDS, row stride KD), the C reverse pass's dw and the sources transpose's
+// partial du / dk.  All of the group's global loads are issued first.
+// ---------------------------------------------------------------------------
+struct FinRows {
+  float u[RQ], k[RQ], h[RQ], dv[RQ], us[RQ], ks[RQ];
+  float gm, xk;
+};
+
+__device__ __forceinline__ void final_load(const BwdParams& p, int b, int hh, long long rowbase,
+                                           int i, int t, FinRows& x) {
+  const int cl = lane_id() & 15, T = p.T;
+  const bool tv = t < T;
+  const int tc = tv ? t : T - 1;
+  ld_row16(brow(p.in.u, b, tc, hh), tv, p.r, x.u);
+  ld_row16(brow(p.in.k, b, tc, hh), tv, p.r, x.k);
+  ld_row16(brow(p.in.h, b, tc, hh), tv, p.r, x.h);
+  x.gm = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                         (long long)tc * p.in.gamma.st +
+                                         (long long)hh * p.in.gamma.sh];
+  // the erase read x = gamma u^ is dropped on fresh tokens: its cotangent dx
+  // reaches neither u nor gamma there
+  x.xk = erase_keep(p.in, b, tc);
+  const unsigned o = (unsigned)((rowbase + (tc - (t - i))) * KD + cl);
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    x.dv[q] = (float)p.g.dwC[o + 16 * q];
+    x.us[q] = (float)p.g.du_src[o + 16 * q];
+    x.ks[q] = (float)p.g.dk_src[o + 16 * q];
+  }
+}
+
+__device__ __forceinline__ void final_close(const BwdParams& p, int b, int hh, int t,
+                                            FinRows& x, const __bf16* dx_row,
+                                            const __bf16* dk_row, const __bf16* dq_row) {
+  const int cl = lane_id() & 15, r = p.r;
+  const bool tv = t < p.T;
+  float dx[RQ], du[RQ], dk[RQ];
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    const int c = cl + 16 * q;
+    dx[q] = x.xk * bf2f(dx_row[c]);
+    du[q] = x.us[q] + bf2f(dk_row[c]) + x.gm * dx[q];
+    dk[q] = x.ks[q] + bf2f(dq_row[c]);
+  }
+  const float ru = l2norm16(x.u);
+  const float rk = l2norm16(x.k);
+  float g = 0.f, ud = 0.f, kd = 0.f;
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    g += x.u[q] * dx[q] + x.h[q] * x.dv[q];
+    ud += du[q] * x.u[q];
+    kd += dk[q] * x.k[q];
+  }
+  const float dgam = row16_sum(g);
+  ud = row16_sum(ud);
+  kd = row16_sum(kd);
+  if (!tv) return;
+  const long long tok = ((long long)b * p.T + t) * p.H + hh;
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    const int c = cl + 16 * q;
+    if (c < r) {
+      p.du[tok * r + c] = f2bf((du[q] - ud * x.u[q]) * ru);
+      p.dk[tok * r + c] = f2bf((dk[q] - kd * x.k[q]) * rk);
+      p.dh[tok * r + c] = f2bf(x.gm * x.dv[q]);
+    }
+  }
+  if (cl == 0) p.dgam[tok] = dgam;
+}
+
 struct GradCSmem {
   ChunkDecay cd;
   float M1[BT * LS];
@@ -891,9 +965,10 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 #pragma unroll
     for (int q = 0; q < PPC; ++q) ppv[q] = *reinterpret_cast<const float4*>(pp + (threadIdx.x + q * CT) * 4);
   }
-  // chunk-uniform output bases, 32-bit lane offsets (keeps addresses out of VGPR pairs)
-  bpan_t* const dx_b = p.g.dxC + rowbase * KD;
-  bpan_t* const dk_b = p.g.dkC + rowbase * KD;
+  // dx and dk stay in the workgroup for the closure tail, rounded to bf16 as the
+  // panels between kernels were: dx into M2 once the applies are done with it,
+  // dk in registers until the dq product has run
+  __bf16 dxr[NB][4], dkr[NB][4];
   // decay cotangent: dg_i = o_i dd_i - u_i dk_i plus the shifted gamma u (.) dx
   // term, closed in registers below (v = dg + xdx, then dg = suffix(v) - xdx)
   float vv[NB][4], xs[NB][4];
@@ -907,19 +982,23 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       const int i = I * BS + r4 + e;
       const float dx = -(__expf(gx_excl(cd, i, c)) * a[I][e] + ap[e]);
       const float dk = __expf(cd.G[BT - 1][c] - cd.G[i][c]) * kl[I][e] + k2[e] - k3[e];
-      const unsigned o = (unsigned)(i * KD + c);
-      dx_b[o] = dx;
-      dk_b[o] = dk;
+      dxr[I][e] = f2bf(dx);
+      dkr[I][e] = f2bf(dk);
       xs[I][e] = Sx[I][e] * dx;
       vv[I][e] = So[I][e] * Sdd[I][e] - Su[I][e] * dk + xs[I][e];
     }
   }
-  __syncthreads();  // every apply has read M1
+  __syncthreads();  // every apply has read M1 and M2
 #pragma unroll
   for (int q = 0; q < PPC; ++q) {
     const int idx = (threadIdx.x + q * CT) * 4;
     *reinterpret_cast<float4*>(&s.M1[(idx / BT) * LS + idx % BT]) = ppv[q];
   }
+  __bf16* const dxl = reinterpret_cast<__bf16*>(s.M2);  // [64][128] bf16 fits M2's 64 x 68 floats
+#pragma unroll
+  for (int I = 0; I < NB; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dxl[(I * BS + r4 + e) * KD + c] = dxr[I][e];
   // dg_i = rowsum + sum_{i' >= i} dg_i' + sum_{i' > i} xdx_i'
   close_decay_column(vv, s.rsum, cb);
   // the C side's part of the log-decay gradient, added to the S side's (written
@@ -939,8 +1018,8 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   }
   __syncthreads();  // P' in M1; PA (dd e^G) staged
   // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
+  f4 dqs[NB];
   {
-    bpan_t* const dq_b = p.g.dqC + rowbase * KD;
     BlkS BX;
     {
       const int kq = (l >> 4) * 8;
@@ -982,54 +1061,27 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
         for (int e = 0; e < 8; ++e) va[e] = s.M1[(I * BS + m) * LS + ks * 32 + kq + e];
         dq = mma3f(split8(va), pw[ks], dq);
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dq_b[(unsigned)((I * BS + r4 + e) * KD + c)] = dq[e];
+      dqs[I] = dq;
     }
   }
-}
-
-// ---------------------------------------------------------------------------
-// Final closure: u, k, h, gamma.  One wave per token.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(NTHREADS) void k_final(BwdParams p) {
-  const int n = blockIdx.y, b = n / p.H, hh = n % p.H;
-  const int t = blockIdx.x * 4 + wave_id();
-  if (t >= p.T) return;
-  const int l = lane_id(), r = p.r;
-  const long long row = ((long long)n * p.Tp + t) * KD;
-  float u0, u1, k0, k1, h0, h1;  // rows loaded before the norms' cross-lane sums
-  ldrow2(p.in.u, b, t, hh, p.T, r, u0, u1);
-  ldrow2(p.in.k, b, t, hh, p.T, r, k0, k1);
-  ldrow2(p.in.h, b, t, hh, p.T, r, h0, h1);
-  const float gm = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
-                                                   (long long)t * p.in.gamma.st +
-                                                   (long long)hh * p.in.gamma.sh];
-  // the erase read x = gamma u^ is dropped on fresh tokens: its cotangent dx
-  // reaches neither u nor gamma there
-  const float xk = erase_keep(p.in, b, t);
-  const float dx0 = xk * p.g.dxC[row + l], dx1 = xk * p.g.dxC[row + l + 64];
-  const float dv0 = p.g.dwC[row + l], dv1 = p.g.dwC[row + l + 64];
-  const float du0 = p.g.du_src[row + l] + p.g.dkC[row + l] + gm * dx0;
-  const float du1 = p.g.du_src[row + l + 64] + p.g.dkC[row + l + 64] + gm * dx1;
-  const float dk0 = p.g.dk_src[row + l] + p.g.dqC[row + l];
-  const float dk1 = p.g.dk_src[row + l + 64] + p.g.dqC[row + l + 64];
-  const float ru = norm2(u0, u1);
-  const float rk = norm2(k0, k1);
-  const float dgam = wave_sum(u0 * dx0 + u1 * dx1 + h0 * dv0 + h1 * dv1);
-  const float ud = wave_sum(du0 * u0 + du1 * u1);
-  const float kd = wave_sum(dk0 * k0 + dk1 * k1);
-  const long long tok = ((long long)b * p.T + t) * p.H + hh;
-  if (l < r) {
-    p.du[tok * r + l] = f2bf((du0 - ud * u0) * ru);
-    p.dk[tok * r + l] = f2bf((dk0 - kd * k0) * rk);
-    p.dh[tok * r + l] = f2bf(gm * dv0);
+  __syncthreads();  // PA, PW and M1 read by every wave: dk and dq take PA's halves
+#pragma unroll
+  for (int I = 0; I < NB; ++I)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s.PA.h[I * BS + r4 + e][c] = dkr[I][e];
+      s.PA.l[I * BS + r4 + e][c] = f2bf(dqs[I][e]);
+    }
+  // closure of u, k, h and gamma: this wave's two four-token groups
+  FinRows f0, f1;
+  final_load(p, b, hh, rowbase, row16(w, 0), t0 + row16(w, 0), f0);
+  final_load(p, b, hh, rowbase, row16(w, 1), t0 + row16(w, 1), f1);
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int i = row16(w, g);
+    final_close(p, b, hh, t0 + i, g ? f1 : f0, dxl + i * KD, s.PA.h[i], s.PA.l[i]);
   }
-  if (l + 64 < r) {
-    p.du[tok * r + l + 64] = f2bf((du1 - ud * u1) * ru);
-    p.dk[tok * r + l + 64] = f2bf((dk1 - kd * k1) * rk);
-    p.dh[tok * r + l + 64] = f2bf(gm * dv1);
-  }
-  if (l == 0) p.dgam[tok] = dgam;
 }
 
 // ---------------------------------------------------------------------------
@@ -1078,7 +1130,6 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   sc.fin = dC0; sc.fin_transposed = 1;
   launch_state("state_c_bwd", sc, n, st);
   SD_LAUNCH("k_grad_c", k_grad_c, chunks, cblk, sizeof(GradCSmem), st, p);
-  SD_LAUNCH("k_final", k_final, rows, blk, 0, st, p);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 

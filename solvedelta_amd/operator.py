@@ -253,15 +253,14 @@ def _dispatch(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, ini
 
 def value_route(r: int, V: int) -> str:
     """How a call of key width r and value width V runs: "main" (r, V <= 128:
-    the 64-token kernels), "wide" (one call of the wide-width kernels, which
-    take r, V <= 256; V above 256 in groups of 256) or "groups" (r <= 128 < V:
-    value groups of 128 columns on the main kernels, each recomputing the
-    predictor)."""
+    the 64-token kernels) or "wide" (the wide-width kernels, which take r, V <=
+    256; V above 256 in groups of 256 columns).  For r <= 128 < V <= 256 one
+    wide call (F+B 1.95 ms at B4 T2048 H8 r=128 V=256 on MI355X) beat two
+    128-column groups on the main kernels, each recomputing the predictor
+    (2.13 ms)."""
     if r <= _MAX_WIDTH and V <= _MAX_WIDTH:
         return "main"
-    if r > _MAX_WIDTH:
-        return "wide"
-    return "groups"
+    return "wide"
 
 
 def _value_groups(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, C0, S0,
