@@ -21,9 +21,10 @@ struct Carver {
 };
 
 // The forward workspace is two regions: `saved` holds what sd_bwd reads (chunk
-// states, inverses, forward token panels, the state passes' key panels, the
-// readout panels and the chunk decay); `scratch` holds the panels only the
-// forward's state passes read (W, U of both ops), free once sd_fwd returns.
+// states, inverses, forward token panels, the output pair P and the chunk
+// decay); `scratch` holds the panels only the forward's state passes read (the
+// decayed keys K^ and W, U of both ops, the readout's Q~), free once sd_fwd
+// returns.  The backward forms K^ and Q~ again from d, chi and u.
 FwdWs carve_fwd(void* saved, void* scratch, int B, int T, int H, size_t* saved_bytes,
                 size_t* scratch_bytes) {
   const size_t n = (size_t)B * H, NT = (T + kBT - 1) / kBT, Tp = NT * kBT;
@@ -39,13 +40,13 @@ FwdWs carve_fwd(void* saved, void* scratch, int B, int T, int H, size_t* saved_b
   w.delta = c.take<fpan_t>(panel);
   w.d = c.take<fpan_t>(panel);
   w.wS = c.take<fpan_t>(panel);
-  w.Kc = c.take<_Float16>(panel);
   w.Gam = c.take<float>(n * NT * kKD);
-  w.Ks = c.take<_Float16>(panel);
-  w.Qs = c.take<_Float16>(panel);
   w.Ps = c.take<_Float16>(n * NT * kBT * kBT);
   if (saved_bytes) *saved_bytes = c.off + 256;
   Carver t{(char*)scratch};
+  w.Kc = t.take<_Float16>(panel);
+  w.Ks = t.take<_Float16>(panel);
+  w.Qs = t.take<_Float16>(panel);
   w.Wc = t.take<_Float16>(panel);
   w.Uc = t.take<float>(panel);
   w.Ws = t.take<_Float16>(panel);
@@ -81,10 +82,11 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   Carver c{(char*)base};
   BwdWs w;
   // Buffers whose last reader runs before the first writer of another share
-  // its storage (kernel order: bprep_s, state_s, grad_s, bprep_c (its head
-  // transposes the sources), state_c, grad_c (its tail closes u, k, h, gamma)):
-  // the C op's cotangent slots take the S op's (last read by grad_s) and dw_C
-  // takes dw_S (last read by bprep_c's head).
+  // its storage (kernel order: bprep_s, state_s, grad_s, src_bwd, bprep_c,
+  // state_c, grad_c (its tail closes u, k, h, gamma)): the C op's cotangent
+  // slots take the S op's (last read by grad_s), dw_C takes dw_S (last read by
+  // src_bwd), and grad_s's de / dchi take the injection panels At1 / B1 (read by
+  // the S reverse pass, written again by bprep_c after src_bwd has read de / dchi).
   w.Ls = c.take<lslot_t>(states);
   w.Lc = w.Ls;
   w.Wk = c.take<__bf16>(panel);
@@ -92,7 +94,10 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.B1t = c.take<__bf16>(panel);
   w.Ant = c.take<__bf16>(panel);
   w.dU = c.take<float>(panel);
-  bpan_t** bpanels[] = {&w.dwS, &w.de, &w.dchi, &w.dd, &w.ddelta, &w.du_src, &w.dk_src};
+  static_assert(sizeof(bpan_t) == sizeof(__bf16), "de / dchi share the bf16 injection panels");
+  w.de = reinterpret_cast<bpan_t*>(w.At1);
+  w.dchi = reinterpret_cast<bpan_t*>(w.B1t);
+  bpan_t** bpanels[] = {&w.dwS, &w.dd, &w.ddelta, &w.du_src, &w.dk_src};
   for (bpan_t** pp : bpanels) *pp = c.take<bpan_t>(panel);
   w.dwC = w.dwS;
   w.uh = c.take<fpan_t>(panel);

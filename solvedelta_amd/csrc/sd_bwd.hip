@@ -228,14 +228,25 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
     // split key panel K^ read as ready-made fragments.
     bf16x8 db[2];
     Frag kf[2];
+    const fpan_t* const dp = p.f.d + rowbase * KD;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       DoutRaw r[8];
+      float kv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r[e] = dout_raw(p, b, t0 + ks * 32 + kq + e, hh, cb * 16 + m);
+      for (int e = 0; e < 8; ++e) {
+        r[e] = dout_raw(p, b, t0 + ks * 32 + kq + e, hh, cb * 16 + m);
+        kv[e] = (float)dp[(ks * 32 + kq + e) * KD + cb * 16 + m];
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) db[ks][e] = (__bf16)dout_val(r[e]);
-      kf[ks] = ldfrag_h(p.f.Ks, kbase + frag_off(cb * 16 + m, ks * 32 + kq, BT));
+      // the decayed keys K^_i = d_i e^{G_C - G_i} of the forward's S pass, formed
+      // again from the saved d (the exponent is <= 0)
+      const int c = cb * 16 + m;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        kv[e] *= __expf(cd.G[BT - 1][c] - cd.G[ks * 32 + kq + e][c]);
+      kf[ks] = split8(kv);
     }
 #pragma unroll
     for (int Jb = 0; Jb < NB; ++Jb) {
@@ -272,7 +283,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
     for (int e = 0; e < 8; ++e) {
       const int i = i0 + e;
       ev[q][e] = (float)p.f.e[(rowbase + i) * KD + c];
-      qv[q][e] = p.f.Qs[rowbase * KD + frag_off(i, c, KD)];
+      qv[q][e] = p.f.chi[(rowbase + i) * KD + c];  // Q~ = chi e^G, scaled below
       d[q][e] = dout_raw(p, b, t0 + i, hh, c);
     }
   }
@@ -298,8 +309,9 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       bf16x8 ah, qh, dh;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        ah[e] = (__bf16)(-ev[q][e] * __expf(cd.G[i0 + e][c]));
-        qh[e] = (__bf16)(float)qv[q][e];    // a transposed bf16 copy of the fp16 panel
+        const float eg = __expf(cd.G[i0 + e][c]);
+        ah[e] = (__bf16)(-ev[q][e] * eg);
+        qh[e] = (__bf16)((float)qv[q][e] * eg);  // Q~ = chi e^G, transposed, bf16
         dh[e] = (__bf16)dout_val(d[q][e]);  // exact in bf16
       }
       const long long ot = cidx * KD * BT + (long long)pc * 8;
@@ -689,7 +701,14 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       }
       bd[ks] = split8(vd);
       bk[ks] = split8(vk);
-      kf[ks] = ldfrag_h(p.f.Kc, kbase + frag_off(cb * 16 + m, ks * 32 + kq, BT));
+      // the C op's decayed keys K^_i = u^_i e^{G_C - G_i} (exponent <= 0), formed
+      // from the normalised u in LDS instead of a saved forward panel
+      float vu[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        vu[e] = s.Uh[ks * 32 + kq + e][cb * 16 + m] *
+                __expf(cd.G[BT - 1][cb * 16 + m] - cd.G[ks * 32 + kq + e][cb * 16 + m]);
+      kf[ks] = split8(vu);
     }
 #pragma unroll
     for (int Jb = 0; Jb < NB; ++Jb) {

@@ -61,11 +61,13 @@ struct FwdWs {
   fpan_t* delta;  // predictor write delta (C-op w)          [n][Tp][128]
   fpan_t* d;      // primal address d = k + C^T k            [n][Tp][128]
   fpan_t* wS;     // S-op w = z - S~^T e                     [n][Tp][128]
-  // transient panels; the forward state passes' MFMA operands W (token-major)
-  // and K (chunk-transposed) are fp16 in fragment order, as are the S readout's
-  // Q~ (token-major) and P ([64][64] per chunk)
-  _Float16* Wc; float* Uc; _Float16* Kc; float* Gam;
-  _Float16* Ws; float* Us; _Float16* Ks; _Float16* Qs; _Float16* Ps;
+  float* Gam;     // chunk decay e^{G_C}                     [n][NT][128]
+  _Float16* Ps;   // S readout's output pair P, fragment order [n][NT][64][64]
+  // forward-only panels: the state passes' MFMA operands W (token-major) and
+  // K^ (chunk-transposed), fp16 in fragment order, U (fp32), and the S
+  // readout's Q~ (token-major, fp16 fragment order)
+  _Float16* Wc; float* Uc; _Float16* Kc;
+  _Float16* Ws; float* Us; _Float16* Ks; _Float16* Qs;
 };
 
 struct FwdParams {
