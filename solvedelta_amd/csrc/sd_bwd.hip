@@ -528,96 +528,161 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Sources transpose: one wave per token.
+// Row pieces: in the per-token closures lane cl = l & 15 of DPP row l >> 4
+// holds the eight consecutive columns 8 cl .. 8 cl + 7 of its token's rows, so
+// a wave takes four tokens and each row reduction is four in-row DPP adds.
+// With VEC (the width a multiple of 8 and every row 16-byte aligned: the
+// launcher checks) a piece is one 16-byte load or store; otherwise the same
+// eight columns move element by element (clamped address + mask), so both
+// variants compute bitwise the same.  Workspace panels are always aligned.
 // ---------------------------------------------------------------------------
+template <bool VEC>
+__device__ __forceinline__ void ld_piece(const __bf16* row, bool tv, int w, float (&x)[8]) {
+  const int c0 = 8 * (lane_id() & 15);
+  if constexpr (VEC) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + (c0 < w ? c0 : w - 8));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = keep_if(tv && c0 < w, bf2f(v[e]));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = c0 + e;
+      x[e] = keep_if(tv && c < w, bf2f(row[c < w ? c : w - 1]));
+    }
+  }
+}
+template <class E>
+__device__ __forceinline__ void ld_panel_piece(const E* row, float keep, float (&x)[8]) {
+  typedef E V8 __attribute__((ext_vector_type(8)));
+  const V8 v = *reinterpret_cast<const V8*>(row + 8 * (lane_id() & 15));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = keep * (float)v[e];
+}
+template <class E>
+__device__ __forceinline__ void st_panel_piece(E* row, const float (&x)[8]) {
+  typedef E V8 __attribute__((ext_vector_type(8)));
+  V8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (E)x[e];
+  *reinterpret_cast<V8*>(row + 8 * (lane_id() & 15)) = v;
+}
+// A bf16 output row of width w (columns past w are not written).
+template <bool VEC>
+__device__ __forceinline__ void st_piece(__bf16* row, int w, const float (&x)[8]) {
+  const int c0 = 8 * (lane_id() & 15);
+  if constexpr (VEC) {
+    if (c0 < w) st_panel_piece(row, x);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (c0 + e < w) row[c0 + e] = f2bf(x[e]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sources transpose (row pieces, four waves of four tokens per workgroup, no
+// LDS): phi, den, e, chi, z and the q / erase / write / value gates closed
+// against the S side's cotangents de, dchi, dw, dd (the closed forms of
+// tests/chunk_model.py::sources_bwd).  Writes dq, derase, dv, dwrite, the
+// partial du / dk panels (closed by the C chunk gradient's tail) and ddelta
+// (read by the C op's backward prep).  A padded token reads the last valid
+// token's (finite) panel rows and masks them: its ddelta row comes out zero.
+// ---------------------------------------------------------------------------
+template <bool VEC>
 __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   const int n = blockIdx.y, b = n / p.H, hh = n % p.H;
-  const int t = blockIdx.x * 4 + wave_id();
-  if (t >= p.Tp) return;
-  const int l = lane_id(), r = p.r, V = p.V;
-  const long long row = ((long long)n * p.Tp + t) * KD;
-  if (t >= p.T) {  // padded token: its ddelta row is read by the C chunk's backward prep
-    p.g.ddelta[row + l] = 0.f;
-    p.g.ddelta[row + l + 64] = 0.f;
-    return;
-  }
-  // every row of the token is loaded before the first reduction: a load issued
-  // after a cross-lane sum waits for it, which made three memory round trips
-  float u0, u1, k0, k1, q0, q1, e0, e1, w0, w1, v0, v1;
-  ldrow2(p.in.u, b, t, hh, p.T, r, u0, u1);
-  ldrow2(p.in.k, b, t, hh, p.T, r, k0, k1);
-  ldrow2(p.in.q, b, t, hh, p.T, r, q0, q1);
-  ldrow2(p.in.erase_raw, b, t, hh, p.T, r, e0, e1);
-  ldrow2(p.in.write_raw, b, t, hh, p.T, V, w0, w1);
-  ldrow2(p.in.v, b, t, hh, p.T, V, v0, v1);
-  const float d0 = (float)p.f.delta[row + l], d1 = (float)p.f.delta[row + l + 64];
-  const float de0 = p.g.de[row + l], de1 = p.g.de[row + l + 64];
-  const float dc0 = p.g.dchi[row + l], dc1 = p.g.dchi[row + l + 64];
-  const float dz0 = p.g.dwS[row + l], dz1 = p.g.dwS[row + l + 64];
-  const float dd0 = p.g.dd[row + l], dd1 = p.g.dd[row + l + 64];  // loaded before any store
-  norm2(u0, u1);
-  norm2(k0, k1);
-  const float rq = norm2(q0, q1);
-  const float usq = wave_sum(u0 * u0 + u1 * u1);
-  const float dsq = wave_sum(d0 * d0 + d1 * d1);
+  const int t = blockIdx.x * 16 + wave_id() * 4 + (lane_id() >> 4);
+  const int r = p.r, V = p.V, T = p.T, c0 = 8 * (lane_id() & 15);
+  const bool tv = t < T;
+  const int tc = tv ? t : T - 1;
+  const long long row = ((long long)n * p.Tp + (t < p.Tp ? t : p.Tp - 1)) * KD;
+  // a padded token's panel rows may hold anything: it reads the last valid
+  // token's (finite) rows and masks them
+  const long long vrow = ((long long)n * p.Tp + tc) * KD;
+  const float keep = tv ? 1.f : 0.f;
+  float u[8], k[8], q[8], er[8], wr[8], v[8], d[8], de[8], dc[8], dz[8], dd[8];
+  ld_piece<VEC>(brow(p.in.u, b, tc, hh), tv, r, u);
+  ld_piece<VEC>(brow(p.in.k, b, tc, hh), tv, r, k);
+  ld_piece<VEC>(brow(p.in.q, b, tc, hh), tv, r, q);
+  ld_piece<VEC>(brow(p.in.erase_raw, b, tc, hh), tv, r, er);
+  ld_piece<VEC>(brow(p.in.write_raw, b, tc, hh), tv, V, wr);
+  ld_piece<VEC>(brow(p.in.v, b, tc, hh), tv, V, v);
+  ld_panel_piece(p.f.delta + vrow, keep, d);
+  ld_panel_piece(p.g.de + vrow, keep, de);
+  ld_panel_piece(p.g.dchi + vrow, keep, dc);
+  ld_panel_piece(p.g.dwS + vrow, keep, dz);
+  ld_panel_piece(p.g.dd + vrow, keep, dd);
+  if (t >= p.Tp) return;  // past the padded chunk: nothing to write
+  auto rsum = [](float (&x)[8], const float (&y)[8]) {
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a += x[e] * y[e];
+    return row16_sum(a);
+  };
+  auto normalise = [&](float (&x)[8]) {
+    const float rs = rsqrtf(rsum(x, x) + 1e-24f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] *= rs;
+    return rs;
+  };
+  normalise(u);
+  normalise(k);
+  const float rq = normalise(q);
+  const float usq = rsum(u, u);
+  const float dsq = rsum(d, d);
   const float N = sqrtf(RHO * RHO + usq * dsq);
   const float sc = RHO / N;
-  const float p0 = sc * d0, p1 = sc * d1;
-  const float den = 1.f + wave_sum(p0 * u0 + p1 * u1);
-  const float se0 = 1.f / (1.f + __expf(-e0)), se1 = 1.f / (1.f + __expf(-e1));
-  const float sw0 = 1.f / (1.f + __expf(-w0)), sw1 = 1.f / (1.f + __expf(-w1));
-  const float b0 = se0 * k0, b1 = se1 * k1;
-  const float sb = wave_sum(u0 * b0 + u1 * b1) / den;
-  const float sq = wave_sum(u0 * q0 + u1 * q1) / den;
-  // z = sigmoid(wr) v
-  const float dv0 = sw0 * dz0, dv1 = sw1 * dz1;
-  const float dwr0 = dz0 * v0 * sw0 * (1.f - sw0), dwr1 = dz1 * v1 * sw1 * (1.f - sw1);
+  float pv[8], se[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    pv[e] = sc * d[e];
+    se[e] = 1.f / (1.f + __expf(-er[e]));
+    bv[e] = se[e] * k[e];
+  }
+  const float den = 1.f + rsum(pv, u);
+  const float sb = rsum(u, bv) / den;
+  const float sq = rsum(u, q) / den;
   // e = b - phi sb ; chi = q - phi sq
-  const float dsb = -wave_sum(p0 * de0 + p1 * de1);
-  const float dsq_ = -wave_sum(p0 * dc0 + p1 * dc1);
+  const float dsb = -rsum(pv, de);
+  const float dsq_ = -rsum(pv, dc);
   const float dub = dsb / den, duq = dsq_ / den;
   const float dden = -(dsb * sb + dsq_ * sq) / den;
-  float dph0 = -sb * de0 - sq * dc0 + dden * u0, dph1 = -sb * de1 - sq * dc1 + dden * u1;
-  float duh0 = dub * b0 + duq * q0 + dden * p0, duh1 = dub * b1 + duq * q1 + dden * p1;
-  const float db0 = de0 + dub * u0, db1 = de1 + dub * u1;
-  const float dqh0 = dc0 + duq * u0, dqh1 = dc1 + duq * u1;
-  const float dkh0 = db0 * se0, dkh1 = db1 * se1;
-  const float der0 = db0 * k0 * se0 * (1.f - se0), der1 = db1 * k1 * se1 * (1.f - se1);
+  float dph[8], duh[8], dqh[8], der[8], dkh[8], dvv[8], dwr[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    dph[e] = -sb * de[e] - sq * dc[e] + dden * u[e];
+    duh[e] = dub * bv[e] + duq * q[e] + dden * pv[e];
+    const float db = de[e] + dub * u[e];
+    dqh[e] = dc[e] + duq * u[e];
+    dkh[e] = db * se[e] + dd[e];
+    der[e] = db * k[e] * se[e] * (1.f - se[e]);
+    // z = sigmoid(wr) v
+    const float sw = 1.f / (1.f + __expf(-wr[e]));
+    dvv[e] = sw * dz[e];
+    dwr[e] = dz[e] * v[e] * sw * (1.f - sw);
+  }
   // phi = rho delta / N,  N^2 = rho^2 + usq dsq
-  const float ds = wave_sum(dph0 * d0 + dph1 * d1);
-  float ddl0 = sc * dph0, ddl1 = sc * dph1;
+  const float ds = rsum(dph, d);
+  const float qd = rsum(dqh, q);
   const float dN = -RHO * ds / (N * N);
   const float dN2 = dN / (2.f * N);
-  duh0 += 2.f * dN2 * dsq * u0;
-  duh1 += 2.f * dN2 * dsq * u1;
-  ddl0 += 2.f * dN2 * usq * d0;
-  ddl1 += 2.f * dN2 * usq * d1;
-  // q L2 norm transpose
-  const float qd = wave_sum(dqh0 * q0 + dqh1 * q1);
-  const float dq0 = (dqh0 - qd * q0) * rq, dq1 = (dqh1 - qd * q1) * rq;
-  const long long tok = ((long long)b * p.T + t) * p.H + hh;
-  if (l < r) {
-    p.dq[tok * r + l] = f2bf(dq0);
-    p.der[tok * r + l] = f2bf(der0);
+  float ddl[8], dq[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    ddl[e] = c0 + e < r ? sc * dph[e] + 2.f * dN2 * usq * d[e] : 0.f;
+    duh[e] += 2.f * dN2 * dsq * u[e];
+    // q L2 norm transpose
+    dq[e] = (dqh[e] - qd * q[e]) * rq;
   }
-  if (l + 64 < r) {
-    p.dq[tok * r + l + 64] = f2bf(dq1);
-    p.der[tok * r + l + 64] = f2bf(der1);
-  }
-  if (l < V) {
-    p.dv[tok * V + l] = f2bf(dv0);
-    p.dwr[tok * V + l] = f2bf(dwr0);
-  }
-  if (l + 64 < V) {
-    p.dv[tok * V + l + 64] = f2bf(dv1);
-    p.dwr[tok * V + l + 64] = f2bf(dwr1);
-  }
-  p.g.ddelta[row + l] = l < r ? ddl0 : 0.f;
-  p.g.ddelta[row + l + 64] = l + 64 < r ? ddl1 : 0.f;
-  p.g.du_src[row + l] = duh0;
-  p.g.du_src[row + l + 64] = duh1;
-  p.g.dk_src[row + l] = dkh0 + dd0;
-  p.g.dk_src[row + l + 64] = dkh1 + dd1;
+  st_panel_piece(p.g.ddelta + row, ddl);
+  if (!tv) return;
+  st_panel_piece(p.g.du_src + row, duh);
+  st_panel_piece(p.g.dk_src + row, dkh);
+  const long long tok = ((long long)b * T + t) * p.H + hh;
+  st_piece<VEC>(p.dq + tok * r, r, dq);
+  st_piece<VEC>(p.der + tok * r, r, der);
+  st_piece<VEC>(p.dv + tok * V, V, dvv);
+  st_piece<VEC>(p.dwr + tok * V, V, dwr);
 }
 
 // ---------------------------------------------------------------------------
@@ -821,41 +886,44 @@ struct FinRows {
   float gm, xk;
 };
 
+template <bool VEC>
 __device__ __forceinline__ void final_load(const BwdParams& p, int b, int hh, long long rowbase,
                                            int i, int t, FinRows& x) {
-  const int cl = lane_id() & 15, T = p.T;
+  const int T = p.T;
   const bool tv = t < T;
   const int tc = tv ? t : T - 1;
-  ld_row16(brow(p.in.u, b, tc, hh), tv, p.r, x.u);
-  ld_row16(brow(p.in.k, b, tc, hh), tv, p.r, x.k);
-  ld_row16(brow(p.in.h, b, tc, hh), tv, p.r, x.h);
+  ld_piece<VEC>(brow(p.in.u, b, tc, hh), tv, p.r, x.u);
+  ld_piece<VEC>(brow(p.in.k, b, tc, hh), tv, p.r, x.k);
+  ld_piece<VEC>(brow(p.in.h, b, tc, hh), tv, p.r, x.h);
   x.gm = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
                                          (long long)tc * p.in.gamma.st +
                                          (long long)hh * p.in.gamma.sh];
   // the erase read x = gamma u^ is dropped on fresh tokens: its cotangent dx
   // reaches neither u nor gamma there
   x.xk = erase_keep(p.in, b, tc);
-  const unsigned o = (unsigned)((rowbase + (tc - (t - i))) * KD + cl);
-#pragma unroll
-  for (int q = 0; q < RQ; ++q) {
-    x.dv[q] = (float)p.g.dwC[o + 16 * q];
-    x.us[q] = (float)p.g.du_src[o + 16 * q];
-    x.ks[q] = (float)p.g.dk_src[o + 16 * q];
-  }
+  const long long prow = (rowbase + (tc - (t - i))) * KD;
+  ld_panel_piece(p.g.dwC + prow, 1.f, x.dv);
+  ld_panel_piece(p.g.du_src + prow, 1.f, x.us);
+  ld_panel_piece(p.g.dk_src + prow, 1.f, x.ks);
 }
 
+template <bool VEC>
 __device__ __forceinline__ void final_close(const BwdParams& p, int b, int hh, int t,
                                             FinRows& x, const __bf16* dx_row,
                                             const __bf16* dk_row, const __bf16* dq_row) {
-  const int cl = lane_id() & 15, r = p.r;
+  const int r = p.r, c0 = 8 * (lane_id() & 15);
   const bool tv = t < p.T;
   float dx[RQ], du[RQ], dk[RQ];
+  {
+    const bf16x8 vx = *reinterpret_cast<const bf16x8*>(dx_row + c0);
+    const bf16x8 vk = *reinterpret_cast<const bf16x8*>(dk_row + c0);
+    const bf16x8 vq = *reinterpret_cast<const bf16x8*>(dq_row + c0);
 #pragma unroll
-  for (int q = 0; q < RQ; ++q) {
-    const int c = cl + 16 * q;
-    dx[q] = x.xk * bf2f(dx_row[c]);
-    du[q] = x.us[q] + bf2f(dk_row[c]) + x.gm * dx[q];
-    dk[q] = x.ks[q] + bf2f(dq_row[c]);
+    for (int q = 0; q < RQ; ++q) {
+      dx[q] = x.xk * bf2f(vx[q]);
+      du[q] = x.us[q] + bf2f(vk[q]) + x.gm * dx[q];
+      dk[q] = x.ks[q] + bf2f(vq[q]);
+    }
   }
   const float ru = l2norm16(x.u);
   const float rk = l2norm16(x.k);
@@ -871,16 +939,17 @@ __device__ __forceinline__ void final_close(const BwdParams& p, int b, int hh, i
   kd = row16_sum(kd);
   if (!tv) return;
   const long long tok = ((long long)b * p.T + t) * p.H + hh;
+  float ou[RQ], ok[RQ], oh[RQ];
 #pragma unroll
   for (int q = 0; q < RQ; ++q) {
-    const int c = cl + 16 * q;
-    if (c < r) {
-      p.du[tok * r + c] = f2bf((du[q] - ud * x.u[q]) * ru);
-      p.dk[tok * r + c] = f2bf((dk[q] - kd * x.k[q]) * rk);
-      p.dh[tok * r + c] = f2bf(x.gm * x.dv[q]);
-    }
+    ou[q] = (du[q] - ud * x.u[q]) * ru;
+    ok[q] = (dk[q] - kd * x.k[q]) * rk;
+    oh[q] = x.gm * x.dv[q];
   }
-  if (cl == 0) p.dgam[tok] = dgam;
+  st_piece<VEC>(p.du + tok * r, r, ou);
+  st_piece<VEC>(p.dk + tok * r, r, ok);
+  st_piece<VEC>(p.dh + tok * r, r, oh);
+  if ((lane_id() & 15) == 0) p.dgam[tok] = dgam;
 }
 
 struct GradCSmem {
@@ -893,6 +962,7 @@ struct GradCSmem {
   LPanel PW;  // delta
 };
 
+template <bool VEC>
 __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GradCSmem& s = *reinterpret_cast<GradCSmem*>(smem_raw);
@@ -1093,13 +1163,13 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     }
   // closure of u, k, h and gamma: this wave's two four-token groups
   FinRows f0, f1;
-  final_load(p, b, hh, rowbase, row16(w, 0), t0 + row16(w, 0), f0);
-  final_load(p, b, hh, rowbase, row16(w, 1), t0 + row16(w, 1), f1);
+  final_load<VEC>(p, b, hh, rowbase, row16(w, 0), t0 + row16(w, 0), f0);
+  final_load<VEC>(p, b, hh, rowbase, row16(w, 1), t0 + row16(w, 1), f1);
   __syncthreads();
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     const int i = row16(w, g);
-    final_close(p, b, hh, t0 + i, g ? f1 : f0, dxl + i * KD, s.PA.h[i], s.PA.l[i]);
+    final_close<VEC>(p, b, hh, t0 + i, g ? f1 : f0, dxl + i * KD, s.PA.h[i], s.PA.l[i]);
   }
 }
 
@@ -1109,6 +1179,18 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
                void* dv, void* derase, void* dwrite, float* dlog_decay, float* dgamma,
                float* dC0, float* dS0, hipStream_t st) {
   const int n = in->B * in->H, NT = (in->T + BT - 1) / BT, Tp = NT * BT;
+  // the sources transpose takes whole 16-byte row pieces when every row allows it
+  auto al16 = [](const sd_view& v) {
+    return ((uintptr_t)v.data & 15) == 0 && v.sb % 8 == 0 && v.st % 8 == 0 && v.sh % 8 == 0;
+  };
+  const bool src_vec = in->r % 8 == 0 && in->V % 8 == 0 && al16(in->u) && al16(in->k) &&
+                       al16(in->q) && al16(in->erase_raw) && al16(in->write_raw) && al16(in->v) &&
+                       ((uintptr_t)dq & 15) == 0 && ((uintptr_t)derase & 15) == 0 &&
+                       ((uintptr_t)dv & 15) == 0 && ((uintptr_t)dwrite & 15) == 0;
+  // so does the C chunk gradient's closure tail
+  const bool fin_vec = in->r % 8 == 0 && al16(in->u) && al16(in->k) && al16(in->h) &&
+                       ((uintptr_t)du & 15) == 0 && ((uintptr_t)dk & 15) == 0 &&
+                       ((uintptr_t)dh & 15) == 0;
   BwdParams p{};
   p.in = *in;
   p.H = in->H; p.T = in->T; p.r = in->r; p.V = in->V; p.NT = NT; p.Tp = Tp;
@@ -1121,8 +1203,9 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   SD_SMEM_ONCE(k_bprep_s, (int)sizeof(BprepSSmem));
   SD_SMEM_ONCE(k_grad_s, (int)sizeof(GradSmem));
   SD_SMEM_ONCE(k_bprep_c, (int)sizeof(BprepCSmem));
-  SD_SMEM_ONCE(k_grad_c, (int)sizeof(GradCSmem));
-  const dim3 chunks(NT, n), rows((Tp + 3) / 4, n), blk(NTHREADS), cblk(CT);
+  SD_SMEM_ONCE(k_grad_c<true>, (int)sizeof(GradCSmem));
+  SD_SMEM_ONCE(k_grad_c<false>, (int)sizeof(GradCSmem));
+  const dim3 chunks(NT, n), blk(NTHREADS), cblk(CT);
   // S memory
   const dim3 chunks_cm(n, NT);  // chunk-major grid of the backward preps
   SD_LAUNCH("k_bprep_s", k_bprep_s, chunks_cm, cblk, sizeof(BprepSSmem), st, p);
@@ -1136,7 +1219,10 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   ss.fin = dS0; ss.fin_transposed = 0;
   launch_state("state_s_bwd", ss, n, st);
   SD_LAUNCH("k_grad_s", k_grad_s, chunks, cblk, sizeof(GradSmem), st, p);
-  SD_LAUNCH("k_src_bwd", k_src_bwd, rows, blk, 0, st, p);
+  if (src_vec)
+    SD_LAUNCH("k_src_bwd", k_src_bwd<true>, dim3(Tp / 16, n), blk, 0, st, p);
+  else
+    SD_LAUNCH("k_src_bwd", k_src_bwd<false>, dim3(Tp / 16, n), blk, 0, st, p);
   // C predictor
   SD_LAUNCH("k_bprep_c", k_bprep_c, chunks_cm, cblk, sizeof(BprepCSmem), st, p);
   StateParams sc{};
@@ -1148,7 +1234,10 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   sc.init = dC_T; sc.init_transposed = 1;
   sc.fin = dC0; sc.fin_transposed = 1;
   launch_state("state_c_bwd", sc, n, st);
-  SD_LAUNCH("k_grad_c", k_grad_c, chunks, cblk, sizeof(GradCSmem), st, p);
+  if (fin_vec)
+    SD_LAUNCH("k_grad_c", k_grad_c<true>, chunks, cblk, sizeof(GradCSmem), st, p);
+  else
+    SD_LAUNCH("k_grad_c", k_grad_c<false>, chunks, cblk, sizeof(GradCSmem), st, p);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 

@@ -87,8 +87,13 @@ def test_backward_extreme_decay_finite():
             [NAMES[i] for i in keep])
 
 
-def test_backward_strided_bitwise():
-    args = make_inputs(1, 40, 2, 16, 16, seed=19, requires_grad=True)
+@pytest.mark.parametrize("T,r,seed", [(40, 16, 19), (100, 128, 23)])
+def test_backward_strided_bitwise(T, r, seed):
+    """Views whose rows are not 16-byte aligned (row stride r + 7) take the
+    per-token closures' element-wise loads, packed inputs their 16-byte pieces:
+    every gradient must agree bitwise (reference test_rebuild_semantics.py:487-537)."""
+    print(f"case strided bitwise T{T} r{r}", flush=True)
+    args = make_inputs(1, T, 2, r, r, seed=seed, requires_grad=True)
     strided = list(a.detach().clone().requires_grad_() for a in args)
     for i in (0, 1, 2, 3, 4, 6, 7):
         x = args[i]
