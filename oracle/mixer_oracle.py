@@ -76,7 +76,8 @@ def rms_norm_gated(x, gate, weight, eps):
 
 def mixer_oracle(params: dict, hidden, *, heads, rk, rv, eps=1e-6, use_short_conv=True,
                  initial_state: Optional[tuple] = None, valid_mask=None, reset_mask=None,
-                 geometry_enabled=True, decay_enabled=True, taps: Optional[list] = None):
+                 geometry_enabled=True, decay_enabled=True, taps: Optional[list] = None,
+                 act_round=None):
     """One mixer layer in FP64.  ``params`` maps the reference module's parameter
     names (in_proj.weight, conv_weight, decay_proj.weight, output_gate_proj.weight/
     .bias, output_norm.weight, output_proj.weight, geometry_write_bias,
@@ -84,12 +85,18 @@ def mixer_oracle(params: dict, hidden, *, heads, rk, rv, eps=1e-6, use_short_con
     output_proj.bias) to tensors.  ``initial_state`` = ((C, S), conv) or None.
     Returns (output [B,T,hidden], (C, S), conv_state).  If ``taps`` is a list,
     the log-decay tensor [B,T,H,r] is appended to it (for conditioning
-    estimates of the decay-rate gradient in tests)."""
+    estimates of the decay-rate gradient in tests).  ``act_round`` (e.g. a
+    round trip through bf16) is applied where a bf16 layer materialises its
+    activations -- the in-projection, the conv4 + SiLU output, the decay and
+    output-gate projections and the operator output -- so that the FP64
+    recurrence runs on the operands the bf16 layer hands its operator; None
+    keeps every activation exact."""
     p = {k: v.double() for k, v in params.items()}
     hidden = hidden.double()
+    rnd = act_round if act_round is not None else (lambda x: x)
     B, T, _ = hidden.shape
     sizes, width, _ = projection_layout(hidden.shape[-1], heads, rk, rv)
-    proj = F.linear(hidden, p["in_proj.weight"], p.get("in_proj.bias"))[..., :width]
+    proj = rnd(F.linear(hidden, p["in_proj.weight"], p.get("in_proj.bias"))[..., :width])
     parts = proj.split(sizes, dim=-1)
     qkv = torch.cat(parts[:3], dim=-1)
     op_init, conv_init = (None, None) if initial_state is None else initial_state
@@ -100,10 +107,11 @@ def mixer_oracle(params: dict, hidden, *, heads, rk, rv, eps=1e-6, use_short_con
                                      valid_mask, reset_mask)
     else:
         qkv = F.silu(qkv)
+    qkv = rnd(qkv)
     q, k, v = qkv.split(sizes[:3], dim=-1)
     u, h, er, wr, geo, dec_h, gate_h = parts[3:]
     view = lambda x, n: x.reshape(B, T, heads, n)
-    log_decay = kda_decay(view(F.linear(dec_h, p["decay_proj.weight"]), rk),
+    log_decay = kda_decay(view(rnd(F.linear(dec_h, p["decay_proj.weight"])), rk),
                           p["associative_log_rate"], p["associative_decay_bias"])
     if not decay_enabled:
         log_decay = torch.zeros_like(log_decay)
@@ -112,14 +120,14 @@ def mixer_oracle(params: dict, hidden, *, heads, rk, rv, eps=1e-6, use_short_con
     gamma = torch.sigmoid(geo + p["geometry_write_bias"].view(1, 1, heads))
     if not geometry_enabled:
         gamma = torch.zeros_like(gamma)
-    gate = view(F.linear(gate_h, p["output_gate_proj.weight"], p["output_gate_proj.bias"]), rv)
+    gate = view(rnd(F.linear(gate_h, p["output_gate_proj.weight"], p["output_gate_proj.bias"])), rv)
     init = None if op_init is None else OracleState(*(s.double() for s in op_init))
     out, st = solvedelta_oracle(
         view(u, rk), view(h, rk), view(q, rk), k.reshape(B, T, heads, 1, rk),
         v.reshape(B, T, heads, 1, rv), log_decay, torch.sigmoid(er).reshape(B, T, heads, 1, rk),
         torch.sigmoid(wr).reshape(B, T, heads, 1, rv), gamma, initial_state=init,
         valid_mask=valid_mask, reset_mask=reset_mask)
-    y = rms_norm_gated(out, gate, p["output_norm.weight"], eps)
+    y = rms_norm_gated(rnd(out), gate, p["output_norm.weight"], eps)
     y = F.linear(y.reshape(B, T, heads * rv), p["output_proj.weight"], p.get("output_proj.bias"))
     return y, (st.predictor, st.S), conv_state
 
