@@ -1015,17 +1015,23 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       kl[I] = mma_blks(A, BL, zero4());
     }
   }
-  float Su[NB][4], Sdd[NB][4], So[NB][4];
+  float Su[NB][4], Sdd[NB][4], Sod[NB][4];
   load_slab(Su, uh, cb);
   load_slab(Sdd, ddp, cb);
-  load_slab(So, dprim, cb);
-  {
+  {  // the C-op output o = d - k enters only as o (.) dd: formed at once, so
+     // neither slab stays live through the applies
     float Sk[NB][4];
+    load_slab(Sod, dprim, cb);
     load_slab(Sk, kh, cb);
 #pragma unroll
     for (int J = 0; J < NB; ++J)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) So[J][e] -= Sk[J][e];  // C-op output o = d - k
+      for (int e = 0; e < 4; ++e) {
+        Sod[J][e] = (Sod[J][e] - Sk[J][e]) * Sdd[J][e];
+        // formed here: left to the compiler, the subtraction sank to its last use
+        // and kept both fp16 slabs live (and spilled) through the applies
+        asm volatile("" : "+v"(Sod[J][e]));
+      }
   }
   Tab1 t1;
   RowF rx, ri;  // exclusive / inclusive row factors
@@ -1055,8 +1061,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     for (int q = 0; q < PPC; ++q) ppv[q] = *reinterpret_cast<const float4*>(pp + (threadIdx.x + q * CT) * 4);
   }
   // dx and dk stay in the workgroup for the closure tail, rounded to bf16 as the
-  // panels between kernels were: dx into M2 once the applies are done with it,
-  // dk in registers until the dq product has run
+  // panels between kernels were: once the applies are done, dx goes into M2 and
+  // dk into the decay tables' storage (nothing reads the decay tables after the
+  // applies)
   __bf16 dxr[NB][4], dkr[NB][4];
   // decay cotangent: dg_i = o_i dd_i - u_i dk_i plus the shifted gamma u (.) dx
   // term, closed in registers below (v = dg + xdx, then dg = suffix(v) - xdx)
@@ -1074,7 +1081,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       dxr[I][e] = f2bf(dx);
       dkr[I][e] = f2bf(dk);
       xs[I][e] = Sx[I][e] * dx;
-      vv[I][e] = So[I][e] * Sdd[I][e] - Su[I][e] * dk + xs[I][e];
+      vv[I][e] = Sod[I][e] - Su[I][e] * dk + xs[I][e];
     }
   }
   __syncthreads();  // every apply has read M1 and M2
@@ -1084,10 +1091,15 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     *reinterpret_cast<float4*>(&s.M1[(idx / BT) * LS + idx % BT]) = ppv[q];
   }
   __bf16* const dxl = reinterpret_cast<__bf16*>(s.M2);  // [64][128] bf16 fits M2's 64 x 68 floats
+  __bf16* const dkl = reinterpret_cast<__bf16*>(&s.cd);  // and the decay tables' 37 KB
+  static_assert(sizeof(ChunkDecay) >= BT * KD * sizeof(__bf16), "dk fits the decay tables");
 #pragma unroll
   for (int I = 0; I < NB; ++I)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dxl[(I * BS + r4 + e) * KD + c] = dxr[I][e];
+    for (int e = 0; e < 4; ++e) {
+      dxl[(I * BS + r4 + e) * KD + c] = dxr[I][e];
+      dkl[(I * BS + r4 + e) * KD + c] = dkr[I][e];
+    }
   // dg_i = rowsum + sum_{i' >= i} dg_i' + sum_{i' > i} xdx_i'
   close_decay_column(vv, s.rsum, cb);
   // the C side's part of the log-decay gradient, added to the S side's (written
@@ -1106,7 +1118,10 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       }
   }
   __syncthreads();  // P' in M1; PA (dd e^G) staged
-  // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0)
+  // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0).
+  // The gathers stay here: hoisted by the scheduler into the early slab loads
+  // they were held in registers through the applies and spilled.
+  __builtin_amdgcn_sched_barrier(0);
   f4 dqs[NB];
   {
     BlkS BX;
@@ -1153,14 +1168,11 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       dqs[I] = dq;
     }
   }
-  __syncthreads();  // PA, PW and M1 read by every wave: dk and dq take PA's halves
+  __syncthreads();  // PA, PW and M1 read by every wave: dq takes PA's low half
 #pragma unroll
   for (int I = 0; I < NB; ++I)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      s.PA.h[I * BS + r4 + e][c] = dkr[I][e];
-      s.PA.l[I * BS + r4 + e][c] = f2bf(dqs[I][e]);
-    }
+    for (int e = 0; e < 4; ++e) s.PA.l[I * BS + r4 + e][c] = f2bf(dqs[I][e]);
   // closure of u, k, h and gamma: this wave's two four-token groups
   FinRows f0, f1;
   final_load<VEC>(p, b, hh, rowbase, row16(w, 0), t0 + row16(w, 0), f0);
@@ -1169,7 +1181,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     const int i = row16(w, g);
-    final_close<VEC>(p, b, hh, t0 + i, g ? f1 : f0, dxl + i * KD, s.PA.h[i], s.PA.l[i]);
+    final_close<VEC>(p, b, hh, t0 + i, g ? f1 : f0, dxl + i * KD, dkl + i * KD, s.PA.l[i]);
   }
 }
 
