@@ -43,6 +43,7 @@ struct DoutRaw {
 };
 // A missing cotangent reads this zero element instead (pointer select, no branch).
 __device__ const __bf16 sd_zero_bf16[1] = {};
+__device__ __align__(16) const __bf16 sd_zero_bf16x8[8] = {};
 __device__ __forceinline__ DoutRaw dout_raw(const BwdParams& p, int b, int t, int h, int c) {
   const bool has = p.dout != nullptr;
   const bool ok = has && t < p.T && c < p.V;
@@ -156,7 +157,44 @@ struct BprepSSmem {
   float P[BT * LS];  // P and N are contiguous: reused as a 64 x 128 staging panel
   float N[BT * LS];
   SPanel64 At, Nt;   // A^T and N^T split once: the MFMA A operands of Wk and dU
+  __bf16 dO[BT][LPS]; // the chunk's output cotangent rows (exact bf16; zero past T, V)
 };
+
+// The chunk's output cotangent rows into LDS, two 8-column pieces per thread:
+// with VEC (V a multiple of 8; rows are then 16-byte aligned) one 16-byte load
+// per piece, otherwise element by element (clamped address + mask).  A missing
+// cotangent stages zeros.
+template <bool VEC>
+__device__ __forceinline__ void stage_dout_rows(const BwdParams& p, int b, int t0, int hh,
+                                                __bf16 (*dst)[LPS]) {
+  constexpr int PER = BT * KD / 8 / CT;
+  bf16x8 v[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 8, i = idx / KD, c = idx % KD, t = t0 + i;
+    if constexpr (VEC) {
+      const bool ok = p.dout != nullptr && t < p.T && c < p.V;
+      const __bf16* base = p.dout ? p.dout : sd_zero_bf16x8;
+      const long long o = p.dout ? (((long long)b * p.T + (t < p.T ? t : p.T - 1)) * p.H + hh) *
+                                           p.V + (c < p.V ? c : p.V - 8)
+                                 : 0;
+      const bf16x8 raw = *reinterpret_cast<const bf16x8*>(base + o);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[q][e] = (__bf16)keep_if(ok, bf2f(raw[e]));
+    } else {
+      DoutRaw r[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = dout_raw(p, b, t, hh, c + e);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[q][e] = (__bf16)dout_val(r[e]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 8;
+    *reinterpret_cast<bf16x8*>(&dst[idx / KD][idx % KD]) = v[q];
+  }
+}
 
 // A fragment of an fp16 panel, re-split into bf16 high + low halves (exact:
 // fp16's 11-bit significand fits the two bf16 halves) for the 3-term product.
@@ -174,12 +212,14 @@ __device__ __forceinline__ Frag ldfrag_h(const _Float16* p, long long off) {
 }
 static_assert(2 * BT * LS >= BT * KD, "P + N hold a 64 x 128 panel");
 
+template <bool VEC>
 __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   BprepSSmem& s = *reinterpret_cast<BprepSSmem*>(smem_raw);
   // chunk-major dispatch, first chunk first: the last chunk, where the reverse
   // state pass starts right after this kernel, is written last
   const int n = blockIdx.x, ch = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  stage_dout_rows<VEC>(p, b, t0, hh, s.dO);  // read below after the first barrier
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
@@ -231,15 +271,12 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
     const fpan_t* const dp = p.f.d + rowbase * KD;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      DoutRaw r[8];
       float kv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        r[e] = dout_raw(p, b, t0 + ks * 32 + kq + e, hh, cb * 16 + m);
+        db[ks][e] = s.dO[ks * 32 + kq + e][cb * 16 + m];
         kv[e] = (float)dp[(ks * 32 + kq + e) * KD + cb * 16 + m];
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) db[ks][e] = (__bf16)dout_val(r[e]);
       // the decayed keys K^_i = d_i e^{G_C - G_i} of the forward's S pass, formed
       // again from the saved d (the exponent is <= 0)
       const int c = cb * 16 + m;
@@ -273,7 +310,6 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   constexpr int NPC = KD * BT / 8 / CT;
   float ev[NPC][8];
   _Float16 qv[NPC][8];
-  DoutRaw d[NPC][8];
 #pragma unroll
   for (int q = 0; q < NPC; ++q) {
     const int pc = threadIdx.x + q * CT, block = pc >> 6, lane = pc & 63;
@@ -284,7 +320,6 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
       const int i = i0 + e;
       ev[q][e] = (float)p.f.e[(rowbase + i) * KD + c];
       qv[q][e] = p.f.chi[(rowbase + i) * KD + c];  // Q~ = chi e^G, scaled below
-      d[q][e] = dout_raw(p, b, t0 + i, hh, c);
     }
   }
   store_du_slab(p.g.dU + rowbase * KD, dus);
@@ -312,7 +347,7 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
         const float eg = __expf(cd.G[i0 + e][c]);
         ah[e] = (__bf16)(-ev[q][e] * eg);
         qh[e] = (__bf16)((float)qv[q][e] * eg);  // Q~ = chi e^G, transposed, bf16
-        dh[e] = (__bf16)dout_val(d[q][e]);  // exact in bf16
+        dh[e] = s.dO[i0 + e][c];  // exact in bf16
       }
       const long long ot = cidx * KD * BT + (long long)pc * 8;
       *reinterpret_cast<bf16x8*>(p.g.Ant + ot) = ah;
@@ -1212,7 +1247,8 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   p.du = (__bf16*)du; p.dh = (__bf16*)dh; p.dq = (__bf16*)dq; p.dk = (__bf16*)dk;
   p.dv = (__bf16*)dv; p.der = (__bf16*)derase; p.dwr = (__bf16*)dwrite;
   p.dg = dlog_decay; p.dgam = dgamma;
-  SD_SMEM_ONCE(k_bprep_s, (int)sizeof(BprepSSmem));
+  SD_SMEM_ONCE(k_bprep_s<true>, (int)sizeof(BprepSSmem));
+  SD_SMEM_ONCE(k_bprep_s<false>, (int)sizeof(BprepSSmem));
   SD_SMEM_ONCE(k_grad_s, (int)sizeof(GradSmem));
   SD_SMEM_ONCE(k_bprep_c, (int)sizeof(BprepCSmem));
   SD_SMEM_ONCE(k_grad_c<true>, (int)sizeof(GradCSmem));
@@ -1220,7 +1256,10 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   const dim3 chunks(NT, n), blk(NTHREADS), cblk(CT);
   // S memory
   const dim3 chunks_cm(n, NT);  // chunk-major grid of the backward preps
-  SD_LAUNCH("k_bprep_s", k_bprep_s, chunks_cm, cblk, sizeof(BprepSSmem), st, p);
+  if (in->V % 8 == 0)
+    SD_LAUNCH("k_bprep_s", k_bprep_s<true>, chunks_cm, cblk, sizeof(BprepSSmem), st, p);
+  else
+    SD_LAUNCH("k_bprep_s", k_bprep_s<false>, chunks_cm, cblk, sizeof(BprepSSmem), st, p);
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
   ss.rev = 1;
