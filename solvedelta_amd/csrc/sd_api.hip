@@ -84,9 +84,13 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   // Buffers whose last reader runs before the first writer of another share
   // its storage (kernel order: bprep_s, state_s, grad_s, src_bwd, bprep_c,
   // state_c, grad_c (its tail closes u, k, h, gamma)): the C op's cotangent
-  // slots take the S op's (last read by grad_s), dw_C takes dw_S (last read by
-  // src_bwd), and grad_s's de / dchi take the injection panels At1 / B1 (read by
-  // the S reverse pass, written again by bprep_c after src_bwd has read de / dchi).
+  // slots take the S op's (last read by grad_s), grad_s's de / dchi take the
+  // injection panels At1 / B1 (read by the S reverse pass, written again by
+  // bprep_c after src_bwd has read de / dchi), and dw_S's storage holds dw_S,
+  // then ddelta (src_bwd overwrites each row piece it has read; bprep_c reads
+  // ddelta), then dw_C (written by the C reverse pass).  The sources
+  // transpose's partial du / dk go to the du / dk gradients themselves, which
+  // the C chunk gradient's tail reads and overwrites.
   w.Ls = c.take<lslot_t>(states);
   w.Lc = w.Ls;
   w.Wk = c.take<__bf16>(panel);
@@ -97,8 +101,9 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   static_assert(sizeof(bpan_t) == sizeof(__bf16), "de / dchi share the bf16 injection panels");
   w.de = reinterpret_cast<bpan_t*>(w.At1);
   w.dchi = reinterpret_cast<bpan_t*>(w.B1t);
-  bpan_t** bpanels[] = {&w.dwS, &w.dd, &w.ddelta, &w.du_src, &w.dk_src};
-  for (bpan_t** pp : bpanels) *pp = c.take<bpan_t>(panel);
+  w.dwS = c.take<bpan_t>(panel);
+  w.dd = c.take<bpan_t>(panel);
+  w.ddelta = w.dwS;
   w.dwC = w.dwS;
   w.uh = c.take<fpan_t>(panel);
   w.kh = c.take<fpan_t>(panel);

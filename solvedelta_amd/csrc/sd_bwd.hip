@@ -593,6 +593,14 @@ __device__ __forceinline__ void ld_panel_piece(const E* row, float keep, float (
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = keep * (float)v[e];
 }
+// The same piece selected (not scaled) by tv: rows that were never written read as 0.
+template <class E>
+__device__ __forceinline__ void ld_panel_piece_sel(const E* row, bool tv, float (&x)[8]) {
+  typedef E V8 __attribute__((ext_vector_type(8)));
+  const V8 v = *reinterpret_cast<const V8*>(row + 8 * (lane_id() & 15));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = keep_if(tv, (float)v[e]);
+}
 template <class E>
 __device__ __forceinline__ void st_panel_piece(E* row, const float (&x)[8]) {
   typedef E V8 __attribute__((ext_vector_type(8)));
@@ -619,9 +627,10 @@ __device__ __forceinline__ void st_piece(__bf16* row, int w, const float (&x)[8]
 // LDS): phi, den, e, chi, z and the q / erase / write / value gates closed
 // against the S side's cotangents de, dchi, dw, dd (the closed forms of
 // tests/chunk_model.py::sources_bwd).  Writes dq, derase, dv, dwrite, the
-// partial du / dk panels (closed by the C chunk gradient's tail) and ddelta
-// (read by the C op's backward prep).  A padded token reads the last valid
-// token's (finite) panel rows and masks them: its ddelta row comes out zero.
+// partial du / dk into the du / dk gradients (closed in place by the C chunk
+// gradient's tail) and ddelta over dw (read by the C op's backward prep).  A
+// padded token reads the last valid token's (finite) panel rows and masks
+// them, and its own dw row selected to zero: its ddelta row comes out zero.
 // ---------------------------------------------------------------------------
 template <bool VEC>
 __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
@@ -645,7 +654,8 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   ld_panel_piece(p.f.delta + vrow, keep, d);
   ld_panel_piece(p.g.de + vrow, keep, de);
   ld_panel_piece(p.g.dchi + vrow, keep, dc);
-  ld_panel_piece(p.g.dwS + vrow, keep, dz);
+  // dw_S from this token's own row: ddelta is written over it below
+  ld_panel_piece_sel(p.g.dwS + row, tv, dz);
   ld_panel_piece(p.g.dd + vrow, keep, dd);
   if (t >= p.Tp) return;  // past the padded chunk: nothing to write
   auto rsum = [](float (&x)[8], const float (&y)[8]) {
@@ -711,9 +721,10 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   }
   st_panel_piece(p.g.ddelta + row, ddl);
   if (!tv) return;
-  st_panel_piece(p.g.du_src + row, duh);
-  st_panel_piece(p.g.dk_src + row, dkh);
   const long long tok = ((long long)b * T + t) * p.H + hh;
+  // partial du / dk, closed in place by the C chunk gradient's tail
+  st_piece<VEC>(p.du + tok * r, r, duh);
+  st_piece<VEC>(p.dk + tok * r, r, dkh);
   st_piece<VEC>(p.dq + tok * r, r, dq);
   st_piece<VEC>(p.der + tok * r, r, der);
   st_piece<VEC>(p.dv + tok * V, V, dvv);
@@ -938,8 +949,10 @@ __device__ __forceinline__ void final_load(const BwdParams& p, int b, int hh, lo
   x.xk = erase_keep(p.in, b, tc);
   const long long prow = (rowbase + (tc - (t - i))) * KD;
   ld_panel_piece(p.g.dwC + prow, 1.f, x.dv);
-  ld_panel_piece(p.g.du_src + prow, 1.f, x.us);
-  ld_panel_piece(p.g.dk_src + prow, 1.f, x.ks);
+  // the sources transpose's partial du / dk, in the gradients this tail overwrites
+  const long long tok = ((long long)b * T + tc) * p.H + hh;
+  ld_piece<VEC>(p.du + tok * p.r, tv, p.r, x.us);
+  ld_piece<VEC>(p.dk + tok * p.r, tv, p.r, x.ks);
 }
 
 template <bool VEC>
@@ -1233,7 +1246,8 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   const bool src_vec = in->r % 8 == 0 && in->V % 8 == 0 && al16(in->u) && al16(in->k) &&
                        al16(in->q) && al16(in->erase_raw) && al16(in->write_raw) && al16(in->v) &&
                        ((uintptr_t)dq & 15) == 0 && ((uintptr_t)derase & 15) == 0 &&
-                       ((uintptr_t)dv & 15) == 0 && ((uintptr_t)dwrite & 15) == 0;
+                       ((uintptr_t)dv & 15) == 0 && ((uintptr_t)dwrite & 15) == 0 &&
+                       ((uintptr_t)du & 15) == 0 && ((uintptr_t)dk & 15) == 0;
   // so does the C chunk gradient's closure tail
   const bool fin_vec = in->r % 8 == 0 && al16(in->u) && al16(in->k) && al16(in->h) &&
                        ((uintptr_t)du & 15) == 0 && ((uintptr_t)dk & 15) == 0 &&

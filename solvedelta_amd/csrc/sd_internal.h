@@ -141,7 +141,7 @@ struct BwdWs {
   float* dU; __bf16* Wk; __bf16* At1; __bf16* B1t; __bf16* Ant;
   bpan_t* dwS; bpan_t* dwC;         // dw of each op           [n][Tp][128]
   bpan_t* de; bpan_t* dchi; bpan_t* dd;
-  bpan_t* ddelta; bpan_t* du_src; bpan_t* dk_src;
+  bpan_t* ddelta;  // shares dw_S's storage (written in place by the sources transpose)
   fpan_t* uh;  // normalised u
   fpan_t* kh;  // normalised keys
   float* Pp;  // P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) of the C op  [n][NT][64][64]
