@@ -165,11 +165,6 @@ constexpr int SWAVES = 4;
 constexpr int SRB = KD / 16 / SWAVES;
 constexpr int STHREADS = SWAVES * 64;
 constexpr int STILES = KD / SCOLS;
-// With AUX the workgroup has four more waves (a second wave per SIMD) that take
-// the work off the recurrence's critical path: the slot and w write-back and,
-// in the forward S pass, the readout.  The four chain waves keep only the
-// recurrence; the two roles share the step's two barriers.
-template <bool AUX> constexpr int state_threads() { return AUX ? 2 * STHREADS : STHREADS; }
 // State-pass prefetch buffers (PF - 1 chunks ahead).  Deeper rings measured no
 // faster on the forward passes and push the reverse passes past 512 registers.
 constexpr int PF = 3;
@@ -225,13 +220,12 @@ struct StateSmem {
   float Gf[KD];       // chunk decay, staged from one 16-byte load per lane of wave 0
 };
 
-template <bool REV, bool OUT, bool AUX = false>
+template <bool REV, bool OUT>
 struct StateFrags {
   using V8 = typename StateT<REV>::V8;
-  // With AUX, an aux wave holds the readout operands in W (Q~ rows) and K[0] (P rows).
   V8 W[4];
-  V8 Q[OUT && !AUX ? 4 : 1];  // readout operands (forward S pass): Q~ rows of this wave's token block
-  V8 P[OUT && !AUX ? 2 : 1];  // and the same rows of P
+  V8 Q[OUT ? 4 : 1];  // readout operands (forward S pass): Q~ rows of this wave's token block
+  V8 P[OUT ? 2 : 1];  // and the same rows of P
   V8 K[SRB][2];
   bf16x8 A1[REV ? SRB : 1][2];
   bf16x8 B1[REV ? HALVES : 1][2];
@@ -244,34 +238,21 @@ __device__ __forceinline__ bf16x8 ldb8(const __bf16* p) { return *reinterpret_ca
 template <class V8, class E>
 __device__ __forceinline__ V8 ldv8(const E* p) { return *reinterpret_cast<const V8*>(p); }
 
-template <bool REV, bool OUT, bool AUX = false>
+template <bool REV, bool OUT>
 __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
-                                                 StateFrags<REV, OUT, AUX>& f) {
+                                                 StateFrags<REV, OUT>& f) {
   using E = typename StateT<REV>::E;
   using V8 = typename StateT<REV>::V8;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int w = wv & (SWAVES - 1), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
   const int tb = w;  // this wave's token block
   const long long cidx = (long long)n * p.NT + ch;
   const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
   const long long wb = rowbase * KD;
-  if constexpr (AUX) {
-    if (wv >= SWAVES) {  // aux wave: the readout operands of its token block, if any
-      if constexpr (OUT) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldv8<V8>(p.Q + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          f.K[0][ks] = ldv8<V8>(p.P + cidx * BT * BT + frag_off(tb * 16 + m, ks * 32 + kq, BT));
-      }
-      return;
-    }
-  }
   const E* Wp = static_cast<const E*>(p.Wneg);
   const E* Kp = static_cast<const E*>(p.Kt);
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldv8<V8>(Wp + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
-  if constexpr (OUT && !AUX) {
+  if constexpr (OUT) {
     static_assert(!REV, "the readout runs in the forward S pass");
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) f.Q[ks] = ldv8<V8>(p.Q + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
@@ -395,30 +376,22 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
   // w = U + Wneg X0 (token block tb, each half).  The work that does not depend
   // on this chunk's w -- Gamma X (+ At1 B1) -- is issued alongside so the
   // independent MFMA chains overlap.
-  // The low and high halves accumulate in separate chains (summed at the end),
-  // so each dependent MFMA chain is half as long.
-  f4 acc[HALVES], acc2[HALVES], ao = zero4(), ao2 = zero4();
+  f4 acc[HALVES], ao = zero4();
 #pragma unroll
-  for (int h = 0; h < HALVES; ++h) {
+  for (int h = 0; h < HALVES; ++h)
     acc[h] = {s.Uf[tb * 16 + r4][h * 16 + m], s.Uf[tb * 16 + r4 + 1][h * 16 + m],
               s.Uf[tb * 16 + r4 + 2][h * 16 + m], s.Uf[tb * 16 + r4 + 3][h * 16 + m]};
-    acc2[h] = zero4();
-  }
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
     for (int h = 0; h < HALVES; ++h) {
       const V8 xh = ldv8<V8>(&s.Xh[h * 16 + m][ks * 32 + kq]);
       const V8 xl = ldv8<V8>(&s.Xl[h * 16 + m][ks * 32 + kq]);
-      acc2[h] = T::mma(cur.W[ks], xl, acc2[h]);
-      if constexpr (OUT) ao2 = T::mma(cur.Q[ks], xl, ao2);
+      acc[h] = T::mma(cur.W[ks], xl, acc[h]);
+      if constexpr (OUT) ao = T::mma(cur.Q[ks], xl, ao);
       acc[h] = T::mma(cur.W[ks], xh, acc[h]);
       if constexpr (OUT) ao = T::mma(cur.Q[ks], xh, ao);
     }
-#pragma unroll
-  for (int h = 0; h < HALVES; ++h)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[h][e] += acc2[h][e];
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
     const float4 g4 = *reinterpret_cast<const float4*>(&s.Gf[(SRB * w + q) * 16 + r4]);
@@ -466,31 +439,24 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
       wh[ks] = ldv8<V8>(&s.wh[h * 16 + m][ks * 32 + kq]);
       wl[ks] = ldv8<V8>(&s.wl[h * 16 + m][ks * 32 + kq]);
     }
-    f4 Y[SRB];
-#pragma unroll
-    for (int q = 0; q < SRB; ++q) {
-      Y[q] = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        Y[q] = T::mma(cur.K[q][ks], wl[ks], Y[q]);
-        X[q][h] = T::mma(cur.K[q][ks], wh[ks], X[q][h]);
-      }
-    }
-    if constexpr (OUT) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        ao2 = T::mma(cur.P[ks], wl[ks], ao2);
-        ao = T::mma(cur.P[ks], wh[ks], ao);
-      }
-    }
 #pragma unroll
     for (int q = 0; q < SRB; ++q)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) X[q][h][e] += Y[q][e];
+      for (int ks = 0; ks < 2; ++ks) {
+        X[q][h] = T::mma(cur.K[q][ks], wl[ks], X[q][h]);
+        X[q][h] = T::mma(cur.K[q][ks], wh[ks], X[q][h]);
+      }
+    if constexpr (OUT) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        ao = T::mma(cur.P[ks], wl[ks], ao);
+        ao = T::mma(cur.P[ks], wh[ks], ao);
+      }
+    }
   }
   if constexpr (OUT) {  // o rows of token block tb, staged for the next step's store
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s.of[tb * 16 + r4 + e][m] = ao[e] + ao2[e];
+    for (int e = 0; e < 4; ++e) s.of[tb * 16 + r4 + e][m] = ao[e];
   }
   // No closing barrier: the next step writes Xh / Xl / Xf / Uf / Gf, whose last
   // readers all ran before this step's second barrier, and writes wh / wl / wf
@@ -498,154 +464,8 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
   // has finished this step's reads of them.
 }
 
-// The same chunk step split between the two roles of an AUX workgroup.  Chain
-// waves (0-3): stage X0, w = U + Wneg X0 and Gamma X (+ At1 B1), stage w,
-// X += Kt w.  Aux waves (4-7, token block w - 4): the slot write-back from the
-// staged X0 and the readout's Q~ X0 between the two barriers, then the w
-// write-back, P w and the readout's store after the second.  Every staging
-// buffer an aux wave reads is written again only after the next barrier it
-// has to pass, so the step needs no third barrier.
 template <bool REV, bool OUT>
-__device__ __forceinline__ void state_step_aux(const StateParams& p, StateSmem<REV>& s, int n,
-                                               int ch, int tile,
-                                               const StateFrags<REV, OUT, true>& cur,
-                                               f4 (&X)[SRB][HALVES]) {
-  static_assert(HALVES == 1, "the aux roles assume 16-column tiles");
-  using T = StateT<REV>;
-  using E = typename T::E;
-  using V8 = typename T::V8;
-  using V4 = typename T::V4;
-  const int NS = p.NT + 1;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const bool chain = wv < SWAVES;
-  const int w = wv & (SWAVES - 1), l = lane_id(), m = l & 15, kq = (l >> 4) * 8, r4 = (l >> 4) * 4;
-  const int tb = w;
-  const int at = threadIdx.x - STHREADS;  // aux thread index (aux waves only)
-  const long long sidx = (long long)n * NS + ch;
-  const long long rowbase = (long long)n * p.Tp + (long long)ch * BT;
-  if (chain) {  // stage X0 split and transposed ([col][row]) for the B operand, fp32 for the slot
-#pragma unroll
-    for (int q = 0; q < SRB; ++q) {
-      const int row0 = (SRB * w + q) * 16 + r4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) s.Xf[row0 + e][m] = X[q][0][e];
-      stage_split4<E, V4>(&s.Xh[m][row0], &s.Xl[m][row0], X[q][0]);
-    }
-    *reinterpret_cast<float4*>(&s.Uf[threadIdx.x / (SCOLS / 4)][(threadIdx.x % (SCOLS / 4)) * 4]) = cur.U4;
-    if (threadIdx.x < KD / 4) *reinterpret_cast<float4*>(&s.Gf[threadIdx.x * 4]) = cur.G4;
-  }
-  __syncthreads();
-  f4 ao = zero4(), ao2 = zero4();
-  if (chain) {
-    // w = U + Wneg X0 (token block tb), low and high halves in separate chains
-    f4 acc, acc2 = zero4();
-    acc = {s.Uf[tb * 16 + r4][m], s.Uf[tb * 16 + r4 + 1][m], s.Uf[tb * 16 + r4 + 2][m],
-           s.Uf[tb * 16 + r4 + 3][m]};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const V8 xh = ldv8<V8>(&s.Xh[m][ks * 32 + kq]);
-      const V8 xl = ldv8<V8>(&s.Xl[m][ks * 32 + kq]);
-      acc2 = T::mma(cur.W[ks], xl, acc2);
-      acc = T::mma(cur.W[ks], xh, acc);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += acc2[e];
-#pragma unroll
-    for (int q = 0; q < SRB; ++q) {
-      const float4 g4 = *reinterpret_cast<const float4*>(&s.Gf[(SRB * w + q) * 16 + r4]);
-      const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
-      for (int e = 0; e < 4; ++e) X[q][0][e] *= gv[e];
-      if constexpr (REV) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-          X[q][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks], cur.B1[0][ks], X[q][0],
-                                                           0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s.wf[tb * 16 + r4 + e][m] = acc[e];
-    stage_split4<E, V4>(&s.wh[m][tb * 16 + r4], &s.wl[m][tb * 16 + r4], acc);
-  } else {
-    if (p.Xs) {  // slot write-back: 128 rows x 16 columns, four elements per piece
-      using S = typename StateT<REV>::Slot;
-      typedef S S4 __attribute__((ext_vector_type(4)));
-      constexpr int C4 = SCOLS / 4;
-#pragma unroll
-      for (int j = 0; j < KD * C4 / STHREADS; ++j) {
-        const int idx = at + j * STHREADS, row = idx / C4, c4 = idx % C4;
-        const float4 v = *reinterpret_cast<const float4*>(&s.Xf[row][c4 * 4]);
-        S4 o;
-        o[0] = (S)v.x; o[1] = (S)v.y; o[2] = (S)v.z; o[3] = (S)v.w;
-        *reinterpret_cast<S4*>(static_cast<S*>(p.Xs) + sidx * KD * KD + (long long)row * KD +
-                               tile * SCOLS + c4 * 4) = o;
-      }
-    }
-    if constexpr (OUT) {  // readout, first term: Q~ X0 (Q~ rows in cur.W)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const V8 xh = ldv8<V8>(&s.Xh[m][ks * 32 + kq]);
-        const V8 xl = ldv8<V8>(&s.Xl[m][ks * 32 + kq]);
-        ao2 = T::mma(cur.W[ks], xl, ao2);
-        ao = T::mma(cur.W[ks], xh, ao);
-      }
-    }
-  }
-  __syncthreads();
-  if (chain) {  // X += Kt w: the recurrence's critical path
-    V8 wh[2], wl[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      wh[ks] = ldv8<V8>(&s.wh[m][ks * 32 + kq]);
-      wl[ks] = ldv8<V8>(&s.wl[m][ks * 32 + kq]);
-    }
-    f4 Y[SRB];
-#pragma unroll
-    for (int q = 0; q < SRB; ++q) {
-      Y[q] = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        Y[q] = T::mma(cur.K[q][ks], wl[ks], Y[q]);
-        X[q][0] = T::mma(cur.K[q][ks], wh[ks], X[q][0]);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < SRB; ++q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) X[q][0][e] += Y[q][e];
-  } else {
-    {  // w write-back: 64 tokens x 16 columns, one 4-column piece per aux thread
-      constexpr int C4 = SCOLS / 4;
-      static_assert(BT * C4 == STHREADS, "one w piece per aux thread");
-      const int tok = at / C4, c4 = at % C4;
-      using WO = typename StateT<REV>::Wout;
-      WO* dst = static_cast<WO*>(p.wout) + (rowbase + tok) * KD + tile * SCOLS + c4 * 4;
-      const float4 v = *reinterpret_cast<const float4*>(&s.wf[tok][c4 * 4]);
-      typedef WO W4 __attribute__((ext_vector_type(4)));
-      W4 o;
-      o[0] = (WO)v.x; o[1] = (WO)v.y; o[2] = (WO)v.z; o[3] = (WO)v.w;
-      *reinterpret_cast<W4*>(dst) = o;
-    }
-    if constexpr (OUT) {  // readout, second term: P w (P rows in cur.K[0]); stored from registers
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const V8 wh = ldv8<V8>(&s.wh[m][ks * 32 + kq]);
-        const V8 wl = ldv8<V8>(&s.wl[m][ks * 32 + kq]);
-        ao2 = T::mma(cur.K[0][ks], wl, ao2);
-        ao = T::mma(cur.K[0][ks], wh, ao);
-      }
-      const int b = n / p.H, hh = n % p.H, col = tile * SCOLS + m;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = ch * BT + tb * 16 + r4 + e;
-        if (t < p.T && col < p.cols)
-          p.out[(((long long)b * p.T + t) * p.H + hh) * p.cols + col] = f2bf(ao[e] + ao2[e]);
-      }
-    }
-  }
-}
-
-template <bool REV, bool OUT, bool AUX>
-__global__ __launch_bounds__(state_threads<AUX>()) void k_state(StateParams p) {
+__global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   __shared__ __align__(16) StateSmem<REV> s;
   const int NS = p.NT + 1;  // state slots per sequence
   // Workgroups are dispatched round-robin over the 8 XCDs by linear id; when the
@@ -663,16 +483,14 @@ __global__ __launch_bounds__(state_threads<AUX>()) void k_state(StateParams p) {
       n = L / STILES;
     }
   }
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const bool chain = !AUX || wv < SWAVES;  // the state rows live in the chain waves
-  const int w = wv & (SWAVES - 1), l = lane_id(), m = l & 15, r4 = (l >> 4) * 4;
+  const int w = wave_id(), l = lane_id(), m = l & 15, r4 = (l >> 4) * 4;
   f4 X[SRB][HALVES];
   for (int q = 0; q < SRB; ++q)
     for (int h = 0; h < HALVES; ++h)
       for (int e = 0; e < 4; ++e) {
         const int row = (SRB * w + q) * 16 + r4 + e, col = tile * SCOLS + h * 16 + m;
         float x = 0.f;
-        if (chain && p.init && row < p.rows && col < p.cols)
+        if (p.init && row < p.rows && col < p.cols)
           x = p.init_transposed ? p.init[(long long)n * p.rows * p.cols + (long long)col * p.rows + row]
                                 : p.init[(long long)n * p.rows * p.cols + (long long)row * p.cols + col];
         X[q][h][e] = x;
@@ -686,31 +504,24 @@ __global__ __launch_bounds__(state_threads<AUX>()) void k_state(StateParams p) {
   // prefetches) so the compiler's wait counts only cover the buffer being
   // consumed; the last PF - 1 or fewer chunks run after the loop.
   auto clampc = [&](int it2) { return chunk_of(it2 < NT ? it2 : NT - 1); };
-  StateFrags<REV, OUT, AUX> f[PF];
-  auto step = [&](int ch, const StateFrags<REV, OUT, AUX>& cur) {
-    if constexpr (AUX)
-      state_step_aux<REV, OUT>(p, s, n, ch, tile, cur, X);
-    else
-      state_step<REV, OUT>(p, s, n, ch, tile, cur, X);
-  };
+  StateFrags<REV, OUT> f[PF];
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j) load_state_frags<REV, OUT, AUX>(p, n, clampc(j), tile, f[j]);
+  for (int j = 0; j < PF - 1; ++j) load_state_frags<REV, OUT>(p, n, clampc(j), tile, f[j]);
   int it = 0;
   for (; it + PF - 1 < NT; it += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      load_state_frags<REV, OUT, AUX>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
-      step(chunk_of(it + j), f[j]);
+      load_state_frags<REV, OUT>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
+      state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X);
     }
   }
 #pragma unroll
   for (int j = 0; j < PF - 1; ++j)
-    if (it + j < NT) step(chunk_of(it + j), f[j]);
-  if constexpr (OUT && !AUX) {  // the last chunk's readout
+    if (it + j < NT) state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X);
+  if constexpr (OUT) {  // the last chunk's readout
     __syncthreads();
     store_readout(p, s, n, NT - 1, tile);
   }
-  if (!chain) return;
   // final state (also kept as slot NT for the backward)
   for (int q = 0; q < SRB; ++q)
     for (int h = 0; h < HALVES; ++h)
@@ -729,17 +540,14 @@ __global__ __launch_bounds__(state_threads<AUX>()) void k_state(StateParams p) {
       }
 }
 
-// Which passes run with aux waves.
-constexpr bool AUX_REV = false, AUX_OUT = false, AUX_FWD = false;
-
 void launch_state(const char* name, const StateParams& sp, int nseq, hipStream_t st) {
-  const dim3 grid(STILES * nseq);
+  const dim3 grid(STILES * nseq), blk(STHREADS);
   if (sp.rev)
-    SD_LAUNCH(name, (k_state<true, false, AUX_REV>), grid, dim3(state_threads<AUX_REV>()), 0, st, sp);
+    SD_LAUNCH(name, (k_state<true, false>), grid, blk, 0, st, sp);
   else if (sp.out)
-    SD_LAUNCH(name, (k_state<false, true, AUX_OUT>), grid, dim3(state_threads<AUX_OUT>()), 0, st, sp);
+    SD_LAUNCH(name, (k_state<false, true>), grid, blk, 0, st, sp);
   else
-    SD_LAUNCH(name, (k_state<false, false, AUX_FWD>), grid, dim3(state_threads<AUX_FWD>()), 0, st, sp);
+    SD_LAUNCH(name, (k_state<false, false>), grid, blk, 0, st, sp);
 }
 
 // ---------------------------------------------------------------------------
