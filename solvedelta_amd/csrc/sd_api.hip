@@ -105,8 +105,7 @@ BwdWs carve_bwd(void* base, int B, int T, int H, size_t* total) {
   w.dd = c.take<bpan_t>(panel);
   w.ddelta = w.dwS;
   w.dwC = w.dwS;
-  w.uh = c.take<fpan_t>(panel);
-  w.kh = c.take<fpan_t>(panel);
+  w.rn = c.take<float>(n * Tp * 2);
   w.Pp = c.take<float>(n * NT * kBT * kBT);
   if (total) *total = c.off + 256;
   return w;

@@ -442,7 +442,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
   // M1_ij = dw_i . w_j (j < i)
-  lds_pair(&s.PA, (const float*)nullptr, s.PW, s.M1, true);
+  lds_pair(s.PA, s.PW, s.M1, true);
   // a = dw X0^T for this wave's column block (K = 128)
   f4 a[NB], bq[NB], kl[NB];
   BlkS BX;
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   stage_dout_panel(s.PA, p, b, t0, hh);
   __syncthreads();
   // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T;  kl = w lam^T
-  lds_pair(&s.PA, (const float*)nullptr, s.PW, s.M2, false);
+  lds_pair(s.PA, s.PW, s.M2, false);
   {
     BlkS BL;
     load_lam_rowsum(lam, XC, cb, BL, s.rsum);
@@ -774,9 +774,15 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
-      l2norm16(ux[g]);
+      const float ru = l2norm16(ux[g]);
       const float rk = l2norm16(kx[g]);
-      if ((l & 15) == 0) s.krs[i] = rk;
+      if ((l & 15) == 0) {
+        s.krs[i] = rk;
+        // the C chunk gradient scales the raw rows by these (0 past T)
+        const bool tv = t0 + i < p.T;
+        *reinterpret_cast<float2*>(p.g.rn + (rowbase + i) * 2) =
+            make_float2(tv ? ru : 0.f, tv ? rk : 0.f);
+      }
 #pragma unroll
       for (int q = 0; q < RQ; ++q) {
         s.Uh[i][cl + 16 * q] = ux[g][q];
@@ -886,18 +892,6 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     store_frag_panel1<BT, KD>(p.g.Wk, rowbase * KD,
                              [&](int i, int c) { return Wst[i * KD + c]; });
   }
-  for (int idx = threadIdx.x * 8; idx < BT * KD; idx += CT * 8) {  // 16-byte pieces
-    const int i = idx / KD, c = idx % KD;
-    typedef fpan_t P8 __attribute__((ext_vector_type(8)));
-    P8 kv, uv;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      kv[e] = (fpan_t)s.Kh[i][c + e];
-      uv[e] = (fpan_t)s.Uh[i][c + e];
-    }
-    *reinterpret_cast<P8*>(p.g.kh + (rowbase + i) * KD + c) = kv;
-    *reinterpret_cast<P8*>(p.g.uh + (rowbase + i) * KD + c) = uv;
-  }
   // chunk-transposed panels, fragment order
   // The reverse pass's injection sum_i At1_ci Kh_i,col is formed as
   // sum_i (At1_ci / |k_i|) k_i,col: its B operand is then the raw key input,
@@ -1005,10 +999,49 @@ struct GradCSmem {
   float M1[BT * LS];
   float M2[BT * LS];
   float gam[BT];      // erase-side gamma: 0 on fresh tokens
+  float rn[BT][2];    // 1 / |u_i|, 1 / |k_i| (0 past T)
   float rsum[4][KD];  // rowsum(X_C (.) lambda) partials
   LPanel PA;  // dw, then dd e^G
   LPanel PW;  // delta
 };
+
+// Normalised u / k of the C chunk gradient, from the raw inputs and the norms
+// the backward prep stored: one element (row j of the chunk, column c), and
+// the 16 x 128 block of rows j0 .. j0+15 as split MFMA fragments (VEC: 16-byte
+// row pieces; the element form reads the same values one by one).
+__device__ __forceinline__ float norm_elem(const sd_view& v, int b, int hh, int t, int T, int r,
+                                          int c, float rn) {
+  const float x = bf2f(brow(v, b, t < T ? t : T - 1, hh)[c < r ? c : r - 1]);
+  return keep_if(t < T && c < r, x) * rn;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void norm_blk(const sd_view& v, int b, int hh, int t0, int T, int r,
+                                         const float (&rn)[BT][2], int which, int j0, BlkS& o) {
+  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8, t = t0 + j0 + m;
+  const __bf16* row = brow(v, b, t < T ? t : T - 1, hh);
+  const float sc = rn[j0 + m][which];
+  Blk raw;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int c0 = ks * 32 + kq;
+    float x[8];
+    if constexpr (VEC) {
+      const bf16x8 pv = *reinterpret_cast<const bf16x8*>(row + (c0 < r ? c0 : r - 8));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = keep_if(t < T && c0 < r, bf2f(pv[e])) * sc;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = c0 + e;
+        x[e] = keep_if(t < T && c < r, bf2f(row[c < r ? c : r - 1])) * sc;
+      }
+    }
+    raw.v[ks][0] = make_float4(x[0], x[1], x[2], x[3]);
+    raw.v[ks][1] = make_float4(x[4], x[5], x[6], x[7]);
+  }
+  split_blk(raw, o);
+}
 
 template <bool VEC>
 __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
@@ -1021,8 +1054,6 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   const bpan_t* dw = p.g.dwC + rowbase * KD;
   const fpan_t* wv = p.f.delta + rowbase * KD;
   const bpan_t* ddp = p.g.dd + rowbase * KD;  // cotangent of the C-op output
-  const fpan_t* kh = p.g.kh + rowbase * KD;  // normalised keys
-  const fpan_t* uh = p.g.uh + rowbase * KD;  // normalised u
   const fpan_t* dprim = p.f.d + rowbase * KD;  // d = k + output
   const xslot_t* X0 = p.f.Xc + sidx * KD * KD;
   const xslot_t* XC = X0 + KD * KD;
@@ -1035,6 +1066,8 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
                                                       (long long)hh * p.in.gamma.sh];
       s.gam[threadIdx.x] = keep_if(t < p.T, gv) * erase_keep(p.in, b, t < p.T ? t : p.T - 1);
     }
+    *reinterpret_cast<float2*>(s.rn[threadIdx.x]) =
+        *reinterpret_cast<const float2*>(p.g.rn + (rowbase + threadIdx.x) * 2);
   }
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
@@ -1047,8 +1080,9 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   load_blk(bLam, lam + cb * 16 * KD, KD);
   load_blk(bXC, XC + cb * 16 * KD, KD);
   // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
-  lds_pair(&s.PA, (const float*)nullptr, s.PW, s.M1, true);
-  lds_pair(nullptr, kh, s.PW, s.M2, false);
+  lds_pair(s.PA, s.PW, s.M1, true);
+  lds_pair_fn([&](int I, BlkS& a) { norm_blk<VEC>(p.in.k, b, hh, t0, p.T, p.r, s.rn, 1, I * BS, a); },
+              s.PW, s.M2, false);
   f4 a[NB], kl[NB];
   {
     BlkS BX, BL;
@@ -1063,14 +1097,23 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       kl[I] = mma_blks(A, BL, zero4());
     }
   }
+  // normalised u / k at row j of the chunk, column cc
+  auto U = [&](int j, int cc) { return norm_elem(p.in.u, b, hh, t0 + j, p.T, p.r, cc, s.rn[j][0]); };
+  auto Kn = [&](int j, int cc) { return norm_elem(p.in.k, b, hh, t0 + j, p.T, p.r, cc, s.rn[j][1]); };
   float Su[NB][4], Sdd[NB][4], Sod[NB][4];
-  load_slab(Su, uh, cb);
+#pragma unroll
+  for (int J = 0; J < NB; ++J)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Su[J][e] = U(J * BS + r4 + e, c);
   load_slab(Sdd, ddp, cb);
   {  // the C-op output o = d - k enters only as o (.) dd: formed at once, so
      // neither slab stays live through the applies
     float Sk[NB][4];
     load_slab(Sod, dprim, cb);
-    load_slab(Sk, kh, cb);
+#pragma unroll
+    for (int J = 0; J < NB; ++J)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Sk[J][e] = Kn(J * BS + r4 + e, c);
 #pragma unroll
     for (int J = 0; J < NB; ++J)
 #pragma unroll
@@ -1091,8 +1134,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   __syncthreads();  // M1, M2 complete; PA free
   // PA <- dd e^G for the dq product (staged now, consumed after the applies)
   stage_panel(s.PA, ddp, [&](int i, int cc) { return __expf(cd.G[i][cc]); });
-  auto U = [&](int j, int cc) { return (float)uh[j * KD + cc]; };
-  auto Xg = [&](int j, int cc) { return s.gam[j] * (float)uh[j * KD + cc]; };
+  auto Xg = [&](int j, int cc) { return s.gam[j] * U(j, cc); };
   auto DO = [&](int j, int cc) { return (float)ddp[j * KD + cc]; };
   float Sx[NB][4];
 #pragma unroll

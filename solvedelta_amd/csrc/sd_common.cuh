@@ -933,18 +933,16 @@ __device__ __forceinline__ void load_split_blk_g(const E* rows, BlkS& o) {
 }
 
 // Pair matrix M = A Y^T over K = 128 (strict: j < i, else j <= i), Y from an LDS
-// panel and A from an LDS panel (Ag == nullptr) or a global fp32 panel.
-template <class EG>
-__device__ void lds_pair(const LPanel* A, const EG* Ag, const LPanel& Y, float* M, bool strict) {
+// panel, A from load_a (lds_pair: another LDS panel).
+// The A block of rows I*16 .. I*16+15 comes from load_a(I, a).
+template <class LoadA>
+__device__ void lds_pair_fn(LoadA&& load_a, const LPanel& Y, float* M, bool strict) {
   const int w = wave_id();
   for (int pp = w; pp < 10; pp += CW) {
     int I = 0, J = pp;
     while (J > I) { J -= I + 1; ++I; }
     BlkS a, y;
-    if (Ag)
-      load_split_blk_g(Ag + I * BS * KD, a);
-    else
-      lblk(*A, I * BS, a);
+    load_a(I, a);
     lblk(Y, J * BS, y);
     const f4 r = mma_blks(a, y, zero4());
 #pragma unroll
@@ -957,6 +955,10 @@ __device__ void lds_pair(const LPanel* A, const EG* Ag, const LPanel& Y, float* 
     const int i = idx / BT, j = idx % BT;
     if ((j / BS) > (i / BS)) M[i * LS + j] = 0.f;
   }
+}
+
+__device__ __forceinline__ void lds_pair(const LPanel& A, const LPanel& Y, float* M, bool strict) {
+  lds_pair_fn([&](int I, BlkS& a) { lblk(A, I * BS, a); }, Y, M, strict);
 }
 
 

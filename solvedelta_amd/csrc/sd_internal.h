@@ -142,8 +142,7 @@ struct BwdWs {
   bpan_t* dwS; bpan_t* dwC;         // dw of each op           [n][Tp][128]
   bpan_t* de; bpan_t* dchi; bpan_t* dd;
   bpan_t* ddelta;  // shares dw_S's storage (written in place by the sources transpose)
-  fpan_t* uh;  // normalised u
-  fpan_t* kh;  // normalised keys
+  float* rn;  // 1 / |u_t|, 1 / |k_t| of every token (0 past T)       [n][Tp][2]
   float* Pp;  // P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic} (i <= l) of the C op  [n][NT][64][64]
 };
 
