@@ -646,6 +646,13 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   __syncthreads();
   // d = k + e^G (X0 k) + sum_j M_ij u_j e^{G_i - G_j}  (this wave's column block)
   const xslot_t* X0 = p.Xc + ((long long)n * (p.NT + 1) + ch) * KD * KD;
+  // The sources phase's rows (delta, q, erase, v, write_raw) are loaded before
+  // the apply as raw 16-bit values (clamped addresses, masked when converted),
+  // so their latency overlaps it.
+  constexpr int RPW = BT / CW;
+  // two 16-bit values per register: element q of a row in the low half of
+  // word q / 2 (even q) or its high half (odd q)
+  unsigned dq_r[2][RQ / 2], qq_r[2][RQ / 2], er_r[2][RQ / 2], vx_r[RPW], wx_r[RPW];
   {
     const int cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
     BlkS BX;
@@ -669,6 +676,34 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       lblk(s.Kp, I * BS, A);
       a1[I] = mma_blks(A, BX, zero4());
     }
+    {
+      const int cl = l & 15;
+      auto raw = [](const void* base, long long idx) -> unsigned {
+        return static_cast<const unsigned short*>(base)[idx];
+      };
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int i = row16(w, g), t = t0 + i, tc = t < T ? t : T - 1;
+        const __bf16* qrow = vrow(in.q, b, tc, hh);
+        const __bf16* erow = vrow(in.erase_raw, b, tc, hh);
+#pragma unroll
+        for (int q2 = 0; q2 < RQ / 2; ++q2) {
+          const int c0 = cl + 32 * q2, c1 = c0 + 16;
+          const int cc0 = c0 < r ? c0 : r - 1, cc1 = c1 < r ? c1 : r - 1;
+          dq_r[g][q2] = raw(delta, i * KD + c0) | raw(delta, i * KD + c1) << 16;
+          qq_r[g][q2] = raw(qrow, cc0) | raw(qrow, cc1) << 16;
+          er_r[g][q2] = raw(erow, cc0) | raw(erow, cc1) << 16;
+        }
+      }
+#pragma unroll
+      for (int rr = 0; rr < RPW; ++rr) {
+        const int t = t0 + w + rr * CW, tc = t < T ? t : T - 1;
+        const __bf16* vr = vrow(in.v, b, tc, hh);
+        const __bf16* wr = vrow(in.write_raw, b, tc, hh);
+        vx_r[rr] = raw(vr, l < V ? l : V - 1) | raw(vr, l + 64 < V ? l + 64 : V - 1) << 16;
+        wx_r[rr] = raw(wr, l < V ? l : V - 1) | raw(wr, l + 64 < V ? l + 64 : V - 1) << 16;
+      }
+    }
     __syncthreads();  // the split keys are dead: d is formed in their place
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
@@ -682,26 +717,35 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     }
   }
   __syncthreads();
-  // sources (16-lane row layout; e overwrites u, chi overwrites k).  Both row
-  // groups' delta, q and erase are loaded before the first row is processed:
-  // the rows' global stores would otherwise hold the next rows' loads behind them.
-  constexpr int RPW = BT / CW;
+  // sources (16-lane row layout; e overwrites u, chi overwrites k), from the
+  // rows loaded before the apply
   float zz[RPW][2];
   {
     const int cl = l & 15;
     float dq_[2][RQ], qq_[2][RQ], er_[2][RQ], vx[RPW][2], wx[RPW][2];
+    // the half of a packed word as fp16 / bf16
+    auto h2f = [](unsigned x, int hi) {
+      return (float)__builtin_bit_cast(_Float16, (unsigned short)(hi ? x >> 16 : x));
+    };
+    auto b2f = [](unsigned x, int hi) { return __uint_as_float(hi ? x & 0xffff0000u : x << 16); };
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      const int i = row16(w, g), t = t0 + i;
+      const bool tv = t0 + row16(w, g) < T;
 #pragma unroll
-      for (int q = 0; q < RQ; ++q) dq_[g][q] = (float)delta[i * KD + cl + 16 * q];
-      load_row16(in.q, b, t, hh, T, r, qq_[g]);
-      load_row16(in.erase_raw, b, t, hh, T, r, er_[g]);
+      for (int q = 0; q < RQ; ++q) {
+        const bool ok = tv && cl + 16 * q < r;
+        dq_[g][q] = h2f(dq_r[g][q / 2], q & 1);
+        qq_[g][q] = keep_if(ok, b2f(qq_r[g][q / 2], q & 1));
+        er_[g][q] = keep_if(ok, b2f(er_r[g][q / 2], q & 1));
+      }
     }
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
-      load_row2(in.v, b, t0 + w + rr * CW, hh, T, V, vx[rr][0], vx[rr][1]);
-      load_row2(in.write_raw, b, t0 + w + rr * CW, hh, T, V, wx[rr][0], wx[rr][1]);
+      const bool tv = t0 + w + rr * CW < T;
+      vx[rr][0] = keep_if(tv && l < V, b2f(vx_r[rr], 0));
+      vx[rr][1] = keep_if(tv && l + 64 < V, b2f(vx_r[rr], 1));
+      wx[rr][0] = keep_if(tv && l < V, b2f(wx_r[rr], 0));
+      wx[rr][1] = keep_if(tv && l + 64 < V, b2f(wx_r[rr], 1));
     }
     {  // d to global memory only now, from this thread's own LDS entries: stored
        // before the loads above, it would have held them (one counter retires both)
