@@ -238,9 +238,11 @@ __device__ __forceinline__ bf16x8 ldb8(const __bf16* p) { return *reinterpret_ca
 template <class V8, class E>
 __device__ __forceinline__ V8 ldv8(const E* p) { return *reinterpret_cast<const V8*>(p); }
 
+// part < 0 loads every fragment; parts 0 / 1 / 2 are the W (+ readout) / K (+ B1) /
+// At1 groups, issued at three points of a step so the loads do not queue up at once.
 template <bool REV, bool OUT>
 __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
-                                                 StateFrags<REV, OUT>& f) {
+                                                 StateFrags<REV, OUT>& f, int part = -1) {
   using E = typename StateT<REV>::E;
   using V8 = typename StateT<REV>::V8;
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
@@ -250,6 +252,7 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
   const long long wb = rowbase * KD;
   const E* Wp = static_cast<const E*>(p.Wneg);
   const E* Kp = static_cast<const E*>(p.Kt);
+  if (part <= 0) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldv8<V8>(Wp + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
   if constexpr (OUT) {
@@ -260,23 +263,29 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
     for (int ks = 0; ks < 2; ++ks)
       f.P[ks] = ldv8<V8>(p.P + cidx * BT * BT + frag_off(tb * 16 + m, ks * 32 + kq, BT));
   }
+  }
+  if (part < 0 || part == 1) {
 #pragma unroll
   for (int q = 0; q < SRB; ++q)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
       f.K[q][ks] = ldv8<V8>(Kp + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
-  {
+  }
+  if (part <= 0) {
     constexpr int C4 = SCOLS / 4;
     static_assert(BT * C4 == STHREADS, "one U piece per thread");
     f.U4 = ld4(p.U + (rowbase + threadIdx.x / C4) * KD + tile * SCOLS + (threadIdx.x % C4) * 4);
+    f.G4 = ld4(p.Gam + cidx * KD + (l & 31) * 4);
   }
-  f.G4 = ld4(p.Gam + cidx * KD + (l & 31) * 4);
   if constexpr (REV) {
+    if (part < 0 || part == 2) {
 #pragma unroll
     for (int q = 0; q < SRB; ++q)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         f.A1[q][ks] = ldb8(p.At1 + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
+    }
+    if (part < 0 || part == 1)
 #pragma unroll
     for (int h = 0; h < HALVES; ++h)
 #pragma unroll
@@ -329,10 +338,11 @@ __device__ __forceinline__ void store_readout(const StateParams& p, const StateS
 // With OUT (forward S pass) the step also forms the chunk's readout
 // o = Q~ X0 + P w for its 16 columns: wave w's token block, from the X0 and w
 // fragments the recurrence loads anyway; o is off the recurrence's critical path.
-template <bool REV, bool OUT>
+template <bool REV, bool OUT, class Prefetch>
 __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>& s, int n, int ch,
                                            int tile, const StateFrags<REV, OUT>& cur,
-                                           f4 (&X)[SRB][HALVES]) {
+                                           f4 (&X)[SRB][HALVES], Prefetch&& prefetch) {
+  prefetch(0);
   static_assert(!OUT || HALVES == 1, "readout tiles are 16 columns wide");
   using T = StateT<REV>;
   using E = typename T::E;
@@ -356,6 +366,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
   *reinterpret_cast<float4*>(&s.Uf[threadIdx.x / (SCOLS / 4)][(threadIdx.x % (SCOLS / 4)) * 4]) = cur.U4;
   if (threadIdx.x < KD / 4) *reinterpret_cast<float4*>(&s.Gf[threadIdx.x * 4]) = cur.G4;
   __syncthreads();
+  prefetch(1);
   if (p.Xs) {  // slot write-back: 128 rows x SCOLS columns, four elements per piece
     using S = typename StateT<REV>::Slot;
     typedef S S4 __attribute__((ext_vector_type(4)));
@@ -414,6 +425,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
     stage_split4<E, V4>(&s.wh[h * 16 + m][tb * 16 + r4], &s.wl[h * 16 + m][tb * 16 + r4], acc[h]);
   }
   __syncthreads();
+  prefetch(2);
   {  // w write-back: 64 tokens x SCOLS columns as float4 pieces
     constexpr int C4 = SCOLS / 4;
     static_assert(BT * C4 == STHREADS, "one w piece per thread");
@@ -511,13 +523,22 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   for (; it + PF - 1 < NT; it += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      load_state_frags<REV, OUT>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
-      state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X);
+      // the S forward pass (with the readout's operands) measured faster with
+      // all of a chunk's loads issued before the step, the other passes with
+      // them spread over the step
+      if constexpr (OUT) {
+        load_state_frags<REV, OUT>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
+        state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X, [](int) {});
+      } else {
+        state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X, [&](int part) {
+          load_state_frags<REV, OUT>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF], part);
+        });
+      }
     }
   }
 #pragma unroll
   for (int j = 0; j < PF - 1; ++j)
-    if (it + j < NT) state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X);
+    if (it + j < NT) state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X, [](int) {});
   if constexpr (OUT) {  // the last chunk's readout
     __syncthreads();
     store_readout(p, s, n, NT - 1, tile);
