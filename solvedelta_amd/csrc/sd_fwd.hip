@@ -238,11 +238,13 @@ __device__ __forceinline__ bf16x8 ldb8(const __bf16* p) { return *reinterpret_ca
 template <class V8, class E>
 __device__ __forceinline__ V8 ldv8(const E* p) { return *reinterpret_cast<const V8*>(p); }
 
-// part < 0 loads every fragment; parts 0 / 1 / 2 are the W (+ readout) / K (+ B1) /
-// At1 groups, issued at three points of a step so the loads do not queue up at once.
+// Fragment groups of a chunk, loaded by mask so a pass can spread its loads
+// over a step (a burst of them stalls the wave at issue).
+enum : unsigned { FW = 1, FUG = 2, FK = 4, FQ = 8, FP = 16, FA1 = 32, FB1 = 64, FALL = 127 };
+
 template <bool REV, bool OUT>
 __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, int ch, int tile,
-                                                 StateFrags<REV, OUT>& f, int part = -1) {
+                                                 StateFrags<REV, OUT>& f, unsigned mask) {
   using E = typename StateT<REV>::E;
   using V8 = typename StateT<REV>::V8;
   const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
@@ -252,48 +254,62 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
   const long long wb = rowbase * KD;
   const E* Wp = static_cast<const E*>(p.Wneg);
   const E* Kp = static_cast<const E*>(p.Kt);
-  if (part <= 0) {
+  if (mask & FW)
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldv8<V8>(Wp + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
+    for (int ks = 0; ks < 4; ++ks) f.W[ks] = ldv8<V8>(Wp + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
   if constexpr (OUT) {
     static_assert(!REV, "the readout runs in the forward S pass");
+    if (mask & FQ)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) f.Q[ks] = ldv8<V8>(p.Q + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
+      for (int ks = 0; ks < 4; ++ks) f.Q[ks] = ldv8<V8>(p.Q + wb + frag_off(tb * 16 + m, ks * 32 + kq, KD));
+    if (mask & FP)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      f.P[ks] = ldv8<V8>(p.P + cidx * BT * BT + frag_off(tb * 16 + m, ks * 32 + kq, BT));
+      for (int ks = 0; ks < 2; ++ks)
+        f.P[ks] = ldv8<V8>(p.P + cidx * BT * BT + frag_off(tb * 16 + m, ks * 32 + kq, BT));
   }
-  }
-  if (part < 0 || part == 1) {
+  if (mask & FK)
 #pragma unroll
-  for (int q = 0; q < SRB; ++q)
+    for (int q = 0; q < SRB; ++q)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      f.K[q][ks] = ldv8<V8>(Kp + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
-  }
-  if (part <= 0) {
+      for (int ks = 0; ks < 2; ++ks)
+        f.K[q][ks] = ldv8<V8>(Kp + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
+  if (mask & FUG) {
     constexpr int C4 = SCOLS / 4;
     static_assert(BT * C4 == STHREADS, "one U piece per thread");
     f.U4 = ld4(p.U + (rowbase + threadIdx.x / C4) * KD + tile * SCOLS + (threadIdx.x % C4) * 4);
     f.G4 = ld4(p.Gam + cidx * KD + (l & 31) * 4);
   }
   if constexpr (REV) {
-    if (part < 0 || part == 2) {
+    if (mask & FA1)
 #pragma unroll
-    for (int q = 0; q < SRB; ++q)
+      for (int q = 0; q < SRB; ++q)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        f.A1[q][ks] = ldb8(p.At1 + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
-    }
-    if (part < 0 || part == 1)
+        for (int ks = 0; ks < 2; ++ks)
+          f.A1[q][ks] = ldb8(p.At1 + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
+    if (mask & FB1)
 #pragma unroll
-    for (int h = 0; h < HALVES; ++h)
+      for (int h = 0; h < HALVES; ++h)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        f.B1[h][ks] =
-            ldb8(p.B1 + cidx * KD * BT + frag_off(tile * SCOLS + h * 16 + m, ks * 32 + kq, BT));
+        for (int ks = 0; ks < 2; ++ks)
+          f.B1[h][ks] =
+              ldb8(p.B1 + cidx * KD * BT + frag_off(tile * SCOLS + h * 16 + m, ks * 32 + kq, BT));
   }
 }
+
+// Where a pass issues the next chunk's fragment groups: before the step
+// (pre) and at its three phases (after its start, after the first barrier,
+// after the second).  Measured per pass on MI355X.
+template <bool REV, bool OUT> struct LoadPlan;
+template <> struct LoadPlan<false, false> {  // C forward
+  static constexpr unsigned pre = 0, part[3] = {FW | FUG, FK, 0};
+};
+template <> struct LoadPlan<false, true> {  // S forward with the readout: one burst before
+  // the step (spreading its groups over the phases measured 1-3 us slower)
+  static constexpr unsigned pre = FALL, part[3] = {0, 0, 0};
+};
+template <> struct LoadPlan<true, false> {  // reverse passes
+  static constexpr unsigned pre = 0, part[3] = {FW | FUG, FK | FB1, FA1};
+};
 
 // Splits four fp32 values into high / low halves of type E and stores each as
 // one 8-byte piece.
@@ -518,22 +534,17 @@ __global__ __launch_bounds__(STHREADS) void k_state(StateParams p) {
   auto clampc = [&](int it2) { return chunk_of(it2 < NT ? it2 : NT - 1); };
   StateFrags<REV, OUT> f[PF];
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j) load_state_frags<REV, OUT>(p, n, clampc(j), tile, f[j]);
+  for (int j = 0; j < PF - 1; ++j) load_state_frags<REV, OUT>(p, n, clampc(j), tile, f[j], FALL);
   int it = 0;
   for (; it + PF - 1 < NT; it += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      // the S forward pass (with the readout's operands) measured faster with
-      // all of a chunk's loads issued before the step, the other passes with
-      // them spread over the step
-      if constexpr (OUT) {
-        load_state_frags<REV, OUT>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF]);
-        state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X, [](int) {});
-      } else {
-        state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X, [&](int part) {
-          load_state_frags<REV, OUT>(p, n, clampc(it + j + PF - 1), tile, f[(j + PF - 1) % PF], part);
-        });
-      }
+      using LP = LoadPlan<REV, OUT>;
+      const int nb = (j + PF - 1) % PF, nch = clampc(it + j + PF - 1);
+      if constexpr (LP::pre != 0) load_state_frags<REV, OUT>(p, n, nch, tile, f[nb], LP::pre);
+      state_step<REV, OUT>(p, s, n, chunk_of(it + j), tile, f[j], X, [&](int part) {
+        if (LP::part[part] != 0) load_state_frags<REV, OUT>(p, n, nch, tile, f[nb], LP::part[part]);
+      });
     }
   }
 #pragma unroll
