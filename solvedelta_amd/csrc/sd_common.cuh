@@ -494,66 +494,93 @@ __device__ __forceinline__ f4 mma16s(const float* av, const float* bv, f4 acc) {
   return acc;
 }
 
-// (I + L)^{-1} for strictly-lower L (64x64, stride LS), in place -> A.
-// Diagonal 16x16 blocks by forward substitution (one lane per column), then
-// off-diagonal blocks A_IJ = -A_II * sum_{K=J}^{I-1} L_IK A_KJ by distance.
-// tmp: 64 x LS scratch.
+// (I + L)^{-1} for strictly-lower L (64x64, stride LS, upper blocks zero), in
+// place -> A, with four barriers.  Diagonal 16x16 blocks D_B by forward
+// substitution (one lane per column), written over L's diagonal blocks; then
+// the 2x2 block recursion, one wave per 16x16 block on the K=16 MFMA:
+//   level 1: A10 = -D1 L10 D0,  A32 = -D3 L32 D2            (over L10, L32)
+//   level 2: X = L[23][01] Inv01:  X20 = L20 D0 + L21 A10, X21 = L21 D1,
+//            X30 = L30 D0 + L31 A10, X31 = L31 D1            (staged in tmp)
+//   level 3: A[23][01] = -Inv23 X: A20 = -D2 X20, A21 = -D2 X21,
+//            A30 = -(A32 X20 + D3 X30), A31 = -(A32 X21 + D3 X31)
+// A block a wave overwrites is read only by that wave, and its LDS reads are
+// drained (lgkmcnt) before the write.  The MFMA output layout (lane: rows
+// (lane>>4)*4+e, column lane&15) is the K=16 B-operand layout, so a product
+// feeds the next one from registers.  tmp: 64 x LS scratch.
 __device__ void unit_lower_inverse(float* L, float* tmp) {
   const int tid = threadIdx.x;
-  // Phase 0: diagonal blocks.  Thread (B, j): block B = tid/16 (tid < 64), column j.
-  float col[BS];
+  const int wv = tid >> 6, l = tid & 63, m = l & 15, r4 = (l >> 4) * 4;
+  // rows m of block (I, K) of a matrix, columns r4..r4+3 (A operand) / rows
+  // r4..r4+3 of block (K, J), column m (B operand)
+  auto rowseg = [&](const float* X, int I, int K, float (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = X[(I * BS + m) * LS + K * BS + r4 + e];
+  };
+  auto colseg = [&](const float* X, int K, int J, float (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = X[(K * BS + r4 + e) * LS + J * BS + m];
+  };
+  auto put = [&](float* X, int I, int J, f4 v, float sign) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) X[(I * BS + r4 + e) * LS + J * BS + m] = sign * v[e];
+  };
+  auto drain = [] { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+  // diagonal blocks: thread (B, j), block B = tid / 16 (tid < 64), column j
   if (tid < NB * BS) {
     const int B = tid / BS, j = tid % BS, B0 = B * BS;
+    float col[BS];
 #pragma unroll
     for (int i = 0; i < BS; ++i) {  // compile-time indices keep col[] in registers
-      float s = (i == j) ? 1.f : 0.f;
+      float sum = (i == j) ? 1.f : 0.f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) s -= L[(B0 + i) * LS + B0 + m] * col[m];
-      col[i] = (i >= j) ? s : 0.f;
+      for (int q = 0; q < i; ++q) sum -= L[(B0 + i) * LS + B0 + q] * col[q];
+      col[i] = (i >= j) ? sum : 0.f;
     }
+    drain();
+#pragma unroll
+    for (int i = 0; i < BS; ++i) L[(B0 + i) * LS + B0 + j] = col[i];
   }
   __syncthreads();
-  if (tid < NB * BS) {
-    const int B = tid / BS, j = tid % BS, B0 = B * BS;
-    for (int i = 0; i < BS; ++i) tmp[(B0 + i) * LS + B0 + j] = col[i];
+  if (wv < 2) {  // level 1
+    const int J = 2 * wv, I = J + 1;
+    float av[4], bv[4];
+    rowseg(L, I, J, av);
+    colseg(L, J, J, bv);
+    const f4 t = mma16s(av, bv, zero4());
+    rowseg(L, I, I, av);
+    const float tv[4] = {t[0], t[1], t[2], t[3]};
+    const f4 a = mma16s(av, tv, zero4());
+    drain();
+    put(L, I, J, a, -1.f);
   }
   __syncthreads();
-  // tmp holds the diagonal inverses; L still holds the strict lower part.
-  // Off-diagonal blocks by distance, one wave per block, on the K=16 MFMA:
-  //   T = sum_{K=J}^{I-1} L_IK A_KJ,   A_IJ = -A_II T.
-  // The MFMA output layout (lane: rows (lane>>4)*4+e, column lane&15) is the
-  // K=16 B-operand layout, so T feeds the second product from registers.
-  for (int dist = 1; dist < NB; ++dist) {
-    const int wv = tid >> 6;
-    if (wv < NB - dist) {
-      const int J = wv, I = J + dist;
-      const int l = tid & 63, m = l & 15, r4 = (l >> 4) * 4;
-      f4 t = zero4();
-      for (int K = J; K < I; ++K) {
-        float av[4], bv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          av[e] = L[(I * BS + m) * LS + K * BS + r4 + e];
-          bv[e] = tmp[(K * BS + r4 + e) * LS + J * BS + m];
-        }
-        t = mma16s(av, bv, t);
-      }
-      float av[4], bv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        av[e] = tmp[(I * BS + m) * LS + I * BS + r4 + e];
-        bv[e] = t[e];
-      }
-      const f4 a = mma16s(av, bv, zero4());
-#pragma unroll
-      for (int e = 0; e < 4; ++e) tmp[(I * BS + r4 + e) * LS + J * BS + m] = -a[e];
+  if (wv < 4) {  // level 2: X(I, J) for I = 2 + wv / 2, J = wv % 2
+    const int I = 2 + wv / 2, J = wv % 2;
+    float av[4], bv[4];
+    rowseg(L, I, J, av);
+    colseg(L, J, J, bv);  // D_J
+    f4 x = mma16s(av, bv, zero4());
+    if (J == 0) {  // + L_I1 A10
+      rowseg(L, I, 1, av);
+      colseg(L, 1, 0, bv);
+      x = mma16s(av, bv, x);
     }
-    __syncthreads();
+    put(tmp, I, J, x, 1.f);
   }
-  // Copy back: A lower (incl. diagonal), zero upper.
-  for (int idx = tid; idx < BT * BT; idx += CT) {
-    const int i = idx / BT, j = idx % BT;
-    L[i * LS + j] = (j / BS <= i / BS) ? tmp[i * LS + j] : 0.f;
+  __syncthreads();
+  if (wv < 4) {  // level 3: A(I, J) = -(A_I2 X2J [I = 3] + D_I X_IJ)
+    const int I = 2 + wv / 2, J = wv % 2;
+    float av[4], bv[4];
+    f4 a = zero4();
+    if (I == 3) {
+      rowseg(L, 3, 2, av);  // A32
+      colseg(tmp, 2, J, bv);
+      a = mma16s(av, bv, a);
+    }
+    rowseg(L, I, I, av);  // D_I
+    colseg(tmp, I, J, bv);
+    a = mma16s(av, bv, a);
+    put(L, I, J, a, -1.f);
   }
   __syncthreads();
 }
