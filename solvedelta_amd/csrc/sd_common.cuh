@@ -507,7 +507,7 @@ __device__ __forceinline__ f4 mma16s(const float* av, const float* bv, f4 acc) {
 // drained (lgkmcnt) before the write.  The MFMA output layout (lane: rows
 // (lane>>4)*4+e, column lane&15) is the K=16 B-operand layout, so a product
 // feeds the next one from registers.  tmp: 64 x LS scratch.
-__device__ void unit_lower_inverse(float* L, float* tmp) {
+__device__ __forceinline__ void unit_lower_inverse(float* L, float* tmp) {
   const int tid = threadIdx.x;
   const int wv = tid >> 6, l = tid & 63, m = l & 15, r4 = (l >> 4) * 4;
   // rows m of block (I, K) of a matrix, columns r4..r4+3 (A operand) / rows
