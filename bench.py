@@ -73,9 +73,10 @@ BYTES_PER_CHUNK = {
     "state_c_bwd": (4 * _H + _P) + (_S + _H),
     "k_grad_s": (6 * _H + _P + 3 * _S) + (3 * _H + _P),      # dw,w,d,e,chi,dO,decay,X0,XC,lam -> de,dchi,dd,dg
     "k_src_bwd": (11 * _H) + (7 * _H),                       # 6 inputs,delta,de,dchi,dw,dd -> 4 grads,ddelta,du,dk
-    "k_bprep_c": (_A + 5 * _H + _P) + (_P + 6 * _H + _A),    # A,u,k,K,dd,ddelta,decay -> dU,Wk,kh,uh,At1,B1,Ant,P'
+    "k_bprep_c": (_A + 5 * _H + _P) + (_P + 4 * _H + _A),    # A,u,k,K,dd,ddelta,decay -> dU,Wk,At1,B1,Ant,P'
     "k_grad_c": (6 * _H + _P + 3 * _S + _A + _P + 5 * _H) + (3 * _H + _P),
-    # dw,delta,dd,kh,uh,d,decay,X0,XC,lam,P',dg, tail: u,k,h,du_src,dk_src -> du,dk,dh,dg
+    # dw,delta,dd,u,k (raw, normalised in-kernel),d,decay,X0,XC,lam,P',dg,
+    # tail: u,k,h and the partial du,dk (in the gradients) -> du,dk,dh,dg
 }
 
 
