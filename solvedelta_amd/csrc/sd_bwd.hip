@@ -219,8 +219,10 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   // chunk-major dispatch, first chunk first: the last chunk, where the reverse
   // state pass starts right after this kernel, is written last
   const int n = blockIdx.x, ch = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
+  float xdec[BS];  // the decay column's loads go out first: their latency overlaps dO's
+  decay_load(gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, xdec);
   stage_dout_rows<VEC>(p, b, t0, hh, s.dO);  // read below after the first barrier
-  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
+  decay_build(s.cd, xdec);
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
   {
