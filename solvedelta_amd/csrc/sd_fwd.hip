@@ -72,18 +72,14 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   const sd_inputs& in = p.in;
   const float* g = (const float*)in.log_decay.data + (long long)b * in.log_decay.sb +
                    (long long)hh * in.log_decay.sh;
-  build_decay(s.cd, g, in.log_decay.st, t0, T, r);
   const int w = wave_id(), l = lane_id();
-  if (threadIdx.x < BT) {  // branch-free: clamped token, then select
-    const int t = t0 + threadIdx.x;
-    const float gv = gamma_at(in.gamma, b, t < T ? t : T - 1, hh);
-    s.gam[threadIdx.x] = keep_if(t < T, gv);
-    s.xm[threadIdx.x] = erase_keep(in, b, t < T ? t : T - 1);
-  }
 {
-    // every row's loads first: a row's reduction would otherwise hold the next
-    // row's loads behind it
+    // every load of the opening phase first (the decay column, then every row's
+    // u and h): a row's reduction would otherwise hold the next row's loads
+    // behind it, and the decay table's build would wait for its own
     const int cl = l & 15;
+    float xdec[BS];
+    decay_load(g, in.log_decay.st, t0, T, r, xdec);
     float ux[2][RQ], hx[2][RQ];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -91,6 +87,13 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
       load_row16(in.u, b, t, hh, T, r, ux[g]);
       load_row16(in.h, b, t, hh, T, r, hx[g]);
     }
+    if (threadIdx.x < BT) {  // branch-free: clamped token, then select
+      const int t = t0 + threadIdx.x;
+      const float gv = gamma_at(in.gamma, b, t < T ? t : T - 1, hh);
+      s.gam[threadIdx.x] = keep_if(t < T, gv);
+      s.xm[threadIdx.x] = erase_keep(in, b, t < T ? t : T - 1);
+    }
+    decay_build(s.cd, xdec);
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
