@@ -753,19 +753,15 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   // chunk-major dispatch, first chunk first: the last chunk, where the reverse
   // state pass starts right after this kernel, is written last
   const int n = blockIdx.x, ch = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
-  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);
   const ChunkDecay& cd = s.cd;
   const long long cidx = (long long)n * p.NT + ch, rowbase = (long long)n * p.Tp + t0;
   const int w = wave_id(), l = lane_id();
-  if (threadIdx.x < BT) {  // clamped token, then select (a guarded load would branch and wait)
-    const int t = t0 + threadIdx.x;
-    const float gv = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
-                                                    (long long)(t < p.T ? t : p.T - 1) * p.in.gamma.st +
-                                                    (long long)hh * p.in.gamma.sh];
-    s.gam[threadIdx.x] = keep_if(t < p.T, gv) * erase_keep(p.in, b, t < p.T ? t : p.T - 1);
-  }
 {
+    // every load of the opening phase first (the decay column, then every
+    // row's u and k), then the decay table's build
     const int cl = l & 15;  // 16-lane rows: every row's loads before the first reduction
+    float xdec[BS];
+    decay_load(gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, xdec);
     float ux[2][RQ], kx[2][RQ];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -773,6 +769,14 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       ld_row16(brow(p.in.u, b, t < p.T ? t : p.T - 1, hh), t < p.T, p.r, ux[g]);
       ld_row16(brow(p.in.k, b, t < p.T ? t : p.T - 1, hh), t < p.T, p.r, kx[g]);
     }
+    if (threadIdx.x < BT) {  // clamped token, then select (a guarded load would branch and wait)
+      const int t = t0 + threadIdx.x;
+      const float gv = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
+                                                      (long long)(t < p.T ? t : p.T - 1) * p.in.gamma.st +
+                                                      (long long)hh * p.in.gamma.sh];
+      s.gam[threadIdx.x] = keep_if(t < p.T, gv) * erase_keep(p.in, b, t < p.T ? t : p.T - 1);
+    }
+    decay_build(s.cd, xdec);
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
