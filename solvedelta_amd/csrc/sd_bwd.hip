@@ -55,25 +55,36 @@ __device__ __forceinline__ DoutRaw dout_raw(const BwdParams& p, int b, int t, in
 __device__ __forceinline__ float dout_val(DoutRaw r) { return keep_if(r.ok, bf2f(r.x)); }
 
 // Stages the chunk's output cotangent (bf16, read in place; padded tokens and
-// columns read 0) as a split LDS panel.  All CT threads; every load is issued
-// before the first split.
-__device__ __forceinline__ void stage_dout_panel(LPanel& P, const BwdParams& p, int b, int t0, int hh) {
-  constexpr int PER = BT * KD / 4 / CT;  // 4-column groups per thread
-  DoutRaw d[PER][4];
+// columns read 0) as a split LDS panel, in two steps: the raw 16-bit loads (two
+// elements per word), issued early, then the split written to LDS.  All CT threads.
+struct DoutPanelRaw { unsigned w[BT * KD / 4 / CT][2]; };
+__device__ __forceinline__ void dout_panel_load(const BwdParams& p, int b, int t0, int hh,
+                                                DoutPanelRaw& o) {
+  constexpr int PER = BT * KD / 4 / CT;
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
+    unsigned short v[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) d[q][e] = dout_raw(p, b, t0 + i, hh, c + e);
+    for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(unsigned short, dout_raw(p, b, t0 + i, hh, c + e).x);
+    o.w[q][0] = (unsigned)v[0] | (unsigned)v[1] << 16;
+    o.w[q][1] = (unsigned)v[2] | (unsigned)v[3] << 16;
   }
+}
+__device__ __forceinline__ void dout_panel_store(LPanel& P, const BwdParams& p, int t0,
+                                                 const DoutPanelRaw& raw) {
+  constexpr int PER = BT * KD / 4 / CT;
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
     bf16x4 hh4, ll4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
+      const unsigned wd = raw.w[q][e >> 1];
+      const float x = __uint_as_float((e & 1) ? wd & 0xffff0000u : wd << 16);
+      const bool ok = p.dout != nullptr && t0 + i < p.T && c + e < p.V;
       __bf16 a, b2;
-      split_bf(dout_val(d[q][e]), a, b2);
+      split_bf(keep_if(ok, x), a, b2);
       hh4[e] = a;
       ll4[e] = b2;
     }
@@ -438,6 +449,8 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const xslot_t* X0 = p.f.Xs + sidx * KD * KD;
   const xslot_t* XC = X0 + KD * KD;
   const lslot_t* lam = p.g.Ls + sidx * KD * KD;
+  DoutPanelRaw doraw;  // the output cotangent's loads go out first; staged after the M1 Gram
+  dout_panel_load(p, b, t0, hh, doraw);
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
@@ -456,7 +469,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
     a[I] = mma_blks(A, BX, zero4());
   }
   __syncthreads();  // PA free
-  stage_dout_panel(s.PA, p, b, t0, hh);
+  dout_panel_store(s.PA, p, t0, doraw);
   __syncthreads();
   // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T;  kl = w lam^T
   lds_pair(s.PA, s.PW, s.M2, false);
