@@ -111,6 +111,17 @@ typedef struct {
 int sd_mask_rows(int B, int T, int H, const uint8_t *flags, int64_t flags_sb, int64_t flags_st,
                  const sd_mask_tensor *tensors, int n, void *stream);
 
+/* The flags sd_mask_rows and the operator's fresh input take, from bool
+ * (one byte, 0 / 1) [B,T] masks, in one launch (no counterpart in the
+ * reference; it replaces the host-side mask arithmetic of its packing step,
+ * causallsso/ops/packing.py:43-60): element (b,t) of valid / reset at
+ * mask[b*sb + t*st]; a null valid mask means every token is valid, a null reset
+ * mask none resets.  Writes flags (uint8 [B,T] contiguous: bit 0 valid, bit 1
+ * valid reset) and fresh (uint8 [B,T] contiguous: 1 on valid reset tokens). */
+int sd_mask_flags(int B, int T, const uint8_t *valid, int64_t valid_sb, int64_t valid_st,
+                  const uint8_t *reset, int64_t reset_sb, int64_t reset_st, uint8_t *flags,
+                  uint8_t *fresh, void *stream);
+
 /* One-token recurrent step (T must be 1). out: bf16 [B,1,H,V] contiguous.
  * C_T / S_T receive the advanced state; they may alias C0 / S0 (in place). */
 int sd_decode(const sd_inputs *in, void *out, float *C_T, float *S_T, void *stream);

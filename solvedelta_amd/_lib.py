@@ -54,6 +54,8 @@ EXPORTS = {
     "sd_mask_rows": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p, ctypes.c_int64,
                                     ctypes.c_int64, ctypes.POINTER(SdMaskTensor), ctypes.c_int,
                                     ctypes.c_void_p]),
+    "sd_mask_flags": (ctypes.c_int, [ctypes.c_int] * 2 + [ctypes.c_void_p, ctypes.c_int64,
+                                     ctypes.c_int64] * 2 + [ctypes.c_void_p] * 3),
     "sd_decode": (ctypes.c_int, [ctypes.POINTER(SdInputs), ctypes.c_void_p, ctypes.c_void_p,
                                  ctypes.c_void_p, ctypes.c_void_p]),
     # mixer frontend / readout (include/solvedelta_mixer.h)

@@ -77,6 +77,49 @@ __global__ __launch_bounds__(256) void k_mask_rows(MaskJobExt jx, int B, int T, 
   }
 }
 
+// In place (every tensor masked in its own contiguous storage): one wave per
+// token reads the token's flag, and only the tokens whose rows change (invalid
+// ones, and valid resets for tensors with reset_fill) write them; the others
+// cost one flag read per wave instead of one per element.
+__global__ __launch_bounds__(256) void k_mask_tokens_inplace(MaskJobExt jx, int B, int T, int H,
+                                                             const uint8_t* __restrict__ flags,
+                                                             long long f_sb, long long f_st) {
+  const long long tok = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= (long long)B * T) return;
+  const int b = (int)(tok / T), t = (int)(tok % T), l = threadIdx.x & 63;
+  const uint8_t f = flags[(long long)b * f_sb + (long long)t * f_st];
+  const bool valid = f & 1, reset = (f & 2) != 0;
+  if (valid && !reset) return;
+  for (int i = 0; i < jx.job.n; ++i) {
+    const sd_mask_tensor& m = jx.job.t[i];
+    const bool fill = valid && reset && m.reset_fill;
+    if (valid && !fill) continue;
+    const long long n = (long long)H * m.width, base = tok * n;
+    if (m.is_fp32) {
+      const float v = fill ? m.reset_value : 0.f;
+      for (long long e = l; e < n; e += 64) ((float*)m.dst)[base + e] = v;
+    } else {
+      const __bf16 v = fill ? (__bf16)m.reset_value : (__bf16)0.f;
+      for (long long e = l; e < n; e += 64) ((__bf16*)m.dst)[base + e] = v;
+    }
+  }
+}
+
+// Packed flags (bit 0 valid, bit 1 valid reset) and the fresh flags from the
+// bool masks, one thread per token.
+__global__ __launch_bounds__(256) void k_mask_flags(int B, int T, const uint8_t* valid,
+                                                    long long v_sb, long long v_st,
+                                                    const uint8_t* reset, long long r_sb,
+                                                    long long r_st, uint8_t* flags, uint8_t* fresh) {
+  const long long tok = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tok >= (long long)B * T) return;
+  const int b = (int)(tok / T), t = (int)(tok % T);
+  const bool v = valid ? valid[(long long)b * v_sb + (long long)t * v_st] != 0 : true;
+  const bool r = v && (reset ? reset[(long long)b * r_sb + (long long)t * r_st] != 0 : false);
+  flags[tok] = (uint8_t)((v ? 1 : 0) | (r ? 2 : 0));
+  fresh[tok] = r ? 1 : 0;
+}
+
 }  // namespace
 }  // namespace sd
 
@@ -107,8 +150,28 @@ extern "C" int sd_mask_rows(int B, int T, int H, const uint8_t* flags, int64_t f
     const long long items = (long long)B * T * H * ((m.width + per - 1) / per);
     work = items > work ? items : work;
   }
+  bool all_inplace = true;
+  for (int i = 0; i < n; ++i) all_inplace = all_inplace && jx.inplace[i];
+  if (all_inplace) {
+    const long long ntok = (long long)B * T;
+    SD_LAUNCH("k_mask_rows", k_mask_tokens_inplace, dim3((unsigned)((ntok + 3) / 4)), dim3(256), 0,
+              (hipStream_t)stream, jx, B, T, H, flags, (long long)flags_sb, (long long)flags_st);
+    return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+  }
   const dim3 grid((unsigned)((work + 255) / 256), (unsigned)n);
   SD_LAUNCH("k_mask_rows", k_mask_rows, grid, dim3(256), 0, (hipStream_t)stream, jx, B, T, H,
             flags, (long long)flags_sb, (long long)flags_st);
+  return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
+}
+
+extern "C" int sd_mask_flags(int B, int T, const uint8_t* valid, int64_t valid_sb,
+                             int64_t valid_st, const uint8_t* reset, int64_t reset_sb,
+                             int64_t reset_st, uint8_t* flags, uint8_t* fresh, void* stream) {
+  if (B < 1 || T < 1) return SD_ERR_SHAPE;
+  if (!flags || !fresh) return SD_ERR_ARG;
+  const long long ntok = (long long)B * T;
+  SD_LAUNCH("k_mask_flags", k_mask_flags, dim3((unsigned)((ntok + 255) / 256)), dim3(256), 0,
+            (hipStream_t)stream, B, T, valid, (long long)valid_sb, (long long)valid_st, reset,
+            (long long)reset_sb, (long long)reset_st, flags, fresh);
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }

@@ -30,10 +30,12 @@ kernels unchanged in shape:
   the predictor's residual is taken before forgetting (h - C_{t-1} u), so the
   decay alone would not reset it.
 
-The masking is one HIP launch each way (sd_mask_rows): the forward copies q,
-keys, the log-decay and gamma (broadcast to [B,T,H]) with invalid rows zeroed
-and reset rows' log-decay killed; the backward zeroes the same rows of their
-gradients in place (and the reset tokens' log-decay gradient), so invalid
+The masking is one HIP launch for the per-token flags (sd_mask_flags) and one
+each way (sd_mask_rows): the forward copies q, keys, the log-decay and gamma
+(broadcast to [B,T,H]) with invalid rows zeroed and reset rows' log-decay
+killed; the backward zeroes the same rows of their gradients in place (one
+wave per token, writing only the rows that change) and the reset tokens'
+log-decay gradient, so invalid
 tokens' inputs and reset tokens' log-decay get zero gradient, as when the
 reference leaves them out of its segments.  erase_raw and write_raw need no
 masking either: their partners on an invalid token (the key, and the write
@@ -60,16 +62,28 @@ RESET_LOG_DECAY = -20.0
 
 
 def _check_masks(valid_mask, reset_mask, B, T, device):
-    if valid_mask is None:
-        valid_mask = torch.ones(B, T, dtype=torch.bool, device=device)
-    if reset_mask is None:
-        reset_mask = torch.zeros(B, T, dtype=torch.bool, device=device)
     for name, m in (("valid_mask", valid_mask), ("reset_mask", reset_mask)):
+        if m is None:
+            continue
         if m.shape != (B, T) or m.dtype != torch.bool:
             raise ValueError(f"{name} must be bool [B,T]")
         if m.device != device:
             raise ValueError(f"{name} must be on the activation device")
     return valid_mask, reset_mask
+
+
+def _flags(valid_mask, reset_mask, B, T, device):
+    """uint8 [B,T] flags (bit 0 valid, bit 1 valid reset) and fresh flags (1 on
+    valid resets) in one launch (sd_mask_flags); a None mask is all-valid / no-reset."""
+    flags = torch.empty(B, T, dtype=torch.uint8, device=device)
+    fresh = torch.empty(B, T, dtype=torch.uint8, device=device)
+    args = []
+    for m in (valid_mask, reset_mask):
+        args += [0, 0, 0] if m is None else [m.data_ptr(), m.stride(0), m.stride(1)]
+    rc = _lib.load().sd_mask_flags(B, T, *args, flags.data_ptr(), fresh.data_ptr(),
+                                   _stream(device))
+    _lib.check(rc, "sd_mask_flags")
+    return flags, fresh
 
 
 def _mask_tensor(src: torch.Tensor, dst: torch.Tensor, reset_fill: bool, reset_value: float):
@@ -136,13 +150,11 @@ def solvedelta_masked_native(u, h, q, keys, values, associative_log_decay, erase
                                       write_raw, geometry_write, initial_state)
     B, T = u.shape[:2]
     valid_mask, reset_mask = _check_masks(valid_mask, reset_mask, B, T, u.device)
-    reset = reset_mask & valid_mask
-    flags = (valid_mask.to(torch.uint8) | (reset.to(torch.uint8) << 1)).contiguous()
+    flags, fresh = _flags(valid_mask, reset_mask, B, T, u.device)
     H = u.shape[2]
     gamma = geometry_write if geometry_write.dim() == 3 else geometry_write.reshape(1, 1, H)
     gamma = gamma.expand(B, T, H).unsqueeze(-1)
     q, keys, g, gamma = _MaskOperands.apply(flags, q, keys, associative_log_decay, gamma)
-    fresh = reset.to(torch.uint8)
     return _dispatch(u, h, q, keys, values, g, erase_raw, write_raw, gamma.squeeze(-1),
                      initial_state, return_final_state, fresh)
 
