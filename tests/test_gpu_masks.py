@@ -164,3 +164,24 @@ def test_reset_after_a_large_state():
           f"|S0| {S0.norm().item():.1e} |S_T| {rs.S.norm().item():.1e}", flush=True)
     assert torch.isfinite(out.float()).all()
     assert e_out < 2e-2 and e_pre < 2e-2 and e_C < 1e-2 and e_S < 1e-2
+
+
+def test_mask_flags_null_and_strided_masks():
+    """sd_mask_flags: None masks mean all-valid / no reset (equal to the dense
+    operator bitwise), and column-strided bool masks (every other column of a
+    wider mask) give the same result as their contiguous copies."""
+    from solvedelta_amd import solvedelta_masked_native, solvedelta_native
+    args = make_inputs(2, 70, 2, 32, 24, seed=161)
+    with torch.no_grad():
+        o1, s1 = solvedelta_masked_native(*args, None, None, return_final_state=True)
+        o2, s2 = solvedelta_native(*args, return_final_state=True)
+    assert torch.equal(o1, o2) and torch.equal(s1.S, s2.S)
+    valid, reset = _masks(2, 140, 162)
+    valid, reset = valid.cuda()[:, ::2], reset.cuda()[:, ::2]
+    assert not valid.is_contiguous()
+    with torch.no_grad():
+        o3, s3 = solvedelta_masked_native(*args, valid, reset, return_final_state=True)
+        o4, s4 = solvedelta_masked_native(*args, valid.contiguous(), reset.contiguous(),
+                                          return_final_state=True)
+    assert torch.equal(o3, o4) and torch.equal(s3.S, s4.S) and torch.equal(s3.predictor, s4.predictor)
+    assert torch.equal(o3[~valid], torch.zeros_like(o3[~valid]))
