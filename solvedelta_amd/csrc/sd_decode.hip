@@ -28,12 +28,13 @@ struct DecodeSmem {
   float u[KD], k[KD], q[KD], eg[KD], hh[KD];
   float delta[KD], d[KD], e[KD], chi[KD], z[VD];
   float4 part[4][32];
-  float red[4][4];
+  float red[4][8];
 };
 
-// Sum of up to four per-thread values over the workgroup (one barrier pair).
+// Sum of up to eight per-thread values over the workgroup (one barrier pair).
 template <int N>
-__device__ __forceinline__ void block_sums(float (&v)[N], float (&red)[4][4]) {
+__device__ __forceinline__ void block_sums(float (&v)[N], float (&red)[4][8]) {
+  static_assert(N <= 8, "eight sums at most");
 #pragma unroll
   for (int m = 0; m < N; ++m) v[m] = wave_sum(v[m]);
   __syncthreads();
@@ -144,12 +145,23 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
     s.eg[c] = (FULL || c < r) ? __expf(gl) : 0.f;
     s.z[c] = vv / (1.f + __expf(-wr));
   }
+  // Every token-vector sum the step needs, in one reduction: the three norms
+  // and the two dual-source products u.b and u.q (b = k sigmoid(erase)), taken
+  // on the raw vectors and rescaled by the norms.
+  float usq, ub, uq, bb;
   {
-    float sq3[3] = {uu * uu, kk * kk, qq * qq};
-    block_sums(sq3, s.red);
-    uu *= rsqrtf(sq3[0] + 1e-24f);
-    kk *= rsqrtf(sq3[1] + 1e-24f);
-    qq *= rsqrtf(sq3[2] + 1e-24f);
+    const float sig = tid < KD ? 1.f / (1.f + __expf(-er)) : 0.f;
+    float sums[5] = {uu * uu, kk * kk, qq * qq, uu * kk * sig, uu * qq};
+    block_sums(sums, s.red);
+    const float ru = rsqrtf(sums[0] + 1e-24f), rk = rsqrtf(sums[1] + 1e-24f),
+                rq = rsqrtf(sums[2] + 1e-24f);
+    usq = sums[0] * ru * ru;
+    ub = sums[3] * ru * rk;
+    uq = sums[4] * ru * rq;
+    uu *= ru;
+    kk *= rk;
+    qq *= rq;
+    bb = kk * sig;
   }
   if (tid < KD) {
     s.u[tid] = uu;
@@ -204,19 +216,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
     }
   }
   // sources: phi = rho delta / sqrt(rho^2 + |u|^2 |delta|^2), den = 1 + phi.u
+  // (|delta|^2 and delta.u in one reduction)
   const float dl = tid < KD ? s.delta[tid] : 0.f;
-  float nrm[2] = {uu * uu, dl * dl};
-  block_sums(nrm, s.red);
-  const float phi = RHO / sqrtf(RHO * RHO + nrm[0] * nrm[1]) * dl;
-  float pd[1] = {phi * uu};
-  block_sums(pd, s.red);
-  const float den = 1.f + pd[0];
-  const float bb = tid < KD ? kk / (1.f + __expf(-er)) : 0.f;
-  float pr2[2] = {uu * bb, uu * qq};
-  block_sums(pr2, s.red);
+  float dsum[2] = {dl * dl, dl * uu};
+  block_sums(dsum, s.red);
+  const float sc = RHO / sqrtf(RHO * RHO + usq * dsum[0]);
+  const float phi = sc * dl;
+  const float den = 1.f + sc * dsum[1];
   if (tid < KD) {
-    s.e[tid] = bb - phi * (pr2[0] / den);
-    s.chi[tid] = qq - phi * (pr2[1] / den);
+    s.e[tid] = bb - phi * (ub / den);
+    s.chi[tid] = qq - phi * (uq / den);
   }
   __syncthreads();
   // S' = D S + d (z - (D S)^T e)^T ;  o = S'^T chi
