@@ -129,11 +129,16 @@ __device__ __forceinline__ void store_du_slab(float* base, const f4 (&v)[NB]) {
 }
 
 // 64x64 N = P A (both 64 x LS in LDS) -> N (64 x LS)
+// N = P A for lower-triangular P and A (block lower): N is block lower too,
+// and block (I, J) sums only K in [16 J, 16 I + 16).
 __device__ void mat64_mul(const float* P, const float* A, float* N) {
   for (int tt = wave_id(); tt < NB * NB; tt += CW) {
     const int I = tt / NB, J = tt % NB;
-    f4 acc = mma_k32([&](int m, int k) { return P[(I * BS + m) * LS + k]; },
-                     [&](int k, int nn) { return A[k * LS + J * BS + nn]; }, BT, zero4());
+    f4 acc = zero4();
+    if (J <= I)
+      acc = mma_k32([&](int m, int k) { return P[(I * BS + m) * LS + k]; },
+                    [&](int k, int nn) { return A[k * LS + J * BS + nn]; }, (I + 1) * BS, zero4(),
+                    J * BS);
 #pragma unroll
     for (int e = 0; e < 4; ++e) N[(I * BS + out_row(e)) * LS + J * BS + out_col()] = acc[e];
   }

@@ -130,9 +130,10 @@ __device__ __forceinline__ void split_bf(float x, __bf16& hi, __bf16& lo) {
 // lambdas fa(m, k) and fb(k, n) as fp32 values.  Both operands are split into
 // bf16 hi + lo parts and multiplied as hi*hi + hi*lo + lo*hi (three MFMAs), which
 // keeps ~16 mantissa bits per product (the dropped lo*lo term is ~2^-16 relative).
-// Output layout: lane holds D[(lane>>4)*4 + e][lane & 15], e = 0..3.
+// Output layout: lane holds D[(lane>>4)*4 + e][lane & 15], e = 0..3.  32-wide K slices
+// wholly below K0 are skipped (the caller knows their products are zero).
 template <class FA, class FB>
-__device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
+__device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc, int K0 = 0) {
   const int l = lane_id();
   const int m = l & 15, kq = (l >> 4) * 8;
   // Gather every operand first (K <= 128) so all loads are in flight together,
@@ -140,7 +141,7 @@ __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
   float av[4][8], bv[4][8];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    if (ks * 32 < K) {
+    if (ks * 32 < K && ks * 32 + 32 > K0) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         av[ks][e] = fa(m, ks * 32 + kq + e);
@@ -150,7 +151,7 @@ __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc) {
   }
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    if (ks * 32 < K) {
+    if (ks * 32 < K && ks * 32 + 32 > K0) {
       bf16x8 ah, al, bh, bl;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
