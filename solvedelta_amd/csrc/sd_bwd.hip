@@ -857,6 +857,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       f4 du = zero4(), wk = zero4();
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
+        if (ks == 0 && Jb >= 2) continue;  // A and N are lower: tokens < 32 reach only j < 32
         float va[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) va[e] = s.A[(ks * 32 + kq + e) * LS + Jb * BS + m];
@@ -866,6 +867,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
       }
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
+        if (ks == 0 && Jb >= 2) continue;
         float vn[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) vn[e] = s.N[(ks * 32 + kq + e) * LS + Jb * BS + m];
