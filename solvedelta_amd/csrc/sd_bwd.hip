@@ -462,30 +462,31 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
   // M1_ij = dw_i . w_j (j < i)
-  lds_pair(s.PA, s.PW, s.M1, true);
+  lds_pair_h(s.PA, s.PW, s.M1, true);  // dw is a bf16 panel
   // a = dw X0^T for this wave's column block (K = 128)
   f4 a[NB], bq[NB], kl[NB];
   BlkS BX;
   load_split_blk_g(X0 + cb * 16 * KD, BX);
 #pragma unroll
   for (int I = 0; I < NB; ++I) {
-    BlkS A;
-    lblk(s.PA, I * BS, A);
-    a[I] = mma_blks(A, BX, zero4());
+    BlkH A;
+    lblk_h(s.PA, I * BS, A);
+    a[I] = mma_blks_h(A, BX, zero4());
   }
   __syncthreads();  // PA free
   dout_panel_store(s.PA, p, t0, doraw);
   __syncthreads();
   // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T;  kl = w lam^T
-  lds_pair(s.PA, s.PW, s.M2, false);
+  lds_pair_h(s.PA, s.PW, s.M2, false);  // dO is bf16
   {
     BlkS BL;
     load_lam_rowsum(lam, XC, cb, BL, s.rsum);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
+      BlkH Ah;
+      lblk_h(s.PA, I * BS, Ah);
+      bq[I] = mma_blks_h(Ah, BX, zero4());
       BlkS A;
-      lblk(s.PA, I * BS, A);
-      bq[I] = mma_blks(A, BX, zero4());
       lblk(s.PW, I * BS, A);
       kl[I] = mma_blks(A, BL, zero4());
     }
@@ -1106,7 +1107,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   load_blk(bLam, lam + cb * 16 * KD, KD);
   load_blk(bXC, XC + cb * 16 * KD, KD);
   // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
-  lds_pair(s.PA, s.PW, s.M1, true);
+  lds_pair_h(s.PA, s.PW, s.M1, true);  // dw is a bf16 panel
   lds_pair_fn([&](int I, BlkS& a) { norm_blk<VEC>(p.in.k, b, hh, t0, p.T, p.r, s.rn, 1, I * BS, a); },
               s.PW, s.M2, false);
   f4 a[NB], kl[NB];
@@ -1116,9 +1117,10 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     lam_rowsum(bLam, bXC, cb, BL, s.rsum);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
+      BlkH Ah;  // dw_C is a bf16 panel
+      lblk_h(s.PA, I * BS, Ah);
+      a[I] = mma_blks_h(Ah, BX, zero4());
       BlkS A;
-      lblk(s.PA, I * BS, A);
-      a[I] = mma_blks(A, BX, zero4());
       lblk(s.PW, I * BS, A);
       kl[I] = mma_blks(A, BL, zero4());
     }

@@ -675,6 +675,18 @@ __device__ __forceinline__ void split_blk(const Blk& b, BlkS& o) {
   }
 }
 
+// An A operand exact in bf16 (staged from a bf16 panel: its low half is zero):
+// the high halves only, two MFMAs per K slice (the A-low term is exactly 0).
+struct BlkH { bf16x8 h[4]; };
+__device__ __forceinline__ f4 mma_blks_h(const BlkH& A, const BlkS& B, f4 acc) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A.h[ks], B.f[ks].l, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A.h[ks], B.f[ks].h, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
 __device__ __forceinline__ f4 mma_blks(const BlkS& A, const BlkS& B, f4 acc) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) acc = mma3f(A.f[ks], B.f[ks], acc);
@@ -953,6 +965,12 @@ __device__ __forceinline__ void lblk(const LPanel& P, int row0, BlkS& o) {
   }
 }
 
+__device__ __forceinline__ void lblk_h(const LPanel& P, int row0, BlkH& o) {
+  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) o.h[ks] = *reinterpret_cast<const bf16x8*>(&P.h[row0 + m][ks * 32 + kq]);
+}
+
 template <class E>
 __device__ __forceinline__ void load_split_blk_g(const E* rows, BlkS& o) {
   Blk raw;
@@ -961,7 +979,7 @@ __device__ __forceinline__ void load_split_blk_g(const E* rows, BlkS& o) {
 }
 
 // Pair matrix M = A Y^T over K = 128 (strict: j < i, else j <= i), Y from an LDS
-// panel, A from load_a (lds_pair: another LDS panel).
+// panel, A from load_a.
 // The A block of rows I*16 .. I*16+15 comes from load_a(I, a).
 template <class LoadA>
 __device__ void lds_pair_fn(LoadA&& load_a, const LPanel& Y, float* M, bool strict) {
@@ -985,8 +1003,28 @@ __device__ void lds_pair_fn(LoadA&& load_a, const LPanel& Y, float* M, bool stri
   }
 }
 
-__device__ __forceinline__ void lds_pair(const LPanel& A, const LPanel& Y, float* M, bool strict) {
-  lds_pair_fn([&](int I, BlkS& a) { lblk(A, I * BS, a); }, Y, M, strict);
+
+// lds_pair with A exact in bf16 (a panel staged from bf16 values: no low half).
+__device__ __forceinline__ void lds_pair_h(const LPanel& A, const LPanel& Y, float* M, bool strict) {
+  const int w = wave_id();
+  for (int pp = w; pp < 10; pp += CW) {
+    int I = 0, J = pp;
+    while (J > I) { J -= I + 1; ++I; }
+    BlkH a;
+    BlkS y;
+    lblk_h(A, I * BS, a);
+    lblk(Y, J * BS, y);
+    const f4 r = mma_blks_h(a, y, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + out_row(e), j = J * BS + out_col();
+      M[i * LS + j] = (strict ? j < i : j <= i) ? r[e] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) M[i * LS + j] = 0.f;
+  }
 }
 
 
