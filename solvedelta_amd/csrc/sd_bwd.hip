@@ -488,7 +488,7 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
       bq[I] = mma_blks_h(Ah, BX, zero4());
       BlkS A;
       lblk(s.PW, I * BS, A);
-      kl[I] = mma_blks(A, BL, zero4());
+      kl[I] = mma_blks_bh(A, BL, zero4());  // lambda is a bf16 slot
     }
   }
   // kl is consumed only by pass B: park it in the dead PA panel (lane-private
@@ -863,7 +863,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) va[e] = s.A[(ks * 32 + kq + e) * LS + Jb * BS + m];
         const Frag fa = split8(va);
-        du = mma3f(fa, bd[ks], du);
+        du = mma2f_bh(fa, bd[ks], du);  // ddelta is a bf16 panel
         wk = mma3f(fa, kf[ks], wk);
       }
 #pragma unroll
@@ -1122,7 +1122,7 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       a[I] = mma_blks_h(Ah, BX, zero4());
       BlkS A;
       lblk(s.PW, I * BS, A);
-      kl[I] = mma_blks(A, BL, zero4());
+      kl[I] = mma_blks_bh(A, BL, zero4());  // lambda is a bf16 slot
     }
   }
   // normalised u / k at row j of the chunk, column cc

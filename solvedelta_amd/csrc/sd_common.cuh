@@ -675,6 +675,18 @@ __device__ __forceinline__ void split_blk(const Blk& b, BlkS& o) {
   }
 }
 
+// A B operand exact in bf16 (split from bf16 values: its low half is zero):
+// two MFMAs per K slice (the B-low term is exactly 0).
+__device__ __forceinline__ f4 mma2f_bh(const Frag& a, const Frag& b, f4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.l, b.h, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.h, b.h, acc, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mma_blks_bh(const BlkS& A, const BlkS& B, f4 acc) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) acc = mma2f_bh(A.f[ks], B.f[ks], acc);
+  return acc;
+}
+
 // An A operand exact in bf16 (staged from a bf16 panel: its low half is zero):
 // the high halves only, two MFMAs per K slice (the A-low term is exactly 0).
 struct BlkH { bf16x8 h[4]; };
