@@ -1042,32 +1042,29 @@ __device__ __forceinline__ float norm_elem(const sd_view& v, int b, int hh, int 
   return keep_if(t < T && c < r, x) * rn;
 }
 
+// The raw rows j0 .. j0+15 of a bf16 input view as A fragments (16 x 128, exact
+// in bf16: no low half; padded tokens and columns >= r read 0).  VEC: 16-byte
+// row pieces; the element form reads the same values one by one.
 template <bool VEC>
-__device__ __forceinline__ void norm_blk(const sd_view& v, int b, int hh, int t0, int T, int r,
-                                         const float (&rn)[BT][2], int which, int j0, BlkS& o) {
+__device__ __forceinline__ void raw_blk_h(const sd_view& v, int b, int hh, int t0, int T, int r,
+                                          int j0, BlkH& o) {
   const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8, t = t0 + j0 + m;
   const __bf16* row = brow(v, b, t < T ? t : T - 1, hh);
-  const float sc = rn[j0 + m][which];
-  Blk raw;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int c0 = ks * 32 + kq;
-    float x[8];
     if constexpr (VEC) {
       const bf16x8 pv = *reinterpret_cast<const bf16x8*>(row + (c0 < r ? c0 : r - 8));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = keep_if(t < T && c0 < r, bf2f(pv[e])) * sc;
+      o.h[ks] = (t < T && c0 < r) ? pv : bf16x8{};
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int c = c0 + e;
-        x[e] = keep_if(t < T && c < r, bf2f(row[c < r ? c : r - 1])) * sc;
+        const __bf16 x = row[c < r ? c : r - 1];
+        o.h[ks][e] = (t < T && c < r) ? x : (__bf16)0.f;
       }
     }
-    raw.v[ks][0] = make_float4(x[0], x[1], x[2], x[3]);
-    raw.v[ks][1] = make_float4(x[4], x[5], x[6], x[7]);
   }
-  split_blk(raw, o);
 }
 
 template <bool VEC>
@@ -1108,8 +1105,26 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   load_blk(bXC, XC + cb * 16 * KD, KD);
   // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
   lds_pair_h(s.PA, s.PW, s.M1, true);  // dw is a bf16 panel
-  lds_pair_fn([&](int I, BlkS& a) { norm_blk<VEC>(p.in.k, b, hh, t0, p.T, p.r, s.rn, 1, I * BS, a); },
-              s.PW, s.M2, false);
+  // M2_li = k^_l . delta_i = (k_l . delta_i) / |k_l|: the raw keys are exact bf16
+  // A operands (two MFMAs per K slice), the norm scales the rows afterwards
+  for (int pp = w; pp < 10; pp += CW) {
+    int I = 0, J = pp;
+    while (J > I) { J -= I + 1; ++I; }
+    BlkH ka;
+    BlkS y;
+    raw_blk_h<VEC>(p.in.k, b, hh, t0, p.T, p.r, I * BS, ka);
+    lblk(s.PW, J * BS, y);
+    const f4 rr = mma_blks_h(ka, y, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + out_row(e), j = J * BS + out_col();
+      s.M2[i * LS + j] = j <= i ? rr[e] * s.rn[i][1] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) s.M2[i * LS + j] = 0.f;
+  }
   f4 a[NB], kl[NB];
   {
     BlkS BX, BL;

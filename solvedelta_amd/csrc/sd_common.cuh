@@ -990,33 +990,10 @@ __device__ __forceinline__ void load_split_blk_g(const E* rows, BlkS& o) {
   split_blk(raw, o);
 }
 
-// Pair matrix M = A Y^T over K = 128 (strict: j < i, else j <= i), Y from an LDS
-// panel, A from load_a.
-// The A block of rows I*16 .. I*16+15 comes from load_a(I, a).
-template <class LoadA>
-__device__ void lds_pair_fn(LoadA&& load_a, const LPanel& Y, float* M, bool strict) {
-  const int w = wave_id();
-  for (int pp = w; pp < 10; pp += CW) {
-    int I = 0, J = pp;
-    while (J > I) { J -= I + 1; ++I; }
-    BlkS a, y;
-    load_a(I, a);
-    lblk(Y, J * BS, y);
-    const f4 r = mma_blks(a, y, zero4());
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = I * BS + out_row(e), j = J * BS + out_col();
-      M[i * LS + j] = (strict ? j < i : j <= i) ? r[e] : 0.f;
-    }
-  }
-  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
-    const int i = idx / BT, j = idx % BT;
-    if ((j / BS) > (i / BS)) M[i * LS + j] = 0.f;
-  }
-}
 
 
-// lds_pair with A exact in bf16 (a panel staged from bf16 values: no low half).
+// Pair matrix M = A Y^T over K = 128 (strict: j < i, else j <= i) from two LDS
+// panels, A exact in bf16 (staged from bf16 values: no low half).
 __device__ __forceinline__ void lds_pair_h(const LPanel& A, const LPanel& Y, float* M, bool strict) {
   const int w = wave_id();
   for (int pp = w; pp < 10; pp += CW) {
