@@ -170,7 +170,9 @@ __device__ __forceinline__ f4 mma_k32(FA fa, FB fb, int K, f4 acc, int K0 = 0) {
 }
 
 // Two products sharing the A operand (A B1 and A B2): A is gathered and split once.
-template <class FA, class FB1, class FB2>
+// B2_EXACT: fb2's values are exact in bf16 (no low half), so its product takes two
+// MFMAs per K slice.
+template <bool B2_EXACT = false, class FA, class FB1, class FB2>
 __device__ __forceinline__ void mma_k32x2(FA fa, FB1 fb1, FB2 fb2, int K, f4& acc1, f4& acc2) {
   const int l = lane_id();
   const int m = l & 15, kq = (l >> 4) * 8;
@@ -203,7 +205,7 @@ __device__ __forceinline__ void mma_k32x2(FA fa, FB1 fb1, FB2 fb2, int K, f4& ac
       acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ch, acc1, 0, 0, 0);
       acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, dh, acc2, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, cl, acc1, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dl, acc2, 0, 0, 0);
+      if constexpr (!B2_EXACT) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dl, acc2, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ch, acc1, 0, 0, 0);
       acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, dh, acc2, 0, 0, 0);
     }

@@ -122,7 +122,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
       const int K = I < 2 ? 32 : 64;
       auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k] * s.gam[k]; };
       f4 aw = zero4(), au = zero4();
-      mma_k32x2(fa,
+      mma_k32x2<true>(fa,  // h is the raw bf16 input: exact
                 [&](int k, int nn) {
                   const int c = cb * 16 + nn;
                   return s.xm[k] * s.Uh[k][c] * __expf(gx_excl(cd, k, c));
