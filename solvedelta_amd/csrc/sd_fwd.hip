@@ -590,6 +590,38 @@ void launch_state(const char* name, const StateParams& sp, int nseq, hipStream_t
 // LDS plan: Pa holds u then e, Pb holds k then chi, Pc holds d then serves as
 // the inverse's scratch once d has been consumed.
 // ---------------------------------------------------------------------------
+// A 64 x 128 panel split into fp16 high / low halves: the A operand of the f16
+// MFMA against fp16 panels (delta, the X0 slot), which enter exactly as they are.
+struct HPanel {
+  _Float16 h[BT][LPS];
+  _Float16 l[BT][LPS];
+};
+__device__ __forceinline__ void hblk(const HPanel& P, int row0, f16x8 (&h)[4], f16x8 (&lo)[4]) {
+  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    h[ks] = *reinterpret_cast<const f16x8*>(&P.h[row0 + m][ks * 32 + kq]);
+    lo[ks] = *reinterpret_cast<const f16x8*>(&P.l[row0 + m][ks * 32 + kq]);
+  }
+}
+// A (split fp16) times B (fp16, exact): two f16 MFMAs per K slice.
+__device__ __forceinline__ f4 mma_h16(const f16x8 (&ah)[4], const f16x8 (&al)[4],
+                                      const f16x8 (&b)[4], f4 acc) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[ks], b[ks], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[ks], b[ks], acc, 0, 0, 0);
+  }
+  return acc;
+}
+// 16 rows of a row-major fp16 panel (row stride KD) as B fragments: lane m reads
+// 8 consecutive K of its row.
+__device__ __forceinline__ void load_f16_blk(const _Float16* rows, f16x8 (&b)[4]) {
+  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) b[ks] = *reinterpret_cast<const f16x8*>(rows + m * KD + ks * 32 + kq);
+}
+
 struct PrepSSmem {
   ChunkDecay cd;
   float M[BT * LS];
@@ -597,7 +629,8 @@ struct PrepSSmem {
   float Pb[BT][GS];
   union {
     float Pc[BT][GS];
-    LPanel Kp;  // keys split once for the M Gram and X0 k (before d), then d's staged Gram form
+    HPanel Kq;  // keys split once into fp16 halves for the M Gram and X0 k (before d)
+    LPanel Kp;  // d's staged Gram form
   };
 };
 
@@ -648,16 +681,15 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
       const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
       const float4 v = *reinterpret_cast<const float4*>(&s.Pb[i][c]);
       const float x[4] = {v.x, v.y, v.z, v.w};
-      bf16x4 hh4, ll4;
+      f16x4 hh4, ll4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        __bf16 a, b2;
-        split_bf(x[e], a, b2);
+        const _Float16 a = (_Float16)x[e];
         hh4[e] = a;
-        ll4[e] = b2;
+        ll4[e] = (_Float16)(x[e] - (float)a);
       }
-      *reinterpret_cast<bf16x4*>(&s.Kp.h[i][c]) = hh4;
-      *reinterpret_cast<bf16x4*>(&s.Kp.l[i][c]) = ll4;
+      *reinterpret_cast<f16x4*>(&s.Kq.h[i][c]) = hh4;
+      *reinterpret_cast<f16x4*>(&s.Kq.l[i][c]) = ll4;
     }
   }
   __syncthreads();
@@ -665,10 +697,10 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   for (int pp = w; pp < 10; pp += CW) {
     int I = 0, J = pp;
     while (J > I) { J -= I + 1; ++I; }
-    BlkS A, D;
-    load_split_blk_g(delta + J * BS * KD, D);
-    lblk(s.Kp, I * BS, A);
-    const f4 acc = mma_blks(A, D, zero4());
+    f16x8 ah[4], al[4], dj[4];
+    load_f16_blk(delta + J * BS * KD, dj);  // delta is an fp16 panel: exact as an f16 operand
+    hblk(s.Kq, I * BS, ah, al);
+    const f4 acc = mma_h16(ah, al, dj, zero4());
     for (int e = 0; e < 4; ++e) {
       const int i = I * BS + out_row(e), j = J * BS + out_col();
       s.M[i * LS + j] = j <= i ? acc[e] : 0.f;
@@ -690,8 +722,8 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   unsigned dq_r[2][RQ / 2], qq_r[2][RQ / 2], er_r[2][RQ / 2], vx_r[RPW], wx_r[RPW];
   {
     const int cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
-    BlkS BX;
-    load_split_blk_g(X0 + cb * 16 * KD, BX);
+    f16x8 BX[4];  // the X0 slot is fp16: exact as an f16 operand
+    load_f16_blk(X0 + cb * 16 * KD, BX);
     float Su[NB][4];
 #pragma unroll
     for (int J = 0; J < NB; ++J)
@@ -707,9 +739,9 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
     f4 a1[NB];  // X0 k for this wave's column block, from the shared split keys
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
-      BlkS A;
-      lblk(s.Kp, I * BS, A);
-      a1[I] = mma_blks(A, BX, zero4());
+      f16x8 ah[4], al[4];
+      hblk(s.Kq, I * BS, ah, al);
+      a1[I] = mma_h16(ah, al, BX, zero4());
     }
     {
       const int cl = l & 15;
