@@ -233,7 +233,7 @@ struct StateFrags {
   bf16x8 A1[REV ? SRB : 1][2];
   bf16x8 B1[REV ? HALVES : 1][2];
   float4 U4;  // U tile piece: token threadIdx / (SCOLS / 4), columns 4 (threadIdx % (SCOLS / 4))
-  float4 G4;  // chunk decay, columns 4 (threadIdx % 32) .. +3 (every wave loads all 128)
+  float4 G4;  // chunk decay, columns 4 threadIdx .. +3 (threads < 32: the only ones that stage it)
 };
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -280,7 +280,7 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
     constexpr int C4 = SCOLS / 4;
     static_assert(BT * C4 == STHREADS, "one U piece per thread");
     f.U4 = ld4(p.U + (rowbase + threadIdx.x / C4) * KD + tile * SCOLS + (threadIdx.x % C4) * 4);
-    f.G4 = ld4(p.Gam + cidx * KD + (l & 31) * 4);
+    if (threadIdx.x < KD / 4) f.G4 = ld4(p.Gam + cidx * KD + threadIdx.x * 4);
   }
   if constexpr (REV) {
     if (mask & FA1)
