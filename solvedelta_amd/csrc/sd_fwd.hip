@@ -221,6 +221,9 @@ struct StateSmem {
   float Uf[BT][XFS];  // U tile, staged from one 16-byte load per thread
   float of[BT][XFS];  // readout tile of the previous chunk (forward S pass), stored one step later
   float Gf[KD];       // chunk decay, staged from one 16-byte load per lane of wave 0
+  // reverse passes: the injection's B1 fragments, loaded by wave 0 only and shared
+  // (every wave multiplies its own At1 rows by the same B1 tile)
+  bf16x8 B1s[REV ? HALVES : 1][2][64];
 };
 
 template <bool REV, bool OUT>
@@ -289,7 +292,7 @@ __device__ __forceinline__ void load_state_frags(const StateParams& p, int n, in
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
           f.A1[q][ks] = ldb8(p.At1 + cidx * KD * BT + frag_off((SRB * w + q) * 16 + m, ks * 32 + kq, BT));
-    if (mask & FB1)
+    if ((mask & FB1) && threadIdx.x < 64)
 #pragma unroll
       for (int h = 0; h < HALVES; ++h)
 #pragma unroll
@@ -384,6 +387,13 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
     }
   *reinterpret_cast<float4*>(&s.Uf[threadIdx.x / (SCOLS / 4)][(threadIdx.x % (SCOLS / 4)) * 4]) = cur.U4;
   if (threadIdx.x < KD / 4) *reinterpret_cast<float4*>(&s.Gf[threadIdx.x * 4]) = cur.G4;
+  if constexpr (REV) {
+    if (threadIdx.x < 64)
+#pragma unroll
+      for (int h = 0; h < HALVES; ++h)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) s.B1s[h][ks][threadIdx.x] = cur.B1[h][ks];
+  }
   __syncthreads();
   prefetch(1);
   if (p.Xs) {  // slot write-back: 128 rows x SCOLS columns, four elements per piece
@@ -432,7 +442,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
       if constexpr (REV) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks], cur.B1[h][ks], X[q][h],
+          X[q][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.A1[q][ks], s.B1s[h][ks][l], X[q][h],
                                                            0, 0, 0);
       }
     }
