@@ -655,6 +655,10 @@ __device__ __forceinline__ void st_piece(__bf16* row, int w, const float (&x)[8]
 // ---------------------------------------------------------------------------
 template <bool VEC>
 __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
+  // No multiply-add contraction: left to the compiler, the two row layouts'
+  // instantiations fused different products and their partial du differed in
+  // the last bit on rare inputs; unfused, both compute bitwise the same.
+#pragma clang fp contract(off)
   const int n = blockIdx.y, b = n / p.H, hh = n % p.H;
   const int t = blockIdx.x * 16 + wave_id() * 4 + (lane_id() >> 4);
   const int r = p.r, V = p.V, T = p.T, c0 = 8 * (lane_id() & 15);
@@ -980,6 +984,9 @@ template <bool VEC>
 __device__ __forceinline__ void final_close(const BwdParams& p, int b, int hh, int t,
                                             FinRows& x, const __bf16* dx_row,
                                             const __bf16* dk_row, const __bf16* dq_row) {
+  // no multiply-add contraction: both row layouts' instantiations compute the
+  // same bits (see k_src_bwd)
+#pragma clang fp contract(off)
   const int r = p.r, c0 = 8 * (lane_id() & 15);
   const bool tv = t < p.T;
   float dx[RQ], du[RQ], dk[RQ];

@@ -91,7 +91,8 @@ def test_backward_extreme_decay_finite():
 def test_backward_strided_bitwise(T, r, seed):
     """Views whose rows are not 16-byte aligned (row stride r + 7) take the
     per-token closures' element-wise loads, packed inputs their 16-byte pieces:
-    every gradient must agree bitwise (reference test_rebuild_semantics.py:487-537)."""
+    every gradient must agree bitwise, over 40 cotangent draws (reference
+    test_rebuild_semantics.py:487-537)."""
     print(f"case strided bitwise T{T} r{r}", flush=True)
     args = make_inputs(1, T, 2, r, r, seed=seed, requires_grad=True)
     strided = list(a.detach().clone().requires_grad_() for a in args)
@@ -101,13 +102,20 @@ def test_backward_strided_bitwise(T, r, seed):
         view = store[..., : x.shape[-1]]
         view.copy_(x.detach())
         strided[i] = view.detach().requires_grad_()
-    o1, s1 = _native()(*args, return_final_state=True)
-    o2, s2 = _native()(*strided, return_final_state=True)
-    cot = [torch.randn_like(o1), torch.randn_like(s1.predictor), torch.randn_like(s1.S)]
-    g1 = torch.autograd.grad((o1, s1.predictor, s1.S), args, cot)
-    g2 = torch.autograd.grad((o2, s2.predictor, s2.S), strided, cot)
-    for a, b in zip(g1, g2):
-        assert torch.equal(a, b)
+    # Many cotangent draws: a difference between the two layouts' arithmetic (a
+    # multiply-add fused in one and not the other) flips a last bit only on rare
+    # inputs, about one draw in fifty.
+    gen = torch.Generator().manual_seed(seed + 100)
+    for draw in range(40):
+        o1, s1 = _native()(*args, return_final_state=True)
+        o2, s2 = _native()(*strided, return_final_state=True)
+        cot = [torch.randn(x.shape, generator=gen).to(x.device, x.dtype)
+               for x in (o1, s1.predictor, s1.S)]
+        g1 = torch.autograd.grad((o1, s1.predictor, s1.S), args, cot)
+        g2 = torch.autograd.grad((o2, s2.predictor, s2.S), strided, cot)
+        bad = [(n, (a.float() - b.float()).abs().max().item(), int((a != b).sum()))
+               for n, a, b in zip(NAMES, g1, g2) if not torch.equal(a, b)]
+        assert not bad, (draw, bad)
 
 
 @pytest.mark.parametrize("V,seed", [(256, 41), (200, 43)])
