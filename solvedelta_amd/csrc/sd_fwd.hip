@@ -421,16 +421,26 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
   for (int h = 0; h < HALVES; ++h)
     acc[h] = {s.Uf[tb * 16 + r4][h * 16 + m], s.Uf[tb * 16 + r4 + 1][h * 16 + m],
               s.Uf[tb * 16 + r4 + 2][h * 16 + m], s.Uf[tb * 16 + r4 + 3][h * 16 + m]};
+  // every X0 fragment is read before the first product: left to itself the
+  // scheduler interleaves the reads with the MFMA chain and exposes one LDS
+  // latency per product
+  V8 xh[HALVES][4], xl[HALVES][4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
     for (int h = 0; h < HALVES; ++h) {
-      const V8 xh = ldv8<V8>(&s.Xh[h * 16 + m][ks * 32 + kq]);
-      const V8 xl = ldv8<V8>(&s.Xl[h * 16 + m][ks * 32 + kq]);
-      acc[h] = T::mma(cur.W[ks], xl, acc[h]);
-      if constexpr (OUT) ao = T::mma(cur.Q[ks], xl, ao);
-      acc[h] = T::mma(cur.W[ks], xh, acc[h]);
-      if constexpr (OUT) ao = T::mma(cur.Q[ks], xh, ao);
+      xh[h][ks] = ldv8<V8>(&s.Xh[h * 16 + m][ks * 32 + kq]);
+      xl[h][ks] = ldv8<V8>(&s.Xl[h * 16 + m][ks * 32 + kq]);
+    }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int h = 0; h < HALVES; ++h) {
+      acc[h] = T::mma(cur.W[ks], xl[h][ks], acc[h]);
+      if constexpr (OUT) ao = T::mma(cur.Q[ks], xl[h][ks], ao);
+      acc[h] = T::mma(cur.W[ks], xh[h][ks], acc[h]);
+      if constexpr (OUT) ao = T::mma(cur.Q[ks], xh[h][ks], ao);
     }
 #pragma unroll
   for (int q = 0; q < SRB; ++q) {
@@ -480,6 +490,7 @@ __device__ __forceinline__ void state_step(const StateParams& p, StateSmem<REV>&
       wh[ks] = ldv8<V8>(&s.wh[h * 16 + m][ks * 32 + kq]);
       wl[ks] = ldv8<V8>(&s.wl[h * 16 + m][ks * 32 + kq]);
     }
+    __builtin_amdgcn_sched_barrier(0);  // all w fragments in flight before the chain
 #pragma unroll
     for (int q = 0; q < SRB; ++q)
 #pragma unroll
