@@ -49,20 +49,33 @@ typedef struct {
   int64_t sb, st, sh; /* strides in elements */
 } sd_view;
 
+/* Token flags of sd_inputs.fresh, and the log-decay a reset token is read with. */
+#define SD_TOK_FRESH 1u
+#define SD_TOK_INVALID 2u
+#define SD_TOK_RESET 4u
+#define SD_RESET_LOG_DECAY (-20.0f)
+
 typedef struct {
   int B, T, H, r, V;
   sd_view u, h, q, k, v, erase_raw, write_raw; /* bf16 */
   sd_view log_decay;                           /* fp32 */
   sd_view gamma;                               /* fp32, no channel axis */
   const float *C0, *S0;                        /* nullable initial state */
-  sd_view fresh; /* uint8 [B,T] at data[b*sb + t*st], nullable: a nonzero entry marks a
-                  * token whose predictor residual reads a zero state (the predictor's
-                  * erase read is dropped exactly).  Together with a killing log-decay
-                  * on that token this is the reference's reset (reference.py:156-227).
-                  * solvedelta_amd.masks uses log-decay -20, which keeps e^-20 ~ 2.1e-9
-                  * of both states before the token (the reference keeps none); decays
-                  * whose 16-token block total exceeds 60 take the kernels' exact but
-                  * slow per-coordinate path. */
+  sd_view fresh; /* uint8 [B,T] token flags at data[b*sb + t*st], nullable (no flags):
+                  *  SD_TOK_FRESH: the token's predictor residual reads a zero state (the
+                  *    predictor's erase read is dropped exactly);
+                  *  SD_TOK_INVALID: the token is read as neutral -- its q, keys, gamma
+                  *    and log-decay as 0 -- so it emits 0 and leaves both states as
+                  *    they were (its u, h, values and gate logits must be finite);
+                  *  SD_TOK_RESET: its log-decay is read as SD_RESET_LOG_DECAY.
+                  * FRESH | RESET on a token is the reference's reset
+                  * (reference.py:156-227) up to e^-20 ~ 2.1e-9 of both states before
+                  * it, which the reference zeroes: a decay whose 16-token block total
+                  * exceeds 60 takes the kernels' exact but slow per-coordinate path.
+                  * Gradients are those of the operands as read: a caller that masks
+                  * with these flags zeroes the gradients of invalid tokens' q, keys,
+                  * gamma and log-decay and of reset tokens' log-decay itself
+                  * (solvedelta_amd.masks does, with sd_mask_rows). */
 } sd_inputs;
 
 /* Forward. out: bf16 [B,T,H,V] contiguous. C_T / S_T nullable.
@@ -96,9 +109,9 @@ int sd_bwd(const sd_inputs *in, const void *fwd_workspace, const void *dout, con
  * [B,T,H,width] tensors into contiguous outputs, keeping the rows of valid
  * tokens and zeroing the others; on valid reset tokens rows with reset_fill
  * set take reset_value.  flags: uint8 [B,T] at flags[b*flags_sb + t*flags_st],
- * bit 0 valid, bit 1 reset.  Used forward (operands: zero invalid tokens, kill
- * the log-decay of reset tokens) and backward (gradients: zero on invalid
- * tokens, zero log-decay gradient on reset tokens).  dst == src masks in place
+ * bit 0 valid, bit 1 reset.  solvedelta_amd.masks uses it on the gradients
+ * (zero on invalid tokens, zero log-decay gradient on reset tokens; the kernels
+ * read the operands masked through the token flags).  dst == src masks in place
  * (src must then be contiguous): only the rows that change are written.
  * Returns SD_ERR_ARG for dst == src with a non-contiguous src. */
 typedef struct {
@@ -117,7 +130,9 @@ int sd_mask_rows(int B, int T, int H, const uint8_t *flags, int64_t flags_sb, in
  * causallsso/ops/packing.py:43-60): element (b,t) of valid / reset at
  * mask[b*sb + t*st]; a null valid mask means every token is valid, a null reset
  * mask none resets.  Writes flags (uint8 [B,T] contiguous: bit 0 valid, bit 1
- * valid reset) and fresh (uint8 [B,T] contiguous: 1 on valid reset tokens). */
+ * valid reset) for sd_mask_rows and the operator's token flags (uint8 [B,T]
+ * contiguous, sd_inputs.fresh): SD_TOK_INVALID on invalid tokens,
+ * SD_TOK_FRESH | SD_TOK_RESET on valid reset tokens, 0 otherwise. */
 int sd_mask_flags(int B, int T, const uint8_t *valid, int64_t valid_sb, int64_t valid_st,
                   const uint8_t *reset, int64_t reset_sb, int64_t reset_st, uint8_t *flags,
                   uint8_t *fresh, void *stream);

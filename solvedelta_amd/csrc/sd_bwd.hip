@@ -228,7 +228,7 @@ __device__ __forceinline__ Frag ldfrag_h(const _Float16* p, long long off) {
 }
 static_assert(2 * BT * LS >= BT * KD, "P + N hold a 64 x 128 panel");
 
-template <bool VEC>
+template <bool VEC, bool FL>  // FL: the call has token flags (sd_inputs.fresh)
 __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   BprepSSmem& s = *reinterpret_cast<BprepSSmem*>(smem_raw);
@@ -236,7 +236,8 @@ __global__ __launch_bounds__(CT) void k_bprep_s(BwdParams p) {
   // state pass starts right after this kernel, is written last
   const int n = blockIdx.x, ch = blockIdx.y, b = n / p.H, hh = n % p.H, t0 = ch * BT;
   float xdec[BS];  // the decay column's loads go out first: their latency overlaps dO's
-  decay_load(gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, xdec);
+  decay_load(gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, xdec, FL ? tok_flag_row(p.in, b) : nullptr,
+             tok_flag_st(p.in));
   stage_dout_rows<VEC>(p, b, t0, hh, s.dO);  // read below after the first barrier
   decay_build(s.cd, xdec);
   const ChunkDecay& cd = s.cd;
@@ -440,6 +441,7 @@ struct GradSmem {
   LPanel PW;  // w
 };
 
+template <bool FL>
 __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GradSmem& s = *reinterpret_cast<GradSmem*>(smem_raw);
@@ -458,7 +460,8 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   dout_panel_load(p, b, t0, hh, doraw);
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
-  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
+  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, FL ? tok_flag_row(p.in, b) : nullptr,
+              tok_flag_st(p.in));  // ends with a barrier
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
   // M1_ij = dw_i . w_j (j < i)
@@ -653,7 +656,7 @@ __device__ __forceinline__ void st_piece(__bf16* row, int w, const float (&x)[8]
 // padded token reads the last valid token's (finite) panel rows and masks
 // them, and its own dw row selected to zero: its ddelta row comes out zero.
 // ---------------------------------------------------------------------------
-template <bool VEC>
+template <bool VEC, bool FL>
 __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   // No multiply-add contraction: left to the compiler, the two row layouts'
   // instantiations fused different products and their partial du differed in
@@ -673,6 +676,7 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
   ld_piece<VEC>(brow(p.in.u, b, tc, hh), tv, r, u);
   ld_piece<VEC>(brow(p.in.k, b, tc, hh), tv, r, k);
   ld_piece<VEC>(brow(p.in.q, b, tc, hh), tv, r, q);
+  const float om = operand_keep_at<FL>(p.in, b, tc);  // invalid tokens' q and keys read 0
   ld_piece<VEC>(brow(p.in.erase_raw, b, tc, hh), tv, r, er);
   ld_piece<VEC>(brow(p.in.write_raw, b, tc, hh), tv, V, wr);
   ld_piece<VEC>(brow(p.in.v, b, tc, hh), tv, V, v);
@@ -695,6 +699,11 @@ __global__ __launch_bounds__(NTHREADS) void k_src_bwd(BwdParams p) {
     for (int e = 0; e < 8; ++e) x[e] *= rs;
     return rs;
   };
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    k[e] *= om;
+    q[e] *= om;
+  }
   normalise(u);
   normalise(k);
   const float rq = normalise(q);
@@ -770,6 +779,7 @@ struct BprepCSmem {
   float krs[BT];  // 1 / |k_i|
 };
 
+template <bool FL>
 __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   BprepCSmem& s = *reinterpret_cast<BprepCSmem*>(smem_raw);
@@ -784,33 +794,40 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     // row's u and k), then the decay table's build
     const int cl = l & 15;  // 16-lane rows: every row's loads before the first reduction
     float xdec[BS];
-    decay_load(gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, xdec);
-    float ux[2][RQ], kx[2][RQ];
+    decay_load(gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, xdec, FL ? tok_flag_row(p.in, b) : nullptr,
+             tok_flag_st(p.in));
+    float ux[2][RQ], kx[2][RQ], km[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int t = t0 + row16(w, g);
       ld_row16(brow(p.in.u, b, t < p.T ? t : p.T - 1, hh), t < p.T, p.r, ux[g]);
       ld_row16(brow(p.in.k, b, t < p.T ? t : p.T - 1, hh), t < p.T, p.r, kx[g]);
+      km[g] = operand_keep_at<FL>(p.in, b, t < p.T ? t : p.T - 1);  // invalid: keys read 0
     }
     if (threadIdx.x < BT) {  // clamped token, then select (a guarded load would branch and wait)
       const int t = t0 + threadIdx.x;
       const float gv = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
                                                       (long long)(t < p.T ? t : p.T - 1) * p.in.gamma.st +
                                                       (long long)hh * p.in.gamma.sh];
-      s.gam[threadIdx.x] = keep_if(t < p.T, gv) * erase_keep(p.in, b, t < p.T ? t : p.T - 1);
+      const unsigned f = tok_flags(p.in, b, t < p.T ? t : p.T - 1);
+      s.gam[threadIdx.x] = keep_if(t < p.T, gv) * operand_keep(f) * erase_keep_f(f);
     }
     decay_build(s.cd, xdec);
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) kx[g][q] *= km[g];
       const float ru = l2norm16(ux[g]);
       const float rk = l2norm16(kx[g]);
       if ((l & 15) == 0) {
-        s.krs[i] = rk;
+        // 0 for an invalid token: the injection and the C chunk gradient pair
+        // these with the raw (unmasked) key rows
+        s.krs[i] = rk * km[g];
         // the C chunk gradient scales the raw rows by these (0 past T)
         const bool tv = t0 + i < p.T;
         *reinterpret_cast<float2*>(p.g.rn + (rowbase + i) * 2) =
-            make_float2(tv ? ru : 0.f, tv ? rk : 0.f);
+            make_float2(tv ? ru : 0.f, tv ? rk * km[g] : 0.f);
       }
 #pragma unroll
       for (int q = 0; q < RQ; ++q) {
@@ -954,7 +971,7 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
 // ---------------------------------------------------------------------------
 struct FinRows {
   float u[RQ], k[RQ], h[RQ], dv[RQ], us[RQ], ks[RQ];
-  float gm, xk;
+  float gm, xk, om;  // gamma, erase keep (0 on fresh tokens), operand keep (0 on invalid)
 };
 
 template <bool VEC>
@@ -970,8 +987,10 @@ __device__ __forceinline__ void final_load(const BwdParams& p, int b, int hh, lo
                                          (long long)tc * p.in.gamma.st +
                                          (long long)hh * p.in.gamma.sh];
   // the erase read x = gamma u^ is dropped on fresh tokens: its cotangent dx
-  // reaches neither u nor gamma there
-  x.xk = erase_keep(p.in, b, tc);
+  // reaches neither u nor gamma there; an invalid token's keys and gamma read 0
+  const unsigned f = tok_flags(p.in, b, tc);
+  x.xk = erase_keep_f(f);
+  x.om = operand_keep(f);
   const long long prow = (rowbase + (tc - (t - i))) * KD;
   ld_panel_piece(p.g.dwC + prow, 1.f, x.dv);
   // the sources transpose's partial du / dk, in the gradients this tail overwrites
@@ -990,6 +1009,9 @@ __device__ __forceinline__ void final_close(const BwdParams& p, int b, int hh, i
   const int r = p.r, c0 = 8 * (lane_id() & 15);
   const bool tv = t < p.T;
   float dx[RQ], du[RQ], dk[RQ];
+  x.gm *= x.om;
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) x.k[q] *= x.om;
   {
     const bf16x8 vx = *reinterpret_cast<const bf16x8*>(dx_row + c0);
     const bf16x8 vk = *reinterpret_cast<const bf16x8*>(dk_row + c0);
@@ -1074,7 +1096,7 @@ __device__ __forceinline__ void raw_blk_h(const sd_view& v, int b, int hh, int t
   }
 }
 
-template <bool VEC>
+template <bool VEC, bool FL>
 __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GradCSmem& s = *reinterpret_cast<GradCSmem*>(smem_raw);
@@ -1095,14 +1117,16 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       const float gv = ((const float*)p.in.gamma.data)[(long long)b * p.in.gamma.sb +
                                                       (long long)(t < p.T ? t : p.T - 1) * p.in.gamma.st +
                                                       (long long)hh * p.in.gamma.sh];
-      s.gam[threadIdx.x] = keep_if(t < p.T, gv) * erase_keep(p.in, b, t < p.T ? t : p.T - 1);
+      const unsigned f = tok_flags(p.in, b, t < p.T ? t : p.T - 1);
+      s.gam[threadIdx.x] = keep_if(t < p.T, gv) * operand_keep(f) * erase_keep_f(f);
     }
     *reinterpret_cast<float2*>(s.rn[threadIdx.x]) =
         *reinterpret_cast<const float2*>(p.g.rn + (rowbase + threadIdx.x) * 2);
   }
   stage_panel(s.PA, dw);
   stage_panel(s.PW, wv);
-  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r);  // ends with a barrier
+  build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, FL ? tok_flag_row(p.in, b) : nullptr,
+              tok_flag_st(p.in));  // ends with a barrier
   const ChunkDecay& cd = s.cd;
   // this wave's X0, lambda and X_C row blocks: loads issued ahead of the two
   // LDS Grams so their latency overlaps them
@@ -1353,19 +1377,33 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   p.du = (__bf16*)du; p.dh = (__bf16*)dh; p.dq = (__bf16*)dq; p.dk = (__bf16*)dk;
   p.dv = (__bf16*)dv; p.der = (__bf16*)derase; p.dwr = (__bf16*)dwrite;
   p.dg = dlog_decay; p.dgam = dgamma;
-  SD_SMEM_ONCE(k_bprep_s<true>, (int)sizeof(BprepSSmem));
-  SD_SMEM_ONCE(k_bprep_s<false>, (int)sizeof(BprepSSmem));
-  SD_SMEM_ONCE(k_grad_s, (int)sizeof(GradSmem));
-  SD_SMEM_ONCE(k_bprep_c, (int)sizeof(BprepCSmem));
-  SD_SMEM_ONCE(k_grad_c<true>, (int)sizeof(GradCSmem));
-  SD_SMEM_ONCE(k_grad_c<false>, (int)sizeof(GradCSmem));
+  // kernels that read token flags are separate instantiations (FL): a call
+  // without flags runs no flag code at all
+  const bool fl = in->fresh.data != nullptr;
+#define SD_BWD_LAUNCH(name, K, grid, blk, smem)  \
+  do {                                            \
+    SD_SMEM_ONCE(K, (int)(smem));                 \
+    SD_LAUNCH(name, K, grid, blk, smem, st, p);   \
+  } while (0)
+#define SD_BWD_LAUNCH_FL(name, K, grid, blk, smem)                  \
+  do {                                                              \
+    if (fl) SD_BWD_LAUNCH(name, (K<true>), grid, blk, smem);        \
+    else SD_BWD_LAUNCH(name, (K<false>), grid, blk, smem);          \
+  } while (0)
+#define SD_BWD_LAUNCH_VFL(name, K, vec, grid, blk, smem)                  \
+  do {                                                                    \
+    if (vec) {                                                            \
+      if (fl) SD_BWD_LAUNCH(name, (K<true, true>), grid, blk, smem);      \
+      else SD_BWD_LAUNCH(name, (K<true, false>), grid, blk, smem);        \
+    } else {                                                              \
+      if (fl) SD_BWD_LAUNCH(name, (K<false, true>), grid, blk, smem);     \
+      else SD_BWD_LAUNCH(name, (K<false, false>), grid, blk, smem);       \
+    }                                                                     \
+  } while (0)
   const dim3 chunks(NT, n), blk(NTHREADS), cblk(CT);
   // S memory
   const dim3 chunks_cm(n, NT);  // chunk-major grid of the backward preps
-  if (in->V % 8 == 0)
-    SD_LAUNCH("k_bprep_s", k_bprep_s<true>, chunks_cm, cblk, sizeof(BprepSSmem), st, p);
-  else
-    SD_LAUNCH("k_bprep_s", k_bprep_s<false>, chunks_cm, cblk, sizeof(BprepSSmem), st, p);
+  SD_BWD_LAUNCH_VFL("k_bprep_s", k_bprep_s, in->V % 8 == 0, chunks_cm, cblk, sizeof(BprepSSmem));
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;
   ss.rev = 1;
@@ -1375,13 +1413,10 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   ss.init = dS_T; ss.init_transposed = 0;
   ss.fin = dS0; ss.fin_transposed = 0;
   launch_state("state_s_bwd", ss, n, st);
-  SD_LAUNCH("k_grad_s", k_grad_s, chunks, cblk, sizeof(GradSmem), st, p);
-  if (src_vec)
-    SD_LAUNCH("k_src_bwd", k_src_bwd<true>, dim3(Tp / 16, n), blk, 0, st, p);
-  else
-    SD_LAUNCH("k_src_bwd", k_src_bwd<false>, dim3(Tp / 16, n), blk, 0, st, p);
+  SD_BWD_LAUNCH_FL("k_grad_s", k_grad_s, chunks, cblk, sizeof(GradSmem));
+  SD_BWD_LAUNCH_VFL("k_src_bwd", k_src_bwd, src_vec, dim3(Tp / 16, n), blk, 0);
   // C predictor
-  SD_LAUNCH("k_bprep_c", k_bprep_c, chunks_cm, cblk, sizeof(BprepCSmem), st, p);
+  SD_BWD_LAUNCH_FL("k_bprep_c", k_bprep_c, chunks_cm, cblk, sizeof(BprepCSmem));
   StateParams sc{};
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
   sc.rev = 1;
@@ -1391,10 +1426,10 @@ int launch_bwd(const sd_inputs* in, const FwdWs& fw, const BwdWs& bw, const void
   sc.init = dC_T; sc.init_transposed = 1;
   sc.fin = dC0; sc.fin_transposed = 1;
   launch_state("state_c_bwd", sc, n, st);
-  if (fin_vec)
-    SD_LAUNCH("k_grad_c", k_grad_c<true>, chunks, cblk, sizeof(GradCSmem), st, p);
-  else
-    SD_LAUNCH("k_grad_c", k_grad_c<false>, chunks, cblk, sizeof(GradCSmem), st, p);
+  SD_BWD_LAUNCH_VFL("k_grad_c", k_grad_c, fin_vec, chunks, cblk, sizeof(GradCSmem));
+#undef SD_BWD_LAUNCH_VFL
+#undef SD_BWD_LAUNCH_FL
+#undef SD_BWD_LAUNCH
   return hipGetLastError() == hipSuccess ? SD_OK : SD_ERR_LAUNCH;
 }
 

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
 #include <stdint.h>
+#include "../../include/solvedelta.h"
 
 namespace sd {
 
@@ -296,14 +297,38 @@ struct ChunkDecay {
 // The chunk's log-decays in registers: thread (J, c) = (tid / 128, tid % 128)
 // holds rows J*16 .. J*16+15 of column c (clamped addresses + select: a guarded
 // load would branch and wait).
-__device__ __forceinline__ void decay_load(const float* g, long long st, int t0, int T, int r,
-                                           float (&x)[BS]) {
+// frow / fst: the batch row of the per-token flags (SD_TOK_INVALID: the
+// log-decay reads as 0; SD_TOK_RESET: it reads as SD_RESET_LOG_DECAY), or null
+// when there are none.  The two cases are separate branches that each issue
+// all of their loads (a branch after the loads would wait for them all before
+// it, in the calls without flags as well).  A wave's 128 threads share one
+// block J, so each lane loads the flags of token J*16 + (lane % 16) and the 16
+// values are read across lanes.
+__device__ __forceinline__ void decay_load_rows(const float* g, long long st, int t0, int T, int r,
+                                                float (&x)[BS]) {
   const int c = threadIdx.x & (KD - 1), J = threadIdx.x / KD;
 #pragma unroll
   for (int i = 0; i < BS; ++i) {
     const int t = t0 + J * BS + i;
     const float v = g[(long long)(t < T ? t : T - 1) * st + (c < r ? c : r - 1)];
     x[i] = keep_if(t < T && c < r, v);
+  }
+}
+__device__ __forceinline__ void decay_load(const float* g, long long st, int t0, int T, int r,
+                                           float (&x)[BS], const uint8_t* frow, long long fst) {
+  if (!frow) {
+    decay_load_rows(g, st, t0, T, r, x);
+    return;
+  }
+  const int c = threadIdx.x & (KD - 1), J = threadIdx.x / KD;
+  const int tf = t0 + J * BS + (threadIdx.x & 15);
+  const int fl = frow[(long long)(tf < T ? tf : T - 1) * fst];
+  decay_load_rows(g, st, t0, T, r, x);
+#pragma unroll
+  for (int i = 0; i < BS; ++i) {
+    const int f = __builtin_amdgcn_readlane(fl, i);
+    x[i] = (f & SD_TOK_INVALID) ? 0.f
+           : ((f & SD_TOK_RESET) ? keep_if(t0 + J * BS + i < T && c < r, SD_RESET_LOG_DECAY) : x[i]);
   }
 }
 
@@ -345,9 +370,9 @@ __device__ __forceinline__ void decay_build(ChunkDecay& cd, float (&x)[BS]) {
 }
 
 __device__ __forceinline__ void build_decay(ChunkDecay& cd, const float* g, long long st, int t0, int T,
-                                            int r) {
+                                            int r, const uint8_t* frow, long long fst) {
   float x[BS];
-  decay_load(g, st, t0, T, r, x);
+  decay_load(g, st, t0, T, r, x, frow, fst);
   decay_build(cd, x);
 }
 

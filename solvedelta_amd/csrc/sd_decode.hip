@@ -128,8 +128,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
     vv = ld(in.v, c, V);
     wr = ld(in.write_raw, c, V);
   }
-  const float gam = ((const float*)in.gamma.data)[(long long)b * in.gamma.sb +
-                                                  (long long)hd * in.gamma.sh];
+  const float gam_raw = ((const float*)in.gamma.data)[(long long)b * in.gamma.sb +
+                                                      (long long)hd * in.gamma.sh];
+  const unsigned tf = tok_flags(in, b, 0);
   const float* C0 = in.C0 ? in.C0 + (long long)n * r * r : nullptr;
   const float* S0 = in.S0 ? in.S0 + (long long)n * r * V : nullptr;
   float4 cv[16], sv[16];
@@ -138,6 +139,13 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
 #pragma unroll
   for (int a = 0; a < 16; ++a) sv[a] = ld4<FULL>(S0, i0 + a, c0, V, r, V);
   __builtin_amdgcn_sched_barrier(0);  // keep every load above the first use
+  // token flags: an invalid token reads q, keys, gamma and the log-decay as 0, a
+  // reset reads the log-decay as the reset value
+  const float om = operand_keep(tf);
+  kk *= om;
+  qq *= om;
+  const float gam = gam_raw * om;
+  if (FULL || (tid & (KD - 1)) < r) gl = decay_eff(tf, gl);
   if (tid >= KD) uu = kk = qq = er = 0.f;
   if (tid < KD) {
     const int c = tid;
@@ -181,7 +189,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_decode(sd_inputs in, __bf16* ou
       acc += c.x * s.u[j] + c.y * s.u[j + 1] + c.z * s.u[j + 2] + c.w * s.u[j + 3];
     }
     acc += __shfl_xor(acc, 1, 64);
-    if (half == 0) s.delta[i] = gam * (s.hh[i] - erase_keep(in, b, 0) * acc);
+    if (half == 0) s.delta[i] = gam * (s.hh[i] - erase_keep_f(tf) * acc);
   }
   __syncthreads();
   // C' = C diag(e^g) + delta u^T in registers; d_j = k_j + sum_i C'_ij k_i

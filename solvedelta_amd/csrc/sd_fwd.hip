@@ -61,6 +61,7 @@ struct PrepCSmem {
   LPanel Yt;          // the L Gram's Y side (u), transformed and split once
 };
 
+template <bool FL>  // FL: the call has token flags (sd_inputs.fresh)
 __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepCSmem& s = *reinterpret_cast<PrepCSmem*>(smem_raw);
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     // behind it, and the decay table's build would wait for its own
     const int cl = l & 15;
     float xdec[BS];
-    decay_load(g, in.log_decay.st, t0, T, r, xdec);
+    decay_load(g, in.log_decay.st, t0, T, r, xdec, FL ? tok_flag_row(in, b) : nullptr, tok_flag_st(in));
     float ux[2][RQ], hx[2][RQ];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -90,8 +91,9 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     if (threadIdx.x < BT) {  // branch-free: clamped token, then select
       const int t = t0 + threadIdx.x;
       const float gv = gamma_at(in.gamma, b, t < T ? t : T - 1, hh);
-      s.gam[threadIdx.x] = keep_if(t < T, gv);
-      s.xm[threadIdx.x] = erase_keep(in, b, t < T ? t : T - 1);
+      const unsigned f = tok_flags(in, b, t < T ? t : T - 1);
+      s.gam[threadIdx.x] = keep_if(t < T, gv) * operand_keep(f);  // 0 on invalid tokens
+      s.xm[threadIdx.x] = erase_keep_f(f);
     }
     decay_build(s.cd, xdec);
 #pragma unroll
@@ -655,6 +657,7 @@ struct PrepSSmem {
   };
 };
 
+template <bool FL>  // FL: the call has token flags (sd_inputs.fresh)
 __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   PrepSSmem& s = *reinterpret_cast<PrepSSmem*>(smem_raw);
@@ -670,17 +673,20 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   {
     const int cl = l & 15;
     // the rows' u / k loads are issued first: their latency overlaps the decay build
-    float ux[2][RQ], kx[2][RQ];
+    float ux[2][RQ], kx[2][RQ], km[2];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int t = t0 + row16(w, g);
       load_row16(in.u, b, t, hh, T, r, ux[g]);
       load_row16(in.k, b, t, hh, T, r, kx[g]);
+      km[g] = operand_keep_at<FL>(in, b, t < T ? t : T - 1);  // invalid tokens' keys read 0
     }
-    build_decay(s.cd, g, in.log_decay.st, t0, T, r);
+    build_decay(s.cd, g, in.log_decay.st, t0, T, r, FL ? tok_flag_row(in, b) : nullptr, tok_flag_st(in));
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const int i = row16(w, g);
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) kx[g][q] *= km[g];
       l2norm16(ux[g]);
       l2norm16(kx[g]);
 #pragma unroll
@@ -774,12 +780,14 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
         const int i = row16(w, g), t = t0 + i, tc = t < T ? t : T - 1;
         const __bf16* qrow = vrow(in.q, b, tc, hh);
         const __bf16* erow = vrow(in.erase_raw, b, tc, hh);
+        // an invalid token's q reads as 0 (all bits of both packed halves cleared)
+        const unsigned qkeep = operand_keep_at<FL>(in, b, tc) != 0.f ? ~0u : 0u;
 #pragma unroll
         for (int q2 = 0; q2 < RQ / 2; ++q2) {
           const int c0 = cl + 32 * q2, c1 = c0 + 16;
           const int cc0 = c0 < r ? c0 : r - 1, cc1 = c1 < r ? c1 : r - 1;
           dq_r[g][q2] = raw(delta, i * KD + c0) | raw(delta, i * KD + c1) << 16;
-          qq_r[g][q2] = raw(qrow, cc0) | raw(qrow, cc1) << 16;
+          qq_r[g][q2] = (raw(qrow, cc0) | raw(qrow, cc1) << 16) & qkeep;
           er_r[g][q2] = raw(erow, cc0) | raw(erow, cc1) << 16;
         }
       }
@@ -983,9 +991,16 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   fp.Wc = w.Wc; fp.Uc = w.Uc; fp.Kc = w.Kc; fp.Gam = w.Gam;
   fp.Ws = w.Ws; fp.Us = w.Us; fp.Ks = w.Ks; fp.Qs = w.Qs; fp.Ps = w.Ps;
 
-  SD_SMEM_ONCE(k_prep_c, (int)prep_c_smem());
-  SD_SMEM_ONCE(k_prep_s, (int)prep_s_smem());
-  SD_LAUNCH("k_prep_c", k_prep_c, dim3(n, NT), dim3(CT), prep_c_smem(), st, fp);
+  // kernels that read token flags are separate instantiations: a call without
+  // flags runs no flag code at all
+  const bool fl = in->fresh.data != nullptr;
+  if (fl) {
+    SD_SMEM_ONCE(k_prep_c<true>, (int)prep_c_smem());
+    SD_LAUNCH("k_prep_c", k_prep_c<true>, dim3(n, NT), dim3(CT), prep_c_smem(), st, fp);
+  } else {
+    SD_SMEM_ONCE(k_prep_c<false>, (int)prep_c_smem());
+    SD_LAUNCH("k_prep_c", k_prep_c<false>, dim3(n, NT), dim3(CT), prep_c_smem(), st, fp);
+  }
 
   StateParams sc{};
   sc.H = in->H; sc.T = in->T; sc.NT = NT; sc.Tp = Tp; sc.rows = in->r; sc.cols = in->r;
@@ -995,7 +1010,13 @@ int launch_fwd(const sd_inputs* in, void* out, float* C_T, float* S_T, const Fwd
   sc.fin = C_T; sc.fin_transposed = 1;
   launch_state("state_c_fwd", sc, n, st);
 
-  SD_LAUNCH("k_prep_s", k_prep_s, dim3(n, NT), dim3(CT), prep_s_smem(), st, fp);
+  if (fl) {
+    SD_SMEM_ONCE(k_prep_s<true>, (int)prep_s_smem());
+    SD_LAUNCH("k_prep_s", k_prep_s<true>, dim3(n, NT), dim3(CT), prep_s_smem(), st, fp);
+  } else {
+    SD_SMEM_ONCE(k_prep_s<false>, (int)prep_s_smem());
+    SD_LAUNCH("k_prep_s", k_prep_s<false>, dim3(n, NT), dim3(CT), prep_s_smem(), st, fp);
+  }
 
   StateParams ss{};
   ss.H = in->H; ss.T = in->T; ss.NT = NT; ss.Tp = Tp; ss.rows = in->r; ss.cols = in->V;

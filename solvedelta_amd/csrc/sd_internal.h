@@ -19,17 +19,38 @@ __device__ __forceinline__ long long frag_off(int row, int col, int C) {
          ((((col & 31) >> 3) << 4) + (row & 15)) * 8 + (col & 7);
 }
 
-// 0 on a token flagged fresh (its predictor residual reads a zero state: the
-// erase read x = gamma u^ of the C op is dropped), 1 otherwise.  t must be a
-// valid token index.
+// Per-token flags (sd_inputs.fresh, bit-coded; include/solvedelta.h): bit 0
+// fresh (the C op's erase read x = gamma u^ is dropped), bit 1 invalid (q,
+// keys, gamma and the log-decay read as 0), bit 2 reset (the log-decay reads as
+// SD_RESET_LOG_DECAY).  t must be a valid token index.
 // The flag's address is selected, not branched on: a load under a branch would
 // wait for every load issued before it.
 static __device__ const uint8_t sd_no_fresh = 0;  // the flag read when no flags are given
+__device__ __forceinline__ const uint8_t* tok_flag_row(const sd_inputs& in, int b) {
+  return in.fresh.data ? (const uint8_t*)in.fresh.data + (long long)b * in.fresh.sb : &sd_no_fresh;
+}
+__device__ __forceinline__ long long tok_flag_st(const sd_inputs& in) {
+  return in.fresh.data ? in.fresh.st : 0;
+}
+__device__ __forceinline__ unsigned tok_flags(const sd_inputs& in, int b, int t) {
+  return tok_flag_row(in, b)[(long long)t * tok_flag_st(in)];
+}
+// operand_keep of token t; 1 without a load in a kernel built without flags (FL)
+template <bool FL>
+__device__ __forceinline__ float operand_keep_at(const sd_inputs& in, int b, int t) {
+  if constexpr (FL) return (tok_flags(in, b, t) & SD_TOK_INVALID) ? 0.f : 1.f;
+  return 1.f;
+}
+// 0 on a fresh token, 1 otherwise
+__device__ __forceinline__ float erase_keep_f(unsigned f) { return (f & SD_TOK_FRESH) ? 0.f : 1.f; }
 __device__ __forceinline__ float erase_keep(const sd_inputs& in, int b, int t) {
-  const uint8_t* fl = in.fresh.data
-                          ? (const uint8_t*)in.fresh.data + (long long)b * in.fresh.sb + (long long)t * in.fresh.st
-                          : &sd_no_fresh;
-  return *fl ? 0.f : 1.f;
+  return erase_keep_f(tok_flags(in, b, t));
+}
+// 0 on an invalid token (its q, keys and gamma read as 0), 1 otherwise
+__device__ __forceinline__ float operand_keep(unsigned f) { return (f & SD_TOK_INVALID) ? 0.f : 1.f; }
+// the log-decay a token's kernels read: 0 when invalid, the reset value on a reset
+__device__ __forceinline__ float decay_eff(unsigned f, float g) {
+  return (f & SD_TOK_INVALID) ? 0.f : ((f & SD_TOK_RESET) ? SD_RESET_LOG_DECAY : g);
 }
 #endif
 

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void k_mask_flags(int B, int T, const uint8_t*
   const bool v = valid ? valid[(long long)b * v_sb + (long long)t * v_st] != 0 : true;
   const bool r = v && (reset ? reset[(long long)b * r_sb + (long long)t * r_st] != 0 : false);
   flags[tok] = (uint8_t)((v ? 1 : 0) | (r ? 2 : 0));
-  fresh[tok] = r ? 1 : 0;
+  fresh[tok] = (uint8_t)(!v ? SD_TOK_INVALID : r ? (SD_TOK_FRESH | SD_TOK_RESET) : 0u);
 }
 
 }  // namespace

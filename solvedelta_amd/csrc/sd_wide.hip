@@ -99,6 +99,10 @@ __global__ __launch_bounds__(WT) void k_w_tokens(TokParams p) {
   // in-chunk inclusive log-decay prefix, one coordinate per thread: the chunk's
   // 32 values are loaded first, then summed
   const int c = threadIdx.x;
+  // token flags (invalid: the log-decay reads 0; reset: the reset value): lane l
+  // holds token t0 + l % 32's, read across lanes below (loaded by every lane)
+  const int fl = tok_flag_row(p.in, b)[(long long)min(t0 + (int)(threadIdx.x & 31), T - 1) *
+                                       tok_flag_st(p.in)];
   if (c < KP) {
     const float* g = (const float*)p.in.log_decay.data + (long long)b * p.in.log_decay.sb +
                      (long long)h * p.in.log_decay.sh + min(c, r - 1);
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(WT) void k_w_tokens(TokParams p) {
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < WBT; ++i) {
-      acc += (t0 + i < T && c < r) ? gv[i] : 0.f;
+      acc += (t0 + i < T && c < r) ? decay_eff(__builtin_amdgcn_readlane(fl, i), gv[i]) : 0.f;
       p.G[(pb + t0 + i) * KP + c] = acc;
     }
   }
@@ -118,12 +122,14 @@ __global__ __launch_bounds__(WT) void k_w_tokens(TokParams p) {
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   static_assert(WBT % (NW * TU) == 0, "tokens per wave");
   for (int i0 = w; i0 < WBT; i0 += NW * TU) {
-    float uu[TU][4], kk[TU][4], qq[TU][4], hv[TU][4], gm[TU], ek[TU];
+    float uu[TU][4], kk[TU][4], qq[TU][4], hv[TU][4], gm[TU], ek[TU], om[TU];
 #pragma unroll
     for (int u = 0; u < TU; ++u) {
       const int tc = min(t0 + i0 + u * NW, T - 1);
+      const unsigned f = tok_flags(p.in, b, tc);
       gm[u] = wgamma(p.in.gamma, b, tc, h);
-      ek[u] = erase_keep(p.in, b, tc);
+      ek[u] = erase_keep_f(f);
+      om[u] = operand_keep(f);  // an invalid token's q, keys and gamma read 0
       const __bf16* ur = wrow(p.in.u, b, tc, h);
       const __bf16* kr = wrow(p.in.k, b, tc, h);
       const __bf16* qr = wrow(p.in.q, b, tc, h);
@@ -141,15 +147,15 @@ __global__ __launch_bounds__(WT) void k_w_tokens(TokParams p) {
     for (int u = 0; u < TU; ++u) {
       const int t = t0 + i0 + u * NW;
       const bool tv = t < T;
-      const float g1 = tv ? gm[u] : 0.f;
+      const float g1 = tv ? gm[u] * om[u] : 0.f;
       const float gx = tv ? g1 * ek[u] : 0.f;  // erase side: 0 on fresh tokens
       float su = 0.f, sk = 0.f, sq = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bool ok = tv && l + 64 * j < r;
         uu[u][j] = ok ? uu[u][j] : 0.f;
-        kk[u][j] = ok ? kk[u][j] : 0.f;
-        qq[u][j] = ok ? qq[u][j] : 0.f;
+        kk[u][j] = ok ? kk[u][j] * om[u] : 0.f;
+        qq[u][j] = ok ? qq[u][j] * om[u] : 0.f;
         hv[u][j] = ok ? hv[u][j] : 0.f;
         su += uu[u][j] * uu[u][j];
         sk += kk[u][j] * kk[u][j];

@@ -31,11 +31,13 @@ kernels unchanged in shape:
   decay alone would not reset it.
 
 The masking is one HIP launch for the per-token flags (sd_mask_flags) and one
-each way (sd_mask_rows): the forward copies q, keys, the log-decay and gamma
-(broadcast to [B,T,H]) with invalid rows zeroed and reset rows' log-decay
-killed; the backward zeroes the same rows of their gradients in place (one
-wave per token, writing only the rows that change) and the reset tokens'
-log-decay gradient, so invalid
+in the backward (sd_mask_rows).  The kernels read q, keys, the log-decay and
+gamma through the token flags they take as their `fresh` input
+(include/solvedelta.h: SD_TOK_INVALID reads the token's q, keys, gamma and
+log-decay as 0, SD_TOK_RESET its log-decay as RESET_LOG_DECAY, SD_TOK_FRESH
+drops its erase read), so the forward copies nothing; the backward zeroes the
+same rows of those operands' gradients in place (one wave per token, writing
+only the rows that change) and the reset tokens' log-decay gradient, so invalid
 tokens' inputs and reset tokens' log-decay get zero gradient, as when the
 reference leaves them out of its segments.  erase_raw and write_raw need no
 masking either: their partners on an invalid token (the key, and the write
@@ -112,15 +114,15 @@ def _mask_rows(flags, srcs, decay_idx, reset_value: float, inplace: bool = False
 _DECAY = 2  # position of the log-decay among the masked operands
 
 
-class _MaskOperands(torch.autograd.Function):
-    """q, keys, log-decay, gamma ([B,T,H,1]) -> copies with invalid tokens zeroed
-    and reset tokens' log-decay set to RESET_LOG_DECAY; the backward masks the
-    gradients the same way (zero log-decay gradient on reset tokens)."""
+class _MaskGrads(torch.autograd.Function):
+    """q, keys, log-decay, gamma ([B,T,H,1]) pass through unchanged (views: the
+    kernels read them masked through the token flags); the backward zeroes the
+    gradients of invalid tokens' rows and reset tokens' log-decay rows."""
 
     @staticmethod
     def forward(ctx, flags, q, keys, log_decay, gamma):
         ctx.save_for_backward(flags)
-        return tuple(_mask_rows(flags, [q, keys, log_decay, gamma], _DECAY, RESET_LOG_DECAY))
+        return q.view_as(q), keys.view_as(keys), log_decay.view_as(log_decay), gamma.view_as(gamma)
 
     @staticmethod
     def backward(ctx, *grads):
@@ -128,9 +130,9 @@ class _MaskOperands(torch.autograd.Function):
         live = [i for i, g in enumerate(grads) if g is not None]
         out = [None] * len(grads)
         if live:
-            # The incoming gradients are this function's alone (the masked
-            # operands feed only the operator), so they are masked in place:
-            # only invalid rows (and reset tokens' log-decay rows) are written.
+            # The incoming gradients are this function's alone (its outputs feed
+            # only the operator), so they are masked in place: only invalid rows
+            # (and reset tokens' log-decay rows) are written.
             srcs = [grads[i].contiguous() for i in live]
             decay = live.index(_DECAY) if _DECAY in live else None
             masked = _mask_rows(flags, srcs, decay, 0.0, inplace=True)
@@ -154,7 +156,7 @@ def solvedelta_masked_native(u, h, q, keys, values, associative_log_decay, erase
     H = u.shape[2]
     gamma = geometry_write if geometry_write.dim() == 3 else geometry_write.reshape(1, 1, H)
     gamma = gamma.expand(B, T, H).unsqueeze(-1)
-    q, keys, g, gamma = _MaskOperands.apply(flags, q, keys, associative_log_decay, gamma)
+    q, keys, g, gamma = _MaskGrads.apply(flags, q, keys, associative_log_decay, gamma)
     return _dispatch(u, h, q, keys, values, g, erase_raw, write_raw, gamma.squeeze(-1),
                      initial_state, return_final_state, fresh)
 

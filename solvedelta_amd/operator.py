@@ -229,8 +229,8 @@ def _dispatch(u, h, q, keys, values, log_decay, erase_raw, write_raw, gamma, ini
               return_final_state, fresh=None):
     """Validated operands -> decode kernel (T = 1, no grad, r, V <= 128, as
     residual_frame/operator.py:198-216) or the chunked kernels, in value groups
-    above the kernels' value width.  `fresh` is an optional uint8 [B,T] mask of
-    tokens whose predictor residual reads a zero state (include/solvedelta.h)."""
+    above the kernels' value width.  `fresh` is the optional uint8 [B,T] token
+    flags the kernels read (fresh, invalid, reset: include/solvedelta.h)."""
     B, T, H, r = u.shape
     V = values.shape[-1]
     if T == 1 and r <= _MAX_WIDTH and V <= _MAX_WIDTH and not torch.is_grad_enabled():

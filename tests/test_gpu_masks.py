@@ -185,3 +185,62 @@ def test_mask_flags_null_and_strided_masks():
                                           return_final_state=True)
     assert torch.equal(o3, o4) and torch.equal(s3.S, s4.S) and torch.equal(s3.predictor, s4.predictor)
     assert torch.equal(o3[~valid], torch.zeros_like(o3[~valid]))
+
+
+@pytest.mark.parametrize("B,T,H,r,V,seed", [(2, 150, 3, 64, 48, 171), (2, 130, 2, 128, 128, 172),
+                                            (1, 96, 2, 160, 144, 173), (3, 1, 2, 32, 40, 174)])
+def test_token_flags_equal_masked_operands(B, T, H, r, V, seed):
+    """The kernels read q, keys, gamma and the log-decay through the token flags:
+    outputs, final states and every gradient are bitwise those of the same
+    operands masked beforehand in torch (invalid rows zeroed, reset rows'
+    log-decay at RESET_LOG_DECAY) with only the fresh bit set -- chunked, wide
+    (r = 160) and decode (T = 1) kernels."""
+    from solvedelta_amd import solvedelta_masked_native, solvedelta_native
+    from solvedelta_amd.masks import RESET_LOG_DECAY
+    from solvedelta_amd.state import SolveDeltaState
+    print(f"case token flags B{B} T{T} H{H} r{r} V{V} seed {seed}", flush=True)
+    grad = T > 1
+    args = make_inputs(B, T, H, r, V, seed=seed, requires_grad=grad,
+                       gamma_shape="H" if seed % 2 else "BTH")
+    C0, S0 = make_state(B, H, r, V, seed=seed + 1, requires_grad=grad)
+    g = torch.Generator().manual_seed(seed + 2)
+    valid = torch.rand(B, T, generator=g) < 0.75
+    reset = valid & (torch.rand(B, T, generator=g) < 0.1)
+    valid, reset = valid.cuda(), reset.cuda()
+
+    def masked():
+        return solvedelta_masked_native(*args, valid, reset,
+                                        initial_state=SolveDeltaState(C0, S0),
+                                        return_final_state=True)
+
+    def manual():
+        u, h, q, k, v, gd, er, wr, gm = args
+        keep = valid[:, :, None]
+        qm = q * keep[..., None].to(q.dtype)
+        km = k * keep[..., None, None].to(k.dtype)
+        gdm = torch.where(reset[:, :, None, None], torch.full_like(gd, RESET_LOG_DECAY),
+                          gd * keep[..., None].to(gd.dtype))
+        gme = gm if gm.dim() == 3 else gm.reshape(1, 1, H).expand(B, T, H)
+        gmm = gme * keep.to(gme.dtype)
+        fresh = reset.to(torch.uint8)  # bit 0 only: the erase read dropped
+        from solvedelta_amd.operator import _dispatch
+        return _dispatch(u, h, qm, km, v, gdm, er, wr, gmm, SolveDeltaState(C0, S0), True,
+                         fresh)
+
+    def run(fn):
+        if not grad:
+            with torch.no_grad():
+                o, st = fn()
+            return [o, st.predictor, st.S]
+        o, st = fn()
+        cg = torch.Generator().manual_seed(seed + 3)
+        cots = [torch.randn(x.shape, generator=cg).to(x.device, x.dtype)
+                for x in (o, st.predictor, st.S)]
+        leaves = list(args) + [C0, S0]
+        return [o, st.predictor, st.S] + list(torch.autograd.grad((o, st.predictor, st.S), leaves, cots))
+
+    a, b = run(masked), run(manual)
+    names = ["out", "C_T", "S_T", "du", "dh", "dq", "dk", "dv", "dlog_decay", "derase", "dwrite",
+             "dgamma", "dC0", "dS0"]
+    bad = [n for n, x, y in zip(names, a, b) if not torch.equal(x, y)]
+    assert not bad, bad
