@@ -23,6 +23,10 @@ FLAGS = [
     # keep the compiler from emitting packed-fp32 VALU ops
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
+    # scheduler: relaxed occupancy targets and memory-clause grouping (the chunk
+    # kernels run one latency-bound workgroup per CU): F+B 0.859 -> 0.854 ms
+    "-mllvm", "-amdgpu-schedule-relaxed-occupancy",
+    "-mllvm", "-amdgpu-sched-strategy=max-memory-clause",
 ]
 
 
