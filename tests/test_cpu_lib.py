@@ -187,3 +187,14 @@ def test_mask_rows_argument_rejection():
     assert call(T * H * w, H * w, w, 0) == _lib.SD_ERR_ARG
     assert call(T * H * w, H * w, w, 0x3000, n=9) == _lib.SD_ERR_SHAPE
     assert lib.sd_mask_rows(0, T, H, flags, T, 1, None, 1, None) == _lib.SD_ERR_SHAPE
+
+
+def test_token_flag_constants_match_the_python_side():
+    """The header's token flags and reset log-decay are the values the masked
+    operator relies on (its RESET_LOG_DECAY)."""
+    from solvedelta_amd.masks import RESET_LOG_DECAY
+    text = open(os.path.join(ROOT, "include", "solvedelta.h")).read()
+    consts = dict(re.findall(r"#define (SD_TOK_\w+) (\d+)u", text))
+    assert consts == {"SD_TOK_FRESH": "1", "SD_TOK_INVALID": "2", "SD_TOK_RESET": "4"}
+    m = re.search(r"#define SD_RESET_LOG_DECAY \(([-\d.]+)f\)", text)
+    assert m and float(m.group(1)) == RESET_LOG_DECAY
