@@ -793,6 +793,10 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
     // every load of the opening phase first (the decay column, then every
     // row's u and k), then the decay table's build
     const int cl = l & 15;  // 16-lane rows: every row's loads before the first reduction
+    // the chunk's (I+L)^-1 (its LDS copy is written after the decay build)
+    static_assert(BT * BT == 2 * 4 * CT, "two 16-byte pieces of (I+L)^-1 per thread");
+    const float4 av0 = *reinterpret_cast<const float4*>(p.f.Ac + cidx * BT * BT + threadIdx.x * 4);
+    const float4 av1 = *reinterpret_cast<const float4*>(p.f.Ac + cidx * BT * BT + (threadIdx.x + CT) * 4);
     float xdec[BS];
     decay_load(gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, xdec, FL ? tok_flag_row(p.in, b) : nullptr,
              tok_flag_st(p.in));
@@ -835,9 +839,12 @@ __global__ __launch_bounds__(CT) void k_bprep_c(BwdParams p) {
         s.Kh[i][cl + 16 * q] = kx[g][q];
       }
     }
+    {
+      const int i0 = threadIdx.x * 4, i1 = (threadIdx.x + CT) * 4;
+      *reinterpret_cast<float4*>(&s.A[(i0 / BT) * LS + i0 % BT]) = av0;
+      *reinterpret_cast<float4*>(&s.A[(i1 / BT) * LS + i1 % BT]) = av1;
+    }
   }
-  for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
-    s.A[(idx / BT) * LS + idx % BT] = p.f.Ac[cidx * BT * BT + idx];
   __syncthreads();
   const bpan_t* ddp = p.g.dd + rowbase * KD;
   // P'_li = sum_c dd_lc u_ic e^{G_lc - G_ic}, i <= l
