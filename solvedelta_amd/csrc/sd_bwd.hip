@@ -464,12 +464,16 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
               tok_flag_st(p.in));  // ends with a barrier
   const ChunkDecay& cd = s.cd;
   const int w = wave_id(), l = lane_id(), cb = w, c = cb * 16 + (l & 15), r4 = (l >> 4) * 4;
+  // this wave's X0 row block: loads issued ahead of the M1 Gram so their latency
+  // overlaps it
+  Blk bX0;
+  load_blk(bX0, X0 + cb * 16 * KD, KD);
   // M1_ij = dw_i . w_j (j < i)
   lds_pair_h(s.PA, s.PW, s.M1, true);  // dw is a bf16 panel
   // a = dw X0^T for this wave's column block (K = 128)
   f4 a[NB], bq[NB], kl[NB];
   BlkS BX;
-  load_split_blk_g(X0 + cb * 16 * KD, BX);
+  split_blk(bX0, BX);
 #pragma unroll
   for (int I = 0; I < NB; ++I) {
     BlkH A;
