@@ -311,9 +311,9 @@ template <bool REV, bool OUT> struct LoadPlan;
 template <> struct LoadPlan<false, false> {  // C forward
   static constexpr unsigned pre = 0, part[3] = {FW | FUG, FK, 0};
 };
-template <> struct LoadPlan<false, true> {  // S forward with the readout: one burst before
-  // the step (spreading its groups over the phases measured 1-3 us slower)
-  static constexpr unsigned pre = FALL, part[3] = {0, 0, 0};
+template <> struct LoadPlan<false, true> {  // S forward with the readout: W, U and the
+  // decay before the step, Q~ and K^ after its start, P after the first barrier
+  static constexpr unsigned pre = FW | FUG, part[3] = {FQ | FK, FP, 0};
 };
 template <> struct LoadPlan<true, false> {  // reverse passes
   static constexpr unsigned pre = 0, part[3] = {FW | FUG, FK | FB1, FA1};
