@@ -119,17 +119,44 @@ __global__ __launch_bounds__(CT) void k_prep_c(FwdParams p) {
     p.Ac[((long long)n * p.NT + ch) * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
   // W = A diag(gamma) (u e^{Gexcl} masked on fresh tokens),  U = A diag(gamma) h
   const long long rowbase = (long long)n * p.Tp + t0;
-  for (int cb = w; cb < w + 1; ++cb) {
+  {
+    const int cb = w;
+    // B operands, the same for every row block I: formed and split once
+    const int m = l & 15, kq = (l >> 4) * 8;
+    bf16x8 bh[2], bl[2], hb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = ks * 32 + kq + e, c = cb * 16 + m;
+        __bf16 h, lo;
+        split_bf(s.xm[k] * s.Uh[k][c] * __expf(gx_excl(cd, k, c)), h, lo);
+        bh[ks][e] = h;
+        bl[ks][e] = lo;
+        hb[ks][e] = s.Hh[k][c];  // h is the raw bf16 input: exact
+      }
+#pragma unroll
     for (int I = 0; I < NB; ++I) {
       const int K = I < 2 ? 32 : 64;
-      auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k] * s.gam[k]; };
       f4 aw = zero4(), au = zero4();
-      mma_k32x2<true>(fa,  // h is the raw bf16 input: exact
-                [&](int k, int nn) {
-                  const int c = cb * 16 + nn;
-                  return s.xm[k] * s.Uh[k][c] * __expf(gx_excl(cd, k, c));
-                },
-                [&](int k, int nn) { return bf2f(s.Hh[k][cb * 16 + nn]); }, K, aw, au);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks * 32 >= K) break;
+        bf16x8 ah, al;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int k = ks * 32 + kq + e;
+          __bf16 h, lo;
+          split_bf(s.M[(I * BS + m) * LS + k] * s.gam[k], h, lo);
+          ah[e] = h;
+          al[e] = lo;
+        }
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh[ks], aw, 0, 0, 0);
+        au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, hb[ks], au, 0, 0, 0);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl[ks], aw, 0, 0, 0);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh[ks], aw, 0, 0, 0);
+        au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, hb[ks], au, 0, 0, 0);
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
