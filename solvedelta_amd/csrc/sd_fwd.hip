@@ -982,14 +982,44 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   __syncthreads();
   // W = A (e e^G), U = A z
   {
-    const int cb = w;
+    const int cb = w, m = l & 15, kq = (l >> 4) * 8;
+    // B operands, the same for every row block I: split once
+    bf16x8 ph[2], pl[2], zh[2], zl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = ks * 32 + kq + e, c = cb * 16 + m;
+        __bf16 h, lo;
+        split_bf(s.Pa[k][c], h, lo);
+        ph[ks][e] = h;
+        pl[ks][e] = lo;
+        split_bf(s.Pb[k][c], h, lo);
+        zh[ks][e] = h;
+        zl[ks][e] = lo;
+      }
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       const int K = I < 2 ? 32 : 64;
-      auto fa = [&](int m, int k) { return s.M[(I * BS + m) * LS + k]; };
       f4 aw = zero4(), au = zero4();
-      mma_k32x2(fa, [&](int k, int nn) { return s.Pa[k][cb * 16 + nn]; },
-                [&](int k, int nn) { return s.Pb[k][cb * 16 + nn]; }, K, aw, au);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks * 32 >= K) break;
+        bf16x8 ah, al;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          __bf16 h, lo;
+          split_bf(s.M[(I * BS + m) * LS + ks * 32 + kq + e], h, lo);
+          ah[e] = h;
+          al[e] = lo;
+        }
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ph[ks], aw, 0, 0, 0);
+        au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, zh[ks], au, 0, 0, 0);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, pl[ks], aw, 0, 0, 0);
+        au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, zl[ks], au, 0, 0, 0);
+        aw = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ph[ks], aw, 0, 0, 0);
+        au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, zh[ks], au, 0, 0, 0);
+      }
       for (int e = 0; e < 4; ++e) {
         const long long row = rowbase + I * BS + out_row(e);
         const int c = cb * 16 + out_col();
