@@ -1079,6 +1079,33 @@ __device__ void stage_ytilde(LPanel& Yt, const ChunkDecay& cd, FY Y) {
   __syncthreads();
 }
 
+// Exact fix-up of a decayed Gram for wild coordinates (their terms were left
+// out of the factored product), then a barrier.
+template <bool EXCL, class FX, class FYR>
+__device__ void gram_wild_fixup(const ChunkDecay& cd, FX X, FYR Yraw, bool strict, float* M,
+                                int ldm = LS) {
+  for (int J = 0; J < NB; ++J) {
+    const int nw = cd.nwild[J];
+    if (nw == 0) continue;
+    const int J0 = J * BS;
+    const int npairs = (BT - J0) * BS;
+    for (int idx = threadIdx.x; idx < npairs; idx += CT) {
+      const int ii = J0 + idx / BS, j = J0 + idx % BS;
+      const bool keep = strict ? (j < ii) : (j <= ii);
+      if (!keep) continue;
+      float sacc = 0.f;
+#pragma unroll 1
+      for (int q = 0; q < nw; ++q) {
+        const int c = cd.wlist[J][q];
+        const float gx = EXCL ? gx_excl(cd, ii, c) : cd.G[ii][c];
+        sacc += X(ii, c) * Yraw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+      }
+      M[ii * ldm + j] += sacc;
+    }
+  }
+  __syncthreads();
+}
+
 // decayed_gram with its Y side staged by stage_ytilde: per pair only the X side
 // (X(i, c) exp(Gx_ic - R_J[c])) is transformed and split; Yraw(j, c) gives the
 // untransformed Y for the exact wild-coordinate fix-up.
@@ -1129,27 +1156,90 @@ __device__ void decayed_gram_yt(const ChunkDecay& cd, FX X, const LPanel& Yt, FY
     if ((j / BS) > (ii / BS)) M[ii * ldm + j] = 0.f;
   }
   __syncthreads();
-  // Exact fix-up for wild coordinates.
-  for (int J = 0; J < NB; ++J) {
-    const int nw = cd.nwild[J];
-    if (nw == 0) continue;
-    const int J0 = J * BS;
-    const int npairs = (BT - J0) * BS;
-    for (int idx = threadIdx.x; idx < npairs; idx += CT) {
-      const int ii = J0 + idx / BS, j = J0 + idx % BS;
-      const bool keep = strict ? (j < ii) : (j <= ii);
-      if (!keep) continue;
-      float sacc = 0.f;
-#pragma unroll 1
-      for (int q = 0; q < nw; ++q) {
-        const int c = cd.wlist[J][q];
-        const float gx = EXCL ? gx_excl(cd, ii, c) : cd.G[ii][c];
-        sacc += X(ii, c) * Yraw(j, c) * __expf(fminf(gx - cd.G[j][c], 0.f));
+  gram_wild_fixup<EXCL>(cd, X, Yraw, strict, M, ldm);
+}
+
+// Two decayed Grams against one staged Y side, in one pass over the block
+// pairs:  M1 = X1 Y~ (j <= i) into M, and M2 = X2 Y~ (j < i) returned in the
+// caller's registers (the pairs p = wave, wave + CW of the 10, in that order)
+// for gram2_second_store.  The two X sides share the decay factor
+// exp(G_ic - R_J[c]) and the B fragments.  Ends with M1's zero blocks written
+// and a barrier; M1's wild-coordinate fix-up is gram_wild_fixup's, as is M2's
+// once it is stored.
+template <class FX1, class FX2>
+__device__ void decayed_gram2_yt(const ChunkDecay& cd, FX1 X1, FX2 X2, const LPanel& Yt, float* M,
+                                 f4 (&acc2)[2]) {
+  const int w = wave_id(), l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int p = w + it * CW;
+    acc2[it] = zero4();
+    if (p >= 10) break;
+    int I = 0, J = p;
+    while (J > I) { J -= I + 1; ++I; }
+    const int I0 = I * BS, J0 = J * BS, i = I0 + m;
+    const float* RJ = cd.R[J];
+    float x1[4][8], x2[4][8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x1[ks][e] = X1(i, ks * 32 + kq + e);
+        x2[ks][e] = X2(i, ks * 32 + kq + e);
       }
-      M[ii * ldm + j] += sacc;
+    BlkS A1, A2, B;
+    lblk(Yt, J0, B);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = ks * 32 + kq + e;
+        const float f = __expf(cd.G[i][c] - RJ[c]);
+        __bf16 h, lo;
+        split_bf(x1[ks][e] * f, h, lo);
+        A1.f[ks].h[e] = h;
+        A1.f[ks].l[e] = lo;
+        split_bf(x2[ks][e] * f, h, lo);
+        A2.f[ks].h[e] = h;
+        A2.f[ks].l[e] = lo;
+      }
+    const f4 r1 = mma_blks(A1, B, zero4());
+    acc2[it] = mma_blks(A2, B, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ii = I0 + out_row(e), j = J0 + out_col();
+      M[ii * LS + j] = j <= ii ? r1[e] : 0.f;
     }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int ii = idx / BT, j = idx % BT;
+    if ((j / BS) > (ii / BS)) M[ii * LS + j] = 0.f;
   }
   __syncthreads();
 }
+
+// The second Gram of decayed_gram2_yt written into M (strict: j < i; zero
+// blocks included), then its barrier.  M must be free for writing.
+__device__ __forceinline__ void gram2_second_store(const f4 (&acc2)[2], float* M) {
+  const int w = wave_id();
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int p = w + it * CW;
+    if (p >= 10) break;
+    int I = 0, J = p;
+    while (J > I) { J -= I + 1; ++I; }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ii = I * BS + out_row(e), j = J * BS + out_col();
+      M[ii * LS + j] = j < ii ? acc2[it][e] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int ii = idx / BT, j = idx % BT;
+    if ((j / BS) > (ii / BS)) M[ii * LS + j] = 0.f;
+  }
+  __syncthreads();
+}
+
 
 }  // namespace sd

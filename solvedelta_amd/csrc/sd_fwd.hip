@@ -953,8 +953,14 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   stage_ytilde(s.Kp, cd, [&](int j, int c) { return s.Pc[j][c]; });
   const fpan_t* const dg_ = p.d + rowbase * KD;
   auto Draw = [&](int j, int c) { return (float)dg_[j * KD + c]; };
-  // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i
-  decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pb[i][c]; }, s.Kp, Draw, false, s.M);
+  // output pair P_ij = sum_c chi_ic d_jc e^{G_ic - G_jc}, j <= i, into M, and the
+  // S-memory Gram L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i, in registers
+  // until P is stored (one pass: both share d's staged form and the decay factors)
+  auto Xchi = [&](int i, int c) { return s.Pb[i][c]; };
+  auto Xe = [&](int i, int c) { return s.Pa[i][c]; };
+  f4 lacc[2];
+  decayed_gram2_yt(cd, Xchi, Xe, s.Kp, s.M, lacc);
+  gram_wild_fixup<false>(cd, Xchi, Draw, false, s.M);
   store_frag_panel1<BT, BT>(p.Ps, cidx * BT * BT, [&](int i, int j) { return s.M[i * LS + j]; });
 #pragma unroll
   for (int q = 0; q < KPC; ++q) {
@@ -964,8 +970,8 @@ __global__ __launch_bounds__(CT) void k_prep_s(FwdParams p) {
   store_frag_panel1<BT, KD>(p.Qs, rowbase * KD,
                             [&](int i, int c) { return s.Pb[i][c] * __expf(cd.G[i][c]); });
   __syncthreads();
-  // S-memory Gram: L_ij = sum_c e_ic d_jc e^{G_ic - G_jc}, j < i
-  decayed_gram_yt<false>(cd, [&](int i, int c) { return s.Pa[i][c]; }, s.Kp, Draw, true, s.M);
+  gram2_second_store(lacc, s.M);
+  gram_wild_fixup<false>(cd, Xe, Draw, true, s.M);
   unit_lower_inverse(s.M, &s.Pc[0][0]);
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT)
     p.As[cidx * BT * BT + idx] = s.M[(idx / BT) * LS + idx % BT];
