@@ -71,25 +71,23 @@ __device__ __forceinline__ void dout_panel_load(const BwdParams& p, int b, int t
     o.w[q][1] = (unsigned)v[2] | (unsigned)v[3] << 16;
   }
 }
-__device__ __forceinline__ void dout_panel_store(LPanel& P, const BwdParams& p, int t0,
+// dO is exact in bf16: it is staged as it is (no low half) into the rows of
+// dst, a [BT][LPS] bf16 array.
+__device__ __forceinline__ void dout_panel_store(__bf16 (*dst)[LPS], const BwdParams& p, int t0,
                                                  const DoutPanelRaw& raw) {
   constexpr int PER = BT * KD / 4 / CT;
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int idx = (threadIdx.x + q * CT) * 4, i = idx / KD, c = idx % KD;
-    bf16x4 hh4, ll4;
+    bf16x4 hh4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const unsigned wd = raw.w[q][e >> 1];
       const float x = __uint_as_float((e & 1) ? wd & 0xffff0000u : wd << 16);
       const bool ok = p.dout != nullptr && t0 + i < p.T && c + e < p.V;
-      __bf16 a, b2;
-      split_bf(keep_if(ok, x), a, b2);
-      hh4[e] = a;
-      ll4[e] = b2;
+      hh4[e] = (__bf16)keep_if(ok, x);
     }
-    *reinterpret_cast<bf16x4*>(&P.h[i][c]) = hh4;
-    *reinterpret_cast<bf16x4*>(&P.l[i][c]) = ll4;
+    *reinterpret_cast<bf16x4*>(&dst[i][c]) = hh4;
   }
 }
 
@@ -456,10 +454,13 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   const xslot_t* X0 = p.f.Xs + sidx * KD * KD;
   const xslot_t* XC = X0 + KD * KD;
   const lslot_t* lam = p.g.Ls + sidx * KD * KD;
-  DoutPanelRaw doraw;  // the output cotangent's loads go out first; staged after the M1 Gram
+  DoutPanelRaw doraw;  // the output cotangent's loads go out first
   dout_panel_load(p, b, t0, hh, doraw);
-  stage_panel(s.PA, dw);
+  // dw and dO are exact in bf16: PA holds dw in its high rows and dO in its low
+  // rows (neither has a low half), so both Grams with w run in one pass
+  stage_panel_bf(s.PA.h, dw);
   stage_panel(s.PW, wv);
+  dout_panel_store(s.PA.l, p, t0, doraw);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, FL ? tok_flag_row(p.in, b) : nullptr,
               tok_flag_st(p.in));  // ends with a barrier
   const ChunkDecay& cd = s.cd;
@@ -468,9 +469,9 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
   // overlaps it
   Blk bX0;
   load_blk(bX0, X0 + cb * 16 * KD, KD);
-  // M1_ij = dw_i . w_j (j < i)
-  lds_pair_h(s.PA, s.PW, s.M1, true);  // dw is a bf16 panel
-  // a = dw X0^T for this wave's column block (K = 128)
+  // M1_ij = dw_i . w_j (j < i) and M2_li = dO_l . w_i (l >= i), one pass
+  lds_pair2_h(s.PA, s.PW, s.M1, s.M2);
+  // a = dw X0^T, bq = dO X0^T for this wave's column block (K = 128);  kl = w lam^T
   f4 a[NB], bq[NB], kl[NB];
   BlkS BX;
   split_blk(bX0, BX);
@@ -480,18 +481,13 @@ __global__ __launch_bounds__(CT) void k_grad_s(BwdParams p) {
     lblk_h(s.PA, I * BS, A);
     a[I] = mma_blks_h(A, BX, zero4());
   }
-  __syncthreads();  // PA free
-  dout_panel_store(s.PA, p, t0, doraw);
-  __syncthreads();
-  // M2_li = dO_l . w_i (l >= i);  bq = dO X0^T;  kl = w lam^T
-  lds_pair_h(s.PA, s.PW, s.M2, false);  // dO is bf16
   {
     BlkS BL;
     load_lam_rowsum(lam, XC, cb, BL, s.rsum);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       BlkH Ah;
-      lblk_h(s.PA, I * BS, Ah);
+      lblk_l(s.PA, I * BS, Ah);
       bq[I] = mma_blks_h(Ah, BX, zero4());
       BlkS A;
       lblk(s.PW, I * BS, A);

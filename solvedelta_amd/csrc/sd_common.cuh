@@ -1010,6 +1010,28 @@ __device__ __forceinline__ void lblk_h(const LPanel& P, int row0, BlkH& o) {
   for (int ks = 0; ks < 4; ++ks) o.h[ks] = *reinterpret_cast<const bf16x8*>(&P.h[row0 + m][ks * 32 + kq]);
 }
 
+// The low-half rows of a panel read as a bf16-exact A operand (a second exact
+// panel staged there; see stage_panel_bf).
+__device__ __forceinline__ void lblk_l(const LPanel& P, int row0, BlkH& o) {
+  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) o.h[ks] = *reinterpret_cast<const bf16x8*>(&P.l[row0 + m][ks * 32 + kq]);
+}
+
+// All CT threads: a [64][128] bf16 panel in global memory (row stride KD),
+// exact in bf16, copied as it is into dst ([BT][LPS] rows).
+__device__ __forceinline__ void stage_panel_bf(__bf16 (*dst)[LPS], const __bf16* src) {
+  constexpr int PER = BT * KD / 8 / CT;  // 16-byte pieces per thread
+  bf16x8 v[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) v[q] = *reinterpret_cast<const bf16x8*>(src + (threadIdx.x + q * CT) * 8);
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 8, i = idx / KD, c = idx % KD;
+    *reinterpret_cast<bf16x8*>(&dst[i][c]) = v[q];
+  }
+}
+
 template <class E>
 __device__ __forceinline__ void load_split_blk_g(const E* rows, BlkS& o) {
   Blk raw;
@@ -1043,6 +1065,37 @@ __device__ __forceinline__ void lds_pair_h(const LPanel& A, const LPanel& Y, flo
   }
 }
 
+
+// Two pair matrices against one Y panel in one pass: M1 = A.h Y^T (j < i) and
+// M2 = A.l Y^T (j <= i), the high and low rows of A holding two bf16-exact
+// panels.  Ends without a barrier, as lds_pair_h.
+__device__ __forceinline__ void lds_pair2_h(const LPanel& A, const LPanel& Y, float* M1, float* M2) {
+  const int w = wave_id();
+  for (int pp = w; pp < 10; pp += CW) {
+    int I = 0, J = pp;
+    while (J > I) { J -= I + 1; ++I; }
+    BlkH a1, a2;
+    BlkS y;
+    lblk_h(A, I * BS, a1);
+    lblk_l(A, I * BS, a2);
+    lblk(Y, J * BS, y);
+    const f4 r1 = mma_blks_h(a1, y, zero4());
+    const f4 r2 = mma_blks_h(a2, y, zero4());
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = I * BS + out_row(e), j = J * BS + out_col();
+      M1[i * LS + j] = j < i ? r1[e] : 0.f;
+      M2[i * LS + j] = j <= i ? r2[e] : 0.f;
+    }
+  }
+  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
+    const int i = idx / BT, j = idx % BT;
+    if ((j / BS) > (i / BS)) {
+      M1[i * LS + j] = 0.f;
+      M2[i * LS + j] = 0.f;
+    }
+  }
+}
 
 // Y side of a decayed Gram staged once for all block pairs:
 //   Yt[j][c] = Y(j, c) exp(R_J[c] - G[j][c])   (J = j / BS; 0 on a wild coordinate of J),
