@@ -1078,28 +1078,34 @@ __device__ __forceinline__ float norm_elem(const sd_view& v, int b, int hh, int 
   return keep_if(t < T && c < r, x) * rn;
 }
 
-// The raw rows j0 .. j0+15 of a bf16 input view as A fragments (16 x 128, exact
-// in bf16: no low half; padded tokens and columns >= r read 0).  VEC: 16-byte
-// row pieces; the element form reads the same values one by one.
+// The raw rows t0 .. t0+63 of a bf16 input view copied into dst ([BT][LPS]
+// rows, exact in bf16; padded tokens and columns >= r read 0), 16-byte row
+// pieces with VEC, element by element otherwise (the same values).
 template <bool VEC>
-__device__ __forceinline__ void raw_blk_h(const sd_view& v, int b, int hh, int t0, int T, int r,
-                                          int j0, BlkH& o) {
-  const int l = lane_id(), m = l & 15, kq = (l >> 4) * 8, t = t0 + j0 + m;
-  const __bf16* row = brow(v, b, t < T ? t : T - 1, hh);
+__device__ __forceinline__ void stage_raw_rows(__bf16 (*dst)[LPS], const sd_view& v, int b, int hh, int t0,
+                                               int T, int r) {
+  constexpr int PER = BT * KD / 8 / CT;
+  bf16x8 x[PER];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int c0 = ks * 32 + kq;
+  for (int q = 0; q < PER; ++q) {
+    const int pc = threadIdx.x + q * CT, i = pc / (KD / 8), c0 = (pc % (KD / 8)) * 8, t = t0 + i;
+    const __bf16* row = brow(v, b, t < T ? t : T - 1, hh);
     if constexpr (VEC) {
       const bf16x8 pv = *reinterpret_cast<const bf16x8*>(row + (c0 < r ? c0 : r - 8));
-      o.h[ks] = (t < T && c0 < r) ? pv : bf16x8{};
+      x[q] = (t < T && c0 < r) ? pv : bf16x8{};
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int c = c0 + e;
-        const __bf16 x = row[c < r ? c : r - 1];
-        o.h[ks][e] = (t < T && c < r) ? x : (__bf16)0.f;
+        const __bf16 val = row[c < r ? c : r - 1];
+        x[q][e] = (t < T && c < r) ? val : (__bf16)0.f;
       }
     }
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int pc = threadIdx.x + q * CT, i = pc / (KD / 8), c0 = (pc % (KD / 8)) * 8;
+    *reinterpret_cast<bf16x8*>(&dst[i][c0]) = x[q];
   }
 }
 
@@ -1130,7 +1136,10 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
     *reinterpret_cast<float2*>(s.rn[threadIdx.x]) =
         *reinterpret_cast<const float2*>(p.g.rn + (rowbase + threadIdx.x) * 2);
   }
-  stage_panel(s.PA, dw);
+  // dw and the raw keys are exact in bf16: PA holds dw in its high rows and the
+  // raw keys in its low rows, so the M1 and M2 Grams run in one pass
+  stage_panel_bf(s.PA.h, dw);
+  stage_raw_rows<VEC>(s.PA.l, p.in.k, b, hh, t0, p.T, p.r);
   stage_panel(s.PW, wv);
   build_decay(s.cd, gptr(p.in, b, hh), p.in.log_decay.st, t0, p.T, p.r, FL ? tok_flag_row(p.in, b) : nullptr,
               tok_flag_st(p.in));  // ends with a barrier
@@ -1141,28 +1150,10 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   load_blk(bX0, X0 + cb * 16 * KD, KD);
   load_blk(bLam, lam + cb * 16 * KD, KD);
   load_blk(bXC, XC + cb * 16 * KD, KD);
-  // M1_ij = dw_i . delta_j (j < i);  M2_li = k_l . delta_i (l >= i)
-  lds_pair_h(s.PA, s.PW, s.M1, true);  // dw is a bf16 panel
-  // M2_li = k^_l . delta_i = (k_l . delta_i) / |k_l|: the raw keys are exact bf16
-  // A operands (two MFMAs per K slice), the norm scales the rows afterwards
-  for (int pp = w; pp < 10; pp += CW) {
-    int I = 0, J = pp;
-    while (J > I) { J -= I + 1; ++I; }
-    BlkH ka;
-    BlkS y;
-    raw_blk_h<VEC>(p.in.k, b, hh, t0, p.T, p.r, I * BS, ka);
-    lblk(s.PW, J * BS, y);
-    const f4 rr = mma_blks_h(ka, y, zero4());
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = I * BS + out_row(e), j = J * BS + out_col();
-      s.M2[i * LS + j] = j <= i ? rr[e] * s.rn[i][1] : 0.f;
-    }
-  }
-  for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
-    const int i = idx / BT, j = idx % BT;
-    if ((j / BS) > (i / BS)) s.M2[i * LS + j] = 0.f;
-  }
+  // M1_ij = dw_i . delta_j (j < i);  M2_li = k^_l . delta_i = (k_l . delta_i) / |k_l|
+  // (l >= i): the raw keys are exact bf16 A operands, the norm scales the rows
+  // afterwards (rn is read after build_decay's barrier)
+  lds_pair2_h(s.PA, s.PW, s.M1, s.M2, [&](int i) { return s.rn[i][1]; });
   f4 a[NB], kl[NB];
   {
     BlkS BX, BL;

@@ -1067,9 +1067,13 @@ __device__ __forceinline__ void lds_pair_h(const LPanel& A, const LPanel& Y, flo
 
 
 // Two pair matrices against one Y panel in one pass: M1 = A.h Y^T (j < i) and
-// M2 = A.l Y^T (j <= i), the high and low rows of A holding two bf16-exact
-// panels.  Ends without a barrier, as lds_pair_h.
-__device__ __forceinline__ void lds_pair2_h(const LPanel& A, const LPanel& Y, float* M1, float* M2) {
+// M2 = diag(s2) A.l Y^T (j <= i), the high and low rows of A holding two
+// bf16-exact panels and s2(i) a row scale of M2.  Ends without a barrier, as
+// lds_pair_h.
+struct NoScale { __device__ float operator()(int) const { return 1.f; } };
+template <class S2 = NoScale>
+__device__ __forceinline__ void lds_pair2_h(const LPanel& A, const LPanel& Y, float* M1, float* M2,
+                                            S2 s2 = S2()) {
   const int w = wave_id();
   for (int pp = w; pp < 10; pp += CW) {
     int I = 0, J = pp;
@@ -1085,7 +1089,7 @@ __device__ __forceinline__ void lds_pair2_h(const LPanel& A, const LPanel& Y, fl
     for (int e = 0; e < 4; ++e) {
       const int i = I * BS + out_row(e), j = J * BS + out_col();
       M1[i * LS + j] = j < i ? r1[e] : 0.f;
-      M2[i * LS + j] = j <= i ? r2[e] : 0.f;
+      M2[i * LS + j] = j <= i ? r2[e] * s2(i) : 0.f;
     }
   }
   for (int idx = threadIdx.x; idx < BT * BT; idx += CT) {
