@@ -1203,9 +1203,27 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   make_rowf<true>(cd, cb, rx);
   make_rowf<false>(cd, cb, ri);
   make_colf(cd, cb, cf);
+  // PA <- dd e^G for the dq product (staged once PA is free, consumed after the
+  // applies): dd's row pieces are loaded before the barrier
+  constexpr int DPC = BT * KD / 8 / CT;  // 16-byte dd pieces per thread
+  bf16x8 ddr[DPC];
+#pragma unroll
+  for (int q = 0; q < DPC; ++q) ddr[q] = *reinterpret_cast<const bf16x8*>(ddp + (threadIdx.x + q * CT) * 8);
   __syncthreads();  // M1, M2 complete; PA free
-  // PA <- dd e^G for the dq product (staged now, consumed after the applies)
-  stage_panel(s.PA, ddp, [&](int i, int cc) { return __expf(cd.G[i][cc]); });
+#pragma unroll
+  for (int q = 0; q < DPC; ++q) {
+    const int idx = (threadIdx.x + q * CT) * 8, i = idx / KD, cc = idx % KD;
+    bf16x8 hh, ll;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 a2, b2;
+      split_bf((float)ddr[q][e] * __expf(cd.G[i][cc + e]), a2, b2);
+      hh[e] = a2;
+      ll[e] = b2;
+    }
+    *reinterpret_cast<bf16x8*>(&s.PA.h[i][cc]) = hh;
+    *reinterpret_cast<bf16x8*>(&s.PA.l[i][cc]) = ll;
+  }
   auto Xg = [&](int j, int cc) { return s.gam[j] * U(j, cc); };
   auto DO = [&](int j, int cc) { return (float)ddp[j * KD + cc]; };
   float Sx[NB][4];
