@@ -1264,6 +1264,22 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       vv[I][e] = Sod[I][e] - Su[I][e] * dk + xs[I][e];
     }
   }
+  // the dq product's X0 column block (K = 128 rows of X0): gathered now so the
+  // latency overlaps the stores and the decay closure below (issued before the
+  // applies, the gathers were held through them and spilled)
+  __builtin_amdgcn_sched_barrier(0);
+  Blk x0raw;
+  {
+    const int kq = (l >> 4) * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (float)X0[(ks * 32 + kq + e) * KD + c];
+      x0raw.v[ks][0] = make_float4(v[0], v[1], v[2], v[3]);
+      x0raw.v[ks][1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  }
   __syncthreads();  // every apply has read M1 and M2
 #pragma unroll
   for (int q = 0; q < PPC; ++q) {
@@ -1298,26 +1314,11 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
       }
   }
   __syncthreads();  // P' in M1; PA (dd e^G) staged
-  // dq = (dd e^G) X0 + P' delta: X0 column block gathered once (K = 128 rows of X0).
-  // The gathers stay here: hoisted by the scheduler into the early slab loads
-  // they were held in registers through the applies and spilled.
-  __builtin_amdgcn_sched_barrier(0);
+  // dq = (dd e^G) X0 + P' delta, from the X0 column block gathered above
   f4 dqs[NB];
   {
     BlkS BX;
-    {
-      const int kq = (l >> 4) * 8;
-      Blk raw;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (float)X0[(ks * 32 + kq + e) * KD + c];
-        raw.v[ks][0] = make_float4(v[0], v[1], v[2], v[3]);
-        raw.v[ks][1] = make_float4(v[4], v[5], v[6], v[7]);
-      }
-      split_blk(raw, BX);
-    }
+    split_blk(x0raw, BX);
     // P' delta: the delta column block's stored hi / lo halves are the B operand
     // as they are (gathered once for the four row blocks)
     Frag pw[2];
