@@ -1171,7 +1171,6 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
   }
   // normalised u / k at row j of the chunk, column cc
   auto U = [&](int j, int cc) { return norm_elem(p.in.u, b, hh, t0 + j, p.T, p.r, cc, s.rn[j][0]); };
-  auto Kn = [&](int j, int cc) { return norm_elem(p.in.k, b, hh, t0 + j, p.T, p.r, cc, s.rn[j][1]); };
   float Su[NB][4], Sdd[NB][4], Sod[NB][4];
 #pragma unroll
   for (int J = 0; J < NB; ++J)
@@ -1185,7 +1184,11 @@ __global__ __launch_bounds__(CT) void k_grad_c(BwdParams p) {
 #pragma unroll
     for (int J = 0; J < NB; ++J)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Sk[J][e] = Kn(J * BS + r4 + e, c);
+      for (int e = 0; e < 4; ++e) {
+        // the raw keys staged in PA's low rows (0 past T and past r), normalised
+        const int j = J * BS + r4 + e;
+        Sk[J][e] = (float)s.PA.l[j][c] * s.rn[j][1];
+      }
 #pragma unroll
     for (int J = 0; J < NB; ++J)
 #pragma unroll
